@@ -1,0 +1,343 @@
+"""Python binding of libminilamma_hip.so (the C ABI in include/minilamma_hip.h).
+
+The binding is ctypes over the C ABI and nothing else: no torch, no CPU
+fallback.  Importing it on a machine where the library was not built raises
+ImportError; calling an op without a GPU raises MlkError from the HIP
+runtime.  Device memory is held by DeviceBuffer (hipMalloc through the ABI);
+host arrays are numpy.
+
+The directory name is not a Python identifier, so callers load this file with
+`load_package()` from __graft_entry__.py (or importlib) under the module name
+`cpp_minilamma_amd`.
+
+Op wrappers mirror the reference's operator surface (include/cuda_ops.h):
+the same argument meaning and the same rejections, raised as MlkError whose
+text carries the caller name, like the reference's std::runtime_error
+"<Caller>: <reason>" messages.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_DIR = os.path.join(HERE, "lib")
+HIP_LIB = os.path.join(LIB_DIR, "libminilamma_hip.so")
+OPS_LIB = os.path.join(LIB_DIR, "libminilamma_ops.so")
+
+MLK_OK, MLK_ERR_INVALID, MLK_ERR_RANGE, MLK_ERR_HIP, MLK_ERR_NO_DEVICE = range(5)
+ROPE_NORMAL, ROPE_NEOX = 0, 1
+QUANT = {"q8_0": 0, "q4_0": 1, "q4_1": 2}
+BLOCK_BYTES = {"q8_0": 34, "q4_0": 18, "q4_1": 20}
+H2D, D2D, D2H = 0, 1, 2
+
+
+class MlkError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(message)
+        self.status = status
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("device_id", C.c_int), ("name", C.c_char * 256), ("arch", C.c_char * 64),
+                ("compute_major", C.c_int), ("compute_minor", C.c_int),
+                ("total_bytes", C.c_size_t), ("multiprocessors", C.c_int),
+                ("clock_khz", C.c_int), ("memory_clock_khz", C.c_int),
+                ("memory_bus_bits", C.c_int), ("runtime_version", C.c_int),
+                ("driver_version", C.c_int)]
+
+
+_vp = C.c_void_p
+_i64 = C.c_int64
+_i32 = C.c_int32
+_f = C.c_float
+
+# name -> argtypes; every op returns mlk_status (int)
+_SIGNATURES = {
+    "mlk_add_rmsnorm_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _f, _vp],
+    "mlk_rmsnorm_f32": [_vp, _vp, _vp, _i64, _i64, _f, _vp],
+    "mlk_swiglu_f32": [_vp, _vp, _vp, _i64, _vp],
+    "mlk_silu_f32": [_vp, _vp, _i64, _vp],
+    "mlk_mul_f32": [_vp, _vp, _vp, _i64, _vp],
+    "mlk_add_f32": [_vp, _vp, _vp, _i64, _vp],
+    "mlk_softmax_f32": [_vp, _vp, _i64, _i64, _vp],
+    "mlk_rope_f32": [_vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _vp, _i32, _f, _i32, _vp, _vp],
+    "mlk_gather_f32": [_vp, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _vp],
+    "mlk_gather_quant": [_i32, _vp, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _vp],
+    "mlk_quantize": [_i32, _vp, _i64, _i64, _vp, _vp],
+    "mlk_fill_normal_f32": [_vp, _i64, _f, _f, C.c_uint64, _vp],
+    "mlk_device_count": [C.POINTER(C.c_int)],
+    "mlk_set_device": [C.c_int],
+    "mlk_get_device": [C.POINTER(C.c_int)],
+    "mlk_get_device_info": [C.c_int, C.POINTER(DeviceInfo)],
+    "mlk_malloc": [C.POINTER(_vp), C.c_size_t],
+    "mlk_free": [_vp],
+    "mlk_memcpy": [_vp, _vp, C.c_size_t, _i32],
+    "mlk_memcpy_async": [_vp, _vp, C.c_size_t, _i32, _vp],
+    "mlk_zero_async": [_vp, C.c_size_t, _vp],
+    "mlk_device_synchronize": [],
+    "mlk_stream_create": [C.POINTER(_vp)],
+    "mlk_stream_destroy": [_vp],
+    "mlk_stream_synchronize": [_vp],
+    "mlk_event_create": [C.POINTER(_vp)],
+    "mlk_event_destroy": [_vp],
+    "mlk_event_record": [_vp, _vp],
+    "mlk_event_synchronize": [_vp],
+    "mlk_event_elapsed_ms": [C.POINTER(_f), _vp, _vp],
+}
+
+
+def _load():
+    if not os.path.exists(HIP_LIB):
+        raise ImportError(
+            f"{HIP_LIB} is missing: build it with `python -c 'import __graft_entry__ as g; "
+            "g.build()'` (hipcc, gfx950). There is no CPU fallback.")
+    lib = C.CDLL(HIP_LIB)
+    for name, args in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = C.c_int
+    lib.mlk_last_error.restype = C.c_char_p
+    lib.mlk_last_error.argtypes = []
+    lib.mlk_status_string.restype = C.c_char_p
+    lib.mlk_status_string.argtypes = [C.c_int]
+    lib.mlk_abi_version.restype = C.c_int
+    lib.mlk_abi_version.argtypes = []
+    lib.mlk_quant_bytes.restype = C.c_int64
+    lib.mlk_quant_bytes.argtypes = [_i32, _i64, _i64]
+    return lib
+
+
+lib = _load()
+
+
+def check(status, caller=None):
+    if status != MLK_OK:
+        msg = lib.mlk_last_error().decode(errors="replace")
+        if caller and not msg.startswith(caller):
+            msg = f"{caller}: {msg}"
+        raise MlkError(status, msg)
+
+
+def exported_symbols():
+    """Names of every C ABI function the binding binds (used by the CPU tests)."""
+    return sorted(list(_SIGNATURES) + ["mlk_last_error", "mlk_status_string",
+                                       "mlk_abi_version", "mlk_quant_bytes"])
+
+
+# ------------------------------------------------------------------ runtime
+
+def device_count():
+    n = C.c_int(0)
+    check(lib.mlk_device_count(C.byref(n)))
+    return n.value
+
+
+def set_device(device_id):
+    check(lib.mlk_set_device(device_id))
+
+
+def device_info(device_id=0):
+    info = DeviceInfo()
+    check(lib.mlk_get_device_info(device_id, C.byref(info)))
+    return {"name": info.name.decode(), "arch": info.arch.decode(),
+            "compute_units": info.multiprocessors, "total_bytes": info.total_bytes,
+            "clock_khz": info.clock_khz, "memory_clock_khz": info.memory_clock_khz,
+            "memory_bus_bits": info.memory_bus_bits, "runtime_version": info.runtime_version,
+            "driver_version": info.driver_version}
+
+
+def synchronize():
+    check(lib.mlk_device_synchronize())
+
+
+class DeviceBuffer:
+    """A device allocation of `nbytes` (hipMalloc), freed on close/GC."""
+
+    def __init__(self, nbytes, dtype=np.float32, shape=None):
+        self.nbytes = int(nbytes)
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(shape) if shape is not None else (self.nbytes // self.dtype.itemsize,)
+        p = _vp()
+        check(lib.mlk_malloc(C.byref(p), self.nbytes), "DeviceBuffer")
+        self.ptr = p.value or 0
+
+    @classmethod
+    def empty(cls, shape, dtype=np.float32):
+        shape = tuple(int(s) for s in np.atleast_1d(shape))
+        dt = np.dtype(dtype)
+        return cls(int(np.prod(shape)) * dt.itemsize, dt, shape)
+
+    @classmethod
+    def from_array(cls, arr):
+        arr = np.ascontiguousarray(arr)
+        buf = cls(arr.nbytes, arr.dtype, arr.shape)
+        buf.upload(arr)
+        return buf
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr, dtype=self.dtype)
+        if arr.nbytes > self.nbytes:
+            raise ValueError("upload exceeds device buffer size")
+        check(lib.mlk_memcpy(self.ptr, arr.ctypes.data, arr.nbytes, H2D), "upload")
+
+    def download(self, shape=None, dtype=None):
+        dt = np.dtype(dtype) if dtype is not None else self.dtype
+        shape = tuple(shape) if shape is not None else (
+            self.shape if dt == self.dtype else (self.nbytes // dt.itemsize,))
+        out = np.empty(shape, dtype=dt)
+        if out.nbytes > self.nbytes:
+            raise ValueError("download exceeds device buffer size")
+        check(lib.mlk_memcpy(out.ctypes.data, self.ptr, out.nbytes, D2H), "download")
+        return out
+
+    def zero(self, stream=None):
+        check(lib.mlk_zero_async(self.ptr, self.nbytes, _sp(stream)), "zero")
+
+    def offset(self, nbytes):
+        """Raw device address nbytes into the buffer (for sub-views)."""
+        return self.ptr + int(nbytes)
+
+    def close(self):
+        if getattr(self, "ptr", 0):
+            lib.mlk_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __int__(self):
+        return self.ptr
+
+
+class Stream:
+    def __init__(self):
+        s = _vp()
+        check(lib.mlk_stream_create(C.byref(s)), "Stream")
+        self.handle = s.value
+
+    def synchronize(self):
+        check(lib.mlk_stream_synchronize(self.handle), "Stream.synchronize")
+
+    def close(self):
+        if self.handle:
+            lib.mlk_stream_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        e = _vp()
+        check(lib.mlk_event_create(C.byref(e)), "Event")
+        self.handle = e.value
+
+    def record(self, stream=None):
+        check(lib.mlk_event_record(self.handle, _sp(stream)), "Event.record")
+
+    def synchronize(self):
+        check(lib.mlk_event_synchronize(self.handle), "Event.synchronize")
+
+    def elapsed_ms(self, end):
+        ms = _f(0.0)
+        check(lib.mlk_event_elapsed_ms(C.byref(ms), self.handle, end.handle), "Event.elapsed_ms")
+        return ms.value
+
+    def close(self):
+        if self.handle:
+            lib.mlk_event_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _sp(stream):
+    if stream is None:
+        return None
+    return stream.handle if isinstance(stream, Stream) else stream
+
+
+def _p(x):
+    """Device address of a DeviceBuffer / int / None."""
+    if x is None:
+        return None
+    return x.ptr if isinstance(x, DeviceBuffer) else int(x)
+
+
+# ---------------------------------------------------------------------- ops
+
+def add_rmsnorm(residual, delta, weight, y, n_rows, dim, eps, stream=None):
+    """residual <- residual + delta; y <- RMSNorm(residual) * weight (row-wise)."""
+    check(lib.mlk_add_rmsnorm_f32(_p(residual), _p(delta), _p(weight), _p(y), n_rows, dim, eps,
+                                  _sp(stream)), "mlk_add_rmsnorm_f32")
+
+
+def rmsnorm(x, weight, y, n_rows, dim, eps, stream=None):
+    check(lib.mlk_rmsnorm_f32(_p(x), _p(weight), _p(y), n_rows, dim, eps, _sp(stream)),
+          "mlk_rmsnorm_f32")
+
+
+def swiglu(gate, up, y, n, stream=None):
+    check(lib.mlk_swiglu_f32(_p(gate), _p(up), _p(y), n, _sp(stream)), "mlk_swiglu_f32")
+
+
+def silu(x, y, n, stream=None):
+    check(lib.mlk_silu_f32(_p(x), _p(y), n, _sp(stream)), "mlk_silu_f32")
+
+
+def mul(a, b, y, n, stream=None):
+    check(lib.mlk_mul_f32(_p(a), _p(b), _p(y), n, _sp(stream)), "mlk_mul_f32")
+
+
+def add(a, b, y, n, stream=None):
+    check(lib.mlk_add_f32(_p(a), _p(b), _p(y), n, _sp(stream)), "mlk_add_f32")
+
+
+def softmax(x, y, n_rows, n, stream=None):
+    check(lib.mlk_softmax_f32(_p(x), _p(y), n_rows, n, _sp(stream)), "mlk_softmax_f32")
+
+
+def rope(q, k, n_tokens, n_heads, n_kv_heads, head_dim, positions=None, pos0=0, theta=10000.0,
+         rope_type=ROPE_NORMAL, q_row_stride=None, k_row_stride=None, err=None, stream=None):
+    qs = q_row_stride if q_row_stride is not None else n_heads * head_dim
+    ks = k_row_stride if k_row_stride is not None else n_kv_heads * head_dim
+    check(lib.mlk_rope_f32(_p(q), _p(k), n_tokens, n_heads, n_kv_heads, head_dim, qs, ks,
+                           _p(positions), pos0, theta, rope_type, _p(err), _sp(stream)),
+          "mlk_rope_f32")
+
+
+def gather_f32(table, vocab, dim, ids, n_tokens, out, token=0, err=None, stream=None):
+    check(lib.mlk_gather_f32(_p(table), vocab, dim, _p(ids), token, n_tokens, _p(out), _p(err),
+                             _sp(stream)), "mlk_gather_f32")
+
+
+def gather_quant(qtype, blocks, vocab, dim, ids, n_tokens, out, token=0, err=None, stream=None):
+    check(lib.mlk_gather_quant(QUANT[qtype], _p(blocks), vocab, dim, _p(ids), token, n_tokens,
+                               _p(out), _p(err), _sp(stream)), "mlk_gather_quant")
+
+
+def quantize(qtype, x, rows, cols, blocks, stream=None):
+    check(lib.mlk_quantize(QUANT[qtype], _p(x), rows, cols, _p(blocks), _sp(stream)),
+          "mlk_quantize")
+
+
+def quant_bytes(qtype, rows, cols):
+    return int(lib.mlk_quant_bytes(QUANT[qtype], rows, cols))
+
+
+def fill_normal(x, n, mean=0.0, std=1.0, seed=0, stream=None):
+    check(lib.mlk_fill_normal_f32(_p(x), n, mean, std, seed, _sp(stream)), "mlk_fill_normal_f32")

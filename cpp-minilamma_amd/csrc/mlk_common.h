@@ -1,0 +1,118 @@
+// mlk_common.h -- shared host/device helpers for the gfx950 kernels.
+//
+// Every .hip file of libminilamma_hip.so includes this header.  It holds the
+// thread-local error message behind mlk_last_error(), the launch-check
+// helper, per-device properties used to size grids, and the wave64 / block
+// reductions the row kernels share.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+
+#include "minilamma_hip.h"
+
+namespace mlk {
+
+constexpr int kWave = 64;  // CDNA wavefront width
+
+// ---------------------------------------------------------------- errors
+
+// Records a printf-style message for mlk_last_error() and returns `status`.
+mlk_status Fail(mlk_status status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Turns a HIP error into MLK_ERR_HIP with "<what>: <hip message>".
+mlk_status FromHip(hipError_t err, const char* what);
+
+// Checks the launch that was just issued.
+inline mlk_status CheckLaunch(const char* kernel) {
+    const hipError_t err = hipGetLastError();
+    return err == hipSuccess ? MLK_OK : FromHip(err, kernel);
+}
+
+inline hipStream_t AsStream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool Aligned(const void* p, uintptr_t n) {
+    return (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0;
+}
+
+// Compute units of the current device (cached per device id).
+int ComputeUnits();
+
+// Grid size for a grid-stride kernel: enough workgroups to cover `work`
+// units of `per_block` each, capped at `waves_per_cu` resident workgroups
+// per compute unit.
+inline unsigned GridFor(int64_t work, int64_t per_block, int blocks_per_cu) {
+    const int64_t need = (work + per_block - 1) / per_block;
+    const int64_t cap = static_cast<int64_t>(ComputeUnits()) * blocks_per_cu;
+    const int64_t g = need < cap ? need : cap;
+    return static_cast<unsigned>(g < 1 ? 1 : g);
+}
+
+// ------------------------------------------------------------ reductions
+
+// Sum over the 64 lanes of a wave; every lane receives the total.  The
+// xor-butterfly gives each lane the same association order, so the result
+// is identical on all lanes and from run to run.
+__device__ inline double WaveSum(double v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        v += __shfl_xor(v, off, kWave);
+    }
+    return v;
+}
+
+__device__ inline float WaveMax(float v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        v = fmaxf(v, __shfl_xor(v, off, kWave));
+    }
+    return v;
+}
+
+// Block-wide sum for blocks of NW waves.  `scratch` holds NW doubles and must
+// not be reused by the caller before the next __syncthreads().  Every thread
+// returns the same value, summed in wave order.
+template <int NW>
+__device__ inline double BlockSum(double v, double* scratch) {
+    v = WaveSum(v);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x % kWave) == 0) {
+        scratch[wave] = v;
+    }
+    __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        total += scratch[i];
+    }
+    return total;
+}
+
+template <int NW>
+__device__ inline float BlockMax(float v, float* scratch) {
+    v = WaveMax(v);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x % kWave) == 0) {
+        scratch[wave] = v;
+    }
+    __syncthreads();
+    float m = scratch[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) {
+        m = fmaxf(m, scratch[i]);
+    }
+    return m;
+}
+
+// Raises a device-side error flag (the flag is only ever set, never read
+// back here, so any nonzero store is enough).
+__device__ inline void RaiseFlag(int32_t* err, int32_t code) {
+    if (err != nullptr) {
+        atomicOr(err, code);
+    }
+}
+
+}  // namespace mlk

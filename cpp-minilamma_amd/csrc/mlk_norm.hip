@@ -1,0 +1,204 @@
+// mlk_norm.hip -- residual add fused with RMSNorm, and plain RMSNorm, over
+// [n_rows, dim] fp32 rows.
+//
+// Semantics follow the CPU ops the reference checks its GPU path against:
+// ForwardAdd (src/forward.cc:213-222) then RmsNorm (src/ops.cc:82-112):
+//   r   = x + delta                          (fp32, written back in place)
+//   ss  = sum((double) r_i^2)
+//   y_i = (float)((double) r_i * (double) w_i * (1 / sqrt(ss / dim + eps)))
+// The reference's device path (src/cuda_ops.cu:151-164, :335-355) used three
+// launches, one float atomicAdd per element into a single address and a
+// stream synchronize; here one workgroup owns one row, keeps it in
+// registers between the reduction and the scaling, and reduces with wave64
+// shuffles plus one LDS exchange across the four waves.  The float64
+// arithmetic is free at this arithmetic intensity (the kernel is HBM bound)
+// and makes y equal the CPU result except for the order of the sum.
+//
+// HBM bytes per row (fused): read x, delta (8*dim), write x', y (8*dim);
+// w (4*dim) is shared by all rows and stays in L2.
+#include "mlk_common.h"
+
+#include <cmath>
+
+namespace mlk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+
+// Vector path: dim % 4 == 0 and dim <= kThreads * 4 * VPT.  Each thread
+// holds VPT float4 of the row in registers.
+template <int VPT, bool kDelta, bool kWriteBack>
+__global__ __launch_bounds__(kThreads) void AddRmsNormVec(float* residual,
+                                                          const float* __restrict__ delta,
+                                                          const float* __restrict__ weight,
+                                                          float* y, int64_t n_rows,
+                                                          int64_t dim, float eps) {
+#pragma clang fp contract(off)
+    __shared__ double partial[2][kWaves];
+    const int tid = threadIdx.x;
+    const int64_t dim4 = dim >> 2;
+    const double inv_dim = 1.0 / static_cast<double>(dim);
+    int parity = 0;
+    for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x, parity ^= 1) {
+        float4* xr = reinterpret_cast<float4*>(residual + row * dim);
+        const float4* dr = reinterpret_cast<const float4*>(delta + (kDelta ? row * dim : 0));
+        float4 r[VPT];
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+            const int64_t i = tid + static_cast<int64_t>(v) * kThreads;
+            r[v] = i < dim4 ? xr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (kDelta) {
+#pragma unroll
+            for (int v = 0; v < VPT; ++v) {
+                const int64_t i = tid + static_cast<int64_t>(v) * kThreads;
+                if (i < dim4) {
+                    const float4 d = dr[i];
+                    r[v].x += d.x;
+                    r[v].y += d.y;
+                    r[v].z += d.z;
+                    r[v].w += d.w;
+                }
+            }
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+            const int64_t i = tid + static_cast<int64_t>(v) * kThreads;
+            if (i < dim4) {
+                if (kWriteBack) xr[i] = r[v];
+                const double a = r[v].x, b = r[v].y, c = r[v].z, d = r[v].w;
+                ss += a * a;
+                ss += b * b;
+                ss += c * c;
+                ss += d * d;
+            }
+        }
+        ss = BlockSum<kWaves>(ss, partial[parity]);
+        const double scale = 1.0 / sqrt(ss * inv_dim + static_cast<double>(eps));
+        const float4* wr = reinterpret_cast<const float4*>(weight);
+        float4* yr = reinterpret_cast<float4*>(y + row * dim);
+#pragma unroll
+        for (int v = 0; v < VPT; ++v) {
+            const int64_t i = tid + static_cast<int64_t>(v) * kThreads;
+            if (i < dim4) {
+                const float4 w = wr[i];
+                float4 o;
+                o.x = static_cast<float>(static_cast<double>(r[v].x) * static_cast<double>(w.x) * scale);
+                o.y = static_cast<float>(static_cast<double>(r[v].y) * static_cast<double>(w.y) * scale);
+                o.z = static_cast<float>(static_cast<double>(r[v].z) * static_cast<double>(w.z) * scale);
+                o.w = static_cast<float>(static_cast<double>(r[v].w) * static_cast<double>(w.w) * scale);
+                yr[i] = o;
+            }
+        }
+    }
+}
+
+// Any width: two passes over the row, the second re-reading the elements
+// the same thread wrote in the first.
+template <bool kDelta, bool kWriteBack>
+__global__ __launch_bounds__(kThreads) void AddRmsNormAny(float* residual,
+                                                          const float* __restrict__ delta,
+                                                          const float* __restrict__ weight,
+                                                          float* y, int64_t n_rows, int64_t dim,
+                                                          float eps) {
+#pragma clang fp contract(off)
+    __shared__ double partial[2][kWaves];
+    const double inv_dim = 1.0 / static_cast<double>(dim);
+    int parity = 0;
+    for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x, parity ^= 1) {
+        float* xr = residual + row * dim;
+        double ss = 0.0;
+        for (int64_t i = threadIdx.x; i < dim; i += kThreads) {
+            float r = xr[i];
+            if (kDelta) r += delta[row * dim + i];
+            if (kWriteBack) xr[i] = r;
+            const double a = r;
+            ss += a * a;
+        }
+        ss = BlockSum<kWaves>(ss, partial[parity]);
+        const double scale = 1.0 / sqrt(ss * inv_dim + static_cast<double>(eps));
+        for (int64_t i = threadIdx.x; i < dim; i += kThreads) {
+            float r = xr[i];
+            if (kDelta && !kWriteBack) r += delta[row * dim + i];
+            y[row * dim + i] =
+                static_cast<float>(static_cast<double>(r) * static_cast<double>(weight[i]) * scale);
+        }
+    }
+}
+
+template <bool kDelta, bool kWriteBack>
+mlk_status Launch(float* residual, const float* delta, const float* weight, float* y,
+                  int64_t n_rows, int64_t dim, float eps, hipStream_t stream) {
+    const unsigned grid = GridFor(n_rows, 1, 8);
+    const bool vec = (dim % 4) == 0 && Aligned(residual, 16) && Aligned(weight, 16) &&
+                     Aligned(y, 16) && (!kDelta || Aligned(delta, 16));
+    const int64_t per_thread = (dim / 4 + kThreads - 1) / kThreads;  // float4 per thread
+    if (vec && per_thread <= 16) {
+#define MLK_NORM_CASE(V)                                                                      \
+    if (per_thread <= V) {                                                                    \
+        hipLaunchKernelGGL((AddRmsNormVec<V, kDelta, kWriteBack>), dim3(grid), dim3(kThreads), \
+                           0, stream, residual, delta, weight, y, n_rows, dim, eps);          \
+        return CheckLaunch("AddRmsNormVec");                                                  \
+    }
+        MLK_NORM_CASE(1)
+        MLK_NORM_CASE(2)
+        MLK_NORM_CASE(4)
+        MLK_NORM_CASE(8)
+        MLK_NORM_CASE(16)
+#undef MLK_NORM_CASE
+    }
+    hipLaunchKernelGGL((AddRmsNormAny<kDelta, kWriteBack>), dim3(grid), dim3(kThreads), 0,
+                       stream, residual, delta, weight, y, n_rows, dim, eps);
+    return CheckLaunch("AddRmsNormAny");
+}
+
+mlk_status CheckNormArgs(const char* caller, const void* x, const void* weight, const void* y,
+                         int64_t n_rows, int64_t dim, float eps) {
+    if (x == nullptr || weight == nullptr || y == nullptr) {
+        return Fail(MLK_ERR_INVALID, "%s: input, weight and output pointers must not be null",
+                    caller);
+    }
+    if (n_rows <= 0 || dim <= 0) {
+        return Fail(MLK_ERR_INVALID, "%s: rows and dim must be positive (got %lld x %lld)", caller,
+                    static_cast<long long>(n_rows), static_cast<long long>(dim));
+    }
+    if (!std::isfinite(eps) || eps <= 0.0f) {
+        return Fail(MLK_ERR_INVALID, "%s: eps must be finite and positive", caller);
+    }
+    return MLK_OK;
+}
+
+}  // namespace
+}  // namespace mlk
+
+using namespace mlk;
+
+extern "C" {
+
+mlk_status mlk_add_rmsnorm_f32(float* residual, const float* delta, const float* weight,
+                               float* y, int64_t n_rows, int64_t dim, float eps, void* stream) {
+    const mlk_status st =
+        CheckNormArgs("mlk_add_rmsnorm_f32", residual, weight, y, n_rows, dim, eps);
+    if (st != MLK_OK) return st;
+    if (delta == nullptr) {
+        return Launch<false, false>(residual, nullptr, weight, y, n_rows, dim, eps,
+                                    AsStream(stream));
+    }
+    if (y == residual || y == delta) {
+        return Fail(MLK_ERR_INVALID, "mlk_add_rmsnorm_f32: output must not alias the residual");
+    }
+    return Launch<true, true>(residual, delta, weight, y, n_rows, dim, eps, AsStream(stream));
+}
+
+mlk_status mlk_rmsnorm_f32(const float* x, const float* weight, float* y, int64_t n_rows,
+                           int64_t dim, float eps, void* stream) {
+    const mlk_status st = CheckNormArgs("mlk_rmsnorm_f32", x, weight, y, n_rows, dim, eps);
+    if (st != MLK_OK) return st;
+    // x is only read (kWriteBack = false), so casting away const is safe.
+    return Launch<false, false>(const_cast<float*>(x), nullptr, weight, y, n_rows, dim, eps,
+                                AsStream(stream));
+}
+
+}  // extern "C"

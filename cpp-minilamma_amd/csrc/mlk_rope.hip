@@ -1,0 +1,251 @@
+// mlk_rope.hip -- rotary position embedding, in place, on Q and K of a batch
+// of tokens with per-token positions.
+//
+// Semantics of Rope (src/ops.cc:177-224): for pair i < head_dim / 2,
+//   angle = (double) pos * pow((double) theta, -2.0 * i / head_dim)
+//   (x0, x1) <- ((float)(x0 c - x1 s), (float)(x0 s + x1 c)),  c, s in double
+// Normal pairs (2i, 2i+1); NeoX pairs (i, i + head_dim/2).  The reference's
+// device kernel (src/cuda_ops.cu:254-299) used fp32 powf/cosf/sinf, whose
+// angle drifts from the double one by ~4e-4 rad at pos 8191 (theta 5e5);
+// here the angle, cos and sin are float64, so the result equals the CPU's.
+//
+// Work layout: a workgroup takes whole tokens (grid-stride).  Its threads
+// form `rows` rows of `lanes` lanes; a lane owns PV consecutive pairs of
+// every head, so its inverse frequencies are computed once per kernel and
+// its cos/sin once per token, then reused across all n_heads + n_kv_heads
+// heads that its row visits.  Q and K are one launch (the reference made
+// two per token).  Each row first loads up to kBatch heads, then rotates
+// and stores them, so several 16-byte loads are in flight per lane.
+//
+// HBM bytes per token: 8 * (n_heads + n_kv_heads) * head_dim (read + write).
+#include "mlk_common.h"
+
+#include <climits>
+#include <cmath>
+
+namespace mlk {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBatch = 8;
+
+template <int PV, bool kNeoX>
+struct Pairs;
+
+// Normal layout, two pairs per lane: one float4 at element 4g.
+template <>
+struct Pairs<2, false> {
+    float4 v;
+    __device__ void Load(const float* head, int g, int) {
+        v = reinterpret_cast<const float4*>(head)[g];
+    }
+    __device__ void Rotate(const double* c, const double* s) {
+        const double a0 = v.x, a1 = v.y, b0 = v.z, b1 = v.w;
+        v.x = static_cast<float>(a0 * c[0] - a1 * s[0]);
+        v.y = static_cast<float>(a0 * s[0] + a1 * c[0]);
+        v.z = static_cast<float>(b0 * c[1] - b1 * s[1]);
+        v.w = static_cast<float>(b0 * s[1] + b1 * c[1]);
+    }
+    __device__ void Store(float* head, int g, int) const {
+        reinterpret_cast<float4*>(head)[g] = v;
+    }
+};
+
+// Normal layout, one pair per lane.
+template <>
+struct Pairs<1, false> {
+    float x0, x1;
+    __device__ void Load(const float* head, int g, int) {
+        x0 = head[2 * g];
+        x1 = head[2 * g + 1];
+    }
+    __device__ void Rotate(const double* c, const double* s) {
+        const double a0 = x0, a1 = x1;
+        x0 = static_cast<float>(a0 * c[0] - a1 * s[0]);
+        x1 = static_cast<float>(a0 * s[0] + a1 * c[0]);
+    }
+    __device__ void Store(float* head, int g, int) const {
+        head[2 * g] = x0;
+        head[2 * g + 1] = x1;
+    }
+};
+
+// NeoX layout, two pairs per lane: float2 at 2g and at half + 2g.
+template <>
+struct Pairs<2, true> {
+    float2 lo, hi;
+    __device__ void Load(const float* head, int g, int half) {
+        lo = reinterpret_cast<const float2*>(head)[g];
+        hi = reinterpret_cast<const float2*>(head + half)[g];
+    }
+    __device__ void Rotate(const double* c, const double* s) {
+        const double a0 = lo.x, a1 = hi.x, b0 = lo.y, b1 = hi.y;
+        lo.x = static_cast<float>(a0 * c[0] - a1 * s[0]);
+        hi.x = static_cast<float>(a0 * s[0] + a1 * c[0]);
+        lo.y = static_cast<float>(b0 * c[1] - b1 * s[1]);
+        hi.y = static_cast<float>(b0 * s[1] + b1 * c[1]);
+    }
+    __device__ void Store(float* head, int g, int half) const {
+        reinterpret_cast<float2*>(head)[g] = lo;
+        reinterpret_cast<float2*>(head + half)[g] = hi;
+    }
+};
+
+// NeoX layout, one pair per lane.
+template <>
+struct Pairs<1, true> {
+    float x0, x1;
+    __device__ void Load(const float* head, int g, int half) {
+        x0 = head[g];
+        x1 = head[g + half];
+    }
+    __device__ void Rotate(const double* c, const double* s) {
+        const double a0 = x0, a1 = x1;
+        x0 = static_cast<float>(a0 * c[0] - a1 * s[0]);
+        x1 = static_cast<float>(a0 * s[0] + a1 * c[0]);
+    }
+    __device__ void Store(float* head, int g, int half) const {
+        head[g] = x0;
+        head[g + half] = x1;
+    }
+};
+
+template <int PV, bool kNeoX>
+__global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64_t n_tokens,
+                                                       int n_heads, int n_kv_heads, int head_dim,
+                                                       int64_t q_stride, int64_t k_stride,
+                                                       const int32_t* positions, int32_t pos0,
+                                                       float theta, int32_t* err, int lanes,
+                                                       int rows) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x;
+    const int lane = tid % lanes;
+    const int row = tid / lanes;
+    if (row >= rows) {
+        return;  // spare threads when kThreads is not a multiple of lanes
+    }
+    const int half = head_dim / 2;
+    const int groups = half / PV;
+    const int heads = n_heads + n_kv_heads;
+    for (int g = lane; g < groups; g += lanes) {
+        double inv_freq[PV];
+#pragma unroll
+        for (int p = 0; p < PV; ++p) {
+            const int i = g * PV + p;
+            inv_freq[p] = pow(static_cast<double>(theta), -2.0 * i / head_dim);
+        }
+        for (int64_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
+            const int32_t pos = positions != nullptr ? positions[t] : pos0 + static_cast<int32_t>(t);
+            if (pos < 0) {
+                if (tid == 0 && g == 0) RaiseFlag(err, 1);
+                continue;
+            }
+            double c[PV], s[PV];
+#pragma unroll
+            for (int p = 0; p < PV; ++p) {
+                sincos(static_cast<double>(pos) * inv_freq[p], &s[p], &c[p]);
+            }
+            float* qt = q + t * q_stride;
+            float* kt = k + t * k_stride;
+            for (int h0 = row; h0 < heads; h0 += rows * kBatch) {
+                Pairs<PV, kNeoX> v[kBatch];
+#pragma unroll
+                for (int b = 0; b < kBatch; ++b) {
+                    const int h = h0 + b * rows;
+                    if (h < heads) {
+                        const float* base = h < n_heads
+                                                ? qt + static_cast<int64_t>(h) * head_dim
+                                                : kt + static_cast<int64_t>(h - n_heads) * head_dim;
+                        v[b].Load(base, g, half);
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < kBatch; ++b) {
+                    const int h = h0 + b * rows;
+                    if (h < heads) {
+                        float* base = h < n_heads ? qt + static_cast<int64_t>(h) * head_dim
+                                                  : kt + static_cast<int64_t>(h - n_heads) * head_dim;
+                        v[b].Rotate(c, s);
+                        v[b].Store(base, g, half);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int PV, bool kNeoX>
+mlk_status LaunchRope(float* q, float* k, int64_t n_tokens, int n_heads, int n_kv_heads,
+                      int head_dim, int64_t qs, int64_t ks, const int32_t* positions,
+                      int32_t pos0, float theta, int32_t* err, hipStream_t stream) {
+    const int groups = head_dim / 2 / PV;
+    const int lanes = groups < kThreads ? groups : kThreads;
+    const int rows = kThreads / lanes;
+    const unsigned grid = GridFor(n_tokens, 1, 8);
+    hipLaunchKernelGGL((RopeKernel<PV, kNeoX>), dim3(grid), dim3(kThreads), 0, stream, q, k,
+                       n_tokens, n_heads, n_kv_heads, head_dim, qs, ks, positions, pos0, theta,
+                       err, lanes, rows);
+    return CheckLaunch("RopeKernel");
+}
+
+}  // namespace
+}  // namespace mlk
+
+using namespace mlk;
+
+extern "C" {
+
+mlk_status mlk_rope_f32(float* q, float* k, int64_t n_tokens, int32_t n_heads,
+                        int32_t n_kv_heads, int32_t head_dim, int64_t q_row_stride,
+                        int64_t k_row_stride, const int32_t* positions, int32_t pos0,
+                        float theta, int32_t rope_type, int32_t* err, void* stream) {
+    const char* caller = "mlk_rope_f32";
+    if (q == nullptr || k == nullptr) {
+        return Fail(MLK_ERR_INVALID, "%s: q and k pointers must not be null", caller);
+    }
+    if (n_tokens < 0) {
+        return Fail(MLK_ERR_INVALID, "%s: n_tokens must not be negative", caller);
+    }
+    if (n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || head_dim % 2 != 0) {
+        return Fail(MLK_ERR_INVALID,
+                    "%s: head counts must be positive and head_dim must be positive and even",
+                    caller);
+    }
+    if (!std::isfinite(theta) || theta <= 0.0f) {
+        return Fail(MLK_ERR_INVALID, "%s: theta must be finite and positive", caller);
+    }
+    if (rope_type != MLK_ROPE_NORMAL && rope_type != MLK_ROPE_NEOX) {
+        return Fail(MLK_ERR_INVALID, "%s: unknown rope type %d", caller, rope_type);
+    }
+    const int64_t q_width = static_cast<int64_t>(n_heads) * head_dim;
+    const int64_t k_width = static_cast<int64_t>(n_kv_heads) * head_dim;
+    if (q_row_stride < q_width || k_row_stride < k_width) {
+        return Fail(MLK_ERR_INVALID, "%s: row strides must cover n_heads * head_dim", caller);
+    }
+    if (positions == nullptr) {
+        if (pos0 < 0) return Fail(MLK_ERR_RANGE, "%s: pos must be non-negative", caller);
+        if (n_tokens > 0 && static_cast<int64_t>(pos0) + n_tokens - 1 > INT32_MAX) {
+            return Fail(MLK_ERR_RANGE, "%s: positions exceed the int32 range", caller);
+        }
+    }
+    if (n_tokens == 0) return MLK_OK;
+    const hipStream_t s = AsStream(stream);
+    const bool neox = rope_type == MLK_ROPE_NEOX;
+    const bool two = head_dim % 4 == 0;
+    if (!neox) {
+        const bool v4 = two && Aligned(q, 16) && Aligned(k, 16) && q_row_stride % 4 == 0 &&
+                        k_row_stride % 4 == 0;
+        return v4 ? LaunchRope<2, false>(q, k, n_tokens, n_heads, n_kv_heads, head_dim,
+                                         q_row_stride, k_row_stride, positions, pos0, theta, err, s)
+                  : LaunchRope<1, false>(q, k, n_tokens, n_heads, n_kv_heads, head_dim,
+                                         q_row_stride, k_row_stride, positions, pos0, theta, err, s);
+    }
+    const bool v2 = two && Aligned(q, 8) && Aligned(k, 8) && q_row_stride % 2 == 0 &&
+                    k_row_stride % 2 == 0;
+    return v2 ? LaunchRope<2, true>(q, k, n_tokens, n_heads, n_kv_heads, head_dim, q_row_stride,
+                                    k_row_stride, positions, pos0, theta, err, s)
+              : LaunchRope<1, true>(q, k, n_tokens, n_heads, n_kv_heads, head_dim, q_row_stride,
+                                    k_row_stride, positions, pos0, theta, err, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,197 @@
+/*
+ * minilamma_hip.h -- C ABI of libminilamma_hip.so, the MI355X (gfx950) kernels
+ * for cpp-minilamma's per-layer memory-bound ops.
+ *
+ * This is the only interface the HIP translation units export.  The C++17
+ * op surface (include/cuda_ops.h, libminilamma_ops.so) and the Python
+ * binding (cpp-minilamma_amd/__init__.py) sit on top of it.
+ *
+ * Conventions
+ *   - every data pointer is a borrowed device pointer unless the name says
+ *     "host"; the library never frees or keeps what it is handed;
+ *   - sizes are int64_t, token ids and positions are int32_t;
+ *   - `stream` is an opaque hipStream_t; NULL is the null stream;
+ *   - kernels are asynchronous on `stream`; nothing synchronizes unless the
+ *     entry point says so;
+ *   - every entry returns an mlk_status; 0 is success, and
+ *     mlk_last_error() gives a message for the calling thread's last failure;
+ *   - validation happens before any launch, so a rejected call changes no
+ *     memory; nothing throws or allocates device memory across this ABI
+ *     except mlk_malloc.
+ *
+ * Reference interfaces replaced (paths are under the reference tree):
+ *   include/cuda_ops.h:11-33        -> the op entries below (one-token
+ *                                      signatures become n_tokens = 1)
+ *   include/cuda_runtime.h:8-42     -> the runtime entries at the end
+ */
+#ifndef MINILAMMA_HIP_H
+#define MINILAMMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    MLK_OK = 0,
+    MLK_ERR_INVALID = 1,     /* bad pointer, shape, eps, theta, position ... */
+    MLK_ERR_RANGE = 2,       /* a token id / position outside its range */
+    MLK_ERR_HIP = 3,         /* the HIP runtime reported an error */
+    MLK_ERR_NO_DEVICE = 4,   /* no usable GPU */
+} mlk_status;
+
+typedef enum { MLK_ROPE_NORMAL = 0, MLK_ROPE_NEOX = 1 } mlk_rope_type; /* include/model.h:37-40 */
+
+typedef enum { MLK_Q8_0 = 0, MLK_Q4_0 = 1, MLK_Q4_1 = 2 } mlk_quant_type;
+
+/* Thread-local message for the last failed call on this thread. */
+const char* mlk_last_error(void);
+/* Static text for a status code. */
+const char* mlk_status_string(int status);
+/* Version of this ABI (bumped on any signature change). */
+int mlk_abi_version(void);
+
+/* ------------------------------------------------------------------ ops */
+
+/*
+ * Residual add fused with RMSNorm over n_rows rows of width dim.
+ *   residual[r] <- residual[r] + delta[r]            (when delta != NULL)
+ *   y[r]        <- residual[r] * weight * 1/sqrt(mean(residual[r]^2) + eps)
+ * The mean of squares, the scale and the per-element product are evaluated
+ * in float64 and the product is rounded once to float, as the CPU RmsNorm
+ * does.  eps must be finite and > 0.  y may not alias residual or delta.
+ * Replaces CudaElementAddDevice + CudaRmsNromDevice (include/cuda_ops.h:16,
+ * :25; src/cuda_ops.cu:335-355, :432-435), which ran as three kernels.
+ */
+mlk_status mlk_add_rmsnorm_f32(float* residual, const float* delta, const float* weight,
+                               float* y, int64_t n_rows, int64_t dim, float eps, void* stream);
+
+/* Plain RMSNorm of x into y (x read-only).  include/cuda_ops.h:15-16. */
+mlk_status mlk_rmsnorm_f32(const float* x, const float* weight, float* y, int64_t n_rows,
+                           int64_t dim, float eps, void* stream);
+
+/* y = silu(gate) * up over n elements, silu(g) = g * (1 / (1 + exp(-g))).
+ * Replaces CudaSiluDevice + CudaElementwiseMulDevice (include/cuda_ops.h:
+ * 19-23, two kernels and an HBM round trip of silu(gate)). */
+mlk_status mlk_swiglu_f32(const float* gate, const float* up, float* y, int64_t n,
+                          void* stream);
+/* y = silu(x).  include/cuda_ops.h:19-20. */
+mlk_status mlk_silu_f32(const float* x, float* y, int64_t n, void* stream);
+/* y = a * b.  include/cuda_ops.h:22-23. */
+mlk_status mlk_mul_f32(const float* a, const float* b, float* y, int64_t n, void* stream);
+/* y = a + b (residual or bias add).  include/cuda_ops.h:25-27. */
+mlk_status mlk_add_f32(const float* a, const float* b, float* y, int64_t n, void* stream);
+
+/* Softmax of each of n_rows rows of width n (max-subtracted, then
+ * normalised).  include/cuda_ops.h:29 (one row there). */
+mlk_status mlk_softmax_f32(const float* x, float* y, int64_t n_rows, int64_t n, void* stream);
+
+/*
+ * Rotary position embedding, in place, on q [n_tokens, n_heads, head_dim]
+ * and k [n_tokens, n_kv_heads, head_dim]; row t of q starts at
+ * q + t * q_row_stride (likewise k), so q and k may be column slices of a
+ * fused QKV activation.  Token t is at position positions[t] (device array)
+ * or, when positions is NULL, at pos0 + t.  For pair i < head_dim/2 the angle
+ * is pos * theta^(-2i/head_dim), computed with cos and sin in float64 and the
+ * rotation rounded once to float (src/ops.cc:177-224).  Normal rotates
+ * (2i, 2i+1), NeoX rotates (i, i + head_dim/2).  A negative entry of
+ * `positions` leaves that token unrotated and, when err != NULL, stores a
+ * nonzero value in *err (the caller clears it).
+ * Replaces CudaRopeDevice (include/cuda_ops.h:32-33, two launches per token).
+ */
+mlk_status mlk_rope_f32(float* q, float* k, int64_t n_tokens, int32_t n_heads,
+                        int32_t n_kv_heads, int32_t head_dim, int64_t q_row_stride,
+                        int64_t k_row_stride, const int32_t* positions, int32_t pos0,
+                        float theta, int32_t rope_type, int32_t* err, void* stream);
+
+/*
+ * Token-embedding gather from an F32 table [vocab, dim]:
+ *   out[t, :] = table[ids[t], :]   (bit-exact row copy)
+ * ids is a device array of n_tokens ids; when ids is NULL the single host
+ * id `token` is used (n_tokens must be 1), which is the reference's
+ * one-token signature.  An id outside [0, vocab) writes a zero row and, when
+ * err != NULL, a nonzero value to *err.
+ * Replaces CudaEmbeddingDevice (include/cuda_ops.h:13).
+ */
+mlk_status mlk_gather_f32(const float* table, int64_t vocab, int64_t dim, const int32_t* ids,
+                          int32_t token, int64_t n_tokens, float* out, int32_t* err,
+                          void* stream);
+
+/*
+ * Token-embedding gather from a block-quantized table, dequantizing only the
+ * gathered rows.  The table is vocab rows of ceil(dim/32) packed blocks
+ * (Q8_0 34 B, Q4_0 18 B, Q4_1 20 B, little-endian fp16 scales, low nibble =
+ * first 16 elements), exactly the layout TensorToQ80/Q40/Q41 produce
+ * (src/quant.cc:136-331).  Outputs equal Q80ToTensor/Q40ToTensor/Q41ToTensor
+ * (src/quant.cc:175-368) of those rows bit for bit.  ids/token/err as in
+ * mlk_gather_f32.  No reference counterpart on the device: the reference
+ * dequantizes the whole table on the host at load (src/gguf_load.cc:370-404).
+ */
+mlk_status mlk_gather_quant(int32_t quant_type, const void* blocks, int64_t vocab, int64_t dim,
+                            const int32_t* ids, int32_t token, int64_t n_tokens, float* out,
+                            int32_t* err, void* stream);
+
+/* Block quantizer on the device: x [rows, cols] -> packed blocks, bit-identical
+ * to TensorToQ80/Q40/Q41 (src/quant.cc:136-331), tail blocks zero padded. */
+mlk_status mlk_quantize(int32_t quant_type, const float* x, int64_t rows, int64_t cols,
+                        void* blocks, void* stream);
+/* Bytes of the packed blocks of a [rows, cols] matrix (0 on bad input). */
+int64_t mlk_quant_bytes(int32_t quant_type, int64_t rows, int64_t cols);
+
+/* Synthetic-input helper (not a reference op): fills x[i] with
+ * mean + std * N(0,1) from a counter-based generator keyed by seed and i, so
+ * the values do not depend on launch shape. */
+mlk_status mlk_fill_normal_f32(float* x, int64_t n, float mean, float std, uint64_t seed,
+                               void* stream);
+
+/* -------------------------------------------------------------- runtime
+ * A thin layer over the HIP runtime for hosts that do not link HIP
+ * themselves (the C++ op surface, ctypes).  Replaces the cudart calls of
+ * src/cuda_runtime.cc:57-161. */
+
+typedef enum { MLK_H2D = 0, MLK_D2D = 1, MLK_D2H = 2 } mlk_copy_kind;
+
+typedef struct {
+    int device_id;
+    char name[256];
+    char arch[64];          /* gcnArchName, e.g. gfx950:sramecc+:xnack- */
+    int compute_major;
+    int compute_minor;
+    size_t total_bytes;
+    int multiprocessors;    /* compute units */
+    int clock_khz;
+    int memory_clock_khz;
+    int memory_bus_bits;
+    int runtime_version;
+    int driver_version;
+} mlk_device_info;
+
+mlk_status mlk_device_count(int* count);
+mlk_status mlk_set_device(int device_id);
+mlk_status mlk_get_device(int* device_id);
+mlk_status mlk_get_device_info(int device_id, mlk_device_info* info);
+mlk_status mlk_malloc(void** ptr, size_t bytes);
+mlk_status mlk_free(void* ptr);
+/* Synchronous copy (hipMemcpy semantics). */
+mlk_status mlk_memcpy(void* dst, const void* src, size_t bytes, int32_t kind);
+mlk_status mlk_memcpy_async(void* dst, const void* src, size_t bytes, int32_t kind,
+                            void* stream);
+/* Fills bytes with zero through a kernel (safe under graph capture). */
+mlk_status mlk_zero_async(void* dst, size_t bytes, void* stream);
+mlk_status mlk_device_synchronize(void);
+mlk_status mlk_stream_create(void** stream);
+mlk_status mlk_stream_destroy(void* stream);
+mlk_status mlk_stream_synchronize(void* stream);
+mlk_status mlk_event_create(void** event);
+mlk_status mlk_event_destroy(void* event);
+mlk_status mlk_event_record(void* event, void* stream);
+mlk_status mlk_event_synchronize(void* event);
+mlk_status mlk_event_elapsed_ms(float* ms, void* start, void* stop);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

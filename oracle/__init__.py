@@ -1,0 +1,302 @@
+"""ctypes bindings for the CPU oracle (liboracle.so) and the compiled reference
+(oracle/_ref/libref*.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as
+the checker and by bench.py's cpu_baseline leg.  The product package never
+imports this module.
+
+Arrays are numpy arrays; every wrapper checks dtype and contiguity and raises
+ValueError when the C function reports ORC_EINVAL (the input the reference
+would throw on).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libref.so")
+REF_AVX2_SO = os.path.join(HERE, "_ref", "libref_avx2.so")
+
+QUANT_TYPES = {"q8_0": 0, "q4_0": 1, "q4_1": 2}
+BLOCK_BYTES = {"q8_0": 34, "q4_0": 18, "q4_1": 20}
+ROPE_NORMAL, ROPE_NEOX = 0, 1
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+_i64 = C.c_int64
+_i32 = C.c_int32
+
+
+def _bind(lib, name, restype, argtypes):
+    fn = getattr(lib, name)
+    fn.restype = restype
+    fn.argtypes = argtypes
+    return fn
+
+
+class _Oracle:
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built; run `make -C oracle`")
+        lib = C.CDLL(path)
+        self.lib = lib
+        self.fp16_to_fp32 = _bind(lib, "orc_fp16_to_fp32", C.c_float, [C.c_uint16])
+        self.fp32_to_fp16 = _bind(lib, "orc_fp32_to_fp16", C.c_uint16, [C.c_float])
+        for q in QUANT_TYPES:
+            setattr(self, f"_quantize_{q}",
+                    _bind(lib, f"orc_quantize_{q}", C.c_int, [_f32p, _i64, _i64, _u8p]))
+            setattr(self, f"_dequantize_{q}",
+                    _bind(lib, f"orc_dequantize_{q}", C.c_int, [_u8p, _i64, _i64, _f32p]))
+        self._gather_f32 = _bind(lib, "orc_gather_f32", C.c_int,
+                                 [_f32p, _i64, _i64, _i32p, _i64, _f32p])
+        self._gather_quant = _bind(lib, "orc_gather_quant", C.c_int,
+                                   [C.c_int, _u8p, _i64, _i64, _i32p, _i64, _f32p])
+        for name in ("add", "mul", "swiglu"):
+            setattr(self, f"_{name}", _bind(lib, f"orc_{name}", None, [_f32p, _f32p, _f32p, _i64]))
+        self._silu = _bind(lib, "orc_silu", None, [_f32p, _f32p, _i64])
+        self._softmax = _bind(lib, "orc_softmax", C.c_int, [_f32p, _f32p, _i64])
+        self._rmsnorm_row = _bind(lib, "orc_rmsnorm_row", C.c_int,
+                                  [_f32p, _f32p, _f32p, _i64, C.c_float])
+        self._add_rmsnorm = _bind(lib, "orc_add_rmsnorm", C.c_int,
+                                  [_f32p, C.c_void_p, _f32p, _f32p, _i64, _i64, C.c_float])
+        self._rope = _bind(lib, "orc_rope", C.c_int,
+                           [_f32p, _f32p, _i64, _i32, _i32, _i32, C.c_void_p, _i32,
+                            C.c_float, _i32])
+        self._chain = _bind(lib, "orc_chain", C.c_int,
+                            [_f32p, _i64, _i64, _i32p, _f32p, _f32p, _f32p, _f32p, C.c_float,
+                             _f32p, _f32p, _i32, _i32, _i32, _i32p, C.c_float,
+                             _f32p, _f32p, _f32p, _i64, _i64, C.c_int])
+        self.parallel_threads = _bind(lib, "orc_parallel_threads", C.c_int, [C.c_int])
+
+    # ---- quant -------------------------------------------------------------
+    def quantize(self, qtype, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, cols = (1, x.shape[0]) if x.ndim == 1 else (int(np.prod(x.shape[:-1])), x.shape[-1])
+        nb = (cols + 31) // 32
+        out = np.zeros(rows * nb * BLOCK_BYTES[qtype], dtype=np.uint8)
+        _check(getattr(self, f"_quantize_{qtype}")(x.reshape(-1), rows, cols, out))
+        return out
+
+    def dequantize(self, qtype, blocks, rows, cols):
+        out = np.zeros(rows * cols, dtype=np.float32)
+        _check(getattr(self, f"_dequantize_{qtype}")(_u8(blocks), rows, cols, out))
+        return out.reshape(rows, cols)
+
+    # ---- gather ------------------------------------------------------------
+    def gather_f32(self, table, ids):
+        table = _f32(table)
+        vocab, dim = table.shape
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.zeros((len(ids), dim), dtype=np.float32)
+        _check(self._gather_f32(table.reshape(-1), vocab, dim, ids, len(ids), out.reshape(-1)))
+        return out
+
+    def gather_quant(self, qtype, blocks, vocab, dim, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        out = np.zeros((len(ids), dim), dtype=np.float32)
+        _check(self._gather_quant(QUANT_TYPES[qtype], _u8(blocks), vocab, dim, ids, len(ids),
+                                  out.reshape(-1)))
+        return out
+
+    # ---- elementwise -------------------------------------------------------
+    def _binary(self, fn, a, b):
+        a, b = _f32(a), _f32(b)
+        if a.shape != b.shape:
+            raise ValueError("shapes must match")
+        y = np.empty_like(a)
+        fn(a.reshape(-1), b.reshape(-1), y.reshape(-1), a.size)
+        return y
+
+    def add(self, a, b):
+        return self._binary(self._add, a, b)
+
+    def mul(self, a, b):
+        return self._binary(self._mul, a, b)
+
+    def swiglu(self, gate, up):
+        return self._binary(self._swiglu, gate, up)
+
+    def silu(self, x):
+        x = _f32(x)
+        y = np.empty_like(x)
+        self._silu(x.reshape(-1), y.reshape(-1), x.size)
+        return y
+
+    def softmax(self, x):
+        x = _f32(x)
+        y = np.empty_like(x)
+        _check(self._softmax(x.reshape(-1), y.reshape(-1), x.size))
+        return y
+
+    # ---- rmsnorm -----------------------------------------------------------
+    def rmsnorm(self, x, w, eps):
+        """Row-wise RmsNorm of a [rows, dim] (or [dim]) array."""
+        x = _f32(x)
+        r = x.copy()
+        y = np.empty_like(x)
+        dim = x.shape[-1]
+        _check(self._add_rmsnorm(r.reshape(-1), None, _f32(w), y.reshape(-1), x.size // dim, dim,
+                                 eps))
+        return y
+
+    def add_rmsnorm(self, residual, delta, w, eps):
+        """Returns (residual + delta, RmsNorm(residual + delta)) row-wise."""
+        r = _f32(residual).copy()
+        delta = _f32(delta)
+        y = np.empty_like(r)
+        dim = r.shape[-1]
+        _check(self._add_rmsnorm(r.reshape(-1), delta.ctypes.data, _f32(w), y.reshape(-1),
+                                 r.size // dim, dim, eps))
+        return r, y
+
+    # ---- rope --------------------------------------------------------------
+    def rope(self, q, k, n_heads, n_kv_heads, head_dim, positions=None, pos0=0,
+             theta=10000.0, rope_type=ROPE_NORMAL):
+        """Returns rotated copies of q [T, H*hd] and k [T, KV*hd]."""
+        q = _f32(q).copy()
+        k = _f32(k).copy()
+        n_tokens = q.size // (n_heads * head_dim)
+        pos_arr = None
+        ptr = None
+        if positions is not None:
+            pos_arr = np.ascontiguousarray(positions, dtype=np.int32)
+            ptr = pos_arr.ctypes.data
+        _check(self._rope(q.reshape(-1), k.reshape(-1), n_tokens, n_heads, n_kv_heads, head_dim,
+                          ptr, pos0, theta, rope_type))
+        return q, k
+
+    # ---- CPU baseline ------------------------------------------------------
+    def chain(self, bufs, n_tokens, n_threads):
+        return self._chain(*_chain_args(bufs, n_tokens, n_threads))
+
+
+def _chain_args(b, n_tokens, n_threads):
+    return (b["table"].reshape(-1), b["vocab"], b["dim"], b["ids"], b["x"].reshape(-1),
+            b["delta"].reshape(-1), b["norm_w"], b["y"].reshape(-1), b["eps"],
+            b["q"].reshape(-1), b["k"].reshape(-1), b["n_heads"], b["n_kv_heads"],
+            b["head_dim"], b["positions"], b["theta"], b["gate"].reshape(-1),
+            b["up"].reshape(-1), b["ffn_out"].reshape(-1), b["ffn_dim"], n_tokens, n_threads)
+
+
+class _Reference:
+    """The reference's own CPU code (oracle/_ref), built from its sources."""
+
+    def __init__(self, path=REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (needs the reference tree)")
+        lib = C.CDLL(path)
+        self.path = path
+        self._rmsnorm_row = _bind(lib, "ref_rmsnorm_row", C.c_int,
+                                  [_f32p, _f32p, _f32p, C.c_int, C.c_float])
+        self._rope_token = _bind(lib, "ref_rope_token", C.c_int,
+                                 [_f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
+                                  C.c_int])
+        self._silu = _bind(lib, "ref_silu", C.c_int, [_f32p, _f32p, C.c_int])
+        self._mul = _bind(lib, "ref_mul", C.c_int, [_f32p, _f32p, _f32p, C.c_int])
+        self._swiglu = _bind(lib, "ref_swiglu", C.c_int, [_f32p, _f32p, _f32p, C.c_int])
+        self._softmax = _bind(lib, "ref_softmax", C.c_int, [_f32p, _f32p, C.c_int])
+        self._quantize = _bind(lib, "ref_quantize", C.c_int,
+                               [C.c_int, _f32p, C.c_int, C.c_int, _u8p])
+        self._dequantize = _bind(lib, "ref_dequantize", C.c_int,
+                                 [C.c_int, _u8p, C.c_int, C.c_int, _f32p])
+        self._dequantize_flat = _bind(lib, "ref_dequantize_flat", C.c_int,
+                                      [C.c_int, _u8p, C.c_int, C.c_int, _f32p])
+        self._chain = _bind(lib, "ref_chain", C.c_int,
+                            [_f32p, _i64, _i64, _i32p, _f32p, _f32p, _f32p, _f32p, C.c_float,
+                             _f32p, _f32p, C.c_int, C.c_int, C.c_int, _i32p, C.c_float,
+                             _f32p, _f32p, _f32p, _i64, _i64, C.c_int])
+
+    def rmsnorm_row(self, x, w, eps):
+        x = _f32(x)
+        y = np.empty_like(x)
+        _check(self._rmsnorm_row(x, _f32(w), y, x.size, eps))
+        return y
+
+    def rope_token(self, q, k, n_heads, n_kv_heads, head_dim, pos, theta, rope_type=ROPE_NORMAL):
+        q = _f32(q).copy()
+        k = _f32(k).copy()
+        _check(self._rope_token(q.reshape(-1), k.reshape(-1), n_heads, n_kv_heads, head_dim, pos,
+                                theta, rope_type))
+        return q, k
+
+    def silu(self, x):
+        x = _f32(x)
+        y = np.empty_like(x)
+        _check(self._silu(x.reshape(-1), y.reshape(-1), x.size))
+        return y
+
+    def mul(self, a, b):
+        a, b = _f32(a), _f32(b)
+        y = np.empty_like(a)
+        _check(self._mul(a.reshape(-1), b.reshape(-1), y.reshape(-1), a.size))
+        return y
+
+    def swiglu(self, g, u):
+        g, u = _f32(g), _f32(u)
+        y = np.empty_like(g)
+        _check(self._swiglu(g.reshape(-1), u.reshape(-1), y.reshape(-1), g.size))
+        return y
+
+    def softmax(self, x):
+        x = _f32(x)
+        y = np.empty_like(x)
+        _check(self._softmax(x.reshape(-1), y.reshape(-1), x.size))
+        return y
+
+    def quantize(self, qtype, x):
+        x = _f32(x)
+        rows, cols = (1, x.shape[0]) if x.ndim == 1 else (int(np.prod(x.shape[:-1])), x.shape[-1])
+        out = np.zeros(rows * ((cols + 31) // 32) * BLOCK_BYTES[qtype], dtype=np.uint8)
+        _check(self._quantize(QUANT_TYPES[qtype], x.reshape(-1), rows, cols, out))
+        return out
+
+    def dequantize(self, qtype, blocks, rows, cols, flat=False):
+        out = np.zeros(rows * cols, dtype=np.float32)
+        fn = self._dequantize_flat if flat else self._dequantize
+        _check(fn(QUANT_TYPES[qtype], _u8(blocks), rows, cols, out))
+        return out.reshape(rows, cols)
+
+    def chain(self, bufs, n_tokens, n_threads):
+        return self._chain(*_chain_args(bufs, n_tokens, n_threads))
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8).reshape(-1)
+
+
+def _check(rc):
+    if rc != 0:
+        raise ValueError(f"oracle rejected the input (status {rc})")
+
+
+_oracle = None
+_reference = {}
+
+
+def oracle() -> _Oracle:
+    """The C restatement; raises FileNotFoundError if liboracle.so is missing."""
+    global _oracle
+    if _oracle is None:
+        _oracle = _Oracle()
+    return _oracle
+
+
+def reference(avx2: bool = False) -> _Reference:
+    """The compiled reference; raises FileNotFoundError when it is not built."""
+    path = REF_AVX2_SO if avx2 else REF_SO
+    if path not in _reference:
+        _reference[path] = _Reference(path)
+    return _reference[path]
+
+
+def reference_available(avx2: bool = False) -> bool:
+    return os.path.exists(REF_AVX2_SO if avx2 else REF_SO)

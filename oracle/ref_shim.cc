@@ -1,0 +1,201 @@
+// ref_shim.cc -- C entry points over the reference's own CPU sources.
+//
+// TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together
+// with the reference's src/{tensor,ops,quant,quantiezd_tensor}.cc,
+// matumal/matuml_ops.cc and thread_pool/thread_pool.cc, straight from where
+// they lie under the reference tree, into oracle/_ref/libref*.so.  Tests use
+// it to pin the C restatement (oracle.c) and tests/golden/make_golden.py
+// writes the golden fixtures from it; bench.py times ref_chain as the
+// "reference" CPU baseline.  Nothing here is reference source: it only
+// converts between raw buffers and the reference's Tensor / block types.
+#include "include/ops.h"
+#include "include/quant.h"
+#include "include/quantized_tensor.h"
+#include "include/tensor.h"
+#include "thread_pool/thread_pool.h"
+
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <stdexcept>
+#include <vector>
+
+using yan_lamma::Block_Q40;
+using yan_lamma::Block_Q41;
+using yan_lamma::Block_Q80;
+using yan_lamma::QuanTensor;
+using yan_lamma::QuantType;
+using yan_lamma::RopeType;
+using yan_lamma::Tensor;
+
+namespace {
+
+Tensor Wrap(const float* p, std::vector<int> shape) {
+    Tensor t(shape);
+    std::memcpy(t.data.data(), p, t.data.size() * sizeof(float));
+    return t;
+}
+
+void Unwrap(const Tensor& t, float* out) {
+    std::memcpy(out, t.data.data(), t.data.size() * sizeof(float));
+}
+
+template <typename F>
+int Guard(F&& f) {
+    try {
+        f();
+        return 0;
+    } catch (const std::exception&) {
+        return 1;
+    }
+}
+
+template <typename Block>
+std::vector<Block> ToBlocks(const uint8_t* raw, size_t count) {
+    std::vector<Block> blocks(count);
+    std::memcpy(blocks.data(), raw, count * sizeof(Block));
+    return blocks;
+}
+
+size_t RowBlocks(int cols) { return (static_cast<size_t>(cols) + 31) / 32; }
+
+}  // namespace
+
+extern "C" {
+
+int ref_rmsnorm_row(const float* x, const float* w, float* y, int dim, float eps) {
+    return Guard([&] { Unwrap(yan_lamma::RmsNorm(Wrap(x, {dim}), Wrap(w, {dim}), eps), y); });
+}
+
+int ref_rope_token(float* q, float* k, int n_heads, int n_kv_heads, int head_dim, int pos,
+                   float theta, int rope_type) {
+    return Guard([&] {
+        Tensor tq = Wrap(q, {n_heads, head_dim});
+        Tensor tk = Wrap(k, {n_kv_heads, head_dim});
+        yan_lamma::Rope(tq, tk, pos, theta,
+                        rope_type == 0 ? RopeType::kNormal : RopeType::kNeoX);
+        Unwrap(tq, q);
+        Unwrap(tk, k);
+    });
+}
+
+int ref_silu(const float* x, float* y, int n) {
+    return Guard([&] { Unwrap(yan_lamma::Silu(Wrap(x, {n})), y); });
+}
+
+int ref_mul(const float* a, const float* b, float* y, int n) {
+    return Guard([&] { Unwrap(yan_lamma::ElementwiseMul(Wrap(a, {n}), Wrap(b, {n})), y); });
+}
+
+int ref_swiglu(const float* g, const float* u, float* y, int n) {
+    return Guard([&] { Unwrap(yan_lamma::SwiGlu(Wrap(g, {n}), Wrap(u, {n})), y); });
+}
+
+int ref_softmax(const float* x, float* y, int n) {
+    return Guard([&] { Unwrap(yan_lamma::SoftMax(Wrap(x, {n})), y); });
+}
+
+// Row-wise block quantizers and dequantizers (std::vector<Block> overloads).
+int ref_quantize(int type, const float* x, int rows, int cols, uint8_t* out) {
+    return Guard([&] {
+        const Tensor t = Wrap(x, {rows, cols});
+        if (type == 0) {
+            const auto b = yan_lamma::TensorToQ80(t);
+            std::memcpy(out, b.data(), b.size() * sizeof(Block_Q80));
+        } else if (type == 1) {
+            const auto b = yan_lamma::TensorToQ40(t);
+            std::memcpy(out, b.data(), b.size() * sizeof(Block_Q40));
+        } else {
+            const auto b = yan_lamma::TensorToQ41(t);
+            std::memcpy(out, b.data(), b.size() * sizeof(Block_Q41));
+        }
+    });
+}
+
+int ref_dequantize(int type, const uint8_t* raw, int rows, int cols, float* out) {
+    return Guard([&] {
+        const size_t n = static_cast<size_t>(rows) * RowBlocks(cols);
+        const std::vector<int> shape{rows, cols};
+        if (type == 0) {
+            Unwrap(yan_lamma::Q80ToTensor(ToBlocks<Block_Q80>(raw, n), shape), out);
+        } else if (type == 1) {
+            Unwrap(yan_lamma::Q40ToTensor(ToBlocks<Block_Q40>(raw, n), shape), out);
+        } else {
+            Unwrap(yan_lamma::Q41ToTensor(ToBlocks<Block_Q41>(raw, n), shape), out);
+        }
+    });
+}
+
+// QuanTensor overloads (src/quantiezd_tensor.cc), the ones the GGUF loader
+// uses on the embedding table; they need cols % 32 == 0.
+int ref_dequantize_flat(int type, const uint8_t* raw, int rows, int cols, float* out) {
+    return Guard([&] {
+        QuanTensor q;
+        q.shape = {rows, cols};
+        const size_t n = static_cast<size_t>(rows) * static_cast<size_t>(cols) / 32;
+        if (type == 0) {
+            q.type = QuantType::kQ80;
+            q.kQ80_data = ToBlocks<Block_Q80>(raw, n);
+            Unwrap(yan_lamma::Q80ToTensor(q), out);
+        } else if (type == 1) {
+            q.type = QuantType::kQ40;
+            q.kQ40_data = ToBlocks<Block_Q40>(raw, n);
+            Unwrap(yan_lamma::Q40ToTensor(q), out);
+        } else {
+            q.type = QuantType::kQ41;
+            q.kQ41_data = ToBlocks<Block_Q41>(raw, n);
+            Unwrap(yan_lamma::Q41ToTensor(q), out);
+        }
+    });
+}
+
+// The per-token op chain as the reference's CPU forward runs it: each op
+// takes and returns Tensor objects (one heap allocation per result).  The
+// embedding row copy and the residual add live in src/forward.cc, which does
+// not build from a few files, so they are written here as the plain Tensor
+// loops src/forward.cc:198-205 and :213-222 are.  n_threads > 1 spreads the
+// tokens over the reference's own ParallelFor (thread_pool/thread_pool.cc).
+int ref_chain(const float* table, int64_t vocab, int64_t dim, const int32_t* ids, float* x,
+              const float* delta, const float* norm_w, float* y, float eps, float* q, float* k,
+              int n_heads, int n_kv_heads, int head_dim, const int32_t* positions, float theta,
+              const float* gate, const float* up, float* ffn_out, int64_t ffn_dim,
+              int64_t n_tokens, int n_threads) {
+    return Guard([&] {
+        const int D = static_cast<int>(dim);
+        const int F = static_cast<int>(ffn_dim);
+        const Tensor w = Wrap(norm_w, {D});
+        auto rows = [&](int begin, int end) {
+            for (int t = begin; t < end; ++t) {
+                if (ids[t] < 0 || ids[t] >= vocab) {
+                    throw std::runtime_error("token id out of range");
+                }
+                Tensor e({D});
+                const float* src = table + static_cast<int64_t>(ids[t]) * dim;
+                for (int i = 0; i < D; ++i) e.data[i] = src[i];
+                const Tensor d = Wrap(delta + t * dim, {D});
+                Tensor h({D});
+                for (int i = 0; i < D; ++i) h.data[i] = e.data[i] + d.data[i];
+                Unwrap(h, x + t * dim);
+                Unwrap(yan_lamma::RmsNorm(h, w, eps), y + t * dim);
+                const int64_t qs = static_cast<int64_t>(n_heads) * head_dim;
+                const int64_t ks = static_cast<int64_t>(n_kv_heads) * head_dim;
+                Tensor tq = Wrap(q + t * qs, {n_heads, head_dim});
+                Tensor tk = Wrap(k + t * ks, {n_kv_heads, head_dim});
+                yan_lamma::Rope(tq, tk, positions[t], theta, RopeType::kNormal);
+                Unwrap(tq, q + t * qs);
+                Unwrap(tk, k + t * ks);
+                Unwrap(yan_lamma::SwiGlu(Wrap(gate + t * ffn_dim, {F}), Wrap(up + t * ffn_dim, {F})),
+                       ffn_out + t * ffn_dim);
+            }
+        };
+        if (n_threads <= 1) {
+            rows(0, static_cast<int>(n_tokens));
+        } else {
+            yan_lamma::SetThreadNum(n_threads);
+            yan_lamma::ParallelFor(static_cast<int>(n_tokens), rows);
+            yan_lamma::SetThreadNum(0);
+        }
+    });
+}
+
+}  // extern "C"

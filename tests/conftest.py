@@ -1,0 +1,79 @@
+"""Shared pytest setup.
+
+Markers: `gpu` tests need an MI355X and the built HIP library; everything
+else runs on the CPU (oracle vs golden fixtures and the compiled reference,
+host logic, library loading and exported symbols).
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a GPU (MI355X) and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def orc():
+    import oracle as O
+    return O.oracle()
+
+
+@pytest.fixture(scope="session")
+def mlk():
+    """The HIP package, with device 0 selected; fails loudly if it is missing."""
+    import __graft_entry__ as g
+    pkg = g.load_package()
+    pkg.set_device(0)
+    return pkg
+
+
+def golden(name):
+    with np.load(os.path.join(GOLDEN, f"{name}.npz"), allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def assert_bits_equal(got, want, what="", nan_equal=False):
+    got = np.ascontiguousarray(got, dtype=np.float32)
+    want = np.ascontiguousarray(want, dtype=np.float32)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    diff = got.view(np.uint32) != want.view(np.uint32)
+    if nan_equal:
+        diff &= ~(np.isnan(got) & np.isnan(want))
+    if diff.any():
+        i = int(np.flatnonzero(diff.reshape(-1))[0])
+        raise AssertionError(f"{what}: {int(diff.sum())} elements differ, first at {i}: "
+                             f"{got.reshape(-1)[i]!r} vs {want.reshape(-1)[i]!r}")
+
+
+def assert_terms_close(got, want, terms_abs, what="", rtol=1e-5):
+    """The reference's bar: |got - want| <= 1e-5 * max(1, sum|terms|)
+    (README.md:7, test/ops_test.cc:520-521).  terms_abs is sum|terms| per
+    element (same shape as want)."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    bound = rtol * np.maximum(1.0, np.asarray(terms_abs, dtype=np.float64))
+    err = np.abs(got - want)
+    bad = err > bound
+    if bad.any():
+        i = int(np.flatnonzero(bad.reshape(-1))[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} elements beyond tolerance, first at {i}: "
+                             f"{got.reshape(-1)[i]!r} vs {want.reshape(-1)[i]!r}")
+
+
+def max_ulp(got, want):
+    a = np.ascontiguousarray(got, dtype=np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(want, dtype=np.float32).view(np.int32).astype(np.int64)
+    return int(np.abs(a - b).max()) if a.size else 0
