@@ -17,8 +17,11 @@
 // is exact in fp32, so only the Q4_1 "+ m" rounds and the result equals the
 // CPU one bit for bit.
 //
-// A workgroup takes whole tokens.  The row's packed blocks (34/18/20 B, so
-// unaligned inside the row) are staged into LDS with 16-byte loads when the
+// Table rows are read with normal loads (Zipf-distributed ids repeat hot
+// rows, which then come from L2 / the MALL); output rows are written with
+// // non-temporal stores.  One wave takes one token (so a T = 4096 batch is
+// resident at once and the LDS barriers are wave-local).  The row's packed
+// blocks (34/18/20 B, so unaligned inside the row) are staged into LDS with 16-byte loads when the
 // row stride allows it, then every lane decodes four consecutive outputs
 // and writes them as one float4, so both the HBM reads and the writes are
 // fully coalesced.
@@ -28,6 +31,7 @@ namespace mlk {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kQThreads = 64;      // one wave per token row in the quantized gather
 constexpr int kChunkBlocks = 128;  // 4096 elements staged per LDS round
 
 template <int QT>
@@ -129,7 +133,7 @@ __device__ inline float4 Decode4(const uint8_t* blk, int w) {
 }
 
 template <int QT>
-__global__ __launch_bounds__(kThreads) void GatherQuantKernel(const uint8_t* __restrict__ blocks,
+__global__ __launch_bounds__(kQThreads) void GatherQuantKernel(const uint8_t* __restrict__ blocks,
                                                               int64_t vocab, int64_t dim,
                                                               const int32_t* __restrict__ ids,
                                                               int32_t token, int64_t n_tokens,
@@ -146,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void GatherQuantKernel(const uint8_t* __r
         float* dst = out + t * dim;
         if (id < 0 || id >= vocab) {
             if (tid == 0) RaiseFlag(err, 1);
-            for (int64_t i = tid; i < dim; i += kThreads) dst[i] = 0.0f;
+            for (int64_t i = tid; i < dim; i += kQThreads) dst[i] = 0.0f;
             continue;
         }
         const uint8_t* row = blocks + static_cast<int64_t>(id) * row_bytes;
@@ -159,22 +163,22 @@ __global__ __launch_bounds__(kThreads) void GatherQuantKernel(const uint8_t* __r
                 // row_bytes and the chunk offset are multiples of 16 here
                 const int n16 = bytes / 16;
                 const uint4* s16 = reinterpret_cast<const uint4*>(src);
-                for (int i = tid; i < n16; i += kThreads) stage[i] = s16[i];
-                for (int i = n16 * 16 + tid; i < bytes; i += kThreads) lds[i] = src[i];
+                for (int i = tid; i < n16; i += kQThreads) stage[i] = s16[i];
+                for (int i = n16 * 16 + tid; i < bytes; i += kQThreads) lds[i] = src[i];
             } else {
-                for (int i = tid; i < bytes; i += kThreads) lds[i] = src[i];
+                for (int i = tid; i < bytes; i += kQThreads) lds[i] = src[i];
             }
             __syncthreads();
             const int64_t e0 = c0 * 32;
             const int n_el = static_cast<int>(dim - e0 < nbc * 32 ? dim - e0 : nbc * 32);
             if (vec) {
                 float4* d4 = reinterpret_cast<float4*>(dst + e0);
-                for (int j = tid; j < n_el / 4; j += kThreads) {
+                for (int j = tid; j < n_el / 4; j += kQThreads) {
                     const int e = 4 * j;
-                    d4[j] = Decode4<QT>(lds + (e >> 5) * kBB, e & 31);
+                    StoreNT(d4 + j, Decode4<QT>(lds + (e >> 5) * kBB, e & 31));
                 }
             } else {
-                for (int e = tid; e < n_el; e += kThreads) {
+                for (int e = tid; e < n_el; e += kQThreads) {
                     dst[e0 + e] = Decode1<QT>(lds + (e >> 5) * kBB, e & 31);
                 }
             }
@@ -205,7 +209,7 @@ __global__ __launch_bounds__(kThreads) void GatherF32Vec(const float4* __restric
 #pragma unroll
             for (int u = 0; u < VPT; ++u) {
                 const int64_t i = base + static_cast<int64_t>(u) * kThreads;
-                if (i < dim4) dst[i] = v[u];
+                if (i < dim4) StoreNT(dst + i, v[u]);
             }
         }
     }
@@ -387,7 +391,7 @@ mlk_status mlk_gather_f32(const float* table, int64_t vocab, int64_t dim, const 
     const mlk_status st = CheckGather("mlk_gather_f32", table, vocab, dim, ids, token, n_tokens, out);
     if (st != MLK_OK || n_tokens == 0) return st;
     const hipStream_t s = AsStream(stream);
-    const unsigned grid = GridFor(n_tokens, 1, 8);
+    const unsigned grid = FullGrid(n_tokens, 1);
     if (dim % 4 == 0 && Aligned(table, 16) && Aligned(out, 16)) {
         hipLaunchKernelGGL(GatherF32Vec<4>, dim3(grid), dim3(kThreads), 0, s,
                            reinterpret_cast<const float4*>(table), vocab, dim / 4, ids, token,
@@ -416,20 +420,20 @@ mlk_status mlk_gather_quant(int32_t quant_type, const void* blocks, int64_t voca
     const int64_t row_bytes = ((dim + 31) / 32) * BlockBytes(quant_type);
     const int wide = (row_bytes % 16 == 0 && Aligned(blocks, 16)) ? 1 : 0;
     const int vec = (dim % 4 == 0 && Aligned(out, 16)) ? 1 : 0;
-    const unsigned grid = GridFor(n_tokens, 1, 8);
+    const unsigned grid = FullGrid(n_tokens, 1);
     const hipStream_t s = AsStream(stream);
     const uint8_t* b = static_cast<const uint8_t*>(blocks);
     switch (quant_type) {
         case MLK_Q8_0:
-            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q8_0>, dim3(grid), dim3(kThreads), 0, s, b,
+            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q8_0>, dim3(grid), dim3(kQThreads), 0, s, b,
                                vocab, dim, ids, token, n_tokens, out, err, wide, vec);
             break;
         case MLK_Q4_0:
-            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_0>, dim3(grid), dim3(kThreads), 0, s, b,
+            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_0>, dim3(grid), dim3(kQThreads), 0, s, b,
                                vocab, dim, ids, token, n_tokens, out, err, wide, vec);
             break;
         default:
-            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_1>, dim3(grid), dim3(kThreads), 0, s, b,
+            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_1>, dim3(grid), dim3(kQThreads), 0, s, b,
                                vocab, dim, ids, token, n_tokens, out, err, wide, vec);
             break;
     }

@@ -9,13 +9,15 @@
 // angle drifts from the double one by ~4e-4 rad at pos 8191 (theta 5e5);
 // here the angle, cos and sin are float64, so the result equals the CPU's.
 //
-// Work layout: a workgroup takes whole tokens (grid-stride).  Its threads
-// form `rows` rows of `lanes` lanes; a lane owns PV consecutive pairs of
-// every head, so its inverse frequencies are computed once per kernel and
-// its cos/sin once per token, then reused across all n_heads + n_kv_heads
-// heads that its row visits.  Q and K are one launch (the reference made
-// two per token).  Each row first loads up to kBatch heads, then rotates
-// and stores them, so several 16-byte loads are in flight per lane.
+// Work layout: workgroups walk the tokens (about four per workgroup at
+// T = 4096).  The threads form `rows` rows of `lanes` lanes; a lane owns PV
+// consecutive pairs of a head, computes its inverse frequencies once per
+// kernel and, per token, issues the loads of its first kBatch heads before
+// evaluating the float64 sincos, so the transcendental latency hides under
+// the memory latency; the same angles then serve every head the row visits.
+// Q and K are one launch (the reference made two per token).  The update is
+// in place, and plain loads/stores measured ~20% faster than non-temporal
+// ones for this read-modify-write pattern on MI355X.
 //
 // HBM bytes per token: 8 * (n_heads + n_kv_heads) * head_dim (read + write).
 #include "mlk_common.h"
@@ -27,7 +29,7 @@ namespace mlk {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kBatch = 8;
+constexpr int kBatch = 5;  // heads loaded per lane before the first rotation
 
 template <int PV, bool kNeoX>
 struct Pairs;
@@ -115,17 +117,18 @@ __global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64
                                                        int n_heads, int n_kv_heads, int head_dim,
                                                        int64_t q_stride, int64_t k_stride,
                                                        const int32_t* positions, int32_t pos0,
-                                                       float theta, int32_t* err, int lanes,
-                                                       int rows) {
+                                                       float theta, int32_t* err) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
+    const int half = head_dim / 2;
+    const int groups = half / PV;
+    const int lanes = groups < kThreads ? groups : kThreads;
+    const int rows = kThreads / lanes;
     const int lane = tid % lanes;
     const int row = tid / lanes;
     if (row >= rows) {
         return;  // spare threads when kThreads is not a multiple of lanes
     }
-    const int half = head_dim / 2;
-    const int groups = half / PV;
     const int heads = n_heads + n_kv_heads;
     for (int g = lane; g < groups; g += lanes) {
         double inv_freq[PV];
@@ -140,35 +143,93 @@ __global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64
                 if (tid == 0 && g == 0) RaiseFlag(err, 1);
                 continue;
             }
-            double c[PV], s[PV];
-#pragma unroll
-            for (int p = 0; p < PV; ++p) {
-                sincos(static_cast<double>(pos) * inv_freq[p], &s[p], &c[p]);
-            }
             float* qt = q + t * q_stride;
             float* kt = k + t * k_stride;
+            double c[PV], s[PV];
+            bool have_angles = false;
             for (int h0 = row; h0 < heads; h0 += rows * kBatch) {
                 Pairs<PV, kNeoX> v[kBatch];
+                float* base[kBatch];
 #pragma unroll
                 for (int b = 0; b < kBatch; ++b) {
                     const int h = h0 + b * rows;
+                    base[b] = nullptr;
                     if (h < heads) {
-                        const float* base = h < n_heads
-                                                ? qt + static_cast<int64_t>(h) * head_dim
-                                                : kt + static_cast<int64_t>(h - n_heads) * head_dim;
-                        v[b].Load(base, g, half);
+                        base[b] = h < n_heads ? qt + static_cast<int64_t>(h) * head_dim
+                                              : kt + static_cast<int64_t>(h - n_heads) * head_dim;
+                        v[b].Load(base[b], g, half);
                     }
+                }
+                if (!have_angles) {
+                    // evaluated while the first batch of loads is in flight
+#pragma unroll
+                    for (int p = 0; p < PV; ++p) {
+                        sincos(static_cast<double>(pos) * inv_freq[p], &s[p], &c[p]);
+                    }
+                    have_angles = true;
                 }
 #pragma unroll
                 for (int b = 0; b < kBatch; ++b) {
-                    const int h = h0 + b * rows;
-                    if (h < heads) {
-                        float* base = h < n_heads ? qt + static_cast<int64_t>(h) * head_dim
-                                                  : kt + static_cast<int64_t>(h - n_heads) * head_dim;
+                    if (base[b] != nullptr) {
                         v[b].Rotate(c, s);
-                        v[b].Store(base, g, half);
+                        v[b].Store(base[b], g, half);
                     }
                 }
+            }
+        }
+    }
+}
+
+// Common case: every lane rotates at most kBatch heads of one pair group per
+// token, so one batch of loads covers the token (the workgroup has
+// lanes * ceil(heads / kBatch) threads: 256 for 8B heads, 512 for 70B).
+// Same arithmetic as RopeKernel, with no batch loop and fewer registers.
+template <int PV, bool kNeoX>
+__global__ __launch_bounds__(1024) void RopeOneBatch(float* q, float* k, int64_t n_tokens,
+                                                     int n_heads, int n_kv_heads, int head_dim,
+                                                     int64_t q_stride, int64_t k_stride,
+                                                     const int32_t* positions, int32_t pos0,
+                                                     float theta, int32_t* err) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x;
+    const int half = head_dim / 2;
+    const int lanes = half / PV;
+    const int rows = blockDim.x / lanes;
+    const int lane = tid % lanes;
+    const int row = tid / lanes;
+    if (row >= rows) return;
+    const int heads = n_heads + n_kv_heads;
+    double inv_freq[PV];
+#pragma unroll
+    for (int p = 0; p < PV; ++p) {
+        inv_freq[p] = pow(static_cast<double>(theta), -2.0 * (lane * PV + p) / head_dim);
+    }
+    for (int64_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
+        const int32_t pos = positions != nullptr ? positions[t] : pos0 + static_cast<int32_t>(t);
+        if (pos < 0) {
+            if (tid == 0) RaiseFlag(err, 1);
+            continue;
+        }
+        Pairs<PV, kNeoX> v[kBatch];
+        float* base[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int h = row + b * rows;
+            base[b] = nullptr;
+            if (h < heads) {
+                base[b] = h < n_heads ? q + t * q_stride + static_cast<int64_t>(h) * head_dim
+                                      : k + t * k_stride + static_cast<int64_t>(h - n_heads) * head_dim;
+                v[b].Load(base[b], lane, half);
+            }
+        }
+        double c[PV], s[PV];  // evaluated while the loads are in flight
+#pragma unroll
+        for (int p = 0; p < PV; ++p) sincos(static_cast<double>(pos) * inv_freq[p], &s[p], &c[p]);
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            if (base[b] != nullptr) {
+                v[b].Rotate(c, s);
+                v[b].Store(base[b], lane, half);
             }
         }
     }
@@ -178,13 +239,23 @@ template <int PV, bool kNeoX>
 mlk_status LaunchRope(float* q, float* k, int64_t n_tokens, int n_heads, int n_kv_heads,
                       int head_dim, int64_t qs, int64_t ks, const int32_t* positions,
                       int32_t pos0, float theta, int32_t* err, hipStream_t stream) {
-    const int groups = head_dim / 2 / PV;
-    const int lanes = groups < kThreads ? groups : kThreads;
-    const int rows = kThreads / lanes;
-    const unsigned grid = GridFor(n_tokens, 1, 8);
+    const int lanes = head_dim / 2 / PV;
+    const int heads = n_heads + n_kv_heads;
+    const int rows = (heads + kBatch - 1) / kBatch;
+    const int64_t threads = (static_cast<int64_t>(lanes) * rows + kWave - 1) / kWave * kWave;
+    if (threads <= 1024) {
+        // about 1024 resident threads' worth of workgroups per CU
+        const int per_cu = static_cast<int>(1024 / threads) > 0 ? static_cast<int>(1024 / threads) : 1;
+        const unsigned grid = GridFor(n_tokens, 1, per_cu);
+        hipLaunchKernelGGL((RopeOneBatch<PV, kNeoX>), dim3(grid), dim3(threads), 0, stream, q, k,
+                           n_tokens, n_heads, n_kv_heads, head_dim, qs, ks, positions, pos0, theta,
+                           err);
+        return CheckLaunch("RopeOneBatch");
+    }
+    const unsigned grid = GridFor(n_tokens, 1, 4);
     hipLaunchKernelGGL((RopeKernel<PV, kNeoX>), dim3(grid), dim3(kThreads), 0, stream, q, k,
                        n_tokens, n_heads, n_kv_heads, head_dim, qs, ks, positions, pos0, theta,
-                       err, lanes, rows);
+                       err);
     return CheckLaunch("RopeKernel");
 }
 
