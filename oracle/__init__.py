@@ -47,6 +47,9 @@ class _Oracle:
         self.lib = lib
         self.fp16_to_fp32 = _bind(lib, "orc_fp16_to_fp32", C.c_float, [C.c_uint16])
         self.fp32_to_fp16 = _bind(lib, "orc_fp32_to_fp16", C.c_uint16, [C.c_float])
+        _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+        self._h2f = _bind(lib, "orc_fp16_to_fp32_array", None, [_u16p, _f32p, _i64])
+        self._f2h = _bind(lib, "orc_fp32_to_fp16_array", None, [_f32p, _u16p, _i64])
         for q in QUANT_TYPES:
             setattr(self, f"_quantize_{q}",
                     _bind(lib, f"orc_quantize_{q}", C.c_int, [_f32p, _i64, _i64, _u8p]))
@@ -72,6 +75,18 @@ class _Oracle:
                              _f32p, _f32p, _i32, _i32, _i32, _i32p, C.c_float,
                              _f32p, _f32p, _f32p, _i64, _i64, C.c_int])
         self.parallel_threads = _bind(lib, "orc_parallel_threads", C.c_int, [C.c_int])
+
+    def fp16_to_fp32_array(self, codes):
+        codes = np.ascontiguousarray(codes, dtype=np.uint16)
+        out = np.empty(codes.shape, np.float32)
+        self._h2f(codes.reshape(-1), out.reshape(-1), codes.size)
+        return out
+
+    def fp32_to_fp16_array(self, x):
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty(x.shape, np.uint16)
+        self._f2h(x.reshape(-1), out.reshape(-1), x.size)
+        return out
 
     # ---- quant -------------------------------------------------------------
     def quantize(self, qtype, x):

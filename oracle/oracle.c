@@ -82,6 +82,20 @@ uint16_t orc_fp32_to_fp16(float value)
     return (uint16_t)(sign | q);
 }
 
+void orc_fp16_to_fp32_array(const uint16_t* in, float* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        out[i] = orc_fp16_to_fp32(in[i]);
+    }
+}
+
+void orc_fp32_to_fp16_array(const float* in, uint16_t* out, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        out[i] = orc_fp32_to_fp16(in[i]);
+    }
+}
+
 /* ------------------------------------------------------------- blocks */
 
 static void put_u16(uint8_t* p, uint16_t v)

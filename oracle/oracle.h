@@ -58,6 +58,10 @@ float orc_fp16_to_fp32(uint16_t bits);
 /* src/quant.cc:31-79: round to nearest even, overflow -> inf, NaN -> quiet. */
 uint16_t orc_fp32_to_fp16(float value);
 
+/* Element-wise array forms of the two conversions above. */
+void orc_fp16_to_fp32_array(const uint16_t* in, float* out, int64_t n);
+void orc_fp32_to_fp16_array(const float* in, uint16_t* out, int64_t n);
+
 /* src/quant.cc:136-174 TensorToQ80 over a [rows, cols] matrix. */
 int orc_quantize_q8_0(const float* x, int64_t rows, int64_t cols, uint8_t* blocks);
 /* src/quant.cc:205-249 TensorToQ40. */

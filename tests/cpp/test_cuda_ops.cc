@@ -1,0 +1,460 @@
+// test_cuda_ops.cc -- the C++ op surface (include/cuda_ops.h) against the
+// CPU oracle, in the shape of the reference's own tests
+// (test/cuda_ops_test.cc and tests/test_cuda_ops.cc of the reference tree).
+//
+//   test_cuda_ops cpu   argument checks that fail before any device work
+//                       (runs without a GPU)
+//   test_cuda_ops gpu   everything else, on device 0
+#include "tests/cpp/test_support.h"
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+
+using namespace yan_lamma;
+using namespace mlk_test;
+
+namespace {
+
+// ------------------------------------------------------ oracle wrappers
+
+Tensor OracleRms(const Tensor& x, const Tensor& w, float eps) {
+    Tensor y(x.shape);
+    const int64_t dim = w.data.size();
+    Require(orc_rmsnorm_row(x.data.data(), w.data.data(), y.data.data(), dim, eps) == ORC_OK,
+            "oracle rmsnorm rejected its input");
+    return y;
+}
+
+Tensor OracleSilu(const Tensor& x) {
+    Tensor y(x.shape);
+    orc_silu(x.data.data(), y.data.data(), x.data.size());
+    return y;
+}
+
+Tensor OracleBinary(void (*f)(const float*, const float*, float*, int64_t), const Tensor& a,
+                    const Tensor& b) {
+    Tensor y(a.shape);
+    f(a.data.data(), b.data.data(), y.data.data(), a.data.size());
+    return y;
+}
+
+Tensor OracleSoftmax(const Tensor& x) {
+    Tensor y(x.shape);
+    Require(orc_softmax(x.data.data(), y.data.data(), x.data.size()) == ORC_OK, "oracle softmax");
+    return y;
+}
+
+// q [T, H * hd], k [T, KV * hd] rotated per token.
+std::pair<Tensor, Tensor> OracleRope(Tensor q, Tensor k, int H, int KV, int hd,
+                                     const std::vector<int>& pos, float theta, RopeType type) {
+    Require(orc_rope(q.data.data(), k.data.data(), static_cast<int64_t>(pos.size()), H, KV, hd,
+                     pos.data(), 0, theta, type == kNormal ? ORC_ROPE_NORMAL : ORC_ROPE_NEOX) ==
+                ORC_OK,
+            "oracle rope");
+    return {q, k};
+}
+
+int QuantIndex(QuantType t) { return t == QuantType::kQ80 ? 0 : (t == QuantType::kQ40 ? 1 : 2); }
+
+std::vector<uint8_t> OracleQuantize(QuantType t, const Tensor& x) {
+    const int64_t cols = x.shape.back(), rows = x.data.size() / cols;
+    const int64_t bb = t == QuantType::kQ80 ? 34 : (t == QuantType::kQ40 ? 18 : 20);
+    std::vector<uint8_t> out(rows * ((cols + 31) / 32) * bb);
+    int rc = t == QuantType::kQ80   ? orc_quantize_q8_0(x.data.data(), rows, cols, out.data())
+             : t == QuantType::kQ40 ? orc_quantize_q4_0(x.data.data(), rows, cols, out.data())
+                                    : orc_quantize_q4_1(x.data.data(), rows, cols, out.data());
+    Require(rc == ORC_OK, "oracle quantize");
+    return out;
+}
+
+std::vector<uint8_t> Bytes(const CudaDeviceBuffer& b) {
+    std::vector<uint8_t> out(b.GetByteSize());
+    b.download(out.data(), out.size());
+    return out;
+}
+
+// ------------------------------------------------------------- cpu cases
+
+void CpuBuildPredicate() { Require(CudaopsBuild() == CudaRuntimeBuilt(), "build predicates"); }
+
+// test/cuda_ops_test.cc:212-295: the checks that run before any device work.
+void CpuRejectsInvalidInputs() {
+    const Tensor x = Values({4}), weight = Values({4}), other = Values({3});
+    const Tensor matrix = Values({2, 2});
+    Tensor empty;
+    empty.shape = {0};
+    int host_word = 0;
+    const void* fake = &host_word;  // never dereferenced: validation fails first
+    RequireError([&] { (void)CudaEmbeddingDevice(nullptr, {3, 4}, 0); }, "must not be null");
+    RequireError([&] { (void)CudaEmbeddingDevice(fake, {12}, 0); }, "expected weight shape");
+    RequireError([&] { (void)CudaEmbeddingDevice(fake, {0, 4}, 0); }, "must be positive");
+    RequireError([&] { (void)CudaEmbeddingDevice(fake, {3, 0}, 0); }, "must be positive");
+    RequireError([&] { (void)CudaEmbeddingDevice(fake, {3, 4}, -1); }, "token_id must be in");
+    RequireError([&] { (void)CudaEmbeddingDevice(fake, {3, 4}, 3); }, "token_id must be in");
+    for (float eps : {0.0f, -1.0f, std::numeric_limits<float>::infinity(),
+                      std::numeric_limits<float>::quiet_NaN()}) {
+        RequireError([&] { (void)CudaRmsNormHost(x, weight, eps); }, "eps must be finite");
+    }
+    RequireError([&] { (void)CudaRmsNormHost(matrix, weight, 1e-5f); }, "expected a 1D");
+    RequireError([&] { (void)CudaRmsNormHost(x, matrix, 1e-5f); }, "expected a 1D");
+    RequireError([&] { (void)CudaRmsNormHost(x, other, 1e-5f); }, "shapes must match");
+    RequireError([&] { (void)CudaRmsNormHost(empty, empty, 1e-5f); }, "must not be empty");
+    const CudaTensor empty_device;
+    RequireError([&] { (void)CudaRmsNromDevice(empty_device, fake, {4}, 1e-5f); },
+                 "expected a 1D");
+    Tensor m = matrix;
+    RequireError([&] { (void)CudaSoftmax(m); }, "expected a 1D");
+    RequireError([&] { (void)CudaSoftmax(empty); }, "must not be empty");
+    RequireError([&] { (void)CudaElementwiseMul(x, matrix); }, "shapes must match");
+    Tensor q = Values({2, 4}), k = Values({1, 4}), v = Values({4}), odd = Values({1, 3});
+    Tensor mismatch = Values({1, 6});
+    for (RopeType t : {kNormal, kNeoX}) {
+        RequireError([&] { CudaRopeHost(v, k, 0, 10000.0f, t); }, "expected 2D");
+        RequireError([&] { CudaRopeHost(q, v, 0, 10000.0f, t); }, "expected 2D");
+        RequireError([&] { CudaRopeHost(odd, odd, 0, 10000.0f, t); }, "must be even");
+        RequireError([&] { CudaRopeHost(q, mismatch, 0, 10000.0f, t); }, "must match");
+        RequireError([&] { CudaRopeHost(q, k, -1, 10000.0f, t); }, "non-negative");
+        for (float theta : {0.0f, -1.0f, std::numeric_limits<float>::infinity(),
+                            std::numeric_limits<float>::quiet_NaN()}) {
+            RequireError([&] { CudaRopeHost(q, k, 0, theta, t); }, "theta must be finite");
+        }
+    }
+    CudaTensor dq, dk;
+    RequireError([&] { CudaRopeDevice(dq, dk, 0, 1, 1, 4, 10000.0f, kNormal, 1); },
+                 "devices must match");
+    RequireError([&] { CudaRopeDevice(dq, dk, -1, 1, 1, 4, 10000.0f); }, "non-negative");
+    RequireError([&] { CudaRopeDevice(dq, dk, 0, 0, 1, 4, 10000.0f); }, "head_dim must be");
+    RequireError([&] { CudaRopeDevice(dq, dk, 0, 1, 1, 3, 10000.0f); }, "head_dim must be");
+    RequireError([&] { CudaRopeDevice(dq, dk, 0, 1, 1, 4, 10000.0f); }, "element count");
+    RequireError([&] { (void)CudaEmbeddingBatchDevice(fake, {3, 4}, {0, 3}); },
+                 "token_id must be in");
+    RequireError([&] { (void)CudaEmbeddingBatchDevice(fake, {3, 4}, {}); }, "must not be empty");
+    RequireError([&] { (void)CudaEmbeddingQuantDevice(fake, QuantType::kF32, {3, 32}, {0}); },
+                 "unsupported quantization type");
+    RequireError([&] { CudaRopeBatchDevice(dq, dk, {0, -2}, 1, 1, 4, 1e4f); }, "non-negative");
+    RequireError([&] { (void)CudaAddRmsNormDevice(dq, nullptr, fake, {4}, 1e-5f); },
+                 "must not be empty");
+    RequireError([&] { (void)CudaQuantizeDevice(dq, QuantType::kQ80); }, "must not be empty");
+}
+
+void CpuTensorChecks() {
+    RequireError([] { Tensor t({2, 0}); }, "must be positive");
+    Tensor t = Values({2, 3});
+    Require(t.At2(1, 2) == t.data[5], "At2 indexing");
+    bool threw = false;
+    try {
+        (void)t.At2(2, 0);
+    } catch (const std::out_of_range&) {
+        threw = true;
+    }
+    Require(threw, "At2 bounds");
+    RequireError([&] { (void)t.Reshape({4, 2}, "Reshape"); }, "cannot reshape");
+    Require(t.Reshape({3, 2}, "Reshape").shape == std::vector<int>({3, 2}), "reshape shape");
+    Require(t.SwitchIdex({1, 1}) == 4, "flat index");
+    RequireError([] { CudaTensor c({3, -1}); }, "must be positive");
+}
+
+// ------------------------------------------------------------- gpu cases
+
+void GpuDeviceInfo() {
+    Require(DeviceCount() > 0, "a GPU is required for the gpu cases");
+    const struct CudaInfo info = GetCudaInfo(0);
+    std::cout << "  " << CudaInfo(info) << std::endl;
+    Require(info.total_bytes > 0, "device memory size");
+    bool threw = false;
+    try {
+        (void)GetCudaInfo(DeviceCount());
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    Require(threw, "an absent device is rejected");
+}
+
+// test/cuda_ops_test.cc:91-103 and tests/test_cuda_ops.cc:27-30.
+void GpuEmbedding() {
+    const Tensor weight = Values({3, 259});
+    CudaDeviceBuffer buffer(weight.data.size() * sizeof(float));
+    buffer.upload(weight.data.data(), weight.data.size() * sizeof(float));
+    for (int token : {0, 2}) {
+        Tensor expected({259});
+        std::copy_n(weight.data.begin() + token * 259, 259, expected.data.begin());
+        const CudaTensor y = CudaEmbeddingDevice(buffer.GetData(), weight.shape, token);
+        Require(y.DeviceId() == 0, "device id");
+        RequireTensor(y.Download(), expected, "embedding", 0.0);
+    }
+    const Tensor table = Random({131, 64}, 7, 0.0f, 0.02f);
+    const CudaTensor d = TensorHostToDevice(table);
+    const std::vector<int> ids{0, 1, 130, 128, 104, 101, 108};
+    const CudaTensor rows = CudaEmbeddingBatchDevice(d.GetData(), table.shape, ids);
+    Tensor expected({static_cast<int>(ids.size()), 64});
+    Require(orc_gather_f32(table.data.data(), 131, 64, ids.data(), ids.size(),
+                           expected.data.data()) == ORC_OK,
+            "oracle gather");
+    RequireTensor(rows.Download(), expected, "batched embedding", 0.0);
+}
+
+// test/cuda_ops_test.cc:105-126.
+void GpuRmsNorm() {
+    for (int n : {1, 7, 259, 1025}) {
+        for (bool zero : {false, true}) {
+            Tensor x = Values({n});
+            if (zero) std::fill(x.data.begin(), x.data.end(), 0.0f);
+            const Tensor weight = Values({n});
+            const auto original = x.data;
+            const Tensor expected = OracleRms(x, weight, 1e-5f);
+            RequireTensor(CudaRmsNormHost(x, weight, 1e-5f), expected, "host rmsnorm");
+            const CudaTensor dx = TensorHostToDevice(x);
+            const CudaTensor dw = TensorHostToDevice(weight);
+            const CudaTensor y = CudaRmsNromDevice(dx, dw.GetData(), weight.shape, 1e-5f);
+            Require(y.DeviceId() == 0, "device id");
+            RequireTensor(y.Download(), expected, "device rmsnorm");
+            Require(x.data == original, "host input unchanged");
+            RequireTensor(dx.Download(), x, "device input unchanged", 0.0);
+        }
+    }
+}
+
+// test/cuda_ops_test.cc:128-153 and tests/test_cuda_ops.cc:5-23.
+void GpuElementwise() {
+    for (const auto& shape :
+         {std::vector<int>{1}, std::vector<int>{86}, std::vector<int>{259}, std::vector<int>{3, 173}}) {
+        Tensor a = Values(shape), b = Values(shape);
+        for (float& v : b.data) v = 0.5f - v;
+        const auto oa = a.data, ob = b.data;
+        RequireTensor(CudaSilu(a), OracleSilu(a), "host silu");
+        RequireTensor(CudaElementwiseMul(a, b), OracleBinary(orc_mul, a, b), "host mul", 0.0);
+        const CudaTensor da = TensorHostToDevice(a), db = TensorHostToDevice(b);
+        RequireTensor(CudaSiluDevice(da).Download(), OracleSilu(a), "device silu");
+        RequireTensor(CudaElementwiseMulDevice(da, db).Download(), OracleBinary(orc_mul, a, b),
+                      "device mul", 0.0);
+        const Tensor sum = OracleBinary(orc_add, a, b);
+        RequireTensor(CudaElementAddDevice(da, db).Download(), sum, "add", 0.0);
+        RequireTensor(OCudaElementAddDevice(da, db.GetData(), shape).Download(), sum, "bias add",
+                      0.0);
+        RequireTensor(CudaSwiGluDevice(da, db).Download(), OracleBinary(orc_swiglu, a, b),
+                      "fused swiglu");
+        RequireTensor(da.Download(), a, "a unchanged", 0.0);
+        RequireTensor(db.Download(), b, "b unchanged", 0.0);
+        Require(a.data == oa && b.data == ob, "host inputs unchanged");
+    }
+    const CudaTensor a = TensorHostToDevice(Values({4})), b = TensorHostToDevice(Values({2, 2}));
+    RequireError([&] { (void)CudaElementAddDevice(a, b); }, "shapes must match");
+    RequireError([&] { (void)OCudaElementAddDevice(a, nullptr, {4}); }, "must not be null");
+    RequireError([&] { (void)OCudaElementAddDevice(a, b.GetData(), {2, 2}); }, "must match");
+    RequireError([&] { (void)CudaElementAddDevice(a, a, 1); }, "device must match");
+    RequireError([&] { (void)CudaSwiGluDevice(a, b); }, "shapes must match");
+}
+
+// test/cuda_ops_test.cc:155-183.
+void GpuSoftmax() {
+    std::vector<Tensor> cases;
+    for (const auto& v : {std::vector<float>{3.0f}, std::vector<float>{2.0f, 2.0f, 2.0f},
+                          std::vector<float>{-5.0f, -2.0f, -9.0f},
+                          std::vector<float>{10000.0f, 10001.0f, -10000.0f},
+                          std::vector<float>{-1000, 0, 1000, 999, -999}}) {
+        Tensor x({static_cast<int>(v.size())});
+        x.data = v;
+        cases.push_back(x);
+    }
+    cases.push_back(Values({259}));
+    cases.push_back(Values({1025}));
+    for (Tensor& x : cases) {
+        const auto original = x.data;
+        const Tensor y = CudaSoftmax(x);
+        RequireTensor(y, OracleSoftmax(x), "softmax");
+        double total = 0.0;
+        for (float v : y.data) {
+            Require(v >= 0.0f, "non-negative");
+            total += v;
+        }
+        Require(std::abs(total - 1.0) <= 1e-5, "sums to one");
+        Require(x.data == original, "input unchanged");
+    }
+}
+
+// test/cuda_ops_test.cc:185-210 and tests/test_cuda_ops.cc:32-49.
+void GpuRope() {
+    for (RopeType type : {kNormal, kNeoX}) {
+        for (int head_dim : {2, 8, 130}) {
+            for (int pos : {0, 7, 63}) {
+                Tensor q = Values({5, head_dim}), k = Waves({2, head_dim}, 0.3f);
+                const auto expected = OracleRope(q, k, 5, 2, head_dim, {pos}, 10000.0f, type);
+                CudaTensor dq = TensorHostToDevice(q), dk = TensorHostToDevice(k);
+                CudaRopeHost(q, k, pos, 10000.0f, type);
+                RequireTensor(q, expected.first, "host q");
+                RequireTensor(k, expected.second, "host k");
+                CudaRopeDevice(dq, dk, pos, 5, 2, head_dim, 10000.0f, type);
+                RequireTensor(dq.Download(), expected.first, "device q");
+                RequireTensor(dk.Download(), expected.second, "device k");
+            }
+        }
+    }
+    CudaTensor dq = TensorHostToDevice(Values({2, 4})), dk = TensorHostToDevice(Values({1, 4}));
+    RequireError([&] { CudaRopeDevice(dq, dk, 0, 3, 1, 4, 1e4f); }, "q element count");
+    RequireError([&] { CudaRopeDevice(dq, dk, 0, 2, 2, 4, 1e4f); }, "k element count");
+    RequireError([&] { CudaRopeDevice(dq, dk, 0, 2, 1, 4, 1e4f, kNormal, 1); }, "devices must");
+}
+
+// Batched RoPE over T tokens equals T one-token calls and the oracle.
+void GpuRopeBatched() {
+    const int T = 9, H = 8, KV = 2, hd = 64;
+    const std::vector<int> pos{0, 1, 5, 100, 4095, 8191, 17, 3, 2047};
+    for (RopeType type : {kNormal, kNeoX}) {
+        const Tensor q = Random({T, H * hd}, 11, 0.0f, 0.02f), k = Random({T, KV * hd}, 12, 0.0f, 0.02f);
+        const auto expected = OracleRope(q, k, H, KV, hd, pos, 500000.0f, type);
+        CudaTensor dq = TensorHostToDevice(q), dk = TensorHostToDevice(k);
+        CudaRopeBatchDevice(dq, dk, pos, H, KV, hd, 500000.0f, type);
+        RequireTensor(dq.Download(), expected.first, "batched q");
+        RequireTensor(dk.Download(), expected.second, "batched k");
+        // the same tokens one at a time through the reference signature
+        Tensor one_q({H * hd}), one_k({KV * hd});
+        for (int t = 0; t < T; ++t) {
+            std::copy_n(q.data.begin() + t * H * hd, H * hd, one_q.data.begin());
+            std::copy_n(k.data.begin() + t * KV * hd, KV * hd, one_k.data.begin());
+            CudaTensor tq = TensorHostToDevice(one_q), tk = TensorHostToDevice(one_k);
+            CudaRopeDevice(tq, tk, pos[t], H, KV, hd, 500000.0f, type);
+            const Tensor gq = tq.Download();
+            const Tensor bq = dq.Download();
+            Require(std::memcmp(gq.data.data(), bq.data.data() + t * H * hd,
+                                H * hd * sizeof(float)) == 0,
+                    "one-token and batched RoPE agree bit for bit");
+        }
+        CudaTensor rq = TensorHostToDevice(q), rk = TensorHostToDevice(k);
+        CudaRopeRangeDevice(rq, rk, 40, H, KV, hd, 500000.0f, type);
+        std::vector<int> range(T);
+        for (int t = 0; t < T; ++t) range[t] = 40 + t;
+        const auto er = OracleRope(q, k, H, KV, hd, range, 500000.0f, type);
+        RequireTensor(rq.Download(), er.first, "range q");
+        RequireTensor(rk.Download(), er.second, "range k");
+    }
+}
+
+// Fused residual add + RMSNorm over [T, D] equals ForwardAdd then RmsNorm.
+void GpuAddRmsNorm() {
+    for (auto shape : {std::vector<int>{1, 64}, std::vector<int>{6, 64}, std::vector<int>{3, 4096},
+                       std::vector<int>{2, 4, 130}, std::vector<int>{2, 8192}}) {
+        const int D = shape.back();
+        const Tensor x = Random(shape, 21, 0.0f, 0.02f), d = Random(shape, 22, 0.0f, 0.02f);
+        const Tensor w = Random({D}, 23, 1.0f, 0.1f);
+        Tensor r = x, y(shape);
+        Require(orc_add_rmsnorm(r.data.data(), d.data.data(), w.data.data(), y.data.data(),
+                                x.data.size() / D, D, 1e-5f) == ORC_OK,
+                "oracle add_rmsnorm");
+        CudaTensor dx = TensorHostToDevice(x);
+        const CudaTensor dd = TensorHostToDevice(d), dw = TensorHostToDevice(w);
+        const CudaTensor dy = CudaAddRmsNormDevice(dx, &dd, dw.GetData(), {D}, 1e-5f);
+        RequireTensor(dx.Download(), r, "residual", 0.0);
+        RequireTensor(dy.Download(), y, "norm");
+        const CudaTensor plain = CudaRmsNormRowsDevice(dx, dw.GetData(), {D}, 1e-5f);
+        RequireTensor(plain.Download(), y, "rows norm");
+        const CudaTensor untouched = CudaAddRmsNormDevice(dx, nullptr, dw.GetData(), {D}, 1e-5f);
+        RequireTensor(untouched.Download(), y, "no-delta norm");
+        RequireTensor(dx.Download(), r, "residual unchanged without delta", 0.0);
+        RequireError([&] { (void)CudaAddRmsNormDevice(dx, &dd, dw.GetData(), {D + 1}, 1e-5f); },
+                     "weight shape");
+        RequireError([&] { (void)CudaAddRmsNormDevice(dx, &dd, dw.GetData(), {D}, 0.0f); },
+                     "eps must be finite");
+    }
+}
+
+void GpuQuantized() {
+    for (QuantType t : {QuantType::kQ80, QuantType::kQ40, QuantType::kQ41}) {
+        for (auto shape : {std::vector<int>{17, 64}, std::vector<int>{9, 100}, std::vector<int>{5, 4096}}) {
+            const Tensor table = Random(shape, 31 + QuantIndex(t), 0.0f, 0.02f);
+            const CudaTensor dt = TensorHostToDevice(table);
+            const CudaDeviceBuffer blocks = CudaQuantizeDevice(dt, t);
+            const std::vector<uint8_t> want = OracleQuantize(t, table);
+            Require(Bytes(blocks) == want, "device quantizer equals TensorToQ* bytes");
+            const std::vector<int> ids{0, shape[0] - 1, 1, 3, 0};
+            const CudaTensor rows = CudaEmbeddingQuantDevice(blocks.GetData(), t, shape, ids);
+            Tensor expected({static_cast<int>(ids.size()), shape[1]});
+            Require(orc_gather_quant(QuantIndex(t), want.data(), shape[0], shape[1], ids.data(),
+                                     ids.size(), expected.data.data()) == ORC_OK,
+                    "oracle quant gather");
+            RequireTensor(rows.Download(), expected, "quantized gather", 0.0);
+        }
+    }
+}
+
+// The reference's forward path issues these ops with every input already
+// on the device: none of them may copy between host and device.
+void GpuNoHostTransfersInDeviceChain() {
+    const int D = 64, H = 4, KV = 2, hd = 16, F = 172;
+    const Tensor table = Random({131, D}, 41, 0.0f, 0.02f);
+    const CudaTensor dt = TensorHostToDevice(table), dw = TensorHostToDevice(Random({D}, 42, 1.0f, 0.1f));
+    CudaTensor delta = TensorHostToDevice(Random({D}, 43, 0.0f, 0.02f));
+    CudaTensor q = TensorHostToDevice(Random({H * hd}, 44)), k = TensorHostToDevice(Random({KV * hd}, 45));
+    const CudaTensor gate = TensorHostToDevice(Random({F}, 46)), up = TensorHostToDevice(Random({F}, 47));
+    CudaTransferStats stats;
+    {
+        CudaStatsScope scope(&stats);
+        for (int pos = 0; pos < 6; ++pos) {
+            CudaTensor h = CudaEmbeddingDevice(dt.GetData(), table.shape, 100 + pos);
+            const CudaTensor y = CudaAddRmsNormDevice(h, &delta, dw.GetData(), {D}, 1e-5f);
+            CudaRopeDevice(q, k, pos, H, KV, hd, 10000.0f);
+            const CudaTensor ff = CudaSwiGluDevice(gate, up);
+            (void)y;
+            (void)ff;
+        }
+    }
+    Require(stats.host_to_device_copies == 0 && stats.host_to_device_bytes == 0, "no H2D");
+    Require(stats.device_to_host_copies == 0 && stats.device_to_host_bytes == 0, "no D2H");
+    {
+        CudaStatsScope scope(&stats);
+        (void)q.Download();
+    }
+    Require(stats.device_to_host_copies == 1 && stats.device_to_host_bytes == H * hd * 4,
+            "one counted download");
+}
+
+void GpuAllocator() {
+    CudaEmptyCache();
+    Require(CudaCachedBytes() == 0, "cache empty");
+    auto stats = std::make_shared<CudaAllocationStats>();
+    const void* first = nullptr;
+    {
+        CudaAllocationScope scope(stats);
+        CudaTensor a({1000});
+        CudaTensor b({2000});
+        first = a.GetData();
+        Require(stats->current_bytes == 12000 && stats->peak_bytes == 12000, "peak counting");
+        a.Reset();
+        Require(stats->current_bytes == 8000, "release counting");
+        CudaTensor c({1000});  // same size class: the freed block comes back
+        Require(c.GetData() == first, "cached block reused");
+    }
+    Require(stats->peak_bytes == 12000, "peak kept");
+    Require(stats->current_bytes == 0, "all released");
+    Require(CudaCachedBytes() > 0, "freed blocks cached");
+    CudaEmptyCache();
+    Require(CudaCachedBytes() == 0, "cache returned to the driver");
+    CudaTensor moved({8});
+    CudaTensor target = std::move(moved);
+    Require(moved.IsEmpty() && moved.shape().empty() && !target.IsEmpty(), "move semantics");
+    target.Reshape({2, 4});
+    Require(target.num_dims() == 2 && target.NumEle() == 8, "reshape keeps the buffer");
+    RequireError([&] { target.Reshape({3, 3}); }, "element count must remain unchanged");
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const std::vector<Case> cases = {
+        {"cpu.build_predicate", CpuBuildPredicate},
+        {"cpu.rejects_invalid_inputs", CpuRejectsInvalidInputs},
+        {"cpu.tensor_checks", CpuTensorChecks},
+        {"gpu.device_info", GpuDeviceInfo},
+        {"gpu.embedding", GpuEmbedding},
+        {"gpu.rmsnorm", GpuRmsNorm},
+        {"gpu.elementwise", GpuElementwise},
+        {"gpu.softmax", GpuSoftmax},
+        {"gpu.rope", GpuRope},
+        {"gpu.rope_batched", GpuRopeBatched},
+        {"gpu.add_rmsnorm", GpuAddRmsNorm},
+        {"gpu.quantized", GpuQuantized},
+        {"gpu.no_host_transfers", GpuNoHostTransfersInDeviceChain},
+        {"gpu.allocator", GpuAllocator},
+    };
+    return Run(argc, argv, cases);
+}
