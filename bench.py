@@ -51,6 +51,14 @@ def parse_args():
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--extra", default=None, help="also measure configs 1, 3, 4 into this JSON file")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--rocprof-report", nargs=5, default=None,
+                   metavar=("KERNEL_TRACE_DIR", "FETCH_DIR", "WRITE_DIR", "CALIB_FETCH_DIR",
+                            "CALIB_WRITE_DIR"),
+                   help="summarize rocprofv3 CSV output of the default command (kernel trace) "
+                        "and of the --pmc FETCH_SIZE / WRITE_SIZE runs into profiles/")
+    p.add_argument("--calibrate", action="store_true",
+                   help="only run the counter-calibration kernel (SiLU over 256 MiB: "
+                        "reads 256 MiB, writes 256 MiB per launch)")
     return p.parse_args()
 
 
@@ -284,8 +292,139 @@ def extra_configs(mlk, workloads, steps, peak):
     return res
 
 
+CALIB_FLOATS = 64 << 20  # 256 MiB per buffer
+
+
+def calibrate(mlk, steps):
+    """A plain streaming kernel of known traffic for scaling rocprofv3's
+    FETCH_SIZE / WRITE_SIZE: SiLU reads one 256 MiB buffer and writes
+    another, on three rotating buffer pairs."""
+    pairs = [(mlk.DeviceBuffer.empty((CALIB_FLOATS,)), mlk.DeviceBuffer.empty((CALIB_FLOATS,)))
+             for _ in range(N_SETS)]
+    for i, (x, _) in enumerate(pairs):
+        mlk.fill_normal(x, CALIB_FLOATS, 0.0, 1.0, 1000 + i)
+    mlk.synchronize()
+    e0, e1 = mlk.Event(), mlk.Event()
+    e0.record()
+    for i in range(steps):
+        x, y = pairs[i % N_SETS]
+        mlk.silu(x, y, CALIB_FLOATS)
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    print(json.dumps({"calibration": "silu", "bytes_read": 4 * CALIB_FLOATS,
+                      "bytes_written": 4 * CALIB_FLOATS, "launches": steps,
+                      "us_per_launch": round(ms * 1e3, 2),
+                      "GBps": round(8 * CALIB_FLOATS / (ms * 1e-3) / 1e9, 1)}))
+
+
+# ------------------------------------------------------- rocprof summaries
+
+CHAIN_KERNELS = {"GatherF32Vec": "gather_f32", "AddRmsNormVec": "add_rmsnorm",
+                 "RopeOneBatch": "rope", "StreamKernel": "swiglu"}
+
+PROFILE_COMMANDS = [
+    "rocprofv3 --kernel-trace --stats -T --output-format csv -d gpurun_out/prof_kt -o bench "
+    "-- python3 bench.py",
+    "rocprofv3 --pmc FETCH_SIZE -T --output-format csv -d gpurun_out/prof_fetch -o bench "
+    "-- python3 bench.py --no-cpu-baseline --steps 5 --warmup 1",
+    "rocprofv3 --pmc WRITE_SIZE -T --output-format csv -d gpurun_out/prof_write -o bench "
+    "-- python3 bench.py --no-cpu-baseline --steps 5 --warmup 1",
+    "rocprofv3 --pmc FETCH_SIZE -T --output-format csv -d gpurun_out/prof_cfetch -o calib "
+    "-- python3 bench.py --calibrate --steps 5",
+    "rocprofv3 --pmc WRITE_SIZE -T --output-format csv -d gpurun_out/prof_cwrite -o calib "
+    "-- python3 bench.py --calibrate --steps 5",
+    "python3 bench.py --rocprof-report gpurun_out/prof_kt gpurun_out/prof_fetch "
+    "gpurun_out/prof_write gpurun_out/prof_cfetch gpurun_out/prof_cwrite",
+]
+
+
+def _one_csv(d, suffix):
+    import glob
+    files = glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {d}")
+    return files[0]
+
+
+def _counter_means(d, counter):
+    """{(kernel, grid): mean counter value in KiB} of a --pmc run."""
+    import csv
+    sums = {}
+    for r in csv.DictReader(open(_one_csv(d, "counter_collection.csv"))):
+        if r["Counter_Name"] != counter:
+            continue
+        key = (r["Kernel_Name"], int(r["Grid_Size"]))
+        acc = sums.setdefault(key, [0.0, 0])
+        acc[0] += float(r["Counter_Value"])
+        acc[1] += 1
+    return {k: v[0] / v[1] for k, v in sums.items()}
+
+
+def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
+    import csv
+    cfg = workloads.CONFIGS["c3_prefill_8b"]
+    T = cfg["tokens"]
+    nbytes = op_bytes(workloads, cfg, T)
+    stats = {r["Name"]: r for r in csv.DictReader(open(_one_csv(kt_dir, "kernel_stats.csv")))}
+    # calibration: SiLU over 256 MiB reads and writes 256 MiB per launch
+    calib_kib = 4 * CALIB_FLOATS / 1024
+    cf = [v for (k, _), v in _counter_means(cfetch_dir, "FETCH_SIZE").items() if k == "StreamKernel"]
+    cw = [v for (k, _), v in _counter_means(cwrite_dir, "WRITE_SIZE").items() if k == "StreamKernel"]
+    f_factor, w_factor = cf[0] / calib_kib, cw[0] / calib_kib
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    rows = []
+    traffic = {}
+    for kname, op in CHAIN_KERNELS.items():
+        st = stats.get(kname)
+        fk = [v for (k, _), v in fetch.items() if k == kname]
+        wk = [v for (k, _), v in write.items() if k == kname]
+        if st is None or not fk or not wk:
+            continue
+        hbm = (fk[0] / f_factor + wk[0] / w_factor) * 1024
+        traffic[op] = hbm
+        avg_us = float(st["AverageNs"]) / 1e3
+        rows.append((op, kname, int(st["Calls"]), avg_us, float(st["MinNs"]) / 1e3,
+                     nbytes[op] / (avg_us * 1e-6) / 1e9, fk[0], wk[0], hbm, nbytes[op]))
+    out = os.path.join(ROOT, "profiles")
+    os.makedirs(out, exist_ok=True)
+    md = ["# Op chain, config 2 (Llama-3-8B shape, T = 4096): rocprofv3 summary", "",
+          "Commands (run from the repo root on one MI355X; the last line writes this file):", ""]
+    md += ["    " + c for c in PROFILE_COMMANDS]
+    md += ["", "Counter calibration (SiLU over 256 MiB: 256 MiB read + 256 MiB written per "
+           "launch): FETCH_SIZE reads %.4f x the true bytes, WRITE_SIZE %.4f x; HBM bytes "
+           "below are the counters divided by these factors." % (f_factor, w_factor), "",
+           "| op | kernel | calls | avg us | min us | algorithmic GB/s (avg) | FETCH_SIZE KiB | "
+           "WRITE_SIZE KiB | HBM bytes / launch | algorithmic bytes / launch |",
+           "|---|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        md.append("| %s | %s | %d | %.2f | %.2f | %.1f | %.0f | %.0f | %.0f | %d |" % r)
+    md += ["", "Other kernels in the same trace (input generation, not timed by bench.py):", ""]
+    for name, st in stats.items():
+        if name not in CHAIN_KERNELS:
+            md.append("- %s: %s calls, avg %.2f us" % (name, st["Calls"],
+                                                        float(st["AverageNs"]) / 1e3))
+    with open(os.path.join(out, "chain_c3_prefill_8b_rocprof.md"), "w") as f:
+        f.write("\n".join(md) + "\n")
+    sw = [r for r in rows if r[0] == "swiglu"][0]
+    with open(PMC_FILE, "w") as f:
+        json.dump({"kernel": "StreamKernel<SwiGluOp> (swiglu)", "workload": "c3_prefill_8b",
+                   "hbm_bytes_per_launch": round(traffic["swiglu"]),
+                   "algorithmic_bytes_per_launch": nbytes["swiglu"],
+                   "fetch_size_kib": round(sw[6], 1), "write_size_kib": round(sw[7], 1),
+                   "fetch_factor": round(f_factor, 5), "write_factor": round(w_factor, 5),
+                   "rocprof_avg_us": round(sw[3], 2),
+                   "per_op_hbm_bytes": {k: round(v) for k, v in traffic.items()},
+                   "commands": PROFILE_COMMANDS}, f, indent=1)
+    print("\n".join(md))
+
+
 def main():
     args = parse_args()
+    if args.rocprof_report:
+        rocprof_report(*args.rocprof_report)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build targets one GPU; --gpus {args.gpus} is not supported "
               "(the per-layer ops are row-independent: a data-parallel shard per GPU needs no "
@@ -293,6 +432,9 @@ def main():
         sys.exit(2)
     mlk = mlk_pkg
     mlk.set_device(0)
+    if args.calibrate:
+        calibrate(mlk, args.steps)
+        return
     peak = workloads.HBM_PEAK_GBS
     cfg = workloads.CONFIGS["c3_prefill_8b"]
     T = cfg["tokens"]
