@@ -214,7 +214,7 @@ def cpu_baseline(mlk, chain, cfg, T, workloads):
     t_st = timed(1, 3)
     return {"value": round(nbytes / t_mt / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": kind,
-            "sample": (f"full config-2 chain (T={T}, 8B shapes), median of 5 reps after 1 warmup; "
+            "sample": (f"full configs[2] chain (T={T}, Llama-3-8B shapes), median of 5 reps after 1 warmup; "
                        f"{build}, ParallelFor over tokens"),
             "ms_per_chain": round(t_mt * 1e3, 2),
             "single_thread_value": round(nbytes / t_st / 1e9, 3),
