@@ -19,6 +19,20 @@ if ROOT not in sys.path:
 GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 
+def load_workloads():
+    """cpp-minilamma_amd/workloads.py (pure Python: importable without the
+    built HIP library)."""
+    import importlib.util
+    name = "cpp_minilamma_amd_workloads"
+    if name not in sys.modules:
+        spec = importlib.util.spec_from_file_location(
+            name, os.path.join(ROOT, "cpp-minilamma_amd", "workloads.py"))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        sys.modules[name] = mod
+    return sys.modules[name]
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a GPU (MI355X) and the built HIP library")
 

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import __graft_entry__ as entry
+from conftest import load_workloads
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INCLUDE = os.path.join(ROOT, "include")
@@ -143,7 +144,7 @@ def test_bench_refuses_more_than_one_gpu():
 
 
 def test_workload_byte_counts_match_the_baseline_table():
-    w = __import__("cpp_minilamma_amd.workloads", fromlist=["x"])
+    w = load_workloads()
     c3 = w.CONFIGS["c3_prefill_8b"]
     c5 = w.CONFIGS["c5_70b"]
     assert w.bytes_add_rmsnorm(4096, 4096) == 268_451_840
@@ -161,7 +162,7 @@ def test_workload_byte_counts_match_the_baseline_table():
 
 
 def test_zipf_ids_are_deterministic_and_in_range():
-    w = __import__("cpp_minilamma_amd.workloads", fromlist=["x"])
+    w = load_workloads()
     a = w.zipf_ids(4096, 128256, 1.1, 7)
     b = w.zipf_ids(4096, 128256, 1.1, 7)
     assert a.dtype == np.int32 and (a == b).all()
