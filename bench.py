@@ -88,11 +88,14 @@ class Chain:
 
     OPS = ("gather_f32", "add_rmsnorm", "rope", "swiglu")
 
-    def __init__(self, mlk, cfg, T, seed, n_sets=N_SETS, ids=None, positions=None):
+    def __init__(self, mlk, cfg, T, seed, n_sets=N_SETS, ids=None, positions=None, table=None):
         self.mlk, self.cfg, self.T = mlk, cfg, T
         D = cfg["dim"]
-        self.table = mlk.DeviceBuffer.empty((cfg["vocab"], D))
-        mlk.fill_normal(self.table, cfg["vocab"] * D, 0.0, 0.02, seed)
+        if table is not None:
+            self.table = table
+        else:
+            self.table = mlk.DeviceBuffer.empty((cfg["vocab"], D))
+            mlk.fill_normal(self.table, cfg["vocab"] * D, 0.0, 0.02, seed)
         self.norm_w = mlk.DeviceBuffer.empty((D,))
         mlk.fill_normal(self.norm_w, D, 1.0, 0.1, seed + 100)
         self.ids_host = ids if ids is not None else workloads.zipf_ids(T, cfg["vocab"], 1.1, seed)
@@ -134,6 +137,25 @@ class Chain:
         stop.record(self.stream)
         stop.synchronize()
         return start.elapsed_ms(stop)
+
+    def run_graph(self, steps, warmup=3):
+        """One chain step captured into a HIP graph on the chain's stream and
+        replayed `steps` times between two events; returns ms per step."""
+        mlk = self.mlk
+        with mlk.Graph.capture(self.stream) as graph:
+            for op in self.OPS:
+                self.launch(self.sets[0], op)
+        for _ in range(warmup):
+            graph.launch()
+        self.stream.synchronize()
+        start, stop = mlk.Event(), mlk.Event()
+        start.record(self.stream)
+        for _ in range(steps):
+            graph.launch()
+        stop.record(self.stream)
+        stop.synchronize()
+        graph.close()
+        return start.elapsed_ms(stop) / steps
 
     def run_ops(self, steps, warmup=3):
         """Per-kernel launch duration: each op launched `steps` times back to
@@ -367,6 +389,14 @@ def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
     T = cfg["tokens"]
     nbytes = op_bytes(workloads, cfg, T)
     stats = {r["Name"]: r for r in csv.DictReader(open(_one_csv(kt_dir, "kernel_stats.csv")))}
+    # per (kernel, grid) durations from the trace: the default run also
+    # launches the chain at decode sizes, so the C3 launches are the
+    # largest grid of each chain kernel
+    launches = {}
+    for r in csv.DictReader(open(_one_csv(kt_dir, "kernel_trace.csv"))):
+        key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
+        launches.setdefault(key, []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     # calibration: SiLU over 256 MiB reads and writes 256 MiB per launch
     calib_kib = 4 * CALIB_FLOATS / 1024
     cf = [v for (k, _), v in _counter_means(cfetch_dir, "FETCH_SIZE").items() if k == "StreamKernel"]
@@ -376,16 +406,23 @@ def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
     write = _counter_means(write_dir, "WRITE_SIZE")
     rows = []
     traffic = {}
+    small = []
     for kname, op in CHAIN_KERNELS.items():
-        st = stats.get(kname)
-        fk = [v for (k, _), v in fetch.items() if k == kname]
-        wk = [v for (k, _), v in write.items() if k == kname]
-        if st is None or not fk or not wk:
+        grids = sorted(g for (k, g) in launches if k == kname)
+        fk = [v for (k, g), v in fetch.items() if k == kname and g == max(g2 for (k2, g2) in fetch
+                                                                           if k2 == kname)]
+        wk = [v for (k, g), v in write.items() if k == kname and g == max(g2 for (k2, g2) in write
+                                                                           if k2 == kname)]
+        if not grids or not fk or not wk:
             continue
+        durs = launches[(kname, grids[-1])]
+        for g in grids[:-1]:
+            d = launches[(kname, g)]
+            small.append((op, kname, g, len(d), sum(d) / len(d)))
         hbm = (fk[0] / f_factor + wk[0] / w_factor) * 1024
         traffic[op] = hbm
-        avg_us = float(st["AverageNs"]) / 1e3
-        rows.append((op, kname, int(st["Calls"]), avg_us, float(st["MinNs"]) / 1e3,
+        avg_us = sum(durs) / len(durs)
+        rows.append((op, kname, len(durs), avg_us, min(durs),
                      nbytes[op] / (avg_us * 1e-6) / 1e9, fk[0], wk[0], hbm, nbytes[op]))
     out = os.path.join(ROOT, "profiles")
     os.makedirs(out, exist_ok=True)
@@ -400,6 +437,11 @@ def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
            "|---|---|---|---|---|---|---|---|---|---|"]
     for r in rows:
         md.append("| %s | %s | %d | %.2f | %.2f | %.1f | %.0f | %.0f | %.0f | %d |" % r)
+    md += ["", "The same kernels at the decode sizes of configs[1] (T = 1 and 64; smaller grids, "
+           "eager and graph-replayed launches together):", "",
+           "| op | kernel | grid (threads) | launches | avg us |", "|---|---|---|---|---|"]
+    for r in small:
+        md.append("| %s | %s | %d | %d | %.2f |" % r)
     md += ["", "Other kernels in the same trace (input generation, not timed by bench.py):", ""]
     for name, st in stats.items():
         if name not in CHAIN_KERNELS:
@@ -475,6 +517,22 @@ def main():
                      "traffic": traffic_from_profiles()},
         "device": mlk.device_info(0),
     }
+    # the same chain as a decode step, T = 1 and 64 tokens at
+    # positions uniform in [0, 8191] (latency-bound: µs per chain, eager
+    # launches and one HIP graph replay per step)
+    c2 = workloads.CONFIGS["c2_decode_8b"]
+    decode = {}
+    for t in (1, 64):
+        pos = workloads.decode_positions(t, c2["max_pos"], c2["seed"])
+        dch = Chain(mlk, c2, t, seed=c2["seed"], n_sets=2, positions=pos, table=chain.table)
+        n = max(args.steps, 100)
+        eager = dch.run(n, args.warmup) / n
+        graph = dch.run_graph(n)
+        decode[str(t)] = {"us_per_chain_eager": round(eager * 1e3, 2),
+                          "us_per_chain_graph": round(graph * 1e3, 2),
+                          "chain_bytes": workloads.bytes_chain(c2, t)}
+        del dch
+    result["decode_c2_8b"] = decode
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(mlk, chain, cfg, T, workloads)
     del chain

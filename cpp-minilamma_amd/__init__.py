@@ -86,6 +86,10 @@ _SIGNATURES = {
     "mlk_event_record": [_vp, _vp],
     "mlk_event_synchronize": [_vp],
     "mlk_event_elapsed_ms": [C.POINTER(_f), _vp, _vp],
+    "mlk_graph_begin_capture": [_vp],
+    "mlk_graph_end_capture": [_vp, C.POINTER(_vp)],
+    "mlk_graph_launch": [_vp, _vp],
+    "mlk_graph_destroy": [_vp],
 }
 
 
@@ -263,6 +267,50 @@ class Event:
             self.close()
         except Exception:
             pass
+
+
+class Graph:
+    """An executable HIP graph captured from the ops issued on `stream`
+    inside `with Graph.capture(stream) as g:`; replay with g.launch()."""
+
+    def __init__(self, stream):
+        self.stream = stream
+        self.handle = None
+
+    @classmethod
+    def capture(cls, stream):
+        return _Capture(cls(stream))
+
+    def launch(self, stream=None):
+        check(lib.mlk_graph_launch(self.handle, _sp(stream or self.stream)), "Graph.launch")
+
+    def close(self):
+        if self.handle:
+            lib.mlk_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _Capture:
+    def __init__(self, graph):
+        self.graph = graph
+
+    def __enter__(self):
+        check(lib.mlk_graph_begin_capture(_sp(self.graph.stream)), "Graph.capture")
+        return self.graph
+
+    def __exit__(self, exc_type, exc, tb):
+        h = _vp()
+        st = lib.mlk_graph_end_capture(_sp(self.graph.stream), C.byref(h))
+        self.graph.handle = h.value
+        if exc_type is None:
+            check(st, "Graph.capture")
+        return False
 
 
 def _sp(stream):

@@ -264,4 +264,45 @@ mlk_status mlk_event_elapsed_ms(float* ms, void* start, void* stop) {
     return err == hipSuccess ? MLK_OK : FromHip(err, "hipEventElapsedTime");
 }
 
+mlk_status mlk_graph_begin_capture(void* stream) {
+    if (stream == nullptr) {
+        return Fail(MLK_ERR_INVALID, "mlk_graph_begin_capture: the null stream cannot be captured");
+    }
+    const hipError_t err =
+        hipStreamBeginCapture(AsStream(stream), hipStreamCaptureModeThreadLocal);
+    return err == hipSuccess ? MLK_OK : FromHip(err, "hipStreamBeginCapture");
+}
+
+mlk_status mlk_graph_end_capture(void* stream, void** graph_exec) {
+    if (stream == nullptr || graph_exec == nullptr) {
+        return Fail(MLK_ERR_INVALID, "mlk_graph_end_capture: null stream or output");
+    }
+    *graph_exec = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t err = hipStreamEndCapture(AsStream(stream), &graph);
+    if (err != hipSuccess) return FromHip(err, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    const hipError_t destroy = hipGraphDestroy(graph);
+    if (err != hipSuccess) return FromHip(err, "hipGraphInstantiate");
+    if (destroy != hipSuccess) {
+        (void)hipGraphExecDestroy(exec);
+        return FromHip(destroy, "hipGraphDestroy");
+    }
+    *graph_exec = exec;
+    return MLK_OK;
+}
+
+mlk_status mlk_graph_launch(void* graph_exec, void* stream) {
+    if (graph_exec == nullptr) return Fail(MLK_ERR_INVALID, "mlk_graph_launch: null graph");
+    const hipError_t err = hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), AsStream(stream));
+    return err == hipSuccess ? MLK_OK : FromHip(err, "hipGraphLaunch");
+}
+
+mlk_status mlk_graph_destroy(void* graph_exec) {
+    if (graph_exec == nullptr) return MLK_OK;
+    const hipError_t err = hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec));
+    return err == hipSuccess ? MLK_OK : FromHip(err, "hipGraphExecDestroy");
+}
+
 }  // extern "C"

@@ -190,6 +190,17 @@ mlk_status mlk_event_record(void* event, void* stream);
 mlk_status mlk_event_synchronize(void* event);
 mlk_status mlk_event_elapsed_ms(float* ms, void* start, void* stop);
 
+/* HIP graphs for launch-bound sequences (decode steps issue a handful of
+ * microsecond kernels): capture the ops issued on `stream` (not the null
+ * stream) between begin and end into an executable graph, then replay it
+ * with one launch.  The ops above record kernels only (no memset or copy
+ * nodes), so a captured sequence replays exactly.  The kernels' pointer
+ * and size arguments are frozen at capture time. */
+mlk_status mlk_graph_begin_capture(void* stream);
+mlk_status mlk_graph_end_capture(void* stream, void** graph_exec);
+mlk_status mlk_graph_launch(void* graph_exec, void* stream);
+mlk_status mlk_graph_destroy(void* graph_exec);
+
 #ifdef __cplusplus
 }
 #endif
