@@ -95,34 +95,43 @@ __device__ inline float Decode1(const uint8_t* blk, int w) {
     }
 }
 
-// Decodes elements w..w+3 (w % 4 == 0) of a block held in LDS.
+// Decodes elements w..w+3 (w % 4 == 0) of a block held in LDS with typed
+// reads: every block starts at an even LDS offset (34, 18 and 20 are even),
+// so d and m are aligned u16 reads; Q4_1 code bytes sit at a multiple of 4
+// (20b + 4 + 4k) and are one u32 read, Q8_0 / Q4_0 code bytes two u16 reads.
 template <int QT>
 __device__ inline float4 Decode4(const uint8_t* blk, int w) {
 #pragma clang fp contract(off)
-    const float d = HalfBits(LoadU16(blk));
+    const float d = HalfBits(*reinterpret_cast<const uint16_t*>(blk));
+    uint32_t codes;  // four code bytes, little-endian
+    if (QT == MLK_Q4_1) {
+        codes = *reinterpret_cast<const uint32_t*>(blk + 4 + (w & 15));
+    } else {
+        const uint16_t* p =
+            reinterpret_cast<const uint16_t*>(blk + 2 + (QT == MLK_Q8_0 ? w : (w & 15)));
+        codes = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 16);
+    }
     float4 o;
     if (QT == MLK_Q8_0) {
-        const uint8_t* q = blk + 2 + w;
-        o.x = d * static_cast<float>(static_cast<int8_t>(q[0]));
-        o.y = d * static_cast<float>(static_cast<int8_t>(q[1]));
-        o.z = d * static_cast<float>(static_cast<int8_t>(q[2]));
-        o.w = d * static_cast<float>(static_cast<int8_t>(q[3]));
+        o.x = d * static_cast<float>(static_cast<int8_t>(codes & 0xFFu));
+        o.y = d * static_cast<float>(static_cast<int8_t>((codes >> 8) & 0xFFu));
+        o.z = d * static_cast<float>(static_cast<int8_t>((codes >> 16) & 0xFFu));
+        o.w = d * static_cast<float>(static_cast<int8_t>(codes >> 24));
     } else {
-        const int base = QT == MLK_Q4_0 ? 2 : 4;
-        const uint8_t* q = blk + base + (w & 15);
-        const uint32_t shift = w < 16 ? 0u : 4u;
+        // element w + j is the low nibble of byte j (w < 16) or its high nibble
+        const uint32_t nib = w < 16 ? codes : (codes >> 4);
         const int bias = QT == MLK_Q4_0 ? 8 : 0;
-        const float c0 = static_cast<float>(static_cast<int>((q[0] >> shift) & 15u) - bias);
-        const float c1 = static_cast<float>(static_cast<int>((q[1] >> shift) & 15u) - bias);
-        const float c2 = static_cast<float>(static_cast<int>((q[2] >> shift) & 15u) - bias);
-        const float c3 = static_cast<float>(static_cast<int>((q[3] >> shift) & 15u) - bias);
+        const float c0 = static_cast<float>(static_cast<int>(nib & 15u) - bias);
+        const float c1 = static_cast<float>(static_cast<int>((nib >> 8) & 15u) - bias);
+        const float c2 = static_cast<float>(static_cast<int>((nib >> 16) & 15u) - bias);
+        const float c3 = static_cast<float>(static_cast<int>((nib >> 24) & 15u) - bias);
         if (QT == MLK_Q4_0) {
             o.x = d * c0;
             o.y = d * c1;
             o.z = d * c2;
             o.w = d * c3;
         } else {
-            const float m = HalfBits(LoadU16(blk + 2));
+            const float m = HalfBits(*reinterpret_cast<const uint16_t*>(blk + 2));
             o.x = d * c0 + m;
             o.y = d * c1 + m;
             o.z = d * c2 + m;

@@ -32,18 +32,18 @@ constexpr int kWaves = kThreads / kWave;
 // 16 (1024 lanes: one float4 per lane at dim 4096).  Measured on MI355X at
 // [4096, 4096]: 16 waves x 1 float4 beats 1 wave x 16 float4 by 25%, and
 // non-temporal hints are worth another ~12%.
-template <int VPT, bool kDelta, bool kWriteBack>
-__global__ __launch_bounds__(1024) void AddRmsNormVec(float* residual,
-                                                      const float* __restrict__ delta,
-                                                      const float* __restrict__ weight, float* y,
-                                                      int64_t n_rows, int64_t dim, float eps) {
+template <int kWaves, int VPT, bool kDelta, bool kWriteBack>
+__global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(float* residual,
+                                                                const float* __restrict__ delta,
+                                                                const float* __restrict__ weight,
+                                                                float* y, int64_t n_rows,
+                                                                int64_t dim, float eps) {
 #pragma clang fp contract(off)
-    __shared__ double partial[2][16];
+    constexpr int lanes = kWave * kWaves;
+    __shared__ double partial[2][kWaves];
     const int tid = threadIdx.x;
-    const int lanes = blockDim.x;
-    const int waves = lanes / kWave;
     const int64_t dim4 = dim >> 2;
-    const double inv_dim = 1.0 / static_cast<double>(dim);
+    const double ddim = static_cast<double>(dim);
     int parity = 0;
     for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x, parity ^= 1) {
         float4* xr = reinterpret_cast<float4*>(residual + row * dim);
@@ -80,14 +80,8 @@ __global__ __launch_bounds__(1024) void AddRmsNormVec(float* residual,
                 ss += d * d;
             }
         }
-        ss = WaveSum(ss);
-        if (waves > 1) {
-            if ((tid % kWave) == 0) partial[parity][tid / kWave] = ss;
-            __syncthreads();
-            ss = 0.0;
-            for (int i = 0; i < waves; ++i) ss += partial[parity][i];
-        }
-        const double scale = 1.0 / sqrt(ss * inv_dim + static_cast<double>(eps));
+        ss = kWaves > 1 ? BlockSum<kWaves>(ss, partial[parity]) : WaveSum(ss);
+        const double scale = 1.0 / sqrt(ss / ddim + static_cast<double>(eps));
         const float4* wr = reinterpret_cast<const float4*>(weight);
         float4* yr = reinterpret_cast<float4*>(y + row * dim);
 #pragma unroll
@@ -116,7 +110,7 @@ __global__ __launch_bounds__(kThreads) void AddRmsNormAny(float* residual,
                                                           float eps) {
 #pragma clang fp contract(off)
     __shared__ double partial[2][kWaves];
-    const double inv_dim = 1.0 / static_cast<double>(dim);
+    const double ddim = static_cast<double>(dim);
     int parity = 0;
     for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x, parity ^= 1) {
         float* xr = residual + row * dim;
@@ -129,7 +123,7 @@ __global__ __launch_bounds__(kThreads) void AddRmsNormAny(float* residual,
             ss += a * a;
         }
         ss = BlockSum<kWaves>(ss, partial[parity]);
-        const double scale = 1.0 / sqrt(ss * inv_dim + static_cast<double>(eps));
+        const double scale = 1.0 / sqrt(ss / ddim + static_cast<double>(eps));
         for (int64_t i = threadIdx.x; i < dim; i += kThreads) {
             float r = xr[i];
             if (kDelta && !kWriteBack) r += delta[row * dim + i];
@@ -146,22 +140,27 @@ mlk_status Launch(float* residual, const float* delta, const float* weight, floa
     const bool vec = (dim % 4) == 0 && Aligned(residual, 16) && Aligned(weight, 16) &&
                      Aligned(y, 16) && (!kDelta || Aligned(delta, 16));
     const int64_t dim4 = dim / 4;
-    if (vec && dim4 <= 1024 * 16) {
-        // lanes: whole waves covering the row, at most 1024; then float4 per lane
-        const int64_t waves = (dim4 + kWave - 1) / kWave;
-        const int lanes = static_cast<int>((waves < 16 ? waves : 16) * kWave);
-        const int64_t vpt = (dim4 + lanes - 1) / lanes;
-#define MLK_NORM_CASE(V)                                                                      \
-    if (vpt <= (V)) {                                                                         \
-        hipLaunchKernelGGL((AddRmsNormVec<V, kDelta, kWriteBack>), dim3(grid), dim3(lanes), 0, \
-                           stream, residual, delta, weight, y, n_rows, dim, eps);             \
-        return CheckLaunch("AddRmsNormVec");                                                  \
+    if (vec && dim4 <= 1024 * 8) {  // beyond 8 float4 per lane the row would spill
+        // waves: the smallest power of two covering the row one float4 per
+        // lane, at most 16; then float4 per lane
+        int64_t waves = 1;
+        while (waves < 16 && waves * kWave < dim4) waves *= 2;
+        const int64_t vpt = (dim4 + waves * kWave - 1) / (waves * kWave);
+#define MLK_NORM_CASE(W, V)                                                                    \
+    if (waves == (W) && vpt <= (V)) {                                                         \
+        hipLaunchKernelGGL((AddRmsNormVec<W, V, kDelta, kWriteBack>), dim3(grid),              \
+                           dim3(kWave * (W)), 0, stream, residual, delta, weight, y, n_rows,   \
+                           dim, eps);                                                          \
+        return CheckLaunch("AddRmsNormVec");                                                   \
     }
-        MLK_NORM_CASE(1)
-        MLK_NORM_CASE(2)
-        MLK_NORM_CASE(4)
-        MLK_NORM_CASE(8)
-        MLK_NORM_CASE(16)
+        MLK_NORM_CASE(1, 1)
+        MLK_NORM_CASE(2, 1)
+        MLK_NORM_CASE(4, 1)
+        MLK_NORM_CASE(8, 1)
+        MLK_NORM_CASE(16, 1)
+        MLK_NORM_CASE(16, 2)
+        MLK_NORM_CASE(16, 4)
+        MLK_NORM_CASE(16, 8)
 #undef MLK_NORM_CASE
     }
     hipLaunchKernelGGL((AddRmsNormAny<kDelta, kWriteBack>), dim3(grid), dim3(kThreads), 0,
