@@ -19,20 +19,19 @@
 //
 // Table rows are read with normal loads (Zipf-distributed ids repeat hot
 // rows, which then come from L2 / the MALL); output rows are written with
-// // non-temporal stores.  One wave takes one token (so a T = 4096 batch is
-// resident at once and the LDS barriers are wave-local).  The row's packed
-// blocks (34/18/20 B, so unaligned inside the row) are staged into LDS with 16-byte loads when the
-// row stride allows it, then every lane decodes four consecutive outputs
-// and writes them as one float4, so both the HBM reads and the writes are
-// fully coalesced.
+// non-temporal stores.  A 1024-lane workgroup takes one token row at a time;
+// each lane decodes four consecutive outputs of one block with aligned u16 /
+// u32 loads of the scale(s) and code bytes and writes them as one float4.
+// (An LDS-staged variant -- 16-byte loads of the packed row, barrier, decode
+// from LDS -- measured 15-25% slower on MI355X: the gather is write-bound
+// and the staging round trip only added latency.)
 #include "mlk_common.h"
 
 namespace mlk {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kQThreads = 64;      // one wave per token row in the quantized gather
-constexpr int kChunkBlocks = 128;  // 4096 elements staged per LDS round
+constexpr int kQThreads = 1024;  // one float4 per lane of a 4096-wide row
 
 template <int QT>
 struct Fmt;
@@ -76,7 +75,7 @@ __device__ inline uint32_t LoadU16(const uint8_t* p) {
     return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);
 }
 
-// Decodes element w (0..31) of a block held in LDS.
+// Decodes element w (0..31) of a block with byte loads (any alignment).
 template <int QT>
 __device__ inline float Decode1(const uint8_t* blk, int w) {
 #pragma clang fp contract(off)
@@ -95,18 +94,25 @@ __device__ inline float Decode1(const uint8_t* blk, int w) {
     }
 }
 
-// Decodes elements w..w+3 (w % 4 == 0) of a block held in LDS with typed
-// reads: every block starts at an even LDS offset (34, 18 and 20 are even),
-// so d and m are aligned u16 reads; Q4_1 code bytes sit at a multiple of 4
-// (20b + 4 + 4k) and are one u32 read, Q8_0 / Q4_0 code bytes two u16 reads.
+// Decodes elements w..w+3 (w % 4 == 0) of block `blk` straight from global
+// memory with aligned loads: every block starts at an even byte offset
+// (34, 18 and 20 are even and rows start 16-byte aligned), so d and m are
+// u16 loads; Q4_1 blocks start 4-byte aligned (20b) so d|m and the four code
+// bytes (20b + 4 + 4k) are one u32 each, Q8_0 / Q4_0 code bytes two u16.
+// The block's bytes are shared by 8 neighbouring lanes, so these small
+// loads hit in L1 after the first.
 template <int QT>
 __device__ inline float4 Decode4(const uint8_t* blk, int w) {
 #pragma clang fp contract(off)
-    const float d = HalfBits(*reinterpret_cast<const uint16_t*>(blk));
+    float d, m = 0.0f;
     uint32_t codes;  // four code bytes, little-endian
     if (QT == MLK_Q4_1) {
+        const uint32_t dm = *reinterpret_cast<const uint32_t*>(blk);
+        d = HalfBits(dm & 0xFFFFu);
+        m = HalfBits(dm >> 16);
         codes = *reinterpret_cast<const uint32_t*>(blk + 4 + (w & 15));
     } else {
+        d = HalfBits(*reinterpret_cast<const uint16_t*>(blk));
         const uint16_t* p =
             reinterpret_cast<const uint16_t*>(blk + 2 + (QT == MLK_Q8_0 ? w : (w & 15)));
         codes = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 16);
@@ -131,7 +137,6 @@ __device__ inline float4 Decode4(const uint8_t* blk, int w) {
             o.z = d * c2;
             o.w = d * c3;
         } else {
-            const float m = HalfBits(*reinterpret_cast<const uint16_t*>(blk + 2));
             o.x = d * c0 + m;
             o.y = d * c1 + m;
             o.z = d * c2 + m;
@@ -141,19 +146,19 @@ __device__ inline float4 Decode4(const uint8_t* blk, int w) {
     return o;
 }
 
+// A workgroup takes one token row per iteration (grid-stride over tokens).
+// vec: dim % 4 == 0 and aligned buffers -> one float4 per lane per step
+// with Decode4; otherwise one element per lane with Decode1 (byte loads).
 template <int QT>
 __global__ __launch_bounds__(kQThreads) void GatherQuantKernel(const uint8_t* __restrict__ blocks,
-                                                              int64_t vocab, int64_t dim,
-                                                              const int32_t* __restrict__ ids,
-                                                              int32_t token, int64_t n_tokens,
-                                                              float* __restrict__ out,
-                                                              int32_t* err, int wide, int vec) {
+                                                               int64_t vocab, int64_t dim,
+                                                               const int32_t* __restrict__ ids,
+                                                               int32_t token, int64_t n_tokens,
+                                                               float* __restrict__ out,
+                                                               int32_t* err, int vec) {
     constexpr int kBB = Fmt<QT>::kBytes;
-    __shared__ uint4 stage[(kChunkBlocks * kBB + 15) / 16];
-    uint8_t* lds = reinterpret_cast<uint8_t*>(stage);
     const int tid = threadIdx.x;
-    const int64_t nb = (dim + 31) / 32;
-    const int64_t row_bytes = nb * kBB;
+    const int64_t row_bytes = ((dim + 31) / 32) * kBB;
     for (int64_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
         const int32_t id = ids != nullptr ? ids[t] : token;
         float* dst = out + t * dim;
@@ -163,33 +168,15 @@ __global__ __launch_bounds__(kQThreads) void GatherQuantKernel(const uint8_t* __
             continue;
         }
         const uint8_t* row = blocks + static_cast<int64_t>(id) * row_bytes;
-        for (int64_t c0 = 0; c0 < nb; c0 += kChunkBlocks) {
-            const int nbc = static_cast<int>(nb - c0 < kChunkBlocks ? nb - c0 : kChunkBlocks);
-            const int bytes = nbc * kBB;
-            const uint8_t* src = row + c0 * kBB;
-            __syncthreads();  // the previous chunk has been decoded
-            if (wide) {
-                // row_bytes and the chunk offset are multiples of 16 here
-                const int n16 = bytes / 16;
-                const uint4* s16 = reinterpret_cast<const uint4*>(src);
-                for (int i = tid; i < n16; i += kQThreads) stage[i] = s16[i];
-                for (int i = n16 * 16 + tid; i < bytes; i += kQThreads) lds[i] = src[i];
-            } else {
-                for (int i = tid; i < bytes; i += kQThreads) lds[i] = src[i];
+        if (vec) {
+            float4* d4 = reinterpret_cast<float4*>(dst);
+            for (int64_t j = tid; j < dim / 4; j += kQThreads) {
+                const int64_t e = 4 * j;
+                StoreNT(d4 + j, Decode4<QT>(row + (e >> 5) * kBB, static_cast<int>(e & 31)));
             }
-            __syncthreads();
-            const int64_t e0 = c0 * 32;
-            const int n_el = static_cast<int>(dim - e0 < nbc * 32 ? dim - e0 : nbc * 32);
-            if (vec) {
-                float4* d4 = reinterpret_cast<float4*>(dst + e0);
-                for (int j = tid; j < n_el / 4; j += kQThreads) {
-                    const int e = 4 * j;
-                    StoreNT(d4 + j, Decode4<QT>(lds + (e >> 5) * kBB, e & 31));
-                }
-            } else {
-                for (int e = tid; e < n_el; e += kQThreads) {
-                    dst[e0 + e] = Decode1<QT>(lds + (e >> 5) * kBB, e & 31);
-                }
+        } else {
+            for (int64_t e = tid; e < dim; e += kQThreads) {
+                dst[e] = Decode1<QT>(row + (e >> 5) * kBB, static_cast<int>(e & 31));
             }
         }
     }
@@ -426,24 +413,24 @@ mlk_status mlk_gather_quant(int32_t quant_type, const void* blocks, int64_t voca
     const mlk_status st =
         CheckGather("mlk_gather_quant", blocks, vocab, dim, ids, token, n_tokens, out);
     if (st != MLK_OK || n_tokens == 0) return st;
-    const int64_t row_bytes = ((dim + 31) / 32) * BlockBytes(quant_type);
-    const int wide = (row_bytes % 16 == 0 && Aligned(blocks, 16)) ? 1 : 0;
-    const int vec = (dim % 4 == 0 && Aligned(out, 16)) ? 1 : 0;
-    const unsigned grid = FullGrid(n_tokens, 1);
+    // the vector path reads d|m and codes as aligned u16/u32 words
+    const int vec = (dim % 4 == 0 && Aligned(out, 16) &&
+                     Aligned(blocks, quant_type == MLK_Q4_1 ? 4 : 2)) ? 1 : 0;
+    const unsigned grid = GridFor(n_tokens, 1, 8);
     const hipStream_t s = AsStream(stream);
     const uint8_t* b = static_cast<const uint8_t*>(blocks);
     switch (quant_type) {
         case MLK_Q8_0:
             hipLaunchKernelGGL(GatherQuantKernel<MLK_Q8_0>, dim3(grid), dim3(kQThreads), 0, s, b,
-                               vocab, dim, ids, token, n_tokens, out, err, wide, vec);
+                               vocab, dim, ids, token, n_tokens, out, err, vec);
             break;
         case MLK_Q4_0:
             hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_0>, dim3(grid), dim3(kQThreads), 0, s, b,
-                               vocab, dim, ids, token, n_tokens, out, err, wide, vec);
+                               vocab, dim, ids, token, n_tokens, out, err, vec);
             break;
         default:
             hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_1>, dim3(grid), dim3(kQThreads), 0, s, b,
-                               vocab, dim, ids, token, n_tokens, out, err, wide, vec);
+                               vocab, dim, ids, token, n_tokens, out, err, vec);
             break;
     }
     return CheckLaunch("GatherQuantKernel");

@@ -476,3 +476,22 @@ def test_empty_batches_are_no_ops(mlk):
     mlk.rope(d, d, 0, 1, 1, 8, pos0=0)
     mlk.gather_f32(d, 2, 8, d, 0, None)
     assert_bits_equal(d.download(), values((2, 8)), "unchanged")
+
+
+@pytest.mark.parametrize("qtype", ["q8_0", "q4_0", "q4_1"])
+@pytest.mark.parametrize("offset", [1, 2, 4])
+def test_gather_quant_unaligned_table(mlk, orc, qtype, offset):
+    """A table that starts 1, 2 or 4 bytes into an allocation (odd offsets
+    force the byte-load path, 2 keeps u16 words aligned but not the Q4_1 u32
+    words)."""
+    rng = np.random.default_rng(offset)
+    vocab, dim = 7, 96
+    table = normal(rng, (vocab, dim), std=0.5)
+    blocks = orc.quantize(qtype, table)
+    buf = mlk.DeviceBuffer(blocks.nbytes + 16, np.uint8)
+    mlk.check(mlk.lib.mlk_memcpy(buf.ptr + offset, blocks.ctypes.data, blocks.nbytes, mlk.H2D))
+    ids = np.array([6, 0, 3, 3, 1], np.int32)
+    d_ids = mlk.DeviceBuffer.from_array(ids)
+    d_o = mlk.DeviceBuffer.empty((len(ids), dim))
+    mlk.gather_quant(qtype, buf.ptr + offset, vocab, dim, d_ids, len(ids), d_o)
+    assert_bits_equal(d_o.download(), orc.gather_quant(qtype, blocks, vocab, dim, ids), "unaligned")
