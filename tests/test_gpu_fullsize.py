@@ -13,11 +13,20 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_bits_equal, assert_terms_close, load_workloads
+from conftest import assert_bits_equal, assert_terms_close, load_workloads, max_ulp
 
 W = load_workloads()
 
 pytestmark = pytest.mark.gpu
+
+
+def ulp_report(what, got, want):
+    """Prints the distribution of ulp distances to the oracle (run pytest -s)."""
+    a = np.ascontiguousarray(got, np.float32).view(np.int32).astype(np.int64).reshape(-1)
+    b = np.ascontiguousarray(want, np.float32).view(np.int32).astype(np.int64).reshape(-1)
+    d = np.abs(a - b)
+    print(f"ULP {what}: n={d.size} exact={np.mean(d == 0):.6f} <=1ulp={np.mean(d <= 1):.6f} "
+          f"max={int(d.max())} max_abs_err={float(np.abs(got - want).max()):.3e}")
 
 
 def device_normal(mlk, shape, mean, std, seed):
@@ -40,6 +49,7 @@ def test_add_rmsnorm_full_size(mlk, orc, name):
     assert_bits_equal(x.download(), er, f"{name} residual")
     got = y.download()
     assert_terms_close(got, ey, np.abs(ey), f"{name} rmsnorm")
+    ulp_report(f"{name} rmsnorm", got, ey)
 
 
 @pytest.mark.parametrize("name", ["c3_prefill_8b", "c5_70b"])
@@ -53,7 +63,9 @@ def test_swiglu_full_size(mlk, orc, name):
     hg, hu = g.download(), u.download()
     del g, u
     exp = orc.swiglu(hg, hu)
-    assert_terms_close(y.download(), exp, np.abs(exp), f"{name} swiglu")
+    got = y.download()
+    assert_terms_close(got, exp, np.abs(exp), f"{name} swiglu")
+    ulp_report(f"{name} swiglu", got, exp)
 
 
 @pytest.mark.parametrize("name", ["c3_prefill_8b", "c5_70b"])
@@ -68,6 +80,8 @@ def test_rope_full_size(mlk, orc, name):
     eq, ek = orc.rope(hq, hk, H, KV, hd, pos0=0, theta=cfg["theta"])
     assert_terms_close(gq, eq, np.abs(eq), f"{name} rope q")
     assert_terms_close(gk, ek, np.abs(ek), f"{name} rope k")
+    ulp_report(f"{name} rope q", gq, eq)
+    ulp_report(f"{name} rope k", gk, ek)
     # a rotation keeps every head's norm
     for before, after, heads in ((hq, gq, H), (hk, gk, KV)):
         n0 = (before.reshape(T, heads, hd).astype(np.float64) ** 2).sum(-1)
