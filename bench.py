@@ -196,6 +196,14 @@ def summarize(per_op, nbytes, peak):
     return out
 
 
+def add_unique(entry, unique_bytes, peak):
+    """Zipf ids repeat hot rows: beside the algorithmic figure, the bytes and
+    GB/s when each distinct table row is counted once."""
+    gbs = unique_bytes / (entry["us"] * 1e-6) / 1e9
+    entry.update(unique_row_bytes=unique_bytes, unique_row_GBps=round(gbs, 1),
+                 unique_row_frac_of_peak=round(gbs / peak, 4))
+
+
 # ------------------------------------------------------------ CPU baseline
 
 def cpu_baseline(mlk, chain, cfg, T, workloads):
@@ -283,7 +291,8 @@ def extra_configs(mlk, workloads, steps, peak):
     T, V, D = c4["tokens"], c4["vocab"], c4["dim"]
     table = mlk.DeviceBuffer.empty((V, D))
     mlk.fill_normal(table, V * D, 0.0, 0.02, c4["seed"])
-    ids = mlk.DeviceBuffer.from_array(workloads.zipf_ids(T, V, 1.1, c4["seed"]))
+    ids_host = workloads.zipf_ids(T, V, 1.1, c4["seed"])
+    ids = mlk.DeviceBuffer.from_array(ids_host)
     outs = [mlk.DeviceBuffer.empty((T, D)) for _ in range(N_SETS)]
     st = mlk.Stream()
     q = {}
@@ -301,6 +310,7 @@ def extra_configs(mlk, workloads, steps, peak):
         e1.synchronize()
         ms = e0.elapsed_ms(e1) / steps
         q[qt] = summarize({qt: ms}, {qt: workloads.bytes_gather_quant(qt, T, D)}, peak)[qt]
+        add_unique(q[qt], workloads.bytes_gather_unique(ids_host, D, qt), peak)
         del blocks
     res["c4_quant_gather"] = q
     del table
@@ -485,6 +495,7 @@ def main():
     nbytes = op_bytes(workloads, cfg, T)
     chain_bytes = sum(nbytes.values())
     ops = summarize(chain.run_ops(args.steps), nbytes, peak)
+    add_unique(ops["gather_f32"], workloads.bytes_gather_unique(chain.ids_host, cfg["dim"]), peak)
     value = chain_bytes * args.steps / (total_ms * 1e-3) / 1e9
     sw = ops["swiglu"]
     result = {

@@ -74,6 +74,16 @@ def bytes_gather_quant(qtype, T, D):
     return T * (-(-D // 32) * BLOCK_BYTES[qtype] + 4 * D) + 4 * T
 
 
+def bytes_gather_unique(ids, D, qtype=None):
+    """Bytes a gather must move when every distinct row is read once (a
+    Zipf(1.1) batch repeats hot rows, which then come from cache): distinct
+    rows of the table, all T output rows, the ids."""
+    ids = np.asarray(ids)
+    T, rows = ids.size, np.unique(ids).size
+    row_bytes = 4 * D if qtype is None else -(-D // 32) * BLOCK_BYTES[qtype]
+    return rows * row_bytes + 4 * T * D + 4 * T
+
+
 def bytes_chain(cfg, T, with_gather=True):
     b = (bytes_add_rmsnorm(T, cfg["dim"]) + bytes_rope(T, cfg["n_heads"], cfg["n_kv_heads"],
                                                         cfg["head_dim"])

@@ -170,3 +170,15 @@ def test_zipf_ids_are_deterministic_and_in_range():
     # Zipf: id 0 is the most frequent and the ranks decay
     counts = np.bincount(a, minlength=10)
     assert counts[0] == counts.max() and counts[0] > counts[9]
+
+
+def test_unique_row_bytes_count_each_distinct_row_once():
+    w = load_workloads()
+    ids = np.array([5, 5, 5, 9, 0], np.int32)
+    # 3 distinct rows read, 5 rows written, 5 ids
+    assert w.bytes_gather_unique(ids, 64) == 3 * 256 + 5 * 256 + 20
+    assert w.bytes_gather_unique(ids, 64, "q8_0") == 3 * 2 * 34 + 5 * 256 + 20
+    # with no repeats it is the algorithmic figure
+    ids = np.arange(7, dtype=np.int32)
+    assert w.bytes_gather_unique(ids, 4096) == w.bytes_gather_f32(7, 4096)
+    assert w.bytes_gather_unique(ids, 4096, "q4_1") == w.bytes_gather_quant("q4_1", 7, 4096)
