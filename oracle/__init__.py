@@ -75,6 +75,13 @@ class _Oracle:
                              _f32p, _f32p, _i32, _i32, _i32, _i32p, C.c_float,
                              _f32p, _f32p, _f32p, _i64, _i64, C.c_int])
         self.parallel_threads = _bind(lib, "orc_parallel_threads", C.c_int, [C.c_int])
+        self._linear_quant = _bind(lib, "orc_linear_quant", C.c_int,
+                                   [C.c_int, _f32p, _u8p, C.c_void_p, _f32p, _i64, _i64, _i64,
+                                    C.c_int])
+        self._linear_f32 = _bind(lib, "orc_linear_f32", C.c_int,
+                                 [_f32p, _f32p, C.c_void_p, _f32p, _i64, _i64, _i64, C.c_int])
+        self._matmul_f32 = _bind(lib, "orc_matmul_f32", C.c_int,
+                                 [_f32p, _f32p, _f32p, _i64, _i64, _i64, C.c_int])
 
     def fp16_to_fp32_array(self, codes):
         codes = np.ascontiguousarray(codes, dtype=np.uint16)
@@ -185,6 +192,35 @@ class _Oracle:
                           ptr, pos0, theta, rope_type))
         return q, k
 
+    # ---- linear ------------------------------------------------------------
+    def linear_quant(self, qtype, x, blocks, out_features, bias=None, n_threads=0):
+        """y = x @ dequant(W)^T (+ bias) for x [rows, in] (or [in])."""
+        x = _f32(x)
+        rows, in_f = (1, x.shape[0]) if x.ndim == 1 else x.shape
+        y = np.empty((rows, out_features), np.float32)
+        b = None if bias is None else _f32(bias)
+        _check(self._linear_quant(QUANT_TYPES[qtype], x.reshape(-1), _u8(blocks),
+                                  None if b is None else b.ctypes.data, y.reshape(-1), rows, in_f,
+                                  out_features, n_threads))
+        return y.reshape(-1) if x.ndim == 1 else y
+
+    def linear_f32(self, x, w, bias=None, n_threads=0):
+        """y = x @ W^T (+ bias), W [out, in]."""
+        x, w = _f32(x), _f32(w)
+        rows, in_f = (1, x.shape[0]) if x.ndim == 1 else x.shape
+        y = np.empty((rows, w.shape[0]), np.float32)
+        b = None if bias is None else _f32(bias)
+        _check(self._linear_f32(x.reshape(-1), w.reshape(-1), None if b is None else b.ctypes.data,
+                                y.reshape(-1), rows, in_f, w.shape[0], n_threads))
+        return y.reshape(-1) if x.ndim == 1 else y
+
+    def matmul_f32(self, a, b, n_threads=0):
+        a, b = _f32(a), _f32(b)
+        c = np.empty((a.shape[0], b.shape[1]), np.float32)
+        _check(self._matmul_f32(a.reshape(-1), b.reshape(-1), c.reshape(-1), a.shape[0],
+                                a.shape[1], b.shape[1], n_threads))
+        return c
+
     # ---- CPU baseline ------------------------------------------------------
     def chain(self, bufs, n_tokens, n_threads):
         return self._chain(*_chain_args(bufs, n_tokens, n_threads))
@@ -225,6 +261,36 @@ class _Reference:
                             [_f32p, _i64, _i64, _i32p, _f32p, _f32p, _f32p, _f32p, C.c_float,
                              _f32p, _f32p, C.c_int, C.c_int, C.c_int, _i32p, C.c_float,
                              _f32p, _f32p, _f32p, _i64, _i64, C.c_int])
+        self._linear_quant = _bind(lib, "ref_linear_quant", C.c_int,
+                                   [C.c_int, _f32p, _u8p, _f32p, C.c_int, C.c_int, C.c_int,
+                                    C.c_int])
+        self._linear_f32 = _bind(lib, "ref_linear_f32", C.c_int,
+                                 [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int])
+        self._matmul_f32 = _bind(lib, "ref_matmul_f32", C.c_int,
+                                 [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int])
+
+    def linear_quant(self, qtype, x, blocks, out_features, n_threads=0):
+        x = _f32(x)
+        rows, in_f = (1, x.shape[0]) if x.ndim == 1 else x.shape
+        y = np.empty((rows, out_features), np.float32)
+        _check(self._linear_quant(QUANT_TYPES[qtype], x.reshape(-1), _u8(blocks), y.reshape(-1),
+                                  rows, in_f, out_features, n_threads))
+        return y.reshape(-1) if x.ndim == 1 else y
+
+    def linear_f32(self, x, w):
+        x, w = _f32(x), _f32(w)
+        rows, in_f = (1, x.shape[0]) if x.ndim == 1 else x.shape
+        y = np.empty((rows, w.shape[0]), np.float32)
+        _check(self._linear_f32(x.reshape(-1), w.reshape(-1), y.reshape(-1), rows, in_f,
+                                w.shape[0]))
+        return y.reshape(-1) if x.ndim == 1 else y
+
+    def matmul_f32(self, a, b):
+        a, b = _f32(a), _f32(b)
+        c = np.empty((a.shape[0], b.shape[1]), np.float32)
+        _check(self._matmul_f32(a.reshape(-1), b.reshape(-1), c.reshape(-1), a.shape[0],
+                                a.shape[1], b.shape[1]))
+        return c
 
     def rmsnorm_row(self, x, w, eps):
         x = _f32(x)

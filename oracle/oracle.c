@@ -490,6 +490,171 @@ int orc_rope(float* q, float* k, int64_t n_tokens, int32_t n_heads, int32_t n_kv
     return ORC_OK;
 }
 
+/* ------------------------------------------------------------- linear */
+
+/* thread_pool/thread_pool.cc:31-90 ParallelFor: n tasks in static
+ * contiguous chunks, the first n % threads chunks one longer; serial when
+ * there are fewer than 16 tasks per thread. */
+typedef void (*par_fn)(void* ctx, int64_t begin, int64_t end);
+
+typedef struct {
+    par_fn fn;
+    void* ctx;
+    int64_t begin, end;
+} par_job;
+
+static void* par_run(void* arg)
+{
+    par_job* j = (par_job*)arg;
+    j->fn(j->ctx, j->begin, j->end);
+    return NULL;
+}
+
+static int par_for(int64_t n, int n_threads, par_fn fn, void* ctx)
+{
+    const int nt = orc_parallel_threads(n_threads);
+    if (n <= 0) {
+        return ORC_OK;
+    }
+    if (nt <= 1 || n / 16 < nt) {
+        fn(ctx, 0, n);
+        return ORC_OK;
+    }
+    par_job* jobs = (par_job*)calloc((size_t)nt, sizeof(par_job));
+    pthread_t* th = (pthread_t*)calloc((size_t)nt, sizeof(pthread_t));
+    if (jobs == NULL || th == NULL) {
+        free(jobs);
+        free(th);
+        return ORC_EINVAL;
+    }
+    const int64_t chunk = n / nt;
+    const int64_t remain = n % nt;
+    int64_t start = 0;
+    int started = 0;
+    for (int i = 0; i < nt; ++i) {
+        jobs[i].fn = fn;
+        jobs[i].ctx = ctx;
+        jobs[i].begin = start;
+        jobs[i].end = start + chunk + (i < remain ? 1 : 0);
+        start = jobs[i].end;
+        if (pthread_create(&th[i], NULL, par_run, &jobs[i]) != 0) {
+            break;
+        }
+        ++started;
+    }
+    for (int i = 0; i < started; ++i) {
+        pthread_join(th[i], NULL);
+    }
+    /* a thread that could not start leaves its chunk to the caller */
+    for (int i = started; i < nt; ++i) {
+        fn(ctx, jobs[i].begin, jobs[i].end);
+    }
+    free(jobs);
+    free(th);
+    return ORC_OK;
+}
+
+typedef struct {
+    int type;  /* -1: F32 weights */
+    const float* x;
+    const void* w;
+    const float* bias;
+    float* y;
+    int64_t in, out;
+} linear_job;
+
+static void linear_outputs(void* arg, int64_t begin, int64_t end)
+{
+    const linear_job* j = (const linear_job*)arg;
+    const int64_t nb = row_blocks(j->in);
+    for (int64_t index = begin; index < end; ++index) {
+        const int64_t row = index / j->out;
+        const int64_t col = index % j->out;
+        const float* xr = j->x + row * j->in;
+        float sum = 0.0f;
+        if (j->type < 0) {
+            const float* wr = (const float*)j->w + col * j->in;
+            for (int64_t k = 0; k < j->in; ++k) {
+                sum += xr[k] * wr[k];
+            }
+        } else {
+            const int64_t bb = kBlockBytes[j->type];
+            const uint8_t* wr = (const uint8_t*)j->w + col * nb * bb;
+            for (int64_t b = 0; b < nb; ++b) {
+                const int64_t left = j->in - b * ORC_QK;
+                const int len = left < ORC_QK ? (int)left : ORC_QK;
+                float w[ORC_QK];
+                dequant_block(j->type, wr + b * bb, len, w);
+                for (int i = 0; i < len; ++i) {
+                    sum += xr[b * ORC_QK + i] * w[i];
+                }
+            }
+        }
+        if (j->bias != NULL) {
+            sum += j->bias[col];
+        }
+        j->y[index] = sum;
+    }
+}
+
+static int linear_common(int type, const float* x, const void* w, const float* bias, float* y,
+                         int64_t rows, int64_t in, int64_t out, int n_threads)
+{
+    if (rows <= 0 || in <= 0 || out <= 0 || rows > 0x7FFFFFFF / out) {
+        return ORC_EINVAL;
+    }
+    linear_job job = {type, x, w, bias, y, in, out};
+    return par_for(rows * out, n_threads, linear_outputs, &job);
+}
+
+int orc_linear_quant(int quant_type, const float* x, const uint8_t* blocks, const float* bias,
+                     float* y, int64_t rows, int64_t in_features, int64_t out_features,
+                     int n_threads)
+{
+    if (quant_type < 0 || quant_type > 2) {
+        return ORC_EINVAL;
+    }
+    return linear_common(quant_type, x, blocks, bias, y, rows, in_features, out_features,
+                         n_threads);
+}
+
+int orc_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
+                   int64_t in_features, int64_t out_features, int n_threads)
+{
+    return linear_common(-1, x, w, bias, y, rows, in_features, out_features, n_threads);
+}
+
+typedef struct {
+    const float* a;
+    const float* b;
+    float* c;
+    int64_t k, n;
+} matmul_job;
+
+static void matmul_outputs(void* arg, int64_t begin, int64_t end)
+{
+    const matmul_job* j = (const matmul_job*)arg;
+    for (int64_t index = begin; index < end; ++index) {
+        const int64_t row = index / j->n;
+        const int64_t col = index % j->n;
+        float sum = 0.0f;
+        for (int64_t k = 0; k < j->k; ++k) {
+            sum += j->a[row * j->k + k] * j->b[k * j->n + col];
+        }
+        j->c[index] = sum;
+    }
+}
+
+int orc_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n,
+                   int n_threads)
+{
+    if (m <= 0 || k <= 0 || n <= 0 || m > 0x7FFFFFFF / n) {
+        return ORC_EINVAL;
+    }
+    matmul_job job = {a, b, c, k, n};
+    return par_for(m * n, n_threads, matmul_outputs, &job);
+}
+
 /* --------------------------------------------------- CPU baseline port */
 
 int orc_parallel_threads(int n_threads)

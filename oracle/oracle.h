@@ -34,6 +34,11 @@
  *   silu/swiglu/mul     closed forms (test/ops_test.cc:713-725), golden.
  *   softmax             float64 closed form, sum to one, golden.
  *   gather/add          closed forms (row copy, IEEE add).
+ *   linear / matmul     the compiled reference (bit for bit against its
+ *                       default build), float64 closed form within the
+ *                       fp32 summation bound, the reference's test vectors
+ *                       (test/cuda_quant_test.cc:33-39, 99-127;
+ *                       tests/test_cuda_linear.cc), bias and tail blocks.
  */
 #ifndef MINILAMMA_ORACLE_H
 #define MINILAMMA_ORACLE_H
@@ -113,6 +118,32 @@ int orc_rope_token(float* q, float* k, int32_t n_heads, int32_t n_kv_heads,
 int orc_rope(float* q, float* k, int64_t n_tokens, int32_t n_heads, int32_t n_kv_heads,
              int32_t head_dim, const int32_t* positions, int32_t pos0,
              float theta, int32_t rope_type);
+
+/* ---- linear layers ----
+ * Weights are [out_features, in_features] row-major (F32) or out_features
+ * rows of ceil(in_features/32) packed blocks (quantized).  x is
+ * [rows, in_features], y is [rows, out_features].  bias (may be NULL) is
+ * added to the finished fp32 sum, as src/cuda_quant.cu:99-110 and
+ * src/cuda_matmul.cc:79-90 add it on the host after the kernel.
+ * n_threads: ParallelFor over the rows * out_features outputs as the
+ * reference does (<= 0: hardware concurrency, 1: serial); the result does
+ * not depend on it. */
+
+/* src/quant.cc:393-463 LinearQuant, which is LinearQ80/Q40/Q41 of the
+ * reference's default build (src/quant.cc:645-650, 865-870, 1089-1094):
+ * sum += x[k] * Dequant(block, i) over k ascending, one fp32 accumulator per
+ * output, dequantized weights as DequantQ80/Q40/Q41 (src/quant.cc:369-391). */
+int orc_linear_quant(int quant_type, const float* x, const uint8_t* blocks, const float* bias,
+                     float* y, int64_t rows, int64_t in_features, int64_t out_features,
+                     int n_threads);
+/* matumal/matuml_ops.cc:146-163 LinearNative applied to each row of x
+ * (sum += x[k] * w[j, k], k ascending). */
+int orc_linear_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
+                   int64_t in_features, int64_t out_features, int n_threads);
+/* matumal/matuml_ops.cc:225-271 MatmulNative / MatmulThread:
+ * c[i, j] = sum_k a[i, k] * b[k, j], k ascending; a [m, k], b [k, n]. */
+int orc_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n,
+                   int n_threads);
 
 /* ---- CPU baseline (bench.py cpu_baseline leg, kind "port") ----
  * thread_pool/thread_pool.cc:31-90 ParallelFor: static contiguous chunks,

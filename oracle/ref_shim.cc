@@ -149,6 +149,45 @@ int ref_dequantize_flat(int type, const uint8_t* raw, int rows, int cols, float*
     });
 }
 
+// Quantized linear: LinearQ80/Q40/Q41 (src/quant.cc), y [rows, out].
+// n_threads > 0 sets the reference thread pool's size for the call.
+int ref_linear_quant(int type, const float* x, const uint8_t* raw, float* y, int rows, int in,
+                     int out, int n_threads) {
+    return Guard([&] {
+        const Tensor tx = Wrap(x, {rows, in});
+        const size_t n = static_cast<size_t>(out) * RowBlocks(in);
+        const std::vector<int> shape{out, in};
+        if (n_threads > 0) yan_lamma::SetThreadNum(n_threads);
+        Tensor r;
+        if (type == 0) {
+            r = yan_lamma::LinearQ80(tx, ToBlocks<Block_Q80>(raw, n), shape);
+        } else if (type == 1) {
+            r = yan_lamma::LinearQ40(tx, ToBlocks<Block_Q40>(raw, n), shape);
+        } else {
+            r = yan_lamma::LinearQ41(tx, ToBlocks<Block_Q41>(raw, n), shape);
+        }
+        yan_lamma::SetThreadNum(0);
+        Unwrap(r, y);
+    });
+}
+
+// F32 linear: Linear(x, W) (src/ops.cc:152-154, the default LinearDispatch
+// mode) on each row of x, since the reference's CPU Linear takes one row.
+int ref_linear_f32(const float* x, const float* w, float* y, int rows, int in, int out) {
+    return Guard([&] {
+        const Tensor tw = Wrap(w, {out, in});
+        for (int r = 0; r < rows; ++r) {
+            Unwrap(yan_lamma::Linear(Wrap(x + static_cast<size_t>(r) * in, {in}), tw),
+                   y + static_cast<size_t>(r) * out);
+        }
+    });
+}
+
+// Matmul(a, b) (src/ops.cc:76-80).
+int ref_matmul_f32(const float* a, const float* b, float* c, int m, int k, int n) {
+    return Guard([&] { Unwrap(yan_lamma::Matmul(Wrap(a, {m, k}), Wrap(b, {k, n})), c); });
+}
+
 // The per-token op chain as the reference's CPU forward runs it: each op
 // takes and returns Tensor objects (one heap allocation per result).  The
 // embedding row copy and the residual add live in src/forward.cc, which does

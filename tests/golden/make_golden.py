@@ -19,6 +19,15 @@ Fixture contents (numpy .npz, no pickles):
   rows_8b_70b.npz  RmsNorm / SwiGLU / Silu rows at the 8B and 70B widths,
                    RoPE heads at positions 0, 1, 4095, 8191 (theta 5e5) for
                    both layouts, softmax rows.
+  linear.npz       LinearQ80/Q40/Q41 (default build) on the weight and input
+                   patterns of the reference's own tests
+                   (test/cuda_quant_test.cc:33-39 at [131, in] for in in
+                   1, 17, 32, 33, 65; tests/cuda_test_support.h:43-47 at
+                   [7, 32] and [7, 86]) and on N(0, 0.02) Llama-3-8B-width
+                   rows; F32 Linear and Matmul on the shapes of
+                   tests/test_cuda_linear.cc and tests/test_cuda_matmul.cc.
+
+Usage: make_golden.py [name ...] writes only the named fixtures.
 """
 from __future__ import annotations
 
@@ -171,10 +180,71 @@ def rows_8b_70b(ref):
     return out
 
 
+def pattern_43(shape):
+    """test/cuda_quant_test.cc:33-39: ((i * 17 + 3) % 43 - 21) / 16."""
+    i = np.arange(int(np.prod(shape)), dtype=np.int64)
+    return (((i * 17 + 3) % 43 - 21).astype(np.float32) / np.float32(16)).reshape(shape)
+
+
+def pattern_sin(shape, phase=0.0):
+    """tests/cuda_test_support.h:43-47: sin(float(i) * 0.19f + phase) * 0.3f,
+    evaluated in float32 like the C++ expression, then sin in float64 and
+    rounded (std::sin of a float argument)."""
+    i = np.arange(int(np.prod(shape)), dtype=np.float32)
+    arg = i * np.float32(0.19) + np.float32(phase)
+    return (np.sin(arg.astype(np.float64)).astype(np.float32) * np.float32(0.3)).reshape(shape)
+
+
+def linear(ref):
+    out = {}
+    qts = ("q8_0", "q4_0", "q4_1")
+    for qt in qts:
+        for inf in (1, 17, 32, 33, 65):
+            w = pattern_43((131, inf))
+            blocks = ref.quantize(qt, w)
+            out[f"p43_{qt}_{inf}_w"] = blocks
+            for rows in (1, 3):
+                x = pattern_43((rows, inf))
+                out[f"p43_{qt}_{inf}_x{rows}"] = x
+                out[f"p43_{qt}_{inf}_y{rows}"] = ref.linear_quant(qt, x, blocks, 131)
+        for cols in (32, 86):
+            w = pattern_sin((7, cols), 0.8)
+            blocks = ref.quantize(qt, w)
+            x = pattern_sin((1, cols))
+            out[f"sin_{qt}_{cols}_w"] = blocks
+            out[f"sin_{qt}_{cols}_x"] = x
+            out[f"sin_{qt}_{cols}_y"] = ref.linear_quant(qt, x, blocks, 7)
+        rng = np.random.default_rng(5)
+        for out_f, inf, rows in ((32, 4096, 3), (8, 14336, 2)):
+            w = normal(rng, (out_f, inf), std=0.02)
+            blocks = ref.quantize(qt, w)
+            x = normal(rng, (rows, inf), std=1.0)
+            tag = f"n_{qt}_{out_f}x{inf}"
+            out[f"{tag}_w"], out[f"{tag}_x"] = blocks, x
+            out[f"{tag}_y"] = ref.linear_quant(qt, x, blocks, out_f)
+    out["sin_bias7"] = pattern_sin((7,), 0.4)
+    w = pattern_sin((17, 33), 0.3)
+    out["f32_w"] = w
+    out["f32_bias"] = pattern_sin((17,), 0.2)
+    out["f32_x"] = pattern_sin((1, 33))
+    out["f32_y"] = ref.linear_f32(out["f32_x"], w)
+    for m, k, n in ((3, 7, 5), (1, 33, 17)):
+        a, b = pattern_sin((m, k)), pattern_sin((k, n), 0.7)
+        out[f"mm_{m}x{k}x{n}_a"], out[f"mm_{m}x{k}x{n}_b"] = a, b
+        out[f"mm_{m}x{k}x{n}_c"] = ref.matmul_f32(a, b)
+    return out
+
+
+FIXTURES = (("tiny_chain", tiny_chain), ("quant", quant), ("dequant_kat", dequant_kat),
+            ("rows_8b_70b", rows_8b_70b), ("linear", linear))
+
+
 def main():
     ref = O.reference()
-    for name, fn in (("tiny_chain", tiny_chain), ("quant", quant), ("dequant_kat", dequant_kat),
-                     ("rows_8b_70b", rows_8b_70b)):
+    wanted = set(sys.argv[1:])
+    for name, fn in FIXTURES:
+        if wanted and name not in wanted:
+            continue
         path = os.path.join(HERE, f"{name}.npz")
         np.savez_compressed(path, **fn(ref))
         print(f"wrote {path} ({os.path.getsize(path)} bytes)")

@@ -462,3 +462,149 @@ def test_planted_q4_nibble_swap_fails_the_kat(orc):
     right = orc.dequantize("q4_0", q40, 1, 32)[0]
     swapped = np.concatenate([right[16:], right[:16]])  # high nibble read as the first 16
     assert not np.array_equal(swapped[:16], 0.5 * (i - 8))
+
+
+# ------------------------------------------------------------------- linear
+
+U = 2.0 ** -24  # unit roundoff of float32
+
+
+def gamma(n):
+    """Higham, Accuracy and Stability of Numerical Algorithms, eq. 3.8: a
+    recursive fp32 dot product of n terms is within gamma_n * sum|x_k w_k| of
+    the exact value, in any summation order."""
+    return n * U / (1 - n * U)
+
+
+def linear_exact(x, w, bias=None):
+    """float64 value and sum of |terms| of x @ w^T (+ bias)."""
+    x64, w64 = np.asarray(x, np.float64), np.asarray(w, np.float64)
+    y = np.atleast_2d(x64) @ w64.T
+    s = np.abs(np.atleast_2d(x64)) @ np.abs(w64).T
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64)
+        s = s + np.abs(np.asarray(bias, np.float64))
+    return y, s
+
+
+def within_dot_bound(got, exact, abs_terms, n):
+    got = np.atleast_2d(np.asarray(got, np.float64))
+    return bool((np.abs(got - exact) <= gamma(n) * abs_terms + 1e-30).all())
+
+
+def test_linear_quant_golden(orc):
+    """LinearQ80/Q40/Q41 of the reference's default build, bit for bit."""
+    g = golden("linear")
+    n = 0
+    for key in list(g):
+        if not key.endswith("_w") or key.startswith("f32"):
+            continue
+        tag = key[:-2]
+        qt = next(q for q in QT if f"_{q}_" in tag)
+        for xk in [k for k in g if k.startswith(tag + "_x")]:
+            yk = tag + "_y" + xk[len(tag) + 2:]
+            x, y = g[xk], g[yk]
+            got = orc.linear_quant(qt, x, g[key], y.shape[-1])
+            assert_bits_equal(got, y, yk)
+            n += 1
+    assert n == 3 * (5 * 2 + 2 + 2)
+
+
+@pytest.mark.parametrize("qt", QT)
+def test_linear_quant_float64_closed_form(orc, qt):
+    """Within the recursive-summation bound of the float64 value of the
+    dequantized product, and within test/cuda_quant_test.cc:60-66's
+    2e-5 * max(1, |y|) on that test's own inputs and shapes."""
+    g = golden("linear")
+    for inf in (1, 17, 32, 33, 65):
+        blocks = g[f"p43_{qt}_{inf}_w"]
+        w = orc.dequantize(qt, blocks, 131, inf)
+        for rows in (1, 3):
+            x = g[f"p43_{qt}_{inf}_x{rows}"]
+            bias = g["sin_bias7"][0] * np.ones(131, np.float32)
+            got = orc.linear_quant(qt, x, blocks, 131, bias=bias)
+            ex, s = linear_exact(x, w, bias)
+            assert within_dot_bound(got, ex, s, inf + 1)
+            near(got, ex)
+    rng = np.random.default_rng(3)
+    for out_f, inf in ((9, 4096), (3, 14336), (5, 70)):
+        w = (rng.standard_normal((out_f, inf)) * 0.02).astype(np.float32)
+        blocks = orc.quantize(qt, w)
+        x = rng.standard_normal((2, inf)).astype(np.float32)
+        ex, s = linear_exact(x, orc.dequantize(qt, blocks, out_f, inf))
+        assert within_dot_bound(orc.linear_quant(qt, x, blocks, out_f), ex, s, inf)
+
+
+def test_linear_f32_and_matmul(orc):
+    g = golden("linear")
+    assert_bits_equal(orc.linear_f32(g["f32_x"], g["f32_w"]), g["f32_y"], "linear f32")
+    got = orc.linear_f32(g["f32_x"], g["f32_w"], bias=g["f32_bias"])
+    assert_bits_equal(got, g["f32_y"] + g["f32_bias"], "bias is one fp32 add after the sum")
+    for m, k, n in ((3, 7, 5), (1, 33, 17)):
+        a, b = g[f"mm_{m}x{k}x{n}_a"], g[f"mm_{m}x{k}x{n}_b"]
+        c = orc.matmul_f32(a, b)
+        assert_bits_equal(c, g[f"mm_{m}x{k}x{n}_c"], "matmul")
+        ex, s = linear_exact(a, b.T)
+        assert within_dot_bound(c, ex, s, k)
+    # Linear(x, W) == Matmul(x, W^T)
+    x, w = g["f32_x"], g["f32_w"]
+    assert_bits_equal(orc.linear_f32(x, w), orc.matmul_f32(x, np.ascontiguousarray(w.T)), "lin")
+
+
+def test_linear_threads_do_not_change_results_and_bad_shapes_raise(orc):
+    rng = np.random.default_rng(8)
+    w = rng.standard_normal((200, 96)).astype(np.float32)
+    x = rng.standard_normal((4, 96)).astype(np.float32)
+    blocks = orc.quantize("q4_1", w)
+    one = orc.linear_quant("q4_1", x, blocks, 200, n_threads=1)
+    assert_bits_equal(orc.linear_quant("q4_1", x, blocks, 200, n_threads=7), one, "threads")
+    assert_bits_equal(orc.linear_f32(x, w, n_threads=5), orc.linear_f32(x, w, n_threads=1), "f")
+    with pytest.raises(ValueError):
+        orc.linear_quant("q8_0", np.zeros((0, 96), np.float32), blocks, 200)
+    with pytest.raises(ValueError):
+        orc.matmul_f32(np.zeros((2, 0), np.float32), np.zeros((0, 3), np.float32))
+
+
+@pytest.mark.parametrize("mutation", ["neighbour_scale", "nibble_swap", "drop_min", "k_reversed"])
+def test_planted_linear_mistakes_fail_the_closed_form(orc, mutation):
+    """A copy of the quantized dot product with one planted mistake, checked
+    like the oracle is: it fails the float64 bound on the golden inputs."""
+    g = golden("linear")
+    qt = "q4_1" if mutation == "drop_min" else ("q4_0" if mutation == "nibble_swap" else "q8_0")
+    blocks, x = g[f"n_{qt}_32x4096_w"], g[f"n_{qt}_32x4096_x"]
+    w = orc.dequantize(qt, blocks, 32, 4096).astype(np.float64)
+    wb = w.reshape(32, 128, 32)
+    if mutation == "neighbour_scale":
+        ratio = np.abs(wb).max(-1, keepdims=True)
+        wb = wb / np.maximum(ratio, 1e-30) * np.roll(ratio, 1, axis=1)
+    elif mutation == "nibble_swap":
+        wb = np.concatenate([wb[..., 16:], wb[..., :16]], axis=-1)
+    elif mutation == "drop_min":
+        raw = blocks.reshape(32, 128, 20)
+        mins = orc.fp16_to_fp32_array(raw[..., 2:4].copy().view(np.uint16)[..., 0])
+        wb = wb - mins[..., None]
+    else:
+        wb = wb[..., ::-1]
+    wrong = x.astype(np.float64) @ wb.reshape(32, 4096).T
+    ex, s = linear_exact(x, w)
+    assert within_dot_bound(g[f"n_{qt}_32x4096_y"], ex, s, 4096)
+    assert not within_dot_bound(wrong, ex, s, 4096)
+
+
+@needs_ref
+def test_linear_oracle_equals_compiled_reference_on_random_inputs(orc):
+    ref = O.reference()
+    rng = np.random.default_rng(12)
+    for qt in QT:
+        for out_f, inf, rows in ((131, 65, 3), (7, 32, 1), (40, 4096, 2), (33, 1, 2)):
+            w = (rng.standard_normal((out_f, inf)) * 0.3).astype(np.float32)
+            blocks = orc.quantize(qt, w)
+            x = rng.standard_normal((rows, inf)).astype(np.float32)
+            assert_bits_equal(orc.linear_quant(qt, x, blocks, out_f),
+                              ref.linear_quant(qt, x, blocks, out_f), qt)
+    w = rng.standard_normal((50, 300)).astype(np.float32)
+    x = rng.standard_normal((3, 300)).astype(np.float32)
+    assert_bits_equal(orc.linear_f32(x, w), ref.linear_f32(x, w), "f32")
+    a = rng.standard_normal((6, 40)).astype(np.float32)
+    assert_bits_equal(orc.matmul_f32(a, w[:40, :9].copy()), ref.matmul_f32(a, w[:40, :9].copy()),
+                      "mm")
