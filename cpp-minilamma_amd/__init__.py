@@ -67,6 +67,9 @@ _SIGNATURES = {
     "mlk_gather_f32": [_vp, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _vp],
     "mlk_gather_quant": [_i32, _vp, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _vp],
     "mlk_quantize": [_i32, _vp, _i64, _i64, _vp, _vp],
+    "mlk_linear_quant": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "mlk_linear_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "mlk_matmul_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "mlk_fill_normal_f32": [_vp, _i64, _f, _f, C.c_uint64, _vp],
     "mlk_device_count": [C.POINTER(C.c_int)],
     "mlk_set_device": [C.c_int],
@@ -381,6 +384,24 @@ def gather_quant(qtype, blocks, vocab, dim, ids, n_tokens, out, token=0, err=Non
 def quantize(qtype, x, rows, cols, blocks, stream=None):
     check(lib.mlk_quantize(QUANT[qtype], _p(x), rows, cols, _p(blocks), _sp(stream)),
           "mlk_quantize")
+
+
+def linear_quant(qtype, x, w_blocks, y, rows, in_features, out_features, bias=None,
+                 stream=None):
+    """y[rows, out] = x[rows, in] @ dequant(W)^T (+ bias)."""
+    check(lib.mlk_linear_quant(QUANT[qtype], _p(x), _p(w_blocks), _p(bias), _p(y), rows,
+                               in_features, out_features, _sp(stream)), "mlk_linear_quant")
+
+
+def linear_f32(x, w, y, rows, in_features, out_features, bias=None, stream=None):
+    """y[rows, out] = x[rows, in] @ W[out, in]^T (+ bias)."""
+    check(lib.mlk_linear_f32(_p(x), _p(w), _p(bias), _p(y), rows, in_features, out_features,
+                             _sp(stream)), "mlk_linear_f32")
+
+
+def matmul(a, b, c, m, k, n, stream=None):
+    """c[m, n] = a[m, k] @ b[k, n]."""
+    check(lib.mlk_matmul_f32(_p(a), _p(b), _p(c), m, k, n, _sp(stream)), "mlk_matmul_f32")
 
 
 def quant_bytes(qtype, rows, cols):

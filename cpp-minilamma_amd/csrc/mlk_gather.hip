@@ -25,51 +25,13 @@
 // (An LDS-staged variant -- 16-byte loads of the packed row, barrier, decode
 // from LDS -- measured 15-25% slower on MI355X: the gather is write-bound
 // and the staging round trip only added latency.)
-#include "mlk_common.h"
+#include "mlk_quant.h"
 
 namespace mlk {
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kQThreads = 1024;  // one float4 per lane of a 4096-wide row
-
-template <int QT>
-struct Fmt;
-template <>
-struct Fmt<MLK_Q8_0> {
-    static constexpr int kBytes = 34;
-};
-template <>
-struct Fmt<MLK_Q4_0> {
-    static constexpr int kBytes = 18;
-};
-template <>
-struct Fmt<MLK_Q4_1> {
-    static constexpr int kBytes = 20;
-};
-
-__host__ __device__ inline int BlockBytes(int qt) {
-    return qt == MLK_Q8_0 ? 34 : (qt == MLK_Q4_0 ? 18 : 20);
-}
-
-// IEEE binary16 -> binary32 with integer operations only.
-__device__ inline float HalfBits(uint32_t h) {
-    const uint32_t sign = (h & 0x8000u) << 16;
-    const uint32_t e = (h >> 10) & 31u;
-    const uint32_t f = h & 1023u;
-    uint32_t bits;
-    if (e == 31u) {
-        bits = sign | 0x7F800000u | (f << 13);
-    } else if (e != 0u) {
-        bits = sign | ((e + 112u) << 23) | (f << 13);
-    } else if (f == 0u) {
-        bits = sign;
-    } else {
-        const uint32_t sh = static_cast<uint32_t>(__clz(f)) - 21u;  // moves the top bit to bit 10
-        bits = sign | ((113u - sh) << 23) | (((f << sh) & 1023u) << 13);
-    }
-    return __uint_as_float(bits);
-}
 
 __device__ inline uint32_t LoadU16(const uint8_t* p) {
     return static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 8);

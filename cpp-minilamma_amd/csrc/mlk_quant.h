@@ -1,0 +1,66 @@
+// mlk_quant.h -- block formats and the fp16 decode shared by the quantized
+// gather and the quantized linear kernels.
+//
+// Packed blocks of 32 elements (include/quantized_tensor.h:10-35 of the
+// reference, little-endian):
+//   Q8_0  34 B: u16 d | i8 qs[32]            w = d * q
+//   Q4_0  18 B: u16 d | u8 qs[16]            w = d * (code - 8)
+//   Q4_1  20 B: u16 d | u16 m | u8 qs[16]    w = d * code + m
+// For Q4 formats, element i < 16 is the low nibble of qs[i] and element
+// i >= 16 the high nibble of qs[i - 16].
+#pragma once
+
+#include "mlk_common.h"
+
+namespace mlk {
+
+template <int QT>
+struct Fmt;
+template <>
+struct Fmt<MLK_Q8_0> {
+    static constexpr int kBytes = 34;
+};
+template <>
+struct Fmt<MLK_Q4_0> {
+    static constexpr int kBytes = 18;
+};
+template <>
+struct Fmt<MLK_Q4_1> {
+    static constexpr int kBytes = 20;
+};
+
+__host__ __device__ inline int BlockBytes(int qt) {
+    return qt == MLK_Q8_0 ? 34 : (qt == MLK_Q4_0 ? 18 : 20);
+}
+
+// IEEE binary16 -> binary32 with integer operations only, so no denormal
+// mode can flush a subnormal scale; inf and NaN payloads are kept.
+__device__ inline float HalfBits(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 31u;
+    const uint32_t f = h & 1023u;
+    uint32_t bits;
+    if (e == 31u) {
+        bits = sign | 0x7F800000u | (f << 13);
+    } else if (e != 0u) {
+        bits = sign | ((e + 112u) << 23) | (f << 13);
+    } else if (f == 0u) {
+        bits = sign;
+    } else {
+        const uint32_t sh = static_cast<uint32_t>(__clz(f)) - 21u;  // moves the top bit to bit 10
+        bits = sign | ((113u - sh) << 23) | (((f << sh) & 1023u) << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// The same conversion with the hardware instruction (v_cvt_f32_f16), for
+// the inner loops of the linear kernels where the integer sequence costs ~10
+// VALU ops per block.  gfx950 runs with f16/f64 denormals preserved (the HIP
+// default mode), so subnormal scales convert exactly; the parity tests hold
+// subnormal-scale blocks to keep that assumption checked.
+__device__ inline float HalfHw(uint32_t h16) {
+    const _Float16 v = __builtin_bit_cast(_Float16, static_cast<uint16_t>(h16));
+    return static_cast<float>(v);
+}
+
+}  // namespace mlk

@@ -22,6 +22,8 @@
  * Reference interfaces replaced (paths are under the reference tree):
  *   include/cuda_ops.h:11-33        -> the op entries below (one-token
  *                                      signatures become n_tokens = 1)
+ *   include/cuda_matmul.h:7-18      -> mlk_linear_f32, mlk_matmul_f32
+ *   include/cuda_quant.h:12-25      -> mlk_linear_quant
  *   include/cuda_runtime.h:8-42     -> the runtime entries at the end
  */
 #ifndef MINILAMMA_HIP_H
@@ -139,6 +141,32 @@ mlk_status mlk_quantize(int32_t quant_type, const float* x, int64_t rows, int64_
                         void* blocks, void* stream);
 /* Bytes of the packed blocks of a [rows, cols] matrix (0 on bad input). */
 int64_t mlk_quant_bytes(int32_t quant_type, int64_t rows, int64_t cols);
+
+/*
+ * Linear layer with a block-quantized weight:
+ *   y[t, j] = sum_k x[t, k] * W[j, k] (+ bias[j])   t < rows, j < out_features
+ * W is out_features rows of ceil(in_features / 32) packed blocks (the layout
+ * above); x [rows, in_features] and y [rows, out_features] are row-major
+ * fp32; bias may be NULL and is added to the finished sum.  The sum is fp32
+ * in an order of the kernel's choosing: within gamma_K * sum_k |x w| of the
+ * exact value, like the reference's serial loop.  y may not alias x or W.
+ * Replaces CudaQ40/Q41/Q80DeviceInputLinear (include/cuda_quant.h:12-25;
+ * kernels src/cuda_quant.cu:29-97, one thread per output).
+ */
+mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_blocks,
+                            const float* bias, float* y, int64_t rows, int64_t in_features,
+                            int64_t out_features, void* stream);
+
+/* The same with an fp32 weight W [out_features, in_features] row-major.
+ * Replaces CudaLinearDevice (include/cuda_matmul.h:16-18; cublasSgemm,
+ * src/cuda_matmul.cc:155-189). */
+mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, float* y,
+                          int64_t rows, int64_t in_features, int64_t out_features, void* stream);
+
+/* c = a @ b for row-major a [m, k], b [k, n], c [m, n].  Replaces CudaMatmul
+ * (include/cuda_matmul.h:7; src/cuda_matmul.cc:199-232). */
+mlk_status mlk_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t k,
+                          int64_t n, void* stream);
 
 /* Synthetic-input helper (not a reference op): fills x[i] with
  * mean + std * N(0,1) from a counter-based generator keyed by seed and i, so

@@ -91,3 +91,33 @@ def max_ulp(got, want):
     a = np.ascontiguousarray(got, dtype=np.float32).view(np.int32).astype(np.int64)
     b = np.ascontiguousarray(want, dtype=np.float32).view(np.int32).astype(np.int64)
     return int(np.abs(a - b).max()) if a.size else 0
+
+
+U32 = 2.0 ** -24  # float32 unit roundoff
+
+
+def dot_exact(x, w, bias=None):
+    """float64 value and sum of |terms| of x @ w^T (+ bias) for x [T, K],
+    w [O, K]."""
+    x64 = np.atleast_2d(np.asarray(x, np.float64))
+    w64 = np.asarray(w, np.float64)
+    y = x64 @ w64.T
+    s = np.abs(x64) @ np.abs(w64).T
+    if bias is not None:
+        b = np.asarray(bias, np.float64)
+        y, s = y + b, s + np.abs(b)
+    return y, s
+
+
+def assert_dot_close(got, exact, abs_terms, n_terms, what=""):
+    """The linear-layer bar: any fp32 summation order of n terms is within
+    gamma_n * sum|terms| of the exact value (Higham, Accuracy and Stability
+    of Numerical Algorithms, eq. 3.8); the reference's serial loop and the
+    kernels are held to the same bound."""
+    got = np.atleast_2d(np.asarray(got, np.float64))
+    gamma = n_terms * U32 / (1 - n_terms * U32)
+    err = np.abs(got - exact)
+    lim = gamma * abs_terms
+    bad = ~(err <= lim)
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {got.size} outside gamma_{n_terms} bound; "
+                           f"worst err {float(err.max()):.3e} vs bound {float(lim.min()):.3e}")

@@ -13,7 +13,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from conftest import assert_bits_equal, assert_terms_close, load_workloads, max_ulp
+from conftest import (assert_bits_equal, assert_dot_close, assert_terms_close, dot_exact,
+                      load_workloads, max_ulp)
 
 W = load_workloads()
 
@@ -164,3 +165,37 @@ def test_decode_chain(mlk, orc, T):
     assert_terms_close(d_k.download(), ek, np.abs(ek), "k")
     eo = orc.swiglu(gate, up)
     assert_terms_close(d_o.download(), eo, np.abs(eo), "ffn")
+
+
+# ------------------------------------------------------------ linear (decode)
+
+@pytest.mark.parametrize("qt,out_f,in_f,T", [
+    ("q8_0", 14336, 4096, 1), ("q8_0", 4096, 14336, 4), ("q4_0", 14336, 4096, 1),
+    ("q4_0", 4096, 14336, 2), ("q4_1", 14336, 4096, 4), ("q4_1", 6144, 4096, 1),
+    ("q8_0", 128256, 4096, 1)])
+def test_quant_linear_decode_full_size(mlk, orc, qt, out_f, in_f, T):
+    """Llama-3-8B projections (gate/up [14336, 4096], down [4096, 14336],
+    fused QKV [6144, 4096], lm_head [128256, 4096]) at decode batch sizes,
+    weights quantized on the device from N(0, 0.02)."""
+    w = device_normal(mlk, (out_f, in_f), 0.0, 0.02, out_f + in_f)
+    blocks = mlk.DeviceBuffer(mlk.quant_bytes(qt, out_f, in_f), np.uint8)
+    mlk.quantize(qt, w, out_f, in_f, blocks)
+    del w
+    x = device_normal(mlk, (T, in_f), 0.0, 1.0, 7 + T)
+    y = mlk.DeviceBuffer.empty((T, out_f))
+    mlk.linear_quant(qt, x, blocks, y, T, in_f, out_f)
+    got = y.download()
+    hb = blocks.download()
+    del blocks
+    ex, s = dot_exact(x.download(), orc.dequantize(qt, hb, out_f, in_f))
+    assert_dot_close(got, ex, s, in_f, f"{qt} {out_f}x{in_f} T={T}")
+
+
+def test_f32_linear_decode_full_size(mlk, orc):
+    out_f, in_f, T = 14336, 4096, 2
+    w = device_normal(mlk, (out_f, in_f), 0.0, 0.02, 3)
+    x = device_normal(mlk, (T, in_f), 0.0, 1.0, 4)
+    y = mlk.DeviceBuffer.empty((T, out_f))
+    mlk.linear_f32(x, w, y, T, in_f, out_f)
+    ex, s = dot_exact(x.download(), w.download())
+    assert_dot_close(y.download(), ex, s, in_f, "f32 14336x4096")

@@ -1,0 +1,178 @@
+"""GPU parity of the linear layers: quantized (Q8_0 / Q4_0 / Q4_1) and F32
+linear, and Matmul, through the C ABI.
+
+The bar (written in conftest.assert_dot_close): every output within
+gamma_K * sum_k |x_k w_k| of the float64 value of the same product with the
+dequantized weights -- the bound any fp32 summation order meets, the
+reference's serial loop included.  On the reference's own test inputs the
+reference's own tolerance 2e-5 * max(1, |y|) (test/cuda_quant_test.cc:60-66)
+is checked as well, and the compiled reference's outputs (tests/golden)
+are held to the same bound.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_dot_close, dot_exact, golden
+
+pytestmark = pytest.mark.gpu
+
+QT = ("q8_0", "q4_0", "q4_1")
+
+
+def normal(rng, shape, std=1.0):
+    return (rng.standard_normal(shape) * std).astype(np.float32)
+
+
+def run_quant(mlk, qt, x, blocks, out_f, bias=None):
+    x = np.atleast_2d(np.ascontiguousarray(x, np.float32))
+    T, K = x.shape
+    d_x = mlk.DeviceBuffer.from_array(x)
+    d_w = mlk.DeviceBuffer.from_array(np.ascontiguousarray(blocks, np.uint8))
+    d_b = None if bias is None else mlk.DeviceBuffer.from_array(np.asarray(bias, np.float32))
+    d_y = mlk.DeviceBuffer.empty((T, out_f))
+    mlk.linear_quant(qt, d_x, d_w, d_y, T, K, out_f, bias=d_b)
+    return d_y.download()
+
+
+def near_reference_tolerance(got, exact):
+    """test/cuda_quant_test.cc:60-66."""
+    got = np.atleast_2d(np.asarray(got, np.float64))
+    assert (np.abs(got - exact) <= 2e-5 * np.maximum(1.0, np.abs(exact))).all()
+
+
+def test_quant_linear_reference_patterns(mlk, orc):
+    """The weight / input patterns and shapes of the reference's own tests
+    (131 outputs, in 1, 17, 32, 33, 65; one and three rows; bias), against
+    float64 and the compiled reference's outputs."""
+    g = golden("linear")
+    for qt in QT:
+        for inf in (1, 17, 32, 33, 65):
+            blocks = g[f"p43_{qt}_{inf}_w"]
+            w = orc.dequantize(qt, blocks, 131, inf)
+            for rows in (1, 3):
+                x = g[f"p43_{qt}_{inf}_x{rows}"]
+                ex, s = dot_exact(x, w)
+                got = run_quant(mlk, qt, x, blocks, 131)
+                assert_dot_close(got, ex, s, inf, f"{qt} in={inf} rows={rows}")
+                near_reference_tolerance(got, ex)
+                assert_dot_close(g[f"p43_{qt}_{inf}_y{rows}"], ex, s, inf, "reference itself")
+                bias = np.linspace(-1, 1, 131).astype(np.float32)
+                got = run_quant(mlk, qt, x, blocks, 131, bias=bias)
+                exb, sb = dot_exact(x, w, bias)
+                assert_dot_close(got, exb, sb, inf + 1, f"{qt} in={inf} bias")
+        for cols in (32, 86):
+            blocks, x = g[f"sin_{qt}_{cols}_w"], g[f"sin_{qt}_{cols}_x"]
+            ex, s = dot_exact(x, orc.dequantize(qt, blocks, 7, cols))
+            assert_dot_close(run_quant(mlk, qt, x, blocks, 7), ex, s, cols, f"{qt} sin {cols}")
+
+
+@pytest.mark.parametrize("qt", QT)
+@pytest.mark.parametrize("shape", [(131, 64, 1), (4099, 4096, 1), (64, 4096, 2), (37, 4096, 3),
+                                   (16, 4096, 4), (33, 14336, 5), (200, 128, 9), (5, 96, 2),
+                                   (1, 4096, 1)])
+def test_quant_linear_shapes(mlk, orc, qt, shape):
+    """The dwordx4 pair path (in % 64 == 0), tails of the 4-row wave groups,
+    token counts 1..9 (chunks of 4), and in % 64 != 0 (byte-load path)."""
+    O, K, T = shape
+    rng = np.random.default_rng(O * 7 + K + T)
+    w = normal(rng, (O, K), 0.02)
+    blocks = orc.quantize(qt, w)
+    x = normal(rng, (T, K))
+    bias = normal(rng, (O,), 0.1)
+    ex, s = dot_exact(x, orc.dequantize(qt, blocks, O, K), bias)
+    got = run_quant(mlk, qt, x, blocks, O, bias=bias)
+    assert_dot_close(got, ex, s, K + 1, f"{qt} {shape}")
+    # the compiled reference's (oracle's) own result meets the same bound
+    assert_dot_close(orc.linear_quant(qt, x, blocks, O, bias=bias), ex, s, K + 1, "oracle")
+
+
+@pytest.mark.parametrize("qt", QT)
+def test_quant_linear_special_scales(mlk, orc, qt):
+    """Subnormal, zero and large fp16 scales (and Q4_1 minima) decode like the
+    CPU: blocks are hand-made, then checked against float64."""
+    rng = np.random.default_rng(1)
+    O, K, T = 8, 256, 2
+    blocks = orc.quantize(qt, normal(rng, (O, K), 0.02)).reshape(O, K // 32, -1).copy()
+    scales = [0x0001, 0x03FF, 0x0000, 0x7BFF, 0x3C00, 0x8001, 0x0400, 0x1234]
+    for j in range(O):
+        blocks[j, :, 0:2] = np.array([scales[j]], np.uint16).view(np.uint8)
+        if qt == "q4_1":
+            blocks[j, :, 2:4] = np.array([scales[(j + 3) % O]], np.uint16).view(np.uint8)
+    blocks = blocks.reshape(-1)
+    x = normal(rng, (T, K), 1e-3)
+    ex, s = dot_exact(x, orc.dequantize(qt, blocks, O, K))
+    assert_dot_close(run_quant(mlk, qt, x, blocks, O), ex, s, K, f"{qt} scales")
+
+
+def test_quant_linear_unaligned_buffers(mlk, orc):
+    """x not 16-byte aligned and blocks only 2-byte aligned take the
+    byte-load path and give the same result."""
+    rng = np.random.default_rng(2)
+    O, K, T = 19, 128, 3
+    for qt in QT:
+        blocks = orc.quantize(qt, normal(rng, (O, K), 0.02))
+        x = normal(rng, (T, K))
+        ex, s = dot_exact(x, orc.dequantize(qt, blocks, O, K))
+        xb = mlk.DeviceBuffer(x.nbytes + 4, np.uint8)
+        wb = mlk.DeviceBuffer(blocks.nbytes + 2, np.uint8)
+        mlk.check(mlk.lib.mlk_memcpy(xb.ptr + 4, x.ctypes.data, x.nbytes, mlk.H2D))
+        mlk.check(mlk.lib.mlk_memcpy(wb.ptr + 2, blocks.ctypes.data, blocks.nbytes, mlk.H2D))
+        y = mlk.DeviceBuffer.empty((T, O))
+        mlk.linear_quant(qt, xb.ptr + 4, wb.ptr + 2, y, T, K, O)
+        assert_dot_close(y.download(), ex, s, K, f"{qt} unaligned")
+
+
+def test_quant_linear_chains_device_outputs(mlk, orc):
+    """test/cuda_quant_test.cc:130-148: the device output of one linear is the
+    next one's input."""
+    rng = np.random.default_rng(4)
+    for qt in QT:
+        w1, w2 = normal(rng, (128, 192), 0.05), normal(rng, (7, 128), 0.05)
+        b1, b2 = orc.quantize(qt, w1), orc.quantize(qt, w2)
+        x = normal(rng, (3, 192))
+        d_x = mlk.DeviceBuffer.from_array(x)
+        d_h = mlk.DeviceBuffer.empty((3, 128))
+        d_y = mlk.DeviceBuffer.empty((3, 7))
+        mlk.linear_quant(qt, d_x, mlk.DeviceBuffer.from_array(b1), d_h, 3, 192, 128)
+        mlk.linear_quant(qt, d_h, mlk.DeviceBuffer.from_array(b2), d_y, 3, 128, 7)
+        h = d_h.download()
+        ex, s = dot_exact(h, orc.dequantize(qt, b2, 7, 128))
+        assert_dot_close(d_y.download(), ex, s, 128, f"{qt} second layer")
+
+
+def run_f32(mlk, x, w, bias=None):
+    x = np.atleast_2d(x)
+    d_y = mlk.DeviceBuffer.empty((x.shape[0], w.shape[0]))
+    d_b = None if bias is None else mlk.DeviceBuffer.from_array(bias)
+    mlk.linear_f32(mlk.DeviceBuffer.from_array(x), mlk.DeviceBuffer.from_array(w), d_y,
+                   x.shape[0], x.shape[1], w.shape[0], bias=d_b)
+    return d_y.download()
+
+
+def test_f32_linear_and_matmul(mlk, orc):
+    g = golden("linear")
+    x, w, b = g["f32_x"], g["f32_w"], g["f32_bias"]
+    ex, s = dot_exact(x, w)
+    assert_dot_close(run_f32(mlk, x, w), ex, s, 33, "tests/test_cuda_linear.cc shape")
+    ex, s = dot_exact(x, w, b)
+    assert_dot_close(run_f32(mlk, x, w, b), ex, s, 34, "bias")
+    rng = np.random.default_rng(6)
+    for O, K, T in ((4096, 4096, 1), (1000, 4096, 3), (77, 1000, 6), (9, 35, 2), (3, 14336, 4)):
+        w = normal(rng, (O, K), 0.02)
+        x = normal(rng, (T, K))
+        bias = normal(rng, (O,))
+        ex, s = dot_exact(x, w, bias)
+        assert_dot_close(run_f32(mlk, x, w, bias), ex, s, K + 1, f"f32 {O}x{K} T={T}")
+    for m, k, n in ((3, 7, 5), (1, 33, 17)):
+        a, bm = g[f"mm_{m}x{k}x{n}_a"], g[f"mm_{m}x{k}x{n}_b"]
+        c = mlk.DeviceBuffer.empty((m, n))
+        mlk.matmul(mlk.DeviceBuffer.from_array(a), mlk.DeviceBuffer.from_array(bm), c, m, k, n)
+        ex, s = dot_exact(a, bm.T)
+        assert_dot_close(c.download(), ex, s, k, "matmul")
+    a, bm = normal(rng, (70, 300)), normal(rng, (300, 45))
+    c = mlk.DeviceBuffer.empty((70, 45))
+    mlk.matmul(mlk.DeviceBuffer.from_array(a), mlk.DeviceBuffer.from_array(bm), c, 70, 300, 45)
+    ex, s = dot_exact(a, bm.T)
+    assert_dot_close(c.download(), ex, s, 300, "matmul 70x300x45")

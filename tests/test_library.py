@@ -60,6 +60,11 @@ CPP_SURFACE = [
     "CudaQuantizeDevice", "CudaRuntimeBuilt", "GetCudaInfo", "DeviceCount", "SetCudaService",
     "CudaMemory", "CudaFreeMemory", "CudaMemcpy", "CudaEmptyCache", "CudaCachedBytes",
     "TensorHostToDevice",
+    # include/cuda_matmul.h, include/cuda_quant.h
+    "cuBLASBuilt", "CudaMatmul", "CudaLinear", "CudaLinearHostDevice", "CudaLinearDevice",
+    "CudaQuantBuilt", "CudaQ40Linear", "CudaQ40DeviceLinear", "CudaQ40DeviceInputLinear",
+    "CudaQ41Linear", "CudaQ41DeviceLinear", "CudaQ41DeviceInputLinear", "CudaQ80Linear",
+    "CudaQ80DeviceLinear", "CudaQ80DeviceInputLinear",
 ]
 
 
@@ -107,6 +112,15 @@ def test_validation_happens_before_any_device_call():
         (lambda: mlk.quantize("q4_1", fake, 1, 32, fake + 1), "2-byte aligned"),
         (lambda: mlk.softmax(fake, fake, 1, 4), "alias"),
         (lambda: mlk.softmax(fake, fake + 64, 0, 4), "must not be empty"),
+        (lambda: mlk.linear_quant("q8_0", fake, fake + 64, fake + 128, 0, 32, 4),
+         "must be positive"),
+        (lambda: mlk.linear_quant("q8_0", None, fake, fake + 64, 1, 32, 4), "must not be null"),
+        (lambda: mlk.linear_quant("q4_0", fake, fake + 64, fake, 1, 32, 4), "alias"),
+        (lambda: mlk.linear_quant("q4_1", fake, fake + 1, fake + 64, 1, 32, 4), "2-byte aligned"),
+        (lambda: mlk.linear_f32(fake, fake + 64, fake + 128, 1, 0, 4), "must be positive"),
+        (lambda: mlk.linear_f32(fake, fake + 64, fake + 2, 1, 4, 4), "4-byte aligned"),
+        (lambda: mlk.matmul(fake, fake + 64, fake, 2, 2, 2), "alias"),
+        (lambda: mlk.matmul(fake, fake + 64, fake + 128, 2, 0, 2), "must be positive"),
     ]
     for call, text in cases:
         with pytest.raises(mlk.MlkError, match=text):
@@ -115,6 +129,8 @@ def test_validation_happens_before_any_device_call():
     assert mlk.lib.mlk_gather_quant(9, None, 1, 1, None, 0, 1, None, None, None) == \
         mlk.MLK_ERR_INVALID
     assert b"unknown quantization type" in mlk.lib.mlk_last_error()
+    assert mlk.lib.mlk_linear_quant(3, None, None, None, None, 1, 1, 1, None) == \
+        mlk.MLK_ERR_INVALID
 
 
 def test_quant_bytes_and_status_strings():
