@@ -50,6 +50,10 @@ def parse_args():
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--extra", default=None, help="also measure configs 1, 3, 4 into this JSON file")
+    p.add_argument("--linear", default=None,
+                   help="only measure the seven linear projections of one Llama-3-8B layer "
+                        "(F32, Q8_0, Q4_0, Q4_1 weights; T = 1, 4, 16 token rows) into this "
+                        "JSON file")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--rocprof-report", nargs=5, default=None,
                    metavar=("KERNEL_TRACE_DIR", "FETCH_DIR", "WRITE_DIR", "CALIB_FETCH_DIR",
@@ -324,6 +328,110 @@ def extra_configs(mlk, workloads, steps, peak):
     return res
 
 
+# ------------------------------------------------------------ linear layers
+
+LINEAR_TYPES = ("q8_0", "q4_0", "q4_1", "f32")
+LINEAR_TOKENS = (1, 4, 16)
+LINEAR_WORKING_SET = 768 << 20  # rotate layer copies until the weights exceed 3x the MALL
+
+
+class LinearLayers:
+    """Device copies of the seven projection weights of one Llama-3-8B layer
+    in one weight format: every matrix has enough copies that one pass over
+    its copies exceeds 768 MB, three times the 256 MB MALL, so a launch never
+    finds its weights in cache (the per-projection loop rotates over a
+    matrix's copies, the whole-layer loop over all of them)."""
+
+    def __init__(self, mlk, cfg, qtype, seed):
+        self.mlk, self.qtype = mlk, qtype
+        self.shapes = workloads.layer_linears(cfg)
+        biggest = max(k * o for _, k, o in self.shapes)
+        tmp = mlk.DeviceBuffer.empty((biggest,)) if qtype != "f32" else None
+        self.copies = {}
+        for j, (name, k, o) in enumerate(self.shapes):
+            n = max(2, -(-LINEAR_WORKING_SET // workloads.weight_bytes(qtype, k, o)))
+            mats = []
+            for c in range(n):
+                sd = seed + 97 * c + j
+                if qtype == "f32":
+                    w = mlk.DeviceBuffer.empty((o, k))
+                    mlk.fill_normal(w, o * k, 0.0, 0.02, sd)
+                else:
+                    mlk.fill_normal(tmp, o * k, 0.0, 0.02, sd)
+                    w = mlk.DeviceBuffer(mlk.quant_bytes(qtype, o, k), np.uint8)
+                    mlk.quantize(qtype, tmp, o, k, w)
+                mats.append(w)
+            self.copies[name] = mats
+        mlk.synchronize()
+        if tmp is not None:
+            tmp.close()
+
+    def n_copies(self, name):
+        return len(self.copies[name])
+
+    def launch(self, i, name, k, o, x, y, T, stream):
+        mats = self.copies[name]
+        w = mats[i % len(mats)]
+        if self.qtype == "f32":
+            self.mlk.linear_f32(x, w, y, T, k, o, stream=stream)
+        else:
+            self.mlk.linear_quant(self.qtype, x, w, y, T, k, o, stream=stream)
+
+
+def linear_bench(mlk, steps, peak, path):
+    """Per-projection launch time (each launched `steps` times back to back
+    over the rotating weight copies, between two events on its stream) and
+    the time of one whole layer's seven projections."""
+    cfg = workloads.CONFIGS["c2_decode_8b"]
+    big = max(max(k, o) for _, k, o in workloads.layer_linears(cfg))
+    T_max = max(LINEAR_TOKENS)
+    x = mlk.DeviceBuffer.empty((T_max, big))
+    y = mlk.DeviceBuffer.empty((T_max, big))
+    mlk.fill_normal(x, T_max * big, 0.0, 1.0, 5)
+    st = mlk.Stream()
+    out = {"workload": "Llama-3-8B layer projections (configs[1] shapes), weights N(0,0.02) "
+                       "quantized on the device; x N(0,1)",
+           "peak_GBps": peak}
+    for qt in LINEAR_TYPES:
+        layers = LinearLayers(mlk, cfg, qt, seed=300)
+        res = {"weight_copies": {n: layers.n_copies(n) for n, _, _ in layers.shapes}}
+        for T in LINEAR_TOKENS:
+            per = {}
+            for name, k, o in layers.shapes:
+                for i in range(3):
+                    layers.launch(i, name, k, o, x, y, T, st)
+                st.synchronize()
+                e0, e1 = mlk.Event(), mlk.Event()
+                e0.record(st)
+                for i in range(3, 3 + steps):  # copies not touched by the warmup
+                    layers.launch(i, name, k, o, x, y, T, st)
+                e1.record(st)
+                e1.synchronize()
+                ms = e0.elapsed_ms(e1) / steps
+                nb = workloads.bytes_linear(qt, T, k, o)
+                gbs = nb / (ms * 1e-3) / 1e9
+                per[name] = {"in": k, "out": o, "us": round(ms * 1e3, 2), "bytes": nb,
+                             "GBps": round(gbs, 1), "frac_of_peak": round(gbs / peak, 4)}
+            e0, e1 = mlk.Event(), mlk.Event()
+            e0.record(st)
+            for i in range(3 + steps, 3 + 2 * steps):
+                for name, k, o in layers.shapes:
+                    layers.launch(i, name, k, o, x, y, T, st)
+            e1.record(st)
+            e1.synchronize()
+            ms = e0.elapsed_ms(e1) / steps
+            nb = sum(workloads.bytes_linear(qt, T, k, o) for _, k, o in layers.shapes)
+            gbs = nb / (ms * 1e-3) / 1e9
+            res[str(T)] = {"layer_us": round(ms * 1e3, 2), "layer_bytes": nb,
+                           "layer_GBps": round(gbs, 1), "layer_frac_of_peak": round(gbs / peak, 4),
+                           "ops": per}
+            print(f"linear {qt} T={T}: layer {ms * 1e3:.1f} us, {gbs:.0f} GB/s", flush=True)
+        out[qt] = res
+        del layers
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+
+
 CALIB_FLOATS = 64 << 20  # 256 MiB per buffer
 
 
@@ -486,6 +594,9 @@ def main():
     mlk.set_device(0)
     if args.calibrate:
         calibrate(mlk, args.steps)
+        return
+    if args.linear:
+        linear_bench(mlk, args.steps, workloads.HBM_PEAK_GBS, args.linear)
         return
     peak = workloads.HBM_PEAK_GBS
     cfg = workloads.CONFIGS["c3_prefill_8b"]

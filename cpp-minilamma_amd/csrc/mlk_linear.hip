@@ -17,18 +17,33 @@
 //
 // Decode-shaped calls (a few token rows, the forward pass's one-token
 // steps) are weight-streaming GEMVs bound by HBM: every weight byte is read
-// once, x stays in L1.  Layout of the work:
-//   - a wave owns kRows consecutive weight rows; each lane owns "pairs" of
-//     two consecutive blocks (64 inputs) of those rows, p = lane, lane + 64,
-//     ..., so a wave's loads cover contiguous spans of every row;
-//   - a pair is 68 / 36 / 40 bytes (Q8_0 / Q4_0 / Q4_1), a whole number of
-//     dwords at a dword-aligned offset when in_features % 64 == 0, so it is
-//     read with dwordx4 loads and the codes realigned with v_alignbyte;
-//   - per block, s = sum code * x over the 32 inputs, then the block's
-//     scale is applied once (Q4_0: d * (s - 8 sum x), Q4_1: d * s + m sum x,
-//     with sum x per block shared by the wave's rows);
-//   - the 64 lane partials are summed with a butterfly at the end.
-// Shapes outside that (in_features % 64 != 0, unaligned pointers) take a
+// once, x stays in L1/L2.  Layout of the work (GemvSplitK):
+//   - a workgroup of four waves owns RW consecutive weight rows; the four
+//     waves split K: wave w takes spans w, w + 4, w + 8, ... (two spans per
+//     loop trip, so each lane has 2 * RW span loads in flight);
+//   - a span is the part of K one wave covers in one step, with every lane
+//     owning a contiguous slice, so that consecutive lanes read consecutive
+//     bytes of the weight row and consecutive float4 of x:
+//       Q8_0  8 blocks (256 inputs); lane: block lane/8, inputs 4*(lane%8)+0..3
+//             (fp16 scale and the four code bytes as three aligned u16 loads)
+//       Q4_0  16 blocks (512 inputs); lane: block lane/4, code bytes
+//             4*(lane%4)+0..3, i.e. inputs 4j..4j+3 (low nibbles) and
+//             16+4j..16+4j+3 (high nibbles), j = lane%4
+//       Q4_1  as Q4_0, with d|m and the code bytes as aligned u32 loads
+//       F32   256 inputs; lane: one float4 (non-temporal load)
+//   - per slice, s = sum code * x, then the block scale is applied once
+//     (Q8_0: d * s; Q4_0: d * (s - 8 * sum x); Q4_1: d * s + m * sum x, the
+//     sum of x taken in the same order as s, so that a Q4_0 slice of all-8
+//     codes folds to exactly zero);
+//   - each lane ends with RW * R partial sums; a transpose-reduce over the
+//     wave leaves one output per lane group, and the four waves' totals are
+//     added in wave order through LDS (deterministic order).
+// The first span of each wave is w, so the four waves of a workgroup read
+// adjacent spans of the same rows at the same time.  Spans past the last
+// block (in_features % 256 or % 512 != 0) are masked per lane.  Token rows
+// come in launches of up to four; RW is 4 for outputs >= 4096 (x reused over
+// more rows) and 2 below (more workgroups for the small K/V projections).
+// Shapes outside that (in_features % 32 != 0, unaligned pointers) take a
 // one-wave-per-row kernel with byte loads.
 #include "mlk_quant.h"
 
@@ -37,96 +52,14 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
-constexpr int kRows = 4;      // weight rows per wave in the GEMV kernels
 constexpr int kMaxTok = 4;    // token rows per GEMV launch
-
-typedef uint32_t U32x4A4 __attribute__((ext_vector_type(4), aligned(4)));
+constexpr int kF32 = -1;      // QT value of F32 weights
 
 __device__ inline float WaveSumF(float v) {
 #pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-        v += __shfl_xor(v, off, kWave);
-    }
+    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
     return v;
 }
-
-template <int QT>
-struct Pair {
-    static constexpr int kBytes = 2 * Fmt<QT>::kBytes;  // 68, 36, 40
-    static constexpr int kWords = kBytes / 4;           // 17, 9, 10
-};
-
-// The dwords of one block pair (dword-aligned), as dwordx4 loads plus a tail.
-template <int QT>
-__device__ inline void LoadPair(const uint8_t* p, uint32_t (&u)[Pair<QT>::kWords]) {
-    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
-    constexpr int n4 = Pair<QT>::kWords / 4;
-#pragma unroll
-    for (int i = 0; i < n4; ++i) {
-        const U32x4A4 v = *reinterpret_cast<const U32x4A4*>(q + 4 * i);
-        u[4 * i + 0] = v.x;
-        u[4 * i + 1] = v.y;
-        u[4 * i + 2] = v.z;
-        u[4 * i + 3] = v.w;
-    }
-#pragma unroll
-    for (int i = 4 * n4; i < Pair<QT>::kWords; ++i) {
-        u[i] = q[i];
-    }
-}
-
-// Block B (0 or 1) of a pair: scale, min (Q4_1) and the code dwords, four
-// elements per dword for Q8_0 (8 dwords), low/high nibble pairs for Q4
-// (4 dwords: byte j of dword i holds elements 4i + j and 16 + 4i + j).
-template <int QT, int B>
-struct BlockOf;
-
-template <int B>
-struct BlockOf<MLK_Q8_0, B> {
-    float d;
-    uint32_t c[8];
-    __device__ inline explicit BlockOf(const uint32_t (&u)[17]) {
-        if (B == 0) {
-            d = HalfHw(u[0] & 0xFFFFu);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) c[i] = __builtin_amdgcn_alignbyte(u[i + 1], u[i], 2);
-        } else {
-            d = HalfHw(u[8] >> 16);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) c[i] = u[9 + i];
-        }
-    }
-};
-
-template <int B>
-struct BlockOf<MLK_Q4_0, B> {
-    float d;
-    uint32_t c[4];
-    __device__ inline explicit BlockOf(const uint32_t (&u)[9]) {
-        if (B == 0) {
-            d = HalfHw(u[0] & 0xFFFFu);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) c[i] = __builtin_amdgcn_alignbyte(u[i + 1], u[i], 2);
-        } else {
-            d = HalfHw(u[4] >> 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) c[i] = u[5 + i];
-        }
-    }
-};
-
-template <int B>
-struct BlockOf<MLK_Q4_1, B> {
-    float d, m;
-    uint32_t c[4];
-    __device__ inline explicit BlockOf(const uint32_t (&u)[10]) {
-        const uint32_t dm = u[5 * B];
-        d = HalfHw(dm & 0xFFFFu);
-        m = HalfHw(dm >> 16);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) c[i] = u[5 * B + 1 + i];
-    }
-};
 
 __device__ inline float SByte(uint32_t w, int j) {
     return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * j)) >> 24);
@@ -135,173 +68,296 @@ __device__ inline float UByte(uint32_t w, int j) {
     return static_cast<float>((w >> (8 * j)) & 0xFFu);
 }
 
-// Adds block B of pair u, times the x block xb (32 inputs for each token),
-// into acc[t].  xsum[t] = sum of the token's 32 inputs (Q4 formats).
-template <int QT, int B, int R>
-__device__ inline void BlockDot(const uint32_t (&u)[Pair<QT>::kWords], const float4 (&xb)[R][8],
-                                const float (&xsum)[R], float (&acc)[R]) {
-    const BlockOf<QT, B> blk(u);
-    float s[R];
+// Zero (m == 0) or keep (m == ~0) the bits of four floats.  Masking with
+// integer ANDs after unconditional loads keeps the compiler from turning a
+// select of loaded values into a branch around each load (which serializes
+// the loads of a span behind one another).
+__device__ inline float4 MaskBits(float4 v, uint32_t m) {
+    return make_float4(__uint_as_float(__float_as_uint(v.x) & m),
+                       __uint_as_float(__float_as_uint(v.y) & m),
+                       __uint_as_float(__float_as_uint(v.z) & m),
+                       __uint_as_float(__float_as_uint(v.w) & m));
+}
+
+// One lane's slice of one span: Load reads it from a weight row (a masked
+// lane, past the row's nb blocks / K inputs, reads block 0 and zeroes the
+// bits with m), XOff locates the matching x.
+template <int QT>
+struct Span;
+
+template <>
+struct Span<MLK_Q8_0> {
+    static constexpr int kElems = 256;
+    static constexpr int kXs = 1;  // float4 of x per token per lane
+    struct Raw {
+        uint32_t d, c;
+    };
+    __device__ static bool Valid(int64_t s, int lane, int64_t nb) { return s * 8 + lane / 8 < nb; }
+    __device__ static Raw Load(const uint8_t* row, int64_t s, int lane, bool ok, uint32_t m) {
+        const uint16_t* b = reinterpret_cast<const uint16_t*>(row + (ok ? (s * 8 + lane / 8) * 34 : 0));
+        const int j = lane % 8;
+        Raw r;
+        r.d = b[0] & m;
+        r.c = (static_cast<uint32_t>(b[1 + 2 * j]) | (static_cast<uint32_t>(b[2 + 2 * j]) << 16)) & m;
+        return r;
+    }
+    __device__ static int64_t XOff(int64_t s, int lane, int i) {
+        (void)i;
+        return s * 256 + 4 * lane;
+    }
+};
+
+template <>
+struct Span<MLK_Q4_0> {
+    static constexpr int kElems = 512;
+    static constexpr int kXs = 2;
+    struct Raw {
+        uint32_t d, c;
+    };
+    __device__ static bool Valid(int64_t s, int lane, int64_t nb) { return s * 16 + lane / 4 < nb; }
+    __device__ static Raw Load(const uint8_t* row, int64_t s, int lane, bool ok, uint32_t m) {
+        const uint16_t* b = reinterpret_cast<const uint16_t*>(row + (ok ? (s * 16 + lane / 4) * 18 : 0));
+        const int j = lane % 4;
+        Raw r;
+        r.d = b[0] & m;
+        r.c = (static_cast<uint32_t>(b[1 + 2 * j]) | (static_cast<uint32_t>(b[2 + 2 * j]) << 16)) & m;
+        return r;
+    }
+    __device__ static int64_t XOff(int64_t s, int lane, int i) {
+        return s * 512 + (lane / 4) * 32 + 4 * (lane % 4) + 16 * i;
+    }
+};
+
+template <>
+struct Span<MLK_Q4_1> {
+    static constexpr int kElems = 512;
+    static constexpr int kXs = 2;
+    struct Raw {
+        uint32_t d, c;  // d: fp16 d | fp16 m << 16
+    };
+    __device__ static bool Valid(int64_t s, int lane, int64_t nb) { return s * 16 + lane / 4 < nb; }
+    __device__ static Raw Load(const uint8_t* row, int64_t s, int lane, bool ok, uint32_t m) {
+        const uint32_t* b = reinterpret_cast<const uint32_t*>(row + (ok ? (s * 16 + lane / 4) * 20 : 0));
+        Raw r;
+        r.d = b[0] & m;
+        r.c = b[1 + lane % 4] & m;
+        return r;
+    }
+    __device__ static int64_t XOff(int64_t s, int lane, int i) {
+        return s * 512 + (lane / 4) * 32 + 4 * (lane % 4) + 16 * i;
+    }
+};
+
+template <>
+struct Span<kF32> {
+    static constexpr int kElems = 256;
+    static constexpr int kXs = 1;
+    struct Raw {
+        float4 w;
+    };
+    // nb here is K / 4 (float4 per row)
+    __device__ static bool Valid(int64_t s, int lane, int64_t nb) { return s * 64 + lane < nb; }
+    __device__ static Raw Load(const uint8_t* row, int64_t s, int lane, bool ok, uint32_t m) {
+        Raw r;
+        r.w = MaskBits(LoadNT(reinterpret_cast<const float4*>(row) + (ok ? s * 64 + lane : 0)), m);
+        return r;
+    }
+    __device__ static int64_t XOff(int64_t s, int lane, int i) {
+        (void)i;
+        return s * 256 + 4 * lane;
+    }
+};
+
+// acc[t] += the lane's slice of one weight row times token t's x slice.
+template <int QT, int R>
+__device__ inline void SliceDot(const typename Span<QT>::Raw& raw,
+                                const float4 (&xv)[R][Span<QT>::kXs], const float (&xs)[R],
+                                float (&acc)[R]) {
+    if constexpr (QT == kF32) {
 #pragma unroll
-    for (int t = 0; t < R; ++t) s[t] = 0.0f;
-    if constexpr (QT == MLK_Q8_0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t c = blk.c[i];
-            const float q0 = SByte(c, 0), q1 = SByte(c, 1), q2 = SByte(c, 2), q3 = SByte(c, 3);
-#pragma unroll
-            for (int t = 0; t < R; ++t) {
-                s[t] = fmaf(q0, xb[t][i].x, s[t]);
-                s[t] = fmaf(q1, xb[t][i].y, s[t]);
-                s[t] = fmaf(q2, xb[t][i].z, s[t]);
-                s[t] = fmaf(q3, xb[t][i].w, s[t]);
-            }
+        for (int t = 0; t < R; ++t) {
+            float a = acc[t];
+            a = fmaf(raw.w.x, xv[t][0].x, a);
+            a = fmaf(raw.w.y, xv[t][0].y, a);
+            a = fmaf(raw.w.z, xv[t][0].z, a);
+            a = fmaf(raw.w.w, xv[t][0].w, a);
+            acc[t] = a;
         }
+    } else if constexpr (QT == MLK_Q8_0) {
+        const float d = HalfHw(raw.d);
+        const float q0 = SByte(raw.c, 0), q1 = SByte(raw.c, 1), q2 = SByte(raw.c, 2),
+                    q3 = SByte(raw.c, 3);
 #pragma unroll
-        for (int t = 0; t < R; ++t) acc[t] = fmaf(blk.d, s[t], acc[t]);
+        for (int t = 0; t < R; ++t) {
+            float s = q0 * xv[t][0].x;
+            s = fmaf(q1, xv[t][0].y, s);
+            s = fmaf(q2, xv[t][0].z, s);
+            s = fmaf(q3, xv[t][0].w, s);
+            acc[t] = fmaf(d, s, acc[t]);
+        }
     } else {
+        const uint32_t lo = raw.c & 0x0F0F0F0Fu;
+        const uint32_t hi = (raw.c >> 4) & 0x0F0F0F0Fu;
+        const float l0 = UByte(lo, 0), l1 = UByte(lo, 1), l2 = UByte(lo, 2), l3 = UByte(lo, 3);
+        const float h0 = UByte(hi, 0), h1 = UByte(hi, 1), h2 = UByte(hi, 2), h3 = UByte(hi, 3);
+        const float d = HalfHw(raw.d & 0xFFFFu);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = blk.c[i] & 0x0F0F0F0Fu;
-            const uint32_t hi = (blk.c[i] >> 4) & 0x0F0F0F0Fu;
-            const float l0 = UByte(lo, 0), l1 = UByte(lo, 1), l2 = UByte(lo, 2), l3 = UByte(lo, 3);
-            const float h0 = UByte(hi, 0), h1 = UByte(hi, 1), h2 = UByte(hi, 2), h3 = UByte(hi, 3);
-#pragma unroll
-            for (int t = 0; t < R; ++t) {
-                s[t] = fmaf(l0, xb[t][i].x, s[t]);
-                s[t] = fmaf(l1, xb[t][i].y, s[t]);
-                s[t] = fmaf(l2, xb[t][i].z, s[t]);
-                s[t] = fmaf(l3, xb[t][i].w, s[t]);
-                s[t] = fmaf(h0, xb[t][i + 4].x, s[t]);
-                s[t] = fmaf(h1, xb[t][i + 4].y, s[t]);
-                s[t] = fmaf(h2, xb[t][i + 4].z, s[t]);
-                s[t] = fmaf(h3, xb[t][i + 4].w, s[t]);
+        for (int t = 0; t < R; ++t) {
+            float s = l0 * xv[t][0].x;
+            s = fmaf(l1, xv[t][0].y, s);
+            s = fmaf(l2, xv[t][0].z, s);
+            s = fmaf(l3, xv[t][0].w, s);
+            s = fmaf(h0, xv[t][1].x, s);
+            s = fmaf(h1, xv[t][1].y, s);
+            s = fmaf(h2, xv[t][1].z, s);
+            s = fmaf(h3, xv[t][1].w, s);
+            if constexpr (QT == MLK_Q4_0) {
+                acc[t] = fmaf(d, fmaf(-8.0f, xs[t], s), acc[t]);
+            } else {
+                const float m = HalfHw(raw.d >> 16);
+                acc[t] = fmaf(m, xs[t], fmaf(d, s, acc[t]));
             }
-        }
-        if constexpr (QT == MLK_Q4_0) {
-#pragma unroll
-            for (int t = 0; t < R; ++t) acc[t] = fmaf(blk.d, fmaf(-8.0f, xsum[t], s[t]), acc[t]);
-        } else {
-#pragma unroll
-            for (int t = 0; t < R; ++t) acc[t] = fmaf(blk.m, xsum[t], fmaf(blk.d, s[t], acc[t]));
         }
     }
 }
 
-// Loads the 32 inputs k0..k0+31 of each of R tokens (16-byte aligned rows);
-// tokens past n_tok repeat the last valid one (their sums are discarded).
-template <int R>
-__device__ inline void LoadXBlock(const float* x, int64_t K, int n_tok, int64_t k0,
-                                  float4 (&xb)[R][8], float (&xsum)[R], bool want_sum) {
+// The lane's x slices of span s for R token rows (rows past n_tok repeat the
+// last valid one; their sums are discarded), zero when the slice is masked.
+// xs = sum of the slice in the order SliceDot sums the codes (Q4 formats).
+template <int QT, int R>
+__device__ inline void LoadX(const float* x, int64_t K, int n_tok, int64_t s, int lane, bool ok,
+                             uint32_t m, float4 (&xv)[R][Span<QT>::kXs], float (&xs)[R]) {
 #pragma unroll
     for (int t = 0; t < R; ++t) {
         const int tt = t < n_tok ? t : n_tok - 1;
-        const float4* p = reinterpret_cast<const float4*>(x + tt * K + k0);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xb[t][i] = p[i];
-        float sx = 0.0f;
-        if (want_sum) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) sx += (xb[t][i].x + xb[t][i].y) + (xb[t][i].z + xb[t][i].w);
+        for (int i = 0; i < Span<QT>::kXs; ++i) {
+            xv[t][i] = MaskBits(
+                *reinterpret_cast<const float4*>(x + tt * K + (ok ? Span<QT>::XOff(s, lane, i) : 0)),
+                m);
         }
-        xsum[t] = sx;
-    }
-}
-
-// Sums acc over the wave and writes y[t, row0 + r] (+ bias) for valid rows
-// and tokens, one output per lane.
-template <int R>
-__device__ inline void StoreRows(float (&acc)[kRows][R], const float* bias, float* y, int64_t O,
-                                 int64_t row0, int n_tok, int lane) {
-#pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
-            const float v = WaveSumF(acc[r][t]);
-            if (lane == r * R + t && t < n_tok && row0 + r < O) {
-                y[t * O + row0 + r] = bias != nullptr ? v + bias[row0 + r] : v;
-            }
+        if constexpr (QT == MLK_Q4_0 || QT == MLK_Q4_1) {
+            float a = xv[t][0].x;
+            a += xv[t][0].y;
+            a += xv[t][0].z;
+            a += xv[t][0].w;
+            a += xv[t][1].x;
+            a += xv[t][1].y;
+            a += xv[t][1].z;
+            a += xv[t][1].w;
+            xs[t] = a;
+        } else {
+            xs[t] = 0.0f;
         }
     }
 }
 
-template <int QT, int R>
-__global__ __launch_bounds__(kThreads) void GemvQuantKernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ bias,
-    float* __restrict__ y, int64_t K, int64_t O, int64_t row_bytes, int n_tok) {
+// Sums N = 2^n values per lane over the wave.  Each step halves the values
+// a lane holds: lanes whose bit o is clear keep the lower half and add the
+// partner's lower half, the others the upper half; after log2(N) steps a
+// lane holds one value, index ReduceIdx(lane), and a plain butterfly over
+// the remaining lane bits completes it.  N - 1 + (6 - log2 N) shuffles
+// instead of 6 * N.
+template <int N>
+__device__ inline float TransposeReduce(float (&v)[N], int lane) {
+#pragma unroll
+    for (int h = N / 2, o = kWave / 2; h >= 1; h /= 2, o /= 2) {
+        const bool upper = (lane & o) != 0;
+#pragma unroll
+        for (int i = 0; i < h; ++i) {
+            const float send = upper ? v[i] : v[i + h];
+            const float keep = upper ? v[i + h] : v[i];
+            v[i] = keep + __shfl_xor(send, o, kWave);
+        }
+    }
+    float r = v[0];
+    constexpr int steps = __builtin_ctz(N);
+#pragma unroll
+    for (int o = (kWave / 2) >> steps; o >= 1; o /= 2) r += __shfl_xor(r, o, kWave);
+    return r;
+}
+
+template <int N>
+__device__ inline int ReduceIdx(int lane) {
+    int idx = 0;
+    int o = kWave / 2;
+#pragma unroll
+    for (int h = N / 2; h >= 1; h /= 2, o /= 2) idx += (lane & o) ? h : 0;
+    return idx;
+}
+
+// nb: blocks per weight row (quantized) or K / 4 (F32).  kTail: K is not a
+// whole number of spans, so the last span is masked per lane (otherwise no
+// lane is ever masked and the masks fold away).
+template <int QT, int R, int RW, bool kTail>
+__global__ __launch_bounds__(kThreads) void GemvSplitK(const float* __restrict__ x,
+                                                       const uint8_t* __restrict__ w,
+                                                       const float* __restrict__ bias,
+                                                       float* __restrict__ y, int64_t K,
+                                                       int64_t O, int64_t row_bytes, int64_t nb,
+                                                       int n_tok) {
+    using S = Span<QT>;
+    constexpr int N = RW * R;
+    static_assert(N <= kWave && (N & (N - 1)) == 0, "RW * R must be a power of two <= 64");
+    __shared__ float red[kWavesPerBlock][N];
     const int lane = threadIdx.x % kWave;
-    const int64_t row0 =
-        (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave) * kRows;
-    if (row0 >= O) return;  // wave-uniform
-    const int64_t P = K / 64;
-    const uint8_t* wr[kRows];
+    const int wave = threadIdx.x / kWave;
+    const int64_t row0 = static_cast<int64_t>(blockIdx.x) * RW;
+    const uint8_t* wr[RW];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        wr[r] = w + (row0 + r < O ? row0 + r : O - 1) * row_bytes;
-    }
-    float acc[kRows][R];
+    for (int r = 0; r < RW; ++r) wr[r] = w + (row0 + r < O ? row0 + r : O - 1) * row_bytes;
+    float acc[RW][R];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
         for (int t = 0; t < R; ++t) acc[r][t] = 0.0f;
-
-    for (int64_t p = lane; p < P; p += kWave) {
-        uint32_t u[kRows][Pair<QT>::kWords];
+    const int64_t NS = (K + S::kElems - 1) / S::kElems;
+    int64_t s = wave;
+    for (; s + kWavesPerBlock < NS; s += 2 * kWavesPerBlock) {
+        const int64_t s1 = s + kWavesPerBlock;
+        const bool ok0 = !kTail || S::Valid(s, lane, nb), ok1 = !kTail || S::Valid(s1, lane, nb);
+        const uint32_t m0 = ok0 ? ~0u : 0u, m1 = ok1 ? ~0u : 0u;
+        typename S::Raw raw0[RW], raw1[RW];
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) LoadPair<QT>(wr[r] + p * Pair<QT>::kBytes, u[r]);
-        float4 xb[R][8];
-        float xsum[R];
-        LoadXBlock<R>(x, K, n_tok, p * 64, xb, xsum, QT != MLK_Q8_0);
+        for (int r = 0; r < RW; ++r) raw0[r] = S::Load(wr[r], s, lane, ok0, m0);
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) BlockDot<QT, 0, R>(u[r], xb, xsum, acc[r]);
-        LoadXBlock<R>(x, K, n_tok, p * 64 + 32, xb, xsum, QT != MLK_Q8_0);
+        for (int r = 0; r < RW; ++r) raw1[r] = S::Load(wr[r], s1, lane, ok1, m1);
+        float4 xv[R][S::kXs];
+        float xs[R];
+        LoadX<QT, R>(x, K, n_tok, s, lane, ok0, m0, xv, xs);
 #pragma unroll
-        for (int r = 0; r < kRows; ++r) BlockDot<QT, 1, R>(u[r], xb, xsum, acc[r]);
+        for (int r = 0; r < RW; ++r) SliceDot<QT, R>(raw0[r], xv, xs, acc[r]);
+        LoadX<QT, R>(x, K, n_tok, s1, lane, ok1, m1, xv, xs);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) SliceDot<QT, R>(raw1[r], xv, xs, acc[r]);
     }
-    StoreRows<R>(acc, bias, y, O, row0, n_tok, lane);
-}
-
-template <int R>
-__global__ __launch_bounds__(kThreads) void GemvF32Kernel(
-    const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
-    float* __restrict__ y, int64_t K, int64_t O, int n_tok) {
-    const int lane = threadIdx.x % kWave;
-    const int64_t row0 =
-        (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave) * kRows;
-    if (row0 >= O) return;
-    const int64_t C = K / 4;
-    const float4* wr[kRows];
+    if (s < NS) {
+        const bool ok0 = !kTail || S::Valid(s, lane, nb);
+        const uint32_t m0 = ok0 ? ~0u : 0u;
+        typename S::Raw raw0[RW];
 #pragma unroll
-    for (int r = 0; r < kRows; ++r) {
-        wr[r] = reinterpret_cast<const float4*>(w + (row0 + r < O ? row0 + r : O - 1) * K);
+        for (int r = 0; r < RW; ++r) raw0[r] = S::Load(wr[r], s, lane, ok0, m0);
+        float4 xv[R][S::kXs];
+        float xs[R];
+        LoadX<QT, R>(x, K, n_tok, s, lane, ok0, m0, xv, xs);
+#pragma unroll
+        for (int r = 0; r < RW; ++r) SliceDot<QT, R>(raw0[r], xv, xs, acc[r]);
     }
-    const float4* xr[R];
+    float v[N];
 #pragma unroll
-    for (int t = 0; t < R; ++t) xr[t] = reinterpret_cast<const float4*>(x + (t < n_tok ? t : n_tok - 1) * K);
-    float acc[kRows][R];
+    for (int r = 0; r < RW; ++r)
 #pragma unroll
-    for (int r = 0; r < kRows; ++r)
-#pragma unroll
-        for (int t = 0; t < R; ++t) acc[r][t] = 0.0f;
-    for (int64_t c = lane; c < C; c += kWave) {
-        float4 wv[kRows];
-#pragma unroll
-        for (int r = 0; r < kRows; ++r) wv[r] = LoadNT(wr[r] + c);
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
-            const float4 xv = xr[t][c];
-#pragma unroll
-            for (int r = 0; r < kRows; ++r) {
-                float a = acc[r][t];
-                a = fmaf(xv.x, wv[r].x, a);
-                a = fmaf(xv.y, wv[r].y, a);
-                a = fmaf(xv.z, wv[r].z, a);
-                a = fmaf(xv.w, wv[r].w, a);
-                acc[r][t] = a;
-            }
-        }
+        for (int t = 0; t < R; ++t) v[r * R + t] = acc[r][t];
+    const float tot = TransposeReduce<N>(v, lane);
+    if ((lane & (kWave / N - 1)) == 0) red[wave][ReduceIdx<N>(lane)] = tot;
+    __syncthreads();
+    if (threadIdx.x < N) {
+        const int i = threadIdx.x;
+        const float sum = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
+        const int r = i / R, t = i % R;
+        const int64_t row = row0 + r;
+        if (t < n_tok && row < O) y[t * O + row] = bias != nullptr ? sum + bias[row] : sum;
     }
-    StoreRows<R>(acc, bias, y, O, row0, n_tok, lane);
 }
 
 // Any shape and alignment: one wave per weight row, every token, byte loads.
@@ -322,7 +378,7 @@ __device__ inline float DecodeAny(const uint8_t* row, int64_t k) {
     }
 }
 
-template <int QT>  // QT < 0: F32 weights
+template <int QT>  // QT == kF32: F32 weights
 __global__ __launch_bounds__(kThreads) void GemvAnyKernel(
     const float* __restrict__ x, const void* __restrict__ w, const float* __restrict__ bias,
     float* __restrict__ y, int64_t K, int64_t O, int64_t row_bytes, int64_t T) {
@@ -334,7 +390,7 @@ __global__ __launch_bounds__(kThreads) void GemvAnyKernel(
         float s = 0.0f;
         for (int64_t k = lane; k < K; k += kWave) {
             float wk;
-            if constexpr (QT < 0) {
+            if constexpr (QT == kF32) {
                 wk = reinterpret_cast<const float*>(wr)[k];
             } else {
                 wk = DecodeAny<QT>(wr, k);
@@ -388,30 +444,49 @@ mlk_status CheckLinear(const char* fn, const float* x, const void* w, float* y, 
     if (!Aligned(x, 4) || !Aligned(y, 4)) {
         return Fail(MLK_ERR_INVALID, "%s: x and y must be 4-byte aligned", fn);
     }
+    if (O > (int64_t{1} << 30)) {
+        return Fail(MLK_ERR_INVALID, "%s: out_features %lld exceeds 2^30", fn,
+                    static_cast<long long>(O));
+    }
     return MLK_OK;
 }
 
-unsigned GemvGrid(int64_t O, int rows_per_wave) {
-    return FullGrid(O, static_cast<int64_t>(kWavesPerBlock) * rows_per_wave);
-}
-
-template <int QT, int R>
-void LaunchGemvQuant(const float* x, const uint8_t* w, const float* bias, float* y, int64_t K,
-                     int64_t O, int64_t row_bytes, int n, hipStream_t s) {
-    hipLaunchKernelGGL((GemvQuantKernel<QT, R>), dim3(GemvGrid(O, kRows)), dim3(kThreads), 0, s,
-                       x, w, bias, y, K, O, row_bytes, n);
-}
-
-template <int QT>
-void GemvQuantChunk(const float* x, const uint8_t* w, const float* bias, float* y, int64_t K,
-                    int64_t O, int64_t row_bytes, int n, hipStream_t s) {
-    if (n == 1) {
-        LaunchGemvQuant<QT, 1>(x, w, bias, y, K, O, row_bytes, n, s);
-    } else if (n == 2) {
-        LaunchGemvQuant<QT, 2>(x, w, bias, y, K, O, row_bytes, n, s);
-    } else {
-        LaunchGemvQuant<QT, 4>(x, w, bias, y, K, O, row_bytes, n, s);
+// Token rows in launches of up to kMaxTok; RW weight rows per workgroup.
+template <int QT, int RW, bool kTail>
+mlk_status GemvRows(const float* x, const uint8_t* w, const float* bias, float* y, int64_t K,
+                    int64_t O, int64_t row_bytes, int64_t nb, int64_t rows, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>((O + RW - 1) / RW));
+    for (int64_t t0 = 0; t0 < rows; t0 += kMaxTok) {
+        const int n = static_cast<int>(rows - t0 < kMaxTok ? rows - t0 : kMaxTok);
+        const float* xt = x + t0 * K;
+        float* yt = y + t0 * O;
+        if (n == 1) {
+            hipLaunchKernelGGL((GemvSplitK<QT, 1, RW, kTail>), grid, dim3(kThreads), 0, s, xt, w,
+                               bias, yt, K, O, row_bytes, nb, n);
+        } else if (n == 2) {
+            hipLaunchKernelGGL((GemvSplitK<QT, 2, RW, kTail>), grid, dim3(kThreads), 0, s, xt, w,
+                               bias, yt, K, O, row_bytes, nb, n);
+        } else {
+            hipLaunchKernelGGL((GemvSplitK<QT, 4, RW, kTail>), grid, dim3(kThreads), 0, s, xt, w,
+                               bias, yt, K, O, row_bytes, nb, n);
+        }
+        const mlk_status st = CheckLaunch("GemvSplitK");
+        if (st != MLK_OK) return st;
     }
+    return MLK_OK;
+}
+
+// RW = 4 reuses each x slice over more rows; below 4096 outputs, RW = 2
+// gives the small projections (K/V: 1024 outputs) enough workgroups.
+template <int QT>
+mlk_status Gemv(const float* x, const uint8_t* w, const float* bias, float* y, int64_t K,
+                int64_t O, int64_t row_bytes, int64_t nb, int64_t rows, hipStream_t s) {
+    if (K % Span<QT>::kElems != 0) {
+        return O >= 4096 ? GemvRows<QT, 4, true>(x, w, bias, y, K, O, row_bytes, nb, rows, s)
+                         : GemvRows<QT, 2, true>(x, w, bias, y, K, O, row_bytes, nb, rows, s);
+    }
+    return O >= 4096 ? GemvRows<QT, 4, false>(x, w, bias, y, K, O, row_bytes, nb, rows, s)
+                     : GemvRows<QT, 2, false>(x, w, bias, y, K, O, row_bytes, nb, rows, s);
 }
 
 }  // namespace
@@ -437,7 +512,8 @@ mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_bl
     const int64_t row_bytes = ((K + 31) / 32) * BlockBytes(quant_type);
     const uint8_t* w = static_cast<const uint8_t*>(w_blocks);
     const hipStream_t s = AsStream(stream);
-    const bool fast = K % 64 == 0 && Aligned(w_blocks, 4) && Aligned(x, 16);
+    const bool fast = K % 32 == 0 && Aligned(x, 16) &&
+                      (quant_type != MLK_Q4_1 || Aligned(w_blocks, 4));
     if (!fast) {
         const unsigned grid = FullGrid(O, kWavesPerBlock);
         switch (quant_type) {
@@ -456,19 +532,12 @@ mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_bl
         }
         return CheckLaunch("GemvAnyKernel");
     }
-    for (int64_t t0 = 0; t0 < rows; t0 += kMaxTok) {
-        const int n = static_cast<int>(rows - t0 < kMaxTok ? rows - t0 : kMaxTok);
-        const float* xt = x + t0 * K;
-        float* yt = y + t0 * O;
-        switch (quant_type) {
-            case MLK_Q8_0: GemvQuantChunk<MLK_Q8_0>(xt, w, bias, yt, K, O, row_bytes, n, s); break;
-            case MLK_Q4_0: GemvQuantChunk<MLK_Q4_0>(xt, w, bias, yt, K, O, row_bytes, n, s); break;
-            default: GemvQuantChunk<MLK_Q4_1>(xt, w, bias, yt, K, O, row_bytes, n, s); break;
-        }
-        st = CheckLaunch("GemvQuantKernel");
-        if (st != MLK_OK) return st;
+    const int64_t nb = K / 32;
+    switch (quant_type) {
+        case MLK_Q8_0: return Gemv<MLK_Q8_0>(x, w, bias, y, K, O, row_bytes, nb, rows, s);
+        case MLK_Q4_0: return Gemv<MLK_Q4_0>(x, w, bias, y, K, O, row_bytes, nb, rows, s);
+        default: return Gemv<MLK_Q4_1>(x, w, bias, y, K, O, row_bytes, nb, rows, s);
     }
-    return MLK_OK;
 }
 
 mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, float* y,
@@ -481,26 +550,12 @@ mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, flo
     const int64_t K = in_features, O = out_features;
     const hipStream_t s = AsStream(stream);
     if (K % 4 != 0 || !Aligned(x, 16) || !Aligned(w, 16)) {
-        hipLaunchKernelGGL(GemvAnyKernel<-1>, dim3(FullGrid(O, kWavesPerBlock)), dim3(kThreads), 0,
+        hipLaunchKernelGGL(GemvAnyKernel<kF32>, dim3(FullGrid(O, kWavesPerBlock)), dim3(kThreads), 0,
                            s, x, static_cast<const void*>(w), bias, y, K, O, K * 4, rows);
         return CheckLaunch("GemvAnyKernel");
     }
-    for (int64_t t0 = 0; t0 < rows; t0 += kMaxTok) {
-        const int n = static_cast<int>(rows - t0 < kMaxTok ? rows - t0 : kMaxTok);
-        const float* xt = x + t0 * K;
-        float* yt = y + t0 * O;
-        const dim3 grid(GemvGrid(O, kRows));
-        if (n == 1) {
-            hipLaunchKernelGGL(GemvF32Kernel<1>, grid, dim3(kThreads), 0, s, xt, w, bias, yt, K, O, n);
-        } else if (n == 2) {
-            hipLaunchKernelGGL(GemvF32Kernel<2>, grid, dim3(kThreads), 0, s, xt, w, bias, yt, K, O, n);
-        } else {
-            hipLaunchKernelGGL(GemvF32Kernel<4>, grid, dim3(kThreads), 0, s, xt, w, bias, yt, K, O, n);
-        }
-        st = CheckLaunch("GemvF32Kernel");
-        if (st != MLK_OK) return st;
-    }
-    return MLK_OK;
+    return Gemv<kF32>(x, reinterpret_cast<const uint8_t*>(w), bias, y, K, O, K * 4, K / 4, rows,
+                      s);
 }
 
 mlk_status mlk_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t k,

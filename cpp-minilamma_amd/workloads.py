@@ -91,3 +91,30 @@ def bytes_chain(cfg, T, with_gather=True):
     if with_gather:
         b += bytes_gather_f32(T, cfg["dim"])
     return b
+
+
+# ------------------------------------------------------- linear layers
+# The seven projections of one Llama layer, (name, in_features,
+# out_features): wq, wk, wv, wo, w_gate, w_up, w_down.
+
+def layer_linears(cfg):
+    D, H, KV, hd, F = cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"]
+    return (("wq", D, H * hd), ("wk", D, KV * hd), ("wv", D, KV * hd), ("wo", H * hd, D),
+            ("w_gate", D, F), ("w_up", D, F), ("w_down", F, D))
+
+
+def weight_bytes(qtype, in_features, out_features):
+    """Bytes of one weight matrix: fp32 [out, in], or out rows of
+    ceil(in / 32) blocks."""
+    if qtype == "f32":
+        return 4 * in_features * out_features
+    return out_features * -(-in_features // 32) * BLOCK_BYTES[qtype]
+
+
+def bytes_linear(qtype, T, in_features, out_features):
+    """Read the weight once, read x [T, in], write y [T, out]."""
+    return weight_bytes(qtype, in_features, out_features) + 4 * T * (in_features + out_features)
+
+
+def flops_linear(T, in_features, out_features):
+    return 2 * T * in_features * out_features

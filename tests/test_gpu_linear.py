@@ -71,10 +71,13 @@ def test_quant_linear_reference_patterns(mlk, orc):
 @pytest.mark.parametrize("qt", QT)
 @pytest.mark.parametrize("shape", [(131, 64, 1), (4099, 4096, 1), (64, 4096, 2), (37, 4096, 3),
                                    (16, 4096, 4), (33, 14336, 5), (200, 128, 9), (5, 96, 2),
-                                   (1, 4096, 1)])
+                                   (1, 4096, 1), (4096, 320, 2), (4095, 4096, 1), (8193, 1056, 3),
+                                   (1024, 4096, 4), (4096, 4096, 7)])
 def test_quant_linear_shapes(mlk, orc, qt, shape):
-    """The dwordx4 pair path (in % 64 == 0), tails of the 4-row wave groups,
-    token counts 1..9 (chunks of 4), and in % 64 != 0 (byte-load path)."""
+    """The split-K path: whole and partial last spans (in % 256 and % 512 !=
+    0, masked per lane), partial last workgroups of 2 and 4 rows (out odd,
+    out around 4096 where the rows per workgroup change), token counts 1..9
+    (launches of up to 4 rows)."""
     O, K, T = shape
     rng = np.random.default_rng(O * 7 + K + T)
     w = normal(rng, (O, K), 0.02)
@@ -159,7 +162,8 @@ def test_f32_linear_and_matmul(mlk, orc):
     ex, s = dot_exact(x, w, b)
     assert_dot_close(run_f32(mlk, x, w, b), ex, s, 34, "bias")
     rng = np.random.default_rng(6)
-    for O, K, T in ((4096, 4096, 1), (1000, 4096, 3), (77, 1000, 6), (9, 35, 2), (3, 14336, 4)):
+    for O, K, T in ((4096, 4096, 1), (1000, 4096, 3), (77, 1000, 6), (9, 35, 2), (3, 14336, 4),
+                    (4097, 100, 3), (14336, 4096, 2), (5, 260, 5)):
         w = normal(rng, (O, K), 0.02)
         x = normal(rng, (T, K))
         bias = normal(rng, (O,))
