@@ -71,6 +71,10 @@ _SIGNATURES = {
     "mlk_linear_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "mlk_matmul_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "mlk_fill_normal_f32": [_vp, _i64, _f, _f, C.c_uint64, _vp],
+    "mlk_kv_write_f32": [_vp, _vp, _i64, _i64, _i32, _i32, _i64, _vp, _i64, _vp, _i64, _vp, _i32,
+                         _i64, _vp, _vp],
+    "mlk_attention_decode_f32": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, _vp,
+                                 _i32, _i64, _i64, _vp, _vp, C.c_size_t, _vp, _vp],
     "mlk_device_count": [C.POINTER(C.c_int)],
     "mlk_set_device": [C.c_int],
     "mlk_get_device": [C.POINTER(C.c_int)],
@@ -114,6 +118,8 @@ def _load():
     lib.mlk_abi_version.argtypes = []
     lib.mlk_quant_bytes.restype = C.c_int64
     lib.mlk_quant_bytes.argtypes = [_i32, _i64, _i64]
+    lib.mlk_attention_workspace_bytes.restype = C.c_int64
+    lib.mlk_attention_workspace_bytes.argtypes = [_i64, _i32, _i32, _i32, _i64]
     return lib
 
 
@@ -131,7 +137,8 @@ def check(status, caller=None):
 def exported_symbols():
     """Names of every C ABI function the binding binds (used by the CPU tests)."""
     return sorted(list(_SIGNATURES) + ["mlk_last_error", "mlk_status_string",
-                                       "mlk_abi_version", "mlk_quant_bytes"])
+                                       "mlk_abi_version", "mlk_quant_bytes",
+                                       "mlk_attention_workspace_bytes"])
 
 
 # ------------------------------------------------------------------ runtime
@@ -402,6 +409,37 @@ def linear_f32(x, w, y, rows, in_features, out_features, bias=None, stream=None)
 def matmul(a, b, c, m, k, n, stream=None):
     """c[m, n] = a[m, k] @ b[k, n]."""
     check(lib.mlk_matmul_f32(_p(a), _p(b), _p(c), m, k, n, _sp(stream)), "mlk_matmul_f32")
+
+
+def kv_write(k_cache, v_cache, n_layers, max_seq, n_kv_heads, head_dim, layer, k, v, n_tokens,
+             positions=None, pos0=0, k_row_stride=None, v_row_stride=None, err=None,
+             stream=None):
+    """Copies k, v rows [n_tokens, n_kv_heads * head_dim] into cache slots
+    (layer, positions[t] or pos0 + t) of caches [n_layers, max_seq,
+    n_kv_heads, head_dim]."""
+    row = n_kv_heads * head_dim
+    check(lib.mlk_kv_write_f32(_p(k_cache), _p(v_cache), n_layers, max_seq, n_kv_heads, head_dim,
+                               layer, _p(k), k_row_stride or row, _p(v), v_row_stride or row,
+                               _p(positions), pos0, n_tokens, _p(err), _sp(stream)),
+          "mlk_kv_write_f32")
+
+
+def attention_workspace_bytes(n_tokens, n_heads, n_kv_heads, head_dim, max_ctx):
+    return int(lib.mlk_attention_workspace_bytes(n_tokens, n_heads, n_kv_heads, head_dim,
+                                                 max_ctx))
+
+
+def attention_decode(q, k_cache, v_cache, n_layers, max_seq, n_heads, n_kv_heads, head_dim,
+                     layer, n_tokens, out, max_ctx, positions=None, pos0=0, workspace=None,
+                     workspace_bytes=0, q_row_stride=None, err=None, stream=None):
+    """out [n_tokens, n_heads, head_dim] = attention of q rows over cache
+    positions 0..pos of `layer` (pos = positions[t] or pos0 + t < max_ctx)."""
+    check(lib.mlk_attention_decode_f32(_p(q), q_row_stride or n_heads * head_dim, _p(k_cache),
+                                       _p(v_cache), n_layers, max_seq, n_heads, n_kv_heads,
+                                       head_dim, layer, _p(positions), pos0, n_tokens, max_ctx,
+                                       _p(out), _p(workspace), workspace_bytes, _p(err),
+                                       _sp(stream)),
+          "mlk_attention_decode_f32")
 
 
 def quant_bytes(qtype, rows, cols):

@@ -24,6 +24,8 @@
  *                                      signatures become n_tokens = 1)
  *   include/cuda_matmul.h:7-18      -> mlk_linear_f32, mlk_matmul_f32
  *   include/cuda_quant.h:12-25      -> mlk_linear_quant
+ *   include/cuda_kvcache.h:23       -> mlk_kv_write_f32
+ *   include/cuda_attention.h:9-13   -> mlk_attention_decode_f32
  *   include/cuda_runtime.h:8-42     -> the runtime entries at the end
  */
 #ifndef MINILAMMA_HIP_H
@@ -167,6 +169,52 @@ mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, flo
  * (include/cuda_matmul.h:7; src/cuda_matmul.cc:199-232). */
 mlk_status mlk_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t k,
                           int64_t n, void* stream);
+
+/*
+ * KV cache write: rows t of k and v (n_kv_heads * head_dim floats each, row
+ * t at k + t * k_row_stride) go to slot (layer, pos_t) of the caches
+ * [n_layers, max_seq, n_kv_heads, head_dim], pos_t = positions[t] (device
+ * array) or pos0 + t.  A position outside [0, max_seq) writes nothing and,
+ * when err != NULL, stores a nonzero value in *err (the caller clears it).
+ * Replaces CudaCache::WriteDevice (include/cuda_kvcache.h:23;
+ * src/cuda_kvcache.cc:209-237, two device copies per token).
+ */
+mlk_status mlk_kv_write_f32(float* k_cache, float* v_cache, int64_t n_layers, int64_t max_seq,
+                            int32_t n_kv_heads, int32_t head_dim, int64_t layer, const float* k,
+                            int64_t k_row_stride, const float* v, int64_t v_row_stride,
+                            const int32_t* positions, int32_t pos0, int64_t n_tokens,
+                            int32_t* err, void* stream);
+
+/* Bytes of workspace mlk_attention_decode_f32 needs for these sizes (0 when
+ * one chunk covers max_ctx and no workspace is used; 0 on bad input). */
+int64_t mlk_attention_workspace_bytes(int64_t n_tokens, int32_t n_heads, int32_t n_kv_heads,
+                                      int32_t head_dim, int64_t max_ctx);
+
+/*
+ * Decode attention over the cache of `layer`: for query row t (q row t at
+ * q + t * q_row_stride, [n_heads, head_dim]) at position pos_t
+ * (positions[t] or pos0 + t), query head i reads KV head
+ * i / (n_heads / n_kv_heads):
+ *   s_j = (q_i . k_j) / sqrt(head_dim),  p = softmax(s_0..s_pos),
+ *   out[t, i] = sum_j p_j v_j
+ * (src/forward.cc:265-298).  Every pos_t must be < max_ctx <= max_seq (a
+ * bound the caller knows, e.g. the cache length); a position outside
+ * [0, max_ctx) gives a zero row and raises *err.  head_dim <= 256.  When
+ * mlk_attention_workspace_bytes() is nonzero, `workspace` must hold that many
+ * bytes (chunk partials); out must not alias q.  Sums are fp32 in the
+ * kernel's order (the reference's tolerance: 2e-5 against float64,
+ * test/cuda_attention_test.cc:108-109).
+ * Replaces CudaAttentionDevice (include/cuda_attention.h:12-13;
+ * src/cuda_attention.cu:77-176, 2 launches, one cudaMalloc and a device
+ * synchronize per call).
+ */
+mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const float* k_cache,
+                                    const float* v_cache, int64_t n_layers, int64_t max_seq,
+                                    int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                    int64_t layer, const int32_t* positions, int32_t pos0,
+                                    int64_t n_tokens, int64_t max_ctx, float* out,
+                                    void* workspace, size_t workspace_bytes, int32_t* err,
+                                    void* stream);
 
 /* Synthetic-input helper (not a reference op): fills x[i] with
  * mean + std * N(0,1) from a counter-based generator keyed by seed and i, so

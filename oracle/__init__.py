@@ -82,6 +82,32 @@ class _Oracle:
                                  [_f32p, _f32p, C.c_void_p, _f32p, _i64, _i64, _i64, C.c_int])
         self._matmul_f32 = _bind(lib, "orc_matmul_f32", C.c_int,
                                  [_f32p, _f32p, _f32p, _i64, _i64, _i64, C.c_int])
+        self._kv_write = _bind(lib, "orc_kv_write", C.c_int,
+                               [_f32p, _f32p, _i64, _i64, _i32, _i32, _i64, _i32p, _i64, _f32p,
+                                _f32p])
+        self._attention = _bind(lib, "orc_attention", C.c_int,
+                                [_f32p, _f32p, _f32p, _i64, _i64, _i32, _i32, _i32, _i64, _i32p,
+                                 _i64, _f32p])
+
+    # ---- attention and KV cache ----------------------------------------------
+    def kv_write(self, k_cache, v_cache, layer, positions, k, v):
+        """Writes k, v [T, KV, hd] into slots (layer, positions[t]) of the caches
+        [L, S, KV, hd] in place."""
+        L, S, KV, hd = k_cache.shape
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        _check(self._kv_write(k_cache.reshape(-1), v_cache.reshape(-1), L, S, KV, hd, layer, pos,
+                              pos.size, _f32(k).reshape(-1), _f32(v).reshape(-1)))
+
+    def attention(self, q, k_cache, v_cache, layer, positions):
+        """out [T, H, hd] for q [T, H, hd] against caches [L, S, KV, hd]."""
+        q = _f32(q)
+        L, S, KV, hd = k_cache.shape
+        T, H = q.shape[0], q.shape[1]
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        out = np.empty((T, H, hd), np.float32)
+        _check(self._attention(q.reshape(-1), _f32(k_cache).reshape(-1), _f32(v_cache).reshape(-1),
+                               L, S, H, KV, hd, layer, pos, T, out.reshape(-1)))
+        return out
 
     def fp16_to_fp32_array(self, codes):
         codes = np.ascontiguousarray(codes, dtype=np.uint16)
@@ -268,6 +294,21 @@ class _Reference:
                                  [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int])
         self._matmul_f32 = _bind(lib, "ref_matmul_f32", C.c_int,
                                  [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int])
+        self._attention = _bind(lib, "ref_attention", C.c_int,
+                                [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                 C.c_int, C.c_int, _f32p])
+
+    def attention(self, q, k_rows, v_rows, n_layers, max_seq, layer, pos):
+        """One query token q [H, hd] at `pos`: k_rows / v_rows [pos + 1, KV, hd]
+        are written to the reference's own KvCache (src/kvcache.cc) slots
+        0..pos of `layer`, then the ForwardAttention loop runs over it."""
+        q = _f32(q)
+        H, hd = q.shape
+        KV = k_rows.shape[1]
+        out = np.empty((H, hd), np.float32)
+        _check(self._attention(q.reshape(-1), _f32(k_rows).reshape(-1), _f32(v_rows).reshape(-1),
+                               n_layers, max_seq, H, KV, hd, layer, pos, out.reshape(-1)))
+        return out
 
     def linear_quant(self, qtype, x, blocks, out_features, n_threads=0):
         x = _f32(x)

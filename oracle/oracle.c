@@ -655,6 +655,89 @@ int orc_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t 
     return par_for(m * n, n_threads, matmul_outputs, &job);
 }
 
+/* ------------------------------------------------ attention, KV cache */
+
+static int kv_args_ok(int64_t n_layers, int64_t max_seq, int32_t n_kv_heads, int32_t head_dim,
+                      int64_t layer)
+{
+    return n_layers > 0 && max_seq > 0 && n_kv_heads > 0 && head_dim > 0 && layer >= 0 &&
+           layer < n_layers;
+}
+
+int orc_kv_write(float* k_cache, float* v_cache, int64_t n_layers, int64_t max_seq,
+                 int32_t n_kv_heads, int32_t head_dim, int64_t layer, const int32_t* positions,
+                 int64_t n_tokens, const float* k, const float* v)
+{
+    if (!kv_args_ok(n_layers, max_seq, n_kv_heads, head_dim, layer) || n_tokens < 0) {
+        return ORC_EINVAL;
+    }
+    const int64_t row = (int64_t)n_kv_heads * head_dim;
+    for (int64_t t = 0; t < n_tokens; ++t) {
+        if (positions[t] < 0 || positions[t] >= max_seq) {
+            return ORC_EINVAL; /* KvCache::Write throws "Pos Out Of Range" */
+        }
+    }
+    for (int64_t t = 0; t < n_tokens; ++t) {
+        const int64_t slot = (layer * max_seq + positions[t]) * row;
+        memcpy(k_cache + slot, k + t * row, (size_t)row * sizeof(float));
+        memcpy(v_cache + slot, v + t * row, (size_t)row * sizeof(float));
+    }
+    return ORC_OK;
+}
+
+int orc_attention(const float* q, const float* k_cache, const float* v_cache, int64_t n_layers,
+                  int64_t max_seq, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                  int64_t layer, const int32_t* positions, int64_t n_tokens, float* out)
+{
+    if (!kv_args_ok(n_layers, max_seq, n_kv_heads, head_dim, layer) || n_tokens < 0 ||
+        n_heads <= 0 || n_heads % n_kv_heads != 0) {
+        return ORC_EINVAL;
+    }
+    for (int64_t t = 0; t < n_tokens; ++t) {
+        if (positions[t] < 0 || positions[t] >= max_seq) {
+            return ORC_EINVAL;
+        }
+    }
+    const int64_t hd = head_dim;
+    const int64_t row = (int64_t)n_kv_heads * hd;
+    const int32_t group = n_heads / n_kv_heads;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* scores = (float*)malloc((size_t)max_seq * sizeof(float));
+    float* probs = (float*)malloc((size_t)max_seq * sizeof(float));
+    if (scores == NULL || probs == NULL) {
+        free(scores);
+        free(probs);
+        return ORC_EINVAL;
+    }
+    for (int64_t t = 0; t < n_tokens; ++t) {
+        const int64_t pos = positions[t];
+        for (int32_t i = 0; i < n_heads; ++i) {
+            const int64_t kvh = i / group;
+            const float* qh = q + (t * n_heads + i) * hd;
+            for (int64_t j = 0; j <= pos; ++j) {
+                const float* kr = k_cache + (layer * max_seq + j) * row + kvh * hd;
+                float dot = 0.0f;
+                for (int64_t d = 0; d < hd; ++d) {
+                    dot += qh[d] * kr[d];
+                }
+                scores[j] = dot * scale;
+            }
+            orc_softmax(scores, probs, pos + 1);
+            float* oh = out + (t * n_heads + i) * hd;
+            for (int64_t d = 0; d < hd; ++d) {
+                float val = 0.0f;
+                for (int64_t j = 0; j <= pos; ++j) {
+                    val += probs[j] * v_cache[(layer * max_seq + j) * row + kvh * hd + d];
+                }
+                oh[d] = val;
+            }
+        }
+    }
+    free(scores);
+    free(probs);
+    return ORC_OK;
+}
+
 /* --------------------------------------------------- CPU baseline port */
 
 int orc_parallel_threads(int n_threads)

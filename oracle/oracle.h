@@ -145,6 +145,25 @@ int orc_linear_f32(const float* x, const float* w, const float* bias, float* y, 
 int orc_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t k, int64_t n,
                    int n_threads);
 
+/* ---- decode attention and the KV cache ----
+ * Caches are [n_layers, max_seq, n_kv_heads, head_dim] fp32 (the layout of
+ * KvCache, include/kvcache.h:8-10, and of CudaCache, include/cuda_kvcache.h:5-6).
+ *
+ * src/kvcache.cc:19-50 KvCache::Write, for n_tokens rows: k and v rows t
+ * ([n_kv_heads, head_dim] each) are copied to slot (layer, positions[t]). */
+int orc_kv_write(float* k_cache, float* v_cache, int64_t n_layers, int64_t max_seq,
+                 int32_t n_kv_heads, int32_t head_dim, int64_t layer, const int32_t* positions,
+                 int64_t n_tokens, const float* k, const float* v);
+/* src/forward.cc:265-298 ForwardAttention after its cache write, for
+ * n_tokens query rows q [n_tokens, n_heads, head_dim] at positions[t]: query
+ * head i reads KV head i / (n_heads / n_kv_heads); score j = (float sum of
+ * q_d * k_d in d order) * (1 / sqrtf(head_dim)) for j = 0..pos; SoftMax
+ * (src/ops.cc:113-134: max, expf(s - max), float sum in order, divide);
+ * out_d = float sum of p_j * v_jd in j order. */
+int orc_attention(const float* q, const float* k_cache, const float* v_cache, int64_t n_layers,
+                  int64_t max_seq, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                  int64_t layer, const int32_t* positions, int64_t n_tokens, float* out);
+
 /* ---- CPU baseline (bench.py cpu_baseline leg, kind "port") ----
  * thread_pool/thread_pool.cc:31-90 ParallelFor: static contiguous chunks,
  * serial when n/16 < threads.  n_threads <= 0 means hardware concurrency. */

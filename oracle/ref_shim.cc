@@ -1,19 +1,21 @@
 // ref_shim.cc -- C entry points over the reference's own CPU sources.
 //
 // TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together
-// with the reference's src/{tensor,ops,quant,quantiezd_tensor}.cc,
+// with the reference's src/{tensor,ops,quant,quantiezd_tensor,kvcache}.cc,
 // matumal/matuml_ops.cc and thread_pool/thread_pool.cc, straight from where
 // they lie under the reference tree, into oracle/_ref/libref*.so.  Tests use
 // it to pin the C restatement (oracle.c) and tests/golden/make_golden.py
 // writes the golden fixtures from it; bench.py times ref_chain as the
 // "reference" CPU baseline.  Nothing here is reference source: it only
 // converts between raw buffers and the reference's Tensor / block types.
+#include "include/kvcache.h"
 #include "include/ops.h"
 #include "include/quant.h"
 #include "include/quantized_tensor.h"
 #include "include/tensor.h"
 #include "thread_pool/thread_pool.h"
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -186,6 +188,41 @@ int ref_linear_f32(const float* x, const float* w, float* y, int rows, int in, i
 // Matmul(a, b) (src/ops.cc:76-80).
 int ref_matmul_f32(const float* a, const float* b, float* c, int m, int k, int n) {
     return Guard([&] { Unwrap(yan_lamma::Matmul(Wrap(a, {m, k}), Wrap(b, {k, n})), c); });
+}
+
+// Decode attention for one query token: the K/V rows 0..pos go through the
+// reference's own KvCache::Write (src/kvcache.cc), then the score / SoftMax /
+// value loops of ForwardAttention (src/forward.cc:265-298, which does not
+// build from a few files) run over KeyPtr / ValPtr with the reference's own
+// SoftMax (src/ops.cc:113-134).
+int ref_attention(const float* q, const float* k_rows, const float* v_rows, int n_layers,
+                  int max_seq, int n_heads, int n_kv_heads, int head_dim, int layer, int pos,
+                  float* out) {
+    return Guard([&] {
+        yan_lamma::KvCache cache(n_layers, max_seq, n_kv_heads, head_dim);
+        const int row = n_kv_heads * head_dim;
+        for (int j = 0; j <= pos; ++j) {
+            cache.Write(layer, j, Wrap(k_rows + j * row, {n_kv_heads, head_dim}),
+                        Wrap(v_rows + j * row, {n_kv_heads, head_dim}));
+        }
+        const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
+        for (int i = 0; i < n_heads; ++i) {
+            const int kv_head = i / (n_heads / n_kv_heads);
+            Tensor scores({pos + 1}, 0.0f);
+            for (int j = 0; j <= pos; ++j) {
+                const float* kp = cache.KeyPtr(layer, j, kv_head);
+                float dot = 0.0f;
+                for (int d = 0; d < head_dim; ++d) dot += q[i * head_dim + d] * kp[d];
+                scores.data[j] = dot * scale;
+            }
+            const Tensor p = yan_lamma::SoftMax(scores);
+            for (int d = 0; d < head_dim; ++d) {
+                float val = 0.0f;
+                for (int j = 0; j <= pos; ++j) val += p.data[j] * cache.ValPtr(layer, j, kv_head)[d];
+                out[i * head_dim + d] = val;
+            }
+        }
+    });
 }
 
 // The per-token op chain as the reference's CPU forward runs it: each op

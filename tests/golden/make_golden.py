@@ -26,6 +26,11 @@ Fixture contents (numpy .npz, no pickles):
                    [7, 32] and [7, 86]) and on N(0, 0.02) Llama-3-8B-width
                    rows; F32 Linear and Matmul on the shapes of
                    tests/test_cuda_linear.cc and tests/test_cuda_matmul.cc.
+  attention.npz    decode attention for one query token (the reference's
+                   KvCache + the ForwardAttention loops over its SoftMax) on
+                   the cases of test/cuda_attention_test.cc:86-88 (their
+                   sin / cos inputs) and on an N(0, 1) GQA case with
+                   head_dim 128 (8 query heads over 2 KV heads, pos 63).
 
 Usage: make_golden.py [name ...] writes only the named fixtures.
 """
@@ -235,8 +240,33 @@ def linear(ref):
     return out
 
 
+def attention(ref):
+    out = {}
+    cases = (("c0", 2, 2, 7, 0, 0), ("c1", 4, 2, 9, 5, 1), ("c2", 4, 1, 133, 130, 1))
+    for name, H, KV, hd, pos, layer in cases:
+        # test/cuda_attention_test.cc:90-103: cache of 2 layers, pos + 2 slots
+        S = pos + 2
+        q = np.sin(np.arange(H * hd, dtype=np.float32) * np.float32(0.17)).reshape(H, hd)
+        i = np.arange(KV * hd, dtype=np.float32)
+        k = np.stack([np.cos(i * np.float32(0.13) + np.float32(t * 0.1)) for t in range(S)])
+        v = np.stack([np.sin(i * np.float32(0.11) - np.float32(t * 0.2)) for t in range(S)])
+        k = k.astype(np.float32).reshape(S, KV, hd)
+        v = v.astype(np.float32).reshape(S, KV, hd)
+        out[f"{name}_q"], out[f"{name}_k"], out[f"{name}_v"] = q.astype(np.float32), k, v
+        out[f"{name}_shape"] = np.array([H, KV, hd, pos, layer, 2, S], np.int32)
+        out[f"{name}_out"] = ref.attention(q, k[:pos + 1], v[:pos + 1], 2, S, layer, pos)
+    rng = np.random.default_rng(21)
+    H, KV, hd, pos = 8, 2, 128, 63
+    q = normal(rng, (H, hd))
+    k, v = normal(rng, (pos + 1, KV, hd)), normal(rng, (pos + 1, KV, hd))
+    out["g_q"], out["g_k"], out["g_v"] = q, k, v
+    out["g_shape"] = np.array([H, KV, hd, pos, 0, 1, pos + 1], np.int32)
+    out["g_out"] = ref.attention(q, k, v, 1, pos + 1, 0, pos)
+    return out
+
+
 FIXTURES = (("tiny_chain", tiny_chain), ("quant", quant), ("dequant_kat", dequant_kat),
-            ("rows_8b_70b", rows_8b_70b), ("linear", linear))
+            ("rows_8b_70b", rows_8b_70b), ("linear", linear), ("attention", attention))
 
 
 def main():

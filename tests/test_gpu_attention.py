@@ -1,0 +1,325 @@
+"""GPU parity of decode attention and the KV cache write, through the C ABI.
+
+The bar (attention_bound): for output element (h, d),
+    |got - exact| <= (2 * D + (n + 6) * u) * sum_j p_j |v_jd|,
+with exact the float64 value, n = pos + 1 attended positions, u = 2^-24,
+and D = gamma_{hd+1} * scale * max_j sum_d |q_d k_jd| the rounding bound of
+one fp32 score: a score error moves p_j by at most 2D relatively, the exp,
+the sum of n terms and the final division add (n + 6) u.  Any fp32
+evaluation order meets it, the reference's serial loops included (the
+oracle is held to the same bound).  On the reference's own test inputs its
+tolerance, 2e-5 against float64 (test/cuda_attention_test.cc:108-109), is
+checked too.  At long contexts the n u term is loose, so structured inputs
+(equal keys with position-coded values; one dominant key in a chosen chunk)
+check that every position and every chunk is counted exactly once.
+The cache write is bit-exact.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from conftest import assert_bits_equal, golden
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+
+
+def attention_exact(q, kc, vc, layer, pos):
+    """float64 out [H, hd], and sum_j p_j |v_jd| and the score bound D, for one
+    query q [H, hd] over cache positions 0..pos of `layer`."""
+    H, hd = q.shape
+    KV = kc.shape[2]
+    g = H // KV
+    n = pos + 1
+    q64 = q.astype(np.float64)
+    out = np.empty((H, hd))
+    pav = np.empty((H, hd))
+    dmax = 0.0
+    gamma = (hd + 1) * U / (1 - (hd + 1) * U)
+    scale = 1.0 / math.sqrt(hd)
+    for kvh in range(KV):
+        k = kc[layer, :n, kvh].astype(np.float64)
+        v = vc[layer, :n, kvh].astype(np.float64)
+        qs = q64[kvh * g:(kvh + 1) * g]
+        s = qs @ k.T * scale
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        out[kvh * g:(kvh + 1) * g] = p @ v
+        pav[kvh * g:(kvh + 1) * g] = p @ np.abs(v)
+        dmax = max(dmax, gamma * scale * float((np.abs(qs) @ np.abs(k).T).max()))
+    return out, pav, dmax, n
+
+
+def assert_attention_close(got, exact, pav, dmax, n, what):
+    bound = (2 * dmax + (n + 6) * U) * pav + 1e-30
+    err = np.abs(np.asarray(got, np.float64) - exact)
+    bad = err > bound
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {err.size} beyond the bound; worst "
+                           f"err {float(err.max()):.3e}, bound there {float(bound.flat[err.argmax()]):.3e}")
+
+
+class Cache:
+    """Device K/V caches [L, S, KV, hd] filled from host arrays."""
+
+    def __init__(self, mlk, kc, vc):
+        self.mlk = mlk
+        self.L, self.S, self.KV, self.hd = kc.shape
+        self.k = mlk.DeviceBuffer.from_array(np.ascontiguousarray(kc))
+        self.v = mlk.DeviceBuffer.from_array(np.ascontiguousarray(vc))
+
+    def attend(self, q, layer, positions, max_ctx=None, pos0=None, err=None):
+        q = np.ascontiguousarray(q, np.float32)
+        T, H, hd = q.shape
+        max_ctx = max_ctx or self.S
+        ws_bytes = self.mlk.attention_workspace_bytes(T, H, self.KV, hd, max_ctx)
+        ws = self.mlk.DeviceBuffer(max(ws_bytes, 4), np.uint8)
+        d_q = self.mlk.DeviceBuffer.from_array(q)
+        out = self.mlk.DeviceBuffer.empty((T, H, hd))
+        d_pos = None if positions is None else self.mlk.DeviceBuffer.from_array(
+            np.asarray(positions, np.int32))
+        self.mlk.attention_decode(d_q, self.k, self.v, self.L, self.S, H, self.KV, hd, layer, T,
+                                  out, max_ctx, positions=d_pos, pos0=pos0 or 0, workspace=ws,
+                                  workspace_bytes=ws_bytes, err=err)
+        return out.download()
+
+
+def random_cache(rng, L, S, KV, hd, std=1.0):
+    kc = (rng.standard_normal((L, S, KV, hd)) * std).astype(np.float32)
+    vc = (rng.standard_normal((L, S, KV, hd)) * std).astype(np.float32)
+    return kc, vc
+
+
+@pytest.mark.parametrize("case", ["c0", "c1", "c2", "g"])
+def test_attention_reference_cases(mlk, orc, case):
+    """test/cuda_attention_test.cc:86-125 (and a head_dim 128 GQA case): the
+    reference's inputs, a future slot populated that must not count."""
+    gd = golden("attention")
+    H, KV, hd, pos, layer, L, S = (int(v) for v in gd[f"{case}_shape"])
+    q, k, v = gd[f"{case}_q"], gd[f"{case}_k"], gd[f"{case}_v"]
+    kc = np.zeros((L, S, KV, hd), np.float32)
+    vc = np.zeros_like(kc)
+    kc[layer, :k.shape[0]], vc[layer, :v.shape[0]] = k, v
+    cache = Cache(mlk, kc, vc)
+    got = cache.attend(q[None], layer, [pos])[0]
+    ex, pav, dmax, n = attention_exact(q, kc, vc, layer, pos)
+    assert_attention_close(got, ex, pav, dmax, n, case)
+    assert np.abs(got - ex).max() <= 2e-5
+    assert_attention_close(gd[f"{case}_out"], ex, pav, dmax, n, "compiled reference")
+
+
+SHAPES = [  # H, KV, hd, positions
+    (32, 8, 128, [0, 1, 63, 64, 65, 511, 4095, 8191]),  # Llama-3-8B
+    (64, 8, 128, [100, 2047]),                           # Llama-3-70B (8 heads per KV head)
+    (8, 8, 64, [0, 300]),                                # MHA
+    (32, 1, 128, [700]),                                 # MQA: 4 head blocks of 8
+    (12, 2, 96, [129]),                                  # 6 heads per KV head
+    (4, 2, 9, [5]), (4, 1, 133, [130]), (2, 2, 7, [0]),  # the reference's head dims
+    (8, 4, 256, [333]), (4, 4, 32, [1000]), (6, 3, 17, [64]),
+]
+
+
+@pytest.mark.parametrize("H,KV,hd,positions", SHAPES)
+def test_attention_shapes_one_token(mlk, orc, H, KV, hd, positions):
+    rng = np.random.default_rng(H * 1000 + hd)
+    S = max(positions) + 1
+    kc, vc = random_cache(rng, 2, S, KV, hd)
+    cache = Cache(mlk, kc, vc)
+    for pos in positions:
+        q = rng.standard_normal((1, H, hd)).astype(np.float32)
+        got = cache.attend(q, 1, [pos])[0]
+        ex, pav, dmax, n = attention_exact(q[0], kc, vc, 1, pos)
+        assert_attention_close(got, ex, pav, dmax, n, f"H{H} KV{KV} hd{hd} pos{pos}")
+        if pos <= 300:
+            ora = orc.attention(q, kc, vc, 1, [pos])[0]
+            assert_attention_close(ora, ex, pav, dmax, n, "oracle")
+
+
+def test_attention_many_tokens_8b_decode(mlk):
+    """64 tokens of an 8B decode step at positions uniform in
+    [0, 8191], activations N(0, 1) * 0.02, positions as a device array."""
+    rng = np.random.default_rng(7)
+    H, KV, hd, S = 32, 8, 128, 8192
+    kc, vc = random_cache(rng, 1, S, KV, hd, std=0.02)
+    cache = Cache(mlk, kc, vc)
+    pos = rng.integers(0, S, size=64).astype(np.int32)
+    pos[:3] = [0, S - 1, 4096]
+    q = (rng.standard_normal((64, H, hd)) * 0.02).astype(np.float32)
+    got = cache.attend(q, 0, pos)
+    for t in range(64):
+        ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, int(pos[t]))
+        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t} pos {pos[t]}")
+    # consecutive positions pos0 .. pos0 + T - 1 (no positions array)
+    got2 = cache.attend(q[:5], 0, None, pos0=8000)
+    for t in range(5):
+        ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, 8000 + t)
+        assert_attention_close(got2[t], ex, pav, dmax, n, f"pos0 token {t}")
+
+
+@pytest.mark.parametrize("S", [64, 700, 8192])
+def test_attention_counts_every_position_once(mlk, S):
+    """Equal keys give equal weights 1/n (exactly: every score is the same),
+    so out is the mean of the value rows 0..pos, here random in [1, 2).
+    Dropping or repeating one position or a chunk moves that mean by about
+    0.3 / n relative (4e-5 at n = 8192), far above the fp32 rounding of the
+    sums (~1e-8 relative)."""
+    KV, hd, H = 2, 64, 4
+    rng = np.random.default_rng(S)
+    kc = np.full((1, S, KV, hd), 0.01, np.float32)
+    vc = (1.0 + rng.random((1, S, KV, hd))).astype(np.float32)
+    cache = Cache(mlk, kc, vc)
+    positions = sorted({0, S - 1, S // 2, *rng.integers(0, S, 5).tolist()})
+    q = rng.standard_normal((len(positions), H, hd)).astype(np.float32)
+    got = cache.attend(q, 0, positions)
+    for t, pos in enumerate(positions):
+        want = vc[0, :pos + 1].astype(np.float64).mean(axis=0)  # [KV, hd]
+        want = np.repeat(want, H // KV, axis=0)
+        rel = np.abs(got[t] - want) / want
+        assert rel.max() <= 2e-6, (pos, float(rel.max()))
+
+
+def test_attention_dominant_key_in_each_chunk(mlk):
+    """One key aligned with q (score 40) at position j*, the rest random and
+    small: out ~ v_j*.  j* is placed in the first, a middle and the last
+    chunk of a long context, so every chunk's partial is rescaled right."""
+    rng = np.random.default_rng(3)
+    H, KV, hd, S = 8, 2, 128, 5000
+    kc = (rng.standard_normal((1, S, KV, hd)) * 0.01).astype(np.float32)
+    vc = rng.standard_normal((1, S, KV, hd)).astype(np.float32)
+    q = rng.standard_normal((1, H, hd)).astype(np.float32)
+    pos = S - 1
+    for jstar in (0, 2500, 4999, 1023, 1024):
+        kc2 = kc.copy()
+        for kvh in range(KV):
+            qs = q[0, kvh * 4]
+            kc2[0, jstar, kvh] = qs / np.dot(qs, qs) * 40 * math.sqrt(hd)
+        cache = Cache(mlk, kc2, vc)
+        got = cache.attend(q, 0, [pos])[0]
+        ex, pav, dmax, n = attention_exact(q[0], kc2, vc, 0, pos)
+        assert_attention_close(got, ex, pav, dmax, n, f"j* {jstar}")
+        # query head 4 * kvh is the aligned one: its output is v_j*
+        for kvh in range(KV):
+            assert np.abs(got[kvh * 4] - vc[0, jstar, kvh]).max() < 1e-3
+
+
+def test_attention_bad_positions_give_zero_rows_and_flag(mlk):
+    rng = np.random.default_rng(5)
+    H, KV, hd, S = 8, 2, 64, 600
+    kc, vc = random_cache(rng, 1, S, KV, hd)
+    cache = Cache(mlk, kc, vc)
+    q = rng.standard_normal((4, H, hd)).astype(np.float32)
+    for max_ctx in (600, 40):  # several chunks, and one chunk
+        err = mlk.DeviceBuffer.from_array(np.zeros(1, np.int32))
+        positions = [3, -1, max_ctx, min(17, max_ctx - 1)]
+        got = cache.attend(q, 0, positions, max_ctx=max_ctx, err=err)
+        assert err.download()[0] != 0
+        assert not got[1].any() and not got[2].any()
+        for t in (0, 3):
+            ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, positions[t])
+            assert_attention_close(got[t], ex, pav, dmax, n, f"valid token {t}")
+        ok = mlk.DeviceBuffer.from_array(np.zeros(1, np.int32))
+        cache.attend(q[:1], 0, [5], max_ctx=max_ctx, err=ok)
+        assert ok.download()[0] == 0
+
+
+def test_attention_rejects_bad_arguments(mlk):
+    kc = mlk.DeviceBuffer.empty((2, 16, 2, 8))
+    vc = mlk.DeviceBuffer.empty((2, 16, 2, 8))
+    q = mlk.DeviceBuffer.empty((1, 4, 8))
+    out = mlk.DeviceBuffer.empty((1, 4, 8))
+
+    def call(**kw):
+        a = dict(n_layers=2, max_seq=16, n_heads=4, n_kv_heads=2, head_dim=8, layer=0,
+                 n_tokens=1, max_ctx=16, pos0=0)
+        a.update(kw)
+        mlk.attention_decode(q, kc, vc, a["n_layers"], a["max_seq"], a["n_heads"],
+                             a["n_kv_heads"], a["head_dim"], a["layer"], a["n_tokens"], out,
+                             a["max_ctx"], pos0=a["pos0"])
+
+    call()
+    for bad in (dict(layer=2), dict(layer=-1), dict(n_heads=3), dict(n_kv_heads=0),
+                dict(head_dim=300), dict(max_ctx=17), dict(max_ctx=0), dict(pos0=16),
+                dict(pos0=-1), dict(n_tokens=0)):
+        with pytest.raises(mlk.MlkError):
+            call(**bad)
+    with pytest.raises(mlk.MlkError):  # several chunks and no workspace
+        mlk.attention_decode(q, kc, vc, 1, 100000, 4, 2, 8, 0, 1, out, 100000, pos0=0)
+
+
+def test_kv_write_slots(mlk):
+    rng = np.random.default_rng(9)
+    L, S, KV, hd = 3, 50, 4, 32
+    kc0, vc0 = random_cache(rng, L, S, KV, hd)
+    d_k, d_v = mlk.DeviceBuffer.from_array(kc0), mlk.DeviceBuffer.from_array(vc0)
+    T = 6
+    # k and v as column slices of a fused [T, (H + 2 KV) hd] QKV activation
+    H = 8
+    qkv = rng.standard_normal((T, (H + 2 * KV) * hd)).astype(np.float32)
+    d_qkv = mlk.DeviceBuffer.from_array(qkv)
+    pos = np.array([49, 0, 7, 8, 30, 12], np.int32)
+    err = mlk.DeviceBuffer.from_array(np.zeros(1, np.int32))
+    stride = (H + 2 * KV) * hd
+    mlk.kv_write(d_k, d_v, L, S, KV, hd, 1, d_qkv.ptr + H * hd * 4,
+                 d_qkv.ptr + (H + KV) * hd * 4, T, positions=mlk.DeviceBuffer.from_array(pos),
+                 k_row_stride=stride, v_row_stride=stride, err=err)
+    want_k, want_v = kc0.copy(), vc0.copy()
+    want_k[1, pos] = qkv[:, H * hd:(H + KV) * hd].reshape(T, KV, hd)
+    want_v[1, pos] = qkv[:, (H + KV) * hd:].reshape(T, KV, hd)
+    assert_bits_equal(d_k.download(), want_k, "k")
+    assert_bits_equal(d_v.download(), want_v, "v")
+    assert err.download()[0] == 0
+    # consecutive positions, contiguous rows, odd row width (scalar path)
+    KV2, hd2 = 3, 5
+    kc2, vc2 = random_cache(rng, 1, 10, KV2, hd2)
+    d_k2, d_v2 = mlk.DeviceBuffer.from_array(kc2), mlk.DeviceBuffer.from_array(vc2)
+    k = rng.standard_normal((4, KV2 * hd2)).astype(np.float32)
+    v = rng.standard_normal((4, KV2 * hd2)).astype(np.float32)
+    mlk.kv_write(d_k2, d_v2, 1, 10, KV2, hd2, 0, mlk.DeviceBuffer.from_array(k),
+                 mlk.DeviceBuffer.from_array(v), 4, pos0=6)
+    kc2[0, 6:10], vc2[0, 6:10] = k.reshape(4, KV2, hd2), v.reshape(4, KV2, hd2)
+    assert_bits_equal(d_k2.download(), kc2, "k2")
+    assert_bits_equal(d_v2.download(), vc2, "v2")
+    # a bad device position writes nothing for that row and raises the flag
+    err = mlk.DeviceBuffer.from_array(np.zeros(1, np.int32))
+    mlk.kv_write(d_k2, d_v2, 1, 10, KV2, hd2, 0, mlk.DeviceBuffer.from_array(k),
+                 mlk.DeviceBuffer.from_array(v), 2,
+                 positions=mlk.DeviceBuffer.from_array(np.array([10, 1], np.int32)), err=err)
+    assert err.download()[0] != 0
+    kc2[0, 1] = k[1].reshape(KV2, hd2)
+    assert_bits_equal(d_k2.download(), kc2, "bad position")
+    with pytest.raises(mlk.MlkError):
+        mlk.kv_write(d_k2, d_v2, 1, 10, KV2, hd2, 1, mlk.DeviceBuffer.from_array(k),
+                     mlk.DeviceBuffer.from_array(v), 1, pos0=0)
+    with pytest.raises(mlk.MlkError):
+        mlk.kv_write(d_k2, d_v2, 1, 10, KV2, hd2, 0, mlk.DeviceBuffer.from_array(k),
+                     mlk.DeviceBuffer.from_array(v), 2, pos0=9)
+
+
+def test_write_then_attend_matches_oracle_decode_loop(mlk, orc):
+    """The forward pass's order (src/forward.cc:237-251): each step writes its
+    k, v at pos and attends over 0..pos; 40 steps through the device and the
+    oracle agree within the bound."""
+    rng = np.random.default_rng(11)
+    H, KV, hd, S, L = 8, 2, 64, 40, 2
+    kc = np.zeros((L, S, KV, hd), np.float32)
+    vc = np.zeros_like(kc)
+    d_k, d_v = mlk.DeviceBuffer.from_array(kc), mlk.DeviceBuffer.from_array(vc)
+    out = mlk.DeviceBuffer.empty((1, H, hd))
+    for pos in range(S):
+        k = rng.standard_normal((1, KV * hd)).astype(np.float32)
+        v = rng.standard_normal((1, KV * hd)).astype(np.float32)
+        q = rng.standard_normal((1, H, hd)).astype(np.float32)
+        mlk.kv_write(d_k, d_v, L, S, KV, hd, 1, mlk.DeviceBuffer.from_array(k),
+                     mlk.DeviceBuffer.from_array(v), 1, pos0=pos)
+        orc.kv_write(kc, vc, 1, [pos], k.reshape(1, KV, hd), v.reshape(1, KV, hd))
+        mlk.attention_decode(mlk.DeviceBuffer.from_array(q), d_k, d_v, L, S, H, KV, hd, 1, 1, out,
+                             pos + 1, pos0=pos)
+        got = out.download()[0]
+        ex, pav, dmax, n = attention_exact(q[0], kc, vc, 1, pos)
+        assert_attention_close(got, ex, pav, dmax, n, f"step {pos}")
+        assert_attention_close(orc.attention(q, kc, vc, 1, [pos])[0], ex, pav, dmax, n, "oracle")
+    assert_bits_equal(d_k.download(), kc, "cache k")

@@ -608,3 +608,133 @@ def test_linear_oracle_equals_compiled_reference_on_random_inputs(orc):
     a = rng.standard_normal((6, 40)).astype(np.float32)
     assert_bits_equal(orc.matmul_f32(a, w[:40, :9].copy()), ref.matmul_f32(a, w[:40, :9].copy()),
                       "mm")
+
+
+# ------------------------------------------------- attention, KV cache
+
+def attention_f64(q, k, v, pos, kv_of=None, scale=None, last=None, values=None):
+    """test/cuda_attention_test.cc:50-80: float64 scores q.k / sqrt(hd),
+    softmax and value sums over positions 0..pos.  q [H, hd], k / v
+    [>= pos + 1, KV, hd].  The keyword arguments plant mistakes (for the
+    planted-mistake test): another query-to-KV-head map, scale, last
+    attended position, or the rows the values come from."""
+    H, hd = q.shape
+    KV = k.shape[1]
+    group = H // KV
+    kv_of = kv_of or (lambda h: h // group)
+    scale = 1.0 / math.sqrt(hd) if scale is None else scale
+    last = pos if last is None else last
+    values = v if values is None else values
+    out = np.empty((H, hd))
+    for h in range(H):
+        kk = k[:last + 1, kv_of(h)].astype(np.float64)
+        s = kk @ q[h].astype(np.float64) * scale
+        p = np.exp(s - s.max())
+        p /= p.sum()
+        out[h] = p @ values[:last + 1, kv_of(h)].astype(np.float64)
+    return out
+
+
+def cache_from_rows(orc, k_rows, v_rows, n_layers, max_seq, layer):
+    L, S = int(n_layers), int(max_seq)
+    KV, hd = k_rows.shape[1], k_rows.shape[2]
+    kc = np.zeros((L, S, KV, hd), np.float32)
+    vc = np.zeros_like(kc)
+    n = k_rows.shape[0]
+    orc.kv_write(kc, vc, layer, np.arange(n), k_rows, v_rows)
+    return kc, vc
+
+
+ATT_CASES = ("c0", "c1", "c2", "g")
+
+
+@pytest.mark.parametrize("case", ATT_CASES)
+def test_attention_golden_and_closed_form(orc, case):
+    """Golden outputs of the compiled reference (bit for bit) and the
+    float64 closed form of the reference's own GPU test within its 2e-5."""
+    g = golden("attention")
+    H, KV, hd, pos, layer, L, S = (int(v) for v in g[f"{case}_shape"])
+    q, k, v = g[f"{case}_q"], g[f"{case}_k"], g[f"{case}_v"]
+    kc, vc = cache_from_rows(orc, k, v, L, S, layer)
+    got = orc.attention(q[None], kc, vc, layer, [pos])[0]
+    assert_bits_equal(got, g[f"{case}_out"], case)
+    near(got, attention_f64(q, k, v, pos))
+
+
+def test_attention_invariants(orc):
+    rng = np.random.default_rng(31)
+    H, KV, hd, S = 8, 2, 32, 40
+    q = rng.standard_normal((H, hd)).astype(np.float32)
+    k = rng.standard_normal((S, KV, hd)).astype(np.float32)
+    v = rng.standard_normal((S, KV, hd)).astype(np.float32)
+    kc, vc = cache_from_rows(orc, k, v, 1, S, 0)
+    # pos 0: one score, softmax 1, the output is the value row itself
+    out0 = orc.attention(q[None], kc, vc, 0, [0])[0]
+    assert_bits_equal(out0, np.repeat(v[0], H // KV, axis=0), "pos 0")
+    # slots after pos take no part
+    kc2, vc2 = kc.copy(), vc.copy()
+    kc2[0, 21:] = 1e30
+    vc2[0, 21:] = np.nan
+    assert_bits_equal(orc.attention(q[None], kc2, vc2, 0, [20]),
+                      orc.attention(q[None], kc, vc, 0, [20]), "future slots")
+    # equal keys: uniform weights, the output is the mean value row
+    kc3 = np.broadcast_to(kc[:, :1], kc.shape).copy()
+    out = orc.attention(q[None], kc3, vc, 0, [S - 1])[0]
+    near(out, np.repeat(v.astype(np.float64).mean(axis=0), H // KV, axis=0), tol=1e-6)
+    # GQA: query head h reads KV head h // (H / KV)
+    vc4 = np.zeros_like(vc)
+    vc4[0, :, 1] = 1.0
+    out = orc.attention(q[None], kc, vc4, 0, [S - 1])[0]
+    near(out[:, 0], (np.arange(H) // (H // KV)).astype(np.float64), tol=1e-6)
+    # several tokens at once equal one call per token
+    pos = np.array([3, 39, 0, 17], np.int32)
+    qs = rng.standard_normal((4, H, hd)).astype(np.float32)
+    batch = orc.attention(qs, kc, vc, 0, pos)
+    for t in range(4):
+        assert_bits_equal(batch[t], orc.attention(qs[t:t + 1], kc, vc, 0, pos[t:t + 1])[0], "t")
+
+
+def test_kv_write_slots_and_rejections(orc):
+    rng = np.random.default_rng(32)
+    L, S, KV, hd = 3, 9, 2, 5
+    kc = rng.standard_normal((L, S, KV, hd)).astype(np.float32)
+    vc = rng.standard_normal((L, S, KV, hd)).astype(np.float32)
+    before_k, before_v = kc.copy(), vc.copy()
+    pos = np.array([4, 0, 8], np.int32)
+    k = rng.standard_normal((3, KV, hd)).astype(np.float32)
+    v = rng.standard_normal((3, KV, hd)).astype(np.float32)
+    orc.kv_write(kc, vc, 2, pos, k, v)
+    want_k, want_v = before_k.copy(), before_v.copy()
+    want_k[2, pos], want_v[2, pos] = k, v
+    assert_bits_equal(kc, want_k, "k slots")
+    assert_bits_equal(vc, want_v, "v slots")
+    for layer, p in ((3, [0]), (-1, [0]), (0, [9]), (0, [-1])):
+        with pytest.raises(ValueError):
+            orc.kv_write(kc, vc, layer, np.array(p, np.int32), k[:1], v[:1])
+    with pytest.raises(ValueError):
+        orc.attention(np.zeros((1, 3, hd), np.float32), kc, vc, 0, [0])  # 3 % 2 != 0
+
+
+@pytest.mark.parametrize("mutation", ["kv_head_mod", "no_scale", "drop_last", "values_from_k"])
+def test_planted_attention_mistakes_fail_the_golden(mutation):
+    g = golden("attention")
+    q, k, v = g["g_q"], g["g_k"], g["g_v"]
+    H, KV, hd, pos = (int(x) for x in g["g_shape"][:4])
+    kw = {"kv_head_mod": dict(kv_of=lambda h: h % KV), "no_scale": dict(scale=1.0),
+          "drop_last": dict(last=pos - 1), "values_from_k": dict(values=k)}[mutation]
+    ref_out = g["g_out"].astype(np.float64)
+    assert np.abs(attention_f64(q, k, v, pos) - ref_out).max() <= 2e-5
+    assert np.abs(attention_f64(q, k, v, pos, **kw) - ref_out).max() > 2e-5
+
+
+@needs_ref
+def test_attention_oracle_equals_compiled_reference_on_random_inputs(orc):
+    ref = O.reference()
+    rng = np.random.default_rng(33)
+    for H, KV, hd, pos in ((32, 8, 128, 200), (6, 3, 17, 9), (4, 4, 64, 0), (8, 1, 96, 77)):
+        q = rng.standard_normal((H, hd)).astype(np.float32)
+        k = rng.standard_normal((pos + 1, KV, hd)).astype(np.float32)
+        v = rng.standard_normal((pos + 1, KV, hd)).astype(np.float32)
+        kc, vc = cache_from_rows(orc, k, v, 2, pos + 3, 1)
+        assert_bits_equal(orc.attention(q[None], kc, vc, 1, [pos])[0],
+                          ref.attention(q, k, v, 2, pos + 3, 1, pos), f"{H}/{KV}/{hd}/{pos}")
