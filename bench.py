@@ -54,6 +54,10 @@ def parse_args():
                    help="only measure the seven linear projections of one Llama-3-8B layer "
                         "(F32, Q8_0, Q4_0, Q4_1 weights; T = 1, 4, 16 token rows) into this "
                         "JSON file")
+    p.add_argument("--attention", default=None,
+                   help="only measure decode attention (Llama-3-8B and 70B head shapes, one "
+                        "token at several context lengths and configs[1]'s 64 tokens) into "
+                        "this JSON file")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--rocprof-report", nargs=5, default=None,
                    metavar=("KERNEL_TRACE_DIR", "FETCH_DIR", "WRITE_DIR", "CALIB_FETCH_DIR",
@@ -432,6 +436,63 @@ def linear_bench(mlk, steps, peak, path):
         json.dump(out, f, indent=1)
 
 
+# ------------------------------------------------------------ attention
+
+ATT_LAYERS = 16  # cache layers rotated per launch: 16 x 64 MB K+V at 8B, S = 8192
+
+
+def attention_bench(mlk, steps, peak, path):
+    """Decode attention launches over a cache of ATT_LAYERS layers (each
+    launch reads another layer, so a pass over the rotation exceeds the
+    MALL), timed between two events on the stream they run on."""
+    out = {"workload": "decode attention over a device KV cache, N(0, 0.02) cache and queries",
+           "peak_GBps": peak}
+    st = mlk.Stream()
+    S = 8192
+    for name, H, KV, hd in (("llama3_8b", 32, 8, 128), ("llama3_70b", 64, 8, 128)):
+        n = ATT_LAYERS * S * KV * hd
+        kc, vc = mlk.DeviceBuffer.empty((n,)), mlk.DeviceBuffer.empty((n,))
+        mlk.fill_normal(kc, n, 0.0, 0.02, 11)
+        mlk.fill_normal(vc, n, 0.0, 0.02, 12)
+        rows = {}
+        cases = [("T1_pos%d" % p, np.array([p], np.int32)) for p in (511, 2047, 4095, 8191)]
+        if name == "llama3_8b":
+            cases.append(("T64_uniform0_8191", workloads.decode_positions(64, S - 1, 42)))
+        for case, pos in cases:
+            T = pos.size
+            q = mlk.DeviceBuffer.empty((T, H * hd))
+            mlk.fill_normal(q, T * H * hd, 0.0, 0.02, 13)
+            o = mlk.DeviceBuffer.empty((T, H * hd))
+            d_pos = mlk.DeviceBuffer.from_array(pos)
+            max_ctx = int(pos.max()) + 1
+            wsb = mlk.attention_workspace_bytes(T, H, KV, hd, max_ctx)
+            ws = mlk.DeviceBuffer(max(wsb, 4), np.uint8)
+
+            def launch(i):
+                mlk.attention_decode(q, kc, vc, ATT_LAYERS, S, H, KV, hd, i % ATT_LAYERS, T, o,
+                                     max_ctx, positions=d_pos, workspace=ws, workspace_bytes=wsb,
+                                     stream=st)
+            for i in range(3):
+                launch(i)
+            st.synchronize()
+            e0, e1 = mlk.Event(), mlk.Event()
+            e0.record(st)
+            for i in range(3, 3 + steps):
+                launch(i)
+            e1.record(st)
+            e1.synchronize()
+            ms = e0.elapsed_ms(e1) / steps
+            nb = workloads.bytes_attention(pos, H, KV, hd)
+            gbs = nb / (ms * 1e-3) / 1e9
+            rows[case] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(gbs, 1),
+                          "frac_of_peak": round(gbs / peak, 4), "workspace_bytes": wsb}
+            print(f"attention {name} {case}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s", flush=True)
+        out[name] = {"n_heads": H, "n_kv_heads": KV, "head_dim": hd, "cases": rows}
+        del kc, vc
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+
+
 CALIB_FLOATS = 64 << 20  # 256 MiB per buffer
 
 
@@ -597,6 +658,9 @@ def main():
         return
     if args.linear:
         linear_bench(mlk, args.steps, workloads.HBM_PEAK_GBS, args.linear)
+        return
+    if args.attention:
+        attention_bench(mlk, args.steps, workloads.HBM_PEAK_GBS, args.attention)
         return
     peak = workloads.HBM_PEAK_GBS
     cfg = workloads.CONFIGS["c3_prefill_8b"]

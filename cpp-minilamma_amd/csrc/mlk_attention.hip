@@ -23,12 +23,15 @@
 //     GB query heads of that KV head's group, and a chunk of positions; it
 //     reads each K and V row of the chunk once for all GB heads (the
 //     reference re-reads them for every query head);
-//   - scores: a half-wave per position, lane l holding head dims
-//     l, l + 32, ... (coalesced 128-byte row segments); the 32 lanes' partial
-//     dot products of P positions x GB heads are summed with one
-//     transpose-reduce (P * GB = 32 values, one result per lane);
-//   - the chunk's softmax (max, exp, sum) in LDS, then the value rows, again a
-//     half-wave per position, with the probabilities broadcast from LDS;
+//   - each wave owns two positions per step (one per half-wave), lane l
+//     holding head dims l, l + 32, ... of K and V (coalesced 128-byte row
+//     segments); it keeps the rows of its next positions loading while it
+//     computes the current ones;
+//   - scores: the 32 lanes' partial dot products of all its positions and
+//     heads are summed with one transpose-reduce;
+//   - a running softmax per head (max, sum, weighted value sum) is updated
+//     with lane shuffles, no LDS round trip or barrier inside the loop;
+//   - the four waves merge their (max, sum, acc) through LDS at the end;
 //   - one chunk covers all positions: the workgroup divides by the sum and
 //     writes out; otherwise it writes (acc, max, sum) to the workspace and
 //     AttnCombine rescales and adds the chunks (max-shifted, like the
@@ -71,48 +74,65 @@ __device__ inline float MaskF(float v, bool keep) {
     return __uint_as_float(__float_as_uint(v) & (keep ? ~0u : 0u));
 }
 
-__device__ inline float WaveSumF(float v) {
+// Sums N (a power of two <= 32) values per lane over the 32 lanes of each
+// half-wave.  Each of the log2(N) steps halves the values a lane holds
+// (lanes with bit o clear keep the lower half and add the partner's lower
+// half, the others the upper half); a butterfly over the remaining lane
+// bits completes the sums.  Lane l then holds the total of value index
+// l >> (5 - log2 N), and the 32 / N lanes of a group hold the same total.
+template <int N>
+__device__ inline float HalfTransposeReduce(float (&v)[N], int hl) {
+    // all sends of a step first, then all shuffles, then the adds: the
+    // step's shuffles are independent and wait on the LDS pipe once
 #pragma unroll
-    for (int o = kWave / 2; o > 0; o /= 2) v += __shfl_xor(v, o, kWave);
-    return v;
-}
-
-// Sums 32 values per lane over the 32 lanes of each half-wave: every step
-// halves the values a lane holds (lanes with bit o clear keep the lower
-// half and add the partner's lower half); after five steps lane l holds the
-// total of value index HalfIdx(l).
-__device__ inline float HalfTransposeReduce(float (&v)[kHalf], int hl) {
-#pragma unroll
-    for (int h = kHalf / 2, o = kHalf / 2; h >= 1; h /= 2, o /= 2) {
+    for (int h = N / 2, o = kHalf / 2; h >= 1; h /= 2, o /= 2) {
         const bool upper = (hl & o) != 0;
+        float send[N / 2 > 0 ? N / 2 : 1], recv[N / 2 > 0 ? N / 2 : 1];
 #pragma unroll
-        for (int i = 0; i < h; ++i) {
-            const float send = upper ? v[i] : v[i + h];
-            const float keep = upper ? v[i + h] : v[i];
-            v[i] = keep + __shfl_xor(send, o, kWave);
-        }
+        for (int i = 0; i < h; ++i) send[i] = upper ? v[i] : v[i + h];
+#pragma unroll
+        for (int i = 0; i < h; ++i) recv[i] = __shfl_xor(send[i], o, kWave);
+#pragma unroll
+        for (int i = 0; i < h; ++i) v[i] = (upper ? v[i + h] : v[i]) + recv[i];
     }
-    return v[0];
-}
-
-__device__ inline int HalfIdx(int hl) {
-    int idx = 0;
+    float r = v[0];
+    constexpr int rest = kHalf / N;
 #pragma unroll
-    for (int h = kHalf / 2, o = kHalf / 2; h >= 1; h /= 2, o /= 2) idx += (hl & o) ? h : 0;
-    return idx;
+    for (int o = rest / 2; o >= 1; o /= 2) r += __shfl_xor(r, o, kWave);
+    return r;
 }
 
-// NQ: head dims per lane (head_dim <= 32 * NQ); GB: query heads per
-// workgroup.  Dynamic LDS: GB * chunk scores + kAttnWaves * GB * 32 * NQ
-// value partials.
-template <int NQ, int GB>
-__global__ __launch_bounds__(kAttnThreads) void AttnChunk(AttnParams p) {
-    constexpr int P = kHalf / GB;  // position steps per transpose-reduce
-    constexpr int W = kHalf * NQ;  // value partials per head
-    extern __shared__ float smem[];
-    float* sc = smem;
-    float* red = smem + GB * p.chunk;
-    __shared__ float ml[GB][2];
+constexpr int Log2(int n) { return n <= 1 ? 0 : 1 + Log2(n / 2); }
+constexpr int MinI(int a, int b) { return a < b ? a : b; }
+
+// One workgroup: one token, one KV head, a block of GB of its query heads,
+// and the positions [j0, j0 + chunk) (cut at pos).  The positions go in
+// sub-chunks of 8 * NPOS: wave w, half h takes positions
+// w * 2 * NPOS + 2 s + h (s < NPOS) of each sub-chunk.  A lane keeps the K
+// and V values of its NPOS positions and head dims l, l + 32, ... in
+// registers (NPOS * NQ <= 16 and NPOS * GB <= 16, which bounds the
+// registers of the loads in flight and of the score partials), and a
+// running softmax per head:
+//   scores   NPOS * GB partial dot products per lane, one transpose-reduce
+//            (lane l then holds the score of (s, h) with
+//            s * GB + h = l >> (5 - log2(NPOS * GB)));
+//   softmax  per-head max and sum over the wave's 2 * NPOS positions by
+//            butterflies over the lane bits of s and of the half; the
+//            running (m, l, acc) is rescaled by exp(m_old - m_new);
+//   values   acc[h] += p(s, h) * v_s, p(s, h) shuffled from its lane.
+// The four waves' (m, l, acc) are merged through LDS at the end.
+// kFull: head_dim == 32 * NQ, so no lane's head dims need masking.
+template <int NQ, int GB, bool kFull>
+__global__ __launch_bounds__(kAttnThreads) void AttnSplit(AttnParams p) {
+    constexpr int NPOS = MinI(16 / GB > 0 ? 16 / GB : 1, 16 / NQ > 0 ? 16 / NQ : 1);
+    constexpr int N = NPOS * GB;
+    constexpr int SHIFT = 5 - Log2(N);        // lane l holds value l >> SHIFT
+    constexpr int OMIN = kHalf / NPOS;        // lowest lane bit of s
+    constexpr int SUB = 2 * kAttnWaves * NPOS;  // positions per sub-chunk
+    constexpr int W = kHalf * NQ;             // head dims per half-wave
+    __shared__ float wm[kAttnWaves][GB];
+    __shared__ float wl[kAttnWaves][GB];
+    __shared__ float wacc[kAttnWaves][GB][W];
 
     const int c = static_cast<int>(blockIdx.x % p.n_chunks);
     const int64_t t = blockIdx.x / p.n_chunks;
@@ -137,15 +157,15 @@ __global__ __launch_bounds__(kAttnThreads) void AttnChunk(AttnParams p) {
     }
     if (j0 > pos) return;  // chunk past the token's last position
     const int cl = static_cast<int>(min(static_cast<int64_t>(p.chunk), pos + 1 - j0));
+    const int n_it = (cl + SUB - 1) / SUB;
     const int lane = threadIdx.x % kWave;
     const int wave = threadIdx.x / kWave;
     const int half = lane / kHalf;
     const int hl = lane % kHalf;
-    const int per_wave = p.chunk / kAttnWaves;
     const float* kbase = p.kc + j0 * p.slot + static_cast<int64_t>(kvh) * p.hd;
     const float* vbase = p.vc + j0 * p.slot + static_cast<int64_t>(kvh) * p.hd;
+    const int jw = wave * 2 * NPOS + half;  // the lane's first position in a sub-chunk
 
-    // ---- scores
     float qr[GB][NQ];
 #pragma unroll
     for (int h = 0; h < GB; ++h) {
@@ -158,116 +178,170 @@ __global__ __launch_bounds__(kAttnThreads) void AttnChunk(AttnParams p) {
                              ok);
         }
     }
-    for (int b = 0; b < per_wave; b += 2 * P) {
-        float part[kHalf];
+
+    // rows past cl read row 0 of the chunk (in bounds); their scores are
+    // replaced by -inf and their weights are zero.  Offsets are 32-bit (a
+    // chunk spans at most 2048 slots of <= 64 KiB), added to the uniform
+    // chunk base.
+    // unsigned offsets from the uniform bases, so the loads take the
+    // scalar-base + 32-bit vector-offset form (immediate offsets for i)
+    const char* kb8 = reinterpret_cast<const char*>(kbase);
+    const char* vb8 = reinterpret_cast<const char*>(vbase);
+    auto at = [](const char* b, uint32_t byte_off) {
+        return *reinterpret_cast<const float*>(b + byte_off);
+    };
+    auto load = [&](int it, float (&kk)[NPOS][NQ], float (&vv)[NPOS][NQ]) {
 #pragma unroll
-        for (int s = 0; s < P; ++s) {
-            const int jl = wave * per_wave + b + 2 * s + half;
-            // rows past the chunk's end read row 0 of the chunk (in bounds);
-            // their scores are replaced below
-            const bool ok = b + 2 * s + half < per_wave && jl < cl;
-            const float* kr = kbase + static_cast<int64_t>(ok ? jl : 0) * p.slot;
-            float kv[NQ];
+        for (int s = 0; s < NPOS; ++s) {
+            const int jl = it * SUB + jw + 2 * s;
+            const uint32_t off = (static_cast<uint32_t>(jl < cl ? jl : 0) *
+                                  static_cast<uint32_t>(p.slot) + static_cast<uint32_t>(hl)) * 4u;
 #pragma unroll
             for (int i = 0; i < NQ; ++i) {
-                const int d = hl + kHalf * i;
-                kv[i] = MaskF(kr[d < p.hd ? d : 0], d < p.hd);
+                if constexpr (kFull) {
+                    kk[s][i] = at(kb8, off + 4u * kHalf * i);
+                    vv[s][i] = at(vb8, off + 4u * kHalf * i);
+                } else {
+                    const bool dok = hl + kHalf * i < p.hd;
+                    const uint32_t o = dok ? off + 4u * kHalf * i : off - 4u * hl;
+                    kk[s][i] = MaskF(at(kb8, o), dok);
+                    vv[s][i] = MaskF(at(vb8, o), dok);
+                }
             }
+        }
+    };
+
+    float m[GB], l[GB], acc[GB][NQ];
+#pragma unroll
+    for (int h = 0; h < GB; ++h) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) acc[h][i] = 0.0f;
+    }
+    const int my_idx = hl >> SHIFT;
+    const int my_s = my_idx / GB, my_h = my_idx % GB;
+
+    // One sub-chunk: scores, running-softmax update, values.  A sub-chunk
+    // past cl (the odd trip of the unrolled loop) is all -inf and changes
+    // nothing.
+    auto step = [&](int it, const float (&kr)[NPOS][NQ], const float (&vr)[NPOS][NQ]) {
+        float part[N];
+#pragma unroll
+        for (int s = 0; s < NPOS; ++s) {
 #pragma unroll
             for (int h = 0; h < GB; ++h) {
                 float a = 0.0f;
 #pragma unroll
-                for (int i = 0; i < NQ; ++i) a = fmaf(qr[h][i], kv[i], a);
+                for (int i = 0; i < NQ; ++i) a = fmaf(qr[h][i], kr[s][i], a);
                 part[s * GB + h] = a;
             }
         }
-        const float tot = HalfTransposeReduce(part, hl);
-        const int idx = HalfIdx(hl);
-        const int s_ = idx / GB, h_ = idx % GB;
-        if (b + 2 * s_ + half < per_wave) {
-            const int jl = wave * per_wave + b + 2 * s_ + half;
-            sc[h_ * p.chunk + jl] = jl < cl ? tot * p.scale : -INFINITY;
-        }
-    }
-    __syncthreads();
-
-    // ---- softmax of the chunk: e_j = exp(s_j - max), sum
-    for (int h = wave; h < GB; h += kAttnWaves) {
-        if (h >= nh) break;
-        float* sh = sc + h * p.chunk;
-        float m = -INFINITY;
-        for (int i = lane; i < cl; i += kWave) m = fmaxf(m, sh[i]);
-        m = WaveMax(m);
-        float l = 0.0f;
-        for (int i = lane; i < p.chunk; i += kWave) {
-            const float e = i < cl ? expf(sh[i] - m) : 0.0f;
-            sh[i] = e;
-            l += e;
-        }
-        l = WaveSumF(l);
-        if (lane == 0) {
-            ml[h][0] = m;
-            ml[h][1] = l;
-        }
-    }
-    __syncthreads();
-
-    // ---- values
-    float acc[GB][NQ];
+        const float tot = HalfTransposeReduce<N>(part, hl);
+        const bool valid = it * SUB + jw + 2 * my_s < cl;
+        const float score = valid ? tot * p.scale : -INFINITY;
+        // per-head max over the wave's positions of this sub-chunk
+        float mx = score;
 #pragma unroll
-    for (int h = 0; h < GB; ++h)
+        for (int o = OMIN; o <= kHalf; o *= 2) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+        float mh[GB];
 #pragma unroll
-        for (int i = 0; i < NQ; ++i) acc[h][i] = 0.0f;
-    const int jend = min((wave + 1) * per_wave, cl);
-#pragma unroll 4
-    for (int jl = wave * per_wave + half; jl < jend; jl += 2) {
-        const float* vr = vbase + static_cast<int64_t>(jl) * p.slot;
-        float vv[NQ];
-#pragma unroll
-        for (int i = 0; i < NQ; ++i) {
-            const int d = hl + kHalf * i;
-            vv[i] = MaskF(vr[d < p.hd ? d : 0], d < p.hd);
-        }
+        for (int h = 0; h < GB; ++h) mh[h] = __shfl(mx, h << SHIFT, kWave);
+        float mine = -INFINITY;
 #pragma unroll
         for (int h = 0; h < GB; ++h) {
-            const float e = sc[h * p.chunk + jl];
+            const float mnew = fmaxf(m[h], mh[h]);
+            const float corr = m[h] == -INFINITY ? 0.0f : expf(m[h] - mnew);
+            m[h] = mnew;
+            l[h] *= corr;
 #pragma unroll
-            for (int i = 0; i < NQ; ++i) acc[h][i] = fmaf(e, vv[i], acc[h][i]);
+            for (int i = 0; i < NQ; ++i) acc[h][i] *= corr;
+            mine = my_h == h ? mnew : mine;
         }
+        const float e = valid ? expf(score - mine) : 0.0f;
+        float ps[NPOS * GB];
+#pragma unroll
+        for (int v = 0; v < NPOS * GB; ++v) ps[v] = __shfl(e, (v << SHIFT) + kHalf * half, kWave);
+        float es = e;
+#pragma unroll
+        for (int o = OMIN; o <= kHalf; o *= 2) es += __shfl_xor(es, o, kWave);
+        float eh[GB];
+#pragma unroll
+        for (int h = 0; h < GB; ++h) eh[h] = __shfl(es, h << SHIFT, kWave);
+#pragma unroll
+        for (int h = 0; h < GB; ++h) l[h] += eh[h];
+#pragma unroll
+        for (int s = 0; s < NPOS; ++s) {
+#pragma unroll
+            for (int h = 0; h < GB; ++h) {
+#pragma unroll
+                for (int i = 0; i < NQ; ++i) acc[h][i] = fmaf(ps[s * GB + h], vr[s][i], acc[h][i]);
+            }
+        }
+    };
+
+    // two register sets, loop unrolled by two: each set is reloaded as soon
+    // as its sub-chunk is done, so one sub-chunk loads while the other
+    // computes, with no copies between the sets
+    float ka[NPOS][NQ], va[NPOS][NQ], kb[NPOS][NQ], vb[NPOS][NQ];
+    load(0, ka, va);
+    for (int it = 0; it < n_it; it += 2) {
+        load(it + 1, kb, vb);
+        step(it, ka, va);
+        load(it + 2, ka, va);
+        step(it + 1, kb, vb);
     }
+
+    // merge the halves (same m and l), then the waves through LDS
 #pragma unroll
     for (int h = 0; h < GB; ++h) {
 #pragma unroll
         for (int i = 0; i < NQ; ++i) {
             const float a = acc[h][i] + __shfl_xor(acc[h][i], kHalf, kWave);
-            if (half == 0) red[(wave * GB + h) * W + hl + kHalf * i] = a;
+            if (half == 0) wacc[wave][h][hl + kHalf * i] = a;
+        }
+        if (lane == 0) {
+            wm[wave][h] = m[h];
+            wl[wave][h] = l[h];
         }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < GB * W; e += kAttnThreads) {
-        const int h = e / W, d = e % W;
+    for (int idx = threadIdx.x; idx < GB * W; idx += kAttnThreads) {
+        const int h = idx / W, d = idx % W;
         if (h >= nh || d >= p.hd) continue;
-        float a = red[h * W + d];
+        float M = wm[0][h];
 #pragma unroll
-        for (int w = 1; w < kAttnWaves; ++w) a += red[(w * GB + h) * W + d];
+        for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][h]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float f = wm[w][h] == -INFINITY ? 0.0f : expf(wm[w][h] - M);
+            L = fmaf(wl[w][h], f, L);
+            A = fmaf(wacc[w][h][d], f, A);
+        }
         const int64_t row = t * p.H + h0 + h;
         if (p.n_chunks == 1) {
-            p.out[row * p.hd + d] = a / ml[h][1];
+            p.out[row * p.hd + d] = A / L;
         } else {
-            p.ws_acc[(row * p.n_chunks + c) * p.hd + d] = a;
+            p.ws_acc[(row * p.n_chunks + c) * p.hd + d] = A;
+            if (d == 0) {
+                p.ws_ml[(row * p.n_chunks + c) * 2] = M;
+                p.ws_ml[(row * p.n_chunks + c) * 2 + 1] = L;
+            }
         }
-    }
-    if (p.n_chunks > 1 && static_cast<int>(threadIdx.x) < nh) {
-        const int64_t row = t * p.H + h0 + threadIdx.x;
-        p.ws_ml[(row * p.n_chunks + c) * 2] = ml[threadIdx.x][0];
-        p.ws_ml[(row * p.n_chunks + c) * 2 + 1] = ml[threadIdx.x][1];
     }
 }
 
 // out = sum_c acc_c exp(m_c - M) / sum_c l_c exp(m_c - M), M = max_c m_c,
 // over the chunks that hold positions 0..pos; one workgroup per (token,
-// query head).
+// query head).  The chunk weights exp(m_c - M) are computed once into LDS
+// (in tiles of kCombineTile chunks).
+constexpr int kCombineTile = 1024;
+
 __global__ __launch_bounds__(kAttnThreads) void AttnCombine(AttnParams p) {
+    __shared__ float wgt[kCombineTile];
+    __shared__ double red[kAttnWaves];
+    __shared__ float redf[kAttnWaves];
     const int64_t row = blockIdx.x;  // t * H + h
     const int64_t t = row / p.H;
     const int32_t pos = TokenPos(p, t);
@@ -278,27 +352,44 @@ __global__ __launch_bounds__(kAttnThreads) void AttnCombine(AttnParams p) {
     }
     const int nc = pos / p.chunk + 1;
     const float* mlr = p.ws_ml + row * p.n_chunks * 2;
-    float M = -INFINITY;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, mlr[2 * c]);
-    float L = 0.0f;
-    for (int c = 0; c < nc; ++c) L += mlr[2 * c + 1] * expf(mlr[2 * c] - M);
+    float mloc = -INFINITY;
+    for (int c = threadIdx.x; c < nc; c += kAttnThreads) mloc = fmaxf(mloc, mlr[2 * c]);
+    const float M = BlockMax<kAttnWaves>(mloc, redf);
+    float lloc = 0.0f;
+    for (int c = threadIdx.x; c < nc; c += kAttnThreads) lloc += mlr[2 * c + 1] * expf(mlr[2 * c] - M);
+    const float L = static_cast<float>(BlockSum<kAttnWaves>(static_cast<double>(lloc), red));
     const float* acc = p.ws_acc + row * p.n_chunks * p.hd;
-    for (int d = threadIdx.x; d < p.hd; d += kAttnThreads) {
-        float a = 0.0f;
-        for (int c = 0; c < nc; ++c) a = fmaf(acc[c * p.hd + d], expf(mlr[2 * c] - M), a);
-        o[d] = a / L;
+    float a = 0.0f;
+    const int d = threadIdx.x;
+    for (int c0 = 0; c0 < nc; c0 += kCombineTile) {
+        const int n = min(kCombineTile, nc - c0);
+        __syncthreads();
+        for (int c = threadIdx.x; c < n; c += kAttnThreads) wgt[c] = expf(mlr[2 * (c0 + c)] - M);
+        __syncthreads();
+        if (d < p.hd) {
+            const float* ac = acc + static_cast<int64_t>(c0) * p.hd + d;
+#pragma unroll 8
+            for (int c = 0; c < n; ++c) a = fmaf(ac[static_cast<int64_t>(c) * p.hd], wgt[c], a);
+        }
     }
+    if (d < p.hd) o[d] = a / L;
+}
+
+template <int NQ, bool kFull>
+hipError_t LaunchSplit(int gb, dim3 grid, hipStream_t s, const AttnParams& p) {
+    switch (gb) {
+        case 1: hipLaunchKernelGGL((AttnSplit<NQ, 1, kFull>), grid, dim3(kAttnThreads), 0, s, p); break;
+        case 2: hipLaunchKernelGGL((AttnSplit<NQ, 2, kFull>), grid, dim3(kAttnThreads), 0, s, p); break;
+        case 4: hipLaunchKernelGGL((AttnSplit<NQ, 4, kFull>), grid, dim3(kAttnThreads), 0, s, p); break;
+        default: hipLaunchKernelGGL((AttnSplit<NQ, 8, kFull>), grid, dim3(kAttnThreads), 0, s, p); break;
+    }
+    return hipGetLastError();
 }
 
 template <int NQ>
-hipError_t LaunchChunk(int gb, dim3 grid, size_t lds, hipStream_t s, const AttnParams& p) {
-    switch (gb) {
-        case 1: hipLaunchKernelGGL((AttnChunk<NQ, 1>), grid, dim3(kAttnThreads), lds, s, p); break;
-        case 2: hipLaunchKernelGGL((AttnChunk<NQ, 2>), grid, dim3(kAttnThreads), lds, s, p); break;
-        case 4: hipLaunchKernelGGL((AttnChunk<NQ, 4>), grid, dim3(kAttnThreads), lds, s, p); break;
-        default: hipLaunchKernelGGL((AttnChunk<NQ, 8>), grid, dim3(kAttnThreads), lds, s, p); break;
-    }
-    return hipGetLastError();
+hipError_t LaunchSplit(int gb, int hd, dim3 grid, hipStream_t s, const AttnParams& p) {
+    return hd == kHalf * NQ ? LaunchSplit<NQ, true>(gb, grid, s, p)
+                            : LaunchSplit<NQ, false>(gb, grid, s, p);
 }
 
 int HeadsPerBlock(int group) {
@@ -313,11 +404,12 @@ int DimsPerLane(int hd) {
     return nq;
 }
 
-// Positions per workgroup: the largest of 64..512 that still gives at least
-// 512 workgroups (two per compute unit), else 64.  (512 keeps the dynamic LDS
-// under 64 KiB: 8 heads x 512 scores + the value partials of head_dim 256.)
+// Positions per workgroup: the largest power of two in 64..2048 that still
+// gives at least 512 workgroups (two per compute unit at the kernel's
+// occupancy), else 64.  Larger chunks mean fewer partials to combine and
+// more sub-chunks per workgroup to overlap loads with arithmetic.
 int ChunkFor(int64_t max_ctx, int64_t base_blocks) {
-    int chunk = 512;
+    int chunk = 2048;
     while (chunk > 64 && base_blocks * ((max_ctx + chunk - 1) / chunk) < 512) chunk /= 2;
     return chunk;
 }
@@ -505,18 +597,16 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
     p.ws_ml = nc > 1 ? static_cast<float*>(workspace) + n_tokens * n_heads * nc * head_dim : nullptr;
     p.err = err;
     const int nq = DimsPerLane(head_dim);
-    const size_t lds = (static_cast<size_t>(gb) * chunk + static_cast<size_t>(kAttnWaves) * gb * kHalf * nq) *
-                       sizeof(float);
     const dim3 grid(static_cast<unsigned>(n_tokens * nc), static_cast<unsigned>(n_kv_heads * n_hblk));
     const hipStream_t s = AsStream(stream);
     hipError_t e;
     switch (nq) {
-        case 1: e = LaunchChunk<1>(gb, grid, lds, s, p); break;
-        case 2: e = LaunchChunk<2>(gb, grid, lds, s, p); break;
-        case 4: e = LaunchChunk<4>(gb, grid, lds, s, p); break;
-        default: e = LaunchChunk<8>(gb, grid, lds, s, p); break;
+        case 1: e = LaunchSplit<1>(gb, head_dim, grid, s, p); break;
+        case 2: e = LaunchSplit<2>(gb, head_dim, grid, s, p); break;
+        case 4: e = LaunchSplit<4>(gb, head_dim, grid, s, p); break;
+        default: e = LaunchSplit<8>(gb, head_dim, grid, s, p); break;
     }
-    if (e != hipSuccess) return FromHip(e, "AttnChunk");
+    if (e != hipSuccess) return FromHip(e, "AttnSplit");
     if (nc > 1) {
         hipLaunchKernelGGL(AttnCombine, dim3(static_cast<unsigned>(n_tokens * n_heads)),
                            dim3(kAttnThreads), 0, s, p);

@@ -118,3 +118,12 @@ def bytes_linear(qtype, T, in_features, out_features):
 
 def flops_linear(T, in_features, out_features):
     return 2 * T * in_features * out_features
+
+
+# ------------------------------------------------------- decode attention
+
+def bytes_attention(positions, n_heads, n_kv_heads, head_dim):
+    """Read the K and V rows 0..pos of each token's KV heads once, read q,
+    write out: 8 * (pos + 1) * KV * hd per token + 8 * H * hd."""
+    pos = np.asarray(positions, np.int64)
+    return int(8 * (pos + 1).sum() * n_kv_heads * head_dim + 8 * pos.size * n_heads * head_dim)
