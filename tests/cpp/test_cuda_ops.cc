@@ -437,6 +437,205 @@ void GpuAllocator() {
     RequireError([&] { target.Reshape({3, 3}); }, "element count must remain unchanged");
 }
 
+// ----------------------------------------------- KV cache and attention
+
+// Argument checks that throw before any device allocation.
+void CpuCacheAndAttentionChecks() {
+    Require(CudaCacheBuild() == CudaRuntimeBuilt(), "cache build predicate");
+    Require(CudaAttentionBuilt() == CudaRuntimeBuilt(), "attention build predicate");
+    RequireError([] { CudaCache c(0, 2, 1, 4); }, "value must be positive");
+    RequireError([] { CudaCache c(1, 2, 1, 4, -1); }, "device_id must be non-negative");
+    const CudaCache empty;
+    Require(empty.Bytes_() == 0 && empty.n_layers() == 0, "empty cache");
+    RequireError([&] { (void)empty.KData(); }, "key cache is empty");
+    RequireError([&] { (void)empty.ReadKey(0, 0); }, "must both be initialized");
+    const Tensor q({2, 3});
+    RequireError([&] { (void)CudaAttentionDecode(q, empty, 0, 0, 2, 1, 3); }, "key cache is empty");
+}
+
+// tests/test_cuda_kv_cache.cc:5-47 of the reference tree: host and device
+// slot writes (checked against the oracle's KvCache::Write), slot / head
+// reads, byte offsets, move, Clear, Reset.
+void GpuKvCache() {
+    const int L = 2, S = 6, KV = 2, hd = 8;
+    std::vector<float> kc(L * S * KV * hd, 0.0f), vc(kc.size(), 0.0f);
+    CudaCache gpu(L, S, KV, hd);
+    Require(gpu.Bytes_() == 2ull * L * S * KV * hd * sizeof(float), "KV allocation bytes");
+    for (int layer : {0, 1}) {
+        for (int pos : {0, 2, 5}) {
+            const Tensor k = Random({KV, hd}, 100 + layer * 7 + pos);
+            const Tensor v = Random({KV, hd}, 200 + layer + pos, 0.7f);
+            const int32_t p = pos;
+            Require(orc_kv_write(kc.data(), vc.data(), L, S, KV, hd, layer, &p, 1, k.data.data(),
+                                 v.data.data()) == ORC_OK,
+                    "oracle kv write");
+            if (pos == 2) {
+                gpu.WriteDevice(layer, pos, TensorHostToDevice(k), TensorHostToDevice(v));
+            } else {
+                gpu.WriteHost(layer, pos, k, v);
+            }
+        }
+    }
+    for (int layer : {0, 1}) {
+        for (int pos : {0, 2, 5}) {
+            const size_t slot = (static_cast<size_t>(layer) * S + pos) * KV * hd;
+            Tensor k({KV, hd}), v({KV, hd}), kh({hd}), vh({hd});
+            std::copy_n(kc.begin() + slot, KV * hd, k.data.begin());
+            std::copy_n(vc.begin() + slot, KV * hd, v.data.begin());
+            std::copy_n(kc.begin() + slot + hd, hd, kh.data.begin());
+            std::copy_n(vc.begin() + slot + hd, hd, vh.data.begin());
+            RequireTensor(gpu.ReadKey(layer, pos), k, "KV key slot", 0.0);
+            RequireTensor(gpu.ReadVal(layer, pos), v, "KV value slot", 0.0);
+            RequireTensor(gpu.ReadHeadKey(layer, pos, 1), kh, "KV head key", 0.0);
+            RequireTensor(gpu.ReadHeadVal(layer, pos, 1), vh, "KV head value", 0.0);
+            Require(gpu.SlotOffsetBytes(layer, pos, 1) == ((layer * S + pos) * 16 + 8) * 4ull,
+                    "KV byte offset");
+        }
+    }
+    RequireError([&] { (void)gpu.ReadKey(2, 0); }, "out of range");
+    RequireError([&] { (void)gpu.ReadVal(0, 6); }, "out of range");
+    RequireError([&] { (void)gpu.ReadHeadKey(0, 0, 2); }, "KV head 2 out of range");
+    RequireError([&] { gpu.WriteHost(0, 0, Tensor({KV, hd + 1}), Tensor({KV, hd + 1})); },
+                 "expected shape [2, 8]");
+    RequireError([&] { gpu.WriteDevice(0, 0, TensorHostToDevice(Tensor({hd})),
+                                       TensorHostToDevice(Tensor({hd}))); },
+                 "expected 2D KV tensor");
+    CudaCache moved(std::move(gpu));
+    Require(gpu.Bytes_() == 0 && moved.Bytes_() > 0, "KV move ownership");
+    moved.Clear();
+    RequireTensor(moved.ReadKey(1, 5), Tensor({KV, hd}, 0.0f), "KV clear", 0.0);
+    RequireTensor(moved.ReadVal(1, 5), Tensor({KV, hd}, 0.0f), "KV value clear", 0.0);
+    moved.Reset();
+    Require(moved.Bytes_() == 0 && moved.n_layers() == 0, "KV release");
+    moved.Reset(1, 2, 1, 8);
+    RequireTensor(moved.ReadKey(0, 1), Tensor({1, 8}, 0.0f), "KV reinitialize", 0.0);
+}
+
+Tensor AttentionFloat64(const Tensor& q, const std::vector<Tensor>& keys,
+                        const std::vector<Tensor>& values, int pos) {
+    // test/cuda_attention_test.cc:50-80 of the reference tree
+    const int heads = q.shape[0], dim = q.shape[1];
+    const int group = heads / keys[0].shape[0];
+    Tensor out(q.shape);
+    for (int h = 0; h < heads; ++h) {
+        std::vector<double> scores(pos + 1);
+        for (int t = 0; t <= pos; ++t) {
+            double dot = 0.0;
+            for (int d = 0; d < dim; ++d) {
+                dot += static_cast<double>(q.data[h * dim + d]) * keys[t].data[(h / group) * dim + d];
+            }
+            scores[t] = dot / std::sqrt(static_cast<double>(dim));
+        }
+        const double mx = *std::max_element(scores.begin(), scores.end());
+        double denom = 0.0;
+        for (double& s : scores) {
+            s = std::exp(s - mx);
+            denom += s;
+        }
+        for (int d = 0; d < dim; ++d) {
+            double value = 0.0;
+            for (int t = 0; t <= pos; ++t) {
+                value += scores[t] / denom * values[t].data[(h / group) * dim + d];
+            }
+            out.data[h * dim + d] = static_cast<float>(value);
+        }
+    }
+    return out;
+}
+
+// test/cuda_attention_test.cc:82-158 of the reference tree: host and device
+// attention within 2e-5 of float64 (a populated future slot must not count),
+// then the argument checks.
+void GpuAttention() {
+    struct Case {
+        int heads, kv_heads, dim, pos, layer;
+    };
+    for (const Case c : {Case{2, 2, 7, 0, 0}, Case{4, 2, 9, 5, 1}, Case{4, 1, 133, 130, 1}}) {
+        CudaCache cache(2, c.pos + 2, c.kv_heads, c.dim);
+        Tensor q({c.heads, c.dim});
+        for (size_t i = 0; i < q.data.size(); ++i) q.data[i] = std::sin(static_cast<float>(i) * 0.17f);
+        std::vector<Tensor> keys, values;
+        for (int t = 0; t < cache.max_seq_len(); ++t) {
+            Tensor k({c.kv_heads, c.dim}), v({c.kv_heads, c.dim});
+            for (size_t i = 0; i < k.data.size(); ++i) {
+                k.data[i] = std::cos(static_cast<float>(i) * 0.13f + t * 0.1f);
+                v.data[i] = std::sin(static_cast<float>(i) * 0.11f - t * 0.2f);
+            }
+            cache.WriteHost(c.layer, t, k, v);
+            keys.push_back(k);
+            values.push_back(v);
+        }
+        const Tensor expected = AttentionFloat64(q, keys, values, c.pos);
+        const Tensor host = CudaAttentionDecode(q, cache, c.layer, c.pos, c.heads, c.kv_heads, c.dim);
+        const CudaTensor dev = CudaAttentionDevice(TensorHostToDevice(q), cache, c.layer, c.pos,
+                                                   c.heads, c.kv_heads, c.dim);
+        Require(dev.DeviceId() == 0, "attention device id");
+        RequireTensor(host, expected, "attention host", 2e-5);
+        RequireTensor(dev.Download(), expected, "attention device", 2e-5);
+    }
+    const CudaCache cache(2, 3, 2, 5);
+    Tensor q({4, 5});
+    auto invalid = [&](int layer, int pos, int heads, int kv, int dim, int device, const char* text) {
+        RequireError([&] { (void)CudaAttentionDecode(q, cache, layer, pos, heads, kv, dim, device); },
+                     text);
+    };
+    invalid(-1, 0, 4, 2, 5, 0, "out of range");
+    invalid(2, 0, 4, 2, 5, 0, "out of range");
+    invalid(0, -1, 4, 2, 5, 0, "out of range");
+    invalid(0, 3, 4, 2, 5, 0, "out of range");
+    invalid(0, 0, 0, 2, 5, 0, "value must be positive");
+    invalid(0, 0, 4, 0, 5, 0, "value must be positive");
+    invalid(0, 0, 4, -2, 5, 0, "value must be positive");
+    invalid(0, 0, 4, 2, 0, 0, "value must be positive");
+    invalid(0, 0, 3, 2, 5, 0, "divide n_heads");
+    invalid(0, 0, 4, 1, 5, 0, "cache n_kv_heads mismatch");
+    invalid(0, 0, 4, 2, 6, 0, "cache head_dim mismatch");
+    invalid(0, 0, 4, 2, 5, -1, "cache device_id mismatch");
+    q.shape = {20};
+    invalid(0, 0, 4, 2, 5, 0, "q shape and element count");
+    q.shape = {4, 5};
+    q.data.pop_back();
+    invalid(0, 0, 4, 2, 5, 0, "q shape and element count");
+    const CudaTensor empty;
+    RequireError([&] { (void)CudaAttentionDevice(empty, cache, 0, 0, 4, 2, 5); }, "q shape");
+}
+
+// The batched additions: a prefill chunk of T rows written in one launch and
+// attended causally over the cache, against the oracle row by row.
+void GpuAttentionBatched() {
+    const int L = 2, S = 300, H = 8, KV = 2, hd = 128, layer = 1, pos0 = 150, T = 37;
+    CudaCache cache(L, S, KV, hd);
+    std::vector<float> kc(static_cast<size_t>(L) * S * KV * hd, 0.0f), vc(kc.size(), 0.0f);
+    const Tensor k0 = Random({pos0, KV, hd}, 31), v0 = Random({pos0, KV, hd}, 32);
+    std::vector<int32_t> first(pos0);
+    for (int i = 0; i < pos0; ++i) first[i] = i;
+    CudaKvWriteBatchDevice(cache, layer, 0, TensorHostToDevice(k0), TensorHostToDevice(v0));
+    Require(orc_kv_write(kc.data(), vc.data(), L, S, KV, hd, layer, first.data(), pos0,
+                         k0.data.data(), v0.data.data()) == ORC_OK, "oracle kv write");
+    const Tensor k = Random({T, KV, hd}, 33), v = Random({T, KV, hd}, 34);
+    const Tensor q = Random({T, H, hd}, 35);
+    CudaKvWriteBatchDevice(cache, layer, pos0, TensorHostToDevice(k), TensorHostToDevice(v));
+    std::vector<int32_t> pos(T);
+    for (int t = 0; t < T; ++t) pos[t] = pos0 + t;
+    Require(orc_kv_write(kc.data(), vc.data(), L, S, KV, hd, layer, pos.data(), T, k.data.data(),
+                         v.data.data()) == ORC_OK, "oracle kv write");
+    RequireTensor(cache.ReadKey(layer, pos0 + 5), [&] {
+        Tensor r({KV, hd});
+        std::copy_n(k.data.begin() + 5 * KV * hd, KV * hd, r.data.begin());
+        return r;
+    }(), "batched write slot", 0.0);
+    const CudaTensor out = CudaAttentionBatchDevice(TensorHostToDevice(q), cache, layer, pos0, H,
+                                                    KV, hd);
+    Tensor want({T, H, hd});
+    Require(orc_attention(q.data.data(), kc.data(), vc.data(), L, S, H, KV, hd, layer, pos.data(),
+                          T, want.data.data()) == ORC_OK, "oracle attention");
+    RequireTensor(out.Download(), want, "batched attention", 2e-5);
+    RequireError([&] { CudaKvWriteBatchDevice(cache, layer, S - 2, TensorHostToDevice(k),
+                                              TensorHostToDevice(v)); }, "out of range");
+    RequireError([&] { (void)CudaAttentionBatchDevice(TensorHostToDevice(q), cache, layer, S - 2,
+                                                      H, KV, hd); }, "out of range");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -444,6 +643,7 @@ int main(int argc, char** argv) {
         {"cpu.build_predicate", CpuBuildPredicate},
         {"cpu.rejects_invalid_inputs", CpuRejectsInvalidInputs},
         {"cpu.tensor_checks", CpuTensorChecks},
+        {"cpu.cache_and_attention_checks", CpuCacheAndAttentionChecks},
         {"gpu.device_info", GpuDeviceInfo},
         {"gpu.embedding", GpuEmbedding},
         {"gpu.rmsnorm", GpuRmsNorm},
@@ -455,6 +655,9 @@ int main(int argc, char** argv) {
         {"gpu.quantized", GpuQuantized},
         {"gpu.no_host_transfers", GpuNoHostTransfersInDeviceChain},
         {"gpu.allocator", GpuAllocator},
+        {"gpu.kv_cache", GpuKvCache},
+        {"gpu.attention", GpuAttention},
+        {"gpu.attention_batched", GpuAttentionBatched},
     };
     return Run(argc, argv, cases);
 }

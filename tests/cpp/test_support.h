@@ -6,6 +6,8 @@
 // and exit status 1 on the first failure.  Expected values come from the CPU
 // oracle (oracle/oracle.h), never from the code under test.
 #pragma once
+#include "include/cuda_attention.h"
+#include "include/cuda_kvcache.h"
 #include "include/cuda_ops.h"
 #include "oracle/oracle.h"
 

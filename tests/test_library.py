@@ -65,6 +65,12 @@ CPP_SURFACE = [
     "CudaQuantBuilt", "CudaQ40Linear", "CudaQ40DeviceLinear", "CudaQ40DeviceInputLinear",
     "CudaQ41Linear", "CudaQ41DeviceLinear", "CudaQ41DeviceInputLinear", "CudaQ80Linear",
     "CudaQ80DeviceLinear", "CudaQ80DeviceInputLinear",
+    # include/cuda_kvcache.h, include/cuda_attention.h
+    "CudaCacheBuild", "CudaCache::Reset", "CudaCache::WriteHost", "CudaCache::WriteDevice",
+    "CudaCache::ReadKey", "CudaCache::ReadVal", "CudaCache::ReadHeadKey", "CudaCache::ReadHeadVal",
+    "CudaCache::KData", "CudaCache::vData", "CudaCache::Bytes_", "CudaCache::Clear",
+    "CudaCache::SlotOffsetBytes", "CudaKvWriteBatchDevice", "CudaAttentionBuilt",
+    "CudaAttentionDecode", "CudaAttentionDevice", "CudaAttentionBatchDevice",
 ]
 
 
