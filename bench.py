@@ -64,6 +64,14 @@ def parse_args():
                             "CALIB_WRITE_DIR"),
                    help="summarize rocprofv3 CSV output of the default command (kernel trace) "
                         "and of the --pmc FETCH_SIZE / WRITE_SIZE runs into profiles/")
+    p.add_argument("--kernel-summary", nargs="+", default=None,
+                   metavar="ARG",
+                   help="OUT_MD TITLE BENCH_JSON KERNEL_TRACE_DIR [FETCH_DIR WRITE_DIR]: write a "
+                        "rocprofv3 summary (per kernel and grid: calls, avg/min us, and HBM bytes "
+                        "from FETCH_SIZE / WRITE_SIZE scaled by the committed calibration) of a "
+                        "--linear or --attention run, with that run's JSON results, into OUT_MD; "
+                        "the commands that produced the inputs are read from the environment "
+                        "variable PROFILE_COMMANDS (one per line)")
     p.add_argument("--calibrate", action="store_true",
                    help="only run the counter-calibration kernel (SiLU over 256 MiB: "
                         "reads 256 MiB, writes 256 MiB per launch)")
@@ -641,8 +649,74 @@ def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
     print("\n".join(md))
 
 
+def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=None):
+    """Markdown summary of a rocprofv3 kernel trace (and optional counter runs)
+    next to the bench JSON of the same command."""
+    import csv
+    launches = {}
+    for r in csv.DictReader(open(_one_csv(kt_dir, "kernel_trace.csv"))):
+        key = (r["Kernel_Name"], int(r["Grid_Size_X"]) * int(r.get("Grid_Size_Y", 1) or 1) *
+               int(r.get("Grid_Size_Z", 1) or 1))
+        launches.setdefault(key, []).append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE") if fetch_dir else {}
+    write = _counter_means(write_dir, "WRITE_SIZE") if write_dir else {}
+    with open(PMC_FILE) as f:
+        calib = json.load(f)
+    ff, wf = calib["fetch_factor"], calib["write_factor"]
+    cmds = [c for c in os.environ.get("PROFILE_COMMANDS", "").split("\n") if c.strip()]
+    md = [f"# {title}: rocprofv3 summary", "", "Commands (repo root, one MI355X):", ""]
+    md += ["    " + c for c in cmds]
+    md += ["", "Kernel durations from the kernel trace (grid = total work-items)"
+           + (", HBM bytes per launch = FETCH_SIZE / %.4f + WRITE_SIZE / %.4f (KiB -> bytes), "
+              "the factors of the committed copy-kernel calibration" % (ff, wf)
+              if fetch else "") + ":", "",
+           "| kernel | grid | calls | avg us | min us |" + (" HBM bytes / launch |" if fetch else ""),
+           "|---|---|---|---|---|" + ("---|" if fetch else "")]
+    def short(name):
+        # "void mlk::(anonymous namespace)::K<...>(args)" -> "K<...>"
+        import re
+        m = re.search(r"(\w+(?:<[^()]*>)?)\(", name)
+        return m.group(1) if m else name
+
+    for (name, grid), d in sorted(launches.items(), key=lambda kv: (short(kv[0][0]), kv[0][1])):
+        if name.startswith("__amd") or "Fill" in name or "Quantize" in name:
+            continue
+        row = "| %s | %d | %d | %.2f | %.2f |" % (short(name), grid, len(d), sum(d) / len(d),
+                                                  min(d))
+        if fetch:
+            fk = [v for (k, g), v in fetch.items() if k == name and g == grid]
+            wk = [v for (k, g), v in write.items() if k == name and g == grid]
+            row += " %s |" % (("%.0f" % ((fk[0] / ff + wk[0] / wf) * 1024)) if fk and wk else "n/a")
+        md.append(row)
+    md += ["", "Results of the same command (bench.py JSON, events around back-to-back "
+           "launches on rotating cold copies):", "",
+           "| case | us | algorithmic GB/s | fraction of 8 TB/s |", "|---|---|---|---|"]
+
+    def walk(node, path):
+        if isinstance(node, dict):
+            if "us" in node and "GBps" in node:
+                md.append("| %s | %.2f | %.1f | %.3f |" % (" / ".join(path), node["us"],
+                                                           node["GBps"], node["frac_of_peak"]))
+            if "layer_us" in node:
+                md.append("| %s | %.2f | %.1f | %.3f |" % (" / ".join(path + ["layer"]),
+                                                           node["layer_us"], node["layer_GBps"],
+                                                           node["layer_frac_of_peak"]))
+            for k, v in node.items():
+                if k not in ("ops",) or isinstance(v, dict):
+                    walk(v, path + ([k] if k not in ("ops", "cases") else []))
+
+    walk(json.load(open(bench_json)), [])
+    with open(out_md, "w") as f:
+        f.write("\n".join(md) + "\n")
+    print("\n".join(md[:40]))
+
+
 def main():
     args = parse_args()
+    if args.kernel_summary:
+        kernel_summary(*args.kernel_summary)
+        return
     if args.rocprof_report:
         rocprof_report(*args.rocprof_report)
         return
