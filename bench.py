@@ -78,25 +78,29 @@ def parse_args():
     return p.parse_args()
 
 
-class ChainSet:
-    """Device buffers of one op-chain input/output set."""
+# buffers each op touches; run_ops rotates an op over extra sets of only these
+OP_FIELDS = {"gather_f32": ("x",), "add_rmsnorm": ("x", "delta", "y"), "rope": ("q", "k"),
+             "swiglu": ("gate", "up", "out")}
+OP_WORKING_SET = 768 << 20  # bytes one pass of an op's rotation touches: 3x the 256 MB MALL
+OP_MAX_SETS = 16  # decode-size buffers stay cache-resident, as in a real decode step
 
-    def __init__(self, mlk, cfg, T, seed):
+
+class ChainSet:
+    """Device buffers of one op-chain input/output set (or of `fields` only)."""
+
+    def __init__(self, mlk, cfg, T, seed, fields=None):
         D, H, KV, hd, F = cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"]
-        E = mlk.DeviceBuffer.empty
-        self.x = E((T, D))
-        self.delta = E((T, D))
-        self.y = E((T, D))
-        self.q = E((T, H * hd))
-        self.k = E((T, KV * hd))
-        self.gate = E((T, F))
-        self.up = E((T, F))
-        self.out = E((T, F))
-        mlk.fill_normal(self.delta, T * D, 0.0, 0.02, seed + 1)
-        mlk.fill_normal(self.q, T * H * hd, 0.0, 0.02, seed + 2)
-        mlk.fill_normal(self.k, T * KV * hd, 0.0, 0.02, seed + 3)
-        mlk.fill_normal(self.gate, T * F, 0.0, 0.02, seed + 4)
-        mlk.fill_normal(self.up, T * F, 0.0, 0.02, seed + 5)
+        shapes = {"x": (T, D), "delta": (T, D), "y": (T, D), "q": (T, H * hd),
+                  "k": (T, KV * hd), "gate": (T, F), "up": (T, F), "out": (T, F)}
+        filled = {"x": 0, "delta": 1, "q": 2, "k": 3, "gate": 4, "up": 5}
+        self.nbytes = 0
+        for name in fields or shapes:
+            buf = mlk.DeviceBuffer.empty(shapes[name])
+            setattr(self, name, buf)
+            self.nbytes += buf.nbytes
+            # x is the gather's output in a chain step; alone it is filled
+            if name in filled and (fields is not None or name != "x"):
+                mlk.fill_normal(buf, buf.nbytes // 4, 0.0, 0.02, seed + filled[name])
 
 
 class Chain:
@@ -173,20 +177,35 @@ class Chain:
         graph.close()
         return start.elapsed_ms(stop) / steps
 
+    def op_sets(self, op):
+        """The chain's sets, plus sets of only `op`'s buffers until one pass
+        over them touches OP_WORKING_SET bytes (or OP_MAX_SETS sets), so no
+        prefill-size launch finds its buffers in the MALL from the previous
+        pass."""
+        sets = list(self.sets)
+        fields = OP_FIELDS[op]
+        one = sum(getattr(self.sets[0], f).nbytes for f in fields)
+        seed = self.cfg["seed"] + 1000
+        while one * len(sets) < OP_WORKING_SET and len(sets) < OP_MAX_SETS:
+            sets.append(ChainSet(self.mlk, self.cfg, self.T, seed + 10 * len(sets), fields))
+        return sets
+
     def run_ops(self, steps, warmup=3):
         """Per-kernel launch duration: each op launched `steps` times back to
-        back over the rotating sets between two events; returns
+        back over its cold rotation (op_sets) between two events; returns
         {op: ms per launch}."""
         mlk = self.mlk
         out = {}
         for op in self.OPS:
+            sets = self.op_sets(op)
+            self.mlk.synchronize()
             for i in range(warmup):
-                self.launch(self.sets[i % len(self.sets)], op)
+                self.launch(sets[i % len(sets)], op)
             self.stream.synchronize()
             start, stop = mlk.Event(), mlk.Event()
             start.record(self.stream)
             for i in range(steps):
-                self.launch(self.sets[i % len(self.sets)], op)
+                self.launch(sets[i % len(sets)], op)
             stop.record(self.stream)
             stop.synchronize()
             out[op] = start.elapsed_ms(stop) / steps
@@ -530,7 +549,7 @@ def calibrate(mlk, steps):
 # ------------------------------------------------------- rocprof summaries
 
 CHAIN_KERNELS = {"GatherF32Vec": "gather_f32", "AddRmsNormVec": "add_rmsnorm",
-                 "RopeOneBatch": "rope", "StreamKernel": "swiglu"}
+                 "RopePipe": "rope", "StreamKernel": "swiglu"}
 
 PROFILE_COMMANDS = [
     "rocprofv3 --kernel-trace --stats -T --output-format csv -d gpurun_out/prof_kt -o bench "

@@ -13,11 +13,13 @@
 // T = 4096).  The threads form `rows` rows of `lanes` lanes; a lane owns PV
 // consecutive pairs of a head, computes its inverse frequencies once per
 // kernel and, per token, issues the loads of its first kBatch heads before
-// evaluating the float64 sincos, so the transcendental latency hides under
+// evaluating the float64 sin and cos, so the transcendental latency hides under
 // the memory latency; the same angles then serve every head the row visits.
 // Q and K are one launch (the reference made two per token).  The update is
-// in place, and plain loads/stores measured ~20% faster than non-temporal
-// ones for this read-modify-write pattern on MI355X.
+// in place with non-temporal loads and stores: on MI355X a cold
+// read-modify-write stream reaches ~6.0 TB/s with them against ~5.3 TB/s
+// with plain ones (plain ones only look faster when the data is still in the
+// 256 MB MALL).
 //
 // HBM bytes per token: 8 * (n_heads + n_kv_heads) * head_dim (read + write).
 #include "mlk_common.h"
@@ -31,6 +33,24 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kBatch = 5;  // heads loaded per lane before the first rotation
 
+// sin and cos of a float64 angle a.  The angle is first reduced by whole
+// turns: a / pi is formed as a double-double, with the product by 1/pi's
+// leading double split exactly by an fma (Dekker's two-product) and the
+// product by its trailing double added, then the nearest even integer n is
+// subtracted exactly (|a / pi| < 2^52), which is Cody and Waite's additive
+// reduction.  sincospi of the remainder, in [-1, 1], then equals sin / cos
+// of a within a few float64 ulps for |a| < 2^31, the angles RoPE forms.
+// Unlike a general sincos this keeps no large-argument (Payne-Hanek)
+// reduction, whose registers would be allocated across the whole kernel.
+__device__ inline void SinCosAngle(double a, double* s, double* c) {
+    constexpr double kInvPiHi = 0x1.45f306dc9c883p-2;    // 1/pi rounded to float64
+    constexpr double kInvPiLo = -0x1.6b01ec5417056p-56;  // 1/pi - kInvPiHi, rounded
+    const double p = a * kInvPiHi;
+    const double e = fma(a, kInvPiHi, -p) + a * kInvPiLo;
+    const double n = 2.0 * rint(0.5 * p);
+    sincospi((p - n) + e, s, c);
+}
+
 template <int PV, bool kNeoX>
 struct Pairs;
 
@@ -39,7 +59,7 @@ template <>
 struct Pairs<2, false> {
     float4 v;
     __device__ void Load(const float* head, int g, int) {
-        v = reinterpret_cast<const float4*>(head)[g];
+        v = LoadNT(reinterpret_cast<const float4*>(head) + g);
     }
     __device__ void Rotate(const double* c, const double* s) {
         const double a0 = v.x, a1 = v.y, b0 = v.z, b1 = v.w;
@@ -49,7 +69,16 @@ struct Pairs<2, false> {
         v.w = static_cast<float>(b0 * s[1] + b1 * c[1]);
     }
     __device__ void Store(float* head, int g, int) const {
-        reinterpret_cast<float4*>(head)[g] = v;
+        StoreNT(reinterpret_cast<float4*>(head) + g, v);
+    }
+    // byte offset of the lane's elements from a row base (32-bit, so the
+    // address is a scalar base plus a 32-bit lane offset)
+    static __device__ uint32_t LaneBytes(int g, int) { return 16u * g; }
+    __device__ void LoadAt(const char* base, uint32_t o, uint32_t) {
+        v = LoadNT(reinterpret_cast<const float4*>(base + o));
+    }
+    __device__ void StoreAt(char* base, uint32_t o, uint32_t) const {
+        StoreNT(reinterpret_cast<float4*>(base + o), v);
     }
 };
 
@@ -58,8 +87,8 @@ template <>
 struct Pairs<1, false> {
     float x0, x1;
     __device__ void Load(const float* head, int g, int) {
-        x0 = head[2 * g];
-        x1 = head[2 * g + 1];
+        x0 = LoadNT(head + 2 * g);
+        x1 = LoadNT(head + 2 * g + 1);
     }
     __device__ void Rotate(const double* c, const double* s) {
         const double a0 = x0, a1 = x1;
@@ -67,8 +96,17 @@ struct Pairs<1, false> {
         x1 = static_cast<float>(a0 * s[0] + a1 * c[0]);
     }
     __device__ void Store(float* head, int g, int) const {
-        head[2 * g] = x0;
-        head[2 * g + 1] = x1;
+        StoreNT(head + 2 * g, x0);
+        StoreNT(head + 2 * g + 1, x1);
+    }
+    static __device__ uint32_t LaneBytes(int g, int) { return 8u * g; }
+    __device__ void LoadAt(const char* base, uint32_t o, uint32_t) {
+        x0 = LoadNT(reinterpret_cast<const float*>(base + o));
+        x1 = LoadNT(reinterpret_cast<const float*>(base + (o + 4u)));
+    }
+    __device__ void StoreAt(char* base, uint32_t o, uint32_t) const {
+        StoreNT(reinterpret_cast<float*>(base + o), x0);
+        StoreNT(reinterpret_cast<float*>(base + (o + 4u)), x1);
     }
 };
 
@@ -77,8 +115,8 @@ template <>
 struct Pairs<2, true> {
     float2 lo, hi;
     __device__ void Load(const float* head, int g, int half) {
-        lo = reinterpret_cast<const float2*>(head)[g];
-        hi = reinterpret_cast<const float2*>(head + half)[g];
+        lo = LoadNT(reinterpret_cast<const float2*>(head) + g);
+        hi = LoadNT(reinterpret_cast<const float2*>(head + half) + g);
     }
     __device__ void Rotate(const double* c, const double* s) {
         const double a0 = lo.x, a1 = hi.x, b0 = lo.y, b1 = hi.y;
@@ -88,8 +126,17 @@ struct Pairs<2, true> {
         hi.y = static_cast<float>(b0 * s[1] + b1 * c[1]);
     }
     __device__ void Store(float* head, int g, int half) const {
-        reinterpret_cast<float2*>(head)[g] = lo;
-        reinterpret_cast<float2*>(head + half)[g] = hi;
+        StoreNT(reinterpret_cast<float2*>(head) + g, lo);
+        StoreNT(reinterpret_cast<float2*>(head + half) + g, hi);
+    }
+    static __device__ uint32_t LaneBytes(int g, int) { return 8u * g; }
+    __device__ void LoadAt(const char* base, uint32_t o, uint32_t half_bytes) {
+        lo = LoadNT(reinterpret_cast<const float2*>(base + o));
+        hi = LoadNT(reinterpret_cast<const float2*>(base + (o + half_bytes)));
+    }
+    __device__ void StoreAt(char* base, uint32_t o, uint32_t half_bytes) const {
+        StoreNT(reinterpret_cast<float2*>(base + o), lo);
+        StoreNT(reinterpret_cast<float2*>(base + (o + half_bytes)), hi);
     }
 };
 
@@ -98,8 +145,8 @@ template <>
 struct Pairs<1, true> {
     float x0, x1;
     __device__ void Load(const float* head, int g, int half) {
-        x0 = head[g];
-        x1 = head[g + half];
+        x0 = LoadNT(head + g);
+        x1 = LoadNT(head + g + half);
     }
     __device__ void Rotate(const double* c, const double* s) {
         const double a0 = x0, a1 = x1;
@@ -107,8 +154,17 @@ struct Pairs<1, true> {
         x1 = static_cast<float>(a0 * s[0] + a1 * c[0]);
     }
     __device__ void Store(float* head, int g, int half) const {
-        head[g] = x0;
-        head[g + half] = x1;
+        StoreNT(head + g, x0);
+        StoreNT(head + g + half, x1);
+    }
+    static __device__ uint32_t LaneBytes(int g, int) { return 4u * g; }
+    __device__ void LoadAt(const char* base, uint32_t o, uint32_t half_bytes) {
+        x0 = LoadNT(reinterpret_cast<const float*>(base + o));
+        x1 = LoadNT(reinterpret_cast<const float*>(base + (o + half_bytes)));
+    }
+    __device__ void StoreAt(char* base, uint32_t o, uint32_t half_bytes) const {
+        StoreNT(reinterpret_cast<float*>(base + o), x0);
+        StoreNT(reinterpret_cast<float*>(base + (o + half_bytes)), x1);
     }
 };
 
@@ -164,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64
                     // evaluated while the first batch of loads is in flight
 #pragma unroll
                     for (int p = 0; p < PV; ++p) {
-                        sincos(static_cast<double>(pos) * inv_freq[p], &s[p], &c[p]);
+                        SinCosAngle(static_cast<double>(pos) * inv_freq[p], &s[p], &c[p]);
                     }
                     have_angles = true;
                 }
@@ -181,58 +237,104 @@ __global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64
 }
 
 // Common case: every lane rotates at most kBatch heads of one pair group per
-// token, so one batch of loads covers the token (the workgroup has
-// lanes * ceil(heads / kBatch) threads: 256 for 8B heads, 512 for 70B).
-// Same arithmetic as RopeKernel, with no batch loop and fewer registers.
+// token, so one batch of loads covers the token.  The threads form `rows`
+// rows; batch slot b < q_slots holds Q head b * rows + row, the later slots
+// K heads (b - q_slots) * rows + row, so which of Q and K a slot reads is
+// uniform and the token's Q and K row addresses stay scalar, each lane
+// keeping one 32-bit offset per slot (256 threads for 8B heads: rows 8,
+// slots 4 + 1; 512 for 70B: rows 16, slots 4 + 1).
+// The workgroup's tokens are t = blockIdx.x + j * gridDim.x; the next
+// token's heads load while the current one's float64 sin, cos and rotation
+// run (two register sets, loop unrolled by two with the last one or two
+// tokens peeled, so no load sits under a branch and no token is loaded
+// twice: a reload would come from HBM, the loads being non-temporal).
+// Same arithmetic as RopeKernel.
 template <int PV, bool kNeoX>
-__global__ __launch_bounds__(1024) void RopeOneBatch(float* q, float* k, int64_t n_tokens,
-                                                     int n_heads, int n_kv_heads, int head_dim,
-                                                     int64_t q_stride, int64_t k_stride,
-                                                     const int32_t* positions, int32_t pos0,
-                                                     float theta, int32_t* err) {
+__global__ __launch_bounds__(1024) void RopePipe(float* q, float* k, int64_t n_tokens,
+                                                 int n_heads, int n_kv_heads, int head_dim,
+                                                 int64_t q_stride, int64_t k_stride,
+                                                 const int32_t* positions, int32_t pos0,
+                                                 float theta, int rows, int q_slots,
+                                                 int32_t* err) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
     const int half = head_dim / 2;
     const int lanes = half / PV;
-    const int rows = blockDim.x / lanes;
     const int lane = tid % lanes;
     const int row = tid / lanes;
     if (row >= rows) return;
-    const int heads = n_heads + n_kv_heads;
+    const int64_t nt = (n_tokens - blockIdx.x + gridDim.x - 1) / gridDim.x;
+    auto token = [&](int64_t j) { return static_cast<int64_t>(blockIdx.x) + j * gridDim.x; };
     double inv_freq[PV];
 #pragma unroll
     for (int p = 0; p < PV; ++p) {
         inv_freq[p] = pow(static_cast<double>(theta), -2.0 * (lane * PV + p) / head_dim);
     }
-    for (int64_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
-        const int32_t pos = positions != nullptr ? positions[t] : pos0 + static_cast<int32_t>(t);
-        if (pos < 0) {
-            if (tid == 0) RaiseFlag(err, 1);
-            continue;
-        }
-        Pairs<PV, kNeoX> v[kBatch];
-        float* base[kBatch];
+    using V = Pairs<PV, kNeoX>;
+    uint32_t off[kBatch];  // byte offset of the lane's elements of the slot's head
+    bool ok[kBatch];       // the slot holds a head
 #pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            const int h = row + b * rows;
-            base[b] = nullptr;
-            if (h < heads) {
-                base[b] = h < n_heads ? q + t * q_stride + static_cast<int64_t>(h) * head_dim
-                                      : k + t * k_stride + static_cast<int64_t>(h - n_heads) * head_dim;
-                v[b].Load(base[b], lane, half);
-            }
-        }
-        double c[PV], s[PV];  // evaluated while the loads are in flight
-#pragma unroll
-        for (int p = 0; p < PV; ++p) sincos(static_cast<double>(pos) * inv_freq[p], &s[p], &c[p]);
-#pragma unroll
-        for (int b = 0; b < kBatch; ++b) {
-            if (base[b] != nullptr) {
-                v[b].Rotate(c, s);
-                v[b].Store(base[b], lane, half);
-            }
-        }
+    for (int b = 0; b < kBatch; ++b) {
+        const int h = (b < q_slots ? b : b - q_slots) * rows + row;
+        ok[b] = h < (b < q_slots ? n_heads : n_kv_heads);
+        off[b] = 4u * static_cast<uint32_t>(h) * static_cast<uint32_t>(head_dim) +
+                 V::LaneBytes(lane, half);
     }
+    const uint32_t half_bytes = 4u * static_cast<uint32_t>(half);
+    // the token's Q or K row: uniform across the workgroup
+    auto row_base = [&](int64_t t, int b) {
+        return reinterpret_cast<char*>(b < q_slots ? q + t * q_stride : k + t * k_stride);
+    };
+    auto load = [&](int64_t t, V (&v)[kBatch]) {
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            if (ok[b]) v[b].LoadAt(row_base(t, b), off[b], half_bytes);
+        }
+    };
+    auto rotate = [&](int64_t t, V (&v)[kBatch]) {
+        const int32_t pos = positions != nullptr ? positions[t] : pos0 + static_cast<int32_t>(t);
+        if (pos < 0) {  // leave the token unrotated, raise the flag
+            if (tid == 0) RaiseFlag(err, 1);
+            return;
+        }
+        double c[PV], sn[PV];
+#pragma unroll
+        for (int p = 0; p < PV; ++p) SinCosAngle(static_cast<double>(pos) * inv_freq[p], &sn[p], &c[p]);
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            if (ok[b]) {
+                v[b].Rotate(c, sn);
+                v[b].StoreAt(row_base(t, b), off[b], half_bytes);
+            }
+        }
+    };
+    V va[kBatch], vb[kBatch];
+    load(token(0), va);
+    int64_t j = 0;
+    for (; j + 2 < nt; j += 2) {  // tokens j, j+1 and j+2 exist
+        load(token(j + 1), vb);
+        rotate(token(j), va);
+        load(token(j + 2), va);
+        rotate(token(j + 1), vb);
+    }
+    // one or two tokens left, j's already loaded; both branches complete,
+    // so no load is pending across a join
+    if (j + 1 < nt) {
+        load(token(j + 1), vb);
+        rotate(token(j), va);
+        rotate(token(j + 1), vb);
+    } else {
+        rotate(token(j), va);
+    }
+}
+
+// Smallest row count whose Q and K slots fit kBatch, or 0 when the rows
+// would need more than 1024 threads.
+inline int PipeRows(int n_heads, int n_kv_heads, int lanes) {
+    for (int rows = (n_heads + n_kv_heads + kBatch - 1) / kBatch; rows * lanes <= 1024; ++rows) {
+        if ((n_heads + rows - 1) / rows + (n_kv_heads + rows - 1) / rows <= kBatch) return rows;
+    }
+    return 0;
 }
 
 template <int PV, bool kNeoX>
@@ -240,17 +342,20 @@ mlk_status LaunchRope(float* q, float* k, int64_t n_tokens, int n_heads, int n_k
                       int head_dim, int64_t qs, int64_t ks, const int32_t* positions,
                       int32_t pos0, float theta, int32_t* err, hipStream_t stream) {
     const int lanes = head_dim / 2 / PV;
-    const int heads = n_heads + n_kv_heads;
-    const int rows = (heads + kBatch - 1) / kBatch;
-    const int64_t threads = (static_cast<int64_t>(lanes) * rows + kWave - 1) / kWave * kWave;
-    if (threads <= 1024) {
+    const int rows = PipeRows(n_heads, n_kv_heads, lanes);
+    // byte offsets within a token's Q or K row are 32-bit
+    const bool offsets_fit =
+        4 * static_cast<int64_t>(n_heads > n_kv_heads ? n_heads : n_kv_heads) * head_dim <= UINT32_MAX;
+    if (rows > 0 && offsets_fit) {
+        const int64_t threads = (static_cast<int64_t>(lanes) * rows + kWave - 1) / kWave * kWave;
         // about 1024 resident threads' worth of workgroups per CU
-        const int per_cu = static_cast<int>(1024 / threads) > 0 ? static_cast<int>(1024 / threads) : 1;
+        const int per_cu = static_cast<int>(1024 / threads);
         const unsigned grid = GridFor(n_tokens, 1, per_cu);
-        hipLaunchKernelGGL((RopeOneBatch<PV, kNeoX>), dim3(grid), dim3(threads), 0, stream, q, k,
-                           n_tokens, n_heads, n_kv_heads, head_dim, qs, ks, positions, pos0, theta,
-                           err);
-        return CheckLaunch("RopeOneBatch");
+        const int q_slots = (n_heads + rows - 1) / rows;
+        hipLaunchKernelGGL((RopePipe<PV, kNeoX>), dim3(grid), dim3(threads), 0, stream, q, k,
+                           n_tokens, n_heads, n_kv_heads, head_dim, qs, ks, positions, pos0,
+                           theta, rows, q_slots, err);
+        return CheckLaunch("RopePipe");
     }
     const unsigned grid = GridFor(n_tokens, 1, 4);
     hipLaunchKernelGGL((RopeKernel<PV, kNeoX>), dim3(grid), dim3(kThreads), 0, stream, q, k,

@@ -190,6 +190,7 @@ ROPE_CASES = [
     (7, 32, 8, 128, 500000.0),  # 8B decode-like
     (3, 64, 8, 128, 500000.0),  # 70B
     (2, 3, 1, 6, 100.0),
+    (2, 128, 128, 128, 10000.0),  # too many heads for one batch per lane: general kernel
 ]
 
 
@@ -218,6 +219,30 @@ def test_rope_matches_oracle(mlk, orc, T, H, KV, hd, theta, rope_type):
     assert_terms_close(d_k.download(), ek, np.abs(ek), "k pos0")
     print(f"rope T={T} H={H} KV={KV} hd={hd} type={rope_type} max ulp: "
           f"{max(max_ulp(gq, exp_q), max_ulp(gk, exp_k))}")
+
+
+# Workgroups walk tokens t = block + j * grid, two per loop trip with the
+# last one or two peeled: token counts that leave every workgroup 1..5
+# tokens (grid: 1024 resident threads per CU in workgroups of 256 threads at
+# 8B heads, 512 at 70B, 64 for the small heads).
+@pytest.mark.parametrize("rope_type", [0, 1])
+@pytest.mark.parametrize("per_cu,H,KV,hd", [(4, 32, 8, 128), (16, 4, 2, 16), (16, 14, 2, 64),
+                                            (2, 64, 8, 128)])
+@pytest.mark.parametrize("trips", [1, 2, 3, 4])
+def test_rope_tokens_per_workgroup(mlk, orc, trips, per_cu, H, KV, hd, rope_type):
+    grid = per_cu * mlk.device_info()["compute_units"]
+    T = trips * grid + 2 * trips + 1  # the first workgroups get one token more
+    rng = np.random.default_rng(trips * 7 + H + rope_type)
+    q = normal(rng, (T, H * hd))
+    k = normal(rng, (T, KV * hd), std=0.3)
+    pos = rng.integers(0, 8192, size=T).astype(np.int32)
+    exp_q, exp_k = orc.rope(q, k, H, KV, hd, positions=pos, theta=500000.0, rope_type=rope_type)
+    d_q = mlk.DeviceBuffer.from_array(q)
+    d_k = mlk.DeviceBuffer.from_array(k)
+    d_pos = mlk.DeviceBuffer.from_array(pos)
+    mlk.rope(d_q, d_k, T, H, KV, hd, positions=d_pos, theta=500000.0, rope_type=rope_type)
+    assert_terms_close(d_q.download(), exp_q, np.abs(exp_q), f"q T={T}")
+    assert_terms_close(d_k.download(), exp_k, np.abs(exp_k), f"k T={T}")
 
 
 def test_rope_golden_positions(mlk):
