@@ -54,6 +54,9 @@ def parse_args():
                    help="only measure the seven linear projections of one Llama-3-8B layer "
                         "(F32, Q8_0, Q4_0, Q4_1 weights; T = 1, 4, 16 token rows) into this "
                         "JSON file")
+    p.add_argument("--gemm", default=None,
+                   help="only measure the seven Llama-3-8B layer projections at prefill row counts "
+                        "(32 to 4096; the matrix-core GEMM) into this JSON file")
     p.add_argument("--attention", default=None,
                    help="only measure decode attention (Llama-3-8B and 70B head shapes, one "
                         "token at several context lengths and configs[1]'s 64 tokens) into "
@@ -373,14 +376,15 @@ class LinearLayers:
     finds its weights in cache (the per-projection loop rotates over a
     matrix's copies, the whole-layer loop over all of them)."""
 
-    def __init__(self, mlk, cfg, qtype, seed):
+    def __init__(self, mlk, cfg, qtype, seed, working_set=LINEAR_WORKING_SET):
         self.mlk, self.qtype = mlk, qtype
         self.shapes = workloads.layer_linears(cfg)
         biggest = max(k * o for _, k, o in self.shapes)
         tmp = mlk.DeviceBuffer.empty((biggest,)) if qtype != "f32" else None
         self.copies = {}
         for j, (name, k, o) in enumerate(self.shapes):
-            n = max(2, -(-LINEAR_WORKING_SET // workloads.weight_bytes(qtype, k, o)))
+            n = max(1 if working_set == 0 else 2,
+                    -(-working_set // workloads.weight_bytes(qtype, k, o)))
             mats = []
             for c in range(n):
                 sd = seed + 97 * c + j
@@ -457,6 +461,72 @@ def linear_bench(mlk, steps, peak, path):
                            "layer_GBps": round(gbs, 1), "layer_frac_of_peak": round(gbs / peak, 4),
                            "ops": per}
             print(f"linear {qt} T={T}: layer {ms * 1e3:.1f} us, {gbs:.0f} GB/s", flush=True)
+        out[qt] = res
+        del layers
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+
+
+# ------------------------------------------------------------ prefill GEMM
+
+GEMM_TOKENS = (8, 16, 32, 64, 128, 512, 4096)
+MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
+
+
+def gemm_bench(mlk, steps, path):
+    """The seven projections of one Llama-3-8B layer at prefill row counts
+    (the matrix-core GEMM path): per-projection launch time, each launched
+    `steps` times back to back between two events on its stream, and one
+    whole layer's seven projections; TFLOP/s = 2 T K O / time against the
+    fp32 MFMA peak.  One weight copy per projection: from 128 rows on these
+    shapes are compute-bound, and below that the split-K launches read each
+    weight byte once per call either way."""
+    cfg = workloads.CONFIGS["c3_prefill_8b"]
+    shapes = workloads.layer_linears(cfg)
+    big = max(max(k, o) for _, k, o in shapes)
+    T_max = max(GEMM_TOKENS)
+    x = mlk.DeviceBuffer.empty((T_max, big))
+    y = mlk.DeviceBuffer.empty((T_max, big))
+    mlk.fill_normal(x, T_max * big, 0.0, 1.0, 5)
+    st = mlk.Stream()
+    out = {"workload": "Llama-3-8B layer projections at prefill row counts, weights N(0,0.02) "
+                       "quantized on the device; x N(0,1)",
+           "peak_TFLOPs": MFMA_FP32_PEAK_TFLOPS}
+    for qt in LINEAR_TYPES:
+        layers = LinearLayers(mlk, cfg, qt, seed=300, working_set=0)
+        res = {}
+        for T in GEMM_TOKENS:
+            per = {}
+            for name, k, o in shapes:
+                for i in range(2):
+                    layers.launch(i, name, k, o, x, y, T, st)
+                st.synchronize()
+                e0, e1 = mlk.Event(), mlk.Event()
+                e0.record(st)
+                for i in range(steps):
+                    layers.launch(i, name, k, o, x, y, T, st)
+                e1.record(st)
+                e1.synchronize()
+                ms = e0.elapsed_ms(e1) / steps
+                tf = workloads.flops_linear(T, k, o) / (ms * 1e-3) / 1e12
+                per[name] = {"in": k, "out": o, "us": round(ms * 1e3, 2),
+                             "TFLOPs": round(tf, 2), "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+            e0, e1 = mlk.Event(), mlk.Event()
+            e0.record(st)
+            for i in range(steps):
+                for name, k, o in shapes:
+                    layers.launch(i, name, k, o, x, y, T, st)
+            e1.record(st)
+            e1.synchronize()
+            ms = e0.elapsed_ms(e1) / steps
+            fl = sum(workloads.flops_linear(T, k, o) for _, k, o in shapes)
+            tf = fl / (ms * 1e-3) / 1e12
+            res[str(T)] = {"layer_us": round(ms * 1e3, 2), "layer_flops": fl,
+                           "layer_TFLOPs": round(tf, 2),
+                           "layer_frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "ops": per}
+            print(f"gemm {qt} T={T}: layer {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s "
+                  f"({100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}%) "
+                  + " ".join(f"{n}={v['TFLOPs']}" for n, v in per.items()), flush=True)
         out[qt] = res
         del layers
     with open(path, "w") as f:
@@ -709,18 +779,26 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
             row += " %s |" % (("%.0f" % ((fk[0] / ff + wk[0] / wf) * 1024)) if fk and wk else "n/a")
         md.append(row)
     md += ["", "Results of the same command (bench.py JSON, events around back-to-back "
-           "launches on rotating cold copies):", "",
-           "| case | us | algorithmic GB/s | fraction of 8 TB/s |", "|---|---|---|---|"]
+           "launches; HBM-bound cases on rotating cold copies, against 8 TB/s; "
+           "matrix-core cases against the 157.3 TFLOP/s fp32 MFMA peak):", "",
+           "| case | us | throughput | fraction of peak |", "|---|---|---|---|"]
+
+    def rate(node, prefix=""):
+        if prefix + "GBps" in node:
+            return "%.1f GB/s" % node[prefix + "GBps"]
+        return "%.2f TFLOP/s" % node[prefix + "TFLOPs"]
 
     def walk(node, path):
         if isinstance(node, dict):
-            if "us" in node and "GBps" in node:
-                md.append("| %s | %.2f | %.1f | %.3f |" % (" / ".join(path), node["us"],
-                                                           node["GBps"], node["frac_of_peak"]))
+            # matrix-core results: per projection only at the largest row count
+            if "us" in node and ("GBps" in node or
+                                 ("TFLOPs" in node and str(max(GEMM_TOKENS)) in path)):
+                md.append("| %s | %.2f | %s | %.3f |" % (" / ".join(path), node["us"], rate(node),
+                                                         node["frac_of_peak"]))
             if "layer_us" in node:
-                md.append("| %s | %.2f | %.1f | %.3f |" % (" / ".join(path + ["layer"]),
-                                                           node["layer_us"], node["layer_GBps"],
-                                                           node["layer_frac_of_peak"]))
+                md.append("| %s | %.2f | %s | %.3f |" % (" / ".join(path + ["layer"]),
+                                                         node["layer_us"], rate(node, "layer_"),
+                                                         node["layer_frac_of_peak"]))
             for k, v in node.items():
                 if k not in ("ops",) or isinstance(v, dict):
                     walk(v, path + ([k] if k not in ("ops", "cases") else []))
@@ -754,6 +832,9 @@ def main():
         return
     if args.attention:
         attention_bench(mlk, args.steps, workloads.HBM_PEAK_GBS, args.attention)
+        return
+    if args.gemm:
+        gemm_bench(mlk, args.steps, args.gemm)
         return
     peak = workloads.HBM_PEAK_GBS
     cfg = workloads.CONFIGS["c3_prefill_8b"]

@@ -67,8 +67,8 @@ _SIGNATURES = {
     "mlk_gather_f32": [_vp, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _vp],
     "mlk_gather_quant": [_i32, _vp, _i64, _i64, _vp, _i32, _i64, _vp, _vp, _vp],
     "mlk_quantize": [_i32, _vp, _i64, _i64, _vp, _vp],
-    "mlk_linear_quant": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
-    "mlk_linear_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "mlk_linear_quant": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, C.c_size_t, _vp],
+    "mlk_linear_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, C.c_size_t, _vp],
     "mlk_matmul_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "mlk_fill_normal_f32": [_vp, _i64, _f, _f, C.c_uint64, _vp],
     "mlk_kv_write_f32": [_vp, _vp, _i64, _i64, _i32, _i32, _i64, _vp, _i64, _vp, _i64, _vp, _i32,
@@ -120,6 +120,8 @@ def _load():
     lib.mlk_quant_bytes.argtypes = [_i32, _i64, _i64]
     lib.mlk_attention_workspace_bytes.restype = C.c_int64
     lib.mlk_attention_workspace_bytes.argtypes = [_i64, _i32, _i32, _i32, _i64]
+    lib.mlk_linear_workspace_bytes.restype = C.c_int64
+    lib.mlk_linear_workspace_bytes.argtypes = [_i64, _i64, _i64]
     return lib
 
 
@@ -138,7 +140,8 @@ def exported_symbols():
     """Names of every C ABI function the binding binds (used by the CPU tests)."""
     return sorted(list(_SIGNATURES) + ["mlk_last_error", "mlk_status_string",
                                        "mlk_abi_version", "mlk_quant_bytes",
-                                       "mlk_attention_workspace_bytes"])
+                                       "mlk_attention_workspace_bytes",
+                                       "mlk_linear_workspace_bytes"])
 
 
 # ------------------------------------------------------------------ runtime
@@ -393,17 +396,53 @@ def quantize(qtype, x, rows, cols, blocks, stream=None):
           "mlk_quantize")
 
 
+def linear_workspace_bytes(rows, in_features, out_features):
+    """Bytes of the optional split-K workspace of a linear call (0: none used)."""
+    return int(lib.mlk_linear_workspace_bytes(rows, in_features, out_features))
+
+
+_linear_ws = {}  # device id -> DeviceBuffer grown to the largest request
+
+
+def _workspace(workspace, rows, in_features, out_features):
+    """(pointer, bytes) for a linear call: workspace is None (no split), a
+    DeviceBuffer, or "auto" (a per-device buffer kept by this module and grown
+    when a call needs more; growing frees the old one, which waits for the
+    device, so do not use "auto" under graph capture)."""
+    if workspace is None:
+        return None, 0
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError(f"workspace must be None, a DeviceBuffer or 'auto', not {workspace!r}")
+        need = linear_workspace_bytes(rows, in_features, out_features)
+        if need == 0:
+            return None, 0
+        dev = C.c_int()
+        check(lib.mlk_get_device(C.byref(dev)))
+        buf = _linear_ws.get(dev.value)
+        if buf is None or buf.nbytes < need:
+            if buf is not None:
+                buf.close()
+            buf = _linear_ws[dev.value] = DeviceBuffer(need, np.uint8)
+        return buf.ptr, buf.nbytes
+    return _p(workspace), workspace.nbytes
+
+
 def linear_quant(qtype, x, w_blocks, y, rows, in_features, out_features, bias=None,
-                 stream=None):
+                 stream=None, workspace="auto"):
     """y[rows, out] = x[rows, in] @ dequant(W)^T (+ bias)."""
+    ws, ws_bytes = _workspace(workspace, rows, in_features, out_features)
     check(lib.mlk_linear_quant(QUANT[qtype], _p(x), _p(w_blocks), _p(bias), _p(y), rows,
-                               in_features, out_features, _sp(stream)), "mlk_linear_quant")
+                               in_features, out_features, ws, ws_bytes, _sp(stream)),
+          "mlk_linear_quant")
 
 
-def linear_f32(x, w, y, rows, in_features, out_features, bias=None, stream=None):
+def linear_f32(x, w, y, rows, in_features, out_features, bias=None, stream=None,
+               workspace="auto"):
     """y[rows, out] = x[rows, in] @ W[out, in]^T (+ bias)."""
+    ws, ws_bytes = _workspace(workspace, rows, in_features, out_features)
     check(lib.mlk_linear_f32(_p(x), _p(w), _p(bias), _p(y), rows, in_features, out_features,
-                             _sp(stream)), "mlk_linear_f32")
+                             ws, ws_bytes, _sp(stream)), "mlk_linear_f32")
 
 
 def matmul(a, b, c, m, k, n, stream=None):

@@ -1,0 +1,383 @@
+// mlk_gemm.hip -- prefill-shaped linear layers on the matrix cores:
+// y[T, O] = x[T, K] W[O, K]^T (+ bias), W fp32 or Q8_0 / Q4_0 / Q4_1 blocks.
+//
+// Semantics are those of the GEMV kernels (mlk_linear.hip; the reference's
+// LinearQ80/Q40/Q41, src/quant.cc:393-463, and cublasSgemm for F32,
+// src/cuda_matmul.cc:142-186): every product is x * dequant(w) in fp32 and
+// the sum is fp32, in an order of this kernel's choosing, within
+// gamma_K * sum_k |x w| of the exact value.  Dequantized weights are the
+// reference's element values: Q8_0 d * q and Q4_0 d * (code - 8) are exact
+// in fp32 (an 11-bit scale times a small integer); Q4_1 is d * code + m
+// rounded once per product and once per sum, as the reference's
+// DequantQ41 (src/quant.cc:369-391).
+//
+// Work layout (one workgroup = 256 threads = 4 waves per BM x 128 tile of
+// y, BM = 128 token rows, or 64 / 32 when T is that small; each wave owns
+// a BM/2 x 64 quarter as BM/32 x 4 tiles of v_mfma_f32_16x16x4_f32, up to
+// 64 accumulators per lane):
+//   - K advances in stages of 32 (one quantization block).  A stage's
+//     x tile [BM tokens][32] and weight tile [128 outputs][32] are staged
+//     through LDS as fp32, rows 36 floats apart (16-byte aligned rows, and
+//     the b128 reads of 8 consecutive lanes fall on all 32 banks);
+//     quantized weights are decoded on the way in, so the matrix cores only
+//     ever see fp32.
+//   - Two LDS buffers: stage s+1's global loads are issued before stage
+//     s's MFMAs and written to the other buffer after them, with one
+//     barrier per stage.
+//   - MFMA operands: lane l supplies row l % 16 and k-slot l / 16.  The
+//     four k-slots of one instruction are taken 4 apart (k = 4 * (l / 16) +
+//     s for step s), so each lane's four consecutive k values come from one
+//     16-byte LDS read and feed four instructions; x and W use the same
+//     assignment, so every product x[t, k] * w[o, k] is formed exactly once.
+//   - Output: lane l, register r of a 16 x 16 tile holds row 4 * (l / 16) +
+//     r, column l % 16; bias is added to the finished sum.
+// Tiles past T or O load zeros (clamped addresses, masked values) and store
+// nothing.  When the tiles are fewer than two per CU (few token rows), K is
+// split over up to 32 workgroups per tile (each split at least 8 stages);
+// the splits write partial sums to a caller-provided workspace and a second
+// kernel adds them in split order (deterministic) plus the bias.
+// FLOPs per call: 2 T O K.
+#include "mlk_quant.h"
+
+namespace mlk {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBN = 128;         // outputs per tile (token rows per tile: BM = 32, 64 or 128)
+constexpr int kBK = 32;          // K per stage: one quantization block
+constexpr int kLd = kBK + 4;     // LDS row stride, floats
+constexpr int kGemmThreads = 256;
+constexpr int kWF32 = -1;        // weight type value of fp32 weights
+
+template <int BM>
+struct GemmSmem {
+    float x[2][BM * kLd];
+    float w[2][kBN * kLd];
+};
+
+__device__ inline float4 Mask4(float4 v, uint32_t m) {
+    return make_float4(__uint_as_float(__float_as_uint(v.x) & m),
+                       __uint_as_float(__float_as_uint(v.y) & m),
+                       __uint_as_float(__float_as_uint(v.z) & m),
+                       __uint_as_float(__float_as_uint(v.w) & m));
+}
+
+// An [R][32] fp32 tile of a row-major [rows, K] matrix (x, or fp32 W):
+// thread tid loads float4 (tid + 256 i) for i < R / 32, 8 per row, so 8
+// consecutive lanes read one row's 128 contiguous bytes.  Rows past `rows`
+// read row 0 and are zeroed.
+template <int R>
+struct F32Tile {
+    static constexpr int kN = R / 32;
+    float4 v[kN];
+    __device__ void Load(const float* p, int64_t rows, int64_t K, int64_t r0, int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kGemmThreads * i;
+            const int64_t r = r0 + (idx >> 3);
+            const int64_t c = k0 + 4 * (idx & 7);
+            const bool ok = r < rows && c < K;
+            v[i] = Mask4(*reinterpret_cast<const float4*>(p + (ok ? r * K + c : 0)),
+                         ok ? ~0u : 0u);
+        }
+    }
+    __device__ void Store(float* s) const {
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kGemmThreads * i;
+            *reinterpret_cast<float4*>(s + (idx >> 3) * kLd + 4 * (idx & 7)) = v[i];
+        }
+    }
+};
+
+// A [128 outputs][32] tile of one block column of quantized W: thread tid
+// decodes half tid & 1 (16 elements) of output row tid >> 1.  Rows past O
+// read row 0 and are zeroed.
+template <int QT>
+struct QuantTile {
+    uint32_t d;        // Q8_0 / Q4_0: the fp16 scale; Q4_1: d | m << 16
+    uint32_t q[4];     // the 16 code bytes this thread needs
+    uint32_t keep;     // ~0 when the row exists
+    __device__ void Load(const uint8_t* w, int64_t O, int64_t row_bytes, int64_t n0, int64_t kb) {
+        const int64_t n = n0 + (threadIdx.x >> 1);
+        const int h = threadIdx.x & 1;
+        keep = n < O ? ~0u : 0u;
+        const uint8_t* blk = w + (n < O ? n : 0) * row_bytes + kb * Fmt<QT>::kBytes;
+        if constexpr (QT == MLK_Q4_1) {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(blk);
+            d = p[0];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = p[1 + i];
+        } else {
+            // Q8_0: codes 16h .. 16h+15 at byte 2 + 16h; Q4_0: all 16 code
+            // bytes at byte 2 (half h takes the low or high nibbles)
+            const uint16_t* p = reinterpret_cast<const uint16_t*>(blk);
+            d = p[0];
+            const int o = QT == MLK_Q8_0 ? 1 + 8 * h : 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = p[o + 2 * i] | (static_cast<uint32_t>(p[o + 2 * i + 1]) << 16);
+        }
+    }
+    __device__ void Store(float* s) const {
+        const int h = threadIdx.x & 1;
+        float* dst = s + (threadIdx.x >> 1) * kLd + 16 * h;
+        float e[16];
+        if constexpr (QT == MLK_Q8_0) {
+            const float sc = HalfHw(d & 0xFFFFu);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int32_t code = static_cast<int32_t>(q[i / 4] << (24 - 8 * (i % 4))) >> 24;
+                e[i] = sc * static_cast<float>(code);
+            }
+        } else if constexpr (QT == MLK_Q4_0) {
+            const float sc = HalfHw(d & 0xFFFFu);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t byte = (q[i / 4] >> (8 * (i % 4))) & 0xFFu;
+                const int code = static_cast<int>(h ? byte >> 4 : byte & 15u);
+                e[i] = sc * static_cast<float>(code - 8);
+            }
+        } else {
+            const float sc = HalfHw(d & 0xFFFFu);
+            const float mn = HalfHw(d >> 16);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t byte = (q[i / 4] >> (8 * (i % 4))) & 0xFFu;
+                const float code = static_cast<float>(h ? byte >> 4 : byte & 15u);
+                e[i] = __fadd_rn(__fmul_rn(sc, code), mn);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *reinterpret_cast<float4*>(dst + 4 * i) =
+                Mask4(make_float4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3]), keep);
+        }
+    }
+};
+
+template <int WT>
+struct WTile : QuantTile<WT> {
+    __device__ void Load(const uint8_t* w, int64_t O, int64_t, int64_t row_bytes, int64_t n0,
+                         int64_t k0) {
+        QuantTile<WT>::Load(w, O, row_bytes, n0, k0 / kBK);
+    }
+};
+template <>
+struct WTile<kWF32> : F32Tile<kBN> {
+    __device__ void Load(const uint8_t* w, int64_t O, int64_t K, int64_t, int64_t n0, int64_t k0) {
+        F32Tile<kBN>::Load(reinterpret_cast<const float*>(w), O, K, n0, k0);
+    }
+};
+
+// Workgroup (tile, split): split `sp` covers K stages [sp * per_split,
+// min((sp + 1) * per_split, all)); with one split it writes y (+ bias),
+// with more it writes its partial sums to partial[sp] ([T, O] each) for
+// SplitKReduce.  A tile is BM token rows x 128 outputs; wave w owns rows
+// (w / 2) * BM / 2 .. + BM / 2 and outputs (w % 2) * 64 .. + 64, i.e.
+// MI = BM / 32 by 4 MFMA tiles.
+template <int WT, int BM>
+__global__ __launch_bounds__(kGemmThreads) void GemmMfma(const float* __restrict__ x,
+                                                         const uint8_t* __restrict__ w,
+                                                         const float* __restrict__ bias,
+                                                         float* __restrict__ y, int64_t T,
+                                                         int64_t K, int64_t O, int64_t row_bytes,
+                                                         int tiles_m, int tiles,
+                                                         int64_t per_split,
+                                                         float* __restrict__ partial) {
+    constexpr int MI = BM / 32;
+    __shared__ GemmSmem<BM> sm;
+    const int tile = static_cast<int>(blockIdx.x) % tiles;
+    const int sp = static_cast<int>(blockIdx.x) / tiles;
+    const int tm = tile % tiles_m;
+    const int tn = tile / tiles_m;
+    const int64_t m0 = static_cast<int64_t>(tm) * BM;
+    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int i16 = lane & 15, kq = lane >> 4;
+
+    f32x4 acc[MI][4];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int64_t all_stages = (K + kBK - 1) / kBK;
+    const int64_t s0 = sp * per_split;
+    const int64_t s1 = s0 + per_split < all_stages ? s0 + per_split : all_stages;
+    F32Tile<BM> xt;
+    WTile<WT> wt;
+    xt.Load(x, T, K, m0, s0 * kBK);
+    wt.Load(w, O, K, row_bytes, n0, s0 * kBK);
+    xt.Store(sm.x[0]);
+    wt.Store(sm.w[0]);
+    __syncthreads();
+    for (int64_t s = s0; s < s1; ++s) {
+        const int buf = static_cast<int>((s - s0) & 1);
+        // next stage's loads (the last stage reloads itself: no branch around
+        // the loads, and the write below goes to a buffer no one reads again)
+        const int64_t k_next = (s + 1 < s1 ? s + 1 : s) * kBK;
+        xt.Load(x, T, K, m0, k_next);
+        wt.Load(w, O, K, row_bytes, n0, k_next);
+        const float* xs = sm.x[buf] + (wm * (BM / 2) + i16) * kLd + 4 * kq;
+        const float* ws = sm.w[buf] + (wn * 64 + i16) * kLd + 4 * kq;
+#pragma unroll
+        for (int kk = 0; kk < kBK; kk += 16) {
+            f32x4 a[MI], b[4];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) a[i] = *reinterpret_cast<const f32x4*>(xs + 16 * i * kLd + kk);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const f32x4*>(ws + 16 * j * kLd + kk);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+#pragma unroll
+                for (int i = 0; i < MI; ++i) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][st], b[j][st],
+                                                                         acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        xt.Store(sm.x[buf ^ 1]);
+        wt.Store(sm.w[buf ^ 1]);
+        __syncthreads();
+    }
+
+    float* out = partial != nullptr ? partial + sp * T * O : y;
+    const float* add = partial != nullptr ? nullptr : bias;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t col = n0 + wn * 64 + 16 * j + i16;
+        if (col >= O) continue;
+        const float b = add != nullptr ? add[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm * (BM / 2) + 16 * i + 4 * kq + r;
+                if (row < T) out[row * O + col] = acc[i][j][r] + b;
+            }
+        }
+    }
+}
+
+// y = sum of the splits' partial sums, in split order, + bias.
+__global__ __launch_bounds__(kGemmThreads) void SplitKReduce(const float* __restrict__ partial,
+                                                             int splits,
+                                                             const float* __restrict__ bias,
+                                                             float* __restrict__ y, int64_t T,
+                                                             int64_t O) {
+    const int64_t n = T * O;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        float v = partial[i];
+        for (int sp = 1; sp < splits; ++sp) v += partial[sp * n + i];
+        y[i] = bias != nullptr ? v + bias[i % O] : v;
+    }
+}
+
+// K splits for a T x O x K product: doubled while the grid holds fewer than
+// two workgroups per CU and every split keeps at least 8 stages (K >= 256).
+struct SplitPlan {
+    int splits = 1;
+    int64_t per_split = 0;
+};
+
+// Token rows per tile: the smallest of 32, 64, 128 that covers T, 128 beyond.
+int TileRows(int64_t T) { return T <= 32 ? 32 : (T <= 64 ? 64 : 128); }
+
+SplitPlan PlanSplits(int64_t T, int64_t K, int64_t O) {
+    const int bm = TileRows(T);
+    const int64_t tiles = ((T + bm - 1) / bm) * ((O + kBN - 1) / kBN);
+    const int64_t stages = (K + kBK - 1) / kBK;
+    const int64_t target = 2 * static_cast<int64_t>(ComputeUnits());
+    int64_t sp = 1;
+    while (tiles * sp < target && stages / (2 * sp) >= 8 && sp < 32) sp *= 2;
+    SplitPlan p;
+    p.per_split = (stages + sp - 1) / sp;
+    p.splits = static_cast<int>((stages + p.per_split - 1) / p.per_split);
+    return p;
+}
+
+template <int BM>
+void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
+                 const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
+                 int tiles_m, int tiles, int64_t per_split, float* partial) {
+    switch (wt) {
+        case MLK_Q8_0:
+            hipLaunchKernelGGL((GemmMfma<MLK_Q8_0, BM>), grid, dim3(kGemmThreads), 0, s, x, w,
+                               bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        case MLK_Q4_0:
+            hipLaunchKernelGGL((GemmMfma<MLK_Q4_0, BM>), grid, dim3(kGemmThreads), 0, s, x, w,
+                               bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        case MLK_Q4_1:
+            hipLaunchKernelGGL((GemmMfma<MLK_Q4_1, BM>), grid, dim3(kGemmThreads), 0, s, x, w,
+                               bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        default:
+            hipLaunchKernelGGL((GemmMfma<kWF32, BM>), grid, dim3(kGemmThreads), 0, s, x, w, bias,
+                               y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+    }
+}
+
+}  // namespace
+
+int64_t GemmWorkspaceBytes(int64_t T, int64_t K, int64_t O) {
+    const SplitPlan p = PlanSplits(T, K, O);
+    return p.splits > 1 ? static_cast<int64_t>(p.splits) * T * O * 4 : 0;
+}
+
+// Launches GemmMfma for a shape the caller has validated: K % 4 == 0 and
+// x / fp32 W 16-byte aligned; for quantized W, K % 32 == 0 and W aligned to
+// its loads (2 bytes, 4 for Q4_1).  K is split over workgroups when the
+// workspace holds GemmWorkspaceBytes(T, K, O) bytes, else not.
+mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, float* y,
+                      int64_t T, int64_t K, int64_t O, int64_t row_bytes, void* workspace,
+                      size_t workspace_bytes, hipStream_t s) {
+    const int bm = TileRows(T);
+    const int64_t tiles_m = (T + bm - 1) / bm;
+    const int64_t tiles_n = (O + kBN - 1) / kBN;
+    const int64_t stages = (K + kBK - 1) / kBK;
+    SplitPlan plan = PlanSplits(T, K, O);
+    float* partial = nullptr;
+    if (plan.splits > 1 && workspace != nullptr &&
+        workspace_bytes >= static_cast<size_t>(plan.splits) * T * O * 4 && Aligned(workspace, 16)) {
+        partial = static_cast<float*>(workspace);
+    } else {
+        plan.splits = 1;
+        plan.per_split = stages;
+    }
+    if (tiles_m * tiles_n * plan.splits > 0x7FFFFFFF || tiles_m > 0x7FFFFFFF) {
+        return Fail(MLK_ERR_INVALID, "linear: %lld x %lld tiles exceed one launch",
+                    static_cast<long long>(tiles_m), static_cast<long long>(tiles_n));
+    }
+    const int tiles = static_cast<int>(tiles_m * tiles_n);
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(tiles) * plan.splits));
+    const uint8_t* wb = static_cast<const uint8_t*>(w);
+    const int tm = static_cast<int>(tiles_m);
+    if (bm == 32) {
+        LaunchTiles<32>(wt, grid, s, x, wb, bias, y, T, K, O, row_bytes, tm, tiles, plan.per_split,
+                        partial);
+    } else if (bm == 64) {
+        LaunchTiles<64>(wt, grid, s, x, wb, bias, y, T, K, O, row_bytes, tm, tiles, plan.per_split,
+                        partial);
+    } else {
+        LaunchTiles<128>(wt, grid, s, x, wb, bias, y, T, K, O, row_bytes, tm, tiles,
+                         plan.per_split, partial);
+    }
+    mlk_status st = CheckLaunch("GemmMfma");
+    if (st != MLK_OK || partial == nullptr) return st;
+    hipLaunchKernelGGL(SplitKReduce, dim3(GridFor(T * O, kGemmThreads, 8)), dim3(kGemmThreads), 0,
+                       s, partial, plan.splits, bias, y, T, O);
+    return CheckLaunch("SplitKReduce");
+}
+
+}  // namespace mlk

@@ -53,6 +53,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWavesPerBlock = kThreads / kWave;
 constexpr int kMaxTok = 4;    // token rows per GEMV launch
+constexpr int kGemmMinRows = 8;  // from here on, the matrix-core GEMM (mlk_gemm.hip)
 constexpr int kF32 = -1;      // QT value of F32 weights
 
 __device__ inline float WaveSumF(float v) {
@@ -496,9 +497,15 @@ using namespace mlk;
 
 extern "C" {
 
+int64_t mlk_linear_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features) {
+    if (rows < kGemmMinRows || rows <= 0 || in_features <= 0 || out_features <= 0) return 0;
+    return GemmWorkspaceBytes(rows, in_features, out_features);
+}
+
 mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_blocks,
                             const float* bias, float* y, int64_t rows, int64_t in_features,
-                            int64_t out_features, void* stream) {
+                            int64_t out_features, void* workspace, size_t workspace_bytes,
+                            void* stream) {
     if (quant_type < MLK_Q8_0 || quant_type > MLK_Q4_1) {
         return Fail(MLK_ERR_INVALID, "mlk_linear_quant: unknown quantization type %d", quant_type);
     }
@@ -532,6 +539,10 @@ mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_bl
         }
         return CheckLaunch("GemvAnyKernel");
     }
+    if (rows >= kGemmMinRows) {
+        return LaunchGemm(quant_type, x, w_blocks, bias, y, rows, K, O, row_bytes, workspace,
+                          workspace_bytes, s);
+    }
     const int64_t nb = K / 32;
     switch (quant_type) {
         case MLK_Q8_0: return Gemv<MLK_Q8_0>(x, w, bias, y, K, O, row_bytes, nb, rows, s);
@@ -541,7 +552,8 @@ mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_bl
 }
 
 mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, float* y,
-                          int64_t rows, int64_t in_features, int64_t out_features, void* stream) {
+                          int64_t rows, int64_t in_features, int64_t out_features,
+                          void* workspace, size_t workspace_bytes, void* stream) {
     mlk_status st = CheckLinear("mlk_linear_f32", x, w, y, rows, in_features, out_features);
     if (st != MLK_OK) return st;
     if (!Aligned(w, 4)) {
@@ -553,6 +565,9 @@ mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, flo
         hipLaunchKernelGGL(GemvAnyKernel<kF32>, dim3(FullGrid(O, kWavesPerBlock)), dim3(kThreads), 0,
                            s, x, static_cast<const void*>(w), bias, y, K, O, K * 4, rows);
         return CheckLaunch("GemvAnyKernel");
+    }
+    if (rows >= kGemmMinRows) {
+        return LaunchGemm(kF32, x, w, bias, y, rows, K, O, K * 4, workspace, workspace_bytes, s);
     }
     return Gemv<kF32>(x, reinterpret_cast<const uint8_t*>(w), bias, y, K, O, K * 4, K / 4, rows,
                       s);

@@ -7,6 +7,7 @@
 // kernel, download y and add the bias on the host.
 #include "include/cuda_matmul.h"
 #include "include/minilamma_hip.h"
+#include "linear_workspace.h"
 
 #include <cstdint>
 #include <stdexcept>
@@ -72,9 +73,11 @@ Tensor LinearHostX(const Tensor& x, const void* w_data, const std::vector<int>& 
     CudaDeviceBuffer xb(x.GetDataSize() * sizeof(float), device_id);
     CudaDeviceBuffer yb(static_cast<size_t>(rows) * out * sizeof(float), device_id);
     xb.upload(x.data.data(), x.GetDataSize() * sizeof(float));
+    CudaDeviceBuffer ws = LinearWorkspace(rows, in, out, device_id);
     Launched(mlk_linear_f32(static_cast<const float*>(xb.GetData()),
                             static_cast<const float*>(w_data), nullptr,
-                            static_cast<float*>(yb.GetData()), rows, in, out, nullptr),
+                            static_cast<float*>(yb.GetData()), rows, in, out, ws.GetData(),
+                            ws.GetByteSize(), nullptr),
              caller);
     Tensor y(OutShape(x.shape, out));
     yb.download(y.data.data(), y.GetDataSize() * sizeof(float));
@@ -137,10 +140,11 @@ CudaTensor CudaLinearDevice(const CudaTensor& x, const void* w_data,
     const int rows = x.num_dims() == 1 ? 1 : x.shape()[0];
     SetCudaService(device_id);
     CudaTensor y(OutShape(x.shape(), w_shape[0]), device_id);
+    CudaDeviceBuffer ws = LinearWorkspace(rows, w_shape[1], w_shape[0], device_id);
     Launched(mlk_linear_f32(static_cast<const float*>(x.GetData()),
                             static_cast<const float*>(w_data), nullptr,
                             static_cast<float*>(y.GetData()), rows, w_shape[1], w_shape[0],
-                            nullptr),
+                            ws.GetData(), ws.GetByteSize(), nullptr),
              caller);
     return y;
 }

@@ -8,6 +8,7 @@
 // after the download, as the reference does.
 #include "include/cuda_quant.h"
 #include "include/minilamma_hip.h"
+#include "linear_workspace.h"
 
 #include <cstdint>
 #include <stdexcept>
@@ -77,8 +78,10 @@ Tensor DeviceWeightHostX(int32_t qt, const std::string& caller, const Tensor& x,
     CudaDeviceBuffer xb(x.GetDataSize() * sizeof(float), device_id);
     CudaDeviceBuffer yb(static_cast<size_t>(rows) * out * sizeof(float), device_id);
     xb.upload(x.data.data(), x.GetDataSize() * sizeof(float));
+    CudaDeviceBuffer ws = LinearWorkspace(rows, shape[1], out, device_id);
     Launched(mlk_linear_quant(qt, static_cast<const float*>(xb.GetData()), device_weight, nullptr,
-                              static_cast<float*>(yb.GetData()), rows, shape[1], out, nullptr),
+                              static_cast<float*>(yb.GetData()), rows, shape[1], out,
+                              ws.GetData(), ws.GetByteSize(), nullptr),
              caller.c_str());
     Tensor y(OutShape(x.shape, out));
     yb.download(y.data.data(), y.GetDataSize() * sizeof(float));
@@ -102,8 +105,10 @@ CudaTensor DeviceWeightDeviceX(int32_t qt, const std::string& caller, const Cuda
     const int rows = x.num_dims() == 1 ? 1 : x.shape()[0];
     SetCudaService(device_id);
     CudaTensor y(OutShape(x.shape(), shape[0]), device_id);
+    CudaDeviceBuffer ws = LinearWorkspace(rows, shape[1], shape[0], device_id);
     Launched(mlk_linear_quant(qt, static_cast<const float*>(x.GetData()), device_weight, nullptr,
-                              static_cast<float*>(y.GetData()), rows, shape[1], shape[0], nullptr),
+                              static_cast<float*>(y.GetData()), rows, shape[1], shape[0],
+                              ws.GetData(), ws.GetByteSize(), nullptr),
              caller.c_str());
     return y;
 }

@@ -152,18 +152,32 @@ int64_t mlk_quant_bytes(int32_t quant_type, int64_t rows, int64_t cols);
  * fp32; bias may be NULL and is added to the finished sum.  The sum is fp32
  * in an order of the kernel's choosing: within gamma_K * sum_k |x w| of the
  * exact value, like the reference's serial loop.  y may not alias x or W.
+ * workspace / workspace_bytes: optional scratch for splitting K (see
+ * mlk_linear_workspace_bytes; NULL, 0 is always valid).
  * Replaces CudaQ40/Q41/Q80DeviceInputLinear (include/cuda_quant.h:12-25;
  * kernels src/cuda_quant.cu:29-97, one thread per output).
  */
 mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_blocks,
                             const float* bias, float* y, int64_t rows, int64_t in_features,
-                            int64_t out_features, void* stream);
+                            int64_t out_features, void* workspace, size_t workspace_bytes,
+                            void* stream);
 
 /* The same with an fp32 weight W [out_features, in_features] row-major.
  * Replaces CudaLinearDevice (include/cuda_matmul.h:16-18; cublasSgemm,
  * src/cuda_matmul.cc:155-189). */
 mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, float* y,
-                          int64_t rows, int64_t in_features, int64_t out_features, void* stream);
+                          int64_t rows, int64_t in_features, int64_t out_features,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device bytes of the optional workspace of mlk_linear_quant / mlk_linear_f32
+ * for this shape on the current device (0: the call uses none).  Calls of
+ * 32 rows or more run on the matrix cores in 128 x 128 output tiles; when
+ * those tiles are fewer than two per compute unit, a workspace of this size
+ * (16-byte aligned, not aliasing x, W or y) lets the call split K over
+ * workgroups and add the partial sums in a fixed order.  Without it (NULL or
+ * smaller) the call is still correct, only slower.  No counterpart in the
+ * reference (cuBLAS keeps its own workspace). */
+int64_t mlk_linear_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features);
 
 /* c = a @ b for row-major a [m, k], b [k, n], c [m, n].  Replaces CudaMatmul
  * (include/cuda_matmul.h:7; src/cuda_matmul.cc:199-232). */

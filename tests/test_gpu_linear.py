@@ -25,14 +25,14 @@ def normal(rng, shape, std=1.0):
     return (rng.standard_normal(shape) * std).astype(np.float32)
 
 
-def run_quant(mlk, qt, x, blocks, out_f, bias=None):
+def run_quant(mlk, qt, x, blocks, out_f, bias=None, workspace="auto"):
     x = np.atleast_2d(np.ascontiguousarray(x, np.float32))
     T, K = x.shape
     d_x = mlk.DeviceBuffer.from_array(x)
     d_w = mlk.DeviceBuffer.from_array(np.ascontiguousarray(blocks, np.uint8))
     d_b = None if bias is None else mlk.DeviceBuffer.from_array(np.asarray(bias, np.float32))
     d_y = mlk.DeviceBuffer.empty((T, out_f))
-    mlk.linear_quant(qt, d_x, d_w, d_y, T, K, out_f, bias=d_b)
+    mlk.linear_quant(qt, d_x, d_w, d_y, T, K, out_f, bias=d_b, workspace=workspace)
     return d_y.download()
 
 
@@ -76,8 +76,8 @@ def test_quant_linear_reference_patterns(mlk, orc):
 def test_quant_linear_shapes(mlk, orc, qt, shape):
     """The split-K path: whole and partial last spans (in % 256 and % 512 !=
     0, masked per lane), partial last workgroups of 2 and 4 rows (out odd,
-    out around 4096 where the rows per workgroup change), token counts 1..9
-    (launches of up to 4 rows)."""
+    out around 4096 where the rows per workgroup change), token counts 1..7
+    (launches of up to 4 rows); 9 rows take the GEMM."""
     O, K, T = shape
     rng = np.random.default_rng(O * 7 + K + T)
     w = normal(rng, (O, K), 0.02)
@@ -89,6 +89,76 @@ def test_quant_linear_shapes(mlk, orc, qt, shape):
     assert_dot_close(got, ex, s, K + 1, f"{qt} {shape}")
     # the compiled reference's (oracle's) own result meets the same bound
     assert_dot_close(orc.linear_quant(qt, x, blocks, O, bias=bias), ex, s, K + 1, "oracle")
+
+
+GEMM_SHAPES = [  # (out, in, rows): 8 rows and more take the matrix-core GEMM
+    (4096, 4096, 128), (1024, 4096, 200), (131, 64, 32), (4097, 96, 33), (300, 4128, 257),
+    (14336, 4096, 64), (4096, 14336, 96), (4096, 4096, 1024)]
+
+
+@pytest.mark.parametrize("wt", QT + ("f32",))
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_linear_gemm_shapes(mlk, orc, wt, shape):
+    """The GEMM path: whole and partial 128-row / 128-output tiles (rows 32,
+    33, 200, 257; outputs 131, 300, 4097), one to 448 K stages of 32 (in
+    4128 = 129 stages: an odd count, so the last stage reads the second LDS
+    buffer), the layer's projection shapes, bias.  Each shape runs with the
+    split-K workspace (when the shape uses one: splits of whole stages, the
+    last one shorter at in = 4128) and without it."""
+    O, K, T = shape
+    rng = np.random.default_rng(O * 3 + K + T)
+    w = normal(rng, (O, K), 0.02)
+    x = normal(rng, (T, K))
+    bias = normal(rng, (O,), 0.1)
+    ws_bytes = mlk.linear_workspace_bytes(T, K, O)
+    outs = []
+    for workspace in ("auto", None):
+        if wt == "f32":
+            ex, s = dot_exact(x, w, bias)
+            got = run_f32(mlk, x, w, bias, workspace=workspace)
+        else:
+            blocks = orc.quantize(wt, w)
+            ex, s = dot_exact(x, orc.dequantize(wt, blocks, O, K), bias)
+            got = run_quant(mlk, wt, x, blocks, O, bias=bias, workspace=workspace)
+        assert_dot_close(got, ex, s, K + 1, f"{wt} {shape} workspace={workspace}")
+        rel = np.abs(got - ex) / s
+        print(f"gemm {wt} {shape} workspace={workspace} ({ws_bytes} B): "
+              f"max |err| / sum|terms| = {float(rel.max()):.2e}")
+        outs.append(got)
+    if ws_bytes == 0:  # no split: the same kernel, the same order
+        np.testing.assert_array_equal(outs[0], outs[1])
+
+
+def test_linear_workspace_sizes(mlk):
+    """The split-K workspace: none below 8 rows (GEMV) or when the tiles
+    already fill the GPU, splits * rows * out * 4 bytes otherwise; a
+    workspace smaller than asked for is ignored (no split), not overrun."""
+    assert mlk.linear_workspace_bytes(7, 4096, 4096) == 0
+    assert mlk.linear_workspace_bytes(8, 4096, 4096) > 0
+    assert mlk.linear_workspace_bytes(4096, 4096, 4096) == 0  # 1024 tiles
+    b = mlk.linear_workspace_bytes(128, 4096, 4096)
+    assert b > 0 and b % (128 * 4096 * 4) == 0
+    rng = np.random.default_rng(9)
+    O, K, T = 1024, 4096, 64
+    w = normal(rng, (O, K), 0.02)
+    x = normal(rng, (T, K))
+    ex, s = dot_exact(x, w)
+    need = mlk.linear_workspace_bytes(T, K, O)
+    small = mlk.DeviceBuffer(need - 16, np.uint8)
+    exact = mlk.DeviceBuffer(need, np.uint8)
+    assert_dot_close(run_f32(mlk, x, w, workspace=small), ex, s, K, "workspace too small")
+    assert_dot_close(run_f32(mlk, x, w, workspace=exact), ex, s, K, "workspace of the size")
+
+
+def test_linear_gemm_f32_ragged_in(mlk):
+    """fp32 weights with in_features % 32 != 0 (the last stage is partly
+    masked) on the GEMM path."""
+    rng = np.random.default_rng(8)
+    for O, K, T in ((200, 100, 40), (129, 36, 130), (64, 4100, 64)):
+        w = normal(rng, (O, K), 0.02)
+        x = normal(rng, (T, K))
+        ex, s = dot_exact(x, w)
+        assert_dot_close(run_f32(mlk, x, w), ex, s, K, f"f32 ragged {O}x{K} T={T}")
 
 
 @pytest.mark.parametrize("qt", QT)
@@ -145,12 +215,12 @@ def test_quant_linear_chains_device_outputs(mlk, orc):
         assert_dot_close(d_y.download(), ex, s, 128, f"{qt} second layer")
 
 
-def run_f32(mlk, x, w, bias=None):
+def run_f32(mlk, x, w, bias=None, workspace="auto"):
     x = np.atleast_2d(x)
     d_y = mlk.DeviceBuffer.empty((x.shape[0], w.shape[0]))
     d_b = None if bias is None else mlk.DeviceBuffer.from_array(bias)
     mlk.linear_f32(mlk.DeviceBuffer.from_array(x), mlk.DeviceBuffer.from_array(w), d_y,
-                   x.shape[0], x.shape[1], w.shape[0], bias=d_b)
+                   x.shape[0], x.shape[1], w.shape[0], bias=d_b, workspace=workspace)
     return d_y.download()
 
 

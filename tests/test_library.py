@@ -135,7 +135,7 @@ def test_validation_happens_before_any_device_call():
     assert mlk.lib.mlk_gather_quant(9, None, 1, 1, None, 0, 1, None, None, None) == \
         mlk.MLK_ERR_INVALID
     assert b"unknown quantization type" in mlk.lib.mlk_last_error()
-    assert mlk.lib.mlk_linear_quant(3, None, None, None, None, 1, 1, 1, None) == \
+    assert mlk.lib.mlk_linear_quant(3, None, None, None, None, 1, 1, 1, None, 0, None) == \
         mlk.MLK_ERR_INVALID
 
 
