@@ -536,14 +536,16 @@ def gemm_bench(mlk, steps, path):
 # ------------------------------------------------------------ attention
 
 ATT_LAYERS = 16  # cache layers rotated per launch: 16 x 64 MB K+V at 8B, S = 8192
+PREFILL_TOKENS = (512, 4096)  # causal prompt chunks from position 0
 
 
 def attention_bench(mlk, steps, peak, path):
     """Decode attention launches over a cache of ATT_LAYERS layers (each
     launch reads another layer, so a pass over the rotation exceeds the
     MALL), timed between two events on the stream they run on."""
-    out = {"workload": "decode attention over a device KV cache, N(0, 0.02) cache and queries",
-           "peak_GBps": peak}
+    out = {"workload": "decode attention over a device KV cache (and causal prefill of a "
+                       "prompt chunk), N(0, 0.02) cache and queries",
+           "peak_GBps": peak, "peak_TFLOPs": MFMA_FP32_PEAK_TFLOPS}
     st = mlk.Stream()
     S = 8192
     for name, H, KV, hd in (("llama3_8b", 32, 8, 128), ("llama3_70b", 64, 8, 128)):
@@ -584,6 +586,33 @@ def attention_bench(mlk, steps, peak, path):
             rows[case] = {"us": round(ms * 1e3, 2), "bytes": nb, "GBps": round(gbs, 1),
                           "frac_of_peak": round(gbs / peak, 4), "workspace_bytes": wsb}
             print(f"attention {name} {case}: {ms * 1e3:.2f} us, {gbs:.0f} GB/s", flush=True)
+        # causal prefill of a prompt chunk at positions 0..T-1 (matrix cores)
+        for T in PREFILL_TOKENS:
+            q = mlk.DeviceBuffer.empty((T, H * hd))
+            mlk.fill_normal(q, T * H * hd, 0.0, 0.02, 14)
+            o = mlk.DeviceBuffer.empty((T, H * hd))
+
+            def launch(i):
+                mlk.attention_prefill(q, kc, vc, ATT_LAYERS, S, H, KV, hd, i % ATT_LAYERS, 0, T,
+                                      o, stream=st)
+            for i in range(2):
+                launch(i)
+            st.synchronize()
+            n_pf = max(2, steps // 10)
+            e0, e1 = mlk.Event(), mlk.Event()
+            e0.record(st)
+            for i in range(2, 2 + n_pf):
+                launch(i)
+            e1.record(st)
+            e1.synchronize()
+            ms = e0.elapsed_ms(e1) / n_pf
+            fl = workloads.flops_prefill_attention(T, H, hd)
+            tf = fl / (ms * 1e-3) / 1e12
+            rows["prefill_T%d" % T] = {"us": round(ms * 1e3, 2), "flops": fl,
+                                       "TFLOPs": round(tf, 2),
+                                       "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+            print(f"attention {name} prefill T={T}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s "
+                  f"({100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}% of fp32 MFMA)", flush=True)
         out[name] = {"n_heads": H, "n_kv_heads": KV, "head_dim": hd, "cases": rows}
         del kc, vc
     with open(path, "w") as f:
@@ -790,9 +819,10 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
 
     def walk(node, path):
         if isinstance(node, dict):
-            # matrix-core results: per projection only at the largest row count
-            if "us" in node and ("GBps" in node or
-                                 ("TFLOPs" in node and str(max(GEMM_TOKENS)) in path)):
+            # GEMM results: per projection only at the largest row count
+            per_op_skipped = ("TFLOPs" in node and len(path) >= 2 and path[-2].isdigit()
+                              and path[-2] != str(max(GEMM_TOKENS)))
+            if "us" in node and ("GBps" in node or "TFLOPs" in node) and not per_op_skipped:
                 md.append("| %s | %.2f | %s | %.3f |" % (" / ".join(path), node["us"], rate(node),
                                                          node["frac_of_peak"]))
             if "layer_us" in node:

@@ -75,6 +75,8 @@ _SIGNATURES = {
                          _i64, _vp, _vp],
     "mlk_attention_decode_f32": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, _vp,
                                  _i32, _i64, _i64, _vp, _vp, C.c_size_t, _vp, _vp],
+    "mlk_attention_prefill_f32": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, _i32,
+                                  _i64, _vp, _vp],
     "mlk_device_count": [C.POINTER(C.c_int)],
     "mlk_set_device": [C.c_int],
     "mlk_get_device": [C.POINTER(C.c_int)],
@@ -479,6 +481,16 @@ def attention_decode(q, k_cache, v_cache, n_layers, max_seq, n_heads, n_kv_heads
                                        _p(out), _p(workspace), workspace_bytes, _p(err),
                                        _sp(stream)),
           "mlk_attention_decode_f32")
+
+
+def attention_prefill(q, k_cache, v_cache, n_layers, max_seq, n_heads, n_kv_heads, head_dim,
+                      layer, pos0, n_tokens, out, q_row_stride=None, stream=None):
+    """out [n_tokens, n_heads, head_dim]: token t (position pos0 + t) attends to
+    cache positions 0..pos0 + t of `layer` (causal prompt chunk)."""
+    check(lib.mlk_attention_prefill_f32(_p(q), q_row_stride or n_heads * head_dim, _p(k_cache),
+                                        _p(v_cache), n_layers, max_seq, n_heads, n_kv_heads,
+                                        head_dim, layer, pos0, n_tokens, _p(out), _sp(stream)),
+          "mlk_attention_prefill_f32")
 
 
 def quant_bytes(qtype, rows, cols):

@@ -1,0 +1,21 @@
+// mlk_attention.h -- the causal prefill attention kernel (mlk_prefill.hip)
+// as used by the attention entry points (mlk_attention.hip).
+#pragma once
+
+#include "mlk_common.h"
+
+namespace mlk {
+
+// The prefill kernel handles head_dim 64 and 128 with 16-byte aligned q
+// rows (q_row_stride % 4 == 0), output and caches.
+bool PrefillSupported(int32_t head_dim, const float* q, int64_t q_row_stride, const float* out,
+                      const float* k_cache, const float* v_cache);
+
+// Tokens t < T at positions pos0 + t, each attending to cache positions
+// 0 .. pos0 + t; kc / vc point at the layer's [max_seq, KV, head_dim] slice,
+// slot = KV * head_dim floats per position.  Arguments already validated.
+mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, const float* vc,
+                         int64_t slot, int32_t H, int32_t KV, int32_t head_dim, int32_t pos0,
+                         int64_t T, float* out, hipStream_t s);
+
+}  // namespace mlk

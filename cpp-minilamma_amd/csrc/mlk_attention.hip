@@ -36,7 +36,7 @@
 //     writes out; otherwise it writes (acc, max, sum) to the workspace and
 //     AttnCombine rescales and adds the chunks (max-shifted, like the
 //     reference's softmax).
-#include "mlk_common.h"
+#include "mlk_attention.h"
 
 #include <math.h>
 
@@ -47,6 +47,7 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kHalf = kWave / 2;  // lanes per position
 constexpr int kMaxHeadDim = 256;
+constexpr int64_t kPrefillMinTokens = 16;  // consecutive positions from here: AttnPrefill
 
 struct AttnParams {
     const float* q;
@@ -559,6 +560,15 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
     if (out >= q && out < q + (n_tokens - 1) * q_row_stride + static_cast<int64_t>(n_heads) * head_dim) {
         return Fail(MLK_ERR_INVALID, "%s: out must not alias q", fn);
     }
+    const int64_t slot = static_cast<int64_t>(n_kv_heads) * head_dim;
+    if (positions == nullptr && n_tokens >= kPrefillMinTokens &&
+        PrefillSupported(head_dim, q, q_row_stride, out, k_cache, v_cache)) {
+        // a prompt chunk at consecutive positions: the matrix-core prefill
+        // kernel (no workspace)
+        return LaunchPrefill(q, q_row_stride, k_cache + layer * max_seq * slot,
+                             v_cache + layer * max_seq * slot, slot, n_heads, n_kv_heads,
+                             head_dim, pos0, n_tokens, out, AsStream(stream));
+    }
     const int group = n_heads / n_kv_heads;
     const int gb = HeadsPerBlock(group);
     const int n_hblk = (group + gb - 1) / gb;
@@ -576,7 +586,6 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
         return Fail(MLK_ERR_INVALID, "%s: launch too large", fn);
     }
     AttnParams p;
-    const int64_t slot = static_cast<int64_t>(n_kv_heads) * head_dim;
     p.q = q;
     p.q_stride = q_row_stride;
     p.kc = k_cache + layer * max_seq * slot;
@@ -613,6 +622,46 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
         return CheckLaunch("AttnCombine");
     }
     return MLK_OK;
+}
+
+mlk_status mlk_attention_prefill_f32(const float* q, int64_t q_row_stride, const float* k_cache,
+                                     const float* v_cache, int64_t n_layers, int64_t max_seq,
+                                     int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                     int64_t layer, int32_t pos0, int64_t n_tokens, float* out,
+                                     void* stream) {
+    const char* fn = "mlk_attention_prefill_f32";
+    mlk_status st = CheckCache(fn, k_cache, v_cache, n_layers, max_seq, n_kv_heads, head_dim,
+                               layer);
+    if (st != MLK_OK) return st;
+    if (q == nullptr || out == nullptr) return Fail(MLK_ERR_INVALID, "%s: q and out must not be null", fn);
+    if (n_heads <= 0 || n_heads % n_kv_heads != 0) {
+        return Fail(MLK_ERR_INVALID,
+                    "%s: n_kv_heads must be non-zero and divide n_heads, got n_heads=%d, "
+                    "n_kv_heads=%d", fn, n_heads, n_kv_heads);
+    }
+    if (n_tokens <= 0 || n_tokens > 0x7FFFFFFF) {
+        return Fail(MLK_ERR_INVALID, "%s: n_tokens %lld out of range", fn,
+                    static_cast<long long>(n_tokens));
+    }
+    if (q_row_stride < static_cast<int64_t>(n_heads) * head_dim) {
+        return Fail(MLK_ERR_INVALID, "%s: q_row_stride must be at least n_heads * head_dim", fn);
+    }
+    if (pos0 < 0 || pos0 + n_tokens > max_seq) {
+        return Fail(MLK_ERR_RANGE, "%s: positions %d..%lld out of range [0, %lld)", fn, pos0,
+                    static_cast<long long>(pos0 + n_tokens - 1), static_cast<long long>(max_seq));
+    }
+    if (!PrefillSupported(head_dim, q, q_row_stride, out, k_cache, v_cache)) {
+        return Fail(MLK_ERR_INVALID,
+                    "%s: needs head_dim 64 or 128, q_row_stride %% 4 == 0 and 16-byte aligned q, "
+                    "out and caches (mlk_attention_decode_f32 takes any shape)", fn);
+    }
+    if (out >= q && out < q + (n_tokens - 1) * q_row_stride + static_cast<int64_t>(n_heads) * head_dim) {
+        return Fail(MLK_ERR_INVALID, "%s: out must not alias q", fn);
+    }
+    const int64_t slot = static_cast<int64_t>(n_kv_heads) * head_dim;
+    return LaunchPrefill(q, q_row_stride, k_cache + layer * max_seq * slot,
+                         v_cache + layer * max_seq * slot, slot, n_heads, n_kv_heads, head_dim,
+                         pos0, n_tokens, out, AsStream(stream));
 }
 
 }  // extern "C"

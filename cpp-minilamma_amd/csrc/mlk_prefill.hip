@@ -1,0 +1,222 @@
+// mlk_prefill.hip -- causal attention of a prompt chunk on the matrix cores.
+//
+// Tokens t < T sit at positions pos0 + t; token t's head h attends to cache
+// positions 0 .. pos0 + t of its KV head g = h / (H / KV) (the reference's
+// ForwardAttention per token, src/forward.cc:265-298, with the chunk's own
+// K/V rows already written to the cache):
+//   s_j = (q . k_j) * (1 / sqrt(hd)),  p = softmax(s),  out = sum_j p_j v_j
+// in fp32.  The dot products and the weighted sum run on
+// v_mfma_f32_16x16x4_f32, so their fp32 summation order differs from the
+// reference's serial loops; the result is held to the same float64 error
+// bound as the decode kernel's (every order of the fp32 sums meets it).
+//
+// Work layout: a workgroup of 4 waves owns 16 consecutive tokens and 4 query
+// heads of one KV head (wave w: head 4 * head_block + w of the group), so
+// the 4 waves share each K/V tile.  Workgroups run in reverse token order,
+// the longest prefixes first.  Per tile of 32 cache positions (staged
+// through two LDS buffers, rows hd + 4 floats apart; the next tile's global
+// loads are issued before the current tile's MFMAs):
+//   - S^T = K Q^T (16 positions x 16 queries per instruction block): K rows
+//     come from LDS, each lane's q row (query l % 16, dims 16c + 4(l / 16)
+//     .. + 3) lives in registers for the whole kernel.  S^T rather than S,
+//     because the MFMA output layout of S^T (lane l, register r: position
+//     4(l / 16) + r, query l % 16) is exactly the B-operand layout of
+//     O^T = V^T P^T, so p never goes through LDS or a transpose.
+//   - Online softmax per query: the running max needs 2 cross-lane
+//     shuffles per tile (the 4 lane groups of a query); the running sum
+//     stays per lane and is reduced once at the end.
+//   - O^T += V^T P^T: V read from LDS one float per lane and step (16
+//     consecutive dims per 16 lanes), 32 accumulators per lane at hd = 128.
+// Positions past the workgroup's last token are clamped on load and masked
+// (-inf score) per query.  FLOPs: 4 * hd * H * sum_t (pos0 + t + 1).
+#include "mlk_attention.h"
+
+#include <cmath>
+
+namespace mlk {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPfThreads = 256;
+constexpr int kPfTokens = 16;  // tokens per workgroup: the MFMA's 16 query columns
+constexpr int kPfTile = 32;    // cache positions per K/V tile
+constexpr int kPfHeads = 4;    // query heads per workgroup, one per wave
+
+template <int HD>
+struct PrefillSmem {
+    float k[2][kPfTile * (HD + 4)];
+    float v[2][kPfTile * (HD + 4)];
+};
+
+template <int HD>
+__global__ __launch_bounds__(kPfThreads) void AttnPrefill(
+    const float* __restrict__ q, int64_t q_stride, const float* __restrict__ kc,
+    const float* __restrict__ vc, int64_t slot, int KV, int H, int32_t pos0, int64_t T,
+    float scale, float* __restrict__ out, int head_blocks) {
+#pragma clang fp contract(off)
+    constexpr int LD = HD + 4;
+    constexpr int NC = HD / 16;                          // 16-dim chunks
+    constexpr int NL = kPfTile * HD / 4 / kPfThreads;    // float4 per thread per K (V) tile
+    __shared__ PrefillSmem<HD> sm;
+    const int group = H / KV;
+    const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
+    int64_t bid = blockIdx.x;
+    const int hb = static_cast<int>(bid % head_blocks);
+    bid /= head_blocks;
+    const int g = static_cast<int>(bid % KV);
+    bid /= KV;
+    const int64_t t0 = (n_tb - 1 - bid) * kPfTokens;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int i16 = lane & 15, kq = lane >> 4;
+    const int hq = hb * kPfHeads + wave;  // query head within the group
+    const bool active = hq < group;
+    const int h = g * group + (active ? hq : 0);
+    const int64_t last_t = (t0 + kPfTokens < T ? t0 + kPfTokens : T) - 1;
+    const int64_t t = t0 + i16 <= last_t ? t0 + i16 : last_t;  // this lane's query token
+    const int64_t my_pos = pos0 + t;
+    const int64_t max_pos = pos0 + last_t;
+
+    f32x4 qv[NC];
+    const float* qrow = q + t * q_stride + static_cast<int64_t>(h) * HD + 4 * kq;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c);
+
+    const float* kb = kc + static_cast<int64_t>(g) * HD;
+    const float* vb = vc + static_cast<int64_t>(g) * HD;
+    float4 kr[NL], vr[NL];
+    auto load = [&](int64_t p0) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kPfThreads * i;
+            const int64_t p = p0 + idx / (HD / 4);
+            const int64_t pos = p <= max_pos ? p : max_pos;
+            const int c4 = idx % (HD / 4);
+            kr[i] = *reinterpret_cast<const float4*>(kb + pos * slot + 4 * c4);
+            vr[i] = *reinterpret_cast<const float4*>(vb + pos * slot + 4 * c4);
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kPfThreads * i;
+            const int o = (idx / (HD / 4)) * LD + 4 * (idx % (HD / 4));
+            *reinterpret_cast<float4*>(&sm.k[buf][o]) = kr[i];
+            *reinterpret_cast<float4*>(&sm.v[buf][o]) = vr[i];
+        }
+    };
+
+    f32x4 acc[NC];  // O^T: acc[c][r] = dim 16c + 4 kq + r of query i16
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY;  // running max of query i16 (equal in its 4 lane groups)
+    float l = 0.0f;       // this lane's part of the running sum
+
+    const int64_t n_tiles = max_pos / kPfTile + 1;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int64_t it = 0; it < n_tiles; ++it) {
+        const int buf = static_cast<int>(it & 1);
+        const int64_t p0 = it * kPfTile;
+        load((it + 1 < n_tiles ? it + 1 : it) * kPfTile);
+        if (active) {
+            f32x4 s[2];
+#pragma unroll
+            for (int pt = 0; pt < 2; ++pt) {
+                s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                const float* krow = &sm.k[buf][(pt * 16 + i16) * LD + 4 * kq];
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    const f32x4 kk = *reinterpret_cast<const f32x4*>(krow + 16 * c);
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[st], qv[c][st], s[pt], 0,
+                                                                     0, 0);
+                    }
+                }
+            }
+            float sv[8];
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int pt = 0; pt < 2; ++pt) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t pos = p0 + pt * 16 + 4 * kq + r;
+                    const float x = pos <= my_pos ? s[pt][r] * scale : -INFINITY;
+                    sv[pt * 4 + r] = x;
+                    tmax = fmaxf(tmax, x);
+                }
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+            const float mnew = fmaxf(m, tmax);  // finite: position 0 is in every query's range
+            const float corr = expf(m - mnew);
+            l *= corr;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) acc[c] *= corr;
+            float pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                pv[i] = expf(sv[i] - mnew);
+                l += pv[i];
+            }
+            m = mnew;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+#pragma unroll
+                for (int pt = 0; pt < 2; ++pt) {
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        const float vv = sm.v[buf][(pt * 16 + 4 * kq + st) * LD + 16 * c + i16];
+                        acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv, pv[pt * 4 + st], acc[c],
+                                                                      0, 0, 0);
+                    }
+                }
+            }
+        }
+        store(buf ^ 1);
+        __syncthreads();
+    }
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
+    if (!active || t0 + i16 > last_t) return;
+    float* orow = out + (t * H + h) * static_cast<int64_t>(HD) + 4 * kq;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        *reinterpret_cast<float4*>(orow + 16 * c) =
+            make_float4(acc[c][0] * inv, acc[c][1] * inv, acc[c][2] * inv, acc[c][3] * inv);
+    }
+}
+
+}  // namespace
+
+bool PrefillSupported(int32_t head_dim, const float* q, int64_t q_row_stride, const float* out,
+                      const float* k_cache, const float* v_cache) {
+    return (head_dim == 64 || head_dim == 128) && q_row_stride % 4 == 0 && Aligned(q, 16) &&
+           Aligned(out, 16) && Aligned(k_cache, 16) && Aligned(v_cache, 16);
+}
+
+mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, const float* vc,
+                         int64_t slot, int32_t H, int32_t KV, int32_t head_dim, int32_t pos0,
+                         int64_t T, float* out, hipStream_t s) {
+    const int group = H / KV;
+    const int head_blocks = (group + kPfHeads - 1) / kPfHeads;
+    const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
+    const int64_t blocks = n_tb * KV * head_blocks;
+    if (blocks > 0x7FFFFFFF) return Fail(MLK_ERR_INVALID, "attention prefill: launch too large");
+    const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if (head_dim == 64) {
+        hipLaunchKernelGGL(AttnPrefill<64>, grid, dim3(kPfThreads), 0, s, q, q_row_stride, kc, vc,
+                           slot, KV, H, pos0, T, scale, out, head_blocks);
+    } else {
+        hipLaunchKernelGGL(AttnPrefill<128>, grid, dim3(kPfThreads), 0, s, q, q_row_stride, kc,
+                           vc, slot, KV, H, pos0, T, scale, out, head_blocks);
+    }
+    return CheckLaunch("AttnPrefill");
+}
+
+}  // namespace mlk

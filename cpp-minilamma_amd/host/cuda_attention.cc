@@ -73,9 +73,19 @@ void CheckArgs(const CudaCache& cache, int layer, int pos, int n_heads, int n_kv
     CheckMul(static_cast<size_t>(n_heads), static_cast<size_t>(head_dim), caller);
 }
 
-// Runs the kernels for T query rows at positions pos0..pos0+T-1 into out.
+// Runs the kernels for T query rows at positions pos0..pos0+T-1 into out: a
+// chunk of 16 or more rows with head_dim 64 / 128 takes the causal prefill
+// kernel (no workspace), anything else the decode kernel.
 void Attend(const float* q, float* out, int64_t T, const CudaCache& cache, int layer, int pos0,
             int n_heads, int n_kv_heads, int head_dim, int device_id, const char* caller) {
+    if (T >= 16 && (head_dim == 64 || head_dim == 128)) {
+        const mlk_status st = mlk_attention_prefill_f32(
+            q, static_cast<int64_t>(n_heads) * head_dim, static_cast<const float*>(cache.KData()),
+            static_cast<const float*>(cache.vData()), cache.n_layers(), cache.max_seq_len(),
+            n_heads, n_kv_heads, head_dim, layer, pos0, T, out, nullptr);
+        if (st != MLK_OK) Throw(caller, mlk_last_error());
+        return;
+    }
     const int64_t max_ctx = static_cast<int64_t>(pos0) + T;
     const int64_t ws_bytes =
         mlk_attention_workspace_bytes(T, n_heads, n_kv_heads, head_dim, max_ctx);

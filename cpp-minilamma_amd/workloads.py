@@ -122,6 +122,13 @@ def flops_linear(T, in_features, out_features):
 
 # ------------------------------------------------------- decode attention
 
+def flops_prefill_attention(T, H, hd, pos0=0):
+    """Causal attention of T tokens at positions pos0 + t: per head and
+    attended position, q.k and p v, 2 hd flops each."""
+    n_pairs = T * pos0 + T * (T + 1) // 2
+    return 4 * hd * H * n_pairs
+
+
 def bytes_attention(positions, n_heads, n_kv_heads, head_dim):
     """Read the K and V rows 0..pos of each token's KV heads once, read q,
     write out: 8 * (pos + 1) * KV * hd per token + 8 * H * hd."""

@@ -25,7 +25,7 @@
  *   include/cuda_matmul.h:7-18      -> mlk_linear_f32, mlk_matmul_f32
  *   include/cuda_quant.h:12-25      -> mlk_linear_quant
  *   include/cuda_kvcache.h:23       -> mlk_kv_write_f32
- *   include/cuda_attention.h:9-13   -> mlk_attention_decode_f32
+ *   include/cuda_attention.h:9-13   -> mlk_attention_decode_f32, mlk_attention_prefill_f32
  *   include/cuda_runtime.h:8-42     -> the runtime entries at the end
  */
 #ifndef MINILAMMA_HIP_H
@@ -217,7 +217,9 @@ int64_t mlk_attention_workspace_bytes(int64_t n_tokens, int32_t n_heads, int32_t
  * mlk_attention_workspace_bytes() is nonzero, `workspace` must hold that many
  * bytes (chunk partials); out must not alias q.  Sums are fp32 in the
  * kernel's order (the reference's tolerance: 2e-5 against float64,
- * test/cuda_attention_test.cc:108-109).
+ * test/cuda_attention_test.cc:108-109).  With positions == NULL, 16 or more
+ * tokens, head_dim 64 or 128 and 16-byte aligned q rows, out and caches, the
+ * call runs mlk_attention_prefill_f32's kernel and uses no workspace.
  * Replaces CudaAttentionDevice (include/cuda_attention.h:12-13;
  * src/cuda_attention.cu:77-176, 2 launches, one cudaMalloc and a device
  * synchronize per call).
@@ -229,6 +231,24 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
                                     int64_t n_tokens, int64_t max_ctx, float* out,
                                     void* workspace, size_t workspace_bytes, int32_t* err,
                                     void* stream);
+
+/*
+ * Causal attention of a prompt chunk: tokens t < n_tokens at positions
+ * pos0 + t (their K/V rows already in the cache, e.g. by mlk_kv_write_f32),
+ * token t attending to cache positions 0 .. pos0 + t -- the per-token
+ * attention of ForwardBatch's token loop (src/forward.cc:482-486, each step
+ * src/forward.cc:265-298) for the whole chunk in one launch, on the matrix
+ * cores.  Same semantics, layout and error bound as mlk_attention_decode_f32
+ * with positions == NULL; needs head_dim 64 or 128, q_row_stride % 4 == 0,
+ * 16-byte aligned q, out and caches, pos0 + n_tokens <= max_seq.  No
+ * workspace.  No counterpart in the reference's device code (it ran the
+ * decode kernel once per token).
+ */
+mlk_status mlk_attention_prefill_f32(const float* q, int64_t q_row_stride, const float* k_cache,
+                                     const float* v_cache, int64_t n_layers, int64_t max_seq,
+                                     int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                     int64_t layer, int32_t pos0, int64_t n_tokens, float* out,
+                                     void* stream);
 
 /* Synthetic-input helper (not a reference op): fills x[i] with
  * mean + std * N(0,1) from a counter-based generator keyed by seed and i, so

@@ -323,3 +323,151 @@ def test_write_then_attend_matches_oracle_decode_loop(mlk, orc):
         assert_attention_close(got, ex, pav, dmax, n, f"step {pos}")
         assert_attention_close(orc.attention(q, kc, vc, 1, [pos])[0], ex, pav, dmax, n, "oracle")
     assert_bits_equal(d_k.download(), kc, "cache k")
+
+
+# ------------------------------------------------------------ prefill
+
+def prefill_exact(q, kc, vc, layer, pos0):
+    """float64 causal attention of T query rows q [T, H, hd] at positions
+    pos0 + t over cache positions 0..pos0 + t; with sum_j p_j |v_jd| [T, H,
+    hd], the per-row score bound D [T, H] and n [T]."""
+    T, H, hd = q.shape
+    KV = kc.shape[2]
+    g = H // KV
+    n_ctx = pos0 + T
+    scale = 1.0 / math.sqrt(hd)
+    gamma = (hd + 1) * U / (1 - (hd + 1) * U)
+    pos = pos0 + np.arange(T)
+    mask = np.arange(n_ctx)[None, :] > pos[:, None]
+    out = np.empty((T, H, hd))
+    pav = np.empty((T, H, hd))
+    dmax = np.empty((T, H))
+    for h in range(H):
+        k = kc[layer, :n_ctx, h // g].astype(np.float64)
+        v = vc[layer, :n_ctx, h // g].astype(np.float64)
+        qh = q[:, h].astype(np.float64)
+        s = qh @ k.T * scale
+        s[mask] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        out[:, h] = p @ v
+        pav[:, h] = p @ np.abs(v)
+        a = np.abs(qh) @ np.abs(k).T
+        a[mask] = 0
+        dmax[:, h] = gamma * scale * a.max(axis=1)
+    return out, pav, dmax, pos + 1
+
+
+def assert_prefill_close(got, exact, pav, dmax, n, what):
+    bound = (2 * dmax[:, :, None] + (n[:, None, None] + 6) * U) * pav + 1e-30
+    err = np.abs(np.asarray(got, np.float64) - exact)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {err.size} beyond the bound; worst "
+                           f"err {float(err.max()):.3e}")
+
+
+def run_prefill(mlk, cache, q, layer, pos0, via_decode=False):
+    q = np.ascontiguousarray(q, np.float32)
+    T, H, hd = q.shape
+    d_q = mlk.DeviceBuffer.from_array(q)
+    out = mlk.DeviceBuffer.empty((T, H, hd))
+    if via_decode:
+        ws_bytes = mlk.attention_workspace_bytes(T, H, cache.KV, hd, pos0 + T)
+        ws = mlk.DeviceBuffer(max(ws_bytes, 4), np.uint8)
+        mlk.attention_decode(d_q, cache.k, cache.v, cache.L, cache.S, H, cache.KV, hd, layer, T,
+                             out, pos0 + T, pos0=pos0, workspace=ws, workspace_bytes=ws_bytes)
+    else:
+        mlk.attention_prefill(d_q, cache.k, cache.v, cache.L, cache.S, H, cache.KV, hd, layer,
+                              pos0, T, out)
+    return out.download()
+
+
+PREFILL_SHAPES = [  # H, KV, hd, T, pos0
+    (32, 8, 128, 100, 0),    # Llama-3-8B heads, a partial last block of 16 tokens
+    (32, 8, 128, 64, 1000),  # a chunk after a prefix
+    (64, 8, 128, 37, 5),     # 70B: 8 heads per KV head, two head blocks
+    (8, 8, 64, 50, 0),       # MHA: one head per KV head, three of four waves idle
+    (32, 1, 128, 20, 3),     # MQA: 32 heads per KV head, 8 head blocks
+    (12, 2, 64, 33, 7),      # 6 heads per KV head: a partly idle second head block
+    (4, 2, 128, 16, 0),      # one block
+    (8, 2, 128, 16, 31),     # pos0 + T just past a 32-position tile
+]
+
+
+@pytest.mark.parametrize("H,KV,hd,T,pos0", PREFILL_SHAPES)
+def test_attention_prefill_shapes(mlk, H, KV, hd, T, pos0):
+    """The causal prefill kernel against float64, through its own entry and
+    through the decode entry (positions == NULL routes there, bit-identical);
+    cache slots past the chunk hold NaN and must never be read."""
+    rng = np.random.default_rng(H * 100 + T + pos0)
+    S = pos0 + T + 40
+    kc, vc = random_cache(rng, 2, S, KV, hd)
+    kc[:, pos0 + T:] = np.nan
+    vc[:, pos0 + T:] = np.nan
+    cache = Cache(mlk, kc, vc)
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    got = run_prefill(mlk, cache, q, 1, pos0)
+    ex, pav, dmax, n = prefill_exact(q, kc, vc, 1, pos0)
+    assert_prefill_close(got, ex, pav, dmax, n, f"prefill H{H} KV{KV} hd{hd} T{T} pos0 {pos0}")
+    np.testing.assert_array_equal(run_prefill(mlk, cache, q, 1, pos0, via_decode=True), got)
+
+
+def test_attention_prefill_counts_exactly_the_prefix(mlk):
+    """Equal keys: every token's output is the mean of the values at
+    positions 0..pos0 + t, so a position counted twice, skipped or leaking
+    from the future (the chunk's own later tokens are in the cache) shows."""
+    rng = np.random.default_rng(11)
+    H, KV, hd, T, pos0 = 32, 8, 128, 300, 77
+    S = pos0 + T
+    kc = np.broadcast_to(rng.standard_normal((1, 1, KV, hd)), (2, S, KV, hd)).astype(np.float32)
+    vc = rng.uniform(1.0, 2.0, (2, S, KV, hd)).astype(np.float32)
+    cache = Cache(mlk, np.ascontiguousarray(kc), vc)
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    got = run_prefill(mlk, cache, q, 0, pos0)
+    csum = np.cumsum(vc[0].astype(np.float64), axis=0)
+    for t in (0, 1, 15, 16, 17, 150, T - 1):
+        n = pos0 + t + 1
+        want = np.repeat(csum[n - 1] / n, H // KV, axis=0)
+        np.testing.assert_allclose(got[t], want, rtol=2e-6, err_msg=f"token {t}")
+
+
+def test_attention_prefill_after_kv_write(mlk, orc):
+    """ForwardBatch's order for one layer: write the chunk's K/V rows, then
+    attend (8B heads, T = 256 at pos0 = 0 and a second chunk at 256),
+    against float64 and the oracle's per-token attention on a sample."""
+    rng = np.random.default_rng(12)
+    H, KV, hd, L, S = 32, 8, 128, 2, 512
+    kc = np.zeros((L, S, KV, hd), np.float32)
+    vc = np.zeros_like(kc)
+    cache = Cache(mlk, kc, vc)
+    for pos0, T in ((0, 256), (256, 200)):
+        k = rng.standard_normal((T, KV * hd)).astype(np.float32)
+        v = rng.standard_normal((T, KV * hd)).astype(np.float32)
+        mlk.kv_write(cache.k, cache.v, L, S, KV, hd, 1, mlk.DeviceBuffer.from_array(k),
+                     mlk.DeviceBuffer.from_array(v), T, pos0=pos0)
+        kc[1, pos0:pos0 + T] = k.reshape(T, KV, hd)
+        vc[1, pos0:pos0 + T] = v.reshape(T, KV, hd)
+        q = rng.standard_normal((T, H, hd)).astype(np.float32)
+        got = run_prefill(mlk, cache, q, 1, pos0)
+        ex, pav, dmax, n = prefill_exact(q, kc, vc, 1, pos0)
+        assert_prefill_close(got, ex, pav, dmax, n, f"chunk at {pos0}")
+        sample = [0, T // 2, T - 1]
+        ora = orc.attention(q[sample], kc, vc, 1, [pos0 + t for t in sample])
+        for i, t in enumerate(sample):
+            assert_attention_close(ora[i], ex[t], pav[t], float(dmax[t].max()), n[t], "oracle")
+
+
+def test_attention_prefill_rejects(mlk):
+    kc = mlk.DeviceBuffer.empty((2, 64, 2, 128))
+    vc = mlk.DeviceBuffer.empty((2, 64, 2, 128))
+    q = mlk.DeviceBuffer.empty((16, 4, 128))
+    out = mlk.DeviceBuffer.empty((16, 4, 128))
+    with pytest.raises(mlk.MlkError, match="out of range"):
+        mlk.attention_prefill(q, kc, vc, 2, 64, 4, 2, 128, 0, 50, 16, out)
+    with pytest.raises(mlk.MlkError, match="head_dim 64 or 128"):
+        mlk.attention_prefill(q, kc, vc, 2, 64, 4, 2, 96, 0, 0, 16, out)
+    with pytest.raises(mlk.MlkError, match="divide n_heads"):
+        mlk.attention_prefill(q, kc, vc, 2, 64, 3, 2, 128, 0, 0, 16, out)
+    with pytest.raises(mlk.MlkError, match="alias"):
+        mlk.attention_prefill(q, kc, vc, 2, 64, 4, 2, 128, 0, 0, 16, q)
