@@ -57,6 +57,10 @@ def parse_args():
     p.add_argument("--gemm", default=None,
                    help="only measure the seven Llama-3-8B layer projections at prefill row counts "
                         "(32 to 4096; the matrix-core GEMM) into this JSON file")
+    p.add_argument("--layer", default=None,
+                   help="only measure one Llama-3-8B layer over a 4096-token prompt chunk "
+                        "(mlk_forward_layer_batch), with a token-by-token comparison, into "
+                        "this JSON file")
     p.add_argument("--attention", default=None,
                    help="only measure decode attention (Llama-3-8B and 70B head shapes, one "
                         "token at several context lengths and configs[1]'s 64 tokens) into "
@@ -533,6 +537,139 @@ def gemm_bench(mlk, steps, path):
         json.dump(out, f, indent=1)
 
 
+# ------------------------------------------------------------ batched layer
+
+LAYER_TOKENS = 4096
+LAYER_LOOP_SAMPLE = 64  # tokens of the token-by-token comparison
+
+
+def _device_layer(mlk, fwd, cfg, wt, seed):
+    """One Llama-3-8B-shaped layer's weights on the device (N(0, 0.02),
+    quantized on the device; norm weights N(1, 0.1)) as LayerWeights, plus
+    the buffers that hold them."""
+    D, F = cfg["dim"], cfg["hidden_dim"]
+    QD, KD = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    shapes = {"wq": (QD, D), "wk": (KD, D), "wv": (KD, D), "wo": (D, QD), "w_gate": (F, D),
+              "w_up": (F, D), "w_down": (D, F)}
+    keep = []
+    tmp = mlk.DeviceBuffer.empty((max(o * i for o, i in shapes.values()),))
+    w = fwd.LayerWeights()
+    for j, (name, (o, i)) in enumerate(shapes.items()):
+        lw = fwd.LinearWeight()
+        if wt == "f32":
+            buf = mlk.DeviceBuffer.empty((o, i))
+            mlk.fill_normal(buf, o * i, 0.0, 0.02, seed + j)
+            lw.type = fwd.WEIGHT_F32
+        else:
+            mlk.fill_normal(tmp, o * i, 0.0, 0.02, seed + j)
+            buf = mlk.DeviceBuffer(mlk.quant_bytes(wt, o, i), np.uint8)
+            mlk.quantize(wt, tmp, o, i, buf)
+            lw.type = mlk.QUANT[wt]
+        lw.data, lw.bias = buf.ptr, None
+        setattr(w, name, lw)
+        keep.append(buf)
+    for name in ("attention_norm", "ffn_norm"):
+        buf = mlk.DeviceBuffer.empty((D,))
+        mlk.fill_normal(buf, D, 1.0, 0.1, seed + 50 + len(keep))
+        setattr(w, name, buf.ptr)
+        keep.append(buf)
+    mlk.synchronize()
+    tmp.close()
+    return w, keep
+
+
+def layer_bench(mlk, steps, path):
+    """One Llama-3-8B layer (attention + SwiGLU FFN) over a T = 4096 prompt
+    chunk at positions 0..4095 through mlk_forward_layer_batch, timed between
+    two events around `steps` calls; beside it the same layer run the
+    reference's way, one token at a time (T = 1 calls at positions 0..63),
+    and the reference's own CPU forward pass (oracle/_ref, one layer, a
+    few tokens)."""
+    import importlib
+    fwd = importlib.import_module(mlk.__name__ + ".forward")
+    cfg = dict(workloads.CONFIGS["c3_prefill_8b"])
+    cfg.update(hidden_dim=cfg["ffn"], max_seq=LAYER_TOKENS)
+    T = LAYER_TOKENS
+    D, KV, hd = cfg["dim"], cfg["n_kv_heads"], cfg["head_dim"]
+    fl_lin = sum(workloads.flops_linear(T, k, o) for _, k, o in workloads.layer_linears(cfg))
+    fl_att = workloads.flops_prefill_attention(T, cfg["n_heads"], hd)
+    out = {"workload": "one Llama-3-8B layer, T = 4096 prompt chunk at positions 0..4095, "
+                       "weights N(0, 0.02) quantized on the device, x N(0, 1)",
+           "layer_flops": fl_lin + fl_att, "linear_flops": fl_lin, "attention_flops": fl_att,
+           "peak_TFLOPs": MFMA_FP32_PEAK_TFLOPS}
+    st = mlk.Stream()
+    kc = mlk.DeviceBuffer.empty((1, T, KV, hd))
+    vc = mlk.DeviceBuffer.empty((1, T, KV, hd))
+    kc.zero()
+    vc.zero()
+    x = mlk.DeviceBuffer.empty((T, D))
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, T, True), np.uint8)
+    ws1 = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, T, True), np.uint8)
+    for wt in ("q8_0", "f32"):
+        w, keep = _device_layer(mlk, fwd, cfg, wt, 400)
+        mlk.fill_normal(x, T * D, 0.0, 1.0, 21)
+        fwd.forward_layer_batch(cfg, w, x, T, kc, vc, 1, T, 0, T, ws, stream=st)
+        st.synchronize()
+        e0, e1 = mlk.Event(), mlk.Event()
+        e0.record(st)
+        for _ in range(steps):
+            fwd.forward_layer_batch(cfg, w, x, T, kc, vc, 1, T, 0, T, ws, stream=st)
+        e1.record(st)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1) / steps
+        # the token loop: token t alone at position t (its cache prefix as
+        # the batched call left it)
+        n = LAYER_LOOP_SAMPLE
+        x1 = mlk.DeviceBuffer.empty((n, D))
+        mlk.fill_normal(x1, n * D, 0.0, 1.0, 22)
+        e2, e3 = mlk.Event(), mlk.Event()
+        e2.record(st)
+        for t in range(n):
+            fwd.forward_layer_batch(cfg, w, x1.ptr + t * D * 4, 1, kc, vc, 1, T, 0, T, ws1,
+                                    pos0=t, stream=st)
+        e3.record(st)
+        e3.synchronize()
+        loop_us = e2.elapsed_ms(e3) / n * 1e3
+        tf = (fl_lin + fl_att) / (ms * 1e-3) / 1e12
+        out[wt] = {"us": round(ms * 1e3, 1), "layer_ms": round(ms, 3),
+                   "tokens_per_s": round(T / (ms * 1e-3), 1),
+                   "TFLOPs": round(tf, 2), "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4),
+                   "token_loop_us_per_token": round(loop_us, 1),
+                   "token_loop_tokens_per_s": round(1e6 / loop_us, 1),
+                   "batch_speedup_over_token_loop": round(loop_us * T / (ms * 1e3), 1)}
+        print(f"layer {wt} T={T}: {ms:.2f} ms ({T / (ms * 1e-3):.0f} tokens/s, {tf:.1f} "
+              f"TFLOP/s); token loop {loop_us:.0f} us/token", flush=True)
+        x1.close()
+        del keep
+    out["cpu_reference"] = layer_cpu_reference(cfg)
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+
+
+def layer_cpu_reference(cfg, n_tokens=2):
+    """The reference's own CPU forward pass (oracle/_ref AVX2 build,
+    ForwardToken) on a one-layer 8B-shaped Q8_0 model with a 256-token
+    vocabulary (so lm_head does not dominate): seconds per token."""
+    try:
+        import oracle as O
+        if not O.reference_available(avx2=True):
+            return None
+        c = dict(vocab=256, dim=cfg["dim"], hidden_dim=cfg["hidden_dim"], layers=1,
+                 n_heads=cfg["n_heads"], n_kv_heads=cfg["n_kv_heads"], head_dim=cfg["head_dim"],
+                 max_seq=64, rope_type=0, theta=cfg["theta"], eps=cfg["eps"])
+        model = O.forward_model(c, seed=1, weight_type="q8_0")
+        ref = O.reference(avx2=True)
+        tokens = np.arange(n_tokens, dtype=np.int32)
+        ref.forward_tokens(model, tokens[:1], tokens[:1])  # warm
+        t0 = time.perf_counter()
+        ref.forward_tokens(model, tokens, tokens)
+        s = (time.perf_counter() - t0) / n_tokens
+        return {"seconds_per_token_layer": round(s, 4), "tokens_per_s": round(1 / s, 2),
+                "threads": os.cpu_count(), "sample": f"{n_tokens} tokens, 1 layer, Q8_0"}
+    except Exception as e:  # the baseline is informative only
+        return {"error": str(e)}
+
+
 # ------------------------------------------------------------ attention
 
 ATT_LAYERS = 16  # cache layers rotated per launch: 16 x 64 MB K+V at 8B, S = 8192
@@ -794,6 +931,7 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
     def short(name):
         # "void mlk::(anonymous namespace)::K<...>(args)" -> "K<...>"
         import re
+        name = name.replace("(anonymous namespace)::", "").replace("mlk::", "")
         m = re.search(r"(\w+(?:<[^()]*>)?)\(", name)
         return m.group(1) if m else name
 
@@ -865,6 +1003,9 @@ def main():
         return
     if args.gemm:
         gemm_bench(mlk, args.steps, args.gemm)
+        return
+    if args.layer:
+        layer_bench(mlk, args.steps, args.layer)
         return
     peak = workloads.HBM_PEAK_GBS
     cfg = workloads.CONFIGS["c3_prefill_8b"]

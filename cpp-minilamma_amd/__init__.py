@@ -143,7 +143,10 @@ def exported_symbols():
     return sorted(list(_SIGNATURES) + ["mlk_last_error", "mlk_status_string",
                                        "mlk_abi_version", "mlk_quant_bytes",
                                        "mlk_attention_workspace_bytes",
-                                       "mlk_linear_workspace_bytes"])
+                                       "mlk_linear_workspace_bytes",
+                                       # bound with their structs in forward.py
+                                       "mlk_forward_layer_workspace_bytes",
+                                       "mlk_forward_layer_batch"])
 
 
 # ------------------------------------------------------------------ runtime

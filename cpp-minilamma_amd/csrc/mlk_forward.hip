@@ -1,0 +1,197 @@
+// mlk_forward.hip -- one transformer layer over a batch of tokens: the
+// reference's ForwardLayerDevice (src/forward.cc:337-384; CPU twin
+// ForwardLayer :385-414) for all T tokens at once, which replaces the token
+// loop of ForwardBatch (:473-488) layer by layer.
+//
+// Per layer, on one stream (x [T, dim] is the residual stream, in place):
+//   h = RmsNorm(x, attention_norm)                    mlk_rmsnorm_f32
+//   q, k, v = h W^T (+ bias)                          mlk_linear_* (GEMM from 8 rows)
+//   RoPE(q, k) at each token's position               mlk_rope_f32
+//   write k, v to the cache; a = attention(q)         mlk_kv_write_f32, then
+//                                                     mlk_attention_prefill_f32
+//                                                     (consecutive positions)
+//                                                     or mlk_attention_decode_f32
+//   x += a Wo^T; h = RmsNorm(x, ffn_norm)             mlk_linear_*, mlk_add_rmsnorm_f32
+//   g = h Wgate^T, u = h Wup^T; g = silu(g) * u       mlk_linear_*, mlk_swiglu_f32
+//   x += g Wdown^T                                    mlk_linear_*, mlk_add_f32
+// Every op keeps the reference's arithmetic (the fused residual add and
+// RmsNorm computes r = x + delta in fp32 and then RmsNorm(r), as
+// ForwardAdd + ForwardRmsForm do); the linear sums and the attention sums
+// are fp32 in the kernels' orders.  All K/V rows of the batch are written
+// before any token attends, so the batch equals the token loop when the
+// positions increase from token to token (a later token never writes a slot
+// an earlier one reads).
+//
+// The intermediates live in the caller's workspace (no allocation here):
+// h, q, k, v, a, a Wo^T, gate, up, then the linear layers' split-K scratch
+// and the decode attention's chunk scratch, each 256-byte aligned.
+#include "mlk_common.h"
+
+namespace mlk {
+namespace {
+
+constexpr int kLinearF32 = MLK_WEIGHT_F32;
+
+struct Plan {
+    int64_t off[10];  // float offsets: h q k v a proj gate up | byte offsets: lin att
+    int64_t lin_bytes = 0, att_bytes = 0, total = 0;
+};
+
+int64_t Align256(int64_t bytes) { return (bytes + 255) / 256 * 256; }
+
+bool Contiguous(const int32_t* positions) { return positions == nullptr; }
+
+Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contiguous) {
+    const int64_t D = c.dim, F = c.hidden_dim;
+    const int64_t QD = static_cast<int64_t>(c.n_heads) * c.head_dim;
+    const int64_t KD = static_cast<int64_t>(c.n_kv_heads) * c.head_dim;
+    const int64_t sizes[8] = {T * D, T * QD, T * KD, T * KD, T * QD, T * D, T * F, T * F};
+    Plan p;
+    int64_t at = 0;
+    for (int i = 0; i < 8; ++i) {
+        p.off[i] = at;
+        at += Align256(sizes[i] * 4);
+    }
+    const int64_t shapes[5][2] = {{D, QD}, {D, KD}, {QD, D}, {D, F}, {F, D}};  // (in, out)
+    for (const auto& s : shapes) {
+        const int64_t b = mlk_linear_workspace_bytes(T, s[0], s[1]);
+        if (b > p.lin_bytes) p.lin_bytes = b;
+    }
+    p.off[8] = at;
+    at += Align256(p.lin_bytes);
+    // the decode kernel's chunk scratch, for the calls that take that path
+    const bool prefill = contiguous && T >= 16 && (c.head_dim == 64 || c.head_dim == 128);
+    p.att_bytes = prefill ? 0
+                          : mlk_attention_workspace_bytes(T, c.n_heads, c.n_kv_heads, c.head_dim,
+                                                          max_ctx);
+    p.off[9] = at;
+    at += Align256(p.att_bytes);
+    p.total = at;
+    return p;
+}
+
+mlk_status Linear(const mlk_linear_weight& w, const float* x, float* y, int64_t T, int64_t in,
+                  int64_t out, void* ws, size_t ws_bytes, void* stream) {
+    if (w.type == kLinearF32) {
+        return mlk_linear_f32(x, static_cast<const float*>(w.data), w.bias, y, T, in, out, ws,
+                              ws_bytes, stream);
+    }
+    return mlk_linear_quant(w.type, x, w.data, w.bias, y, T, in, out, ws, ws_bytes, stream);
+}
+
+mlk_status CheckConfig(const char* fn, const mlk_layer_config* c) {
+    if (c == nullptr) return Fail(MLK_ERR_INVALID, "%s: config must not be null", fn);
+    if (c->dim <= 0 || c->hidden_dim <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 ||
+        c->head_dim <= 0 || c->n_heads % c->n_kv_heads != 0) {
+        return Fail(MLK_ERR_INVALID,
+                    "%s: dims and head counts must be positive and n_kv_heads must divide "
+                    "n_heads (dim %lld, hidden %lld, heads %d / %d, head_dim %d)",
+                    fn, static_cast<long long>(c->dim), static_cast<long long>(c->hidden_dim),
+                    c->n_heads, c->n_kv_heads, c->head_dim);
+    }
+    return MLK_OK;
+}
+
+mlk_status CheckWeight(const char* fn, const char* name, const mlk_linear_weight& w) {
+    if (w.data == nullptr) return Fail(MLK_ERR_INVALID, "%s: weight %s is null", fn, name);
+    if (w.type != kLinearF32 && (w.type < MLK_Q8_0 || w.type > MLK_Q4_1)) {
+        return Fail(MLK_ERR_INVALID, "%s: weight %s has unknown type %d", fn, name, w.type);
+    }
+    return MLK_OK;
+}
+
+}  // namespace
+}  // namespace mlk
+
+using namespace mlk;
+
+extern "C" {
+
+int64_t mlk_forward_layer_workspace_bytes(const mlk_layer_config* cfg, int64_t n_tokens,
+                                          int64_t max_ctx, int32_t consecutive_positions) {
+    if (cfg == nullptr || n_tokens <= 0 || max_ctx <= 0 ||
+        CheckConfig("mlk_forward_layer_workspace_bytes", cfg) != MLK_OK) {
+        return 0;
+    }
+    return MakePlan(*cfg, n_tokens, max_ctx, consecutive_positions != 0).total;
+}
+
+mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_weights* w,
+                                   float* x, int64_t n_tokens, const int32_t* positions,
+                                   int32_t pos0, float* k_cache, float* v_cache,
+                                   int64_t n_layers, int64_t max_seq, int64_t layer,
+                                   int64_t max_ctx, void* workspace, size_t workspace_bytes,
+                                   int32_t* err, void* stream) {
+    const char* fn = "mlk_forward_layer_batch";
+    mlk_status st = CheckConfig(fn, cfg);
+    if (st != MLK_OK) return st;
+    if (w == nullptr || x == nullptr) return Fail(MLK_ERR_INVALID, "%s: weights and x must not be null", fn);
+    if (w->attention_norm == nullptr || w->ffn_norm == nullptr) {
+        return Fail(MLK_ERR_INVALID, "%s: norm weights must not be null", fn);
+    }
+    const struct {
+        const char* name;
+        const mlk_linear_weight* w;
+    } lins[] = {{"wq", &w->wq}, {"wk", &w->wk}, {"wv", &w->wv}, {"wo", &w->wo},
+                {"w_gate", &w->w_gate}, {"w_up", &w->w_up}, {"w_down", &w->w_down}};
+    for (const auto& l : lins) {
+        st = CheckWeight(fn, l.name, *l.w);
+        if (st != MLK_OK) return st;
+    }
+    if (n_tokens <= 0) return Fail(MLK_ERR_INVALID, "%s: n_tokens must be positive", fn);
+    if (!Aligned(k_cache, 16) || !Aligned(v_cache, 16)) {
+        return Fail(MLK_ERR_INVALID, "%s: the caches must be 16-byte aligned", fn);
+    }
+    const bool contiguous = Contiguous(positions);
+    if (max_ctx <= 0 || max_ctx > max_seq || (contiguous && pos0 + n_tokens > max_ctx)) {
+        return Fail(MLK_ERR_RANGE, "%s: max_ctx %lld must cover the positions and be <= max_seq "
+                    "%lld", fn, static_cast<long long>(max_ctx), static_cast<long long>(max_seq));
+    }
+    const Plan p = MakePlan(*cfg, n_tokens, max_ctx, contiguous);
+    if (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < p.total ||
+        !Aligned(workspace, 256)) {
+        return Fail(MLK_ERR_INVALID,
+                    "%s: a 256-byte aligned workspace of %lld bytes is needed (got %zu)", fn,
+                    static_cast<long long>(p.total), workspace_bytes);
+    }
+    const mlk_layer_config& c = *cfg;
+    const int64_t T = n_tokens, D = c.dim, F = c.hidden_dim;
+    const int64_t QD = static_cast<int64_t>(c.n_heads) * c.head_dim;
+    const int64_t KD = static_cast<int64_t>(c.n_kv_heads) * c.head_dim;
+    char* base = static_cast<char*>(workspace);
+    auto buf = [&](int i) { return reinterpret_cast<float*>(base + p.off[i]); };
+    float *h = buf(0), *q = buf(1), *k = buf(2), *v = buf(3), *a = buf(4), *proj = buf(5),
+          *gate = buf(6), *up = buf(7);
+    void* lin_ws = p.lin_bytes > 0 ? base + p.off[8] : nullptr;
+    void* att_ws = p.att_bytes > 0 ? base + p.off[9] : nullptr;
+    const size_t lin_b = static_cast<size_t>(p.lin_bytes);
+    const float eps = c.rms_norm_eps;
+
+#define MLK_TRY(call)              \
+    do {                           \
+        const mlk_status s_ = (call); \
+        if (s_ != MLK_OK) return s_;  \
+    } while (0)
+    MLK_TRY(mlk_rmsnorm_f32(x, w->attention_norm, h, T, D, eps, stream));
+    MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
+    MLK_TRY(Linear(w->wk, h, k, T, D, KD, lin_ws, lin_b, stream));
+    MLK_TRY(Linear(w->wv, h, v, T, D, KD, lin_ws, lin_b, stream));
+    MLK_TRY(mlk_rope_f32(q, k, T, c.n_heads, c.n_kv_heads, c.head_dim, QD, KD, positions, pos0,
+                         c.rope_theta, c.rope_type, err, stream));
+    MLK_TRY(mlk_kv_write_f32(k_cache, v_cache, n_layers, max_seq, c.n_kv_heads, c.head_dim, layer,
+                             k, KD, v, KD, positions, pos0, T, err, stream));
+    MLK_TRY(mlk_attention_decode_f32(q, QD, k_cache, v_cache, n_layers, max_seq, c.n_heads,
+                                     c.n_kv_heads, c.head_dim, layer, positions, pos0, T, max_ctx,
+                                     a, att_ws, static_cast<size_t>(p.att_bytes), err, stream));
+    MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
+    MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
+    MLK_TRY(Linear(w->w_gate, h, gate, T, D, F, lin_ws, lin_b, stream));
+    MLK_TRY(Linear(w->w_up, h, up, T, D, F, lin_ws, lin_b, stream));
+    MLK_TRY(mlk_swiglu_f32(gate, up, gate, T * F, stream));
+    MLK_TRY(Linear(w->w_down, gate, proj, T, F, D, lin_ws, lin_b, stream));
+    MLK_TRY(mlk_add_f32(x, proj, x, T * D, stream));
+#undef MLK_TRY
+    return MLK_OK;
+}
+
+}  // extern "C"

@@ -250,6 +250,63 @@ mlk_status mlk_attention_prefill_f32(const float* q, int64_t q_row_stride, const
                                      int64_t layer, int32_t pos0, int64_t n_tokens, float* out,
                                      void* stream);
 
+/* ------------------------------------------------------ batched forward
+ * One transformer layer over a batch of tokens: the reference's
+ * ForwardLayerDevice (src/forward.cc:337-384) for all tokens at once, i.e.
+ * ForwardBatch (src/forward.cc:473-488) without its token loop, layer by
+ * layer.  No counterpart in the reference (its batch runs one token at a
+ * time through the whole model). */
+
+enum { MLK_WEIGHT_F32 = -1 };  /* mlk_linear_weight.type of fp32 weights */
+
+typedef struct {
+    int32_t type;        /* MLK_WEIGHT_F32, MLK_Q8_0, MLK_Q4_0 or MLK_Q4_1 */
+    const void* data;    /* [out, in]: fp32 row-major, or out rows of ceil(in / 32) blocks */
+    const float* bias;   /* [out] or NULL */
+} mlk_linear_weight;
+
+/* A layer's device weights (the reference's Layer, include/model.h:41-55). */
+typedef struct {
+    const float* attention_norm;          /* [dim] */
+    mlk_linear_weight wq, wk, wv, wo;     /* [H*hd, dim], [KV*hd, dim] x2, [dim, H*hd] */
+    const float* ffn_norm;                /* [dim] */
+    mlk_linear_weight w_gate, w_up, w_down; /* [hidden, dim] x2, [dim, hidden] */
+} mlk_layer_weights;
+
+/* The ModelConfig fields a layer uses (include/model.h:57-81). */
+typedef struct {
+    int64_t dim, hidden_dim;
+    int32_t n_heads, n_kv_heads, head_dim, rope_type;  /* rope_type: mlk_rope_type */
+    float rope_theta, rms_norm_eps;
+} mlk_layer_config;
+
+/* Device bytes of the workspace of mlk_forward_layer_batch for n_tokens
+ * tokens attending up to max_ctx positions; consecutive_positions != 0 when
+ * the call passes positions == NULL (0 on bad input). */
+int64_t mlk_forward_layer_workspace_bytes(const mlk_layer_config* cfg, int64_t n_tokens,
+                                          int64_t max_ctx, int32_t consecutive_positions);
+
+/*
+ * x [n_tokens, dim] (the residual stream, updated in place) through layer
+ * `layer`: RmsNorm -> q/k/v linears (+ bias) -> RoPE -> K/V rows written to
+ * the caches -> attention -> wo, residual add -> RmsNorm -> SwiGLU FFN,
+ * residual add, with the reference's op semantics (each op as its own entry
+ * above documents).  Token t sits at positions[t] (device array) or
+ * pos0 + t (positions == NULL); all tokens' K/V rows are written before
+ * any token attends, so the result equals the reference's token loop when
+ * the positions increase along the batch.  Every position is < max_ctx <=
+ * max_seq.  The workspace (256-byte aligned, at least
+ * mlk_forward_layer_workspace_bytes(cfg, n_tokens, max_ctx, positions ==
+ * NULL)) holds every intermediate; the caches must be 16-byte aligned.  A device-side position error raises
+ * *err as the op entries do.
+ */
+mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_weights* w,
+                                   float* x, int64_t n_tokens, const int32_t* positions,
+                                   int32_t pos0, float* k_cache, float* v_cache,
+                                   int64_t n_layers, int64_t max_seq, int64_t layer,
+                                   int64_t max_ctx, void* workspace, size_t workspace_bytes,
+                                   int32_t* err, void* stream);
+
 /* Synthetic-input helper (not a reference op): fills x[i] with
  * mean + std * N(0,1) from a counter-based generator keyed by seed and i, so
  * the values do not depend on launch shape. */

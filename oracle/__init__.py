@@ -251,6 +251,128 @@ class _Oracle:
     def chain(self, bufs, n_tokens, n_threads):
         return self._chain(*_chain_args(bufs, n_tokens, n_threads))
 
+    # ---- forward pass ------------------------------------------------------
+    def linear(self, w, x, out_features, bias=None):
+        """A model linear: w = ("f32", W [out, in]) or (qtype, blocks)."""
+        kind, data = w
+        if kind == "f32":
+            return self.linear_f32(x, data, bias)
+        return self.linear_quant(kind, x, data, out_features, bias)
+
+    def forward_tokens(self, model, tokens, positions, mistake=None):
+        """The reference's CPU forward pass restated over the ops above:
+        ForwardBatch's loop (src/forward.cc:473-488) of ForwardToken
+        (:432-472) for tokens[t] at positions[t], one token at a time over
+        one KV cache:
+          x = Embedding(token)                               :198-205
+          per layer (ForwardLayer :385-414):
+            h = RmsNorm(x, attention_norm)
+            q, k, v = Linear(h, wq / wk / wv) + optional bias  :328-336, 223-236
+            Rope(q, k, pos)
+            write k, v at pos; a = ForwardAttention            :265-298
+            r = x + Linear(a, wo)                              :213-222
+            h2 = RmsNorm(r, ffn_norm)
+            x = r + Linear(SwiGlu(Linear(h2, w_gate), Linear(h2, w_up)), w_down)
+          logits = Linear(RmsNorm(x, final_norm), lm_head)   ComputeLogits :415-424
+        model: forward_model() layout.  Returns (logits [T, vocab], hidden
+        [T, layers + 1, dim]: the residual stream entering each layer and
+        leaving the last).  `mistake` plants one error, for the tests that
+        show the pinning catches it."""
+        c = model["config"]
+        D, H, KV, hd = c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"]
+        L, F, V = c["layers"], c["hidden_dim"], c["vocab"]
+        kc = np.zeros((L, c["max_seq"], KV, hd), np.float32)
+        vc = np.zeros_like(kc)
+        T = len(tokens)
+        logits = np.empty((T, V), np.float32)
+        hidden = np.empty((T, L + 1, D), np.float32)
+        for t in range(T):
+            pos = int(positions[t])
+            if "embedding" in model:
+                x = self.gather_f32(model["embedding"], np.array([tokens[t]], np.int32))[0]
+            else:
+                qt, blocks = model["embedding_q"]
+                x = self.gather_quant(qt, blocks, V, D, np.array([tokens[t]], np.int32))[0]
+            for li, lw in enumerate(model["layers"]):
+                hidden[t, li] = x
+                h = self.rmsnorm(x, lw["ffn_norm" if mistake == "swap_norms" else "attention_norm"],
+                                 c["eps"])
+                q = self.linear(lw["wq"], h, H * hd, lw.get("bq"))
+                k = self.linear(lw["wk"], h, KV * hd, lw.get("bk"))
+                v = self.linear(lw["wv"], h, KV * hd, lw.get("bv"))
+                if mistake != "no_rope_on_k":
+                    q, k = self.rope(q[None], k[None], H, KV, hd, positions=[pos],
+                                     theta=c["theta"], rope_type=c["rope_type"])
+                else:
+                    q, _ = self.rope(q[None], k[None], H, KV, hd, positions=[pos],
+                                     theta=c["theta"], rope_type=c["rope_type"])
+                    k = k[None]
+                self.kv_write(kc, vc, li, [pos], k.reshape(1, KV, hd), v.reshape(1, KV, hd))
+                a = self.attention(q.reshape(1, H, hd), kc, vc, li,
+                                   [pos - 1 if mistake == "exclusive_attention" and pos > 0
+                                    else pos])
+                o = self.linear(lw["wo"], a.reshape(-1), D)
+                r = x if mistake == "no_attention_residual" else self.add(x, o)
+                if mistake == "no_attention_residual":
+                    r = o
+                h2 = self.rmsnorm(r, lw["ffn_norm"], c["eps"])
+                g = self.linear(lw["w_gate"], h2, F)
+                u = self.linear(lw["w_up"], h2, F)
+                f = self.swiglu(u, g) if mistake == "swap_gate_up" else self.swiglu(g, u)
+                x = self.add(r, self.linear(lw["w_down"], f, D))
+            hidden[t, L] = x
+            logits[t] = self.linear(model["lm_head"], self.rmsnorm(x, model["final_norm"],
+                                                                   c["eps"]), V)
+        return logits, hidden
+
+
+LINEAR_NAMES = ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")
+FORWARD_MISTAKES = ("swap_norms", "no_rope_on_k", "exclusive_attention", "no_attention_residual",
+                    "swap_gate_up")
+
+
+def linear_shapes(c):
+    """[out, in] of each layer linear for a forward_model config."""
+    D, F = c["dim"], c["hidden_dim"]
+    QD, KD = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    return {"wq": (QD, D), "wk": (KD, D), "wv": (KD, D), "wo": (D, QD), "w_gate": (F, D),
+            "w_up": (F, D), "w_down": (D, F)}
+
+
+def forward_model(config, seed, weight_type="f32", biases=False, quant_embedding=None,
+                  std=0.02):
+    """A random model in the layout forward_tokens takes: config keys vocab,
+    dim, hidden_dim, layers, n_heads, n_kv_heads, head_dim, max_seq,
+    rope_type, theta, eps; weights N(0, std) (norm weights N(1, 0.1)),
+    quantized by the restated quantizer when weight_type is a qtype;
+    quant_embedding: a qtype to keep the token table as blocks."""
+    rng = np.random.default_rng(seed)
+    orc = oracle()
+    c = dict(config)
+
+    def lin(out_f, in_f):
+        w = (rng.standard_normal((out_f, in_f)) * std).astype(np.float32)
+        return ("f32", w) if weight_type == "f32" else (weight_type, orc.quantize(weight_type, w))
+
+    model = {"config": c, "layers": []}
+    table = (rng.standard_normal((c["vocab"], c["dim"])) * std).astype(np.float32)
+    if quant_embedding:
+        model["embedding_q"] = (quant_embedding, orc.quantize(quant_embedding, table))
+    else:
+        model["embedding"] = table
+    for _ in range(c["layers"]):
+        lw = {"attention_norm": (1 + 0.1 * rng.standard_normal(c["dim"])).astype(np.float32),
+              "ffn_norm": (1 + 0.1 * rng.standard_normal(c["dim"])).astype(np.float32)}
+        for name, (o, i) in linear_shapes(c).items():
+            lw[name] = lin(o, i)
+        if biases:
+            for b, n in (("bq", "wq"), ("bk", "wk"), ("bv", "wv")):
+                lw[b] = (rng.standard_normal(linear_shapes(c)[n][0]) * 0.1).astype(np.float32)
+        model["layers"].append(lw)
+    model["final_norm"] = (1 + 0.1 * rng.standard_normal(c["dim"])).astype(np.float32)
+    model["lm_head"] = lin(c["vocab"], c["dim"])
+    return model
+
 
 def _chain_args(b, n_tokens, n_threads):
     return (b["table"].reshape(-1), b["vocab"], b["dim"], b["ids"], b["x"].reshape(-1),
@@ -297,6 +419,11 @@ class _Reference:
         self._attention = _bind(lib, "ref_attention", C.c_int,
                                 [_f32p, _f32p, _f32p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                  C.c_int, C.c_int, _f32p])
+        vp = C.c_void_p
+        self._forward_tokens = _bind(lib, "ref_forward_tokens", C.c_int,
+                                     [_i32p, C.c_float, C.c_float, _f32p, C.POINTER(vp), _i32p,
+                                      C.POINTER(vp), C.POINTER(vp), _f32p, _i32p, _i32p, C.c_int,
+                                      _f32p])
 
     def attention(self, q, k_rows, v_rows, n_layers, max_seq, layer, pos):
         """One query token q [H, hd] at `pos`: k_rows / v_rows [pos + 1, KV, hd]
@@ -385,6 +512,46 @@ class _Reference:
 
     def chain(self, bufs, n_tokens, n_threads):
         return self._chain(*_chain_args(bufs, n_tokens, n_threads))
+
+    def forward_tokens(self, model, tokens, positions):
+        """The reference's own ForwardToken loop (ref_forward_tokens) over a
+        forward_model(); returns logits [T, vocab].  The F32 token table
+        only: the reference dequantizes a quantized one at load."""
+        c = model["config"]
+        keep = []
+
+        def ptr(a):
+            if a is None:
+                return None
+            keep.append(a)
+            return a.ctypes.data
+
+        cfg = np.array([c["vocab"], c["dim"], c["hidden_dim"], c["layers"], c["n_heads"],
+                        c["n_kv_heads"], c["head_dim"], c["max_seq"], c["rope_type"]], np.int32)
+        norms, types, weights, biases = [], [], [], []
+        kinds = {"f32": -1, **QUANT_TYPES}
+        for lw in model["layers"]:
+            norms += [ptr(_f32(lw["attention_norm"])), ptr(_f32(lw["ffn_norm"]))]
+            for name in LINEAR_NAMES:
+                kind, data = lw[name]
+                types.append(kinds[kind])
+                weights.append(ptr(_f32(data) if kind == "f32" else _u8(data)))
+            for b in ("bq", "bk", "bv"):
+                biases.append(ptr(None if lw.get(b) is None else _f32(lw[b])))
+        kind, data = model["lm_head"]
+        types.append(kinds[kind])
+        weights.append(ptr(_f32(data) if kind == "f32" else _u8(data)))
+        vp = C.c_void_p
+        n_w = len(weights)
+        logits = np.empty((len(tokens), c["vocab"]), np.float32)
+        emb = _f32(model["embedding"])
+        fn = self._forward_tokens
+        _check(fn(cfg, c["theta"], c["eps"], emb, (vp * len(norms))(*norms),
+                  np.array(types, np.int32), (vp * n_w)(*weights),
+                  (vp * len(biases))(*biases), _f32(model["final_norm"]),
+                  np.ascontiguousarray(tokens, np.int32),
+                  np.ascontiguousarray(positions, np.int32), len(tokens), logits.reshape(-1)))
+        return logits
 
 
 def _f32(a):

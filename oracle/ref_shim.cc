@@ -1,14 +1,18 @@
 // ref_shim.cc -- C entry points over the reference's own CPU sources.
 //
 // TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together
-// with the reference's src/{tensor,ops,quant,quantiezd_tensor,kvcache}.cc,
-// matumal/matuml_ops.cc and thread_pool/thread_pool.cc, straight from where
-// they lie under the reference tree, into oracle/_ref/libref*.so.  Tests use
+// with the reference's CPU sources (the ops, the quantizers, the KV cache,
+// the forward pass and the CPU builds of its device-layer files, which only
+// throw), straight from where they lie under the reference tree, into
+// oracle/_ref/libref*.so.  Tests use
 // it to pin the C restatement (oracle.c) and tests/golden/make_golden.py
 // writes the golden fixtures from it; bench.py times ref_chain as the
 // "reference" CPU baseline.  Nothing here is reference source: it only
 // converts between raw buffers and the reference's Tensor / block types.
+#include "include/context.h"
+#include "include/forward.h"
 #include "include/kvcache.h"
+#include "include/model.h"
 #include "include/ops.h"
 #include "include/quant.h"
 #include "include/quantized_tensor.h"
@@ -60,6 +64,30 @@ std::vector<Block> ToBlocks(const uint8_t* raw, size_t count) {
 }
 
 size_t RowBlocks(int cols) { return (static_cast<size_t>(cols) + 31) / 32; }
+
+// A linear weight [out, in] of type t (-1 F32, 0 Q8_0, 1 Q4_0, 2 Q4_1) as
+// the reference's QuanTensor.
+QuanTensor MakeWeight(int t, const void* data, int out, int in) {
+    QuanTensor w;
+    w.shape = {out, in};
+    const size_t n = static_cast<size_t>(out) * RowBlocks(in);
+    const uint8_t* raw = static_cast<const uint8_t*>(data);
+    if (t < 0) {
+        w.type = QuantType::kF32;
+        const float* f = static_cast<const float*>(data);
+        w.kF32_data.assign(f, f + static_cast<size_t>(out) * in);
+    } else if (t == 0) {
+        w.type = QuantType::kQ80;
+        w.kQ80_data = ToBlocks<Block_Q80>(raw, n);
+    } else if (t == 1) {
+        w.type = QuantType::kQ40;
+        w.kQ40_data = ToBlocks<Block_Q40>(raw, n);
+    } else {
+        w.type = QuantType::kQ41;
+        w.kQ41_data = ToBlocks<Block_Q41>(raw, n);
+    }
+    return w;
+}
 
 }  // namespace
 
@@ -270,6 +298,68 @@ int ref_chain(const float* table, int64_t vocab, int64_t dim, const int32_t* ids
             yan_lamma::SetThreadNum(n_threads);
             yan_lamma::ParallelFor(static_cast<int>(n_tokens), rows);
             yan_lamma::SetThreadNum(0);
+        }
+    });
+}
+
+// The reference's own CPU forward pass over an in-memory Model: ForwardToken
+// (src/forward.cc) for tokens[t] at positions[t], t = 0..T-1, one at a time
+// with one Context, exactly the loop of ForwardBatch; the logits of every
+// step go to logits [T, vocab].
+//   cfg      vocab, dim, hidden_dim, layers, n_heads, n_kv_heads, head_dim,
+//            max_seq_len, rope_type
+//   norms    per layer: attention_norm, ffn_norm
+//   types    per layer: wq wk wv wo w_gate w_up w_down, then lm_head
+//            (-1 F32, 0 Q8_0, 1 Q4_0, 2 Q4_1); weights the same order
+//   biases   per layer: bq bk bv (NULL: none)
+int ref_forward_tokens(const int32_t* cfg, float theta, float eps, const float* embedding,
+                       const float* const* norms, const int32_t* types,
+                       const void* const* weights, const float* const* biases,
+                       const float* final_norm, const int32_t* tokens,
+                       const int32_t* positions, int n_tokens, float* logits) {
+    return Guard([&] {
+        yan_lamma::Model model;
+        yan_lamma::ModelConfig& c = model.config;
+        c.vocab_size = cfg[0];
+        c.dim = cfg[1];
+        c.hidden_dim = cfg[2];
+        c.layers = cfg[3];
+        c.n_heads = cfg[4];
+        c.n_kv_heads = cfg[5];
+        c.head_dim = cfg[6];
+        c.max_seq_len = cfg[7];
+        c.rope_type = cfg[8] == 0 ? RopeType::kNormal : RopeType::kNeoX;
+        c.rope_theta = theta;
+        c.rms_norm_eps = eps;
+        const int D = c.dim, F = c.hidden_dim, QD = c.n_heads * c.head_dim,
+                  KD = c.n_kv_heads * c.head_dim;
+        model.embedding_data_ = Wrap(embedding, {c.vocab_size, D});
+        model.n_layers_.resize(c.layers);
+        for (int l = 0; l < c.layers; ++l) {
+            yan_lamma::Layer& L = model.n_layers_[l];
+            const int32_t* t = types + 7 * l;
+            const void* const* w = weights + 7 * l;
+            L.attention_norm = Wrap(norms[2 * l], {D});
+            L.ffn_norm = Wrap(norms[2 * l + 1], {D});
+            L.wq = MakeWeight(t[0], w[0], QD, D);
+            L.wk = MakeWeight(t[1], w[1], KD, D);
+            L.wv = MakeWeight(t[2], w[2], KD, D);
+            L.wo = MakeWeight(t[3], w[3], D, QD);
+            L.w_gate = MakeWeight(t[4], w[4], F, D);
+            L.w_up = MakeWeight(t[5], w[5], F, D);
+            L.w_down = MakeWeight(t[6], w[6], D, F);
+            if (biases[3 * l] != nullptr) L.bq = Wrap(biases[3 * l], {QD});
+            if (biases[3 * l + 1] != nullptr) L.bk = Wrap(biases[3 * l + 1], {KD});
+            if (biases[3 * l + 2] != nullptr) L.bv = Wrap(biases[3 * l + 2], {KD});
+        }
+        model.final_norm = Wrap(final_norm, {D});
+        model.lm_head_ = MakeWeight(types[7 * c.layers], weights[7 * c.layers], c.vocab_size, D);
+        model.is_loaded = true;
+        yan_lamma::Context ctx(&model);
+        for (int t = 0; t < n_tokens; ++t) {
+            ctx.pos = static_cast<size_t>(positions[t]);
+            Unwrap(yan_lamma::ForwardToken(model, ctx, tokens[t]),
+                   logits + static_cast<size_t>(t) * c.vocab_size);
         }
     });
 }

@@ -57,6 +57,26 @@ def golden(name):
         return {k: f[k] for k in f.files}
 
 
+def tiny_model():
+    """The reference's tiny model and its own forward-pass logits
+    (tests/golden/tiny_forward.npz) as (model, tokens, positions, logits) in
+    oracle.forward_model layout."""
+    g = golden("tiny_forward")
+    keys = ("vocab", "dim", "hidden_dim", "layers", "n_heads", "n_kv_heads", "head_dim",
+            "max_seq", "rope_type")
+    config = {k: int(v) for k, v in zip(keys, g["config"])}
+    config["theta"], config["eps"] = (float(v) for v in g["theta_eps"])
+    layers = []
+    for i in range(config["layers"]):
+        lw = {n: g[f"l{i}_{n}"] for n in ("attention_norm", "ffn_norm")}
+        for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+            lw[n] = ("f32", g[f"l{i}_{n}"])
+        layers.append(lw)
+    model = {"config": config, "embedding": g["embedding"], "layers": layers,
+             "final_norm": g["final_norm"], "lm_head": ("f32", g["lm_head"])}
+    return model, g["tokens"], g["positions"], g["logits"]
+
+
 def assert_bits_equal(got, want, what="", nan_equal=False):
     got = np.ascontiguousarray(got, dtype=np.float32)
     want = np.ascontiguousarray(want, dtype=np.float32)

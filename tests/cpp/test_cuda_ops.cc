@@ -636,6 +636,84 @@ void GpuAttentionBatched() {
                                                       H, KV, hd); }, "out of range");
 }
 
+// The batched layer (include/cuda_forward.h): one call over T tokens equals
+// T single-token calls at the same positions (the reference's own batch
+// test, test/forward_test.cc:118-183), for the decode (head_dim 32) and the
+// prefill (head_dim 64) attention kernels, fp32 and Q8_0 weights with a q
+// bias, within the reference's device-forward tolerance 1e-5 + 1e-4 |x|
+// (test/forward_test.cc:276-285).
+void GpuForwardLayerBatched() {
+    for (const int hd : {32, 64}) {
+        for (QuantType t : {QuantType::kF32, QuantType::kQ80}) {
+            CudaLayerConfig c;
+            c.dim = 128;
+            c.hidden_dim = 200;
+            c.n_heads = 4;
+            c.n_kv_heads = 2;
+            c.head_dim = hd;
+            c.rope_theta = 10000.0f;
+            const int T = 20, S = 32, QD = c.n_heads * hd, KD = c.n_kv_heads * hd;
+            std::vector<CudaTensor> keep;
+            std::vector<CudaDeviceBuffer> blocks;
+            auto weight = [&](int out, int in, uint64_t seed) {
+                CudaLinearWeight w;
+                w.type = t;
+                keep.push_back(TensorHostToDevice(Random({out, in}, seed, 0.0f, 0.05f)));
+                if (t == QuantType::kF32) {
+                    w.data = keep.back().GetData();
+                } else {
+                    blocks.push_back(CudaQuantizeDevice(keep.back(), t));
+                    w.data = blocks.back().GetData();
+                }
+                return w;
+            };
+            blocks.reserve(8);
+            keep.reserve(16);
+            CudaLayerWeights w;
+            w.wq = weight(QD, c.dim, 1);
+            w.wk = weight(KD, c.dim, 2);
+            w.wv = weight(KD, c.dim, 3);
+            w.wo = weight(c.dim, QD, 4);
+            w.w_gate = weight(c.hidden_dim, c.dim, 5);
+            w.w_up = weight(c.hidden_dim, c.dim, 6);
+            w.w_down = weight(c.dim, c.hidden_dim, 7);
+            keep.push_back(TensorHostToDevice(Random({QD}, 8, 0.0f, 0.1f)));
+            w.wq.bias = static_cast<const float*>(keep.back().GetData());
+            keep.push_back(TensorHostToDevice(Random({c.dim}, 9, 1.0f, 0.1f)));
+            w.attention_norm = static_cast<const float*>(keep.back().GetData());
+            keep.push_back(TensorHostToDevice(Random({c.dim}, 10, 1.0f, 0.1f)));
+            w.ffn_norm = static_cast<const float*>(keep.back().GetData());
+            const Tensor x0 = Random({T, c.dim}, 11);
+            CudaCache batched(2, S, c.n_kv_heads, hd), single(2, S, c.n_kv_heads, hd);
+            batched.Clear();
+            single.Clear();
+            CudaTensor xb = TensorHostToDevice(x0);
+            CudaForwardLayerBatchDevice(c, w, xb, batched, 1, 0);
+            const Tensor got = xb.Download();
+            Tensor want({T, c.dim});
+            for (int i = 0; i < T; ++i) {
+                Tensor row({1, c.dim});
+                std::copy_n(x0.data.begin() + static_cast<size_t>(i) * c.dim, c.dim,
+                            row.data.begin());
+                CudaTensor xr = TensorHostToDevice(row);
+                CudaForwardLayerBatchDevice(c, w, xr, single, 1, i);
+                const Tensor r = xr.Download();
+                std::copy_n(r.data.begin(), c.dim, want.data.begin() + static_cast<size_t>(i) * c.dim);
+            }
+            for (size_t i = 0; i < want.data.size(); ++i) {
+                Require(std::isfinite(got.data[i]), "batched layer output finite");
+                Require(std::abs(got.data[i] - want.data[i]) <= 1e-5f + 1e-4f * std::abs(want.data[i]),
+                        "batched layer equals the token loop (hd " + std::to_string(hd) + ")");
+            }
+            RequireTensor(batched.ReadKey(1, T - 1), single.ReadKey(1, T - 1), "cache slot", 1e-5);
+            RequireError([&] { CudaForwardLayerBatchDevice(c, w, xb, batched, 1, S - 5); },
+                         "out of range");
+            RequireError([&] { CudaForwardLayerBatchDevice(c, w, xb, batched, 2, 0); },
+                         "layer 2 out of range");
+        }
+    }
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -658,6 +736,7 @@ int main(int argc, char** argv) {
         {"gpu.kv_cache", GpuKvCache},
         {"gpu.attention", GpuAttention},
         {"gpu.attention_batched", GpuAttentionBatched},
+        {"gpu.forward_layer_batched", GpuForwardLayerBatched},
     };
     return Run(argc, argv, cases);
 }

@@ -7,6 +7,7 @@
 // oracle (oracle/oracle.h), never from the code under test.
 #pragma once
 #include "include/cuda_attention.h"
+#include "include/cuda_forward.h"
 #include "include/cuda_kvcache.h"
 #include "include/cuda_ops.h"
 #include "oracle/oracle.h"

@@ -31,6 +31,10 @@ Fixture contents (numpy .npz, no pickles):
                    the cases of test/cuda_attention_test.cc:86-88 (their
                    sin / cos inputs) and on an N(0, 1) GQA case with
                    head_dim 128 (8 query heads over 2 KV heads, pos 63).
+  tiny_forward.npz the reference's tiny model (model/tinymodel, its float32
+                   weights as the model file holds them) and the logits of
+                   its own CPU forward pass (the ForwardToken loop of
+                   ForwardBatch) for a 9-token prompt at positions 0..8.
 
 Usage: make_golden.py [name ...] writes only the named fixtures.
 """
@@ -265,8 +269,63 @@ def attention(ref):
     return out
 
 
+REF_ROOT = os.environ.get("MINILAMMA_REFERENCE", "/root/reference")  # the reference tree
+TINY_DIR = os.path.join(REF_ROOT, "model", "tinymodel")
+TINY_TOKENS = [128, 104, 101, 108, 108, 111, 32, 119, 111]  # BOS "hello wo"
+
+
+def tiny_model():
+    """The reference's tiny model (model/tinymodel: model.json lists the
+    tensors, model.bin holds them as raw little-endian float32) in
+    oracle.forward_model layout."""
+    import json
+    with open(os.path.join(TINY_DIR, "model.json")) as f:
+        meta = json.load(f)
+    raw = np.fromfile(os.path.join(TINY_DIR, "model.bin"), dtype="<f4")
+    t = {e["name"]: raw[e["offset"] // 4:(e["offset"] + e["byte_size"]) // 4].reshape(e["shape"])
+         for e in meta["tensors"]}
+    c = meta["config"]
+    config = dict(vocab=c["vocab_size"], dim=c["dim"], hidden_dim=c["hidden_dim"],
+                  layers=c["layers"], n_heads=c["n_heads"], n_kv_heads=c["n_kv_heads"],
+                  head_dim=c["head_dim"], max_seq=c["max_seq_len"], rope_type=0,
+                  theta=c["rope_theta"], eps=c["rms_norm_eps"])
+    layers = []
+    for i in range(config["layers"]):
+        p = f"layers.{i}."
+        lw = {n: t[p + n].astype(np.float32) for n in ("attention_norm", "ffn_norm")}
+        for n in O.LINEAR_NAMES:
+            lw[n] = ("f32", t[p + n].astype(np.float32))
+        layers.append(lw)
+    return {"config": config, "embedding": t["token_embedding"].astype(np.float32),
+            "layers": layers, "final_norm": t["final_norm"].astype(np.float32),
+            "lm_head": ("f32", t["lm_head"].astype(np.float32))}
+
+
+def tiny_forward(ref):
+    """The reference's ForwardToken loop (its own CPU forward pass) on its
+    tiny model, for a 9-token prompt at positions 0..8: the weights (as the
+    model file holds them), the config and every step's logits."""
+    m = tiny_model()
+    out = {"config": np.array([m["config"][k] for k in ("vocab", "dim", "hidden_dim", "layers",
+                                                       "n_heads", "n_kv_heads", "head_dim",
+                                                       "max_seq", "rope_type")], np.int32),
+           "theta_eps": np.array([m["config"]["theta"], m["config"]["eps"]], np.float32),
+           "embedding": m["embedding"], "final_norm": m["final_norm"],
+           "lm_head": m["lm_head"][1]}
+    for i, lw in enumerate(m["layers"]):
+        for n in ("attention_norm", "ffn_norm"):
+            out[f"l{i}_{n}"] = lw[n]
+        for n in O.LINEAR_NAMES:
+            out[f"l{i}_{n}"] = lw[n][1]
+    out["tokens"] = np.array(TINY_TOKENS, np.int32)
+    out["positions"] = np.arange(len(TINY_TOKENS), dtype=np.int32)
+    out["logits"] = ref.forward_tokens(m, out["tokens"], out["positions"])
+    return out
+
+
 FIXTURES = (("tiny_chain", tiny_chain), ("quant", quant), ("dequant_kat", dequant_kat),
-            ("rows_8b_70b", rows_8b_70b), ("linear", linear), ("attention", attention))
+            ("rows_8b_70b", rows_8b_70b), ("linear", linear), ("attention", attention),
+            ("tiny_forward", tiny_forward))
 
 
 def main():

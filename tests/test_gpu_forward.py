@@ -1,0 +1,144 @@
+"""GPU parity of the batched forward pass (mlk_forward_layer_batch through
+cpp_minilamma_amd.forward.DeviceModel): the reference's ForwardBatch without
+its token loop.
+
+The bar is the reference's own for its device forward pass against its CPU
+one: |got - want| <= 1e-5 + 1e-4 |want| on every logit
+(test/forward_test.cc:276-285).  `want` is the reference's CPU forward
+pass: its own logits on its tiny model (tests/golden/tiny_forward.npz,
+written by the compiled reference), and elsewhere the oracle's restatement
+of the ForwardToken loop, which equals the compiled reference bit for bit
+(tests/test_oracle.py).  The reference's batch tests are mirrored: one batch
+equals prefill + single decode steps equals token by token
+(test/forward_test.cc:118-183).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import tiny_model
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_forward_close(got, want, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert np.isfinite(got).all(), f"{what}: non-finite"
+    err = np.abs(got - want)
+    lim = 1e-5 + 1e-4 * np.abs(want)
+    bad = err > lim
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {got.size} logits outside "
+                           f"1e-5 + 1e-4|x|; worst err {float(err.max()):.3e}")
+
+
+@pytest.fixture(scope="module")
+def fwd(mlk):
+    import importlib
+    return importlib.import_module(mlk.__name__ + ".forward")
+
+
+def test_tiny_model_batch_matches_reference(fwd):
+    """The reference's tiny model: the whole 9-token prompt as one batch
+    (GEMM linears, decode attention at head_dim 8) gives the logits the
+    reference's CPU forward pass gives for each token."""
+    model, tokens, positions, logits = tiny_model()
+    dm = fwd.DeviceModel(model)
+    got = dm.forward(tokens, pos0=0, all_logits=True)
+    assert_forward_close(got, logits, "batch of 9")
+
+
+def test_tiny_model_prefill_then_decode_and_token_by_token(fwd):
+    """test/forward_test.cc:118-183: a prefill batch followed by single
+    decode tokens, and every token alone, give the same logits."""
+    model, tokens, positions, logits = tiny_model()
+    dm = fwd.DeviceModel(model)
+    got = dm.forward(tokens[:6], pos0=0, all_logits=True)
+    assert_forward_close(got, logits[:6], "prefill of 6")
+    for t in range(6, len(tokens)):
+        assert_forward_close(dm.forward(tokens[t:t + 1], pos0=t), logits[t], f"decode {t}")
+    single = fwd.DeviceModel(model)
+    for t in range(len(tokens)):
+        assert_forward_close(single.forward(tokens[t:t + 1], pos0=t), logits[t], f"token {t}")
+
+
+CASES = [  # config overrides, weight type, biases, tokens in the prefill batch
+    (dict(dim=256, hidden_dim=512, n_heads=4, n_kv_heads=2, head_dim=64), "f32", True, 40),
+    (dict(dim=256, hidden_dim=512, n_heads=4, n_kv_heads=2, head_dim=64), "q8_0", True, 40),
+    (dict(dim=512, hidden_dim=768, n_heads=4, n_kv_heads=1, head_dim=128), "q4_0", False, 33),
+    (dict(dim=256, hidden_dim=384, n_heads=8, n_kv_heads=2, head_dim=32, rope_type=1), "q4_1",
+     True, 20),
+    (dict(dim=512, hidden_dim=1024, n_heads=8, n_kv_heads=8, head_dim=64, layers=3), "q8_0",
+     False, 64),
+]
+
+
+@pytest.mark.parametrize("over,wt,biases,T", CASES)
+def test_forward_batch_matches_oracle(orc, fwd, over, wt, biases, T):
+    """Random models (GQA, MQA, MHA; NeoX; head_dim 32 / 64 / 128 so both
+    attention kernels run; every weight type; q/k/v biases): a prefill batch
+    of T tokens, then 3 single decode tokens, against the reference's
+    ForwardToken loop over the same tokens."""
+    cfg = dict(vocab=300, layers=2, max_seq=128, rope_type=0, theta=10000.0, eps=1e-5)
+    cfg.update(over)
+    model = O.forward_model(cfg, seed=T + len(over), weight_type=wt, biases=biases)
+    rng = np.random.default_rng(T)
+    tokens = rng.integers(0, cfg["vocab"], T + 3).astype(np.int32)
+    positions = np.arange(T + 3, dtype=np.int32)
+    want, hidden = orc.forward_tokens(model, tokens, positions)
+    dm = fwd.DeviceModel(model)
+    x = dm.hidden(tokens[:T], pos0=0)
+    np.testing.assert_allclose(x.download(), hidden[:T, -1], rtol=1e-4, atol=1e-5,
+                               err_msg="residual stream after the last layer")
+    got = dm.logits(x, T).download()
+    assert_forward_close(got, want[:T], f"prefill {wt}")
+    for t in range(T, T + 3):
+        assert_forward_close(dm.forward(tokens[t:t + 1], pos0=t), want[t], f"decode {t}")
+
+
+def test_forward_batch_positions_with_gaps(orc, fwd):
+    """Increasing positions with gaps (the device positions array: RoPE,
+    cache slots and the decode attention kernel read it): equal to the token
+    loop at the same positions."""
+    cfg = dict(vocab=200, dim=256, hidden_dim=384, layers=2, n_heads=4, n_kv_heads=2,
+               head_dim=64, max_seq=256, rope_type=0, theta=10000.0, eps=1e-5)
+    model = O.forward_model(cfg, seed=3, weight_type="q8_0", biases=True)
+    tokens = np.arange(1, 25, dtype=np.int32) * 7 % 200
+    positions = np.cumsum(np.arange(1, 25) % 4 + 1).astype(np.int32) - 2
+    want, _ = orc.forward_tokens(model, tokens, positions)
+    dm = fwd.DeviceModel(model)
+    got = dm.logits(dm.hidden(tokens, positions=positions), len(tokens)).download()
+    assert_forward_close(got, want, "gapped positions")
+
+
+@pytest.mark.parametrize("qt", ["q8_0", "q4_0", "q4_1"])
+def test_forward_batch_quantized_token_table(orc, fwd, qt):
+    """The token table kept as GGUF-style blocks on the device and gathered
+    from them (the reference dequantizes it at load): same logits as the
+    token loop over the dequantized table."""
+    cfg = dict(vocab=257, dim=256, hidden_dim=384, layers=2, n_heads=4, n_kv_heads=2,
+               head_dim=64, max_seq=64, rope_type=0, theta=10000.0, eps=1e-5)
+    model = O.forward_model(cfg, seed=9, weight_type=qt, quant_embedding=qt)
+    tokens = np.array([256, 0, 17, 3, 200, 99, 5, 5, 8, 1, 2, 3, 4, 128, 64, 32, 1, 0],
+                      np.int32)
+    positions = np.arange(tokens.size, dtype=np.int32)
+    want, _ = orc.forward_tokens(model, tokens, positions)
+    dm = fwd.DeviceModel(model)
+    got = dm.forward(tokens, pos0=0, all_logits=True)
+    assert_forward_close(got, want, f"{qt} token table")
+
+
+def test_forward_layer_rejects(mlk, fwd):
+    cfg = dict(dim=64, hidden_dim=128, n_heads=4, n_kv_heads=3, head_dim=16, theta=1e4,
+               eps=1e-5)
+    w = fwd.LayerWeights()
+    x = mlk.DeviceBuffer.empty((4, 64))
+    kc = mlk.DeviceBuffer.empty((1, 16, 3, 16))
+    ws = mlk.DeviceBuffer(1 << 20, np.uint8)
+    with pytest.raises(mlk.MlkError, match="divide n_heads"):
+        fwd.forward_layer_batch(cfg, w, x, 4, kc, kc, 1, 16, 0, 16, ws)
+    cfg["n_kv_heads"] = 2
+    with pytest.raises(mlk.MlkError, match="norm weights"):
+        fwd.forward_layer_batch(cfg, w, x, 4, kc, kc, 1, 16, 0, 16, ws)

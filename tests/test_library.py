@@ -71,6 +71,8 @@ CPP_SURFACE = [
     "CudaCache::KData", "CudaCache::vData", "CudaCache::Bytes_", "CudaCache::Clear",
     "CudaCache::SlotOffsetBytes", "CudaKvWriteBatchDevice", "CudaAttentionBuilt",
     "CudaAttentionDecode", "CudaAttentionDevice", "CudaAttentionBatchDevice",
+    # include/cuda_forward.h
+    "CudaForwardLayerBatchDevice",
 ]
 
 

@@ -738,3 +738,74 @@ def test_attention_oracle_equals_compiled_reference_on_random_inputs(orc):
         kc, vc = cache_from_rows(orc, k, v, 2, pos + 3, 1)
         assert_bits_equal(orc.attention(q[None], kc, vc, 1, [pos])[0],
                           ref.attention(q, k, v, 2, pos + 3, 1, pos), f"{H}/{KV}/{hd}/{pos}")
+
+
+# ------------------------------------------------------------ forward pass
+
+from conftest import tiny_model  # noqa: E402
+
+
+def test_forward_tokens_matches_reference_tiny_model(orc):
+    """The restated ForwardToken loop reproduces the reference's own CPU
+    forward pass on its tiny model bit for bit (tests/golden/tiny_forward)."""
+    model, tokens, positions, logits = tiny_model()
+    got, hidden = orc.forward_tokens(model, tokens, positions)
+    assert_bits_equal(got, logits, "tiny model logits")
+    assert_bits_equal(hidden[:, 0], model["embedding"][tokens], "layer 0 input = embedding row")
+
+
+@pytest.mark.parametrize("mistake", O.FORWARD_MISTAKES)
+def test_forward_tokens_planted_mistakes_fail(orc, mistake):
+    """Each planted wiring mistake moves the logits of a random GQA model
+    (norm weights N(1, 0.1): the tiny model's are all 1, so a swap of its two
+    norms would not show) away from the pinned result."""
+    cfg = dict(vocab=131, dim=64, hidden_dim=100, layers=2, n_heads=4, n_kv_heads=2,
+               head_dim=16, max_seq=32, rope_type=0, theta=10000.0, eps=1e-5)
+    model = O.forward_model(cfg, seed=5, biases=True)
+    tokens, positions = np.array([1, 7, 99, 3, 60], np.int32), np.arange(5, dtype=np.int32)
+    want, _ = orc.forward_tokens(model, tokens, positions)
+    if O.reference_available():
+        assert_bits_equal(want, O.reference().forward_tokens(model, tokens, positions), "pin")
+    got, _ = orc.forward_tokens(model, tokens, positions, mistake=mistake)
+    assert np.abs(got - want).max() > 1e-4, mistake
+
+
+def test_forward_tokens_zero_blocks_keep_the_embedding(orc):
+    """Closed form of the wiring: with wo and w_down zero, both residual
+    adds add zero, so every layer passes the embedding row through and the
+    logits are lm_head . RmsNorm(embedding row)."""
+    model, tokens, positions, _ = tiny_model()
+    for lw in model["layers"]:
+        lw["wo"] = ("f32", np.zeros_like(lw["wo"][1]))
+        lw["w_down"] = ("f32", np.zeros_like(lw["w_down"][1]))
+    got, hidden = orc.forward_tokens(model, tokens, positions)
+    emb = model["embedding"][tokens]
+    for li in range(hidden.shape[1]):
+        assert_bits_equal(hidden[:, li], emb, f"residual stream at {li}")
+    c = model["config"]
+    want = orc.linear_f32(orc.rmsnorm(emb, model["final_norm"], c["eps"]), model["lm_head"][1])
+    assert_bits_equal(got, want, "logits")
+
+
+FORWARD_CASES = [  # config overrides, weight type, biases, positions
+    (dict(), "f32", False, "contiguous"),
+    (dict(n_kv_heads=2, head_dim=64, dim=128, hidden_dim=200), "q8_0", True, "contiguous"),
+    (dict(n_kv_heads=1, rope_type=1), "q4_0", False, "gaps"),
+    (dict(n_heads=6, n_kv_heads=3, head_dim=16, dim=96, layers=3), "q4_1", True, "contiguous"),
+]
+
+
+@needs_ref
+@pytest.mark.parametrize("over,wt,biases,pos_kind", FORWARD_CASES)
+def test_forward_tokens_matches_compiled_reference(orc, over, wt, biases, pos_kind):
+    """GQA / MQA / NeoX, quantized weights, q/k/v biases and increasing
+    positions with gaps: bit-identical to the compiled ForwardToken loop."""
+    cfg = dict(vocab=131, dim=32, hidden_dim=86, layers=2, n_heads=4, n_kv_heads=4, head_dim=8,
+               max_seq=64, rope_type=0, theta=10000.0, eps=1e-5)
+    cfg.update(over)
+    model = O.forward_model(cfg, seed=len(over) + 3, weight_type=wt, biases=biases)
+    tokens = np.array([5, 9, 100, 3, 7, 8, 64, 1, 2, 130], np.int32)
+    positions = (np.arange(10) if pos_kind == "contiguous"
+                 else np.array([0, 1, 3, 4, 9, 10, 11, 20, 21, 40])).astype(np.int32)
+    got, _ = orc.forward_tokens(model, tokens, positions)
+    assert_bits_equal(got, O.reference().forward_tokens(model, tokens, positions), "logits")
