@@ -66,27 +66,31 @@ __device__ inline float4 Mask4(float4 v, uint32_t m) {
 // An [R][32] fp32 tile of a row-major [rows, K] matrix (x, or fp32 W):
 // thread tid loads float4 (tid + 256 i) for i < R / 32, 8 per row, so 8
 // consecutive lanes read one row's 128 contiguous bytes.  Rows past `rows`
-// read row 0 and are zeroed.
+// read row 0 and are zeroed -- at Store, so that nothing consumes the
+// loaded values before the MFMAs of the stage in between have been issued.
 template <int R>
 struct F32Tile {
     static constexpr int kN = R / 32;
     float4 v[kN];
+    uint32_t keep;  // bit i: float4 i is in range
     __device__ void Load(const float* p, int64_t rows, int64_t K, int64_t r0, int64_t k0) {
+        keep = 0;
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
             const int idx = static_cast<int>(threadIdx.x) + kGemmThreads * i;
             const int64_t r = r0 + (idx >> 3);
             const int64_t c = k0 + 4 * (idx & 7);
             const bool ok = r < rows && c < K;
-            v[i] = Mask4(*reinterpret_cast<const float4*>(p + (ok ? r * K + c : 0)),
-                         ok ? ~0u : 0u);
+            keep |= static_cast<uint32_t>(ok) << i;
+            v[i] = *reinterpret_cast<const float4*>(p + (ok ? r * K + c : 0));
         }
     }
     __device__ void Store(float* s) const {
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
             const int idx = static_cast<int>(threadIdx.x) + kGemmThreads * i;
-            *reinterpret_cast<float4*>(s + (idx >> 3) * kLd + 4 * (idx & 7)) = v[i];
+            *reinterpret_cast<float4*>(s + (idx >> 3) * kLd + 4 * (idx & 7)) =
+                Mask4(v[i], ((keep >> i) & 1u) ? ~0u : 0u);
         }
     }
 };
@@ -170,6 +174,38 @@ struct WTile<kWF32> : F32Tile<kBN> {
     }
 };
 
+// Instruction order of one K stage (the scheduler's groups, in order): the
+// first half's operand reads; the next stage's global loads one per MFMA;
+// the second half's operand reads one per MFMA; the rest of the first
+// half's MFMAs; the next stage's LDS writes spread over the second half's
+// MFMAs.  Left to itself the scheduler sinks the global loads to their use
+// (the LDS writes after the MFMAs), which exposes the load latency every
+// stage; with the loads first and the writes last it serializes the
+// address and write work around the MFMA stream instead.
+template <int MI>
+__device__ inline void InterleaveStage() {
+    constexpr int kMfma = 0x008, kVmemRead = 0x020, kDsRead = 0x100, kDsWrite = 0x200;
+    constexpr int kOperands = MI + 4;   // b128 reads per half: MI x rows, 4 W rows
+    constexpr int kHalf = 16 * MI;      // MFMAs per half stage
+    __builtin_amdgcn_sched_group_barrier(kDsRead, kOperands, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kVmemRead, 1, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kOperands; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsRead, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(kMfma, kHalf - 8 - kOperands, 0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kMfma, kHalf / 8, 0);
+        __builtin_amdgcn_sched_group_barrier(kDsWrite, 1, 0);
+    }
+}
+
 // Workgroup (tile, split): split `sp` covers K stages [sp * per_split,
 // min((sp + 1) * per_split, all)); with one split it writes y (+ bias),
 // with more it writes its partial sums to partial[sp] ([T, O] each) for
@@ -245,6 +281,7 @@ __global__ __launch_bounds__(kGemmThreads) void GemmMfma(const float* __restrict
         }
         xt.Store(sm.x[buf ^ 1]);
         wt.Store(sm.w[buf ^ 1]);
+        InterleaveStage<MI>();
         __syncthreads();
     }
 
