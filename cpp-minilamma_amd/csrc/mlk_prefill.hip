@@ -28,7 +28,9 @@
 //   - O^T += V^T P^T: V read from LDS one float per lane and step (16
 //     consecutive dims per 16 lanes), 32 accumulators per lane at hd = 128.
 // Positions past the workgroup's last token are clamped on load and masked
-// (-inf score) per query.  FLOPs: 4 * hd * H * sum_t (pos0 + t + 1).
+// (-inf score) per query.  A wave whose head is past its group (head counts
+// per KV head that are not a multiple of 4) computes on head 0's query and
+// stores nothing: no branch around the loop body.  FLOPs: 4 * hd * H * sum_t (pos0 + t + 1).
 #include "mlk_attention.h"
 
 #include <cmath>
@@ -44,9 +46,40 @@ constexpr int kPfTile = 32;    // cache positions per K/V tile
 constexpr int kPfHeads = 4;    // query heads per workgroup, one per wave
 
 template <int HD>
-struct PrefillSmem {
+struct __align__(16) PrefillSmem {
     float k[2][kPfTile * (HD + 4)];
     float v[2][kPfTile * (HD + 4)];
+};
+
+// The next K and V tiles in registers: thread tid holds float4 tid + 256 i
+// of the [32][HD] tiles (positions past max_pos read max_pos's row).
+template <int HD>
+struct KvTile {
+    static constexpr int NL = kPfTile * HD / 4 / kPfThreads;
+    float4 k[NL], v[NL];
+    const float* kb;
+    const float* vb;
+    int64_t slot, max_pos;
+    __device__ void Load(int64_t p0) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kPfThreads * i;
+            const int64_t p = p0 + idx / (HD / 4);
+            const int64_t pos = p <= max_pos ? p : max_pos;
+            const int c4 = idx % (HD / 4);
+            k[i] = *reinterpret_cast<const float4*>(kb + pos * slot + 4 * c4);
+            v[i] = *reinterpret_cast<const float4*>(vb + pos * slot + 4 * c4);
+        }
+    }
+    __device__ void Store(float* ks, float* vs) const {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kPfThreads * i;
+            const int o = (idx / (HD / 4)) * (HD + 4) + 4 * (idx % (HD / 4));
+            *reinterpret_cast<float4*>(ks + o) = k[i];
+            *reinterpret_cast<float4*>(vs + o) = v[i];
+        }
+    }
 };
 
 template <int HD>
@@ -57,7 +90,6 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
 #pragma clang fp contract(off)
     constexpr int LD = HD + 4;
     constexpr int NC = HD / 16;                          // 16-dim chunks
-    constexpr int NL = kPfTile * HD / 4 / kPfThreads;    // float4 per thread per K (V) tile
     __shared__ PrefillSmem<HD> sm;
     const int group = H / KV;
     const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
@@ -83,29 +115,13 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
 #pragma unroll
     for (int c = 0; c < NC; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c);
 
-    const float* kb = kc + static_cast<int64_t>(g) * HD;
-    const float* vb = vc + static_cast<int64_t>(g) * HD;
-    float4 kr[NL], vr[NL];
-    auto load = [&](int64_t p0) {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int idx = static_cast<int>(threadIdx.x) + kPfThreads * i;
-            const int64_t p = p0 + idx / (HD / 4);
-            const int64_t pos = p <= max_pos ? p : max_pos;
-            const int c4 = idx % (HD / 4);
-            kr[i] = *reinterpret_cast<const float4*>(kb + pos * slot + 4 * c4);
-            vr[i] = *reinterpret_cast<const float4*>(vb + pos * slot + 4 * c4);
-        }
-    };
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int idx = static_cast<int>(threadIdx.x) + kPfThreads * i;
-            const int o = (idx / (HD / 4)) * LD + 4 * (idx % (HD / 4));
-            *reinterpret_cast<float4*>(&sm.k[buf][o]) = kr[i];
-            *reinterpret_cast<float4*>(&sm.v[buf][o]) = vr[i];
-        }
-    };
+    KvTile<HD> tile;
+    tile.kb = kc + static_cast<int64_t>(g) * HD;
+    tile.vb = vc + static_cast<int64_t>(g) * HD;
+    tile.slot = slot;
+    tile.max_pos = max_pos;
+    auto load = [&](int64_t p0) { tile.Load(p0); };
+    auto store = [&](int buf) { tile.Store(sm.k[buf], sm.v[buf]); };
 
     f32x4 acc[NC];  // O^T: acc[c][r] = dim 16c + 4 kq + r of query i16
 #pragma unroll
@@ -121,7 +137,7 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
         const int buf = static_cast<int>(it & 1);
         const int64_t p0 = it * kPfTile;
         load((it + 1 < n_tiles ? it + 1 : it) * kPfTile);
-        if (active) {
+        {  // idle waves (a head block past the group) compute too, unstored
             f32x4 s[2];
 #pragma unroll
             for (int pt = 0; pt < 2; ++pt) {
