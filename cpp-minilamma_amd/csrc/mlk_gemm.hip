@@ -341,6 +341,235 @@ SplitPlan PlanSplits(int64_t T, int64_t K, int64_t O) {
     return p;
 }
 
+// ------------------------------------------------------------- skinny
+// Few token rows: the weights dominate, so each wave streams its 16
+// output rows of W straight from HBM into MFMA B-operand registers (no LDS
+// round trip for W; non-temporal loads), eight 32-k stages in flight, and
+// only x, small and shared by the workgroup, goes through LDS.  A lane's
+// eight k-slots of a stage are consecutive (k = 8 * (lane / 16) + 0..7), so
+// an F32 row is read as whole 128-byte lines and a Q8_0 lane reads eight
+// consecutive code bytes; x is read from LDS in the same order, so every
+// product x[t, k] * w[o, k] is still formed once.  Workgroup = 4 waves =
+// 64 output rows x all T rows x one K chunk; the chunks' partial sums are
+// added by SplitKReduce in chunk order.
+
+constexpr int kSkThreads = 256;
+constexpr int kSkRows = 64;  // output rows per workgroup (16 per wave)
+
+template <int WT>
+struct WFrag;
+
+template <>
+struct WFrag<kWF32> {
+    static constexpr int kDepth = 4;  // stages per x chunk / in flight
+    f32x4 a, b;
+    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
+        const f32x4* p = reinterpret_cast<const f32x4*>(w + row * row_bytes) + (k + 8 * q) / 4;
+        a = __builtin_nontemporal_load(p);
+        b = __builtin_nontemporal_load(p + 1);
+    }
+    __device__ float Get(int j) const { return j < 4 ? a[j & 3] : b[j & 3]; }
+};
+
+template <>
+struct WFrag<MLK_Q8_0> {
+    static constexpr int kDepth = 8;
+    uint32_t d, c0, c1;  // the fp16 scale; codes 8q .. 8q + 7 of the block
+    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(w + row * row_bytes + (k / 32) * 34);
+        d = __builtin_nontemporal_load(p);
+        c0 = __builtin_nontemporal_load(p + 1 + 4 * q) |
+             (static_cast<uint32_t>(__builtin_nontemporal_load(p + 2 + 4 * q)) << 16);
+        c1 = __builtin_nontemporal_load(p + 3 + 4 * q) |
+             (static_cast<uint32_t>(__builtin_nontemporal_load(p + 4 + 4 * q)) << 16);
+    }
+    __device__ float Get(int j) const {
+        const uint32_t c = j < 4 ? c0 : c1;
+        const int32_t code = static_cast<int32_t>(c << (24 - 8 * (j & 3))) >> 24;
+        return HalfHw(d) * static_cast<float>(code);
+    }
+};
+
+template <>
+struct WFrag<MLK_Q4_0> {
+    static constexpr int kDepth = 8;
+    uint32_t d, c0, c1;  // the scale; code bytes 8 (q & 1) .. + 7 (nibble q >> 1)
+    int hi;
+    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(w + row * row_bytes + (k / 32) * 18);
+        const int o = 1 + 4 * (q & 1);
+        d = __builtin_nontemporal_load(p);
+        c0 = __builtin_nontemporal_load(p + o) |
+             (static_cast<uint32_t>(__builtin_nontemporal_load(p + o + 1)) << 16);
+        c1 = __builtin_nontemporal_load(p + o + 2) |
+             (static_cast<uint32_t>(__builtin_nontemporal_load(p + o + 3)) << 16);
+        hi = q >> 1;
+    }
+    __device__ float Get(int j) const {
+        const uint32_t byte = ((j < 4 ? c0 : c1) >> (8 * (j & 3))) & 0xFFu;
+        const int code = static_cast<int>(hi ? byte >> 4 : byte & 15u);
+        return HalfHw(d) * static_cast<float>(code - 8);
+    }
+};
+
+template <>
+struct WFrag<MLK_Q4_1> {
+    static constexpr int kDepth = 8;
+    uint32_t dm, c0, c1;  // d | m << 16; code bytes 8 (q & 1) .. + 7 (nibble q >> 1)
+    int hi;
+    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(w + row * row_bytes + (k / 32) * 20);
+        dm = __builtin_nontemporal_load(p);
+        c0 = __builtin_nontemporal_load(p + 1 + 2 * (q & 1));
+        c1 = __builtin_nontemporal_load(p + 2 + 2 * (q & 1));
+        hi = q >> 1;
+    }
+    __device__ float Get(int j) const {
+        const uint32_t byte = ((j < 4 ? c0 : c1) >> (8 * (j & 3))) & 0xFFu;
+        const float code = static_cast<float>(hi ? byte >> 4 : byte & 15u);
+        return __fadd_rn(__fmul_rn(HalfHw(dm & 0xFFFFu), code), HalfHw(dm >> 16));
+    }
+};
+
+// The x rows of one K chunk, [16 TT][chunk] in LDS (rows chunk + 4 floats
+// apart), staged through registers one chunk ahead.
+template <int TT, int CHUNK>
+struct XChunk {
+    static constexpr int kRows = 16 * TT;
+    static constexpr int kN = kRows * CHUNK / 4 / kSkThreads;  // 4-float vectors per thread
+    f32x4 v[kN];
+    __device__ void Load(const float* x, int64_t T, int64_t K, int64_t k0) {
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kSkThreads * i;
+            const int64_t t = idx / (CHUNK / 4);
+            const int64_t r = t < T ? t : T - 1;
+            v[i] = *reinterpret_cast<const f32x4*>(x + r * K + k0 + 4 * (idx % (CHUNK / 4)));
+        }
+    }
+    __device__ void Store(float* s) const {
+#pragma unroll
+        for (int i = 0; i < kN; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kSkThreads * i;
+            *reinterpret_cast<f32x4*>(s + (idx / (CHUNK / 4)) * (CHUNK + 4) +
+                                      4 * (idx % (CHUNK / 4))) = v[i];
+        }
+    }
+};
+
+// Workgroup (row group, chunk): 64 output rows over one K chunk of 32 D.
+// Every weight load and the chunk's x rows are issued before anything is
+// computed (one round of memory latency per workgroup); the chunk's sums go
+// to partial[chunk] for SplitKReduce, or straight to y (+ bias) when K is one
+// chunk.
+template <int WT, int TT>
+__global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict__ x,
+                                                         const uint8_t* __restrict__ w,
+                                                         const float* __restrict__ bias,
+                                                         float* __restrict__ y, int64_t T,
+                                                         int64_t K, int64_t O, int64_t row_bytes,
+                                                         int row_groups,
+                                                         float* __restrict__ partial) {
+    constexpr int D = WFrag<WT>::kDepth;
+    constexpr int kChunk = 32 * D;
+    __shared__ __align__(16) float xs[16 * TT * (kChunk + 4)];
+    const int rg = static_cast<int>(blockIdx.x) % row_groups;
+    const int sp = static_cast<int>(blockIdx.x) / row_groups;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int i16 = lane & 15, q = lane >> 4;
+    const int64_t row = static_cast<int64_t>(rg) * kSkRows + wave * 16 + i16;
+    const int64_t wrow = row < O ? row : O - 1;
+    const int64_t k0 = static_cast<int64_t>(sp) * kChunk;
+
+    WFrag<WT> ring[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u) ring[u].Load(w, wrow, row_bytes, k0 + 32 * u, q);
+    XChunk<TT, kChunk> xc;
+    xc.Load(x, T, K, k0);
+    xc.Store(xs);
+    __syncthreads();
+    f32x4 acc[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+        float xa[TT][8];
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+            const float* src = xs + (tt * 16 + i16) * (kChunk + 4) + 32 * u + 8 * q;
+            const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
+            const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xa[tt][e] = lo[e];
+                xa[tt][4 + e] = hi[e];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float wv = ring[u].Get(j);
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[tt][j], wv, acc[tt], 0, 0, 0);
+            }
+        }
+    }
+    if (row >= O) return;
+    float* out = partial != nullptr ? partial + sp * T * O : y;
+    const float b = partial == nullptr && bias != nullptr ? bias[row] : 0.0f;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t t = tt * 16 + 4 * q + r;
+            if (t < T) out[t * O + row] = acc[tt][r] + b;
+        }
+    }
+}
+
+int SkinnyChunk(int wt) { return wt == kWF32 ? 32 * WFrag<kWF32>::kDepth : 32 * 8; }
+
+// The skinny kernel takes one K chunk per workgroup: K / chunk splits.
+SplitPlan PlanSkinny(int wt, int64_t K, int64_t) {
+    const int64_t chunk = SkinnyChunk(wt);
+    SplitPlan p;
+    p.per_split = chunk;
+    p.splits = static_cast<int>(K / chunk);
+    return p;
+}
+
+// Where the skinny kernel measured faster than the tiled one on the 8B
+// layer's projections: Q4_0 up to 32 rows, Q4_1 up to 16 (the fewest weight
+// bytes per MFMA; Q8_0 and F32 stay tiled).
+bool SkinnyApplies(int wt, int64_t T, int64_t K) {
+    const bool rows = (wt == MLK_Q4_0 && T <= 32) || (wt == MLK_Q4_1 && T <= 16);
+    return rows && K % SkinnyChunk(wt) == 0 && K / SkinnyChunk(wt) <= 4096;
+}
+
+template <int TT>
+void LaunchSkinnyT(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
+                   const float* bias, float* y, int64_t T, int64_t K, int64_t O,
+                   int64_t row_bytes, int groups, float* partial) {
+    switch (wt) {
+        case MLK_Q8_0:
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q8_0, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias,
+                               y, T, K, O, row_bytes, groups, partial);
+            break;
+        case MLK_Q4_0:
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_0, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias,
+                               y, T, K, O, row_bytes, groups, partial);
+            break;
+        case MLK_Q4_1:
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_1, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias,
+                               y, T, K, O, row_bytes, groups, partial);
+            break;
+        default:
+            hipLaunchKernelGGL((GemmSkinny<kWF32, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias, y,
+                               T, K, O, row_bytes, groups, partial);
+            break;
+    }
+}
+
 template <int BM>
 void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
                  const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
@@ -367,18 +596,47 @@ void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t
 
 }  // namespace
 
-int64_t GemmWorkspaceBytes(int64_t T, int64_t K, int64_t O) {
-    const SplitPlan p = PlanSplits(T, K, O);
+int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O) {
+    const SplitPlan p = SkinnyApplies(wt, T, K) ? PlanSkinny(wt, K, O) : PlanSplits(T, K, O);
     return p.splits > 1 ? static_cast<int64_t>(p.splits) * T * O * 4 : 0;
 }
 
 // Launches GemmMfma for a shape the caller has validated: K % 4 == 0 and
 // x / fp32 W 16-byte aligned; for quantized W, K % 32 == 0 and W aligned to
 // its loads (2 bytes, 4 for Q4_1).  K is split over workgroups when the
-// workspace holds GemmWorkspaceBytes(T, K, O) bytes, else not.
+// workspace holds GemmWorkspaceBytes(wt, T, K, O) bytes, else not.  Shapes
+// SkinnyApplies accepts take GemmSkinny (when K is more than one chunk, only
+// with the workspace; without it the tiled kernel).
 mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, float* y,
                       int64_t T, int64_t K, int64_t O, int64_t row_bytes, void* workspace,
                       size_t workspace_bytes, hipStream_t s) {
+    const SplitPlan sk = PlanSkinny(wt, K, O);
+    const bool sk_ws = sk.splits == 1 ||
+                       (workspace != nullptr && Aligned(workspace, 16) &&
+                        workspace_bytes >= static_cast<size_t>(sk.splits) * T * O * 4);
+    if (SkinnyApplies(wt, T, K) && sk_ws) {
+        const SplitPlan plan = sk;
+        float* partial = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+        const int64_t groups = (O + kSkRows - 1) / kSkRows;
+        if (groups * plan.splits > 0x7FFFFFFF) {
+            return Fail(MLK_ERR_INVALID, "linear: %lld output rows exceed one launch",
+                        static_cast<long long>(O));
+        }
+        const dim3 grid(static_cast<unsigned>(groups * plan.splits));
+        const uint8_t* wb = static_cast<const uint8_t*>(w);
+        if (T <= 16) {
+            LaunchSkinnyT<1>(wt, grid, s, x, wb, bias, y, T, K, O, row_bytes,
+                             static_cast<int>(groups), partial);
+        } else {
+            LaunchSkinnyT<2>(wt, grid, s, x, wb, bias, y, T, K, O, row_bytes,
+                             static_cast<int>(groups), partial);
+        }
+        mlk_status st = CheckLaunch("GemmSkinny");
+        if (st != MLK_OK || partial == nullptr) return st;
+        hipLaunchKernelGGL(SplitKReduce, dim3(GridFor(T * O, kGemmThreads, 8)),
+                           dim3(kGemmThreads), 0, s, partial, plan.splits, bias, y, T, O);
+        return CheckLaunch("SplitKReduce");
+    }
     const int bm = TileRows(T);
     const int64_t tiles_m = (T + bm - 1) / bm;
     const int64_t tiles_n = (O + kBN - 1) / kBN;

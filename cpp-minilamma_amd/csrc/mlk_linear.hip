@@ -499,7 +499,15 @@ extern "C" {
 
 int64_t mlk_linear_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features) {
     if (rows < kGemmMinRows || rows <= 0 || in_features <= 0 || out_features <= 0) return 0;
-    return GemmWorkspaceBytes(rows, in_features, out_features);
+    // the plans differ by weight type (the skinny kernel's K chunk): the
+    // larger serves every type
+    int64_t most = 0;
+    for (const int wt : {kF32, static_cast<int>(MLK_Q8_0), static_cast<int>(MLK_Q4_0),
+                         static_cast<int>(MLK_Q4_1)}) {
+        const int64_t b = GemmWorkspaceBytes(wt, rows, in_features, out_features);
+        if (b > most) most = b;
+    }
+    return most;
 }
 
 mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_blocks,

@@ -68,11 +68,11 @@ __device__ inline float HalfHw(uint32_t h16) {
 // row_bytes per output row.  Needs K % 4 == 0 and 16-byte aligned x (and
 // fp32 W); quantized W needs K % 32 == 0 and its load alignment (2 bytes,
 // 4 for Q4_1).
-// K is split over workgroups when `workspace` holds GemmWorkspaceBytes(T,
+// K is split over workgroups when `workspace` holds GemmWorkspaceBytes(wt, T,
 // K, O) bytes (16-byte aligned), else not.
 mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, float* y,
                       int64_t T, int64_t K, int64_t O, int64_t row_bytes, void* workspace,
                       size_t workspace_bytes, hipStream_t s);
-int64_t GemmWorkspaceBytes(int64_t T, int64_t K, int64_t O);
+int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O);
 
 }  // namespace mlk

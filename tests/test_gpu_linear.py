@@ -129,6 +129,35 @@ def test_linear_gemm_shapes(mlk, orc, wt, shape):
         np.testing.assert_array_equal(outs[0], outs[1])
 
 
+SKINNY_SHAPES = [  # (out, in, rows): Q4_0 with 8..32 rows, Q4_1 with 8..16, in a multiple of 256,
+    # take the skinny kernel (the other types and rows run the tiled GEMM on the same shapes)
+    (4096, 4096, 8), (1024, 4096, 9), (100, 256, 16), (4097, 512, 17), (64, 4096, 31),
+    (14336, 4096, 32), (4096, 14336, 12), (130, 768, 25)]
+
+
+@pytest.mark.parametrize("wt", QT + ("f32",))
+@pytest.mark.parametrize("shape", SKINNY_SHAPES)
+def test_linear_skinny_shapes(mlk, orc, wt, shape):
+    """The skinny path (W streamed straight into MFMA registers): 16- and
+    32-row token tiles (rows 8..32, partial tiles), output counts not a
+    multiple of the 64-row workgroup (100, 130, 4097), one to 56 K chunks,
+    split-K over the workspace and unsplit."""
+    O, K, T = shape
+    rng = np.random.default_rng(O + 5 * K + T)
+    w = normal(rng, (O, K), 0.02)
+    x = normal(rng, (T, K))
+    bias = normal(rng, (O,), 0.1)
+    if wt == "f32":
+        ex, s = dot_exact(x, w, bias)
+    else:
+        blocks = orc.quantize(wt, w)
+        ex, s = dot_exact(x, orc.dequantize(wt, blocks, O, K), bias)
+    for workspace in ("auto", None):
+        got = (run_f32(mlk, x, w, bias, workspace=workspace) if wt == "f32" else
+               run_quant(mlk, wt, x, blocks, O, bias=bias, workspace=workspace))
+        assert_dot_close(got, ex, s, K + 1, f"{wt} {shape} workspace={workspace}")
+
+
 def test_linear_workspace_sizes(mlk):
     """The split-K workspace: none below 8 rows (GEMV) or when the tiles
     already fill the GPU, splits * rows * out * 4 bytes otherwise; a
