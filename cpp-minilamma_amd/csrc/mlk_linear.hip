@@ -17,7 +17,10 @@
 //
 // Decode-shaped calls (a few token rows, the forward pass's one-token
 // steps) are weight-streaming GEMVs bound by HBM: every weight byte is read
-// once, x stays in L1/L2.  Layout of the work (GemvSplitK):
+// once.  One token row of quantized weights with in_features % 64 == 0
+// takes GemvStream (two-block pieces per lane, x in LDS, described at the
+// kernel); other calls below 8 rows take GemvSplitK.  Layout of the work
+// (GemvSplitK):
 //   - a workgroup of four waves owns RW consecutive weight rows; the four
 //     waves split K: wave w takes spans w, w + 4, w + 8, ... (two spans per
 //     loop trip, so each lane has 2 * RW span loads in flight);
@@ -403,6 +406,286 @@ __global__ __launch_bounds__(kThreads) void GemvAnyKernel(
     }
 }
 
+// ------------------------------------------------------------ piece GEMV
+// Quantized weights with in_features % 64 == 0 and 4-byte aligned blocks:
+// a lane owns a piece -- two consecutive blocks of one weight row, 68 / 36 /
+// 40 bytes (Q8_0 / Q4_0 / Q4_1), read with 4-byte aligned 16-byte loads --
+// and the 64 lanes of a wave cover 4096 inputs of the row per pass, so a
+// wave reads a 4096-wide row as one contiguous run.  The loads are plain,
+// not non-temporal: a lane's 16-byte loads are 68 bytes apart, so each
+// cache line is read by several of a piece's loads, and a non-temporal
+// load, which does not keep the line in L1, fetches it again from L2 for
+// each (measured about 1.5x slower).  A wave owns R rows; the R pieces at
+// one position are decoded against the same x values.  Per block, the codes
+// are summed against x and the scale applied once, as in GemvSplitK; the
+// byte and nibble positions inside a piece are compile-time constants (one
+// v_cvt_f32_i32 with a byte select and one FMA per Q8_0 weight).  The
+// partial sums of the 64 lanes are added by one transpose-reduce.
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
+template <int QT>
+struct Piece;
+template <>
+struct Piece<MLK_Q8_0> {
+    static constexpr int kWords = 17;
+};
+template <>
+struct Piece<MLK_Q4_0> {
+    static constexpr int kWords = 9;
+};
+template <>
+struct Piece<MLK_Q4_1> {
+    static constexpr int kWords = 10;
+};
+
+template <int N>
+__device__ inline void LoadWords(const uint8_t* p, uint32_t (&w)[N]) {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i + 4 <= N; i += 4) {
+        const u32x4a v = *reinterpret_cast<const u32x4a*>(q + i);
+        w[i] = v.x;
+        w[i + 1] = v.y;
+        w[i + 2] = v.z;
+        w[i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = N / 4 * 4; i < N; ++i) w[i] = q[i];
+}
+
+// Byte `b` of a piece (static), as the word index and bit shift.
+__device__ constexpr int WordOf(int b) { return b / 4; }
+__device__ constexpr int ShiftOf(int b) { return 8 * (b % 4); }
+
+// x[t][32 blk .. + 31] of the lane's 64 inputs (xp[t]) into registers.
+template <int T>
+__device__ inline void LoadBlockX(const float* const (&xp)[T], int blk, float (&xv)[T][32]) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = *reinterpret_cast<const float4*>(xp[t] + 32 * blk + 4 * i);
+            xv[t][4 * i] = v.x;
+            xv[t][4 * i + 1] = v.y;
+            xv[t][4 * i + 2] = v.z;
+            xv[t][4 * i + 3] = v.w;
+        }
+    }
+}
+
+// acc[r][t] += block `blk` of the R pieces times xv[t] (that block's x).
+template <int QT, int R, int T, int blk>
+__device__ inline void PieceBlock(const uint32_t (&wd)[R][Piece<QT>::kWords],
+                                  const float (&xv)[T][32], float (&acc)[R][T]) {
+    if constexpr (QT == MLK_Q8_0) {
+        constexpr int base = 34 * blk;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float d = HalfHw(blk == 0 ? wd[r][0] & 0xFFFFu : wd[r][8] >> 16);
+            float sv[T];
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int b = base + 2 + i;
+                const float c = SByte(wd[r][WordOf(b)], ShiftOf(b) / 8);
+#pragma unroll
+                for (int t = 0; t < T; ++t) sv[t] = i == 0 ? c * xv[t][0] : fmaf(c, xv[t][i], sv[t]);
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[r][t] = fmaf(d, sv[t], acc[r][t]);
+        }
+    } else {
+        // byte j of the block's codes holds element j (low nibble) and j + 16
+        constexpr int base = QT == MLK_Q4_0 ? 18 * blk + 2 : 20 * blk + 4;
+        float xs[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            float a = xv[t][0];
+            a += xv[t][16];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) {
+                a += xv[t][j];
+                a += xv[t][16 + j];
+            }
+            xs[t] = a;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float sv[T];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int b = base + j;
+                const uint32_t word = wd[r][WordOf(b)];
+                const float lo = UByte(word & 0x0F0F0F0Fu, ShiftOf(b) / 8);
+                const float hi = UByte((word >> 4) & 0x0F0F0F0Fu, ShiftOf(b) / 8);
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    sv[t] = j == 0 ? lo * xv[t][0] : fmaf(lo, xv[t][j], sv[t]);
+                    sv[t] = fmaf(hi, xv[t][16 + j], sv[t]);
+                }
+            }
+            if constexpr (QT == MLK_Q4_0) {
+                const float d = HalfHw(blk == 0 ? wd[r][0] & 0xFFFFu : wd[r][4] >> 16);
+#pragma unroll
+                for (int t = 0; t < T; ++t) acc[r][t] = fmaf(d, fmaf(-8.0f, xs[t], sv[t]), acc[r][t]);
+            } else {
+                const uint32_t dm = wd[r][5 * blk];
+                const float d = HalfHw(dm & 0xFFFFu), m = HalfHw(dm >> 16);
+#pragma unroll
+                for (int t = 0; t < T; ++t) acc[r][t] = fmaf(m, xs[t], fmaf(d, sv[t], acc[r][t]));
+            }
+        }
+    }
+}
+
+// The streaming kernel: a workgroup of 8 waves requests its first weight
+// step, then copies x into LDS (input k at k + 4 (k / 64): each lane's 64
+// inputs start 68 floats after the previous lane's, so the 16-byte reads of
+// 16 lanes fall on 64 distinct banks).  Each wave then walks `per_wave`
+// consecutive groups of R rows, one step per (group, 4096-input pass), and
+// issues the next step's weight loads before computing the current step, so
+// the loads of one step overlap the decode and FMAs of the previous one.
+// Without that every wave loads, waits, then computes (measured: 8B layer,
+// Q8_0, 88 -> 68 us).  Loading two steps ahead measured slower than one.
+// Lanes past the row's last piece (K % 4096 != 0, kTail) read piece 0 with
+// their weight words masked to zero.
+constexpr int kStreamThreads = 512;
+constexpr int kStreamDepth = 1;  // steps loaded ahead of the one computed
+// (the kernel asks for 4 waves per SIMD, at most 128 VGPRs: two 8-wave
+// workgroups per CU)
+constexpr int kStreamWaves = kStreamThreads / kWave;
+
+__host__ __device__ inline int64_t XPad(int64_t k) { return k + 4 * (k / 64); }
+
+struct StreamStep {
+    int64_t row0;
+    int pass;
+    __device__ void Advance(int passes, int rows) {
+        if (++pass == passes) {
+            pass = 0;
+            row0 += rows;
+        }
+    }
+};
+
+// `live` false: a prefetch past the wave's last step, which every lane
+// points at the first piece of the matrix (one cache line, never used).
+template <int QT, int R, bool kTail>
+__device__ inline void StreamLoad(const uint8_t* w, int64_t row0, int64_t O, int64_t row_bytes,
+                                  int pass, int lane, int64_t pieces, bool live,
+                                  uint32_t (&wd)[R][Piece<QT>::kWords]) {
+    constexpr int PB = 4 * Piece<QT>::kWords;
+    const int64_t piece = static_cast<int64_t>(pass) * kWave + lane;
+    const bool ok = !kTail || piece < pieces;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + r < O ? row0 + r : O - 1;
+        LoadWords(live ? w + row * row_bytes + (ok ? piece : 0) * PB : w, wd[r]);
+    }
+    if constexpr (kTail) {
+        const uint32_t m = ok ? ~0u : 0u;
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int i = 0; i < Piece<QT>::kWords; ++i) wd[r][i] &= m;
+    }
+}
+
+template <int QT, int R, bool kTail>
+__device__ inline void StreamCompute(const uint32_t (&wd)[R][Piece<QT>::kWords],
+                                     const float* xs, int pass, int lane, int64_t pieces,
+                                     float (&acc)[R][1]) {
+    const int64_t piece = static_cast<int64_t>(pass) * kWave + lane;
+    const bool ok = !kTail || piece < pieces;
+    const float* const xp[1] = {xs + (ok ? XPad(64 * piece) : 0)};
+    float xv[1][32];
+    LoadBlockX(xp, 0, xv);
+    PieceBlock<QT, R, 1, 0>(wd, xv, acc);
+    LoadBlockX(xp, 1, xv);
+    PieceBlock<QT, R, 1, 1>(wd, xv, acc);
+}
+
+template <int R>
+__device__ inline void StreamFinish(float (&acc)[R][1], int64_t row0, int lane,
+                                    const float* __restrict__ bias, float* __restrict__ y,
+                                    int64_t O) {
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        v[r] = acc[r][0];
+        acc[r][0] = 0.0f;
+    }
+    const float tot = TransposeReduce<R>(v, lane);
+    if ((lane & (kWave / R - 1)) == 0) {
+        const int64_t row = row0 + ReduceIdx<R>(lane);
+        if (row < O) y[row] = bias != nullptr ? tot + bias[row] : tot;
+    }
+}
+
+template <int QT, int R, bool kTail>
+// w is not __restrict__: loads through a restrict-qualified read-only
+// pointer are marked invariant, and the compiler then sinks the first
+// steps' weight loads past the barrier to their first use.
+__global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* __restrict__ x,
+                                                             const uint8_t* w,
+                                                             const float* __restrict__ bias,
+                                                             float* __restrict__ y, int64_t K,
+                                                             int64_t O, int64_t row_bytes,
+                                                             int64_t groups, int per_wave) {
+    extern __shared__ __align__(16) float xs[];
+    const int lane = threadIdx.x % kWave;
+    // wave-uniform (scalar) loop bounds, so the step loop needs no exec masks
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    const int64_t g_first = (static_cast<int64_t>(blockIdx.x) * kStreamWaves + wave) * per_wave;
+    // a wave past the last group loads group 0 and leaves after the barrier
+    const int64_t g0 = g_first < groups ? g_first : 0;
+    const int64_t pieces = K / 64;
+    const int passes = static_cast<int>((pieces + kWave - 1) / kWave);
+    const int64_t n_steps = ((g0 + per_wave < groups ? g0 + per_wave : groups) - g0) * passes;
+    float acc[R][1];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r][0] = 0.0f;
+    // Steps in order: (rows g0 R .., pass 0 .. passes - 1), then the next
+    // group.  D + 1 register buffers: step st + D is loaded while step st is
+    // computed.  `ld` is the next step to load, `cur` the one computed.  The
+    // prefetches are unconditional (past the last step they read one shared
+    // line): a load issued on one path only makes the compiler wait for
+    // every outstanding load before the next step's arithmetic.
+    constexpr int D = kStreamDepth;
+    uint32_t wbuf[D + 1][R][Piece<QT>::kWords];
+    StreamStep ld{g0 * R, 0}, cur{g0 * R, 0};
+    // the first D steps are requested before x is copied to LDS, so the copy
+    // and the barrier overlap their latency
+    int64_t next = 0;  // the next step to load
+#pragma unroll
+    for (int b = 0; b < D; ++b) {
+        StreamLoad<QT, R, kTail>(w, ld.row0, O, row_bytes, ld.pass, lane, pieces, next < n_steps,
+                                 wbuf[b]);
+        ld.Advance(passes, R);
+        ++next;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    for (int64_t i = threadIdx.x; i < K / 4; i += kStreamThreads) {
+        *reinterpret_cast<float4*>(xs + XPad(4 * i)) = reinterpret_cast<const float4*>(x)[i];
+    }
+    __syncthreads();
+    if (g_first >= groups) return;
+    for (int64_t st = 0; st < n_steps; st += D + 1) {
+#pragma unroll
+        for (int b = 0; b <= D; ++b) {
+            StreamLoad<QT, R, kTail>(w, ld.row0, O, row_bytes, ld.pass, lane, pieces,
+                                     next < n_steps, wbuf[(b + D) % (D + 1)]);
+            ld.Advance(passes, R);
+            ++next;
+            __builtin_amdgcn_sched_barrier(0);
+            if (st + b < n_steps) {
+                StreamCompute<QT, R, kTail>(wbuf[b], xs, cur.pass, lane, pieces, acc);
+                if (cur.pass == passes - 1) StreamFinish<R>(acc, cur.row0, lane, bias, y, O);
+                cur.Advance(passes, R);
+            }
+        }
+    }
+}
+
 // c = a @ b for a [m, k], b [k, n]: 16 x 16 output tiles, k staged through
 // LDS in steps of 16 (the reference's Matmul is a test-surface op).
 constexpr int kMmTile = 16;
@@ -475,6 +758,38 @@ mlk_status GemvRows(const float* x, const uint8_t* w, const float* bias, float* 
         if (st != MLK_OK) return st;
     }
     return MLK_OK;
+}
+
+// One token row (the decode step) with in_features % 64 == 0, 4-byte
+// aligned blocks and x small enough for LDS; two or more rows take
+// GemvSplitK, whose registers hold several rows' x.  Each wave gets enough
+// row groups for about four waves per SIMD over the whole GPU.
+// Rows per wave: two for the Q4 formats (x read from LDS once per two rows);
+// one for Q8_0, whose double-buffered pieces would otherwise take 68
+// registers and leave one 8-wave workgroup per CU.
+template <int QT>
+constexpr int StreamRows() { return QT == MLK_Q8_0 ? 1 : 2; }
+
+bool StreamFits(int64_t K) { return K % 64 == 0 && XPad(K) * 4 <= 64 * 1024; }
+
+template <int QT>
+mlk_status GemvStreamLaunch(const float* x, const uint8_t* w, const float* bias, float* y,
+                            int64_t K, int64_t O, int64_t row_bytes, hipStream_t s) {
+    constexpr int R = StreamRows<QT>();
+    const int64_t groups = (O + R - 1) / R;
+    const int64_t want = static_cast<int64_t>(ComputeUnits()) * 16;
+    const int64_t per_wave = groups > want ? (groups + want - 1) / want : 1;
+    const int64_t waves = (groups + per_wave - 1) / per_wave;
+    const dim3 grid(static_cast<unsigned>((waves + kStreamWaves - 1) / kStreamWaves));
+    const size_t lds = static_cast<size_t>(XPad(K)) * 4;
+    if (K % 4096 != 0) {
+        hipLaunchKernelGGL((GemvStream<QT, R, true>), grid, dim3(kStreamThreads), lds, s, x, w,
+                           bias, y, K, O, row_bytes, groups, static_cast<int>(per_wave));
+    } else {
+        hipLaunchKernelGGL((GemvStream<QT, R, false>), grid, dim3(kStreamThreads), lds, s, x, w,
+                           bias, y, K, O, row_bytes, groups, static_cast<int>(per_wave));
+    }
+    return CheckLaunch("GemvStream");
 }
 
 // RW = 4 reuses each x slice over more rows; below 4096 outputs, RW = 2
@@ -550,6 +865,13 @@ mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_bl
     if (rows >= kGemmMinRows) {
         return LaunchGemm(quant_type, x, w_blocks, bias, y, rows, K, O, row_bytes, workspace,
                           workspace_bytes, s);
+    }
+    if (rows == 1 && StreamFits(K) && Aligned(w_blocks, 4)) {
+        switch (quant_type) {
+            case MLK_Q8_0: return GemvStreamLaunch<MLK_Q8_0>(x, w, bias, y, K, O, row_bytes, s);
+            case MLK_Q4_0: return GemvStreamLaunch<MLK_Q4_0>(x, w, bias, y, K, O, row_bytes, s);
+            default: return GemvStreamLaunch<MLK_Q4_1>(x, w, bias, y, K, O, row_bytes, s);
+        }
     }
     const int64_t nb = K / 32;
     switch (quant_type) {

@@ -91,6 +91,34 @@ def test_quant_linear_shapes(mlk, orc, qt, shape):
     assert_dot_close(orc.linear_quant(qt, x, blocks, O, bias=bias), ex, s, K + 1, "oracle")
 
 
+STREAM_SHAPES = [  # (out, in): one token row, in % 64 == 0 and x within 64 KiB of LDS
+    (14336, 4096), (4096, 14336), (8193, 8192), (5, 4160), (3, 64), (14337, 128),
+    (4096, 15360), (1, 4096), (300, 16384)]
+
+
+@pytest.mark.parametrize("qt", QT)
+@pytest.mark.parametrize("shape", STREAM_SHAPES)
+def test_quant_linear_decode_row(mlk, orc, qt, shape):
+    """One token row takes the streaming GEMV (two-block pieces per lane, x
+    in LDS, the next step's loads ahead of the current one): whole 4096-input
+    passes and a partial last pass (in 4160, 14336: lanes past the row's last
+    piece masked), several row groups per wave (out 14337 over in 128), odd
+    out with two rows per wave, and in 16384, whose x does not fit the LDS,
+    on the split-K kernel."""
+    O, K = shape
+    rng = np.random.default_rng(O + 3 * K)
+    w = normal(rng, (O, K), 0.02)
+    blocks = orc.quantize(qt, w)
+    x = normal(rng, (1, K))
+    bias = normal(rng, (O,), 0.1)
+    ex, s = dot_exact(x, orc.dequantize(qt, blocks, O, K), bias)
+    got = run_quant(mlk, qt, x, blocks, O, bias=bias)
+    assert_dot_close(got, ex, s, K + 1, f"{qt} {shape}")
+    got2 = run_quant(mlk, qt, x, blocks, O)
+    ex2, s2 = dot_exact(x, orc.dequantize(qt, blocks, O, K))
+    assert_dot_close(got2, ex2, s2, K, f"{qt} {shape} no bias")
+
+
 GEMM_SHAPES = [  # (out, in, rows): 8 rows and more take the matrix-core GEMM
     (4096, 4096, 128), (1024, 4096, 200), (131, 64, 32), (4097, 96, 33), (300, 4128, 257),
     (14336, 4096, 64), (4096, 14336, 96), (4096, 4096, 1024)]
@@ -191,11 +219,13 @@ def test_linear_gemm_f32_ragged_in(mlk):
 
 
 @pytest.mark.parametrize("qt", QT)
-def test_quant_linear_special_scales(mlk, orc, qt):
+@pytest.mark.parametrize("T", [1, 2])
+def test_quant_linear_special_scales(mlk, orc, qt, T):
     """Subnormal, zero and large fp16 scales (and Q4_1 minima) decode like the
-    CPU: blocks are hand-made, then checked against float64."""
+    CPU, on the streaming (one row) and split-K kernels: blocks are
+    hand-made, then checked against float64."""
     rng = np.random.default_rng(1)
-    O, K, T = 8, 256, 2
+    O, K = 8, 256
     blocks = orc.quantize(qt, normal(rng, (O, K), 0.02)).reshape(O, K // 32, -1).copy()
     scales = [0x0001, 0x03FF, 0x0000, 0x7BFF, 0x3C00, 0x8001, 0x0400, 0x1234]
     for j in range(O):
