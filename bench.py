@@ -641,9 +641,65 @@ def layer_bench(mlk, steps, path):
               f"TFLOP/s); token loop {loop_us:.0f} us/token", flush=True)
         x1.close()
         del keep
+    out["decode"] = decode_layer_bench(mlk, fwd, steps)
     out["cpu_reference"] = layer_cpu_reference(cfg)
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
+
+
+DECODE_COPIES = 4   # layers rotated per call: 4 x 232 MB of Q8_0 weights exceed the MALL
+DECODE_POS = 8191   # the token's position: it attends to 8192 cache rows
+
+
+def decode_layer_bench(mlk, fwd, steps):
+    """One decode step of one Llama-3-8B layer: a single token at position
+    8191 (the top of configs[1]'s position range) through
+    mlk_forward_layer_batch, rotating over DECODE_COPIES layers' weights and
+    caches so that every call reads its weights and K/V from HBM, timed
+    between two events.  Bytes = the layer's weights + the K/V rows
+    attended + activations (each read once)."""
+    cfg = dict(workloads.CONFIGS["c2_decode_8b"])
+    S = DECODE_POS + 1
+    cfg.update(hidden_dim=cfg["ffn"], max_seq=S)
+    D, KV, hd = cfg["dim"], cfg["n_kv_heads"], cfg["head_dim"]
+    st = mlk.Stream()
+    L = DECODE_COPIES
+    kc = mlk.DeviceBuffer.empty((L, S, KV, hd))
+    vc = mlk.DeviceBuffer.empty((L, S, KV, hd))
+    mlk.fill_normal(kc, L * S * KV * hd, 0.0, 0.02, 31)
+    mlk.fill_normal(vc, L * S * KV * hd, 0.0, 0.02, 32)
+    x = mlk.DeviceBuffer.empty((1, D))
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, S, True), np.uint8)
+    res = {"workload": f"one Llama-3-8B layer, one token at position {DECODE_POS} (8192 cache "
+                       f"rows), weights and caches of {L} layers rotated, weights N(0, 0.02)"}
+    for wt in ("q8_0", "q4_0", "f32"):
+        layers = [_device_layer(mlk, fwd, cfg, wt, 500 + 10 * i) for i in range(L)]
+        mlk.fill_normal(x, D, 0.0, 1.0, 23)
+
+        def run(i):
+            fwd.forward_layer_batch(cfg, layers[i][0], x, 1, kc, vc, L, S, i, S, ws,
+                                    pos0=DECODE_POS, stream=st)
+        for i in range(L):
+            run(i)
+        st.synchronize()
+        e0, e1 = mlk.Event(), mlk.Event()
+        e0.record(st)
+        for _ in range(steps):
+            for i in range(L):
+                run(i)
+        e1.record(st)
+        e1.synchronize()
+        us = e0.elapsed_ms(e1) / (steps * L) * 1e3
+        nb = sum(workloads.bytes_linear(wt, 1, k, o) for _, k, o in workloads.layer_linears(cfg))
+        nb += workloads.bytes_attention([DECODE_POS], cfg["n_heads"], KV, hd)
+        gbs = nb / (us * 1e-6) / 1e9
+        res[wt] = {"us_per_layer": round(us, 1), "bytes": nb, "GBps": round(gbs, 1),
+                   "frac_of_peak": round(gbs / workloads.HBM_PEAK_GBS, 4),
+                   "tokens_per_s_32_layers": round(1e6 / (32 * us), 1)}
+        print(f"decode layer {wt} at position {DECODE_POS}: {us:.1f} us ({gbs:.0f} GB/s, "
+              f"{1e6 / (32 * us):.0f} tokens/s over 32 layers)", flush=True)
+        del layers
+    return res
 
 
 def layer_cpu_reference(cfg, n_tokens=2):

@@ -18,7 +18,9 @@
 //
 // The path is HBM-bound: every attended K and V row is read once per
 // (token, KV head), 8 * head_dim bytes per position, and the arithmetic per
-// byte is a few flops.  Layout of the work (flash-decoding):
+// byte is a few flops.  head_dim 64 and 128 with a 16-byte aligned key cache
+// take AttnDecodeMf (matrix cores, described at the kernel); other head
+// dims take AttnSplit.  Layout of AttnSplit's work (flash-decoding):
 //   - a workgroup (4 waves) owns one token, one KV head, a block of up to
 //     GB query heads of that KV head's group, and a chunk of positions; it
 //     reads each K and V row of the chunk once for all GB heads (the
@@ -40,8 +42,12 @@
 
 #include <math.h>
 
+#include <utility>
+
 namespace mlk {
 namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kAttnThreads = 256;
 constexpr int kAttnWaves = kAttnThreads / kWave;
@@ -333,6 +339,239 @@ __global__ __launch_bounds__(kAttnThreads) void AttnSplit(AttnParams p) {
     }
 }
 
+// ------------------------------------------------------------ MFMA decode
+// head_dim 64 / 128: v_mfma_f32_4x4x1_16b_f32 (16 blocks of a 4 x 4 outer
+// product per instruction; block b's A values come from lanes 4b + i, or
+// with CBSZ = 4 from lanes 4 ABID + i for every block, B from lanes 4b + j,
+// and D[b][i][j] lands in lane 4b + j, register i).  A workgroup owns one
+// token, one KV head, a group of up to 4 of its query heads (the A rows) and
+// a chunk of positions; each wave takes tiles of 64 positions:
+//   scores   lane l = position p0 + l, register i = head i: for each head
+//            dim d one MFMA with A = q broadcast from the block of d (a
+//            register holds q of 4 heads x 16 dims, lane 4b + i = q[i][16k
+//            + b], selected by ABID = b) and B = the lane's own K[p][d].  No
+//            cross-lane sum: each lane streams its own K row.
+//   softmax  per head, the tile maximum by DPP row operations (no LDS), the
+//            running (m, l) rescaled by exp(m_old - m_new); l stays a per-lane
+//            partial sum until the end.
+//   values   p goes through 1 KB of the wave's LDS to lanes 4b + i = p_i(16R
+//            + b); then per position one MFMA per 64 head dims with A = p
+//            broadcast (ABID = position within the 16) and B = V[p][64 hh +
+//            lane] (coalesced 256-byte row segments): lane l, register i
+//            accumulates out[head i][64 hh + l].
+// The 4 waves' (m, l, out) are merged through LDS; chunks are combined by
+// AttnCombine as for AttnSplit.
+constexpr int kMfTile = 64;   // positions per tile: one per lane
+constexpr int kMfHeads = 4;   // query heads per workgroup: the MFMA's A rows
+
+template <int CTRL, int ROW_MASK>
+__device__ inline float Dpp(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL,
+                                                      ROW_MASK, 0xF, false));
+}
+
+// Maximum / sum over the 64 lanes (uniform result): xor 1 and 2 within
+// quads, mirrors within half-rows and rows, then row broadcasts into lane 63.
+__device__ inline float WaveMaxDpp(float v) {
+    v = fmaxf(v, Dpp<0xB1, 0xF>(v, v));
+    v = fmaxf(v, Dpp<0x4E, 0xF>(v, v));
+    v = fmaxf(v, Dpp<0x141, 0xF>(v, v));
+    v = fmaxf(v, Dpp<0x140, 0xF>(v, v));
+    v = fmaxf(v, Dpp<0x142, 0xA>(v, v));
+    v = fmaxf(v, Dpp<0x143, 0xC>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ inline float WaveSumDpp(float v) {
+    v += Dpp<0xB1, 0xF>(0.0f, v);
+    v += Dpp<0x4E, 0xF>(0.0f, v);
+    v += Dpp<0x141, 0xF>(0.0f, v);
+    v += Dpp<0x140, 0xF>(0.0f, v);
+    v += Dpp<0x142, 0xA>(0.0f, v);
+    v += Dpp<0x143, 0xC>(0.0f, v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ inline float Comp(const float4& v, int e) {
+    return e == 0 ? v.x : (e == 1 ? v.y : (e == 2 ? v.z : v.w));
+}
+
+// sc += q (4 heads x 16 dims, broadcast from block b for dim 16k + b) times
+// the lane's K at those dims, k4 = its float4 16k / 4 .. + 3.  ABID must be
+// a constant: the 16 instructions come from a parameter pack.
+template <int... Bs>
+__device__ inline f32x4 QkDims(float q, const float4* k4, f32x4 sc,
+                               std::integer_sequence<int, Bs...>) {
+    ((sc = __builtin_amdgcn_mfma_f32_4x4x1f32(q, Comp(k4[Bs / 4], Bs % 4), sc, 4, Bs, 0)), ...);
+    return sc;
+}
+
+// acc[hh] += p (4 heads, broadcast from block S = the position within the
+// 16) times V[position][64 hh + lane].
+template <int NH, int S>
+__device__ inline void PvOne(float pr, const float (&v)[NH], f32x4 (&acc)[NH]) {
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) {
+        acc[hh] = __builtin_amdgcn_mfma_f32_4x4x1f32(pr, v[hh], acc[hh], 4, S, 0);
+    }
+}
+
+template <int NH, int... Ss>
+__device__ inline void PvPositions(float pr, const float (&v)[16][NH], f32x4 (&acc)[NH],
+                                   std::integer_sequence<int, Ss...>) {
+    (PvOne<NH, Ss>(pr, v[Ss], acc), ...);
+}
+
+// V[ps][64 hh + lane] of the 16 positions from ps0 (rows past pos read row
+// pos; their weights are zero).
+template <int NH>
+__device__ inline void LoadMfV(const float* vbase, int64_t slot, int64_t ps0, int64_t pos,
+                               int lane, float (&v)[16][NH]) {
+#pragma unroll
+    for (int s2 = 0; s2 < 16; ++s2) {
+        const int64_t ps = ps0 + s2;
+        const int64_t pr = ps <= pos ? ps : pos;
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) v[s2][hh] = vbase[pr * slot + 64 * hh + lane];
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void AttnDecodeMf(AttnParams p, int tpw) {
+    constexpr int NK = HD / 4;   // float4 per K row
+    constexpr int NQ = HD / 16;  // q registers
+    constexpr int NH = HD / 64;  // 64-dim parts of the output
+    __shared__ __align__(16) float ptile[kAttnWaves][kMfTile * kMfHeads];
+    __shared__ float wm[kAttnWaves][kMfHeads], wl[kAttnWaves][kMfHeads];
+    __shared__ float wo[kAttnWaves][kMfHeads][HD];
+
+    const int c = static_cast<int>(blockIdx.x % p.n_chunks);
+    const int64_t t = blockIdx.x / p.n_chunks;
+    const int kvh = static_cast<int>(blockIdx.y) / p.n_hblk;
+    const int hb = static_cast<int>(blockIdx.y) % p.n_hblk;
+    const int h0 = kvh * p.group + hb * kMfHeads;
+    const int nh = min(kMfHeads, p.group - hb * kMfHeads);
+    const int32_t pos = TokenPos(p, t);
+    const int64_t j0 = static_cast<int64_t>(c) * p.chunk;
+    if (pos < 0 || pos >= p.max_ctx) {
+        if (c == 0) {
+            if (threadIdx.x == 0) RaiseFlag(p.err, 1);
+            if (p.n_chunks == 1) {
+                for (int e = threadIdx.x; e < nh * HD; e += kAttnThreads) {
+                    p.out[(t * p.H + h0 + e / HD) * HD + e % HD] = 0.0f;
+                }
+            }
+        }
+        return;
+    }
+    if (j0 > pos) return;  // chunk past the token's last position
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int bq = lane / 4, iq = lane % 4;
+
+    float qr[NQ];  // lane 4b + i: q[h0 + i][16k + b]
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const bool ok = iq < nh;
+        qr[k] = MaskF(p.q[t * p.q_stride + static_cast<int64_t>(h0 + (ok ? iq : 0)) * HD + 16 * k +
+                          bq],
+                      ok);
+    }
+    const float* kbase = p.kc + static_cast<int64_t>(kvh) * HD;
+    const float* vbase = p.vc + static_cast<int64_t>(kvh) * HD;
+    float m[kMfHeads], lsum[kMfHeads];
+    f32x4 acc[NH];
+#pragma unroll
+    for (int r = 0; r < kMfHeads; ++r) {
+        m[r] = -INFINITY;
+        lsum[r] = 0.0f;
+    }
+#pragma unroll
+    for (int hh = 0; hh < NH; ++hh) acc[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int tt = 0; tt < tpw; ++tt) {
+        const int64_t p0 = j0 + static_cast<int64_t>(tt * kAttnWaves + wave) * kMfTile;
+        if (p0 > pos) break;
+        const int64_t mine = p0 + lane;
+        const bool valid = mine <= pos;
+        const int64_t row = valid ? mine : pos;
+        // the lane's K row, then the first 16 positions' V values
+        float4 kr[NK];
+#pragma unroll
+        for (int e = 0; e < NK; ++e) {
+            kr[e] = *reinterpret_cast<const float4*>(kbase + row * p.slot + 4 * e);
+        }
+        float vr[4][16][NH];
+        LoadMfV<NH>(vbase, p.slot, p0 + 0, pos, lane, vr[0]);
+        LoadMfV<NH>(vbase, p.slot, p0 + 16, pos, lane, vr[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            sc = QkDims(qr[k], kr + 4 * k, sc, std::make_integer_sequence<int, 16>{});
+        }
+        LoadMfV<NH>(vbase, p.slot, p0 + 32, pos, lane, vr[2]);
+        LoadMfV<NH>(vbase, p.slot, p0 + 48, pos, lane, vr[3]);
+        float pv[kMfHeads];
+#pragma unroll
+        for (int r = 0; r < kMfHeads; ++r) {
+            const float sv = valid ? sc[r] * p.scale : -INFINITY;
+            const float mnew = fmaxf(m[r], WaveMaxDpp(sv));  // finite: lane 0 is valid
+            const float corr = m[r] == -INFINITY ? 0.0f : expf(m[r] - mnew);
+            pv[r] = valid ? expf(sv - mnew) : 0.0f;
+            lsum[r] = lsum[r] * corr + pv[r];
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) acc[hh][r] *= corr;
+            m[r] = mnew;
+        }
+        // p to lanes 4b + i = p_i(16 R + b) through the wave's LDS
+        float* pt = ptile[wave];
+        *reinterpret_cast<float4*>(pt + 4 * lane) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        float pr[4];
+#pragma unroll
+        for (int R = 0; R < 4; ++R) pr[R] = pt[kMfTile * R + lane];
+#pragma unroll
+        for (int R = 0; R < 4; ++R) {
+            PvPositions<NH>(pr[R], vr[R], acc, std::make_integer_sequence<int, 16>{});
+        }
+    }
+    // merge: l over lanes, then the 4 waves through LDS
+#pragma unroll
+    for (int r = 0; r < kMfHeads; ++r) {
+        const float L = WaveSumDpp(lsum[r]);
+        if (lane == 0) {
+            wm[wave][r] = m[r];
+            wl[wave][r] = L;
+        }
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) wo[wave][r][64 * hh + lane] = acc[hh][r];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < nh * HD; idx += kAttnThreads) {
+        const int r = idx / HD, d = idx % HD;
+        float M = wm[0][r];
+#pragma unroll
+        for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][r]);
+        float L = 0.0f, A = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kAttnWaves; ++w) {
+            const float f = wm[w][r] == -INFINITY ? 0.0f : expf(wm[w][r] - M);
+            L = fmaf(wl[w][r], f, L);
+            A = fmaf(wo[w][r][d], f, A);
+        }
+        const int64_t orow = t * p.H + h0 + r;
+        if (p.n_chunks == 1) {
+            p.out[orow * HD + d] = A / L;
+        } else {
+            p.ws_acc[(orow * p.n_chunks + c) * HD + d] = A;
+            if (d == 0) {
+                p.ws_ml[(orow * p.n_chunks + c) * 2] = M;
+                p.ws_ml[(orow * p.n_chunks + c) * 2 + 1] = L;
+            }
+        }
+    }
+}
+
 // out = sum_c acc_c exp(m_c - M) / sum_c l_c exp(m_c - M), M = max_c m_c,
 // over the chunks that hold positions 0..pos; one workgroup per (token,
 // query head).  The chunk weights exp(m_c - M) are computed once into LDS
@@ -413,6 +652,29 @@ int ChunkFor(int64_t max_ctx, int64_t base_blocks) {
     int chunk = 2048;
     while (chunk > 64 && base_blocks * ((max_ctx + chunk - 1) / chunk) < 512) chunk /= 2;
     return chunk;
+}
+
+// The MFMA kernel's launch: query heads in groups of 4; a workgroup's chunk
+// is 4 waves x tpw tiles of 64 positions, tpw 1 unless that makes more than
+// 16384 workgroups (then fewer partial results to combine).
+struct MfPlan {
+    int n_hblk, tpw, chunk;
+    int64_t nc;
+};
+
+bool MfSupported(int32_t head_dim) { return head_dim == 64 || head_dim == 128; }
+
+MfPlan PlanMf(int64_t n_tokens, int32_t n_kv_heads, int group, int64_t max_ctx) {
+    MfPlan m;
+    m.n_hblk = (group + kMfHeads - 1) / kMfHeads;
+    const int64_t base = n_tokens * n_kv_heads * m.n_hblk;
+    const int64_t per_tile = static_cast<int64_t>(kAttnWaves) * kMfTile;
+    int tpw = 1;
+    while (tpw < 32 && base * ((max_ctx + per_tile * tpw - 1) / (per_tile * tpw)) > 16384) tpw *= 2;
+    m.tpw = tpw;
+    m.chunk = static_cast<int>(per_tile * tpw);
+    m.nc = (max_ctx + m.chunk - 1) / m.chunk;
+    return m;
 }
 
 // Copies n_tokens rows of k and v into their cache slots.
@@ -516,7 +778,12 @@ int64_t mlk_attention_workspace_bytes(int64_t n_tokens, int32_t n_heads, int32_t
     const int group = n_heads / n_kv_heads;
     const int64_t base = n_tokens * n_kv_heads * ((group + HeadsPerBlock(group) - 1) / HeadsPerBlock(group));
     const int chunk = ChunkFor(max_ctx, base);
-    const int64_t nc = (max_ctx + chunk - 1) / chunk;
+    int64_t nc = (max_ctx + chunk - 1) / chunk;
+    if (MfSupported(head_dim)) {
+        // either kernel may run (the MFMA one needs a 16-byte aligned key cache)
+        const int64_t nmf = PlanMf(n_tokens, n_kv_heads, group, max_ctx).nc;
+        if (nmf > nc) nc = nmf;
+    }
     if (nc == 1) return 0;
     return n_tokens * n_heads * nc * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
 }
@@ -570,13 +837,16 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
                              head_dim, pos0, n_tokens, out, AsStream(stream));
     }
     const int group = n_heads / n_kv_heads;
-    const int gb = HeadsPerBlock(group);
+    const bool mf = MfSupported(head_dim) && Aligned(k_cache, 16);
+    const MfPlan mp = PlanMf(n_tokens, n_kv_heads, group, max_ctx);
+    const int gb = mf ? kMfHeads : HeadsPerBlock(group);
     const int n_hblk = (group + gb - 1) / gb;
     const int64_t base = n_tokens * n_kv_heads * n_hblk;
-    const int chunk = ChunkFor(max_ctx, base);
+    const int chunk = mf ? mp.chunk : ChunkFor(max_ctx, base);
     const int64_t nc = (max_ctx + chunk - 1) / chunk;
-    const int64_t need = mlk_attention_workspace_bytes(n_tokens, n_heads, n_kv_heads, head_dim,
-                                                       max_ctx);
+    const int64_t need = nc > 1 ? n_tokens * n_heads * nc * (head_dim + 2) *
+                                      static_cast<int64_t>(sizeof(float))
+                                : 0;
     if (nc > 1 && (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need ||
                    !Aligned(workspace, 4))) {
         return Fail(MLK_ERR_INVALID, "%s: workspace of %lld bytes needed (got %zu)", fn,
@@ -609,13 +879,22 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
     const dim3 grid(static_cast<unsigned>(n_tokens * nc), static_cast<unsigned>(n_kv_heads * n_hblk));
     const hipStream_t s = AsStream(stream);
     hipError_t e;
+    if (mf) {
+        if (head_dim == 64) {
+            hipLaunchKernelGGL(AttnDecodeMf<64>, grid, dim3(kAttnThreads), 0, s, p, mp.tpw);
+        } else {
+            hipLaunchKernelGGL(AttnDecodeMf<128>, grid, dim3(kAttnThreads), 0, s, p, mp.tpw);
+        }
+        e = hipGetLastError();
+    } else {
     switch (nq) {
         case 1: e = LaunchSplit<1>(gb, head_dim, grid, s, p); break;
         case 2: e = LaunchSplit<2>(gb, head_dim, grid, s, p); break;
         case 4: e = LaunchSplit<4>(gb, head_dim, grid, s, p); break;
         default: e = LaunchSplit<8>(gb, head_dim, grid, s, p); break;
     }
-    if (e != hipSuccess) return FromHip(e, "AttnSplit");
+    }
+    if (e != hipSuccess) return FromHip(e, mf ? "AttnDecodeMf" : "AttnSplit");
     if (nc > 1) {
         hipLaunchKernelGGL(AttnCombine, dim3(static_cast<unsigned>(n_tokens * n_heads)),
                            dim3(kAttnThreads), 0, s, p);
