@@ -149,6 +149,16 @@ __device__ inline float BlockMax(float v, float* scratch) {
 
 // Raises a device-side error flag (the flag is only ever set, never read
 // back here, so any nonzero store is enough).
+// SwiGLU of one element: s = g * (1 / (1 + exp(-g))) rounded to float, then
+// s * u (src/ops.cc:135-151), without contraction; shared by the element-wise
+// kernel and the fused gate/up GEMV so both round alike.
+__device__ inline float SwiGluF(float g, float u) {
+#pragma clang fp contract(off)
+    const float sig = 1.0f / (1.0f + expf(-g));
+    const float s = g * sig;
+    return s * u;
+}
+
 __device__ inline void RaiseFlag(int32_t* err, int32_t code) {
     if (err != nullptr) {
         atomicOr(err, code);

@@ -25,11 +25,7 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 4;
 
 struct SwiGluOp {
-    __device__ float operator()(float g, float u) const {
-        const float sig = 1.0f / (1.0f + expf(-g));
-        const float s = g * sig;
-        return s * u;
-    }
+    __device__ float operator()(float g, float u) const { return SwiGluF(g, u); }
 };
 struct SiluOp {
     __device__ float operator()(float x, float) const {

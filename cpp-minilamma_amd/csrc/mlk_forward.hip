@@ -3,7 +3,9 @@
 // ForwardLayer :385-414) for all T tokens at once, which replaces the token
 // loop of ForwardBatch (:473-488) layer by layer.
 //
-// Per layer, on one stream (x [T, dim] is the residual stream, in place):
+// Per layer, on one stream (x [T, dim] is the residual stream, in place;
+// for one token with quantized weights q/k/v are one launch, gate/up carry
+// the SwiGLU and the down projection adds into x, see below):
 //   h = RmsNorm(x, attention_norm)                    mlk_rmsnorm_f32
 //   q, k, v = h W^T (+ bias)                          mlk_linear_* (GEMM from 8 rows)
 //   RoPE(q, k) at each token's position               mlk_rope_f32
@@ -26,6 +28,7 @@
 // h, q, k, v, a, a Wo^T, gate, up, then the linear layers' split-K scratch
 // and the decode attention's chunk scratch, each 256-byte aligned.
 #include "mlk_common.h"
+#include "mlk_quant.h"
 
 namespace mlk {
 namespace {
@@ -77,6 +80,16 @@ mlk_status Linear(const mlk_linear_weight& w, const float* x, float* y, int64_t 
                               ws_bytes, stream);
     }
     return mlk_linear_quant(w.type, x, w.data, w.bias, y, T, in, out, ws, ws_bytes, stream);
+}
+
+// A weight the one-row streaming GEMV takes (quantized, in_features a
+// multiple of 64 that fits its LDS, 4-byte aligned blocks).
+bool RowStreamable(const mlk_linear_weight& w, int64_t in) {
+    return w.type != kLinearF32 && StreamFits(in) && Aligned(w.data, 4);
+}
+
+StreamSeg Seg(const mlk_linear_weight& w, float* y, int64_t rows, const float* res = nullptr) {
+    return StreamSeg{static_cast<const uint8_t*>(w.data), w.bias, y, res, rows, 0};
 }
 
 mlk_status CheckConfig(const char* fn, const mlk_layer_config* c) {
@@ -172,10 +185,31 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         const mlk_status s_ = (call); \
         if (s_ != MLK_OK) return s_;  \
     } while (0)
+    // One token (the decode step) with quantized weights: q, k and v in one
+    // launch, gate and up with SwiGLU in the epilogue, and the down
+    // projection adding into x (the same per-element arithmetic as the
+    // separate kernels).
+    const hipStream_t hs = AsStream(stream);
+    const bool row = T == 1;
+    const bool qkv1 = row && w->wq.type == w->wk.type && w->wq.type == w->wv.type &&
+                      RowStreamable(w->wq, D) && RowStreamable(w->wk, D) &&
+                      RowStreamable(w->wv, D);
+    const bool ffn1 = row && w->w_gate.type == w->w_up.type && RowStreamable(w->w_gate, D) &&
+                      RowStreamable(w->w_up, D);
+    const bool down1 = row && RowStreamable(w->w_down, F);
     MLK_TRY(mlk_rmsnorm_f32(x, w->attention_norm, h, T, D, eps, stream));
-    MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
-    MLK_TRY(Linear(w->wk, h, k, T, D, KD, lin_ws, lin_b, stream));
-    MLK_TRY(Linear(w->wv, h, v, T, D, KD, lin_ws, lin_b, stream));
+    if (qkv1) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->wq, q, QD);
+        a.seg[1] = Seg(w->wk, k, KD);
+        a.seg[2] = Seg(w->wv, v, KD);
+        a.n_seg = 3;
+        MLK_TRY(LinearRowStream(w->wq.type, h, D, a, kStreamPlain, hs));
+    } else {
+        MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
+        MLK_TRY(Linear(w->wk, h, k, T, D, KD, lin_ws, lin_b, stream));
+        MLK_TRY(Linear(w->wv, h, v, T, D, KD, lin_ws, lin_b, stream));
+    }
     MLK_TRY(mlk_rope_f32(q, k, T, c.n_heads, c.n_kv_heads, c.head_dim, QD, KD, positions, pos0,
                          c.rope_theta, c.rope_type, err, stream));
     MLK_TRY(mlk_kv_write_f32(k_cache, v_cache, n_layers, max_seq, c.n_kv_heads, c.head_dim, layer,
@@ -185,11 +219,26 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
                                      a, att_ws, static_cast<size_t>(p.att_bytes), err, stream));
     MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
     MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
-    MLK_TRY(Linear(w->w_gate, h, gate, T, D, F, lin_ws, lin_b, stream));
-    MLK_TRY(Linear(w->w_up, h, up, T, D, F, lin_ws, lin_b, stream));
-    MLK_TRY(mlk_swiglu_f32(gate, up, gate, T * F, stream));
-    MLK_TRY(Linear(w->w_down, gate, proj, T, F, D, lin_ws, lin_b, stream));
-    MLK_TRY(mlk_add_f32(x, proj, x, T * D, stream));
+    if (ffn1) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->w_gate, gate, F);
+        a.seg[1] = Seg(w->w_up, gate, F);
+        a.n_seg = 2;
+        MLK_TRY(LinearRowStream(w->w_gate.type, h, D, a, kStreamSwiGlu, hs));
+    } else {
+        MLK_TRY(Linear(w->w_gate, h, gate, T, D, F, lin_ws, lin_b, stream));
+        MLK_TRY(Linear(w->w_up, h, up, T, D, F, lin_ws, lin_b, stream));
+        MLK_TRY(mlk_swiglu_f32(gate, up, gate, T * F, stream));
+    }
+    if (down1) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->w_down, x, D, x);
+        a.n_seg = 1;
+        MLK_TRY(LinearRowStream(w->w_down.type, gate, F, a, kStreamAdd, hs));
+    } else {
+        MLK_TRY(Linear(w->w_down, gate, proj, T, F, D, lin_ws, lin_b, stream));
+        MLK_TRY(mlk_add_f32(x, proj, x, T * D, stream));
+    }
 #undef MLK_TRY
     return MLK_OK;
 }

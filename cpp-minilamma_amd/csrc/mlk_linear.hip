@@ -556,30 +556,52 @@ constexpr int kStreamWaves = kStreamThreads / kWave;
 
 __host__ __device__ inline int64_t XPad(int64_t k) { return k + 4 * (k / 64); }
 
+__device__ inline const StreamSeg& SegAt(const StreamArgs& a, int s) {
+    return s == 0 ? a.seg[0] : (s == 1 ? a.seg[1] : a.seg[2]);
+}
+
 struct StreamStep {
+    int seg;
     int64_t row0;
     int pass;
-    __device__ void Advance(int passes, int rows) {
-        if (++pass == passes) {
-            pass = 0;
+    // The passes of a group in order, then: (plain, add) the next R rows,
+    // moving to the next segment at the end of one; (SwiGLU) the same rows of
+    // the up segment, then the next R rows of the gate segment.
+    template <int MODE>
+    __device__ void Advance(const StreamArgs& a, int passes, int rows) {
+        if (++pass < passes) return;
+        pass = 0;
+        if constexpr (MODE == kStreamSwiGlu) {
+            if (seg == 0) {
+                seg = 1;
+                return;
+            }
+            seg = 0;
             row0 += rows;
+            return;
+        }
+        row0 += rows;
+        if (row0 >= SegAt(a, seg).rows && seg + 1 < a.n_seg) {
+            ++seg;
+            row0 = 0;
         }
     }
 };
 
 // `live` false: a prefetch past the wave's last step, which every lane
-// points at the first piece of the matrix (one cache line, never used).
+// points at the first piece of the first matrix (one cache line, never used).
 template <int QT, int R, bool kTail>
-__device__ inline void StreamLoad(const uint8_t* w, int64_t row0, int64_t O, int64_t row_bytes,
-                                  int pass, int lane, int64_t pieces, bool live,
+__device__ inline void StreamLoad(const StreamArgs& a, const StreamStep& st, int64_t row_bytes,
+                                  int lane, int64_t pieces, bool live,
                                   uint32_t (&wd)[R][Piece<QT>::kWords]) {
     constexpr int PB = 4 * Piece<QT>::kWords;
-    const int64_t piece = static_cast<int64_t>(pass) * kWave + lane;
+    const StreamSeg& sg = SegAt(a, st.seg);
+    const int64_t piece = static_cast<int64_t>(st.pass) * kWave + lane;
     const bool ok = !kTail || piece < pieces;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const int64_t row = row0 + r < O ? row0 + r : O - 1;
-        LoadWords(live ? w + row * row_bytes + (ok ? piece : 0) * PB : w, wd[r]);
+        const int64_t row = st.row0 + r < sg.rows ? st.row0 + r : sg.rows - 1;
+        LoadWords(live ? sg.w + row * row_bytes + (ok ? piece : 0) * PB : a.seg[0].w, wd[r]);
     }
     if constexpr (kTail) {
         const uint32_t m = ok ? ~0u : 0u;
@@ -604,10 +626,12 @@ __device__ inline void StreamCompute(const uint32_t (&wd)[R][Piece<QT>::kWords],
     PieceBlock<QT, R, 1, 1>(wd, xv, acc);
 }
 
-template <int R>
-__device__ inline void StreamFinish(float (&acc)[R][1], int64_t row0, int lane,
-                                    const float* __restrict__ bias, float* __restrict__ y,
-                                    int64_t O) {
+// The R rows' sums over the wave, then the epilogue.  SwiGLU: the gate
+// segment's sums stay in `gate` (the lanes that will write each row hold
+// it) until the up segment's step for the same rows.
+template <int R, int MODE>
+__device__ inline void StreamFinish(float (&acc)[R][1], const StreamArgs& a, const StreamStep& st,
+                                    int lane, float& gate) {
     float v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -615,21 +639,31 @@ __device__ inline void StreamFinish(float (&acc)[R][1], int64_t row0, int lane,
         acc[r][0] = 0.0f;
     }
     const float tot = TransposeReduce<R>(v, lane);
-    if ((lane & (kWave / R - 1)) == 0) {
-        const int64_t row = row0 + ReduceIdx<R>(lane);
-        if (row < O) y[row] = bias != nullptr ? tot + bias[row] : tot;
+    const StreamSeg& sg = SegAt(a, st.seg);
+    const int64_t row = st.row0 + ReduceIdx<R>(lane);
+    const float val = row < sg.rows && sg.bias != nullptr ? tot + sg.bias[row] : tot;
+    if constexpr (MODE == kStreamSwiGlu) {
+        if (st.seg == 0) {
+            gate = val;
+            return;
+        }
+    }
+    if ((lane & (kWave / R - 1)) != 0 || row >= sg.rows) return;
+    if constexpr (MODE == kStreamSwiGlu) {
+        sg.y[row] = SwiGluF(gate, val);
+    } else if constexpr (MODE == kStreamAdd) {
+        sg.y[row] = sg.res[row] + val;
+    } else {
+        sg.y[row] = val;
     }
 }
 
-template <int QT, int R, bool kTail>
-// w is not __restrict__: loads through a restrict-qualified read-only
-// pointer are marked invariant, and the compiler then sinks the first
-// steps' weight loads past the barrier to their first use.
-__global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* __restrict__ x,
-                                                             const uint8_t* w,
-                                                             const float* __restrict__ bias,
-                                                             float* __restrict__ y, int64_t K,
-                                                             int64_t O, int64_t row_bytes,
+// x and the weights are not __restrict__: loads through restrict-qualified
+// read-only pointers are marked invariant, and the compiler then sinks the
+// first steps' weight loads past the barrier to their first use.
+template <int QT, int R, bool kTail, int MODE>
+__global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, StreamArgs a,
+                                                             int64_t K, int64_t row_bytes,
                                                              int64_t groups, int per_wave) {
     extern __shared__ __align__(16) float xs[];
     const int lane = threadIdx.x % kWave;
@@ -640,27 +674,40 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* __r
     const int64_t g0 = g_first < groups ? g_first : 0;
     const int64_t pieces = K / 64;
     const int passes = static_cast<int>((pieces + kWave - 1) / kWave);
-    const int64_t n_steps = ((g0 + per_wave < groups ? g0 + per_wave : groups) - g0) * passes;
+    const int per_group = MODE == kStreamSwiGlu ? 2 * passes : passes;
+    const int64_t n_steps = ((g0 + per_wave < groups ? g0 + per_wave : groups) - g0) * per_group;
+    // the first group's segment and row
+    StreamStep first{0, 0, 0};
+    if constexpr (MODE == kStreamSwiGlu) {
+        first.row0 = g0 * R;
+    } else {
+        int64_t g = g0;
+        while (first.seg + 1 < a.n_seg && g >= SegAt(a, first.seg).groups) {
+            g -= SegAt(a, first.seg).groups;
+            ++first.seg;
+        }
+        first.row0 = g * R;
+    }
     float acc[R][1];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r][0] = 0.0f;
-    // Steps in order: (rows g0 R .., pass 0 .. passes - 1), then the next
-    // group.  D + 1 register buffers: step st + D is loaded while step st is
-    // computed.  `ld` is the next step to load, `cur` the one computed.  The
-    // prefetches are unconditional (past the last step they read one shared
-    // line): a load issued on one path only makes the compiler wait for
-    // every outstanding load before the next step's arithmetic.
+    float gate = 0.0f;
+    // Steps in order (StreamStep::Advance).  D + 1 register buffers: step
+    // st + D is loaded while step st is computed.  `ld` is the next step to
+    // load, `cur` the one computed.  The prefetches are unconditional (past
+    // the last step they read one shared line): a load issued on one path
+    // only makes the compiler wait for every outstanding load before the next
+    // step's arithmetic.
     constexpr int D = kStreamDepth;
     uint32_t wbuf[D + 1][R][Piece<QT>::kWords];
-    StreamStep ld{g0 * R, 0}, cur{g0 * R, 0};
+    StreamStep ld = first, cur = first;
     // the first D steps are requested before x is copied to LDS, so the copy
     // and the barrier overlap their latency
     int64_t next = 0;  // the next step to load
 #pragma unroll
     for (int b = 0; b < D; ++b) {
-        StreamLoad<QT, R, kTail>(w, ld.row0, O, row_bytes, ld.pass, lane, pieces, next < n_steps,
-                                 wbuf[b]);
-        ld.Advance(passes, R);
+        StreamLoad<QT, R, kTail>(a, ld, row_bytes, lane, pieces, next < n_steps, wbuf[b]);
+        ld.Advance<MODE>(a, passes, R);
         ++next;
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -672,15 +719,15 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* __r
     for (int64_t st = 0; st < n_steps; st += D + 1) {
 #pragma unroll
         for (int b = 0; b <= D; ++b) {
-            StreamLoad<QT, R, kTail>(w, ld.row0, O, row_bytes, ld.pass, lane, pieces,
-                                     next < n_steps, wbuf[(b + D) % (D + 1)]);
-            ld.Advance(passes, R);
+            StreamLoad<QT, R, kTail>(a, ld, row_bytes, lane, pieces, next < n_steps,
+                                     wbuf[(b + D) % (D + 1)]);
+            ld.Advance<MODE>(a, passes, R);
             ++next;
             __builtin_amdgcn_sched_barrier(0);
             if (st + b < n_steps) {
                 StreamCompute<QT, R, kTail>(wbuf[b], xs, cur.pass, lane, pieces, acc);
-                if (cur.pass == passes - 1) StreamFinish<R>(acc, cur.row0, lane, bias, y, O);
-                cur.Advance(passes, R);
+                if (cur.pass == passes - 1) StreamFinish<R, MODE>(acc, a, cur, lane, gate);
+                cur.Advance<MODE>(a, passes, R);
             }
         }
     }
@@ -770,24 +817,38 @@ mlk_status GemvRows(const float* x, const uint8_t* w, const float* bias, float* 
 template <int QT>
 constexpr int StreamRows() { return QT == MLK_Q8_0 ? 1 : 2; }
 
-bool StreamFits(int64_t K) { return K % 64 == 0 && XPad(K) * 4 <= 64 * 1024; }
+template <int QT, int R, int MODE>
+void LaunchStreamT(dim3 grid, size_t lds, hipStream_t s, const float* x, const StreamArgs& a,
+                   int64_t K, int64_t row_bytes, int64_t groups, int per_wave) {
+    if (K % 4096 != 0) {
+        hipLaunchKernelGGL((GemvStream<QT, R, true, MODE>), grid, dim3(kStreamThreads), lds, s, x,
+                           a, K, row_bytes, groups, per_wave);
+    } else {
+        hipLaunchKernelGGL((GemvStream<QT, R, false, MODE>), grid, dim3(kStreamThreads), lds, s, x,
+                           a, K, row_bytes, groups, per_wave);
+    }
+}
 
 template <int QT>
-mlk_status GemvStreamLaunch(const float* x, const uint8_t* w, const float* bias, float* y,
-                            int64_t K, int64_t O, int64_t row_bytes, hipStream_t s) {
+mlk_status StreamLaunch(const float* x, StreamArgs a, int mode, int64_t K, int64_t row_bytes,
+                        hipStream_t s) {
     constexpr int R = StreamRows<QT>();
-    const int64_t groups = (O + R - 1) / R;
+    int64_t groups = 0;
+    for (int i = 0; i < a.n_seg; ++i) {
+        a.seg[i].groups = (a.seg[i].rows + R - 1) / R;
+        groups += a.seg[i].groups;
+    }
+    if (mode == kStreamSwiGlu) groups = a.seg[0].groups;
     const int64_t want = static_cast<int64_t>(ComputeUnits()) * 16;
     const int64_t per_wave = groups > want ? (groups + want - 1) / want : 1;
     const int64_t waves = (groups + per_wave - 1) / per_wave;
     const dim3 grid(static_cast<unsigned>((waves + kStreamWaves - 1) / kStreamWaves));
     const size_t lds = static_cast<size_t>(XPad(K)) * 4;
-    if (K % 4096 != 0) {
-        hipLaunchKernelGGL((GemvStream<QT, R, true>), grid, dim3(kStreamThreads), lds, s, x, w,
-                           bias, y, K, O, row_bytes, groups, static_cast<int>(per_wave));
-    } else {
-        hipLaunchKernelGGL((GemvStream<QT, R, false>), grid, dim3(kStreamThreads), lds, s, x, w,
-                           bias, y, K, O, row_bytes, groups, static_cast<int>(per_wave));
+    const int pw = static_cast<int>(per_wave);
+    switch (mode) {
+        case kStreamAdd: LaunchStreamT<QT, R, kStreamAdd>(grid, lds, s, x, a, K, row_bytes, groups, pw); break;
+        case kStreamSwiGlu: LaunchStreamT<QT, R, kStreamSwiGlu>(grid, lds, s, x, a, K, row_bytes, groups, pw); break;
+        default: LaunchStreamT<QT, R, kStreamPlain>(grid, lds, s, x, a, K, row_bytes, groups, pw); break;
     }
     return CheckLaunch("GemvStream");
 }
@@ -806,6 +867,29 @@ mlk_status Gemv(const float* x, const uint8_t* w, const float* bias, float* y, i
 }
 
 }  // namespace
+
+bool StreamFits(int64_t K) { return K % 64 == 0 && K > 0 && XPad(K) * 4 <= 64 * 1024; }
+
+mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
+                           hipStream_t s) {
+    if (qt < MLK_Q8_0 || qt > MLK_Q4_1 || !StreamFits(K) || !Aligned(x, 16) || a.n_seg < 1 ||
+        a.n_seg > 3 || (mode == kStreamSwiGlu && (a.n_seg != 2 || a.seg[0].rows != a.seg[1].rows))) {
+        return Fail(MLK_ERR_INVALID, "linear (one row): unsupported shape for the streaming kernel");
+    }
+    for (int i = 0; i < a.n_seg; ++i) {
+        if (a.seg[i].w == nullptr || !Aligned(a.seg[i].w, 4) || a.seg[i].y == nullptr ||
+            a.seg[i].rows <= 0 || (mode == kStreamAdd && a.seg[i].res == nullptr)) {
+            return Fail(MLK_ERR_INVALID, "linear (one row): bad segment %d", i);
+        }
+    }
+    const int64_t row_bytes = (K / 32) * BlockBytes(qt);
+    switch (qt) {
+        case MLK_Q8_0: return StreamLaunch<MLK_Q8_0>(x, a, mode, K, row_bytes, s);
+        case MLK_Q4_0: return StreamLaunch<MLK_Q4_0>(x, a, mode, K, row_bytes, s);
+        default: return StreamLaunch<MLK_Q4_1>(x, a, mode, K, row_bytes, s);
+    }
+}
+
 }  // namespace mlk
 
 using namespace mlk;
@@ -867,11 +951,10 @@ mlk_status mlk_linear_quant(int32_t quant_type, const float* x, const void* w_bl
                           workspace_bytes, s);
     }
     if (rows == 1 && StreamFits(K) && Aligned(w_blocks, 4)) {
-        switch (quant_type) {
-            case MLK_Q8_0: return GemvStreamLaunch<MLK_Q8_0>(x, w, bias, y, K, O, row_bytes, s);
-            case MLK_Q4_0: return GemvStreamLaunch<MLK_Q4_0>(x, w, bias, y, K, O, row_bytes, s);
-            default: return GemvStreamLaunch<MLK_Q4_1>(x, w, bias, y, K, O, row_bytes, s);
-        }
+        StreamArgs a{};
+        a.seg[0] = StreamSeg{w, bias, y, nullptr, O, 0};
+        a.n_seg = 1;
+        return LinearRowStream(quant_type, x, K, a, kStreamPlain, s);
     }
     const int64_t nb = K / 32;
     switch (quant_type) {

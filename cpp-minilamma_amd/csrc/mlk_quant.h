@@ -63,6 +63,33 @@ __device__ inline float HalfHw(uint32_t h16) {
     return static_cast<float>(v);
 }
 
+// One token row through the streaming GEMV (mlk_linear.hip), for up to three
+// weight matrices with the same in_features in one launch.  Segment i: its
+// blocks w (4-byte aligned), rows outputs y[0 .. rows) (+ bias), and for
+// kStreamAdd the residual res (y[row] = res[row] + sum; res may be y).
+// kStreamSwiGlu: segments 0 and 1 are gate and up with equal rows, y of
+// segment 1 receives SwiGlu(gate, up) (segment 0's y is not written).
+enum StreamMode { kStreamPlain = 0, kStreamAdd = 1, kStreamSwiGlu = 2 };
+
+struct StreamSeg {
+    const uint8_t* w;
+    const float* bias;
+    float* y;
+    const float* res;
+    int64_t rows;
+    int64_t groups;  // set by the launcher
+};
+
+struct StreamArgs {
+    StreamSeg seg[3];
+    int n_seg;
+};
+
+// in_features % 64 == 0 and x (16-byte aligned) fits the kernel's LDS
+bool StreamFits(int64_t K);
+mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
+                           hipStream_t s);
+
 // Prefill-shaped linear on the matrix cores (mlk_gemm.hip): y [T, O] =
 // x [T, K] W^T (+ bias), W fp32 (wt = -1) or MLK_Q8_0/Q4_0/Q4_1 blocks of
 // row_bytes per output row.  Needs K % 4 == 0 and 16-byte aligned x (and
