@@ -693,7 +693,7 @@ def decode_layer_bench(mlk, fwd, steps):
         nb = sum(workloads.bytes_linear(wt, 1, k, o) for _, k, o in workloads.layer_linears(cfg))
         nb += workloads.bytes_attention([DECODE_POS], cfg["n_heads"], KV, hd)
         gbs = nb / (us * 1e-6) / 1e9
-        res[wt] = {"us_per_layer": round(us, 1), "bytes": nb, "GBps": round(gbs, 1),
+        res[wt] = {"us": round(us, 1), "bytes": nb, "GBps": round(gbs, 1),
                    "frac_of_peak": round(gbs / workloads.HBM_PEAK_GBS, 4),
                    "tokens_per_s_32_layers": round(1e6 / (32 * us), 1)}
         print(f"decode layer {wt} at position {DECODE_POS}: {us:.1f} us ({gbs:.0f} GB/s, "
