@@ -344,98 +344,108 @@ SplitPlan PlanSplits(int64_t T, int64_t K, int64_t O) {
 // ------------------------------------------------------------- skinny
 // Few token rows: the weights dominate, so each wave streams its 16
 // output rows of W straight from HBM into MFMA B-operand registers (no LDS
-// round trip for W; non-temporal loads), eight 32-k stages in flight, and
-// only x, small and shared by the workgroup, goes through LDS.  A lane's
-// eight k-slots of a stage are consecutive (k = 8 * (lane / 16) + 0..7), so
-// an F32 row is read as whole 128-byte lines and a Q8_0 lane reads eight
-// consecutive code bytes; x is read from LDS in the same order, so every
-// product x[t, k] * w[o, k] is still formed once.  Workgroup = 4 waves =
-// 64 output rows x all T rows x one K chunk; the chunks' partial sums are
-// added by SplitKReduce in chunk order.
+// round trip for W), the whole chunk's loads in flight at once, and only x,
+// small and shared by the workgroup, goes through LDS.  Which inputs a
+// lane's k-slot takes per stage is set by WChunk (below); x is read from LDS
+// in the same order.  Workgroup = 4 waves = 64 output rows x all T rows x
+// one K chunk; the chunks' partial sums are added by SplitKReduce in chunk
+// order.
 
 constexpr int kSkThreads = 256;
 constexpr int kSkRows = 64;  // output rows per workgroup (16 per wave)
 
+// A lane's weights of one K chunk, and the chunk offset of the inputs its
+// k-slot takes in stage u (8 consecutive inputs per stage; A and B use the
+// same assignment, so each product x[t, k] * w[o, k] is formed once).
+//   F32    4 stages of 32 inputs: the lane's k-slot q reads 8q .. 8q + 7 of
+//          each 32 (two 16-byte non-temporal loads per stage).
+//   Q8_0 / Q4_0 / Q4_1   8 stages: the lane owns a piece, the two blocks 2q
+//          and 2q + 1 of the 8-block chunk (68 / 36 / 40 bytes, 4-byte
+//          aligned, read as 16-byte loads), and stage u takes its inputs
+//          8u .. 8u + 7; byte and nibble positions are compile-time constants.
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+
 template <int WT>
-struct WFrag;
+struct WChunk;
 
 template <>
-struct WFrag<kWF32> {
-    static constexpr int kDepth = 4;  // stages per x chunk / in flight
-    f32x4 a, b;
-    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
-        const f32x4* p = reinterpret_cast<const f32x4*>(w + row * row_bytes) + (k + 8 * q) / 4;
-        a = __builtin_nontemporal_load(p);
-        b = __builtin_nontemporal_load(p + 1);
+struct WChunk<kWF32> {
+    static constexpr int kStages = 4;
+    static constexpr bool kPieces = false;
+    f32x4 a[kStages], b[kStages];
+    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k0, int q) {
+#pragma unroll
+        for (int u = 0; u < kStages; ++u) {
+            const f32x4* p =
+                reinterpret_cast<const f32x4*>(w + row * row_bytes) + (k0 + 32 * u + 8 * q) / 4;
+            a[u] = __builtin_nontemporal_load(p);
+            b[u] = __builtin_nontemporal_load(p + 1);
+        }
     }
-    __device__ float Get(int j) const { return j < 4 ? a[j & 3] : b[j & 3]; }
+    __device__ float Get(int u, int j) const { return j < 4 ? a[u][j & 3] : b[u][j & 3]; }
+    __device__ static int XOff(int u, int q) { return 32 * u + 8 * q; }
+};
+
+template <int QT>
+struct PieceChunk {
+    static constexpr int kStages = 8;
+    static constexpr bool kPieces = true;
+    static constexpr int kBlock = QT == MLK_Q8_0 ? 34 : (QT == MLK_Q4_0 ? 18 : 20);
+    static constexpr int kWords = 2 * kBlock / 4;
+    uint32_t wd[kWords];
+    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k0, int q) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(w + row * row_bytes +
+                                                              (k0 / 32 + 2 * q) * kBlock);
+#pragma unroll
+        for (int i = 0; i + 4 <= kWords; i += 4) {
+            const u32x4a v = *reinterpret_cast<const u32x4a*>(p + i);
+            wd[i] = v.x;
+            wd[i + 1] = v.y;
+            wd[i + 2] = v.z;
+            wd[i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = kWords / 4 * 4; i < kWords; ++i) wd[i] = p[i];
+    }
+    __device__ uint32_t Byte(int b) const { return (wd[b / 4] >> (8 * (b % 4))) & 0xFFu; }
+    __device__ float Get(int u, int j) const {
+        const int e = 8 * u + j;  // input within the piece
+        const int blk = e / 32, i = e % 32;
+        if constexpr (QT == MLK_Q8_0) {
+            const uint32_t d = blk == 0 ? wd[0] & 0xFFFFu : wd[8] >> 16;
+            const int b = 34 * blk + 2 + i;
+            const int32_t code = static_cast<int32_t>(wd[b / 4] << (24 - 8 * (b % 4))) >> 24;
+            return HalfHw(d) * static_cast<float>(code);
+        } else if constexpr (QT == MLK_Q4_0) {
+            const uint32_t d = blk == 0 ? wd[0] & 0xFFFFu : wd[4] >> 16;
+            const uint32_t byte = Byte(18 * blk + 2 + i % 16);
+            const int code = static_cast<int>(i < 16 ? byte & 15u : byte >> 4);
+            return HalfHw(d) * static_cast<float>(code - 8);
+        } else {
+            const uint32_t dm = wd[5 * blk];
+            const uint32_t byte = Byte(20 * blk + 4 + i % 16);
+            const float code = static_cast<float>(i < 16 ? byte & 15u : byte >> 4);
+            return __fadd_rn(__fmul_rn(HalfHw(dm & 0xFFFFu), code), HalfHw(dm >> 16));
+        }
+    }
+    // inputs 64q + 8u .. of the chunk, in the padded LDS layout (4 floats
+    // after every 64, so the 4 k-slots' reads start on different banks)
+    __device__ static int XOff(int u, int q) { return 68 * q + 8 * u; }
 };
 
 template <>
-struct WFrag<MLK_Q8_0> {
-    static constexpr int kDepth = 8;
-    uint32_t d, c0, c1;  // the fp16 scale; codes 8q .. 8q + 7 of the block
-    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(w + row * row_bytes + (k / 32) * 34);
-        d = __builtin_nontemporal_load(p);
-        c0 = __builtin_nontemporal_load(p + 1 + 4 * q) |
-             (static_cast<uint32_t>(__builtin_nontemporal_load(p + 2 + 4 * q)) << 16);
-        c1 = __builtin_nontemporal_load(p + 3 + 4 * q) |
-             (static_cast<uint32_t>(__builtin_nontemporal_load(p + 4 + 4 * q)) << 16);
-    }
-    __device__ float Get(int j) const {
-        const uint32_t c = j < 4 ? c0 : c1;
-        const int32_t code = static_cast<int32_t>(c << (24 - 8 * (j & 3))) >> 24;
-        return HalfHw(d) * static_cast<float>(code);
-    }
-};
-
+struct WChunk<MLK_Q8_0> : PieceChunk<MLK_Q8_0> {};
 template <>
-struct WFrag<MLK_Q4_0> {
-    static constexpr int kDepth = 8;
-    uint32_t d, c0, c1;  // the scale; code bytes 8 (q & 1) .. + 7 (nibble q >> 1)
-    int hi;
-    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
-        const uint16_t* p = reinterpret_cast<const uint16_t*>(w + row * row_bytes + (k / 32) * 18);
-        const int o = 1 + 4 * (q & 1);
-        d = __builtin_nontemporal_load(p);
-        c0 = __builtin_nontemporal_load(p + o) |
-             (static_cast<uint32_t>(__builtin_nontemporal_load(p + o + 1)) << 16);
-        c1 = __builtin_nontemporal_load(p + o + 2) |
-             (static_cast<uint32_t>(__builtin_nontemporal_load(p + o + 3)) << 16);
-        hi = q >> 1;
-    }
-    __device__ float Get(int j) const {
-        const uint32_t byte = ((j < 4 ? c0 : c1) >> (8 * (j & 3))) & 0xFFu;
-        const int code = static_cast<int>(hi ? byte >> 4 : byte & 15u);
-        return HalfHw(d) * static_cast<float>(code - 8);
-    }
-};
-
+struct WChunk<MLK_Q4_0> : PieceChunk<MLK_Q4_0> {};
 template <>
-struct WFrag<MLK_Q4_1> {
-    static constexpr int kDepth = 8;
-    uint32_t dm, c0, c1;  // d | m << 16; code bytes 8 (q & 1) .. + 7 (nibble q >> 1)
-    int hi;
-    __device__ void Load(const uint8_t* w, int64_t row, int64_t row_bytes, int64_t k, int q) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(w + row * row_bytes + (k / 32) * 20);
-        dm = __builtin_nontemporal_load(p);
-        c0 = __builtin_nontemporal_load(p + 1 + 2 * (q & 1));
-        c1 = __builtin_nontemporal_load(p + 2 + 2 * (q & 1));
-        hi = q >> 1;
-    }
-    __device__ float Get(int j) const {
-        const uint32_t byte = ((j < 4 ? c0 : c1) >> (8 * (j & 3))) & 0xFFu;
-        const float code = static_cast<float>(hi ? byte >> 4 : byte & 15u);
-        return __fadd_rn(__fmul_rn(HalfHw(dm & 0xFFFFu), code), HalfHw(dm >> 16));
-    }
-};
+struct WChunk<MLK_Q4_1> : PieceChunk<MLK_Q4_1> {};
 
-// The x rows of one K chunk, [16 TT][chunk] in LDS (rows chunk + 4 floats
-// apart), staged through registers one chunk ahead.
-template <int TT, int CHUNK>
+// The x rows of one K chunk, [16 TT][chunk] in LDS (rows RS floats apart;
+// with kPad, input k of a row at k + 4 (k / 64)), staged through registers.
+template <int TT, int CHUNK, bool kPad>
 struct XChunk {
     static constexpr int kRows = 16 * TT;
+    static constexpr int RS = (kPad ? CHUNK + CHUNK / 16 : CHUNK) + 4;
     static constexpr int kN = kRows * CHUNK / 4 / kSkThreads;  // 4-float vectors per thread
     f32x4 v[kN];
     __device__ void Load(const float* x, int64_t T, int64_t K, int64_t k0) {
@@ -451,8 +461,9 @@ struct XChunk {
 #pragma unroll
         for (int i = 0; i < kN; ++i) {
             const int idx = static_cast<int>(threadIdx.x) + kSkThreads * i;
-            *reinterpret_cast<f32x4*>(s + (idx / (CHUNK / 4)) * (CHUNK + 4) +
-                                      4 * (idx % (CHUNK / 4))) = v[i];
+            const int k = 4 * (idx % (CHUNK / 4));
+            *reinterpret_cast<f32x4*>(s + (idx / (CHUNK / 4)) * RS + (kPad ? k + 4 * (k / 64) : k)) =
+                v[i];
         }
     }
 };
@@ -470,9 +481,11 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
                                                          int64_t K, int64_t O, int64_t row_bytes,
                                                          int row_groups,
                                                          float* __restrict__ partial) {
-    constexpr int D = WFrag<WT>::kDepth;
+    using WC = WChunk<WT>;
+    constexpr int D = WC::kStages;
     constexpr int kChunk = 32 * D;
-    __shared__ __align__(16) float xs[16 * TT * (kChunk + 4)];
+    using XC = XChunk<TT, kChunk, WC::kPieces>;
+    __shared__ __align__(16) float xs[16 * TT * XC::RS];
     const int rg = static_cast<int>(blockIdx.x) % row_groups;
     const int sp = static_cast<int>(blockIdx.x) / row_groups;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -481,10 +494,9 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
     const int64_t wrow = row < O ? row : O - 1;
     const int64_t k0 = static_cast<int64_t>(sp) * kChunk;
 
-    WFrag<WT> ring[D];
-#pragma unroll
-    for (int u = 0; u < D; ++u) ring[u].Load(w, wrow, row_bytes, k0 + 32 * u, q);
-    XChunk<TT, kChunk> xc;
+    WC wc;
+    wc.Load(w, wrow, row_bytes, k0, q);
+    XC xc;
     xc.Load(x, T, K, k0);
     xc.Store(xs);
     __syncthreads();
@@ -496,7 +508,7 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
         float xa[TT][8];
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
-            const float* src = xs + (tt * 16 + i16) * (kChunk + 4) + 32 * u + 8 * q;
+            const float* src = xs + (tt * 16 + i16) * XC::RS + WC::XOff(u, q);
             const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
             const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
@@ -507,7 +519,7 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float wv = ring[u].Get(j);
+            const float wv = wc.Get(u, j);
 #pragma unroll
             for (int tt = 0; tt < TT; ++tt) {
                 acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[tt][j], wv, acc[tt], 0, 0, 0);
@@ -527,7 +539,7 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
     }
 }
 
-int SkinnyChunk(int wt) { return wt == kWF32 ? 32 * WFrag<kWF32>::kDepth : 32 * 8; }
+int SkinnyChunk(int wt) { return wt == kWF32 ? 32 * WChunk<kWF32>::kStages : 32 * 8; }
 
 // The skinny kernel takes one K chunk per workgroup: K / chunk splits.
 SplitPlan PlanSkinny(int wt, int64_t K, int64_t) {
@@ -539,10 +551,9 @@ SplitPlan PlanSkinny(int wt, int64_t K, int64_t) {
 }
 
 // Where the skinny kernel measured faster than the tiled one on the 8B
-// layer's projections: Q4_0 up to 32 rows, Q4_1 up to 16 (the fewest weight
-// bytes per MFMA; Q8_0 and F32 stay tiled).
+// layer's projections: the quantized types up to 32 rows (F32 stays tiled).
 bool SkinnyApplies(int wt, int64_t T, int64_t K) {
-    const bool rows = (wt == MLK_Q4_0 && T <= 32) || (wt == MLK_Q4_1 && T <= 16);
+    const bool rows = wt != kWF32 && T <= 32;
     return rows && K % SkinnyChunk(wt) == 0 && K / SkinnyChunk(wt) <= 4096;
 }
 

@@ -157,8 +157,8 @@ def test_linear_gemm_shapes(mlk, orc, wt, shape):
         np.testing.assert_array_equal(outs[0], outs[1])
 
 
-SKINNY_SHAPES = [  # (out, in, rows): Q4_0 with 8..32 rows, Q4_1 with 8..16, in a multiple of 256,
-    # take the skinny kernel (the other types and rows run the tiled GEMM on the same shapes)
+SKINNY_SHAPES = [  # (out, in, rows): quantized weights with 8..32 rows, in a multiple of 256, take
+    # the skinny kernel (F32 runs the tiled GEMM on the same shapes)
     (4096, 4096, 8), (1024, 4096, 9), (100, 256, 16), (4097, 512, 17), (64, 4096, 31),
     (14336, 4096, 32), (4096, 14336, 12), (130, 768, 25)]
 
