@@ -649,15 +649,17 @@ def layer_bench(mlk, steps, path):
 
 DECODE_COPIES = 4   # layers rotated per call: 4 x 232 MB of Q8_0 weights exceed the MALL
 DECODE_POS = 8191   # the token's position: it attends to 8192 cache rows
+DECODE_BATCH = 16   # tokens of the batched decode case (configs[1] positions)
 
 
 def decode_layer_bench(mlk, fwd, steps):
-    """One decode step of one Llama-3-8B layer: a single token at position
-    8191 (the top of configs[1]'s position range) through
-    mlk_forward_layer_batch, rotating over DECODE_COPIES layers' weights and
-    caches so that every call reads its weights and K/V from HBM, timed
-    between two events.  Bytes = the layer's weights + the K/V rows
-    attended + activations (each read once)."""
+    """One decode step of one Llama-3-8B layer through mlk_forward_layer_batch:
+    a single token at position 8191 (the top of configs[1]'s position
+    range), and a batch of DECODE_BATCH tokens at positions uniform in
+    0..8191; rotating over DECODE_COPIES layers' weights and caches so that
+    every call reads its weights and K/V from HBM, timed between two events.
+    Bytes = the layer's weights + the K/V rows attended + activations (each
+    read once)."""
     cfg = dict(workloads.CONFIGS["c2_decode_8b"])
     S = DECODE_POS + 1
     cfg.update(hidden_dim=cfg["ffn"], max_seq=S)
@@ -672,32 +674,43 @@ def decode_layer_bench(mlk, fwd, steps):
     ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, S, True), np.uint8)
     res = {"workload": f"one Llama-3-8B layer, one token at position {DECODE_POS} (8192 cache "
                        f"rows), weights and caches of {L} layers rotated, weights N(0, 0.02)"}
+    # a batch of DECODE_BATCH tokens at positions uniform in [0, 8191]
+    rng = np.random.default_rng(42)
+    bpos = np.sort(rng.choice(S, DECODE_BATCH, replace=False)).astype(np.int32)
+    bpos[-1] = DECODE_POS
+    d_bpos = mlk.DeviceBuffer.from_array(bpos)
+    xb = mlk.DeviceBuffer.empty((DECODE_BATCH, D))
+    wsb = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, DECODE_BATCH, S, False), np.uint8)
     for wt in ("q8_0", "q4_0", "f32"):
         layers = [_device_layer(mlk, fwd, cfg, wt, 500 + 10 * i) for i in range(L)]
-        mlk.fill_normal(x, D, 0.0, 1.0, 23)
+        for T, xx, w_s, kw in ((1, x, ws, dict(pos0=DECODE_POS)),
+                               (DECODE_BATCH, xb, wsb, dict(positions=d_bpos))):
+            mlk.fill_normal(xx, T * D, 0.0, 1.0, 23)
 
-        def run(i):
-            fwd.forward_layer_batch(cfg, layers[i][0], x, 1, kc, vc, L, S, i, S, ws,
-                                    pos0=DECODE_POS, stream=st)
-        for i in range(L):
-            run(i)
-        st.synchronize()
-        e0, e1 = mlk.Event(), mlk.Event()
-        e0.record(st)
-        for _ in range(steps):
+            def run(i):
+                fwd.forward_layer_batch(cfg, layers[i][0], xx, T, kc, vc, L, S, i, S, w_s,
+                                        stream=st, **kw)
             for i in range(L):
                 run(i)
-        e1.record(st)
-        e1.synchronize()
-        us = e0.elapsed_ms(e1) / (steps * L) * 1e3
-        nb = sum(workloads.bytes_linear(wt, 1, k, o) for _, k, o in workloads.layer_linears(cfg))
-        nb += workloads.bytes_attention([DECODE_POS], cfg["n_heads"], KV, hd)
-        gbs = nb / (us * 1e-6) / 1e9
-        res[wt] = {"us": round(us, 1), "bytes": nb, "GBps": round(gbs, 1),
-                   "frac_of_peak": round(gbs / workloads.HBM_PEAK_GBS, 4),
-                   "tokens_per_s_32_layers": round(1e6 / (32 * us), 1)}
-        print(f"decode layer {wt} at position {DECODE_POS}: {us:.1f} us ({gbs:.0f} GB/s, "
-              f"{1e6 / (32 * us):.0f} tokens/s over 32 layers)", flush=True)
+            st.synchronize()
+            e0, e1 = mlk.Event(), mlk.Event()
+            e0.record(st)
+            for _ in range(steps):
+                for i in range(L):
+                    run(i)
+            e1.record(st)
+            e1.synchronize()
+            us = e0.elapsed_ms(e1) / (steps * L) * 1e3
+            nb = sum(workloads.bytes_linear(wt, T, k, o) for _, k, o in workloads.layer_linears(cfg))
+            nb += workloads.bytes_attention([DECODE_POS] if T == 1 else bpos, cfg["n_heads"], KV, hd)
+            gbs = nb / (us * 1e-6) / 1e9
+            key = wt if T == 1 else f"{wt}_T{T}"
+            res[key] = {"tokens": T, "us": round(us, 1), "bytes": nb, "GBps": round(gbs, 1),
+                        "frac_of_peak": round(gbs / workloads.HBM_PEAK_GBS, 4),
+                        "tokens_per_s_32_layers": round(T * 1e6 / (32 * us), 1)}
+            where = f"at position {DECODE_POS}" if T == 1 else "at positions uniform in 0..8191"
+            print(f"decode layer {wt}, {T} token(s) {where}: {us:.1f} us ({gbs:.0f} GB/s, "
+                  f"{T * 1e6 / (32 * us):.0f} tokens/s over 32 layers)", flush=True)
         del layers
     return res
 

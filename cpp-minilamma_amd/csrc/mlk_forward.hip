@@ -4,8 +4,8 @@
 // loop of ForwardBatch (:473-488) layer by layer.
 //
 // Per layer, on one stream (x [T, dim] is the residual stream, in place;
-// for one token with quantized weights q/k/v are one launch, gate/up carry
-// the SwiGLU and the down projection adds into x, see below):
+// for 1 and for 8..32 tokens with quantized weights q/k/v are one launch,
+// gate/up carry the SwiGLU and the down projection adds into x, see below):
 //   h = RmsNorm(x, attention_norm)                    mlk_rmsnorm_f32
 //   q, k, v = h W^T (+ bias)                          mlk_linear_* (GEMM from 8 rows)
 //   RoPE(q, k) at each token's position               mlk_rope_f32
@@ -44,6 +44,11 @@ int64_t Align256(int64_t bytes) { return (bytes + 255) / 256 * 256; }
 
 bool Contiguous(const int32_t* positions) { return positions == nullptr; }
 
+// Token counts whose linear layers run the skinny GEMM (8..32 rows): with
+// quantized weights the layer fuses them as the one-token path does, with
+// the epilogues in the split-K reduction.
+bool FusedRows(int64_t T) { return T >= 8 && T <= 32; }
+
 Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contiguous) {
     const int64_t D = c.dim, F = c.hidden_dim;
     const int64_t QD = static_cast<int64_t>(c.n_heads) * c.head_dim;
@@ -59,6 +64,13 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
     for (const auto& s : shapes) {
         const int64_t b = mlk_linear_workspace_bytes(T, s[0], s[1]);
         if (b > p.lin_bytes) p.lin_bytes = b;
+    }
+    if (FusedRows(T)) {  // q/k/v, gate/up and down as fused skinny launches
+        const int64_t fused[3][2] = {{D, QD + 2 * KD}, {D, 2 * F}, {F, D}};  // (in, all outputs)
+        for (const auto& s : fused) {
+            const int64_t b = SkinnyFusedWorkspaceBytes(MLK_Q8_0, T, s[0], s[1]);
+            if (b > p.lin_bytes) p.lin_bytes = b;
+        }
     }
     p.off[8] = at;
     at += Align256(p.lin_bytes);
@@ -188,7 +200,8 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     // One token (the decode step) with quantized weights: q, k and v in one
     // launch, gate and up with SwiGLU in the epilogue, and the down
     // projection adding into x (the same per-element arithmetic as the
-    // separate kernels).
+    // separate kernels).  8..32 tokens: the same groups as skinny GEMM
+    // launches, with the epilogues in their split-K reductions.
     const hipStream_t hs = AsStream(stream);
     const bool row = T == 1;
     const bool qkv1 = row && w->wq.type == w->wk.type && w->wq.type == w->wv.type &&
@@ -197,6 +210,13 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     const bool ffn1 = row && w->w_gate.type == w->w_up.type && RowStreamable(w->w_gate, D) &&
                       RowStreamable(w->w_up, D);
     const bool down1 = row && RowStreamable(w->w_down, F);
+    const bool mid = FusedRows(T);
+    const bool qkvm = mid && w->wq.type == w->wk.type && w->wq.type == w->wv.type &&
+                      w->wq.type != kLinearF32 && SkinnyFusedApplies(w->wq.type, T, D);
+    const bool ffnm = mid && w->w_gate.type == w->w_up.type && w->w_gate.type != kLinearF32 &&
+                      SkinnyFusedApplies(w->w_gate.type, T, D);
+    const bool downm = mid && w->w_down.type != kLinearF32 &&
+                       SkinnyFusedApplies(w->w_down.type, T, F);
     MLK_TRY(mlk_rmsnorm_f32(x, w->attention_norm, h, T, D, eps, stream));
     if (qkv1) {
         StreamArgs a{};
@@ -205,6 +225,13 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[2] = Seg(w->wv, v, KD);
         a.n_seg = 3;
         MLK_TRY(LinearRowStream(w->wq.type, h, D, a, kStreamPlain, hs));
+    } else if (qkvm) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->wq, q, QD);
+        a.seg[1] = Seg(w->wk, k, KD);
+        a.seg[2] = Seg(w->wv, v, KD);
+        a.n_seg = 3;
+        MLK_TRY(LinearSkinnyFused(w->wq.type, h, T, D, a, kStreamPlain, lin_ws, lin_b, hs));
     } else {
         MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
         MLK_TRY(Linear(w->wk, h, k, T, D, KD, lin_ws, lin_b, stream));
@@ -225,6 +252,12 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[1] = Seg(w->w_up, gate, F);
         a.n_seg = 2;
         MLK_TRY(LinearRowStream(w->w_gate.type, h, D, a, kStreamSwiGlu, hs));
+    } else if (ffnm) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->w_gate, gate, F);
+        a.seg[1] = Seg(w->w_up, gate, F);
+        a.n_seg = 2;
+        MLK_TRY(LinearSkinnyFused(w->w_gate.type, h, T, D, a, kStreamSwiGlu, lin_ws, lin_b, hs));
     } else {
         MLK_TRY(Linear(w->w_gate, h, gate, T, D, F, lin_ws, lin_b, stream));
         MLK_TRY(Linear(w->w_up, h, up, T, D, F, lin_ws, lin_b, stream));
@@ -235,6 +268,11 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[0] = Seg(w->w_down, x, D, x);
         a.n_seg = 1;
         MLK_TRY(LinearRowStream(w->w_down.type, gate, F, a, kStreamAdd, hs));
+    } else if (downm) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->w_down, x, D, x);
+        a.n_seg = 1;
+        MLK_TRY(LinearSkinnyFused(w->w_down.type, gate, T, F, a, kStreamAdd, lin_ws, lin_b, hs));
     } else {
         MLK_TRY(Linear(w->w_down, gate, proj, T, F, D, lin_ws, lin_b, stream));
         MLK_TRY(mlk_add_f32(x, proj, x, T * D, stream));

@@ -468,26 +468,44 @@ struct XChunk {
     }
 };
 
+// Up to three weight matrices with the same K in one launch: their row
+// groups are numbered one segment after another, and their partial sums
+// fill adjacent columns of the partial rows (segment s from column col0[s]).
+// One segment without a partial buffer writes y (+ bias) directly.
+struct SkinnyArgs {
+    const uint8_t* w[3];
+    int64_t rows[3];
+    int64_t col0[3];
+    int g0[3];       // first row group of each segment
+    int n_seg;
+    int row_groups;  // all segments
+    int64_t cols;    // columns of a partial row: the segments' rows together
+    const float* bias;
+    float* y;
+};
+
 // Workgroup (row group, chunk): 64 output rows over one K chunk of 32 D.
 // Every weight load and the chunk's x rows are issued before anything is
 // computed (one round of memory latency per workgroup); the chunk's sums go
-// to partial[chunk] for SplitKReduce, or straight to y (+ bias) when K is one
-// chunk.
+// to partial[chunk] for the reduction, or straight to y (+ bias) when K is
+// one chunk.
 template <int WT, int TT>
 __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict__ x,
-                                                         const uint8_t* __restrict__ w,
-                                                         const float* __restrict__ bias,
-                                                         float* __restrict__ y, int64_t T,
-                                                         int64_t K, int64_t O, int64_t row_bytes,
-                                                         int row_groups,
+                                                         SkinnyArgs a, int64_t T, int64_t K,
+                                                         int64_t row_bytes,
                                                          float* __restrict__ partial) {
     using WC = WChunk<WT>;
     constexpr int D = WC::kStages;
     constexpr int kChunk = 32 * D;
     using XC = XChunk<TT, kChunk, WC::kPieces>;
     __shared__ __align__(16) float xs[16 * TT * XC::RS];
-    const int rg = static_cast<int>(blockIdx.x) % row_groups;
-    const int sp = static_cast<int>(blockIdx.x) / row_groups;
+    const int rgall = static_cast<int>(blockIdx.x) % a.row_groups;
+    const int sp = static_cast<int>(blockIdx.x) / a.row_groups;
+    const int seg = (a.n_seg > 2 && rgall >= a.g0[2]) ? 2 : ((a.n_seg > 1 && rgall >= a.g0[1]) ? 1 : 0);
+    const int rg = rgall - (seg == 2 ? a.g0[2] : (seg == 1 ? a.g0[1] : 0));
+    const int64_t O = seg == 2 ? a.rows[2] : (seg == 1 ? a.rows[1] : a.rows[0]);
+    const uint8_t* w = seg == 2 ? a.w[2] : (seg == 1 ? a.w[1] : a.w[0]);
+    const int64_t col0 = seg == 2 ? a.col0[2] : (seg == 1 ? a.col0[1] : 0);
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int i16 = lane & 15, q = lane >> 4;
     const int64_t row = static_cast<int64_t>(rg) * kSkRows + wave * 16 + i16;
@@ -527,15 +545,63 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
         }
     }
     if (row >= O) return;
-    float* out = partial != nullptr ? partial + sp * T * O : y;
-    const float b = partial == nullptr && bias != nullptr ? bias[row] : 0.0f;
+    if (partial != nullptr) {
+        float* out = partial + sp * T * a.cols + col0 + row;
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t t = tt * 16 + 4 * q + r;
+                if (t < T) out[t * a.cols] = acc[tt][r];
+            }
+        }
+        return;
+    }
+    const float b = a.bias != nullptr ? a.bias[row] : 0.0f;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t t = tt * 16 + 4 * q + r;
-            if (t < T) out[t * O + row] = acc[tt][r] + b;
+            if (t < T) a.y[t * O + row] = acc[tt][r] + b;
         }
+    }
+}
+
+// The reduction of a fused skinny launch: each output's partial sums added in
+// chunk order (as SplitKReduce), then (+ bias) and the mode's epilogue:
+// plain y_s = v; add y_s = res_s + v; SwiGLU y_1 = SwiGlu(gate, up) with
+// gate and up the two segments' sums for the same row.
+__global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* __restrict__ partial,
+                                                                  int splits, int64_t T,
+                                                                  int64_t cols, StreamArgs a,
+                                                                  int mode, int64_t out_cols) {
+    const int64_t n = T * out_cols, stride = T * cols;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t t = i / out_cols, c = i % out_cols;
+        auto sum = [&](int64_t col) {
+            const float* pp = partial + t * cols + col;
+            float v = pp[0];
+            for (int sp = 1; sp < splits; ++sp) v += pp[sp * stride];
+            return v;
+        };
+        if (mode == kStreamSwiGlu) {
+            const int64_t F = a.seg[0].rows;
+            float g = sum(c), u = sum(F + c);
+            if (a.seg[0].bias != nullptr) g += a.seg[0].bias[c];
+            if (a.seg[1].bias != nullptr) u += a.seg[1].bias[c];
+            a.seg[1].y[t * F + c] = SwiGluF(g, u);
+            continue;
+        }
+        const int s = (a.n_seg > 2 && c >= a.seg[0].rows + a.seg[1].rows) ? 2
+                      : ((a.n_seg > 1 && c >= a.seg[0].rows) ? 1 : 0);
+        const StreamSeg& sg = s == 2 ? a.seg[2] : (s == 1 ? a.seg[1] : a.seg[0]);
+        const int64_t local = c - (s == 2 ? a.seg[0].rows + a.seg[1].rows : (s == 1 ? a.seg[0].rows : 0));
+        float v = sum(c);
+        if (sg.bias != nullptr) v += sg.bias[local];
+        const int64_t at = t * sg.rows + local;
+        sg.y[at] = mode == kStreamAdd ? sg.res[at] + v : v;
     }
 }
 
@@ -558,27 +624,41 @@ bool SkinnyApplies(int wt, int64_t T, int64_t K) {
 }
 
 template <int TT>
-void LaunchSkinnyT(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
-                   const float* bias, float* y, int64_t T, int64_t K, int64_t O,
-                   int64_t row_bytes, int groups, float* partial) {
+void LaunchSkinnyT(int wt, dim3 grid, hipStream_t s, const float* x, const SkinnyArgs& a,
+                   int64_t T, int64_t K, int64_t row_bytes, float* partial) {
     switch (wt) {
         case MLK_Q8_0:
-            hipLaunchKernelGGL((GemmSkinny<MLK_Q8_0, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias,
-                               y, T, K, O, row_bytes, groups, partial);
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q8_0, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
+                               row_bytes, partial);
             break;
         case MLK_Q4_0:
-            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_0, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias,
-                               y, T, K, O, row_bytes, groups, partial);
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_0, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
+                               row_bytes, partial);
             break;
         case MLK_Q4_1:
-            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_1, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias,
-                               y, T, K, O, row_bytes, groups, partial);
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_1, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
+                               row_bytes, partial);
             break;
         default:
-            hipLaunchKernelGGL((GemmSkinny<kWF32, TT>), grid, dim3(kSkThreads), 0, s, x, w, bias, y,
-                               T, K, O, row_bytes, groups, partial);
+            hipLaunchKernelGGL((GemmSkinny<kWF32, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
+                               row_bytes, partial);
             break;
     }
+}
+
+mlk_status LaunchSkinny(int wt, const float* x, const SkinnyArgs& a, int64_t T, int64_t K,
+                        int64_t row_bytes, int splits, float* partial, hipStream_t s) {
+    if (static_cast<int64_t>(a.row_groups) * splits > 0x7FFFFFFF) {
+        return Fail(MLK_ERR_INVALID, "linear: %lld output rows exceed one launch",
+                    static_cast<long long>(a.cols));
+    }
+    const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.row_groups) * splits));
+    if (T <= 16) {
+        LaunchSkinnyT<1>(wt, grid, s, x, a, T, K, row_bytes, partial);
+    } else {
+        LaunchSkinnyT<2>(wt, grid, s, x, a, T, K, row_bytes, partial);
+    }
+    return CheckLaunch("GemmSkinny");
 }
 
 template <int BM>
@@ -629,20 +709,19 @@ mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, 
         const SplitPlan plan = sk;
         float* partial = plan.splits > 1 ? static_cast<float*>(workspace) : nullptr;
         const int64_t groups = (O + kSkRows - 1) / kSkRows;
-        if (groups * plan.splits > 0x7FFFFFFF) {
+        if (groups > 0x7FFFFFFF) {
             return Fail(MLK_ERR_INVALID, "linear: %lld output rows exceed one launch",
                         static_cast<long long>(O));
         }
-        const dim3 grid(static_cast<unsigned>(groups * plan.splits));
-        const uint8_t* wb = static_cast<const uint8_t*>(w);
-        if (T <= 16) {
-            LaunchSkinnyT<1>(wt, grid, s, x, wb, bias, y, T, K, O, row_bytes,
-                             static_cast<int>(groups), partial);
-        } else {
-            LaunchSkinnyT<2>(wt, grid, s, x, wb, bias, y, T, K, O, row_bytes,
-                             static_cast<int>(groups), partial);
-        }
-        mlk_status st = CheckLaunch("GemmSkinny");
+        SkinnyArgs a{};
+        a.w[0] = static_cast<const uint8_t*>(w);
+        a.rows[0] = O;
+        a.n_seg = 1;
+        a.row_groups = static_cast<int>(groups);
+        a.cols = O;
+        a.bias = bias;
+        a.y = y;
+        mlk_status st = LaunchSkinny(wt, x, a, T, K, row_bytes, plan.splits, partial, s);
         if (st != MLK_OK || partial == nullptr) return st;
         hipLaunchKernelGGL(SplitKReduce, dim3(GridFor(T * O, kGemmThreads, 8)),
                            dim3(kGemmThreads), 0, s, partial, plan.splits, bias, y, T, O);
@@ -684,6 +763,59 @@ mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, 
     hipLaunchKernelGGL(SplitKReduce, dim3(GridFor(T * O, kGemmThreads, 8)), dim3(kGemmThreads), 0,
                        s, partial, plan.splits, bias, y, T, O);
     return CheckLaunch("SplitKReduce");
+}
+
+bool SkinnyFusedApplies(int wt, int64_t T, int64_t K) {
+    return wt != kWF32 && T >= 1 && SkinnyApplies(wt, T, K);
+}
+
+int64_t SkinnyFusedWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t cols) {
+    return static_cast<int64_t>(PlanSkinny(wt, K, cols).splits) * T * cols * 4;
+}
+
+// T token rows through up to three quantized weight matrices with the same K
+// (StreamArgs segments) in one skinny launch, then one reduction with the
+// mode's epilogue.  The partial sums always go through the workspace.
+mlk_status LinearSkinnyFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& sa,
+                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s) {
+    if (!SkinnyFusedApplies(wt, T, K) || sa.n_seg < 1 || sa.n_seg > 3 || !Aligned(x, 16) ||
+        (mode == kStreamSwiGlu && (sa.n_seg != 2 || sa.seg[0].rows != sa.seg[1].rows))) {
+        return Fail(MLK_ERR_INVALID, "linear (fused rows): unsupported shape");
+    }
+    SkinnyArgs a{};
+    int64_t cols = 0, groups = 0;
+    for (int i = 0; i < sa.n_seg; ++i) {
+        const StreamSeg& g = sa.seg[i];
+        if (g.w == nullptr || g.y == nullptr || g.rows <= 0 || !Aligned(g.w, 4) ||
+            (mode == kStreamAdd && g.res == nullptr)) {
+            return Fail(MLK_ERR_INVALID, "linear (fused rows): bad segment %d", i);
+        }
+        a.w[i] = g.w;
+        a.rows[i] = g.rows;
+        a.col0[i] = cols;
+        a.g0[i] = static_cast<int>(groups);
+        cols += g.rows;
+        groups += (g.rows + kSkRows - 1) / kSkRows;
+    }
+    a.n_seg = sa.n_seg;
+    a.row_groups = static_cast<int>(groups);
+    a.cols = cols;
+    const SplitPlan plan = PlanSkinny(wt, K, cols);
+    const int64_t need = static_cast<int64_t>(plan.splits) * T * cols * 4;
+    if (workspace == nullptr || !Aligned(workspace, 16) ||
+        static_cast<int64_t>(workspace_bytes) < need || groups > 0x3FFFFFFF) {
+        return Fail(MLK_ERR_INVALID, "linear (fused rows): workspace of %lld bytes needed",
+                    static_cast<long long>(need));
+    }
+    float* partial = static_cast<float*>(workspace);
+    const int64_t row_bytes = (K / 32) * BlockBytes(wt);
+    mlk_status st = LaunchSkinny(wt, x, a, T, K, row_bytes, plan.splits, partial, s);
+    if (st != MLK_OK) return st;
+    const int64_t out_cols = mode == kStreamSwiGlu ? sa.seg[0].rows : cols;
+    hipLaunchKernelGGL(SplitKReduceFused, dim3(GridFor(T * out_cols, kGemmThreads, 8)),
+                       dim3(kGemmThreads), 0, s, partial, plan.splits, T, cols, sa, mode,
+                       out_cols);
+    return CheckLaunch("SplitKReduceFused");
 }
 
 }  // namespace mlk

@@ -90,6 +90,16 @@ bool StreamFits(int64_t K);
 mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
                            hipStream_t s);
 
+// T token rows (up to 32) through up to three quantized weight matrices with
+// the same K (a multiple of 256) in one skinny launch (mlk_gemm.hip), then
+// one split-K reduction with the mode's epilogue (segments and modes as for
+// LinearRowStream).  The workspace holds SkinnyFusedWorkspaceBytes(wt, T, K,
+// sum of the segments' rows) bytes.
+bool SkinnyFusedApplies(int wt, int64_t T, int64_t K);
+int64_t SkinnyFusedWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t cols);
+mlk_status LinearSkinnyFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& a,
+                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s);
+
 // Prefill-shaped linear on the matrix cores (mlk_gemm.hip): y [T, O] =
 // x [T, K] W^T (+ bias), W fp32 (wt = -1) or MLK_Q8_0/Q4_0/Q4_1 blocks of
 // row_bytes per output row.  Needs K % 4 == 0 and 16-byte aligned x (and

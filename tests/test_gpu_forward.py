@@ -145,21 +145,24 @@ def test_forward_layer_rejects(mlk, fwd):
 
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0", "q4_1"])
-def test_decode_layer_fused_equals_op_by_op(mlk, fwd, wt):
-    """One token through a layer with quantized weights takes the fused
-    launches (q/k/v in one, gate/up with the SwiGLU epilogue, down adding
-    into x).  Their per-element arithmetic is the separate ops', so the layer
-    equals the same layer composed from the individual entry points bit for
-    bit (residual stream, K/V cache rows)."""
-    cfg = dict(vocab=64, dim=512, hidden_dim=1408, layers=1, n_heads=8, n_kv_heads=2,
+@pytest.mark.parametrize("T", [1, 12, 24])
+def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T):
+    """One token (streaming GEMVs) and 8..32 tokens (skinny GEMMs) through a
+    layer with quantized weights take fused launches: q/k/v in one, gate/up
+    with the SwiGLU epilogue, down adding into x (for 8..32 tokens the
+    epilogues run in the split-K reduction).  Their per-element arithmetic
+    is the separate ops', so the layer equals the same layer composed from
+    the individual entry points bit for bit (residual stream, K/V cache
+    rows); 24 consecutive tokens also take the prefill attention kernel."""
+    cfg = dict(vocab=64, dim=512, hidden_dim=1536, layers=1, n_heads=8, n_kv_heads=2,
                head_dim=64, max_seq=128, rope_type=0, theta=10000.0, eps=1e-5)
     model = O.forward_model(cfg, seed=11, weight_type=wt, biases=True)
-    D, F, H, KV, hd, S = 512, 1408, 8, 2, 64, 128
+    D, F, H, KV, hd, S = 512, 1536, 8, 2, 64, 128
     QD, KD, pos = H * hd, KV * hd, 37
     lw = model["layers"][0]
     dm = fwd.DeviceModel(model)
     rng = np.random.default_rng(5)
-    x0 = rng.standard_normal((1, D)).astype(np.float32)
+    x0 = rng.standard_normal((T, D)).astype(np.float32)
     kc0 = (rng.standard_normal((1, S, KV, hd)) * 0.5).astype(np.float32)
     vc0 = rng.standard_normal((1, S, KV, hd)).astype(np.float32)
     B = mlk.DeviceBuffer.from_array
@@ -167,8 +170,8 @@ def test_decode_layer_fused_equals_op_by_op(mlk, fwd, wt):
     # fused: the layer entry point
     x = B(x0)
     kc, vc = B(kc0), B(vc0)
-    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, S, True), np.uint8)
-    fwd.forward_layer_batch(cfg, dm.layers[0], x, 1, kc, vc, 1, S, 0, S, ws, pos0=pos)
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, S, True), np.uint8)
+    fwd.forward_layer_batch(cfg, dm.layers[0], x, T, kc, vc, 1, S, 0, S, ws, pos0=pos)
     got = x.download()
 
     # the same layer op by op
@@ -179,25 +182,25 @@ def test_decode_layer_fused_equals_op_by_op(mlk, fwd, wt):
     an, fn = up(np.asarray(lw["attention_norm"], np.float32)), up(np.asarray(lw["ffn_norm"], np.float32))
     x2, kc2, vc2 = B(x0), B(kc0), B(vc0)
     e = mlk.DeviceBuffer.empty
-    h, q, k, v, a, proj = e((1, D)), e((1, QD)), e((1, KD)), e((1, KD)), e((1, QD)), e((1, D))
-    g, u = e((1, F)), e((1, F))
-    mlk.rmsnorm(x2, an, h, 1, D, cfg["eps"])
-    mlk.linear_quant(wt, h, w["wq"], q, 1, D, QD, bias=bias["wq"])
-    mlk.linear_quant(wt, h, w["wk"], k, 1, D, KD, bias=bias["wk"])
-    mlk.linear_quant(wt, h, w["wv"], v, 1, D, KD, bias=bias["wv"])
-    mlk.rope(q, k, 1, H, KV, hd, pos0=pos, theta=cfg["theta"])
-    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, 1, pos0=pos)
-    nws = mlk.attention_workspace_bytes(1, H, KV, hd, S)
+    h, q, k, v, a, proj = e((T, D)), e((T, QD)), e((T, KD)), e((T, KD)), e((T, QD)), e((T, D))
+    g, u = e((T, F)), e((T, F))
+    mlk.rmsnorm(x2, an, h, T, D, cfg["eps"])
+    mlk.linear_quant(wt, h, w["wq"], q, T, D, QD, bias=bias["wq"])
+    mlk.linear_quant(wt, h, w["wk"], k, T, D, KD, bias=bias["wk"])
+    mlk.linear_quant(wt, h, w["wv"], v, T, D, KD, bias=bias["wv"])
+    mlk.rope(q, k, T, H, KV, hd, pos0=pos, theta=cfg["theta"])
+    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, pos0=pos)
+    nws = mlk.attention_workspace_bytes(T, H, KV, hd, S)
     aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
-    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, 1, a, S, pos0=pos, workspace=aws,
+    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, pos0=pos, workspace=aws,
                          workspace_bytes=aws.nbytes)
-    mlk.linear_quant(wt, a, w["wo"], proj, 1, QD, D)
-    mlk.add_rmsnorm(x2, proj, fn, h, 1, D, cfg["eps"])
-    mlk.linear_quant(wt, h, w["w_gate"], g, 1, D, F)
-    mlk.linear_quant(wt, h, w["w_up"], u, 1, D, F)
-    mlk.swiglu(g, u, g, F)
-    mlk.linear_quant(wt, g, w["w_down"], proj, 1, F, D)
-    mlk.add(x2, proj, x2, D)
+    mlk.linear_quant(wt, a, w["wo"], proj, T, QD, D)
+    mlk.add_rmsnorm(x2, proj, fn, h, T, D, cfg["eps"])
+    mlk.linear_quant(wt, h, w["w_gate"], g, T, D, F)
+    mlk.linear_quant(wt, h, w["w_up"], u, T, D, F)
+    mlk.swiglu(g, u, g, T * F)
+    mlk.linear_quant(wt, g, w["w_down"], proj, T, F, D)
+    mlk.add(x2, proj, x2, T * D)
     want = x2.download()
     np.testing.assert_array_equal(got, want)
     np.testing.assert_array_equal(kc.download(), kc2.download())
