@@ -147,8 +147,6 @@ __device__ inline float BlockMax(float v, float* scratch) {
     return m;
 }
 
-// Raises a device-side error flag (the flag is only ever set, never read
-// back here, so any nonzero store is enough).
 // SwiGLU of one element: s = g * (1 / (1 + exp(-g))) rounded to float, then
 // s * u (src/ops.cc:135-151), without contraction; shared by the element-wise
 // kernel and the fused gate/up GEMV so both round alike.
@@ -159,6 +157,44 @@ __device__ inline float SwiGluF(float g, float u) {
     return s * u;
 }
 
+// sin and cos of a float64 angle a.  The angle is first reduced by whole
+// turns: a / pi is formed as a double-double, with the product by 1/pi's
+// leading double split exactly by an fma (Dekker's two-product) and the
+// product by its trailing double added, then the nearest even integer n is
+// subtracted exactly (|a / pi| < 2^52), which is Cody and Waite's additive
+// reduction.  sincospi of the remainder, in [-1, 1], then equals sin / cos
+// of a within a few float64 ulps for |a| < 2^31, the angles RoPE forms.
+// Unlike a general sincos this keeps no large-argument (Payne-Hanek)
+// reduction, whose registers would be allocated across the whole kernel.
+__device__ inline void SinCosAngle(double a, double* s, double* c) {
+    constexpr double kInvPiHi = 0x1.45f306dc9c883p-2;    // 1/pi rounded to float64
+    constexpr double kInvPiLo = -0x1.6b01ec5417056p-56;  // 1/pi - kInvPiHi, rounded
+    const double p = a * kInvPiHi;
+    const double e = fma(a, kInvPiHi, -p) + a * kInvPiLo;
+    const double n = 2.0 * rint(0.5 * p);
+    sincospi((p - n) + e, s, c);
+}
+
+// RoPE of one pair (x0, x1) of a head at position pos, pair index i
+// (src/ops.cc:177-224): angle = (double) pos * pow((double) theta, -2.0 * i /
+// head_dim), cos and sin in float64, each output rounded once to float.  The
+// fused q/k/v epilogues use these; the RoPE kernels write the same
+// expressions.
+__device__ inline void RopeCosSin(int32_t pos, int i, int head_dim, float theta, double* c,
+                                  double* s) {
+    const double inv_freq = pow(static_cast<double>(theta), -2.0 * i / head_dim);
+    SinCosAngle(static_cast<double>(pos) * inv_freq, s, c);
+}
+
+__device__ inline void RopeRotate(float x0, float x1, double c, double s, float* r0, float* r1) {
+#pragma clang fp contract(off)
+    const double a0 = x0, a1 = x1;
+    *r0 = static_cast<float>(a0 * c - a1 * s);
+    *r1 = static_cast<float>(a0 * s + a1 * c);
+}
+
+// Raises a device-side error flag (the flag is only ever set, never read
+// back here, so any nonzero store is enough).
 __device__ inline void RaiseFlag(int32_t* err, int32_t code) {
     if (err != nullptr) {
         atomicOr(err, code);

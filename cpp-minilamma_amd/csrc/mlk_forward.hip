@@ -164,8 +164,19 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         if (st != MLK_OK) return st;
     }
     if (n_tokens <= 0) return Fail(MLK_ERR_INVALID, "%s: n_tokens must be positive", fn);
+    if (k_cache == nullptr || v_cache == nullptr || k_cache == v_cache) {
+        return Fail(MLK_ERR_INVALID, "%s: key and value caches must be distinct buffers", fn);
+    }
     if (!Aligned(k_cache, 16) || !Aligned(v_cache, 16)) {
         return Fail(MLK_ERR_INVALID, "%s: the caches must be 16-byte aligned", fn);
+    }
+    if (n_layers <= 0 || max_seq <= 0 || max_seq > 0x7FFFFFFF) {
+        return Fail(MLK_ERR_INVALID, "%s: cache dimensions out of range (layers %lld, max_seq %lld)",
+                    fn, static_cast<long long>(n_layers), static_cast<long long>(max_seq));
+    }
+    if (layer < 0 || layer >= n_layers) {
+        return Fail(MLK_ERR_RANGE, "%s: layer %lld out of range [0, %lld)", fn,
+                    static_cast<long long>(layer), static_cast<long long>(n_layers));
     }
     const bool contiguous = Contiguous(positions);
     if (max_ctx <= 0 || max_ctx > max_seq || (contiguous && pos0 + n_tokens > max_ctx)) {
@@ -217,30 +228,41 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
                       SkinnyFusedApplies(w->w_gate.type, T, D);
     const bool downm = mid && w->w_down.type != kLinearF32 &&
                        SkinnyFusedApplies(w->w_down.type, T, F);
+    // The fused q/k/v launches also rotate q and k (normal-layout pairs) and
+    // write k and v into the cache rows, in place of mlk_rope_f32 and
+    // mlk_kv_write_f32; the NeoX layout keeps the separate launches.
+    const bool rope_fused = (qkvm || (qkv1 && StreamRopeFits(D, c.head_dim))) &&
+                            c.rope_type == MLK_ROPE_NORMAL && c.head_dim % 2 == 0;
+    if (rope_fused && positions == nullptr && (pos0 < 0 || pos0 + T > max_seq)) {
+        return Fail(MLK_ERR_RANGE, "%s: positions %d..%lld out of range [0, %lld)", fn, pos0,
+                    static_cast<long long>(pos0 + T - 1), static_cast<long long>(max_seq));
+    }
     MLK_TRY(mlk_rmsnorm_f32(x, w->attention_norm, h, T, D, eps, stream));
-    if (qkv1) {
+    if (qkv1 || qkvm) {
+        const int64_t slot = KD;
         StreamArgs a{};
         a.seg[0] = Seg(w->wq, q, QD);
-        a.seg[1] = Seg(w->wk, k, KD);
-        a.seg[2] = Seg(w->wv, v, KD);
+        a.seg[1] = Seg(w->wk, rope_fused ? k_cache + layer * max_seq * slot : k, KD);
+        a.seg[2] = Seg(w->wv, rope_fused ? v_cache + layer * max_seq * slot : v, KD);
         a.n_seg = 3;
-        MLK_TRY(LinearRowStream(w->wq.type, h, D, a, kStreamPlain, hs));
-    } else if (qkvm) {
-        StreamArgs a{};
-        a.seg[0] = Seg(w->wq, q, QD);
-        a.seg[1] = Seg(w->wk, k, KD);
-        a.seg[2] = Seg(w->wv, v, KD);
-        a.n_seg = 3;
-        MLK_TRY(LinearSkinnyFused(w->wq.type, h, T, D, a, kStreamPlain, lin_ws, lin_b, hs));
+        a.rope = RopeArgs{positions, pos0, c.head_dim, c.rope_theta, slot, max_seq, err};
+        const int mode = rope_fused ? kStreamQkvRope : kStreamPlain;
+        if (qkv1) {
+            MLK_TRY(LinearRowStream(w->wq.type, h, D, a, mode, hs));
+        } else {
+            MLK_TRY(LinearSkinnyFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs));
+        }
     } else {
         MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
         MLK_TRY(Linear(w->wk, h, k, T, D, KD, lin_ws, lin_b, stream));
         MLK_TRY(Linear(w->wv, h, v, T, D, KD, lin_ws, lin_b, stream));
     }
-    MLK_TRY(mlk_rope_f32(q, k, T, c.n_heads, c.n_kv_heads, c.head_dim, QD, KD, positions, pos0,
-                         c.rope_theta, c.rope_type, err, stream));
-    MLK_TRY(mlk_kv_write_f32(k_cache, v_cache, n_layers, max_seq, c.n_kv_heads, c.head_dim, layer,
-                             k, KD, v, KD, positions, pos0, T, err, stream));
+    if (!rope_fused) {
+        MLK_TRY(mlk_rope_f32(q, k, T, c.n_heads, c.n_kv_heads, c.head_dim, QD, KD, positions,
+                             pos0, c.rope_theta, c.rope_type, err, stream));
+        MLK_TRY(mlk_kv_write_f32(k_cache, v_cache, n_layers, max_seq, c.n_kv_heads, c.head_dim,
+                                 layer, k, KD, v, KD, positions, pos0, T, err, stream));
+    }
     MLK_TRY(mlk_attention_decode_f32(q, QD, k_cache, v_cache, n_layers, max_seq, c.n_heads,
                                      c.n_kv_heads, c.head_dim, layer, positions, pos0, T, max_ctx,
                                      a, att_ws, static_cast<size_t>(p.att_bytes), err, stream));

@@ -594,6 +594,43 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
             a.seg[1].y[t * F + c] = SwiGluF(g, u);
             continue;
         }
+        if (mode == kStreamQkvRope) {
+            // unit c: a (2i, 2i+1) pair of the q then k columns, then one v column
+            const RopeArgs& r = a.rope;
+            const int32_t pos = r.positions != nullptr ? r.positions[t]
+                                                       : r.pos0 + static_cast<int32_t>(t);
+            const bool cache_ok = pos >= 0 && pos < r.max_seq;
+            if (c == 0 && !cache_ok) RaiseFlag(r.err, 1);
+            const int64_t QD = a.seg[0].rows, KD = a.seg[1].rows, pairs = (QD + KD) / 2;
+            if (c >= pairs) {
+                const int64_t local = c - pairs;
+                float v = sum(QD + KD + local);
+                if (a.seg[2].bias != nullptr) v += a.seg[2].bias[local];
+                if (cache_ok) a.seg[2].y[pos * r.kv_stride + local] = v;
+                continue;
+            }
+            const int64_t col = 2 * c;
+            const bool is_k = col >= QD;
+            const StreamSeg& sg = is_k ? a.seg[1] : a.seg[0];
+            const int64_t local = is_k ? col - QD : col;
+            float x0 = sum(col), x1 = sum(col + 1);
+            if (sg.bias != nullptr) {
+                x0 += sg.bias[local];
+                x1 += sg.bias[local + 1];
+            }
+            float r0 = x0, r1 = x1;
+            if (pos >= 0) {
+                double cs, sn;
+                RopeCosSin(pos, static_cast<int>(local % r.head_dim) / 2, r.head_dim, r.theta, &cs,
+                           &sn);
+                RopeRotate(x0, x1, cs, sn, &r0, &r1);
+            }
+            if (is_k && !cache_ok) continue;
+            float* y = is_k ? sg.y + pos * r.kv_stride : sg.y + t * QD;
+            y[local] = r0;
+            y[local + 1] = r1;
+            continue;
+        }
         const int s = (a.n_seg > 2 && c >= a.seg[0].rows + a.seg[1].rows) ? 2
                       : ((a.n_seg > 1 && c >= a.seg[0].rows) ? 1 : 0);
         const StreamSeg& sg = s == 2 ? a.seg[2] : (s == 1 ? a.seg[1] : a.seg[0]);
@@ -779,7 +816,8 @@ int64_t SkinnyFusedWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t cols) {
 mlk_status LinearSkinnyFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& sa,
                              int mode, void* workspace, size_t workspace_bytes, hipStream_t s) {
     if (!SkinnyFusedApplies(wt, T, K) || sa.n_seg < 1 || sa.n_seg > 3 || !Aligned(x, 16) ||
-        (mode == kStreamSwiGlu && (sa.n_seg != 2 || sa.seg[0].rows != sa.seg[1].rows))) {
+        (mode == kStreamSwiGlu && (sa.n_seg != 2 || sa.seg[0].rows != sa.seg[1].rows)) ||
+        (mode == kStreamQkvRope && !QkvRopeArgsOk(sa))) {
         return Fail(MLK_ERR_INVALID, "linear (fused rows): unsupported shape");
     }
     SkinnyArgs a{};
@@ -811,7 +849,10 @@ mlk_status LinearSkinnyFused(int wt, const float* x, int64_t T, int64_t K, const
     const int64_t row_bytes = (K / 32) * BlockBytes(wt);
     mlk_status st = LaunchSkinny(wt, x, a, T, K, row_bytes, plan.splits, partial, s);
     if (st != MLK_OK) return st;
-    const int64_t out_cols = mode == kStreamSwiGlu ? sa.seg[0].rows : cols;
+    const int64_t out_cols = mode == kStreamSwiGlu    ? sa.seg[0].rows
+                             : mode == kStreamQkvRope ? (sa.seg[0].rows + sa.seg[1].rows) / 2 +
+                                                            sa.seg[2].rows
+                                                      : cols;
     hipLaunchKernelGGL(SplitKReduceFused, dim3(GridFor(T * out_cols, kGemmThreads, 8)),
                        dim3(kGemmThreads), 0, s, partial, plan.splits, T, cols, sa, mode,
                        out_cols);

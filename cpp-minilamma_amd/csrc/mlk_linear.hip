@@ -628,10 +628,13 @@ __device__ inline void StreamCompute(const uint32_t (&wd)[R][Piece<QT>::kWords],
 
 // The R rows' sums over the wave, then the epilogue.  SwiGLU: the gate
 // segment's sums stay in `gate` (the lanes that will write each row hold
-// it) until the up segment's step for the same rows.
+// it) until the up segment's step for the same rows.  q/k/v RoPE: with one
+// row per step an even q or k row waits in `gate` for its odd partner (a
+// wave's run starts at an even group, so the pair is its next step); with
+// two, the pair is the step's two rows, exchanged between the wave halves.
 template <int R, int MODE>
 __device__ inline void StreamFinish(float (&acc)[R][1], const StreamArgs& a, const StreamStep& st,
-                                    int lane, float& gate) {
+                                    int lane, float& gate, int32_t pos, const double2* rope_cs) {
     float v[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -647,6 +650,42 @@ __device__ inline void StreamFinish(float (&acc)[R][1], const StreamArgs& a, con
             gate = val;
             return;
         }
+    }
+    if constexpr (MODE == kStreamQkvRope) {
+        static_assert(R == 1 || R == 2, "pairs are one step of two rows or two steps of one");
+        const bool writer = (lane & (kWave / R - 1)) == 0;
+        const bool cache_ok = pos >= 0 && pos < a.rope.max_seq;
+        if (st.seg == 2) {
+            if (writer && cache_ok) sg.y[pos * a.rope.kv_stride + row] = val;
+            return;
+        }
+        float x0, x1;
+        if constexpr (R == 1) {
+            if ((row & 1) == 0) {
+                gate = val;
+                return;
+            }
+            x0 = gate;
+            x1 = val;
+        } else {
+            const float other = __shfl_xor(val, kWave / 2, kWave);
+            x0 = (row & 1) ? other : val;
+            x1 = (row & 1) ? val : other;
+        }
+        float r0 = x0, r1 = x1;
+        if (pos >= 0) {
+            const double2 cs = rope_cs[static_cast<int>(row % a.rope.head_dim) / 2];
+            RopeRotate(x0, x1, cs.x, cs.y, &r0, &r1);
+        }
+        if (!writer || (st.seg == 1 && !cache_ok)) return;
+        float* y = st.seg == 1 ? sg.y + pos * a.rope.kv_stride : sg.y;
+        if constexpr (R == 1) {
+            y[row - 1] = r0;
+            y[row] = r1;
+        } else {
+            y[row] = (row & 1) ? r1 : r0;
+        }
+        return;
     }
     if ((lane & (kWave / R - 1)) != 0 || row >= sg.rows) return;
     if constexpr (MODE == kStreamSwiGlu) {
@@ -692,6 +731,11 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, 
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r][0] = 0.0f;
     float gate = 0.0f;
+    // the token's position (q/k/v RoPE): a uniform load, requested first
+    int32_t pos = 0;
+    if constexpr (MODE == kStreamQkvRope) {
+        pos = a.rope.positions != nullptr ? a.rope.positions[0] : a.rope.pos0;
+    }
     // Steps in order (StreamStep::Advance).  D + 1 register buffers: step
     // st + D is loaded while step st is computed.  `ld` is the next step to
     // load, `cur` the one computed.  The prefetches are unconditional (past
@@ -714,6 +758,23 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, 
     for (int64_t i = threadIdx.x; i < K / 4; i += kStreamThreads) {
         *reinterpret_cast<float4*>(xs + XPad(4 * i)) = reinterpret_cast<const float4*>(x)[i];
     }
+    // q/k/v RoPE: the (cos, sin) of every pair index of a head, after x in
+    // LDS, computed once per workgroup while the first steps load (the
+    // epilogue then only rotates, so the float64 sin and cos take no
+    // registers in the step loop)
+    double2* rope_cs = reinterpret_cast<double2*>(xs + XPad(K));
+    if constexpr (MODE == kStreamQkvRope) {
+        if (pos >= 0) {
+            for (int i = threadIdx.x; i < a.rope.head_dim / 2; i += kStreamThreads) {
+                double cs, sn;
+                RopeCosSin(pos, i, a.rope.head_dim, a.rope.theta, &cs, &sn);
+                rope_cs[i] = make_double2(cs, sn);
+            }
+        }
+        if (blockIdx.x == 0 && threadIdx.x == 0 && (pos < 0 || pos >= a.rope.max_seq)) {
+            RaiseFlag(a.rope.err, 1);
+        }
+    }
     __syncthreads();
     if (g_first >= groups) return;
     for (int64_t st = 0; st < n_steps; st += D + 1) {
@@ -726,7 +787,7 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, 
             __builtin_amdgcn_sched_barrier(0);
             if (st + b < n_steps) {
                 StreamCompute<QT, R, kTail>(wbuf[b], xs, cur.pass, lane, pieces, acc);
-                if (cur.pass == passes - 1) StreamFinish<R, MODE>(acc, a, cur, lane, gate);
+                if (cur.pass == passes - 1) StreamFinish<R, MODE>(acc, a, cur, lane, gate, pos, rope_cs);
                 cur.Advance<MODE>(a, passes, R);
             }
         }
@@ -840,14 +901,20 @@ mlk_status StreamLaunch(const float* x, StreamArgs a, int mode, int64_t K, int64
     }
     if (mode == kStreamSwiGlu) groups = a.seg[0].groups;
     const int64_t want = static_cast<int64_t>(ComputeUnits()) * 16;
-    const int64_t per_wave = groups > want ? (groups + want - 1) / want : 1;
+    int64_t per_wave = groups > want ? (groups + want - 1) / want : 1;
+    // q/k/v RoPE with one row per group: runs of whole pairs (the segments'
+    // group counts are even, so every run starts on an even row)
+    if (mode == kStreamQkvRope && R == 1) per_wave += per_wave % 2;
     const int64_t waves = (groups + per_wave - 1) / per_wave;
     const dim3 grid(static_cast<unsigned>((waves + kStreamWaves - 1) / kStreamWaves));
-    const size_t lds = static_cast<size_t>(XPad(K)) * 4;
+    // x, then (q/k/v RoPE) a (cos, sin) pair per pair index of a head, 8-byte aligned
+    size_t lds = static_cast<size_t>(XPad(K)) * 4;
+    if (mode == kStreamQkvRope) lds = (lds + 15) / 16 * 16 + static_cast<size_t>(a.rope.head_dim / 2) * 16;
     const int pw = static_cast<int>(per_wave);
     switch (mode) {
         case kStreamAdd: LaunchStreamT<QT, R, kStreamAdd>(grid, lds, s, x, a, K, row_bytes, groups, pw); break;
         case kStreamSwiGlu: LaunchStreamT<QT, R, kStreamSwiGlu>(grid, lds, s, x, a, K, row_bytes, groups, pw); break;
+        case kStreamQkvRope: LaunchStreamT<QT, R, kStreamQkvRope>(grid, lds, s, x, a, K, row_bytes, groups, pw); break;
         default: LaunchStreamT<QT, R, kStreamPlain>(grid, lds, s, x, a, K, row_bytes, groups, pw); break;
     }
     return CheckLaunch("GemvStream");
@@ -868,7 +935,19 @@ mlk_status Gemv(const float* x, const uint8_t* w, const float* bias, float* y, i
 
 }  // namespace
 
+bool QkvRopeArgsOk(const StreamArgs& a) {
+    const int64_t hd = a.rope.head_dim;
+    return a.n_seg == 3 && hd > 0 && hd % 2 == 0 && a.seg[0].rows % hd == 0 &&
+           a.seg[1].rows % hd == 0 && a.seg[2].rows % 2 == 0 &&
+           a.rope.kv_stride >= a.seg[1].rows && a.rope.kv_stride >= a.seg[2].rows &&
+           a.rope.max_seq > 0;
+}
+
 bool StreamFits(int64_t K) { return K % 64 == 0 && K > 0 && XPad(K) * 4 <= 64 * 1024; }
+
+bool StreamRopeFits(int64_t K, int64_t head_dim) {
+    return StreamFits(K) && head_dim > 0 && XPad(K) * 4 + head_dim / 2 * 16 <= 64 * 1024;
+}
 
 mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
                            hipStream_t s) {
@@ -881,6 +960,9 @@ mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& 
             a.seg[i].rows <= 0 || (mode == kStreamAdd && a.seg[i].res == nullptr)) {
             return Fail(MLK_ERR_INVALID, "linear (one row): bad segment %d", i);
         }
+    }
+    if (mode == kStreamQkvRope && (!QkvRopeArgsOk(a) || !StreamRopeFits(K, a.rope.head_dim))) {
+        return Fail(MLK_ERR_INVALID, "linear (one row): bad q/k/v RoPE segments");
     }
     const int64_t row_bytes = (K / 32) * BlockBytes(qt);
     switch (qt) {

@@ -69,7 +69,15 @@ __device__ inline float HalfHw(uint32_t h16) {
 // kStreamAdd the residual res (y[row] = res[row] + sum; res may be y).
 // kStreamSwiGlu: segments 0 and 1 are gate and up with equal rows, y of
 // segment 1 receives SwiGlu(gate, up) (segment 0's y is not written).
-enum StreamMode { kStreamPlain = 0, kStreamAdd = 1, kStreamSwiGlu = 2 };
+// kStreamQkvRope: segments q, k and v of attention heads of `rope.head_dim`
+// (both even row counts, multiples of head_dim); each token's q and k rows
+// are rotated in normal-layout pairs (2i, 2i+1) at the token's position as
+// mlk_rope_f32 does (RopeRotatePair), q lands in segment 0's y and k and v in
+// their cache rows: y + pos * rope.kv_stride for segments 1 and 2.  A
+// position outside [0, max_seq) raises rope.err and writes no cache row (q is
+// still rotated when pos >= 0, left as is below 0), as mlk_rope_f32 followed
+// by mlk_kv_write_f32 would.
+enum StreamMode { kStreamPlain = 0, kStreamAdd = 1, kStreamSwiGlu = 2, kStreamQkvRope = 3 };
 
 struct StreamSeg {
     const uint8_t* w;
@@ -80,13 +88,28 @@ struct StreamSeg {
     int64_t groups;  // set by the launcher
 };
 
+struct RopeArgs {
+    const int32_t* positions;  // per token, or null: pos0 + t
+    int32_t pos0;
+    int32_t head_dim;
+    float theta;
+    int64_t kv_stride;  // floats between cache rows of consecutive positions
+    int64_t max_seq;
+    int32_t* err;
+};
+
 struct StreamArgs {
     StreamSeg seg[3];
     int n_seg;
+    RopeArgs rope;  // kStreamQkvRope only
 };
 
 // in_features % 64 == 0 and x (16-byte aligned) fits the kernel's LDS
 bool StreamFits(int64_t K);
+// the shape rules of kStreamQkvRope above, and x plus its (cos, sin) table
+// within the streaming kernel's LDS
+bool QkvRopeArgsOk(const StreamArgs& a);
+bool StreamRopeFits(int64_t K, int64_t head_dim);
 mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
                            hipStream_t s);
 

@@ -33,24 +33,6 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kBatch = 5;  // heads loaded per lane before the first rotation
 
-// sin and cos of a float64 angle a.  The angle is first reduced by whole
-// turns: a / pi is formed as a double-double, with the product by 1/pi's
-// leading double split exactly by an fma (Dekker's two-product) and the
-// product by its trailing double added, then the nearest even integer n is
-// subtracted exactly (|a / pi| < 2^52), which is Cody and Waite's additive
-// reduction.  sincospi of the remainder, in [-1, 1], then equals sin / cos
-// of a within a few float64 ulps for |a| < 2^31, the angles RoPE forms.
-// Unlike a general sincos this keeps no large-argument (Payne-Hanek)
-// reduction, whose registers would be allocated across the whole kernel.
-__device__ inline void SinCosAngle(double a, double* s, double* c) {
-    constexpr double kInvPiHi = 0x1.45f306dc9c883p-2;    // 1/pi rounded to float64
-    constexpr double kInvPiLo = -0x1.6b01ec5417056p-56;  // 1/pi - kInvPiHi, rounded
-    const double p = a * kInvPiHi;
-    const double e = fma(a, kInvPiHi, -p) + a * kInvPiLo;
-    const double n = 2.0 * rint(0.5 * p);
-    sincospi((p - n) + e, s, c);
-}
-
 template <int PV, bool kNeoX>
 struct Pairs;
 

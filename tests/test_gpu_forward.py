@@ -146,18 +146,25 @@ def test_forward_layer_rejects(mlk, fwd):
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0", "q4_1"])
 @pytest.mark.parametrize("T", [1, 12, 24])
-def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T):
+@pytest.mark.parametrize("case", ["pos0", "positions", "bad_position", "neox"])
+def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
     """One token (streaming GEMVs) and 8..32 tokens (skinny GEMMs) through a
-    layer with quantized weights take fused launches: q/k/v in one, gate/up
-    with the SwiGLU epilogue, down adding into x (for 8..32 tokens the
-    epilogues run in the split-K reduction).  Their per-element arithmetic
-    is the separate ops', so the layer equals the same layer composed from
-    the individual entry points bit for bit (residual stream, K/V cache
-    rows); 24 consecutive tokens also take the prefill attention kernel."""
+    layer with quantized weights take fused launches: q/k/v in one, which
+    also rotates q and k (normal layout) and writes k and v into the cache,
+    gate/up with the SwiGLU epilogue, down adding into x (for 8..32 tokens
+    the epilogues run in the split-K reduction).  Their per-element
+    arithmetic is the separate ops', so the layer equals the same layer
+    composed from the individual entry points bit for bit (residual stream,
+    K/V cache rows, error flag).  Cases: consecutive positions from pos0 (24
+    tokens also take the prefill attention kernel); scattered positions;
+    one position at max_seq (flagged, its cache row not written, its
+    attention output zero); the NeoX layout (separate RoPE and K/V write)."""
+    S = 128
     cfg = dict(vocab=64, dim=512, hidden_dim=1536, layers=1, n_heads=8, n_kv_heads=2,
-               head_dim=64, max_seq=128, rope_type=0, theta=10000.0, eps=1e-5)
+               head_dim=64, max_seq=S, rope_type=1 if case == "neox" else 0, theta=10000.0,
+               eps=1e-5)
     model = O.forward_model(cfg, seed=11, weight_type=wt, biases=True)
-    D, F, H, KV, hd, S = 512, 1536, 8, 2, 64, 128
+    D, F, H, KV, hd = 512, 1536, 8, 2, 64
     QD, KD, pos = H * hd, KV * hd, 37
     lw = model["layers"][0]
     dm = fwd.DeviceModel(model)
@@ -166,12 +173,21 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T):
     kc0 = (rng.standard_normal((1, S, KV, hd)) * 0.5).astype(np.float32)
     vc0 = rng.standard_normal((1, S, KV, hd)).astype(np.float32)
     B = mlk.DeviceBuffer.from_array
+    positions = None
+    if case in ("positions", "bad_position"):
+        pv = np.sort(rng.choice(S, T, replace=False)).astype(np.int32)
+        if case == "bad_position":
+            pv[T // 2] = S
+        positions = B(pv)
+    contiguous = positions is None
+    flag, flag2 = B(np.zeros(1, np.int32)), B(np.zeros(1, np.int32))
 
     # fused: the layer entry point
     x = B(x0)
     kc, vc = B(kc0), B(vc0)
-    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, S, True), np.uint8)
-    fwd.forward_layer_batch(cfg, dm.layers[0], x, T, kc, vc, 1, S, 0, S, ws, pos0=pos)
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, S, contiguous), np.uint8)
+    fwd.forward_layer_batch(cfg, dm.layers[0], x, T, kc, vc, 1, S, 0, S, ws, positions=positions,
+                            pos0=pos, err=flag)
     got = x.download()
 
     # the same layer op by op
@@ -188,12 +204,13 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T):
     mlk.linear_quant(wt, h, w["wq"], q, T, D, QD, bias=bias["wq"])
     mlk.linear_quant(wt, h, w["wk"], k, T, D, KD, bias=bias["wk"])
     mlk.linear_quant(wt, h, w["wv"], v, T, D, KD, bias=bias["wv"])
-    mlk.rope(q, k, T, H, KV, hd, pos0=pos, theta=cfg["theta"])
-    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, pos0=pos)
+    mlk.rope(q, k, T, H, KV, hd, positions=positions, pos0=pos, theta=cfg["theta"],
+             rope_type=cfg["rope_type"], err=flag2)
+    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, positions=positions, pos0=pos, err=flag2)
     nws = mlk.attention_workspace_bytes(T, H, KV, hd, S)
     aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
-    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, pos0=pos, workspace=aws,
-                         workspace_bytes=aws.nbytes)
+    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, positions=positions,
+                         pos0=pos, workspace=aws, workspace_bytes=aws.nbytes, err=flag2)
     mlk.linear_quant(wt, a, w["wo"], proj, T, QD, D)
     mlk.add_rmsnorm(x2, proj, fn, h, T, D, cfg["eps"])
     mlk.linear_quant(wt, h, w["w_gate"], g, T, D, F)
@@ -205,3 +222,8 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T):
     np.testing.assert_array_equal(got, want)
     np.testing.assert_array_equal(kc.download(), kc2.download())
     np.testing.assert_array_equal(vc.download(), vc2.download())
+    assert int(flag.download()[0]) == int(flag2.download()[0]) == (1 if case == "bad_position" else 0)
+    if case == "bad_position":
+        # the rows of the other positions were written, the cache outside them kept
+        kept = np.setdiff1d(np.arange(S), pv)
+        np.testing.assert_array_equal(kc.download()[0, kept], kc0[0, kept])
