@@ -158,14 +158,17 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
     K/V cache rows, error flag).  Cases: consecutive positions from pos0 (24
     tokens also take the prefill attention kernel); scattered positions;
     one position at max_seq (flagged, its cache row not written, its
-    attention output zero); the NeoX layout (separate RoPE and K/V write)."""
-    S = 128
+    attention output zero); the NeoX layout (separate RoPE and K/V write).
+    The cache spans several attention chunks, so the decode attention's
+    in-kernel merge of them (after the fused q/k/v launch) is compared with
+    the separate merge launch."""
+    S = 1024
     cfg = dict(vocab=64, dim=512, hidden_dim=1536, layers=1, n_heads=8, n_kv_heads=2,
                head_dim=64, max_seq=S, rope_type=1 if case == "neox" else 0, theta=10000.0,
                eps=1e-5)
     model = O.forward_model(cfg, seed=11, weight_type=wt, biases=True)
     D, F, H, KV, hd = 512, 1536, 8, 2, 64
-    QD, KD, pos = H * hd, KV * hd, 37
+    QD, KD, pos = H * hd, KV * hd, 700
     lw = model["layers"][0]
     dm = fwd.DeviceModel(model)
     rng = np.random.default_rng(5)
