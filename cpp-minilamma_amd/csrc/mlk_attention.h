@@ -18,4 +18,18 @@ mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, 
                          int64_t slot, int32_t H, int32_t KV, int32_t head_dim, int32_t pos0,
                          int64_t T, float* out, hipStream_t s);
 
+// Decode tokens at any positions (positions[t], or pos0 + t) on the same
+// matrix-core tiles: a workgroup holds 16 tokens and shares each K/V tile
+// among them, over one chunk of TileChunk() cache positions.  With more than
+// one chunk it writes (acc, m, l) partials to ws_acc / ws_ml ([T, H, n_chunks,
+// hd] / [.., 2], n_chunks = ceil(max_ctx / chunk)) for AttnCombine; with one
+// it writes out.  Invalid positions raise err (their rows are zeroed by the
+// merge, or here with one chunk).  Arguments already validated.
+int TileChunk(int64_t T, int32_t H, int32_t KV, int64_t max_ctx);
+mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* kc,
+                            const float* vc, int64_t slot, int32_t H, int32_t KV,
+                            int32_t head_dim, const int32_t* positions, int32_t pos0, int64_t T,
+                            int64_t max_ctx, float* out, float* ws_acc, float* ws_ml,
+                            int32_t* err, hipStream_t s);
+
 }  // namespace mlk

@@ -54,6 +54,7 @@ constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kHalf = kWave / 2;  // lanes per position
 constexpr int kMaxHeadDim = 256;
 constexpr int64_t kPrefillMinTokens = 16;  // consecutive positions from here: AttnPrefill
+constexpr int64_t kTileMinTokens = 4;      // other batches from here: AttnPrefill's chunked form
 
 struct AttnParams {
     const float* q;
@@ -783,6 +784,11 @@ int64_t mlk_attention_workspace_bytes(int64_t n_tokens, int32_t n_heads, int32_t
         // either kernel may run (the MFMA one needs a 16-byte aligned key cache)
         const int64_t nmf = PlanMf(n_tokens, n_kv_heads, group, max_ctx).nc;
         if (nmf > nc) nc = nmf;
+        if (n_tokens >= kTileMinTokens) {  // or the shared-tile kernel (aligned buffers)
+            const int tchunk = TileChunk(n_tokens, n_heads, n_kv_heads, max_ctx);
+            const int64_t ntl = (max_ctx + tchunk - 1) / tchunk;
+            if (ntl > nc) nc = ntl;
+        }
     }
     if (nc == 1) return 0;
     return n_tokens * n_heads * nc * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
@@ -835,6 +841,45 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
         return LaunchPrefill(q, q_row_stride, k_cache + layer * max_seq * slot,
                              v_cache + layer * max_seq * slot, slot, n_heads, n_kv_heads,
                              head_dim, pos0, n_tokens, out, AsStream(stream));
+    }
+    if (n_tokens >= kTileMinTokens && PrefillSupported(head_dim, q, q_row_stride, out, k_cache, v_cache) &&
+        Aligned(workspace, 16)) {
+        // several decode tokens: 16 per workgroup share each K/V tile of a
+        // chunk of positions (the prefill kernel's matrix-core tiles), then
+        // AttnCombine merges the chunks
+        const int tchunk = TileChunk(n_tokens, n_heads, n_kv_heads, max_ctx);
+        const int64_t tnc = (max_ctx + tchunk - 1) / tchunk;
+        const int64_t need = tnc > 1 ? n_tokens * n_heads * tnc * (head_dim + 2) *
+                                           static_cast<int64_t>(sizeof(float))
+                                     : 0;
+        if (tnc > 1 && (workspace == nullptr || static_cast<int64_t>(workspace_bytes) < need)) {
+            return Fail(MLK_ERR_INVALID, "%s: workspace of %lld bytes needed (got %zu)", fn,
+                        static_cast<long long>(need), workspace_bytes);
+        }
+        if (n_tokens * n_heads > 0x7FFFFFFF) return Fail(MLK_ERR_INVALID, "%s: launch too large", fn);
+        float* ws_acc = tnc > 1 ? static_cast<float*>(workspace) : nullptr;
+        float* ws_ml = tnc > 1 ? ws_acc + n_tokens * n_heads * tnc * head_dim : nullptr;
+        const hipStream_t s = AsStream(stream);
+        st = LaunchDecodeTile(q, q_row_stride, k_cache + layer * max_seq * slot,
+                              v_cache + layer * max_seq * slot, slot, n_heads, n_kv_heads,
+                              head_dim, positions, pos0, n_tokens, max_ctx, out, ws_acc, ws_ml,
+                              err, s);
+        if (st != MLK_OK || tnc == 1) return st;
+        AttnParams p{};
+        p.positions = positions;
+        p.pos0 = pos0;
+        p.max_ctx = max_ctx;
+        p.H = n_heads;
+        p.hd = head_dim;
+        p.chunk = tchunk;
+        p.n_chunks = static_cast<int>(tnc);
+        p.out = out;
+        p.ws_acc = ws_acc;
+        p.ws_ml = ws_ml;
+        p.err = err;
+        hipLaunchKernelGGL(AttnCombine, dim3(static_cast<unsigned>(n_tokens * n_heads)),
+                           dim3(kAttnThreads), 0, s, p);
+        return CheckLaunch("AttnCombine");
     }
     const int group = n_heads / n_kv_heads;
     const bool mf = MfSupported(head_dim) && Aligned(k_cache, 16);

@@ -82,11 +82,23 @@ struct KvTile {
     }
 };
 
-template <int HD>
+// kChunked (decode tokens at any positions, AttnDecodeTile below): the
+// token's position comes from `positions`, and the workgroup covers one
+// chunk of cache positions, writing partials for AttnCombine.
+struct TileChunks {
+    const int32_t* positions;  // per token, or null: pos0 + t
+    int64_t max_ctx;
+    int chunk, n_chunks;
+    float* ws_acc;  // [T, H, n_chunks, hd]
+    float* ws_ml;   // [T, H, n_chunks, 2]
+    int32_t* err;
+};
+
+template <int HD, bool kChunked>
 __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const float* __restrict__ q, int64_t q_stride, const float* __restrict__ kc,
     const float* __restrict__ vc, int64_t slot, int KV, int H, int32_t pos0, int64_t T,
-    float scale, float* __restrict__ out, int head_blocks) {
+    float scale, float* __restrict__ out, int head_blocks, TileChunks tc) {
 #pragma clang fp contract(off)
     constexpr int LD = HD + 4;
     constexpr int NC = HD / 16;                          // 16-dim chunks
@@ -98,6 +110,11 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     bid /= head_blocks;
     const int g = static_cast<int>(bid % KV);
     bid /= KV;
+    int ck = 0;  // the chunk (kChunked)
+    if constexpr (kChunked) {
+        ck = static_cast<int>(bid / n_tb);
+        bid %= n_tb;
+    }
     const int64_t t0 = (n_tb - 1 - bid) * kPfTokens;
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
@@ -107,8 +124,34 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const int h = g * group + (active ? hq : 0);
     const int64_t last_t = (t0 + kPfTokens < T ? t0 + kPfTokens : T) - 1;
     const int64_t t = t0 + i16 <= last_t ? t0 + i16 : last_t;  // this lane's query token
-    const int64_t my_pos = pos0 + t;
-    const int64_t max_pos = pos0 + last_t;
+    int64_t my_pos = pos0 + t;
+    int64_t max_pos = pos0 + last_t;
+    int64_t p_begin = 0, p_end = max_pos + 1;  // cache positions of this workgroup
+    bool valid = true;
+    if constexpr (kChunked) {
+        const int32_t pt = tc.positions != nullptr ? tc.positions[t] : pos0 + static_cast<int32_t>(t);
+        valid = pt >= 0 && pt < tc.max_ctx;
+        if (!valid && ck == 0 && hb == 0 && g == 0 && t0 + i16 <= last_t) RaiseFlag(tc.err, 1);
+        my_pos = valid ? pt : -1;  // an invalid token attends nothing
+        // the block's last position: the maximum over its 16 tokens
+        int32_t mx = static_cast<int32_t>(my_pos);
+#pragma unroll
+        for (int o = 1; o < 16; o *= 2) mx = max(mx, __shfl_xor(mx, o, kWave));
+        max_pos = mx;
+        p_begin = static_cast<int64_t>(ck) * tc.chunk;
+        p_end = p_begin + tc.chunk < max_pos + 1 ? p_begin + tc.chunk : max_pos + 1;
+        if (p_begin >= p_end) {  // no token of the block reaches this chunk
+            if (tc.n_chunks == 1 && active && t0 + i16 <= last_t) {
+                // every token invalid, and no merge follows: zero rows
+                float* orow = out + (t * H + h) * static_cast<int64_t>(HD) + 4 * kq;
+#pragma unroll
+                for (int cc = 0; cc < NC; ++cc) {
+                    *reinterpret_cast<float4*>(orow + 16 * cc) = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+            return;
+        }
+    }
 
     f32x4 qv[NC];
     const float* qrow = q + t * q_stride + static_cast<int64_t>(h) * HD + 4 * kq;
@@ -129,14 +172,14 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     float m = -INFINITY;  // running max of query i16 (equal in its 4 lane groups)
     float l = 0.0f;       // this lane's part of the running sum
 
-    const int64_t n_tiles = max_pos / kPfTile + 1;
-    load(0);
+    const int64_t n_tiles = (p_end - p_begin + kPfTile - 1) / kPfTile;
+    load(p_begin);
     store(0);
     __syncthreads();
     for (int64_t it = 0; it < n_tiles; ++it) {
         const int buf = static_cast<int>(it & 1);
-        const int64_t p0 = it * kPfTile;
-        load((it + 1 < n_tiles ? it + 1 : it) * kPfTile);
+        const int64_t p0 = p_begin + it * kPfTile;
+        load(p_begin + (it + 1 < n_tiles ? it + 1 : it) * kPfTile);
         {  // idle waves (a head block past the group) compute too, unstored
             f32x4 s[2];
 #pragma unroll
@@ -167,15 +210,20 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
             }
             tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
             tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-            const float mnew = fmaxf(m, tmax);  // finite: position 0 is in every query's range
-            const float corr = expf(m - mnew);
+            // finite: position 0 is in every query's range.  In a chunk, a
+            // token before the chunk (or invalid) sees only -inf: it is
+            // referenced to 0 and keeps m = -inf, l = 0 (AttnCombine never
+            // reads that partial).
+            const float mnew = fmaxf(m, tmax);
+            const float mref = kChunked && mnew == -INFINITY ? 0.0f : mnew;
+            const float corr = expf(m - mref);
             l *= corr;
 #pragma unroll
             for (int c = 0; c < NC; ++c) acc[c] *= corr;
             float pv[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                pv[i] = expf(sv[i] - mnew);
+                pv[i] = expf(sv[i] - mref);
                 l += pv[i];
             }
             m = mnew;
@@ -198,6 +246,30 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     l += __shfl_xor(l, 16, kWave);
     l += __shfl_xor(l, 32, kWave);
     if (!active || t0 + i16 > last_t) return;
+    if constexpr (kChunked) {
+        const int64_t row = t * H + h;
+        if (tc.n_chunks > 1) {  // unnormalized partials, merged by AttnCombine
+            float* arow = tc.ws_acc + (row * tc.n_chunks + ck) * HD + 4 * kq;
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) {
+                *reinterpret_cast<float4*>(arow + 16 * cc) =
+                    make_float4(acc[cc][0], acc[cc][1], acc[cc][2], acc[cc][3]);
+            }
+            if (kq == 0) {
+                tc.ws_ml[(row * tc.n_chunks + ck) * 2] = m;
+                tc.ws_ml[(row * tc.n_chunks + ck) * 2 + 1] = l;
+            }
+            return;
+        }
+        if (!valid) {  // one chunk: the row is final here
+            float* orow = out + row * HD + 4 * kq;
+#pragma unroll
+            for (int cc = 0; cc < NC; ++cc) {
+                *reinterpret_cast<float4*>(orow + 16 * cc) = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            return;
+        }
+    }
     float* orow = out + (t * H + h) * static_cast<int64_t>(HD) + 4 * kq;
     const float inv = 1.0f / l;
 #pragma unroll
@@ -225,14 +297,50 @@ mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, 
     if (blocks > 0x7FFFFFFF) return Fail(MLK_ERR_INVALID, "attention prefill: launch too large");
     const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
     const dim3 grid(static_cast<unsigned>(blocks));
+    const TileChunks none{};
     if (head_dim == 64) {
-        hipLaunchKernelGGL(AttnPrefill<64>, grid, dim3(kPfThreads), 0, s, q, q_row_stride, kc, vc,
-                           slot, KV, H, pos0, T, scale, out, head_blocks);
+        hipLaunchKernelGGL((AttnPrefill<64, false>), grid, dim3(kPfThreads), 0, s, q, q_row_stride,
+                           kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks, none);
     } else {
-        hipLaunchKernelGGL(AttnPrefill<128>, grid, dim3(kPfThreads), 0, s, q, q_row_stride, kc,
-                           vc, slot, KV, H, pos0, T, scale, out, head_blocks);
+        hipLaunchKernelGGL((AttnPrefill<128, false>), grid, dim3(kPfThreads), 0, s, q,
+                           q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
+                           none);
     }
     return CheckLaunch("AttnPrefill");
+}
+
+int TileChunk(int64_t T, int32_t H, int32_t KV, int64_t max_ctx) {
+    const int group = H / KV;
+    const int64_t base = (T + kPfTokens - 1) / kPfTokens * KV * ((group + kPfHeads - 1) / kPfHeads);
+    int chunk = 2048;
+    while (chunk > 256 && base * ((max_ctx + chunk - 1) / chunk) < 512) chunk /= 2;
+    return chunk;
+}
+
+mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* kc,
+                            const float* vc, int64_t slot, int32_t H, int32_t KV,
+                            int32_t head_dim, const int32_t* positions, int32_t pos0, int64_t T,
+                            int64_t max_ctx, float* out, float* ws_acc, float* ws_ml,
+                            int32_t* err, hipStream_t s) {
+    const int group = H / KV;
+    const int head_blocks = (group + kPfHeads - 1) / kPfHeads;
+    const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
+    const int chunk = TileChunk(T, H, KV, max_ctx);
+    const int64_t nc = (max_ctx + chunk - 1) / chunk;
+    const int64_t blocks = n_tb * KV * head_blocks * nc;
+    if (blocks > 0x7FFFFFFF) return Fail(MLK_ERR_INVALID, "attention decode: launch too large");
+    TileChunks tc{positions, max_ctx, chunk, static_cast<int>(nc), ws_acc, ws_ml, err};
+    const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if (head_dim == 64) {
+        hipLaunchKernelGGL((AttnPrefill<64, true>), grid, dim3(kPfThreads), 0, s, q, q_row_stride,
+                           kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks, tc);
+    } else {
+        hipLaunchKernelGGL((AttnPrefill<128, true>), grid, dim3(kPfThreads), 0, s, q,
+                           q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
+                           tc);
+    }
+    return CheckLaunch("AttnPrefill (decode tokens)");
 }
 
 }  // namespace mlk

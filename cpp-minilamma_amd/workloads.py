@@ -129,6 +129,13 @@ def flops_prefill_attention(T, H, hd, pos0=0):
     return 4 * hd * H * n_pairs
 
 
+def flops_decode_attention(positions, n_heads, head_dim):
+    """Decode tokens at the given positions: per head and attended position
+    (0..pos), q.k and p v, 2 hd flops each."""
+    pos = np.asarray(positions, np.int64)
+    return int(4 * head_dim * n_heads * (pos + 1).sum())
+
+
 def bytes_attention(positions, n_heads, n_kv_heads, head_dim):
     """Read the K and V rows 0..pos of each token's KV heads once, read q,
     write out: 8 * (pos + 1) * KV * hd per token + 8 * H * hd."""
