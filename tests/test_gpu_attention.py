@@ -226,6 +226,43 @@ def test_attention_bad_positions_give_zero_rows_and_flag(mlk):
         assert ok.download()[0] == 0
 
 
+@pytest.mark.parametrize("H,KV,hd,T,S", [(32, 8, 128, 21, 3000), (6, 2, 64, 4, 300),
+                                         (8, 8, 64, 40, 700), (12, 2, 128, 17, 256)])
+def test_attention_shared_tiles_any_positions(mlk, H, KV, hd, T, S):
+    """4 or more decode tokens at arbitrary (unsorted, repeated) positions
+    take the shared-tile kernel: 16 tokens per workgroup over chunks of the
+    cache, merged afterwards.  Shapes cover a partial token block, a GQA
+    group that is not a multiple of 4 (idle waves), one chunk (S = 256) and
+    many."""
+    rng = np.random.default_rng(T * 100 + hd)
+    kc, vc = random_cache(rng, 2, S, KV, hd)
+    cache = Cache(mlk, kc, vc)
+    pos = rng.integers(0, S, size=T).astype(np.int32)
+    pos[0] = S - 1
+    pos[-1] = 0
+    if T > 4:
+        pos[2] = pos[3]
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    got = cache.attend(q, 1, pos)
+    for t in range(T):
+        ex, pav, dmax, n = attention_exact(q[t], kc, vc, 1, int(pos[t]))
+        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t} pos {pos[t]}")
+
+
+def test_attention_shared_tiles_all_invalid_one_chunk(mlk):
+    """Every token of a block out of range with a single chunk: no merge
+    follows, so the kernel itself zeroes the rows and raises the flag."""
+    rng = np.random.default_rng(8)
+    H, KV, hd, S = 8, 2, 64, 64
+    kc, vc = random_cache(rng, 1, S, KV, hd)
+    cache = Cache(mlk, kc, vc)
+    q = rng.standard_normal((5, H, hd)).astype(np.float32)
+    err = mlk.DeviceBuffer.from_array(np.zeros(1, np.int32))
+    got = cache.attend(q, 0, [-1, 40, 41, -7, 63], max_ctx=40, err=err)
+    assert err.download()[0] != 0
+    assert not got.any()
+
+
 def test_attention_rejects_bad_arguments(mlk):
     kc = mlk.DeviceBuffer.empty((2, 16, 2, 8))
     vc = mlk.DeviceBuffer.empty((2, 16, 2, 8))
