@@ -489,14 +489,21 @@ struct SkinnyArgs {
 // computed (one round of memory latency per workgroup); the chunk's sums go
 // to partial[chunk] for the reduction, or straight to y (+ bias) when K is
 // one chunk.
-template <int WT, int TT>
+// NP > 1 (quantized weights, up to 16 rows): the workgroup takes NP
+// consecutive chunks, all of their loads in flight at once, so the partial
+// sums (written and read once each by the reduction) shrink NP times.
+template <int WT, int TT, int NP>
 __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict__ x,
                                                          SkinnyArgs a, int64_t T, int64_t K,
                                                          int64_t row_bytes,
                                                          float* __restrict__ partial) {
     using WC = WChunk<WT>;
     constexpr int D = WC::kStages;
-    constexpr int kChunk = 32 * D;
+    constexpr int kSub = 32 * D;  // inputs of one chunk
+    constexpr int kChunk = kSub * NP;
+    static_assert(NP == 1 || WC::kPieces, "several chunks per workgroup: quantized weights");
+    // padded LDS offset of chunk p's inputs (4 floats after every 64)
+    constexpr int kSubX = WC::kPieces ? kSub + kSub / 16 : kSub;
     using XC = XChunk<TT, kChunk, WC::kPieces>;
     __shared__ __align__(16) float xs[16 * TT * XC::RS];
     const int rgall = static_cast<int>(blockIdx.x) % a.row_groups;
@@ -512,8 +519,9 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
     const int64_t wrow = row < O ? row : O - 1;
     const int64_t k0 = static_cast<int64_t>(sp) * kChunk;
 
-    WC wc;
-    wc.Load(w, wrow, row_bytes, k0, q);
+    WC wc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) wc[p].Load(w, wrow, row_bytes, k0 + p * kSub, q);
     XC xc;
     xc.Load(x, T, K, k0);
     xc.Store(xs);
@@ -522,11 +530,12 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < D; ++u) {
+    for (int pu = 0; pu < NP * D; ++pu) {
+        const int p = pu / D, u = pu % D;
         float xa[TT][8];
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) {
-            const float* src = xs + (tt * 16 + i16) * XC::RS + WC::XOff(u, q);
+            const float* src = xs + (tt * 16 + i16) * XC::RS + p * kSubX + WC::XOff(u, q);
             const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
             const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
 #pragma unroll
@@ -537,7 +546,7 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float wv = wc.Get(u, j);
+            const float wv = wc[p].Get(u, j);
 #pragma unroll
             for (int tt = 0; tt < TT; ++tt) {
                 acc[tt] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa[tt][j], wv, acc[tt], 0, 0, 0);
@@ -644,9 +653,16 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
 
 int SkinnyChunk(int wt) { return wt == kWF32 ? 32 * WChunk<kWF32>::kStages : 32 * 8; }
 
-// The skinny kernel takes one K chunk per workgroup: K / chunk splits.
-SplitPlan PlanSkinny(int wt, int64_t K, int64_t) {
-    const int64_t chunk = SkinnyChunk(wt);
+// Chunks per workgroup: two for quantized weights up to 16 rows (one tile
+// of x rows) when K allows, else one.
+int SkinnyPieces(int wt, int64_t T, int64_t K) {
+    return wt != kWF32 && T <= 16 && K % (2 * SkinnyChunk(wt)) == 0 ? 2 : 1;
+}
+
+// The skinny kernel takes SkinnyPieces chunks per workgroup: K / (that many
+// chunks) splits.
+SplitPlan PlanSkinny(int wt, int64_t T, int64_t K) {
+    const int64_t chunk = SkinnyChunk(wt) * SkinnyPieces(wt, T, K);
     SplitPlan p;
     p.per_split = chunk;
     p.splits = static_cast<int>(K / chunk);
@@ -660,25 +676,27 @@ bool SkinnyApplies(int wt, int64_t T, int64_t K) {
     return rows && K % SkinnyChunk(wt) == 0 && K / SkinnyChunk(wt) <= 4096;
 }
 
-template <int TT>
+template <int TT, int NP>
 void LaunchSkinnyT(int wt, dim3 grid, hipStream_t s, const float* x, const SkinnyArgs& a,
                    int64_t T, int64_t K, int64_t row_bytes, float* partial) {
     switch (wt) {
         case MLK_Q8_0:
-            hipLaunchKernelGGL((GemmSkinny<MLK_Q8_0, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
-                               row_bytes, partial);
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q8_0, TT, NP>), grid, dim3(kSkThreads), 0, s, x, a,
+                               T, K, row_bytes, partial);
             break;
         case MLK_Q4_0:
-            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_0, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
-                               row_bytes, partial);
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_0, TT, NP>), grid, dim3(kSkThreads), 0, s, x, a,
+                               T, K, row_bytes, partial);
             break;
         case MLK_Q4_1:
-            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_1, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
-                               row_bytes, partial);
+            hipLaunchKernelGGL((GemmSkinny<MLK_Q4_1, TT, NP>), grid, dim3(kSkThreads), 0, s, x, a,
+                               T, K, row_bytes, partial);
             break;
         default:
-            hipLaunchKernelGGL((GemmSkinny<kWF32, TT>), grid, dim3(kSkThreads), 0, s, x, a, T, K,
-                               row_bytes, partial);
+            if constexpr (NP == 1) {
+                hipLaunchKernelGGL((GemmSkinny<kWF32, TT, 1>), grid, dim3(kSkThreads), 0, s, x, a,
+                                   T, K, row_bytes, partial);
+            }
             break;
     }
 }
@@ -690,10 +708,12 @@ mlk_status LaunchSkinny(int wt, const float* x, const SkinnyArgs& a, int64_t T, 
                     static_cast<long long>(a.cols));
     }
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.row_groups) * splits));
-    if (T <= 16) {
-        LaunchSkinnyT<1>(wt, grid, s, x, a, T, K, row_bytes, partial);
+    if (SkinnyPieces(wt, T, K) == 2) {
+        LaunchSkinnyT<1, 2>(wt, grid, s, x, a, T, K, row_bytes, partial);
+    } else if (T <= 16) {
+        LaunchSkinnyT<1, 1>(wt, grid, s, x, a, T, K, row_bytes, partial);
     } else {
-        LaunchSkinnyT<2>(wt, grid, s, x, a, T, K, row_bytes, partial);
+        LaunchSkinnyT<2, 1>(wt, grid, s, x, a, T, K, row_bytes, partial);
     }
     return CheckLaunch("GemmSkinny");
 }
@@ -725,7 +745,7 @@ void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t
 }  // namespace
 
 int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O) {
-    const SplitPlan p = SkinnyApplies(wt, T, K) ? PlanSkinny(wt, K, O) : PlanSplits(T, K, O);
+    const SplitPlan p = SkinnyApplies(wt, T, K) ? PlanSkinny(wt, T, K) : PlanSplits(T, K, O);
     return p.splits > 1 ? static_cast<int64_t>(p.splits) * T * O * 4 : 0;
 }
 
@@ -738,7 +758,7 @@ int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O) {
 mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, float* y,
                       int64_t T, int64_t K, int64_t O, int64_t row_bytes, void* workspace,
                       size_t workspace_bytes, hipStream_t s) {
-    const SplitPlan sk = PlanSkinny(wt, K, O);
+    const SplitPlan sk = PlanSkinny(wt, T, K);
     const bool sk_ws = sk.splits == 1 ||
                        (workspace != nullptr && Aligned(workspace, 16) &&
                         workspace_bytes >= static_cast<size_t>(sk.splits) * T * O * 4);
@@ -807,7 +827,7 @@ bool SkinnyFusedApplies(int wt, int64_t T, int64_t K) {
 }
 
 int64_t SkinnyFusedWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t cols) {
-    return static_cast<int64_t>(PlanSkinny(wt, K, cols).splits) * T * cols * 4;
+    return static_cast<int64_t>(PlanSkinny(wt, T, K).splits) * T * cols * 4;
 }
 
 // T token rows through up to three quantized weight matrices with the same K
@@ -838,7 +858,7 @@ mlk_status LinearSkinnyFused(int wt, const float* x, int64_t T, int64_t K, const
     a.n_seg = sa.n_seg;
     a.row_groups = static_cast<int>(groups);
     a.cols = cols;
-    const SplitPlan plan = PlanSkinny(wt, K, cols);
+    const SplitPlan plan = PlanSkinny(wt, T, K);
     const int64_t need = static_cast<int64_t>(plan.splits) * T * cols * 4;
     if (workspace == nullptr || !Aligned(workspace, 16) ||
         static_cast<int64_t>(workspace_bytes) < need || groups > 0x3FFFFFFF) {
