@@ -489,7 +489,7 @@ struct SkinnyArgs {
 // computed (one round of memory latency per workgroup); the chunk's sums go
 // to partial[chunk] for the reduction, or straight to y (+ bias) when K is
 // one chunk.
-// NP > 1 (quantized weights, up to 16 rows): the workgroup takes NP
+// NP > 1 (quantized weights): the workgroup takes NP
 // consecutive chunks, all of their loads in flight at once, so the partial
 // sums (written and read once each by the reduction) shrink NP times.
 template <int WT, int TT, int NP>
@@ -653,10 +653,10 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
 
 int SkinnyChunk(int wt) { return wt == kWF32 ? 32 * WChunk<kWF32>::kStages : 32 * 8; }
 
-// Chunks per workgroup: two for quantized weights up to 16 rows (one tile
-// of x rows) when K allows, else one.
+// Chunks per workgroup: two for quantized weights when K is a multiple of
+// two chunks, else one.
 int SkinnyPieces(int wt, int64_t T, int64_t K) {
-    return wt != kWF32 && T <= 16 && K % (2 * SkinnyChunk(wt)) == 0 ? 2 : 1;
+    return wt != kWF32 && T <= 32 && K % (2 * SkinnyChunk(wt)) == 0 ? 2 : 1;
 }
 
 // The skinny kernel takes SkinnyPieces chunks per workgroup: K / (that many
@@ -709,7 +709,11 @@ mlk_status LaunchSkinny(int wt, const float* x, const SkinnyArgs& a, int64_t T, 
     }
     const dim3 grid(static_cast<unsigned>(static_cast<int64_t>(a.row_groups) * splits));
     if (SkinnyPieces(wt, T, K) == 2) {
-        LaunchSkinnyT<1, 2>(wt, grid, s, x, a, T, K, row_bytes, partial);
+        if (T <= 16) {
+            LaunchSkinnyT<1, 2>(wt, grid, s, x, a, T, K, row_bytes, partial);
+        } else {
+            LaunchSkinnyT<2, 2>(wt, grid, s, x, a, T, K, row_bytes, partial);
+        }
     } else if (T <= 16) {
         LaunchSkinnyT<1, 1>(wt, grid, s, x, a, T, K, row_bytes, partial);
     } else {
