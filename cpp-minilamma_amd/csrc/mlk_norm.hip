@@ -45,6 +45,15 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(float* residual,
     const int64_t dim4 = dim >> 2;
     const double ddim = static_cast<double>(dim);
     int parity = 0;
+    // the norm weight is the same for every row: loaded once, before the
+    // first row's reduction, so no row waits on it after its sum
+    const float4* wr = reinterpret_cast<const float4*>(weight);
+    float4 wv[VPT];
+#pragma unroll
+    for (int v = 0; v < VPT; ++v) {
+        const int64_t i = tid + static_cast<int64_t>(v) * lanes;
+        wv[v] = i < dim4 ? wr[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x, parity ^= 1) {
         float4* xr = reinterpret_cast<float4*>(residual + row * dim);
         const float4* dr = reinterpret_cast<const float4*>(delta + (kDelta ? row * dim : 0));
@@ -82,13 +91,12 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(float* residual,
         }
         ss = kWaves > 1 ? BlockSum<kWaves>(ss, partial[parity]) : WaveSum(ss);
         const double scale = 1.0 / sqrt(ss / ddim + static_cast<double>(eps));
-        const float4* wr = reinterpret_cast<const float4*>(weight);
         float4* yr = reinterpret_cast<float4*>(y + row * dim);
 #pragma unroll
         for (int v = 0; v < VPT; ++v) {
             const int64_t i = tid + static_cast<int64_t>(v) * lanes;
             if (i < dim4) {
-                const float4 w = wr[i];
+                const float4 w = wv[v];
                 float4 o;
                 o.x = static_cast<float>(static_cast<double>(r[v].x) * static_cast<double>(w.x) * scale);
                 o.y = static_cast<float>(static_cast<double>(r[v].y) * static_cast<double>(w.y) * scale);
