@@ -578,6 +578,7 @@ __global__ __launch_bounds__(kAttnThreads) void AttnDecodeMf(AttnParams p, int t
 // query head).  The chunk weights exp(m_c - M) are computed once into LDS
 // (in tiles of kCombineTile chunks).
 constexpr int kCombineTile = 1024;
+constexpr int kCombinePre = 32;  // partials per thread requested before the reductions
 
 __global__ __launch_bounds__(kAttnThreads) void AttnCombine(AttnParams p) {
     __shared__ float wgt[kCombineTile];
@@ -593,24 +594,40 @@ __global__ __launch_bounds__(kAttnThreads) void AttnCombine(AttnParams p) {
     }
     const int nc = pos / p.chunk + 1;
     const float* mlr = p.ws_ml + row * p.n_chunks * 2;
+    const float* acc = p.ws_acc + row * p.n_chunks * p.hd;
+    const int d = threadIdx.x;
+    // the first kCombinePre chunks' partials of this thread's dim, requested
+    // before the reductions below (clamped rows past nc are never used)
+    float pre[kCombinePre];
+#pragma unroll
+    for (int c = 0; c < kCombinePre; ++c) {
+        const int cc = c < nc ? c : nc - 1;
+        pre[c] = acc[static_cast<int64_t>(cc) * p.hd + (d < p.hd ? d : 0)];
+    }
     float mloc = -INFINITY;
     for (int c = threadIdx.x; c < nc; c += kAttnThreads) mloc = fmaxf(mloc, mlr[2 * c]);
     const float M = BlockMax<kAttnWaves>(mloc, redf);
     float lloc = 0.0f;
     for (int c = threadIdx.x; c < nc; c += kAttnThreads) lloc += mlr[2 * c + 1] * expf(mlr[2 * c] - M);
     const float L = static_cast<float>(BlockSum<kAttnWaves>(static_cast<double>(lloc), red));
-    const float* acc = p.ws_acc + row * p.n_chunks * p.hd;
     float a = 0.0f;
-    const int d = threadIdx.x;
     for (int c0 = 0; c0 < nc; c0 += kCombineTile) {
         const int n = min(kCombineTile, nc - c0);
         __syncthreads();
         for (int c = threadIdx.x; c < n; c += kAttnThreads) wgt[c] = expf(mlr[2 * (c0 + c)] - M);
         __syncthreads();
         if (d < p.hd) {
+            int c = 0;
+            if (c0 == 0) {
+#pragma unroll
+                for (int cp = 0; cp < kCombinePre; ++cp) {
+                    if (cp < n) a = fmaf(pre[cp], wgt[cp], a);
+                }
+                c = n < kCombinePre ? n : kCombinePre;
+            }
             const float* ac = acc + static_cast<int64_t>(c0) * p.hd + d;
 #pragma unroll 8
-            for (int c = 0; c < n; ++c) a = fmaf(ac[static_cast<int64_t>(c) * p.hd], wgt[c], a);
+            for (; c < n; ++c) a = fmaf(ac[static_cast<int64_t>(c) * p.hd], wgt[c], a);
         }
     }
     if (d < p.hd) o[d] = a / L;
