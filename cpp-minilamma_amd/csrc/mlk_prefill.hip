@@ -309,12 +309,16 @@ mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, 
     return CheckLaunch("AttnPrefill");
 }
 
+// Positions per chunk: a power of two from 256 up to the whole context,
+// halved while the grid has fewer than 512 workgroups.  Large batches then
+// take the context in one chunk (no partials, no merge).
 int TileChunk(int64_t T, int32_t H, int32_t KV, int64_t max_ctx) {
     const int group = H / KV;
     const int64_t base = (T + kPfTokens - 1) / kPfTokens * KV * ((group + kPfHeads - 1) / kPfHeads);
-    int chunk = 2048;
+    int64_t chunk = 256;
+    while (chunk < max_ctx && chunk < (int64_t{1} << 30)) chunk *= 2;
     while (chunk > 256 && base * ((max_ctx + chunk - 1) / chunk) < 512) chunk /= 2;
-    return chunk;
+    return static_cast<int>(chunk);
 }
 
 mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* kc,
