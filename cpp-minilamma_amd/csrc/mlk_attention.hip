@@ -54,7 +54,7 @@ constexpr int kAttnWaves = kAttnThreads / kWave;
 constexpr int kHalf = kWave / 2;  // lanes per position
 constexpr int kMaxHeadDim = 256;
 constexpr int64_t kPrefillMinTokens = 16;  // consecutive positions from here: AttnPrefill
-constexpr int64_t kTileMinTokens = 4;      // other batches from here: AttnPrefill's chunked form
+constexpr int64_t kTileMinTokens = 5;      // other batches from here: AttnPrefill's chunked form
 
 struct AttnParams {
     const float* q;

@@ -226,11 +226,11 @@ def test_attention_bad_positions_give_zero_rows_and_flag(mlk):
         assert ok.download()[0] == 0
 
 
-@pytest.mark.parametrize("H,KV,hd,T,S", [(32, 8, 128, 21, 3000), (6, 2, 64, 4, 300),
+@pytest.mark.parametrize("H,KV,hd,T,S", [(32, 8, 128, 21, 3000), (6, 2, 64, 5, 300),
                                          (8, 8, 64, 40, 700), (12, 2, 128, 17, 256),
                                          (8, 8, 64, 1024, 600)])
 def test_attention_shared_tiles_any_positions(mlk, H, KV, hd, T, S):
-    """4 or more decode tokens at arbitrary (unsorted, repeated) positions
+    """5 or more decode tokens at arbitrary (unsorted, repeated) positions
     take the shared-tile kernel: 16 tokens per workgroup over chunks of the
     cache, merged afterwards.  Shapes cover a partial token block, a GQA
     group that is not a multiple of 4 (idle waves), one chunk (S = 256) and
