@@ -144,6 +144,25 @@ def test_forward_layer_rejects(mlk, fwd):
         fwd.forward_layer_batch(cfg, w, x, 4, kc, kc, 1, 16, 0, 16, ws)
 
 
+def test_forward_layer_rejects_cache_arguments(mlk, fwd):
+    """The layer checks the caches before its first launch: the fused q/k/v
+    launch writes cache rows directly, so a bad layer index or a shared
+    K/V buffer must never reach a kernel."""
+    cfg = dict(vocab=64, dim=512, hidden_dim=1536, layers=1, n_heads=8, n_kv_heads=2,
+               head_dim=64, max_seq=32, rope_type=0, theta=10000.0, eps=1e-5)
+    model = O.forward_model(cfg, seed=2, weight_type="q8_0")
+    dm = fwd.DeviceModel(model)
+    x = mlk.DeviceBuffer.empty((1, 512))
+    kc, vc = mlk.DeviceBuffer.empty((1, 32, 2, 64)), mlk.DeviceBuffer.empty((1, 32, 2, 64))
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, 32, True), np.uint8)
+    with pytest.raises(mlk.MlkError, match="layer 1 out of range"):
+        fwd.forward_layer_batch(cfg, dm.layers[0], x, 1, kc, vc, 1, 32, 1, 32, ws, pos0=3)
+    with pytest.raises(mlk.MlkError, match="distinct"):
+        fwd.forward_layer_batch(cfg, dm.layers[0], x, 1, kc, kc, 1, 32, 0, 32, ws, pos0=3)
+    with pytest.raises(mlk.MlkError, match="out of range"):
+        fwd.forward_layer_batch(cfg, dm.layers[0], x, 1, kc, vc, 1, 32, 0, 32, ws, pos0=-1)
+
+
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0", "q4_1"])
 @pytest.mark.parametrize("T", [1, 12, 24])
 @pytest.mark.parametrize("case", ["pos0", "positions", "bad_position", "neox"])
