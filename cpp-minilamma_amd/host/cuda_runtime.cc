@@ -1,10 +1,14 @@
 // cuda_runtime.cc -- device runtime of the op surface (include/cuda_runtime.h)
 // over the C ABI of libminilamma_hip.so.  No HIP header is included here.
 //
-// Semantics follow the reference runtime (src/cuda_runtime.cc of the
-// reference tree): errors throw std::runtime_error "<what>: <message>",
-// zero-byte allocations are nullptr, copies of zero bytes are no-ops, and
-// host <-> device copies are counted for the thread's active stats.
+// Behaviour callers rely on (the reference's src/cuda_runtime.cc): errors
+// throw std::runtime_error "<what>: <message>", zero-byte allocations are
+// nullptr, copies of zero bytes are no-ops, and every host <-> device copy
+// is counted.  The counts go to two places: the CudaModelWeights that the
+// reference's internal::CudaStatsScope (src/internal/cuda_stats.h) makes
+// active through internal::active_cuda_stats, which this library defines
+// in place of the reference's runtime, and this library's own
+// CudaTransferStats scope.
 //
 // Allocation goes through a per-device caching allocator instead of one
 // hipMalloc/hipFree per tensor (the reference allocates every op result
@@ -13,6 +17,7 @@
 // the null stream, and synchronous copies on it wait for earlier kernels.
 #include "include/cuda_runtime.h"
 #include "include/minilamma_hip.h"
+#include "include/model.h"
 
 #include <algorithm>
 #include <map>
@@ -24,6 +29,12 @@
 #include <vector>
 
 namespace yan_lamma {
+namespace internal {
+// Declared by the reference in src/internal/cuda_stats.h; its
+// CudaStatsScope points this at the model whose forward pass is running.
+thread_local CudaModelWeights* active_cuda_stats = nullptr;
+}  // namespace internal
+
 namespace {
 
 thread_local std::shared_ptr<CudaAllocationStats> g_active_allocations;
@@ -124,6 +135,17 @@ BlockCache& Cache() {
     return *cache;
 }
 
+// One copy of `bytes` bytes added to a set of transfer counters (the same
+// four fields in CudaTransferStats and in the model's CudaModelWeights);
+// device-to-device copies are not transfers.
+template <class Counters>
+void Count(Counters* counters, CudaMemoryKind kind, size_t bytes) {
+    if (counters == nullptr || kind == CudaMemoryKind::kDeviceDevice) return;
+    const bool to_device = kind == CudaMemoryKind::kHostDevice;
+    (to_device ? counters->host_to_device_copies : counters->device_to_host_copies) += 1;
+    (to_device ? counters->host_to_device_bytes : counters->device_to_host_bytes) += bytes;
+}
+
 int32_t ToKind(CudaMemoryKind kind) {
     switch (kind) {
         case CudaMemoryKind::kHostDevice: return MLK_H2D;
@@ -135,16 +157,14 @@ int32_t ToKind(CudaMemoryKind kind) {
 
 }  // namespace
 
+// Scopes install their target for the thread and put the outer one back.
 CudaAllocationScope::CudaAllocationScope(std::shared_ptr<CudaAllocationStats> stats)
-    : previous_(std::move(g_active_allocations)) {
-    g_active_allocations = std::move(stats);
-}
+    : previous_(std::exchange(g_active_allocations, std::move(stats))) {}
 
-CudaAllocationScope::~CudaAllocationScope() { g_active_allocations = std::move(previous_); }
+CudaAllocationScope::~CudaAllocationScope() { g_active_allocations.swap(previous_); }
 
-CudaStatsScope::CudaStatsScope(CudaTransferStats* stats) : previous_(g_active_transfers) {
-    g_active_transfers = stats;
-}
+CudaStatsScope::CudaStatsScope(CudaTransferStats* stats)
+    : previous_(std::exchange(g_active_transfers, stats)) {}
 
 CudaStatsScope::~CudaStatsScope() { g_active_transfers = previous_; }
 
@@ -156,7 +176,7 @@ int DeviceCount() {
     return n;
 }
 
-void SetCudaService(int device_id) { Check(mlk_set_device(device_id), "hipSetDevice"); }
+void SetCudaService(int device_id) { Check(mlk_set_device(device_id), "cudaSetDevice"); }
 
 struct CudaInfo GetCudaInfo(int device_id) {
     mlk_device_info raw{};
@@ -173,12 +193,17 @@ struct CudaInfo GetCudaInfo(int device_id) {
 }
 
 std::string CudaInfo(const struct CudaInfo& info) {
-    std::ostringstream out;
-    out << "[HIP] device_id=" << info.device_id << " name=\"" << info.name << "\""
-        << " compute=" << info.compute_major << '.' << info.compute_minor
-        << " total_bytes=" << info.total_bytes << " runtime_version=" << info.runtime_version
-        << " driver_version=" << info.driver_version;
-    return out.str();
+    const std::pair<const char*, std::string> fields[] = {
+        {"device_id", std::to_string(info.device_id)},
+        {"name", '"' + info.name + '"'},
+        {"compute", std::to_string(info.compute_major) + "." + std::to_string(info.compute_minor)},
+        {"total_bytes", std::to_string(info.total_bytes)},
+        {"runtime_version", std::to_string(info.runtime_version)},
+        {"driver_version", std::to_string(info.driver_version)},
+    };
+    std::string line = "[HIP]";
+    for (const auto& field : fields) line += std::string(" ") + field.first + "=" + field.second;
+    return line;
 }
 
 void* CudaMemory(size_t byte_size) {
@@ -203,86 +228,100 @@ void CudaMemcpy(void* des, const void* src, size_t bytes, CudaMemoryKind kind) {
         throw std::runtime_error("cudaMemcpy requires non-null src and dst for non-empty copies");
     }
     Check(mlk_memcpy(des, src, bytes, ToKind(kind)), "hipMemcpy");
-    if (CudaTransferStats* s = g_active_transfers) {
-        if (kind == CudaMemoryKind::kHostDevice) {
-            ++s->host_to_device_copies;
-            s->host_to_device_bytes += bytes;
-        } else if (kind == CudaMemoryKind::kDeviceHost) {
-            ++s->device_to_host_copies;
-            s->device_to_host_bytes += bytes;
-        }
-    }
+    Count(internal::active_cuda_stats, kind, bytes);
+    Count(g_active_transfers, kind, bytes);
 }
 
 // ---------------------------------------------------------- device buffer
+//
+// A buffer is empty or owns one block of the cache above.  Its fields
+// change in three ways only: Reset claims a block (and charges the active
+// allocation scope), ReSet returns it (and refunds the scope that was
+// charged), and a move exchanges two buffers' states.  ReSet clears the
+// fields before handing the block back, so a failure there never leaves a
+// buffer pointing at memory it no longer owns.
 
-CudaDeviceBuffer::CudaDeviceBuffer(CudaDeviceBuffer&& other) noexcept
-    : data_(std::exchange(other.data_, nullptr)),
-      byte_size_(std::exchange(other.byte_size_, 0)),
-      device_id_(std::exchange(other.device_id_, 0)),
-      allocation_stats_(std::move(other.allocation_stats_)) {}
+namespace {
+
+void Charge(CudaAllocationStats* scope, size_t bytes) {
+    if (scope == nullptr) return;
+    scope->current_bytes += bytes;
+    scope->peak_bytes = std::max(scope->peak_bytes, scope->current_bytes);
+}
+
+void Refund(CudaAllocationStats* scope, size_t bytes) {
+    if (scope != nullptr) scope->current_bytes -= bytes;
+}
+
+// The checks of a host transfer of `bytes` bytes with a buffer of
+// `capacity` bytes (the reference's texts, which its tests match on).
+void CheckHostTransfer(const char* verb, size_t bytes, size_t capacity, const void* host,
+                       const void* device) {
+    if (bytes > capacity) {
+        throw std::runtime_error(std::string("CUDA ") + verb + " exceeds device buffer size");
+    }
+    if (host == nullptr || device == nullptr) {
+        throw std::runtime_error(std::string("CUDA ") + verb +
+                                 " requires non-null host and device pointers");
+    }
+}
+
+}  // namespace
+
+CudaDeviceBuffer::CudaDeviceBuffer(size_t byte_size, int device_id) { Reset(byte_size, device_id); }
+
+CudaDeviceBuffer::CudaDeviceBuffer(CudaDeviceBuffer&& other) noexcept {
+    // *this starts empty, so the exchange leaves `other` empty.
+    std::swap(data_, other.data_);
+    std::swap(byte_size_, other.byte_size_);
+    std::swap(device_id_, other.device_id_);
+    allocation_stats_.swap(other.allocation_stats_);
+}
 
 CudaDeviceBuffer& CudaDeviceBuffer::operator=(CudaDeviceBuffer&& other) noexcept {
     if (this != &other) {
-        ReleaseDevice();
-        data_ = std::exchange(other.data_, nullptr);
-        byte_size_ = std::exchange(other.byte_size_, 0);
-        device_id_ = std::exchange(other.device_id_, 0);
-        allocation_stats_ = std::move(other.allocation_stats_);
+        CudaDeviceBuffer previous(std::move(*this));  // returned when it goes out of scope
+        std::swap(data_, other.data_);
+        std::swap(byte_size_, other.byte_size_);
+        std::swap(device_id_, other.device_id_);
+        allocation_stats_.swap(other.allocation_stats_);
     }
     return *this;
 }
 
 void CudaDeviceBuffer::ReSet() {
-    if (data_ != nullptr) {
-        SetCudaService(device_id_);
-        CudaFreeMemory(data_);
-        if (allocation_stats_) allocation_stats_->current_bytes -= byte_size_;
-    }
-    data_ = nullptr;
-    byte_size_ = 0;
-    device_id_ = 0;
+    void* block = std::exchange(data_, nullptr);
+    const size_t held = std::exchange(byte_size_, 0);
+    const std::shared_ptr<CudaAllocationStats> scope = std::move(allocation_stats_);
     allocation_stats_.reset();
+    device_id_ = 0;
+    if (block == nullptr) return;
+    Refund(scope.get(), held);
+    Cache().Give(block);  // the cache knows the block's device
 }
 
 void CudaDeviceBuffer::Reset(size_t byte_size, int device_id) {
     ReSet();
-    if (byte_size == 0) {
-        device_id_ = device_id;
-        return;
+    if (byte_size > 0) {
+        SetCudaService(device_id);
+        data_ = Cache().Take(device_id, byte_size);
+        byte_size_ = byte_size;
+        allocation_stats_ = g_active_allocations;
+        Charge(allocation_stats_.get(), byte_size);
     }
-    SetCudaService(device_id);
-    data_ = CudaMemory(byte_size);
-    byte_size_ = byte_size;
-    device_id_ = device_id;
-    allocation_stats_ = g_active_allocations;
-    if (allocation_stats_) {
-        allocation_stats_->current_bytes += byte_size;
-        allocation_stats_->peak_bytes =
-            std::max(allocation_stats_->peak_bytes, allocation_stats_->current_bytes);
-    }
+    device_id_ = device_id;  // an empty buffer still records its device
 }
-
-CudaDeviceBuffer::CudaDeviceBuffer(size_t byte_size, int device_id) { Reset(byte_size, device_id); }
 
 void CudaDeviceBuffer::upload(const void* src, size_t byte_size) {
     if (byte_size == 0) return;
-    if (byte_size > byte_size_) throw std::runtime_error("CUDA upload exceeds device buffer size");
-    if (src == nullptr || data_ == nullptr) {
-        throw std::runtime_error("CUDA upload requires non-null host and device pointers");
-    }
+    CheckHostTransfer("upload", byte_size, byte_size_, src, data_);
     SetCudaService(device_id_);
     CudaMemcpy(data_, src, byte_size, CudaMemoryKind::kHostDevice);
 }
 
 void CudaDeviceBuffer::download(void* des, size_t byte_size) const {
     if (byte_size == 0) return;
-    if (byte_size > byte_size_) {
-        throw std::runtime_error("CUDA download exceeds device buffer size");
-    }
-    if (des == nullptr || data_ == nullptr) {
-        throw std::runtime_error("CUDA download requires non-null host and device pointers");
-    }
+    CheckHostTransfer("download", byte_size, byte_size_, des, data_);
     SetCudaService(device_id_);
     CudaMemcpy(des, data_, byte_size, CudaMemoryKind::kDeviceHost);
 }
@@ -291,11 +330,8 @@ void CudaDeviceBuffer::ReleaseDevice() noexcept {
     try {
         ReSet();
     } catch (...) {
-        // a failed release must not escape a destructor or a move
+        // ReSet cleared the fields before it failed; nothing is left to undo
     }
-    data_ = nullptr;
-    byte_size_ = 0;
-    device_id_ = 0;
 }
 
 CudaDeviceBuffer::~CudaDeviceBuffer() { ReleaseDevice(); }

@@ -1,51 +1,37 @@
 // cuda_tensor.cc -- move-only fp32 device tensor (include/cuda_tensor.h).
 //
-// Semantics of the reference's device tensor (src/cuda_tensor.cc of the
-// reference tree): shapes are non-empty with positive dimensions, Reset
-// replaces the allocation only after every check passed, Reshape keeps the
-// allocation and requires the same element count, uploads and downloads
-// require the host shape to match.
+// A CudaTensor is a shape, a device id, an element count and one device
+// buffer; all four change together or not at all.  Behaviour callers rely
+// on (the reference's src/cuda_tensor.cc): shapes are non-empty with
+// positive dimensions, a failed Reset leaves the tensor as it was, Reshape
+// keeps the allocation and the element count, uploads and downloads need a
+// non-empty tensor and a host tensor of exactly its shape.  Messages keep
+// the reference's caller names and phrases, which its tests match on.
 #include "include/cuda_tensor.h"
 
-#include <limits>
+#include "host_checks.h"
+
 #include <stdexcept>
 #include <string>
 #include <utility>
 
 namespace yan_lamma {
 namespace {
+using hostcheck::Raise;
+using hostcheck::ShapeText;
 
-std::string Join(const std::vector<int>& shape) {
-    std::string s = "[";
-    for (size_t i = 0; i < shape.size(); ++i) {
-        if (i) s += ", ";
-        s += std::to_string(shape[i]);
+// The checks shared by UploadFromHost and DownloadToHost: a device tensor to
+// copy with, and a host tensor of the same shape and length.
+void CheckHostPeer(const CudaTensor& dev, const Tensor& host, const char* caller,
+                   const char* verb) {
+    if (dev.IsEmpty()) Raise(caller, std::string("cannot ") + verb + " an empty tensor");
+    if (host.shape != dev.shape()) {
+        Raise(caller, "expected host shape " + ShapeText(dev.shape()) + ", got " +
+                          ShapeText(host.shape));
     }
-    return s + "]";
-}
-
-size_t CheckedCount(const std::vector<int>& shape, const std::string& caller) {
-    if (shape.empty()) throw std::runtime_error(caller + ": shape must not be empty");
-    size_t total = 1;
-    for (size_t axis = 0; axis < shape.size(); ++axis) {
-        if (shape[axis] <= 0) {
-            throw std::runtime_error(caller + ": dimension at axis " + std::to_string(axis) +
-                                     " must be positive, got " + std::to_string(shape[axis]) +
-                                     " in shape " + Join(shape));
-        }
-        const size_t d = static_cast<size_t>(shape[axis]);
-        if (total > std::numeric_limits<size_t>::max() / d) {
-            throw std::runtime_error(caller + ": shape element count overflow for " + Join(shape));
-        }
-        total *= d;
-    }
-    return total;
-}
-
-void CheckHostShape(const Tensor& host, const std::vector<int>& shape, const std::string& caller) {
-    if (host.shape != shape) {
-        throw std::runtime_error(caller + ": expected host shape " + Join(shape) + ", got " +
-                                 Join(host.shape));
+    if (host.data.size() != dev.NumEle()) {
+        Raise(caller, "expected " + std::to_string(dev.NumEle()) + " host elements, got " +
+                          std::to_string(host.data.size()));
     }
 }
 
@@ -53,100 +39,81 @@ void CheckHostShape(const Tensor& host, const std::vector<int>& shape, const std
 
 CudaTensor::CudaTensor(const std::vector<int>& shape, int device_id) { Reset(shape, device_id); }
 
-CudaTensor::CudaTensor(CudaTensor&& other) noexcept
-    : shape_(std::move(other.shape_)),
-      device_id_(std::exchange(other.device_id_, 0)),
-      numel_(std::exchange(other.numel_, 0)),
-      cuda_buffer_(std::move(other.cuda_buffer_)) {
-    other.shape_.clear();
+CudaTensor::CudaTensor(CudaTensor&& other) noexcept {
+    // *this starts as a default tensor; exchanging leaves `other` as one.
+    shape_.swap(other.shape_);
+    std::swap(device_id_, other.device_id_);
+    std::swap(numel_, other.numel_);
+    std::swap(cuda_buffer_, other.cuda_buffer_);
 }
 
 CudaTensor& CudaTensor::operator=(CudaTensor&& other) noexcept {
     if (this != &other) {
-        cuda_buffer_ = std::move(other.cuda_buffer_);
-        shape_ = std::move(other.shape_);
-        device_id_ = std::exchange(other.device_id_, 0);
-        numel_ = std::exchange(other.numel_, 0);
-        other.shape_.clear();
+        CudaTensor previous(std::move(*this));  // released when it goes out of scope
+        CudaTensor incoming(std::move(other));
+        shape_.swap(incoming.shape_);
+        std::swap(device_id_, incoming.device_id_);
+        std::swap(numel_, incoming.numel_);
+        std::swap(cuda_buffer_, incoming.cuda_buffer_);
     }
     return *this;
 }
 
 void CudaTensor::Reset() {
-    cuda_buffer_.ReSet();
-    shape_.clear();
-    device_id_ = 0;
-    numel_ = 0;
+    CudaTensor previous(std::move(*this));
+    previous.cuda_buffer_.ReSet();  // release now, so a failure is reported
 }
 
 void CudaTensor::Reset(const std::vector<int>& shape, int device_id) {
-    const size_t numel = CheckedCount(shape, "CudaTensor::Reset");
-    std::vector<int> new_shape(shape);
-    CudaDeviceBuffer new_buffer(numel * sizeof(float), device_id);
-    cuda_buffer_ = std::move(new_buffer);
-    shape_ = std::move(new_shape);
-    device_id_ = device_id;
-    numel_ = numel;
+    // Build the new state completely (this may throw), then take it over.
+    CudaTensor fresh;
+    fresh.numel_ = hostcheck::ElementCount(shape, "CudaTensor::Reset", /*scalar_ok=*/false);
+    fresh.cuda_buffer_.Reset(fresh.numel_ * sizeof(float), device_id);
+    fresh.shape_ = shape;
+    fresh.device_id_ = device_id;
+    *this = std::move(fresh);
 }
 
 void CudaTensor::Reshape(const std::vector<int>& shape) {
-    const size_t numel = CheckedCount(shape, "CudaTensor::Reshape");
-    if (IsEmpty() || numel != numel_) {
-        throw std::runtime_error(
-            "CudaTensor::Reshape: element count must remain unchanged on a non-empty tensor");
+    const size_t count =
+        hostcheck::ElementCount(shape, "CudaTensor::Reshape", /*scalar_ok=*/false);
+    if (IsEmpty() || count != numel_) {
+        Raise("CudaTensor::Reshape", "element count must remain unchanged on a non-empty tensor");
     }
     shape_ = shape;
 }
 
 void CudaTensor::UploadFromHost(const Tensor& src) {
-    if (IsEmpty()) {
-        throw std::runtime_error("CudaTensor::UploadFromHost: cannot upload to an empty tensor");
-    }
-    CheckHostShape(src, shape_, "CudaTensor::UploadFromHost");
-    if (src.data.size() != NumEle()) {
-        throw std::runtime_error("CudaTensor::UploadFromHost: expected " +
-                                 std::to_string(NumEle()) + " host elements, got " +
-                                 std::to_string(src.data.size()));
-    }
+    CheckHostPeer(*this, src, "CudaTensor::UploadFromHost", "upload to");
     cuda_buffer_.upload(src.data.data(), Bytes());
 }
 
 void CudaTensor::DownloadToHost(Tensor& dst) const {
-    if (IsEmpty()) {
-        throw std::runtime_error("CudaTensor::DownloadToHost: cannot download an empty tensor");
-    }
-    CheckHostShape(dst, shape_, "CudaTensor::DownloadToHost");
-    if (dst.data.size() != NumEle()) {
-        throw std::runtime_error("CudaTensor::DownloadToHost: expected " +
-                                 std::to_string(NumEle()) + " host elements, got " +
-                                 std::to_string(dst.data.size()));
-    }
+    CheckHostPeer(*this, dst, "CudaTensor::DownloadToHost", "download");
     cuda_buffer_.download(dst.data.data(), Bytes());
 }
 
 Tensor CudaTensor::Download() const {
-    if (IsEmpty()) {
-        throw std::runtime_error("CudaTensor::Download: cannot download an empty tensor");
-    }
-    Tensor dst(shape_);
-    DownloadToHost(dst);
-    return dst;
+    if (IsEmpty()) Raise("CudaTensor::Download", "cannot download an empty tensor");
+    Tensor host(shape_);
+    cuda_buffer_.download(host.data.data(), Bytes());
+    return host;
 }
 
-const void* CudaTensor::GetData() const { return cuda_buffer_.GetData(); }
 void* CudaTensor::GetData() { return cuda_buffer_.GetData(); }
+const void* CudaTensor::GetData() const { return cuda_buffer_.GetData(); }
 bool CudaTensor::IsEmpty() const { return cuda_buffer_.IsEmpty(); }
 size_t CudaTensor::NumEle() const { return numel_; }
 int CudaTensor::num_dims() const { return static_cast<int>(shape_.size()); }
 size_t CudaTensor::Bytes() const { return cuda_buffer_.GetByteSize(); }
 int CudaTensor::DeviceId() const { return device_id_; }
+std::string CudaTensor::ShapeStringShort() const { return ShapeText(shape_); }
 const CudaDeviceBuffer& CudaTensor::buffer() const { return cuda_buffer_; }
 const std::vector<int>& CudaTensor::shape() const { return shape_; }
-std::string CudaTensor::ShapeStringShort() const { return Join(shape_); }
 
 CudaTensor TensorHostToDevice(const Tensor& src, int device_id) {
-    CudaTensor dst(src.shape, device_id);
-    dst.UploadFromHost(src);
-    return dst;
+    CudaTensor dev(src.shape, device_id);
+    dev.UploadFromHost(src);
+    return dev;
 }
 }  // namespace yan_lamma

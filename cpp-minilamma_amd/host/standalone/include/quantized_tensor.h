@@ -1,4 +1,7 @@
-// quantized_tensor.h -- GGUF-style 32-element block formats.
+// quantized_tensor.h -- stand-in for the part of the reference's
+// quantized-tensor header this library uses (GGUF-style 32-element block
+// formats), found only when the library is built on its own: inside the
+// reference tree its own include/quantized_tensor.h is found instead.
 //
 // Same enumerators, constants and packed block layouts as the reference
 // (include/quantized_tensor.h:10-36 of the reference tree): the quantized

@@ -1,9 +1,10 @@
-// tensor.h -- host fp32 tensor used by the op surface and its host variants.
-//
-// Same declarations and member layout as the reference's host tensor
-// (include/tensor.h:6-41 of the reference tree) so that the op-surface
-// library links against either this implementation
-// (cpp-minilamma_amd/host/tensor.cc) or the reference's own src/tensor.cc.
+// tensor.h -- stand-in for the reference's host tensor header, used only when
+// this library is built on its own (this directory comes after the
+// repository root on the include path, so inside the reference tree its own
+// include/tensor.h is found instead).  Same declarations and member layout
+// as the reference (include/tensor.h:6-41 of the reference tree), so the
+// op-surface library links against either cpp-minilamma_amd/host/tensor.cc
+// or the reference's own src/tensor.cc.
 #pragma once
 #include <cstddef>
 #include <string>

@@ -91,9 +91,10 @@ def test_op_surface_library_exports_the_reference_ops():
 
 def test_host_sources_include_no_hip_header():
     host = os.path.join(ROOT, "cpp-minilamma_amd", "host")
-    for f in os.listdir(host):
-        text = open(os.path.join(host, f)).read()
-        assert "hip_runtime" not in text and "cuda_runtime_api" not in text, f
+    for top, _, files in os.walk(host):
+        for f in files:
+            text = open(os.path.join(top, f)).read()
+            assert "hip_runtime" not in text and "cuda_runtime_api" not in text, f
 
 
 def test_validation_happens_before_any_device_call():
