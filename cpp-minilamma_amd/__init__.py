@@ -77,6 +77,8 @@ _SIGNATURES = {
                                  _i32, _i64, _i64, _vp, _vp, C.c_size_t, _vp, _vp],
     "mlk_attention_prefill_f32": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64, _i32,
                                   _i64, _vp, _vp],
+    "mlk_attention_decode_f32_noalloc": [_vp, _i64, _vp, _vp, _i64, _i64, _i32, _i32, _i32, _i64,
+                                         _vp, _i32, _i64, _i64, _vp, _vp, _vp],
     "mlk_device_count": [C.POINTER(C.c_int)],
     "mlk_set_device": [C.c_int],
     "mlk_get_device": [C.POINTER(C.c_int)],
@@ -122,6 +124,8 @@ def _load():
     lib.mlk_quant_bytes.argtypes = [_i32, _i64, _i64]
     lib.mlk_attention_workspace_bytes.restype = C.c_int64
     lib.mlk_attention_workspace_bytes.argtypes = [_i64, _i32, _i32, _i32, _i64]
+    lib.mlk_attention_noalloc_scratch_bytes.restype = C.c_size_t
+    lib.mlk_attention_noalloc_scratch_bytes.argtypes = []
     lib.mlk_linear_workspace_bytes.restype = C.c_int64
     lib.mlk_linear_workspace_bytes.argtypes = [_i64, _i64, _i64]
     return lib
@@ -484,6 +488,21 @@ def attention_decode(q, k_cache, v_cache, n_layers, max_seq, n_heads, n_kv_heads
                                        _p(out), _p(workspace), workspace_bytes, _p(err),
                                        _sp(stream)),
           "mlk_attention_decode_f32")
+
+
+def attention_decode_noalloc(q, k_cache, v_cache, n_layers, max_seq, n_heads, n_kv_heads,
+                             head_dim, layer, n_tokens, out, max_ctx, positions=None, pos0=0,
+                             q_row_stride=None, err=None, stream=None):
+    """attention_decode without a workspace: the chunk partials go to the
+    library's fixed per-GPU scratch (attention_noalloc_scratch_bytes())."""
+    check(lib.mlk_attention_decode_f32_noalloc(
+        _p(q), q_row_stride or n_heads * head_dim, _p(k_cache), _p(v_cache), n_layers, max_seq,
+        n_heads, n_kv_heads, head_dim, layer, _p(positions), pos0, n_tokens, max_ctx, _p(out),
+        _p(err), _sp(stream)), "mlk_attention_decode_f32_noalloc")
+
+
+def attention_noalloc_scratch_bytes():
+    return int(lib.mlk_attention_noalloc_scratch_bytes())
 
 
 def attention_prefill(q, k_cache, v_cache, n_layers, max_seq, n_heads, n_kv_heads, head_dim,

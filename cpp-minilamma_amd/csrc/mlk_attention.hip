@@ -42,6 +42,7 @@
 
 #include <math.h>
 
+#include <mutex>
 #include <utility>
 
 namespace mlk {
@@ -963,6 +964,85 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
         return CheckLaunch("AttnCombine");
     }
     return MLK_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------- no-allocation decode attention
+//
+// mlk_attention_decode_f32_noalloc keeps its chunk partials (per token, head
+// and chunk: head_dim weighted sums, the running max and the sum) in this
+// file-scope device array instead of a caller workspace.  Every GPU the
+// library runs on holds its own copy, at its own address, until the process
+// ends.  In host code `scratch` names a host-side stand-in, never the
+// device memory: the address each device uses comes from
+// hipGetSymbolAddress, taken once per device with that device current, and
+// only that address reaches a kernel.  The kernels write every partial the
+// combine step reads in the same call, so nothing needs clearing between
+// calls; calls that overlap on one GPU share the array and race.
+namespace mlk {
+namespace {
+constexpr size_t kScratchBytes = size_t{64} << 20;
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+}  // namespace mlk
+
+static __device__ __align__(256) unsigned char scratch[mlk::kScratchBytes];
+
+namespace mlk {
+namespace {
+// The device address of `scratch` on the current device, looked up on the
+// first call there.
+mlk_status ScratchOnCurrentDevice(const char* fn, void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return FromHip(e, "hipGetDevice");
+    if (dev < 0 || dev >= kScratchDevices) {
+        return Fail(MLK_ERR_INVALID, "%s: device %d beyond the %d devices this entry supports", fn,
+                    dev, kScratchDevices);
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return FromHip(e, "hipGetSymbolAddress(scratch)");
+        if (ptr == nullptr) return Fail(MLK_ERR_HIP, "%s: no device address for the scratch", fn);
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return MLK_OK;
+}
+}  // namespace
+}  // namespace mlk
+
+extern "C" {
+
+size_t mlk_attention_noalloc_scratch_bytes(void) { return mlk::kScratchBytes; }
+
+mlk_status mlk_attention_decode_f32_noalloc(const float* q, int64_t q_row_stride,
+                                            const float* k_cache, const float* v_cache,
+                                            int64_t n_layers, int64_t max_seq, int32_t n_heads,
+                                            int32_t n_kv_heads, int32_t head_dim, int64_t layer,
+                                            const int32_t* positions, int32_t pos0,
+                                            int64_t n_tokens, int64_t max_ctx, float* out,
+                                            int32_t* err, void* stream) {
+    const char* fn = "mlk_attention_decode_f32_noalloc";
+    const int64_t need =
+        mlk_attention_workspace_bytes(n_tokens, n_heads, n_kv_heads, head_dim, max_ctx);
+    if (need > static_cast<int64_t>(mlk::kScratchBytes)) {
+        return Fail(MLK_ERR_INVALID,
+                    "%s: %lld bytes of chunk partials exceed the %zu-byte scratch of this entry "
+                    "(fewer tokens or a smaller max_ctx, or mlk_attention_decode_f32 with a "
+                    "workspace)", fn, static_cast<long long>(need), mlk::kScratchBytes);
+    }
+    void* ws = nullptr;
+    const mlk_status st = mlk::ScratchOnCurrentDevice(fn, &ws);
+    if (st != MLK_OK) return st;
+    return mlk_attention_decode_f32(q, q_row_stride, k_cache, v_cache, n_layers, max_seq, n_heads,
+                                    n_kv_heads, head_dim, layer, positions, pos0, n_tokens,
+                                    max_ctx, out, ws, mlk::kScratchBytes, err, stream);
 }
 
 mlk_status mlk_attention_prefill_f32(const float* q, int64_t q_row_stride, const float* k_cache,

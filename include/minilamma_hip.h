@@ -233,6 +233,30 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
                                     void* stream);
 
 /*
+ * mlk_attention_decode_f32 for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same arguments, semantics
+ * and results as mlk_attention_decode_f32 without the workspace: the chunk
+ * partials go to a fixed device array of the library, one per GPU, of
+ * mlk_attention_noalloc_scratch_bytes() bytes (64 MiB), held from the first
+ * call on that GPU until the process ends.  Calls needing more than that
+ * (mlk_attention_workspace_bytes() of the shape) are rejected with
+ * MLK_ERR_INVALID before any launch; at max_ctx 8192 every batch up to 256
+ * tokens of the 8B and 70B head shapes fits.  Nothing is allocated and no
+ * allocating routine is called.  Every call on one GPU uses the same array:
+ * calls that overlap on one GPU (other streams, other threads) race.
+ */
+mlk_status mlk_attention_decode_f32_noalloc(const float* q, int64_t q_row_stride,
+                                            const float* k_cache, const float* v_cache,
+                                            int64_t n_layers, int64_t max_seq, int32_t n_heads,
+                                            int32_t n_kv_heads, int32_t head_dim, int64_t layer,
+                                            const int32_t* positions, int32_t pos0,
+                                            int64_t n_tokens, int64_t max_ctx, float* out,
+                                            int32_t* err, void* stream);
+/* Bytes of that fixed device array. */
+size_t mlk_attention_noalloc_scratch_bytes(void);
+
+/*
  * Causal attention of a prompt chunk: tokens t < n_tokens at positions
  * pos0 + t (their K/V rows already in the cache, e.g. by mlk_kv_write_f32),
  * token t attending to cache positions 0 .. pos0 + t -- the per-token
