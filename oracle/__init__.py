@@ -17,7 +17,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(HERE, "liboracle.so")
+# MLK_ORACLE_LIB selects another build of the same source (the sanitizer test
+# runs the oracle tests against an AddressSanitizer + UBSan build)
+ORACLE_SO = os.environ.get("MLK_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libref.so")
 REF_AVX2_SO = os.path.join(HERE, "_ref", "libref_avx2.so")
 
@@ -405,10 +407,15 @@ class _Reference:
                                  [C.c_int, _u8p, C.c_int, C.c_int, _f32p])
         self._dequantize_flat = _bind(lib, "ref_dequantize_flat", C.c_int,
                                       [C.c_int, _u8p, C.c_int, C.c_int, _f32p])
+        vp = C.c_void_p
         self._chain = _bind(lib, "ref_chain", C.c_int,
-                            [_f32p, _i64, _i64, _i32p, _f32p, _f32p, _f32p, _f32p, C.c_float,
+                            [vp, _i32p, vp, _f32p, _f32p, _f32p, _f32p, C.c_float,
                              _f32p, _f32p, C.c_int, C.c_int, C.c_int, _i32p, C.c_float,
-                             _f32p, _f32p, _f32p, _i64, _i64, C.c_int])
+                             _f32p, _f32p, _f32p, _i64, _i64, _i64, C.c_int])
+        self._embedding_model = _bind(lib, "ref_embedding_model", vp, [_f32p, _i64, _i64])
+        self._model_free = _bind(lib, "ref_model_free", None, [vp])
+        self._gather_quant = _bind(lib, "ref_gather_quant", C.c_int,
+                                   [C.c_int, _u8p, _i64, _i64, _i32p, _i64, _f32p, C.c_int])
         self._linear_quant = _bind(lib, "ref_linear_quant", C.c_int,
                                    [C.c_int, _f32p, _u8p, _f32p, C.c_int, C.c_int, C.c_int,
                                     C.c_int])
@@ -510,8 +517,50 @@ class _Reference:
         _check(fn(QUANT_TYPES[qtype], _u8(blocks), rows, cols, out))
         return out.reshape(rows, cols)
 
+    def embedding_model(self, table):
+        """A reference Model holding only the F32 token table (one copy);
+        free it with free_model."""
+        table = _f32(table)
+        handle = self._embedding_model(table.reshape(-1), table.shape[0], table.shape[1])
+        if not handle:
+            raise MemoryError("ref_embedding_model failed")
+        return handle
+
+    def free_model(self, handle):
+        self._model_free(handle)
+
     def chain(self, bufs, n_tokens, n_threads):
-        return self._chain(*_chain_args(bufs, n_tokens, n_threads))
+        """The chain over the reference's own Embedding, ForwardAdd, RmsNorm,
+        Rope and SwiGlu (ref_chain).  bufs as for the oracle's chain; a
+        bufs["model"] handle (embedding_model) is used as it is, else one is
+        made from bufs["table"] for the call.  bufs["table"] None means no
+        gather: bufs["x_in"] rows are the residual input."""
+        b = bufs
+        model, own = b.get("model"), False
+        if model is None and b.get("table") is not None:
+            model, own = self.embedding_model(b["table"]), True
+        try:
+            x_in = None if model is not None else _f32(b["x_in"]).ctypes.data
+            ids = b["ids"] if model is not None else np.zeros(1, np.int32)
+            return self._chain(model, ids, x_in,
+                               b["x"].reshape(-1), b["delta"].reshape(-1), b["norm_w"],
+                               b["y"].reshape(-1), b["eps"], b["q"].reshape(-1),
+                               b["k"].reshape(-1), b["n_heads"], b["n_kv_heads"], b["head_dim"],
+                               b["positions"], b["theta"], b["gate"].reshape(-1),
+                               b["up"].reshape(-1), b["ffn_out"].reshape(-1), b["dim"],
+                               b["ffn_dim"], n_tokens, n_threads)
+        finally:
+            if own:
+                self.free_model(model)
+
+    def gather_quant(self, qtype, blocks, vocab, dim, ids, n_threads=1):
+        """Rows ids of a block-quantized table through the reference's own
+        Q*ToTensor (ref_gather_quant); returns [T, dim]."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        out = np.empty((ids.size, dim), np.float32)
+        _check(self._gather_quant(QUANT_TYPES[qtype], _u8(blocks), vocab, dim, ids, ids.size,
+                                  out.reshape(-1), n_threads))
+        return out
 
     def forward_tokens(self, model, tokens, positions):
         """The reference's own ForwardToken loop (ref_forward_tokens) over a

@@ -17,6 +17,7 @@
 #include "include/quant.h"
 #include "include/quantized_tensor.h"
 #include "include/tensor.h"
+#include "src/internal/forward.h"
 #include "thread_pool/thread_pool.h"
 
 #include <cmath>
@@ -218,67 +219,77 @@ int ref_matmul_f32(const float* a, const float* b, float* c, int m, int k, int n
     return Guard([&] { Unwrap(yan_lamma::Matmul(Wrap(a, {m, k}), Wrap(b, {k, n})), c); });
 }
 
-// Decode attention for one query token: the K/V rows 0..pos go through the
-// reference's own KvCache::Write (src/kvcache.cc), then the score / SoftMax /
-// value loops of ForwardAttention (src/forward.cc:265-298, which does not
-// build from a few files) run over KeyPtr / ValPtr with the reference's own
-// SoftMax (src/ops.cc:113-134).
+// Decode attention for one query token: the K/V rows 0..pos-1 go into the
+// reference's own KvCache (src/kvcache.cc) with KvCache::Write, then the
+// reference's own ForwardAttention (src/forward.cc:265-298, exported through
+// src/internal/forward.h) writes row pos and attends over 0..pos.
 int ref_attention(const float* q, const float* k_rows, const float* v_rows, int n_layers,
                   int max_seq, int n_heads, int n_kv_heads, int head_dim, int layer, int pos,
                   float* out) {
     return Guard([&] {
         yan_lamma::KvCache cache(n_layers, max_seq, n_kv_heads, head_dim);
         const int row = n_kv_heads * head_dim;
-        for (int j = 0; j <= pos; ++j) {
+        for (int j = 0; j < pos; ++j) {
             cache.Write(layer, j, Wrap(k_rows + j * row, {n_kv_heads, head_dim}),
                         Wrap(v_rows + j * row, {n_kv_heads, head_dim}));
         }
-        const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
-        for (int i = 0; i < n_heads; ++i) {
-            const int kv_head = i / (n_heads / n_kv_heads);
-            Tensor scores({pos + 1}, 0.0f);
-            for (int j = 0; j <= pos; ++j) {
-                const float* kp = cache.KeyPtr(layer, j, kv_head);
-                float dot = 0.0f;
-                for (int d = 0; d < head_dim; ++d) dot += q[i * head_dim + d] * kp[d];
-                scores.data[j] = dot * scale;
-            }
-            const Tensor p = yan_lamma::SoftMax(scores);
-            for (int d = 0; d < head_dim; ++d) {
-                float val = 0.0f;
-                for (int j = 0; j <= pos; ++j) val += p.data[j] * cache.ValPtr(layer, j, kv_head)[d];
-                out[i * head_dim + d] = val;
-            }
-        }
+        const yan_lamma::Model unused;  // ForwardAttention's CPU path reads nothing from it
+        Unwrap(yan_lamma::ForwardAttention(unused, Wrap(q, {n_heads, head_dim}),
+                                           Wrap(k_rows + pos * row, {n_kv_heads, head_dim}),
+                                           Wrap(v_rows + pos * row, {n_kv_heads, head_dim}),
+                                           layer, pos, cache, n_heads, n_kv_heads, head_dim),
+               out);
     });
 }
 
-// The per-token op chain as the reference's CPU forward runs it: each op
-// takes and returns Tensor objects (one heap allocation per result).  The
-// embedding row copy and the residual add live in src/forward.cc, which does
-// not build from a few files, so they are written here as the plain Tensor
-// loops src/forward.cc:198-205 and :213-222 are.  n_threads > 1 spreads the
-// tokens over the reference's own ParallelFor (thread_pool/thread_pool.cc).
-int ref_chain(const float* table, int64_t vocab, int64_t dim, const int32_t* ids, float* x,
+// A Model holding only an F32 token table [vocab, dim] (copied once), for the
+// reference's own Embedding (src/forward.cc:198-205) in ref_chain.
+void* ref_embedding_model(const float* table, int64_t vocab, int64_t dim) {
+    try {
+        auto* model = new yan_lamma::Model();
+        model->config.vocab_size = static_cast<int>(vocab);
+        model->config.dim = static_cast<int>(dim);
+        model->embedding_data_ = Wrap(table, {static_cast<int>(vocab), static_cast<int>(dim)});
+        model->is_loaded = true;
+        return model;
+    } catch (const std::exception&) {
+        return nullptr;
+    }
+}
+
+void ref_model_free(void* model) { delete static_cast<yan_lamma::Model*>(model); }
+
+// The per-token op chain as the reference's CPU forward runs it, every op the
+// reference's own function on Tensor objects (one heap allocation per
+// result): Embedding and ForwardAdd (src/forward.cc:198-222, exported through
+// src/internal/forward.h), RmsNorm, Rope, SwiGlu (src/ops.cc).  With
+// model == NULL there is no gather: row t of x_in is the residual input (the
+// 70B chain).  n_threads > 1 spreads the tokens over the reference's own
+// ParallelFor (thread_pool/thread_pool.cc).
+int ref_chain(const void* model, const int32_t* ids, const float* x_in, float* x,
               const float* delta, const float* norm_w, float* y, float eps, float* q, float* k,
               int n_heads, int n_kv_heads, int head_dim, const int32_t* positions, float theta,
-              const float* gate, const float* up, float* ffn_out, int64_t ffn_dim,
+              const float* gate, const float* up, float* ffn_out, int64_t dim, int64_t ffn_dim,
               int64_t n_tokens, int n_threads) {
     return Guard([&] {
+        const auto* m = static_cast<const yan_lamma::Model*>(model);
+        const yan_lamma::Model unused;
         const int D = static_cast<int>(dim);
         const int F = static_cast<int>(ffn_dim);
         const Tensor w = Wrap(norm_w, {D});
         auto rows = [&](int begin, int end) {
             for (int t = begin; t < end; ++t) {
-                if (ids[t] < 0 || ids[t] >= vocab) {
-                    throw std::runtime_error("token id out of range");
+                Tensor e;
+                if (m != nullptr) {
+                    if (ids[t] < 0 || ids[t] >= m->config.vocab_size) {
+                        throw std::runtime_error("token id out of range");
+                    }
+                    e = yan_lamma::Embedding(*m, ids[t]);
+                } else {
+                    e = Wrap(x_in + t * dim, {D});
                 }
-                Tensor e({D});
-                const float* src = table + static_cast<int64_t>(ids[t]) * dim;
-                for (int i = 0; i < D; ++i) e.data[i] = src[i];
-                const Tensor d = Wrap(delta + t * dim, {D});
-                Tensor h({D});
-                for (int i = 0; i < D; ++i) h.data[i] = e.data[i] + d.data[i];
+                const Tensor h = yan_lamma::ForwardAdd(m != nullptr ? *m : unused, e,
+                                                       Wrap(delta + t * dim, {D}));
                 Unwrap(h, x + t * dim);
                 Unwrap(yan_lamma::RmsNorm(h, w, eps), y + t * dim);
                 const int64_t qs = static_cast<int64_t>(n_heads) * head_dim;
@@ -290,6 +301,43 @@ int ref_chain(const float* table, int64_t vocab, int64_t dim, const int32_t* ids
                 Unwrap(tk, k + t * ks);
                 Unwrap(yan_lamma::SwiGlu(Wrap(gate + t * ffn_dim, {F}), Wrap(up + t * ffn_dim, {F})),
                        ffn_out + t * ffn_dim);
+            }
+        };
+        if (n_threads <= 1) {
+            rows(0, static_cast<int>(n_tokens));
+        } else {
+            yan_lamma::SetThreadNum(n_threads);
+            yan_lamma::ParallelFor(static_cast<int>(n_tokens), rows);
+            yan_lamma::SetThreadNum(0);
+        }
+    });
+}
+
+// The quantized token gather on the CPU: each token's row of blocks through
+// the reference's own dequantizer (Q80ToTensor / Q40ToTensor / Q41ToTensor,
+// the std::vector<Block> overloads of src/quant.cc) into out [T, dim].  The
+// reference has no quantized gather (it dequantizes the whole table at load,
+// src/gguf_load.cc:370-404); this is its per-row equivalent, timed as the C4
+// CPU baseline.  n_threads > 1 spreads the tokens over ParallelFor.
+int ref_gather_quant(int type, const uint8_t* blocks, int64_t vocab, int64_t dim,
+                     const int32_t* ids, int64_t n_tokens, float* out, int n_threads) {
+    return Guard([&] {
+        const size_t nb = RowBlocks(static_cast<int>(dim));
+        const size_t row_bytes = nb * (type == 0 ? sizeof(Block_Q80)
+                                                 : (type == 1 ? sizeof(Block_Q40) : sizeof(Block_Q41)));
+        const std::vector<int> shape{1, static_cast<int>(dim)};
+        auto rows = [&](int begin, int end) {
+            for (int t = begin; t < end; ++t) {
+                if (ids[t] < 0 || ids[t] >= vocab) throw std::runtime_error("token id out of range");
+                const uint8_t* raw = blocks + static_cast<size_t>(ids[t]) * row_bytes;
+                float* dst = out + t * dim;
+                if (type == 0) {
+                    Unwrap(yan_lamma::Q80ToTensor(ToBlocks<Block_Q80>(raw, nb), shape), dst);
+                } else if (type == 1) {
+                    Unwrap(yan_lamma::Q40ToTensor(ToBlocks<Block_Q40>(raw, nb), shape), dst);
+                } else {
+                    Unwrap(yan_lamma::Q41ToTensor(ToBlocks<Block_Q41>(raw, nb), shape), dst);
+                }
             }
         };
         if (n_threads <= 1) {

@@ -27,7 +27,7 @@ Fixture contents (numpy .npz, no pickles):
                    rows; F32 Linear and Matmul on the shapes of
                    tests/test_cuda_linear.cc and tests/test_cuda_matmul.cc.
   attention.npz    decode attention for one query token (the reference's
-                   KvCache + the ForwardAttention loops over its SoftMax) on
+                   own KvCache and ForwardAttention) on
                    the cases of test/cuda_attention_test.cc:86-88 (their
                    sin / cos inputs) and on an N(0, 1) GQA case with
                    head_dim 128 (8 query heads over 2 KV heads, pos 63).

@@ -388,6 +388,58 @@ needs_ref = pytest.mark.skipif(not O.reference_available(),
 
 
 @needs_ref
+def test_reference_chain_baselines_match_the_golden_chain(orc):
+    """The reference chain the CPU baseline times (the reference's own
+    Embedding, ForwardAdd, RmsNorm, Rope, SwiGlu): with a model handle, with
+    the table passed per call, and without a gather (the 70B chain: the
+    gathered rows given as the residual input), on 1 and 2 threads."""
+    ref = O.reference()
+    g = golden("tiny_chain")
+    T = len(g["ids"])
+    H, KV, hd, F, D = (int(g[k]) for k in ("n_heads", "n_kv_heads", "head_dim", "ffn_dim", "dim"))
+    model = ref.embedding_model(g["table"])
+    try:
+        for threads in (1, 2):
+            for mode in ("handle", "table", "no_gather"):
+                ids = np.tile(g["ids"], 8)
+                n = len(ids)
+                b = dict(table=g["table"], vocab=int(g["vocab"]), dim=D, ids=ids,
+                         x=np.empty((n, D), np.float32), delta=np.tile(g["delta"], (8, 1)),
+                         norm_w=g["norm_w"], y=np.empty((n, D), np.float32), eps=float(g["eps"]),
+                         q=np.tile(g["q"], (8, 1)), k=np.tile(g["k"], (8, 1)), n_heads=H,
+                         n_kv_heads=KV, head_dim=hd, positions=np.tile(g["positions"], 8),
+                         theta=float(g["theta"]), gate=np.tile(g["gate"], (8, 1)),
+                         up=np.tile(g["up"], (8, 1)), ffn_out=np.empty((n, F), np.float32),
+                         ffn_dim=F)
+                if mode == "handle":
+                    b["model"] = model
+                elif mode == "no_gather":
+                    b["table"] = None
+                    b["x_in"] = np.tile(g["gathered"], (8, 1))
+                assert ref.chain(b, n, threads) == 0, mode
+                assert_bits_equal(b["x"][-T:], g["residual_out"], mode + " residual")
+                assert_bits_equal(b["y"][:T], g["norm_out"], mode + " y")
+                assert_bits_equal(b["q"][-T:], g["q_out"], mode + " q")
+                assert_bits_equal(b["k"][:T], g["k_out"], mode + " k")
+                assert_bits_equal(b["ffn_out"][-T:], g["ffn_out"], mode + " ffn")
+    finally:
+        ref.free_model(model)
+
+
+@needs_ref
+def test_reference_quantized_gather_baseline_matches_the_oracle(orc):
+    ref = O.reference()
+    rng = np.random.default_rng(5)
+    table = (rng.standard_normal((50, 96)) * 0.02).astype(np.float32)
+    ids = rng.integers(0, 50, 40).astype(np.int32)
+    for qt in QT:
+        blocks = orc.quantize(qt, table)
+        want = orc.gather_quant(qt, blocks, 50, 96, ids)
+        for threads in (1, 2):
+            assert_bits_equal(ref.gather_quant(qt, blocks, 50, 96, ids, threads), want, qt)
+
+
+@needs_ref
 def test_oracle_equals_compiled_reference_on_random_inputs(orc):
     ref = O.reference()
     rng = np.random.default_rng(11)
