@@ -8,17 +8,20 @@ Llama-3-8B-shape prefill chain at T = 4096 tokens, fp32:
 One step is one pass of the four kernels over one of three rotating buffer
 sets (~1 GB each, so no step finds its inputs in the 256 MB MALL).  Inputs
 are synthetic, generated on the device, resident in HBM before timing.
-`value` is whole-chain algorithmic GB/s over K timed steps (events only at
-the two ends).  Per-kernel durations come from a second timed pass that
-launches each kernel K times back to back between two HIP events recorded
-on the stream the kernels run on.
+`value` is whole-chain GB/s over K timed steps (events only at the two
+ends); the gather counts each distinct table row once (Zipf ids repeat hot
+rows, which come from cache).  Per-kernel durations come from a second
+timed pass that launches each kernel K times back to back between two HIP
+events recorded on the stream the kernels run on.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra FILE]
+The same run measures the other configs of BASELINE.json into "configs":
+configs[0] (the tiny chain), configs[1] (decode steps at T = 1..64, eager
+and graph-replayed), configs[3] (Q8_0/Q4_0/Q4_1 gathers) and configs[4]
+(the 70B chain), each beside the reference's CPU code timed on this host.
+Before each measured section a ZeroKernel launch of 4096 * (100 + i) bytes
+marks section i in a rocprofv3 trace (bench.py --rocprof-report uses it).
 
---extra FILE also measures configs 1, 3 and 4 (decode latency at T = 1..64,
-the quantized gathers, the 70B chain) and writes them to FILE as JSON; it is
-off by default so a rocprofv3 summary of the default command holds only the
-chain's launches.
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 from __future__ import annotations
 
@@ -49,7 +52,6 @@ def parse_args():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
     p.add_argument("--warmup", type=int, default=10)
-    p.add_argument("--extra", default=None, help="also measure configs 1, 3, 4 into this JSON file")
     p.add_argument("--linear", default=None,
                    help="only measure the seven linear projections of one Llama-3-8B layer "
                         "(F32, Q8_0, Q4_0, Q4_1 weights; T = 1, 4, 16 token rows) into this "
@@ -93,9 +95,11 @@ OP_MAX_SETS = 16  # decode-size buffers stay cache-resident, as in a real decode
 
 
 class ChainSet:
-    """Device buffers of one op-chain input/output set (or of `fields` only)."""
+    """Device buffers of one op-chain input/output set (or of `fields` only).
+    x is the gather's output in a chain step; it is filled when the set has
+    no gather (`fill_x`) or holds only some fields."""
 
-    def __init__(self, mlk, cfg, T, seed, fields=None):
+    def __init__(self, mlk, cfg, T, seed, fields=None, fill_x=False):
         D, H, KV, hd, F = cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"]
         shapes = {"x": (T, D), "delta": (T, D), "y": (T, D), "q": (T, H * hd),
                   "k": (T, KV * hd), "gate": (T, F), "up": (T, F), "out": (T, F)}
@@ -105,31 +109,36 @@ class ChainSet:
             buf = mlk.DeviceBuffer.empty(shapes[name])
             setattr(self, name, buf)
             self.nbytes += buf.nbytes
-            # x is the gather's output in a chain step; alone it is filled
-            if name in filled and (fields is not None or name != "x"):
+            if name in filled and (fields is not None or fill_x or name != "x"):
                 mlk.fill_normal(buf, buf.nbytes // 4, 0.0, 0.02, seed + filled[name])
 
 
 class Chain:
-    """gather -> add+RMSNorm -> RoPE -> SwiGLU on rotating sets."""
+    """gather -> add+RMSNorm -> RoPE -> SwiGLU on rotating sets (without the
+    gather when `gather` is False: the 70B config has none)."""
 
-    OPS = ("gather_f32", "add_rmsnorm", "rope", "swiglu")
-
-    def __init__(self, mlk, cfg, T, seed, n_sets=N_SETS, ids=None, positions=None, table=None):
+    def __init__(self, mlk, cfg, T, seed, n_sets=N_SETS, ids=None, positions=None, table=None,
+                 gather=True):
         self.mlk, self.cfg, self.T = mlk, cfg, T
+        self.OPS = (("gather_f32",) if gather else ()) + ("add_rmsnorm", "rope", "swiglu")
         D = cfg["dim"]
-        if table is not None:
+        self.table = None
+        if gather and table is not None:
             self.table = table
-        else:
+        elif gather:
             self.table = mlk.DeviceBuffer.empty((cfg["vocab"], D))
             mlk.fill_normal(self.table, cfg["vocab"] * D, 0.0, 0.02, seed)
         self.norm_w = mlk.DeviceBuffer.empty((D,))
         mlk.fill_normal(self.norm_w, D, 1.0, 0.1, seed + 100)
-        self.ids_host = ids if ids is not None else workloads.zipf_ids(T, cfg["vocab"], 1.1, seed)
-        self.ids = mlk.DeviceBuffer.from_array(self.ids_host)
+        self.ids_host = None
+        if gather:
+            self.ids_host = ids if ids is not None else workloads.zipf_ids(T, cfg["vocab"], 1.1,
+                                                                           seed)
+            self.ids = mlk.DeviceBuffer.from_array(self.ids_host)
         self.positions_host = positions
         self.positions = mlk.DeviceBuffer.from_array(positions) if positions is not None else None
-        self.sets = [ChainSet(mlk, cfg, T, seed + 10 * (i + 1)) for i in range(n_sets)]
+        self.sets = [ChainSet(mlk, cfg, T, seed + 10 * (i + 1), fill_x=not gather)
+                     for i in range(n_sets)]
         self.stream = mlk.Stream()
         mlk.synchronize()
 
@@ -246,52 +255,45 @@ def add_unique(entry, unique_bytes, peak):
                  unique_row_frac_of_peak=round(gbs / peak, 4))
 
 
-# ------------------------------------------------------------ CPU baseline
+# ------------------------------------------------------------ CPU baselines
 
-def cpu_baseline(mlk, chain, cfg, T, workloads):
-    """The reference's own CPU ops (oracle/_ref, AVX2/FMA build) over the same
-    chain, one token at a time as ForwardBatch runs them; ThreadPool variant
-    (ParallelFor over tokens) and single thread.  Falls back to the C port
-    (oracle/liboracle.so) when the reference build is absent."""
+def _cpu_impl():
+    """The reference's own CPU code (AVX2/FMA build of its sources), or the C
+    port (oracle/liboracle.so) where that build is absent."""
     import oracle as O
 
-    D, H, KV, hd, F = cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"]
-    s = chain.sets[0]
-    bufs = dict(table=chain.table.download(), vocab=cfg["vocab"], dim=D, ids=chain.ids_host,
-                x=np.empty((T, D), np.float32), delta=s.delta.download(),
-                norm_w=chain.norm_w.download(), y=np.empty((T, D), np.float32), eps=cfg["eps"],
-                q=s.q.download(), k=s.k.download(), n_heads=H, n_kv_heads=KV, head_dim=hd,
-                positions=np.arange(T, dtype=np.int32), theta=cfg["theta"],
-                gate=s.gate.download(), up=s.up.download(), ffn_out=np.empty((T, F), np.float32),
-                ffn_dim=F)
     if O.reference_available(avx2=True):
-        impl, kind, build = O.reference(avx2=True), "reference", "oracle/_ref/libref_avx2.so"
-    else:
-        impl, kind, build = O.oracle(), "port", "oracle/liboracle.so"
-    # the box's CPU share for one GPU is 16 cores, whatever nproc reports
-    threads = max(1, min(16, os.cpu_count() or 1))
-    nbytes = workloads.bytes_chain(cfg, T)
+        return O.reference(avx2=True), "reference", "oracle/_ref/libref_avx2.so"
+    return O.oracle(), "port", "oracle/liboracle.so"
 
-    def timed(n_threads, reps):
-        times = []
-        for _ in range(reps + 1):  # first rep is warmup
-            t0 = time.perf_counter()
-            rc = impl.chain(bufs, T, n_threads)
-            times.append(time.perf_counter() - t0)
-            if rc != 0:
-                raise RuntimeError(f"CPU baseline failed (status {rc})")
-        return statistics.median(times[1:])
 
-    t_mt = timed(threads, 5)
-    t_st = timed(1, 3)
-    return {"value": round(nbytes / t_mt / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": kind,
-            "sample": (f"full configs[2] chain (T={T}, Llama-3-8B shapes), median of 5 reps after 1 warmup; "
-                       f"{build}, ParallelFor over tokens"),
-            "ms_per_chain": round(t_mt * 1e3, 2),
-            "single_thread_value": round(nbytes / t_st / 1e9, 3),
-            "single_thread_ms_per_chain": round(t_st * 1e3, 2),
-            "cpu_model": _cpu_model()}
+def _cpu_threads():
+    """Threads for the multi-threaded baselines: the CPUs this process may
+    run on, capped at 16, the GPU box's CPU share for one GPU (nproc there
+    reports the whole host)."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = os.cpu_count() or 1
+    return max(1, min(16, avail))
+
+
+def _host_facts():
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    return {"nproc": os.cpu_count(), "affinity_cpus": affinity, "cpu_model": _cpu_model()}
+
+
+def _median_s(fn, reps):
+    """Median wall time of `reps` calls of fn after one warmup call."""
+    times = []
+    for _ in range(reps + 1):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times[1:])
 
 
 def _cpu_model():
@@ -305,6 +307,61 @@ def _cpu_model():
     return "unknown"
 
 
+def chain_host_bufs(chain, cfg, rows):
+    """Host copies of the first `rows` token rows of a chain's set 0 (the
+    CPU baseline's inputs) and its output arrays."""
+    D, H, KV, hd, F = cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"]
+    s = chain.sets[0]
+    pos = (chain.positions_host[:rows] if chain.positions_host is not None
+           else np.arange(rows, dtype=np.int32))
+    bufs = dict(table=None, vocab=cfg.get("vocab", 1), dim=D, ids=None,
+                x=np.empty((rows, D), np.float32), delta=s.delta.download((rows, D)),
+                norm_w=chain.norm_w.download(), y=np.empty((rows, D), np.float32),
+                eps=cfg["eps"], q=s.q.download((rows, H * hd)), k=s.k.download((rows, KV * hd)),
+                n_heads=H, n_kv_heads=KV, head_dim=hd, positions=np.ascontiguousarray(pos, np.int32),
+                theta=cfg["theta"], gate=s.gate.download((rows, F)), up=s.up.download((rows, F)),
+                ffn_out=np.empty((rows, F), np.float32), ffn_dim=F)
+    if chain.table is not None:
+        bufs["table"] = chain.table.download()
+        bufs["ids"] = np.ascontiguousarray(chain.ids_host[:rows], np.int32)
+    else:
+        bufs["x_in"] = s.x.download((rows, D))
+    return bufs
+
+
+def cpu_chain_baseline(bufs, rows, nbytes, sample, reps=5):
+    """The chain on the CPU, one token at a time as ForwardBatch runs it:
+    spread over tokens with the reference's ParallelFor, and on one thread.
+    `nbytes`: the bytes the GPU figure of the same workload counts."""
+    impl, kind, build = _cpu_impl()
+    threads = _cpu_threads()
+    model = None
+    if kind == "reference" and bufs.get("table") is not None:
+        model = bufs["model"] = impl.embedding_model(bufs["table"])
+    elif kind == "port" and bufs.get("table") is None:
+        # the C port always gathers: the residual rows become a table read in order
+        bufs.update(table=bufs["x_in"], ids=np.arange(rows, dtype=np.int32), vocab=rows)
+
+    def run(n_threads):
+        rc = impl.chain(bufs, rows, n_threads)
+        if rc != 0:
+            raise RuntimeError(f"CPU baseline failed (status {rc})")
+
+    try:
+        t_mt = _median_s(lambda: run(threads), reps)
+        t_st = _median_s(lambda: run(1), max(1, reps - 2))
+    finally:
+        if model is not None:
+            impl.free_model(model)
+            bufs.pop("model", None)
+    return {"value": round(nbytes / t_mt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": kind, "sample": f"{sample}; {build}, ParallelFor over tokens; median of "
+                                    f"{reps} reps after 1 warmup",
+            "ms_per_chain": round(t_mt * 1e3, 3),
+            "single_thread_value": round(nbytes / t_st / 1e9, 3),
+            "single_thread_ms_per_chain": round(t_st * 1e3, 3), **_host_facts()}
+
+
 def traffic_from_profiles():
     """HBM bytes per SwiGLU launch from the committed rocprofv3 --pmc runs."""
     try:
@@ -314,21 +371,125 @@ def traffic_from_profiles():
         return None
 
 
-# ------------------------------------------------------------ extra configs
+def counter_traffic():
+    """{section: {op: HBM bytes per launch}} from the committed rocprofv3
+    --pmc runs of this command (bench.py --rocprof-report), or {}."""
+    try:
+        with open(PMC_FILE) as f:
+            return json.load(f).get("per_section_hbm_bytes", {})
+    except (OSError, ValueError):
+        return {}
 
-def extra_configs(mlk, workloads, steps, peak):
-    res = {}
-    c8 = workloads.CONFIGS["c2_decode_8b"]
-    dec = {}
-    for T in c8["tokens"]:
-        pos = workloads.decode_positions(T, c8["max_pos"], c8["seed"])
-        ch = Chain(mlk, c8, T, seed=c8["seed"], n_sets=2, positions=pos)
+
+def add_counter(entry, hbm_bytes, peak):
+    """Beside the algorithmic figure: the HBM bytes the counters measured for
+    this launch, and the rate they give."""
+    if not hbm_bytes:
+        return
+    gbs = hbm_bytes / (entry["us"] * 1e-6) / 1e9
+    entry.update(counter_bytes=int(hbm_bytes), counter_GBps=round(gbs, 1),
+                 counter_frac_of_peak=round(gbs / peak, 4))
+
+
+def gather_fractions(entry):
+    """A Zipf gather's frac_of_peak counts each distinct table row once (hot
+    rows come from cache); the algorithmic fraction is kept beside it."""
+    entry["algorithmic_frac_of_peak"] = entry["frac_of_peak"]
+    entry["frac_of_peak"] = entry["unique_row_frac_of_peak"]
+    entry["frac_basis"] = "unique table rows"
+
+
+# ------------------------------------------------------------ sections
+# Before each measured section a ZeroKernel launch of 4096 * (PHASE_BASE + i)
+# bytes (a grid of PHASE_BASE + i workgroups of 256) marks section i in a
+# rocprofv3 trace, so the summary can tell which config each launch belongs
+# to (the chain kernels run at several shapes in one command).
+
+PHASE_BASE = 100
+PHASES = ("c3_chain", "c3_ops", "c2_decode", "c1_tiny", "c4_gather", "c5_chain", "c5_ops")
+
+
+class Marks:
+    def __init__(self, mlk):
+        self.mlk = mlk
+        self.buf = mlk.DeviceBuffer(4096 * (PHASE_BASE + len(PHASES) + 1), np.uint8)
+
+    def __call__(self, phase, stream=None):
+        n = 4096 * (PHASE_BASE + PHASES.index(phase) + 1)
+        self.mlk.check(self.mlk.lib.mlk_zero_async(self.buf.ptr, n,
+                                                   None if stream is None else stream.handle),
+                       "mark")
+
+
+def phase_of_grid(grid):
+    """The section a ZeroKernel launch of `grid` work-items marks, or None."""
+    i = grid // 256 - PHASE_BASE - 1
+    return PHASES[i] if grid % 256 == 0 and 0 <= i < len(PHASES) else None
+
+
+# ------------------------------------------------------------ other configs
+
+def c1_tiny(mlk, steps, warmup, marks):
+    """the tiny chain (6 tokens at positions 0..5) on the GPU,
+    eager and graph-replayed, and on the CPU."""
+    c1 = workloads.CONFIGS["c1_tiny"]
+    ids = np.array(c1["ids"], np.int32)
+    T = ids.size
+    ch = Chain(mlk, c1, T, seed=c1["seed"], n_sets=1, ids=ids)
+    n = max(steps, 200)
+    marks("c1_tiny", ch.stream)
+    eager = ch.run(n, warmup) / n
+    graph = ch.run_graph(n)
+    out = {"tokens": T, "us_per_chain_eager": round(eager * 1e3, 2),
+           "us_per_chain_graph": round(graph * 1e3, 2),
+           "chain_bytes": workloads.bytes_chain(c1, T)}
+    bufs = chain_host_bufs(ch, c1, T)
+    impl, kind, build = _cpu_impl()
+    model = impl.embedding_model(bufs["table"]) if kind == "reference" else None
+    if model is not None:
+        bufs["model"] = model
+    reps = 2000
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        impl.chain(bufs, T, 1)
+    t = (time.perf_counter() - t0) / reps
+    if model is not None:
+        impl.free_model(model)
+    out["cpu_baseline"] = {"us_per_chain": round(t * 1e6, 2), "unit": "us", "cores": 1,
+                           "kind": kind,
+                           "sample": f"the whole chain (6 tokens), mean of {reps} calls, the "
+                                     f"Python call overhead included; {build}",
+                           **_host_facts()}
+    return out
+
+
+def c2_decode(mlk, steps, warmup, marks, table):
+    """the 8B chain as a decode step at T = 1..64 tokens at
+    positions uniform in [0, 8191]: latency-bound, µs per chain, eager
+    launches and one HIP graph replay per step."""
+    c2 = workloads.CONFIGS["c2_decode_8b"]
+    out = {}
+    first = True
+    for t in c2["tokens"]:
+        pos = workloads.decode_positions(t, c2["max_pos"], c2["seed"])
+        dch = Chain(mlk, c2, t, seed=c2["seed"], n_sets=2, positions=pos, table=table)
+        if first:
+            marks("c2_decode", dch.stream)
+            first = False
         n = max(steps, 100)
-        total = ch.run(n, 10)
-        dec[str(T)] = {"us_per_chain": round(total * 1e3 / n, 2),
-                       "ops": summarize(ch.run_ops(n), op_bytes(workloads, c8, T), peak)}
-        del ch
-    res["c2_decode_8b"] = dec
+        eager = dch.run(n, warmup) / n
+        graph = dch.run_graph(n)
+        out[str(t)] = {"us_per_chain_eager": round(eager * 1e3, 2),
+                       "us_per_chain_graph": round(graph * 1e3, 2),
+                       "chain_bytes": workloads.bytes_chain(c2, t)}
+        del dch
+    return out
+
+
+def c4_gathers(mlk, steps, peak, marks, with_cpu):
+    """Q8_0 / Q4_0 / Q4_1 token gathers, T = 4096 Zipf(1.1) ids
+    from a [128256, 4096] table quantized on the device, cold output rotation;
+    beside them the reference's dequantizer over the same rows on the CPU."""
     c4 = workloads.CONFIGS["c4_quant_gather"]
     T, V, D = c4["tokens"], c4["vocab"], c4["dim"]
     table = mlk.DeviceBuffer.empty((V, D))
@@ -337,33 +498,84 @@ def extra_configs(mlk, workloads, steps, peak):
     ids = mlk.DeviceBuffer.from_array(ids_host)
     outs = [mlk.DeviceBuffer.empty((T, D)) for _ in range(N_SETS)]
     st = mlk.Stream()
-    q = {}
+    counters = counter_traffic().get("c4_gather", {})
+    res, cpu = {}, {}
+    marks("c4_gather", st)
     for qt in ("q8_0", "q4_0", "q4_1"):
         blocks = mlk.DeviceBuffer(mlk.quant_bytes(qt, V, D), np.uint8)
         mlk.quantize(qt, table, V, D, blocks, stream=st)
         for i in range(10):
             mlk.gather_quant(qt, blocks, V, D, ids, T, outs[i % N_SETS], stream=st)
-        e0, e1 = mlk.Event(), mlk.Event()
         st.synchronize()
+        e0, e1 = mlk.Event(), mlk.Event()
         e0.record(st)
         for i in range(steps):
             mlk.gather_quant(qt, blocks, V, D, ids, T, outs[i % N_SETS], stream=st)
         e1.record(st)
         e1.synchronize()
         ms = e0.elapsed_ms(e1) / steps
-        q[qt] = summarize({qt: ms}, {qt: workloads.bytes_gather_quant(qt, T, D)}, peak)[qt]
-        add_unique(q[qt], workloads.bytes_gather_unique(ids_host, D, qt), peak)
+        e = summarize({qt: ms}, {qt: workloads.bytes_gather_quant(qt, T, D)}, peak)[qt]
+        add_unique(e, workloads.bytes_gather_unique(ids_host, D, qt), peak)
+        gather_fractions(e)
+        add_counter(e, counters.get(qt), peak)
+        res[qt] = e
+        if with_cpu:
+            impl, kind, build = _cpu_impl()
+            hb = blocks.download(dtype=np.uint8)
+            threads = _cpu_threads() if kind == "reference" else 1
+
+            def run(n):
+                if kind == "reference":
+                    impl.gather_quant(qt, hb, V, D, ids_host, n)
+                else:
+                    impl.gather_quant(qt, hb, V, D, ids_host)
+
+            t_mt = _median_s(lambda: run(threads), 5)
+            t_st = _median_s(lambda: run(1), 3)
+            nb = workloads.bytes_gather_unique(ids_host, D, qt)
+            cpu[qt] = {"value": round(nb / t_mt / 1e9, 3), "unit": "GB/s (unique rows)",
+                       "cores": threads, "kind": kind,
+                       "sample": f"the whole gather ({T} rows), each row's blocks through the "
+                                 f"reference's Q*ToTensor; {build}, ParallelFor over tokens; "
+                                 "median of 5 reps after 1 warmup",
+                       "ms": round(t_mt * 1e3, 3), "single_thread_ms": round(t_st * 1e3, 3),
+                       "single_thread_value": round(nb / t_st / 1e9, 3), **_host_facts()}
+            del hb
         del blocks
-    res["c4_quant_gather"] = q
-    del table
-    c5 = dict(workloads.CONFIGS["c5_70b"], vocab=1)
-    T = c5["tokens"]
-    ch = Chain(mlk, c5, T, seed=c5["seed"], n_sets=2, ids=np.zeros(T, np.int32))
-    total = ch.run(steps, 5)
-    ops = summarize(ch.run_ops(steps), op_bytes(workloads, c5, T), peak)
-    ops.pop("gather_f32")  # the 70B config has no gather
-    res["c5_70b"] = {"ops": ops}
+    if with_cpu:
+        res["cpu_baseline"] = cpu
     return res
+
+
+def c5_chain(mlk, steps, warmup, peak, marks, with_cpu):
+    """the Llama-3-70B-shape chain add+RMSNorm -> RoPE -> SwiGLU
+    at T = 8192 (no gather), cold rotating sets; beside it the reference's CPU
+    chain over a 1024-token sample of the same rows."""
+    c5 = workloads.CONFIGS["c5_70b"]
+    T = c5["tokens"]
+    ch = Chain(mlk, c5, T, seed=c5["seed"], n_sets=2, gather=False)
+    marks("c5_chain", ch.stream)
+    total = ch.run(steps, warmup)
+    nbytes = {"add_rmsnorm": workloads.bytes_add_rmsnorm(T, c5["dim"]),
+              "rope": workloads.bytes_rope(T, c5["n_heads"], c5["n_kv_heads"], c5["head_dim"]),
+              "swiglu": workloads.bytes_swiglu(T, c5["ffn"])}
+    marks("c5_ops", ch.stream)
+    ops = summarize(ch.run_ops(steps), nbytes, peak)
+    for op, hbm in counter_traffic().get("c5_ops", {}).items():
+        if op in ops:
+            add_counter(ops[op], hbm, peak)
+    chain_bytes = workloads.bytes_chain(c5, T, with_gather=False)
+    gbs = chain_bytes * steps / (total * 1e-3) / 1e9
+    out = {"tokens": T, "us_per_chain": round(total * 1e3 / steps, 2), "chain_bytes": chain_bytes,
+           "GBps": round(gbs, 1), "frac_of_peak": round(gbs / peak, 4), "ops": ops}
+    if with_cpu:
+        rows = 1024
+        bufs = chain_host_bufs(ch, c5, rows)
+        out["cpu_baseline"] = cpu_chain_baseline(
+            bufs, rows, workloads.bytes_chain(c5, rows, with_gather=False),
+            f"{rows} of the {T} token rows (the per-token work is the same for every row)")
+    del ch
+    return out
 
 
 # ------------------------------------------------------------ linear layers
@@ -869,17 +1081,18 @@ def calibrate(mlk, steps):
 
 CHAIN_KERNELS = {"GatherF32Vec": "gather_f32", "AddRmsNormVec": "add_rmsnorm",
                  "RopePipe": "rope", "StreamKernel": "swiglu"}
+GATHER_QUANT_ORDER = ("q8_0", "q4_0", "q4_1")  # the order c4_gathers runs them in
 
 PROFILE_COMMANDS = [
-    "rocprofv3 --kernel-trace --stats -T --output-format csv -d gpurun_out/prof_kt -o bench "
+    "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof_kt -o bench "
     "-- python3 bench.py",
-    "rocprofv3 --pmc FETCH_SIZE -T --output-format csv -d gpurun_out/prof_fetch -o bench "
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_fetch -o bench "
     "-- python3 bench.py --no-cpu-baseline --steps 5 --warmup 1",
-    "rocprofv3 --pmc WRITE_SIZE -T --output-format csv -d gpurun_out/prof_write -o bench "
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_write -o bench "
     "-- python3 bench.py --no-cpu-baseline --steps 5 --warmup 1",
-    "rocprofv3 --pmc FETCH_SIZE -T --output-format csv -d gpurun_out/prof_cfetch -o calib "
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof_cfetch -o calib "
     "-- python3 bench.py --calibrate --steps 5",
-    "rocprofv3 --pmc WRITE_SIZE -T --output-format csv -d gpurun_out/prof_cwrite -o calib "
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof_cwrite -o calib "
     "-- python3 bench.py --calibrate --steps 5",
     "python3 bench.py --rocprof-report gpurun_out/prof_kt gpurun_out/prof_fetch "
     "gpurun_out/prof_write gpurun_out/prof_cfetch gpurun_out/prof_cwrite",
@@ -908,81 +1121,192 @@ def _counter_means(d, counter):
     return {k: v[0] / v[1] for k, v in sums.items()}
 
 
+def _short(name):
+    """"void mlk::(anonymous namespace)::K<...>(args)" -> "K<...>"."""
+    import re
+    name = name.replace("(anonymous namespace)::", "").replace("mlk::", "")
+    m = re.search(r"(\w+(?:<[^()]*>)?)\(", name)
+    return m.group(1) if m else name
+
+
+def _base(name):
+    return _short(name).split("<")[0]
+
+
+def _sections(rows):
+    """rows: (dispatch_id, kernel name, grid, value) in any order.  Walks them
+    in dispatch order, assigning each launch to the section the last marker
+    (a ZeroKernel of a marking grid) opened; returns
+    {section: [(short name, grid, value)]}.  Input generation, quantization
+    and copy kernels are left out, except that QuantizeKernel launches are
+    kept as separators."""
+    out = {}
+    phase = None
+    for _, name, grid, value in sorted(rows, key=lambda r: r[0]):
+        base = _base(name)
+        if base == "ZeroKernel":
+            phase = phase_of_grid(grid) or phase
+            continue
+        if phase is None or base in ("FillNormalKernel",) or base.startswith("__amd"):
+            continue
+        out.setdefault(phase, []).append((_short(name), base, grid, value))
+    return out
+
+
+def _op_of(section_rows):
+    """Labels each launch of a section with its op: the chain kernels by name,
+    the quantized gathers by their place after each QuantizeKernel."""
+    labelled = []
+    q = -1
+    for short, base, grid, value in section_rows:
+        if base == "QuantizeKernel":
+            q += 1
+            continue
+        if base == "GatherQuantKernel":
+            op = GATHER_QUANT_ORDER[q] if 0 <= q < len(GATHER_QUANT_ORDER) else base
+        else:
+            op = CHAIN_KERNELS.get(base, short)
+        labelled.append((op, short, grid, value))
+    return labelled
+
+
 def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
     import csv
-    cfg = workloads.CONFIGS["c3_prefill_8b"]
-    T = cfg["tokens"]
-    nbytes = op_bytes(workloads, cfg, T)
-    stats = {r["Name"]: r for r in csv.DictReader(open(_one_csv(kt_dir, "kernel_stats.csv")))}
-    # per (kernel, grid) durations from the trace: the default run also
-    # launches the chain at decode sizes, so the C3 launches are the
-    # largest grid of each chain kernel
-    launches = {}
-    for r in csv.DictReader(open(_one_csv(kt_dir, "kernel_trace.csv"))):
-        key = (r["Kernel_Name"], int(r["Grid_Size_X"]))
-        launches.setdefault(key, []).append(
-            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    peak = workloads.HBM_PEAK_GBS
+    trace = [(int(r["Dispatch_Id"]), r["Kernel_Name"], int(r["Grid_Size_X"]) *
+              int(r.get("Grid_Size_Y", 1) or 1) * int(r.get("Grid_Size_Z", 1) or 1),
+              (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+             for r in csv.DictReader(open(_one_csv(kt_dir, "kernel_trace.csv")))]
+
+    def counters(d, counter):
+        return [(int(r["Dispatch_Id"]), r["Kernel_Name"], int(r["Grid_Size"]),
+                 float(r["Counter_Value"]))
+                for r in csv.DictReader(open(_one_csv(d, "counter_collection.csv")))
+                if r["Counter_Name"] == counter]
+
     # calibration: SiLU over 256 MiB reads and writes 256 MiB per launch
     calib_kib = 4 * CALIB_FLOATS / 1024
-    cf = [v for (k, _), v in _counter_means(cfetch_dir, "FETCH_SIZE").items() if k == "StreamKernel"]
-    cw = [v for (k, _), v in _counter_means(cwrite_dir, "WRITE_SIZE").items() if k == "StreamKernel"]
-    f_factor, w_factor = cf[0] / calib_kib, cw[0] / calib_kib
-    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
-    write = _counter_means(write_dir, "WRITE_SIZE")
-    rows = []
+    cf = [v for _, n, _, v in counters(cfetch_dir, "FETCH_SIZE") if _base(n) == "StreamKernel"]
+    cw = [v for _, n, _, v in counters(cwrite_dir, "WRITE_SIZE") if _base(n) == "StreamKernel"]
+    f_factor, w_factor = (sum(cf) / len(cf)) / calib_kib, (sum(cw) / len(cw)) / calib_kib
+    durations = {k: _op_of(v) for k, v in _sections(trace).items()}
+    fetch = {k: _op_of(v) for k, v in _sections(counters(fetch_dir, "FETCH_SIZE")).items()}
+    write = {k: _op_of(v) for k, v in _sections(counters(write_dir, "WRITE_SIZE")).items()}
+
+    def mean(xs):
+        return sum(xs) / len(xs) if xs else None
+
+    def table(section, nbytes):
+        """(op, kernel, calls, avg us, min us, algorithmic GB/s, FETCH KiB,
+        WRITE KiB, HBM bytes, algorithmic bytes) per op of a section (its
+        largest grid per op: the per-op timing pass)."""
+        rows = []
+        for op in dict.fromkeys(o for o, *_ in durations.get(section, [])):
+            grids = [g for o, _, g, _ in durations[section] if o == op]
+            g = max(grids)
+            d = [v for o, _, gg, v in durations[section] if o == op and gg == g]
+            kname = [k for o, k, gg, _ in durations[section] if o == op and gg == g][0]
+            fk = mean([v for o, _, gg, v in fetch.get(section, []) if o == op and gg == g])
+            wk = mean([v for o, _, gg, v in write.get(section, []) if o == op and gg == g])
+            hbm = (fk / f_factor + wk / w_factor) * 1024 if fk is not None and wk is not None else None
+            avg = mean(d)
+            nb = nbytes.get(op)
+            rows.append((op, kname, len(d), avg, min(d),
+                         nb / (avg * 1e-6) / 1e9 if nb else float("nan"), fk, wk, hbm, nb))
+        return rows
+
+    def fmt(r):
+        op, k, n, avg, mn, gbs, fk, wk, hbm, nb = r
+        f = lambda x, spec: (spec % x) if x is not None else "n/a"  # noqa: E731
+        return "| %s | %s | %d | %.2f | %.2f | %.1f | %s | %s | %s | %s |" % (
+            op, k, n, avg, mn, gbs, f(fk, "%.0f"), f(wk, "%.0f"), f(hbm, "%.0f"), f(nb, "%d"))
+
+    head = ["| op | kernel | calls | avg us | min us | algorithmic GB/s (avg) | FETCH_SIZE KiB | "
+            "WRITE_SIZE KiB | HBM bytes / launch | algorithmic bytes / launch |",
+            "|---|---|---|---|---|---|---|---|---|---|"]
+    preamble = ["Commands (run from the repo root on one MI355X; the last line writes this "
+                "file and the other summaries of the same command):", ""]
+    preamble += ["    " + c for c in PROFILE_COMMANDS]
+    preamble += ["", "Counter calibration (SiLU over 256 MiB: 256 MiB read + 256 MiB written per "
+                 "launch): FETCH_SIZE reads %.4f x the true bytes, WRITE_SIZE %.4f x; HBM bytes "
+                 "below are the counters divided by these factors.  Launches are attributed to "
+                 "configs by the section markers bench.py launches (a ZeroKernel whose grid "
+                 "names the section); the rows are each op's per-launch timing pass (its "
+                 "largest grid in the section)." % (f_factor, w_factor), ""]
+    out_dir = os.path.join(ROOT, "profiles")
+    os.makedirs(out_dir, exist_ok=True)
     traffic = {}
-    small = []
-    for kname, op in CHAIN_KERNELS.items():
-        grids = sorted(g for (k, g) in launches if k == kname)
-        fk = [v for (k, g), v in fetch.items() if k == kname and g == max(g2 for (k2, g2) in fetch
-                                                                           if k2 == kname)]
-        wk = [v for (k, g), v in write.items() if k == kname and g == max(g2 for (k2, g2) in write
-                                                                           if k2 == kname)]
-        if not grids or not fk or not wk:
-            continue
-        durs = launches[(kname, grids[-1])]
-        for g in grids[:-1]:
-            d = launches[(kname, g)]
-            small.append((op, kname, g, len(d), sum(d) / len(d)))
-        hbm = (fk[0] / f_factor + wk[0] / w_factor) * 1024
-        traffic[op] = hbm
-        avg_us = sum(durs) / len(durs)
-        rows.append((op, kname, len(durs), avg_us, min(durs),
-                     nbytes[op] / (avg_us * 1e-6) / 1e9, fk[0], wk[0], hbm, nbytes[op]))
-    out = os.path.join(ROOT, "profiles")
-    os.makedirs(out, exist_ok=True)
-    md = ["# Op chain, config 2 (Llama-3-8B shape, T = 4096): rocprofv3 summary", "",
-          "Commands (run from the repo root on one MI355X; the last line writes this file):", ""]
-    md += ["    " + c for c in PROFILE_COMMANDS]
-    md += ["", "Counter calibration (SiLU over 256 MiB: 256 MiB read + 256 MiB written per "
-           "launch): FETCH_SIZE reads %.4f x the true bytes, WRITE_SIZE %.4f x; HBM bytes "
-           "below are the counters divided by these factors." % (f_factor, w_factor), "",
-           "| op | kernel | calls | avg us | min us | algorithmic GB/s (avg) | FETCH_SIZE KiB | "
-           "WRITE_SIZE KiB | HBM bytes / launch | algorithmic bytes / launch |",
-           "|---|---|---|---|---|---|---|---|---|---|"]
-    for r in rows:
-        md.append("| %s | %s | %d | %.2f | %.2f | %.1f | %.0f | %.0f | %.0f | %d |" % r)
-    md += ["", "The same kernels at the decode sizes of configs[1] (T = 1 and 64; smaller grids, "
-           "eager and graph-replayed launches together):", "",
-           "| op | kernel | grid (threads) | launches | avg us |", "|---|---|---|---|---|"]
-    for r in small:
-        md.append("| %s | %s | %d | %d | %.2f |" % r)
-    md += ["", "Other kernels in the same trace (input generation, not timed by bench.py):", ""]
-    for name, st in stats.items():
-        if name not in CHAIN_KERNELS:
-            md.append("- %s: %s calls, avg %.2f us" % (name, st["Calls"],
-                                                        float(st["AverageNs"]) / 1e3))
-    with open(os.path.join(out, "chain_c3_prefill_8b_rocprof.md"), "w") as f:
-        f.write("\n".join(md) + "\n")
-    sw = [r for r in rows if r[0] == "swiglu"][0]
+
+    def write_md(fname, title, parts, unique=None):
+        """unique: {op: unique-row bytes} of Zipf gathers, quoted beside."""
+        md = [f"# {title}: rocprofv3 summary", ""] + preamble
+        for sub, rows, note in parts:
+            md += [f"## {sub}", ""] + ([note, ""] if note else []) + head + [fmt(r) for r in rows] + [""]
+            ur = [r for r in rows if unique and r[0] in unique]
+            if ur:
+                md += ["Zipf gathers, each distinct table row counted once (the fraction bench.py "
+                       "quotes):", "", "| op | unique-row bytes / launch | GB/s (avg us) | "
+                       "fraction of 8 TB/s |", "|---|---|---|---|"]
+                for r in ur:
+                    gbs = unique[r[0]] / (r[3] * 1e-6) / 1e9
+                    md.append("| %s | %d | %.1f | %.4f |" % (r[0], unique[r[0]], gbs, gbs / peak))
+                md.append("")
+        with open(os.path.join(out_dir, fname), "w") as f:
+            f.write("\n".join(md))
+        return md
+
+    c3 = workloads.CONFIGS["c3_prefill_8b"]
+    c3_rows = table("c3_ops", op_bytes(workloads, c3, c3["tokens"]))
+    c4 = workloads.CONFIGS["c4_quant_gather"]
+    c4_rows = table("c4_gather", {q: workloads.bytes_gather_quant(q, c4["tokens"], c4["dim"])
+                                  for q in GATHER_QUANT_ORDER})
+    c5 = workloads.CONFIGS["c5_70b"]
+    T5 = c5["tokens"]
+    c5_rows = table("c5_ops", {"add_rmsnorm": workloads.bytes_add_rmsnorm(T5, c5["dim"]),
+                               "rope": workloads.bytes_rope(T5, c5["n_heads"], c5["n_kv_heads"],
+                                                            c5["head_dim"]),
+                               "swiglu": workloads.bytes_swiglu(T5, c5["ffn"])})
+    for sec, rows in (("c3_ops", c3_rows), ("c4_gather", c4_rows), ("c5_ops", c5_rows)):
+        traffic[sec] = {r[0]: round(r[8]) for r in rows if r[8] is not None}
+    ids3 = workloads.zipf_ids(c3["tokens"], c3["vocab"], 1.1, c3["seed"])
+    md = write_md("chain_c3_prefill_8b_rocprof.md",
+                  "Op chain, configs[2] (Llama-3-8B shape, T = 4096)",
+                  [("Per-launch timing pass (bench.py ops)", c3_rows,
+                    "The gather's table rows repeat (Zipf ids): its counter bytes are below its "
+                    "algorithmic bytes, and its fraction of peak is quoted on distinct rows.")],
+                  {"gather_f32": workloads.bytes_gather_unique(ids3, c3["dim"])})
+    ids4 = workloads.zipf_ids(c4["tokens"], c4["vocab"], 1.1, c4["seed"])
+    write_md("gather_quant_c4_rocprof.md",
+             "Quantized token gathers, configs[3] (table 128256 x 4096, T = 4096 Zipf(1.1) ids)",
+             [("Q8_0 / Q4_0 / Q4_1 gathers", c4_rows,
+               "Hot rows repeat: counter bytes fall below the algorithmic bytes.")],
+             {q: workloads.bytes_gather_unique(ids4, c4["dim"], q) for q in GATHER_QUANT_ORDER})
+    write_md("chain_c5_70b_rocprof.md", "Op chain, configs[4] (Llama-3-70B shape, T = 8192)",
+             [("Per-launch timing pass (bench.py configs.c5_70b.ops)", c5_rows, None)])
+    # decode and tiny: latency-bound; every launch of the sections by kernel and grid
+    lines = ["# Decode steps, configs[1], and the tiny chain, configs[0]: rocprofv3 summary",
+             ""] + preamble
+    for sec, title in (("c2_decode", "configs[1]: 8B chain at T = 1..64 (eager and graph-replayed launches)"),
+                       ("c1_tiny", "configs[0]: tiny chain, 6 tokens")):
+        lines += [f"## {title}", "", "| op | kernel | grid (work-items) | launches | avg us | min us |",
+                  "|---|---|---|---|---|---|"]
+        groups = {}
+        for op, k, g, v in durations.get(sec, []):
+            groups.setdefault((op, k, g), []).append(v)
+        for (op, k, g), d in sorted(groups.items(), key=lambda kv: (kv[0][0], kv[0][2])):
+            lines.append("| %s | %s | %d | %d | %.2f | %.2f |" % (op, k, g, len(d), mean(d), min(d)))
+        lines.append("")
+    with open(os.path.join(out_dir, "chain_decode_tiny_rocprof.md"), "w") as f:
+        f.write("\n".join(lines))
+    sw = [r for r in c3_rows if r[0] == "swiglu"][0]
     with open(PMC_FILE, "w") as f:
         json.dump({"kernel": "StreamKernel<SwiGluOp> (swiglu)", "workload": "c3_prefill_8b",
-                   "hbm_bytes_per_launch": round(traffic["swiglu"]),
-                   "algorithmic_bytes_per_launch": nbytes["swiglu"],
+                   "hbm_bytes_per_launch": round(sw[8]),
+                   "algorithmic_bytes_per_launch": sw[9],
                    "fetch_size_kib": round(sw[6], 1), "write_size_kib": round(sw[7], 1),
                    "fetch_factor": round(f_factor, 5), "write_factor": round(w_factor, 5),
                    "rocprof_avg_us": round(sw[3], 2),
-                   "per_op_hbm_bytes": {k: round(v) for k, v in traffic.items()},
+                   "per_section_hbm_bytes": traffic,
                    "commands": PROFILE_COMMANDS}, f, indent=1)
     print("\n".join(md))
 
@@ -1093,12 +1417,21 @@ def main():
     peak = workloads.HBM_PEAK_GBS
     cfg = workloads.CONFIGS["c3_prefill_8b"]
     T = cfg["tokens"]
+    marks = Marks(mlk)
     chain = Chain(mlk, cfg, T, seed=cfg["seed"])
+    marks("c3_chain", chain.stream)
     total_ms = chain.run(args.steps, args.warmup)
     nbytes = op_bytes(workloads, cfg, T)
-    chain_bytes = sum(nbytes.values())
+    unique_gather = workloads.bytes_gather_unique(chain.ids_host, cfg["dim"])
+    # the gather's hot Zipf rows come from cache: each distinct row counts once
+    chain_bytes = sum(nbytes.values()) - nbytes["gather_f32"] + unique_gather
+    marks("c3_ops", chain.stream)
     ops = summarize(chain.run_ops(args.steps), nbytes, peak)
-    add_unique(ops["gather_f32"], workloads.bytes_gather_unique(chain.ids_host, cfg["dim"]), peak)
+    add_unique(ops["gather_f32"], unique_gather, peak)
+    gather_fractions(ops["gather_f32"])
+    for op, hbm in counter_traffic().get("c3_ops", {}).items():
+        if op in ops:
+            add_counter(ops[op], hbm, peak)
     value = chain_bytes * args.steps / (total_ms * 1e-3) / 1e9
     sw = ops["swiglu"]
     result = {
@@ -1120,6 +1453,7 @@ def main():
                    "n_kv_heads": cfg["n_kv_heads"], "head_dim": cfg["head_dim"],
                    "ffn_dim": cfg["ffn"], "vocab": cfg["vocab"], "rope_theta": cfg["theta"],
                    "positions": "0..T-1", "chain_bytes": chain_bytes,
+                   "chain_bytes_algorithmic": sum(nbytes.values()),
                    "rotating_sets": N_SETS},
         "frac_of_peak": round(value / peak, 4),
         "us_per_chain": round(total_ms * 1e3 / args.steps, 2),
@@ -1131,29 +1465,18 @@ def main():
                      "traffic": traffic_from_profiles()},
         "device": mlk.device_info(0),
     }
-    # the same chain as a decode step, T = 1 and 64 tokens at
-    # positions uniform in [0, 8191] (latency-bound: µs per chain, eager
-    # launches and one HIP graph replay per step)
-    c2 = workloads.CONFIGS["c2_decode_8b"]
-    decode = {}
-    for t in (1, 64):
-        pos = workloads.decode_positions(t, c2["max_pos"], c2["seed"])
-        dch = Chain(mlk, c2, t, seed=c2["seed"], n_sets=2, positions=pos, table=chain.table)
-        n = max(args.steps, 100)
-        eager = dch.run(n, args.warmup) / n
-        graph = dch.run_graph(n)
-        decode[str(t)] = {"us_per_chain_eager": round(eager * 1e3, 2),
-                          "us_per_chain_graph": round(graph * 1e3, 2),
-                          "chain_bytes": workloads.bytes_chain(c2, t)}
-        del dch
-    result["decode_c2_8b"] = decode
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(mlk, chain, cfg, T, workloads)
+    with_cpu = not args.no_cpu_baseline
+    if with_cpu:
+        result["cpu_baseline"] = cpu_chain_baseline(
+            chain_host_bufs(chain, cfg, T), T, chain_bytes,
+            f"the whole configs[2] chain (T={T}, Llama-3-8B shapes)")
+    configs = {"c1_tiny": None, "c2_decode_8b": c2_decode(mlk, args.steps, args.warmup, marks,
+                                                          chain.table)}
     del chain
-    if args.extra:
-        extra = extra_configs(mlk, workloads, max(10, args.steps // 2), peak)
-        with open(args.extra, "w") as f:
-            json.dump(extra, f, indent=1)
+    configs["c1_tiny"] = c1_tiny(mlk, args.steps, args.warmup, marks)
+    configs["c4_quant_gather"] = c4_gathers(mlk, args.steps, peak, marks, with_cpu)
+    configs["c5_70b"] = c5_chain(mlk, args.steps, args.warmup, peak, marks, with_cpu)
+    result["configs"] = configs
     print(json.dumps(result))
 
 

@@ -175,14 +175,24 @@ __device__ inline void SinCosAngle(double a, double* s, double* c) {
     sincospi((p - n) + e, s, c);
 }
 
-// RoPE of one pair (x0, x1) of a head at position pos, pair index i
-// (src/ops.cc:177-224): angle = (double) pos * pow((double) theta, -2.0 * i /
-// head_dim), cos and sin in float64, each output rounded once to float.  The
-// fused q/k/v epilogues use these; the RoPE kernels write the same
-// expressions.
-__device__ inline void RopeCosSin(int32_t pos, int i, int head_dim, float theta, double* c,
-                                  double* s) {
-    const double inv_freq = pow(static_cast<double>(theta), -2.0 * i / head_dim);
+// RoPE's inverse frequencies theta^(-2i / head_dim), one per pair index i,
+// evaluated on the host with the C library's pow exactly as the CPU Rope
+// does (src/ops.cc:200-206), so every angle pos * inv[i] equals the
+// reference's bit for bit; kernels take the table by value (kernel
+// arguments), so no device memory or copy is involved.  head_dim up to
+// 2 * kRopePairs.
+constexpr int kRopePairs = 128;
+struct RopeFreqs {
+    double inv[kRopePairs];
+};
+// Fills the table for head_dim / 2 pairs (head_dim even, <= 2 * kRopePairs).
+RopeFreqs MakeRopeFreqs(float theta, int head_dim);
+
+// RoPE of one pair (x0, x1) of a head at position pos with inverse
+// frequency inv_freq (src/ops.cc:177-224): angle = (double) pos * inv_freq,
+// cos and sin in float64, each output rounded once to float.  The fused
+// q/k/v epilogues use these; the RoPE kernels write the same expressions.
+__device__ inline void RopeCosSin(int32_t pos, double inv_freq, double* c, double* s) {
     SinCosAngle(static_cast<double>(pos) * inv_freq, s, c);
 }
 

@@ -179,6 +179,10 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
                     static_cast<long long>(layer), static_cast<long long>(n_layers));
     }
     const bool contiguous = Contiguous(positions);
+    if (contiguous && pos0 < 0) {
+        return Fail(MLK_ERR_RANGE, "%s: positions %d..%lld out of range (pos must be "
+                    "non-negative)", fn, pos0, static_cast<long long>(pos0 + n_tokens - 1));
+    }
     if (max_ctx <= 0 || max_ctx > max_seq || (contiguous && pos0 + n_tokens > max_ctx)) {
         return Fail(MLK_ERR_RANGE, "%s: max_ctx %lld must cover the positions and be <= max_seq "
                     "%lld", fn, static_cast<long long>(max_ctx), static_cast<long long>(max_seq));
@@ -232,7 +236,8 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     // write k and v into the cache rows, in place of mlk_rope_f32 and
     // mlk_kv_write_f32; the NeoX layout keeps the separate launches.
     const bool rope_fused = (qkvm || (qkv1 && StreamRopeFits(D, c.head_dim))) &&
-                            c.rope_type == MLK_ROPE_NORMAL && c.head_dim % 2 == 0;
+                            c.rope_type == MLK_ROPE_NORMAL && c.head_dim % 2 == 0 &&
+                            c.head_dim <= 2 * kRopePairs;
     if (rope_fused && positions == nullptr && (pos0 < 0 || pos0 + T > max_seq)) {
         return Fail(MLK_ERR_RANGE, "%s: positions %d..%lld out of range [0, %lld)", fn, pos0,
                     static_cast<long long>(pos0 + T - 1), static_cast<long long>(max_seq));
@@ -245,7 +250,8 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[1] = Seg(w->wk, rope_fused ? k_cache + layer * max_seq * slot : k, KD);
         a.seg[2] = Seg(w->wv, rope_fused ? v_cache + layer * max_seq * slot : v, KD);
         a.n_seg = 3;
-        a.rope = RopeArgs{positions, pos0, c.head_dim, c.rope_theta, slot, max_seq, err};
+        a.rope = RopeArgs{positions, pos0, c.head_dim, slot, max_seq, err,
+                          MakeRopeFreqs(c.rope_theta, c.head_dim)};
         const int mode = rope_fused ? kStreamQkvRope : kStreamPlain;
         if (qkv1) {
             MLK_TRY(LinearRowStream(w->wq.type, h, D, a, mode, hs));

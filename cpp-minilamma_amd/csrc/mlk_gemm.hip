@@ -630,8 +630,7 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
             float r0 = x0, r1 = x1;
             if (pos >= 0) {
                 double cs, sn;
-                RopeCosSin(pos, static_cast<int>(local % r.head_dim) / 2, r.head_dim, r.theta, &cs,
-                           &sn);
+                RopeCosSin(pos, r.freq.inv[static_cast<int>(local % r.head_dim) / 2], &cs, &sn);
                 RopeRotate(x0, x1, cs, sn, &r0, &r1);
             }
             if (is_k && !cache_ok) continue;

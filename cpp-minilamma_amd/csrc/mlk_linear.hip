@@ -778,7 +778,7 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, 
         if (pos >= 0) {
             for (int i = threadIdx.x; i < a.rope.head_dim / 2; i += kStreamThreads) {
                 double cs, sn;
-                RopeCosSin(pos, i, a.rope.head_dim, a.rope.theta, &cs, &sn);
+                RopeCosSin(pos, a.rope.freq.inv[i], &cs, &sn);
                 rope_cs[i] = make_double2(cs, sn);
             }
         }
@@ -948,7 +948,8 @@ mlk_status Gemv(const float* x, const uint8_t* w, const float* bias, float* y, i
 
 bool QkvRopeArgsOk(const StreamArgs& a) {
     const int64_t hd = a.rope.head_dim;
-    return a.n_seg == 3 && hd > 0 && hd % 2 == 0 && a.seg[0].rows % hd == 0 &&
+    return a.n_seg == 3 && hd > 0 && hd % 2 == 0 && hd <= 2 * kRopePairs &&
+           a.seg[0].rows % hd == 0 &&
            a.seg[1].rows % hd == 0 && a.seg[2].rows % 2 == 0 &&
            a.rope.kv_stride >= a.seg[1].rows && a.rope.kv_stride >= a.seg[2].rows &&
            a.rope.max_seq > 0;

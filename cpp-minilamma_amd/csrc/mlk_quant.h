@@ -91,11 +91,11 @@ struct StreamSeg {
 struct RopeArgs {
     const int32_t* positions;  // per token, or null: pos0 + t
     int32_t pos0;
-    int32_t head_dim;
-    float theta;
+    int32_t head_dim;           // <= 2 * kRopePairs
     int64_t kv_stride;  // floats between cache rows of consecutive positions
     int64_t max_seq;
     int32_t* err;
+    RopeFreqs freq;             // inverse frequencies of the head's pairs
 };
 
 struct StreamArgs {

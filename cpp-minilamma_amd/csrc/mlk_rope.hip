@@ -8,6 +8,9 @@
 // device kernel (src/cuda_ops.cu:254-299) used fp32 powf/cosf/sinf, whose
 // angle drifts from the double one by ~4e-4 rad at pos 8191 (theta 5e5);
 // here the angle, cos and sin are float64, so the result equals the CPU's.
+// The pow factors are evaluated once per call on the host with the C
+// library's pow (the CPU's own), so the angles are the reference's bit for
+// bit, and handed to the kernel in its arguments.
 //
 // Work layout: workgroups walk the tokens (about four per workgroup at
 // T = 4096).  The threads form `rows` rows of `lanes` lanes; a lane owns PV
@@ -150,12 +153,16 @@ struct Pairs<1, true> {
     }
 };
 
+// General form (any head count and even head_dim): inverse frequencies from
+// the host table when head_dim <= 2 * kRopePairs, else from the device pow
+// (same expression; it may differ from the C library's in the last bit).
 template <int PV, bool kNeoX>
 __global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64_t n_tokens,
                                                        int n_heads, int n_kv_heads, int head_dim,
                                                        int64_t q_stride, int64_t k_stride,
                                                        const int32_t* positions, int32_t pos0,
-                                                       float theta, int32_t* err) {
+                                                       float theta, const RopeFreqs f,
+                                                       int32_t* err) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
     const int half = head_dim / 2;
@@ -173,7 +180,8 @@ __global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64
 #pragma unroll
         for (int p = 0; p < PV; ++p) {
             const int i = g * PV + p;
-            inv_freq[p] = pow(static_cast<double>(theta), -2.0 * i / head_dim);
+            inv_freq[p] = half <= kRopePairs ? f.inv[i]
+                                             : pow(static_cast<double>(theta), -2.0 * i / head_dim);
         }
         for (int64_t t = blockIdx.x; t < n_tokens; t += gridDim.x) {
             const int32_t pos = positions != nullptr ? positions[t] : pos0 + static_cast<int32_t>(t);
@@ -236,7 +244,7 @@ __global__ __launch_bounds__(1024) void RopePipe(float* q, float* k, int64_t n_t
                                                  int n_heads, int n_kv_heads, int head_dim,
                                                  int64_t q_stride, int64_t k_stride,
                                                  const int32_t* positions, int32_t pos0,
-                                                 float theta, int rows, int q_slots,
+                                                 const RopeFreqs f, int rows, int q_slots,
                                                  int32_t* err) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
@@ -249,9 +257,7 @@ __global__ __launch_bounds__(1024) void RopePipe(float* q, float* k, int64_t n_t
     auto token = [&](int64_t j) { return static_cast<int64_t>(blockIdx.x) + j * gridDim.x; };
     double inv_freq[PV];
 #pragma unroll
-    for (int p = 0; p < PV; ++p) {
-        inv_freq[p] = pow(static_cast<double>(theta), -2.0 * (lane * PV + p) / head_dim);
-    }
+    for (int p = 0; p < PV; ++p) inv_freq[p] = f.inv[lane * PV + p];
     using V = Pairs<PV, kNeoX>;
     uint32_t off[kBatch];  // byte offset of the lane's elements of the slot's head
     bool ok[kBatch];       // the slot holds a head
@@ -324,7 +330,9 @@ mlk_status LaunchRope(float* q, float* k, int64_t n_tokens, int n_heads, int n_k
                       int head_dim, int64_t qs, int64_t ks, const int32_t* positions,
                       int32_t pos0, float theta, int32_t* err, hipStream_t stream) {
     const int lanes = head_dim / 2 / PV;
-    const int rows = PipeRows(n_heads, n_kv_heads, lanes);
+    const bool table = head_dim / 2 <= kRopePairs;
+    const RopeFreqs f = MakeRopeFreqs(theta, table ? head_dim : 2);
+    const int rows = table ? PipeRows(n_heads, n_kv_heads, lanes) : 0;
     // byte offsets within a token's Q or K row are 32-bit
     const bool offsets_fit =
         4 * static_cast<int64_t>(n_heads > n_kv_heads ? n_heads : n_kv_heads) * head_dim <= UINT32_MAX;
@@ -336,13 +344,13 @@ mlk_status LaunchRope(float* q, float* k, int64_t n_tokens, int n_heads, int n_k
         const int q_slots = (n_heads + rows - 1) / rows;
         hipLaunchKernelGGL((RopePipe<PV, kNeoX>), dim3(grid), dim3(threads), 0, stream, q, k,
                            n_tokens, n_heads, n_kv_heads, head_dim, qs, ks, positions, pos0,
-                           theta, rows, q_slots, err);
+                           f, rows, q_slots, err);
         return CheckLaunch("RopePipe");
     }
     const unsigned grid = GridFor(n_tokens, 1, 4);
     hipLaunchKernelGGL((RopeKernel<PV, kNeoX>), dim3(grid), dim3(kThreads), 0, stream, q, k,
                        n_tokens, n_heads, n_kv_heads, head_dim, qs, ks, positions, pos0, theta,
-                       err);
+                       f, err);
     return CheckLaunch("RopeKernel");
 }
 

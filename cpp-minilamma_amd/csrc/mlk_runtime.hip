@@ -5,6 +5,8 @@
 // 57-161): device count / selection / properties, malloc, free and memcpy.
 #include "mlk_common.h"
 
+#include <cmath>
+
 #include <cstring>
 #include <mutex>
 
@@ -28,6 +30,15 @@ mlk_status FromHip(hipError_t err, const char* what) {
         return Fail(MLK_ERR_NO_DEVICE, "%s: %s", what, hipGetErrorString(err));
     }
     return Fail(MLK_ERR_HIP, "%s: %s", what, hipGetErrorString(err));
+}
+
+RopeFreqs MakeRopeFreqs(float theta, int head_dim) {
+    RopeFreqs f{};
+    const int half = head_dim / 2 < kRopePairs ? head_dim / 2 : kRopePairs;
+    for (int i = 0; i < half; ++i) {
+        f.inv[i] = std::pow(static_cast<double>(theta), -2.0 * i / head_dim);
+    }
+    return f;
 }
 
 int ComputeUnits() {

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from conftest import tiny_model
+from conftest import assert_bits_equal, tiny_model
 
 pytestmark = pytest.mark.gpu
 
@@ -161,6 +161,19 @@ def test_forward_layer_rejects_cache_arguments(mlk, fwd):
         fwd.forward_layer_batch(cfg, dm.layers[0], x, 1, kc, kc, 1, 32, 0, 32, ws, pos0=3)
     with pytest.raises(mlk.MlkError, match="out of range"):
         fwd.forward_layer_batch(cfg, dm.layers[0], x, 1, kc, vc, 1, 32, 0, 32, ws, pos0=-1)
+    # the NeoX layout and F32 weights keep the separate RoPE and q/k/v
+    # launches: a negative position is still rejected before the first one
+    for rope_type, wt, T in ((1, "q8_0", 1), (0, "f32", 1), (0, "q8_0", 2)):
+        c2 = dict(cfg, rope_type=rope_type)
+        m2 = O.forward_model(c2, seed=3, weight_type=wt)
+        d2 = fwd.DeviceModel(m2)
+        x2 = mlk.DeviceBuffer.empty((T, 512))
+        before = x2.download()
+        ws2 = mlk.DeviceBuffer(fwd.layer_workspace_bytes(c2, T, 32, True), np.uint8)
+        with pytest.raises(mlk.MlkError, match="out of range"):
+            fwd.forward_layer_batch(c2, d2.layers[0], x2, T, kc, vc, 1, 32, 0, 32, ws2, pos0=-1)
+        mlk.synchronize()
+        assert_bits_equal(x2.download(), before, f"x untouched (rope {rope_type}, {wt}, T {T})")
 
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0", "q4_1"])
