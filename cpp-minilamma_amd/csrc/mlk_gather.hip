@@ -27,6 +27,8 @@
 // and the staging round trip only added latency.)
 #include "mlk_quant.h"
 
+#include <type_traits>
+
 namespace mlk {
 namespace {
 
@@ -57,7 +59,13 @@ __device__ inline float Decode1(const uint8_t* blk, int w) {
 }
 
 // Decodes elements w..w+3 (w % 4 == 0) of block `blk` straight from global
-// memory with aligned loads: every block starts at an even byte offset
+// memory with aligned loads.  The scales go through the hardware conversion
+// (v_cvt_f32_f16, one instruction instead of the integer sequence of
+// HalfBits, which made the Q4_1 gather VALU-bound); gfx950 keeps fp16
+// denormals, so subnormal scales convert exactly (the parity tests hold
+// blocks with scale 0x0001), and a NaN scale still gives NaN outputs (its
+// quiet bit is set one step earlier than on the CPU, where the product
+// sets it).  Every block starts at an even byte offset
 // (34, 18 and 20 are even and rows start 16-byte aligned), so d and m are
 // u16 loads; Q4_1 blocks start 4-byte aligned (20b) so d|m and the four code
 // bytes (20b + 4 + 4k) are one u32 each, Q8_0 / Q4_0 code bytes two u16.
@@ -70,11 +78,11 @@ __device__ inline float4 Decode4(const uint8_t* blk, int w) {
     uint32_t codes;  // four code bytes, little-endian
     if (QT == MLK_Q4_1) {
         const uint32_t dm = *reinterpret_cast<const uint32_t*>(blk);
-        d = HalfBits(dm & 0xFFFFu);
-        m = HalfBits(dm >> 16);
+        d = HalfHw(dm & 0xFFFFu);
+        m = HalfHw(dm >> 16);
         codes = *reinterpret_cast<const uint32_t*>(blk + 4 + (w & 15));
     } else {
-        d = HalfBits(*reinterpret_cast<const uint16_t*>(blk));
+        d = HalfHw(*reinterpret_cast<const uint16_t*>(blk));
         const uint16_t* p =
             reinterpret_cast<const uint16_t*>(blk + 2 + (QT == MLK_Q8_0 ? w : (w & 15)));
         codes = static_cast<uint32_t>(p[0]) | (static_cast<uint32_t>(p[1]) << 16);
@@ -108,10 +116,14 @@ __device__ inline float4 Decode4(const uint8_t* blk, int w) {
     return o;
 }
 
-// A workgroup takes one token row per iteration (grid-stride over tokens).
-// vec: dim % 4 == 0 and aligned buffers -> one float4 per lane per step
-// with Decode4; otherwise one element per lane with Decode1 (byte loads).
-template <int QT>
+// A workgroup takes one token row per iteration (grid-stride over tokens;
+// the launch gives every token its own workgroup up to 16 per CU).
+// U > 0: dim == 4 * U * kQThreads and aligned buffers (the 8B and 70B
+// widths): each lane decodes U float4 at compile-time offsets, all their
+// loads issued before the first store.  U == 0: any width; vec (dim % 4 ==
+// 0, aligned buffers) -> one float4 per lane per step with Decode4,
+// otherwise one element per lane with Decode1 (byte loads).
+template <int QT, int U>
 __global__ __launch_bounds__(kQThreads) void GatherQuantKernel(const uint8_t* __restrict__ blocks,
                                                                int64_t vocab, int64_t dim,
                                                                const int32_t* __restrict__ ids,
@@ -130,7 +142,17 @@ __global__ __launch_bounds__(kQThreads) void GatherQuantKernel(const uint8_t* __
             continue;
         }
         const uint8_t* row = blocks + static_cast<int64_t>(id) * row_bytes;
-        if (vec) {
+        if constexpr (U > 0) {
+            float4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int e = 4 * (tid + u * kQThreads);
+                v[u] = Decode4<QT>(row + (e >> 5) * kBB, e & 31);
+            }
+            float4* d4 = reinterpret_cast<float4*>(dst);
+#pragma unroll
+            for (int u = 0; u < U; ++u) StoreNT(d4 + tid + u * kQThreads, v[u]);
+        } else if (vec) {
             float4* d4 = reinterpret_cast<float4*>(dst);
             for (int64_t j = tid; j < dim / 4; j += kQThreads) {
                 const int64_t e = 4 * j;
@@ -378,22 +400,29 @@ mlk_status mlk_gather_quant(int32_t quant_type, const void* blocks, int64_t voca
     // the vector path reads d|m and codes as aligned u16/u32 words
     const int vec = (dim % 4 == 0 && Aligned(out, 16) &&
                      Aligned(blocks, quant_type == MLK_Q4_1 ? 4 : 2)) ? 1 : 0;
-    const unsigned grid = GridFor(n_tokens, 1, 8);
+    // one token per workgroup up to 16 workgroups per CU: measured 81-84% of
+    // HBM peak by distinct rows at configs[3], against 66-78% with 8 per CU
+    const unsigned grid = GridFor(n_tokens, 1, 16);
     const hipStream_t s = AsStream(stream);
     const uint8_t* b = static_cast<const uint8_t*>(blocks);
+    const int u = !vec ? 0 : (dim == 4 * kQThreads ? 1 : (dim == 8 * kQThreads ? 2 : 0));
+    auto launch = [&](auto qt) {
+        constexpr int Q = decltype(qt)::value;
+        if (u == 1) {
+            hipLaunchKernelGGL((GatherQuantKernel<Q, 1>), dim3(grid), dim3(kQThreads), 0, s, b,
+                               vocab, dim, ids, token, n_tokens, out, err, vec);
+        } else if (u == 2) {
+            hipLaunchKernelGGL((GatherQuantKernel<Q, 2>), dim3(grid), dim3(kQThreads), 0, s, b,
+                               vocab, dim, ids, token, n_tokens, out, err, vec);
+        } else {
+            hipLaunchKernelGGL((GatherQuantKernel<Q, 0>), dim3(grid), dim3(kQThreads), 0, s, b,
+                               vocab, dim, ids, token, n_tokens, out, err, vec);
+        }
+    };
     switch (quant_type) {
-        case MLK_Q8_0:
-            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q8_0>, dim3(grid), dim3(kQThreads), 0, s, b,
-                               vocab, dim, ids, token, n_tokens, out, err, vec);
-            break;
-        case MLK_Q4_0:
-            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_0>, dim3(grid), dim3(kQThreads), 0, s, b,
-                               vocab, dim, ids, token, n_tokens, out, err, vec);
-            break;
-        default:
-            hipLaunchKernelGGL(GatherQuantKernel<MLK_Q4_1>, dim3(grid), dim3(kQThreads), 0, s, b,
-                               vocab, dim, ids, token, n_tokens, out, err, vec);
-            break;
+        case MLK_Q8_0: launch(std::integral_constant<int, MLK_Q8_0>{}); break;
+        case MLK_Q4_0: launch(std::integral_constant<int, MLK_Q4_0>{}); break;
+        default: launch(std::integral_constant<int, MLK_Q4_1>{}); break;
     }
     return CheckLaunch("GatherQuantKernel");
 }

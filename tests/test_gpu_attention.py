@@ -206,19 +206,29 @@ def test_attention_dominant_key_in_each_chunk(mlk):
             assert np.abs(got[kvh * 4] - vc[0, jstar, kvh]).max() < 1e-3
 
 
-def test_attention_bad_positions_give_zero_rows_and_flag(mlk):
-    rng = np.random.default_rng(5)
+@pytest.mark.parametrize("T", [4, 6, 21])
+def test_attention_bad_positions_give_zero_rows_and_flag(mlk, T):
+    """Invalid positions (negative, at or past max_ctx) beside valid ones: 4
+    tokens take the per-token kernel; 6 and 21 the shared-tile kernel, whose
+    token blocks then mix valid and invalid rows (zero rows, and partials
+    the merge must skip), over one chunk (max_ctx 40) and several (600)."""
+    rng = np.random.default_rng(5 + T)
     H, KV, hd, S = 8, 2, 64, 600
     kc, vc = random_cache(rng, 1, S, KV, hd)
     cache = Cache(mlk, kc, vc)
-    q = rng.standard_normal((4, H, hd)).astype(np.float32)
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
     for max_ctx in (600, 40):  # several chunks, and one chunk
         err = mlk.DeviceBuffer.from_array(np.zeros(1, np.int32))
         positions = [3, -1, max_ctx, min(17, max_ctx - 1)]
+        positions += [int(p) for p in rng.integers(0, max_ctx, T - 4)]
+        if T > 4:
+            positions[-1] = -7  # an invalid row in a later token block too
         got = cache.attend(q, 0, positions, max_ctx=max_ctx, err=err)
         assert err.download()[0] != 0
-        assert not got[1].any() and not got[2].any()
-        for t in (0, 3):
+        bad = [t for t, p in enumerate(positions) if p < 0 or p >= max_ctx]
+        for t in bad:
+            assert not got[t].any(), f"token {t} at {positions[t]}: not a zero row"
+        for t in (t for t in range(T) if t not in bad):
             ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, positions[t])
             assert_attention_close(got[t], ex, pav, dmax, n, f"valid token {t}")
         ok = mlk.DeviceBuffer.from_array(np.zeros(1, np.int32))
