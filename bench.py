@@ -977,7 +977,8 @@ def attention_bench(mlk, steps, peak, path):
         rows = {}
         cases = [("T1_pos%d" % p, np.array([p], np.int32)) for p in (511, 2047, 4095, 8191)]
         if name == "llama3_8b":
-            cases.append(("T64_uniform0_8191", workloads.decode_positions(64, S - 1, 42)))
+            for t in (16, 64):
+                cases.append((f"T{t}_uniform0_8191", workloads.decode_positions(t, S - 1, 42)))
         for case, pos in cases:
             T = pos.size
             q = mlk.DeviceBuffer.empty((T, H * hd))
