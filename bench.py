@@ -777,6 +777,12 @@ def _device_layer(mlk, fwd, cfg, wt, seed):
             buf = mlk.DeviceBuffer(mlk.quant_bytes(wt, o, i), np.uint8)
             mlk.quantize(wt, tmp, o, i, buf)
             lw.type = mlk.QUANT[wt]
+            n_planar = mlk.quant_planar_bytes(wt, o, i)
+            if n_planar > 0:  # the planar copy the 2..32-token calls run on
+                pl = mlk.DeviceBuffer(n_planar, np.uint8)
+                mlk.quant_to_planar(wt, buf, o, i, pl)
+                lw.planar = pl.ptr
+                keep.append(pl)
         lw.data, lw.bias = buf.ptr, None
         setattr(w, name, lw)
         keep.append(buf)

@@ -69,6 +69,8 @@ _SIGNATURES = {
     "mlk_quantize": [_i32, _vp, _i64, _i64, _vp, _vp],
     "mlk_linear_quant": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, C.c_size_t, _vp],
     "mlk_linear_f32": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, C.c_size_t, _vp],
+    "mlk_quant_to_planar": [_i32, _vp, _i64, _i64, _vp, _vp],
+    "mlk_linear_planar": [_i32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, C.c_size_t, _vp],
     "mlk_matmul_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "mlk_fill_normal_f32": [_vp, _i64, _f, _f, C.c_uint64, _vp],
     "mlk_kv_write_f32": [_vp, _vp, _i64, _i64, _i32, _i32, _i64, _vp, _i64, _vp, _i64, _vp, _i32,
@@ -128,6 +130,10 @@ def _load():
     lib.mlk_attention_noalloc_scratch_bytes.argtypes = []
     lib.mlk_linear_workspace_bytes.restype = C.c_int64
     lib.mlk_linear_workspace_bytes.argtypes = [_i64, _i64, _i64]
+    lib.mlk_quant_planar_bytes.restype = C.c_int64
+    lib.mlk_quant_planar_bytes.argtypes = [_i32, _i64, _i64]
+    lib.mlk_linear_planar_workspace_bytes.restype = C.c_int64
+    lib.mlk_linear_planar_workspace_bytes.argtypes = [_i64, _i64, _i64]
     return lib
 
 
@@ -148,6 +154,8 @@ def exported_symbols():
                                        "mlk_abi_version", "mlk_quant_bytes",
                                        "mlk_attention_workspace_bytes",
                                        "mlk_linear_workspace_bytes",
+                                       "mlk_quant_planar_bytes",
+                                       "mlk_linear_planar_workspace_bytes",
                                        # bound with their structs in forward.py
                                        "mlk_forward_layer_workspace_bytes",
                                        "mlk_forward_layer_batch"])
@@ -444,6 +452,52 @@ def linear_quant(qtype, x, w_blocks, y, rows, in_features, out_features, bias=No
     check(lib.mlk_linear_quant(QUANT[qtype], _p(x), _p(w_blocks), _p(bias), _p(y), rows,
                                in_features, out_features, ws, ws_bytes, _sp(stream)),
           "mlk_linear_quant")
+
+
+def quant_planar_bytes(qtype, rows, cols):
+    """Bytes of the planar layout of a [rows, cols] Q8_0 / Q4_0 matrix (0: none)."""
+    return int(lib.mlk_quant_planar_bytes(QUANT[qtype], rows, cols))
+
+
+def quant_to_planar(qtype, w_blocks, rows, cols, planar, stream=None):
+    """Repack [rows, cols] blocks into the planar layout (a buffer of
+    quant_planar_bytes bytes)."""
+    check(lib.mlk_quant_to_planar(QUANT[qtype], _p(w_blocks), rows, cols, _p(planar),
+                                  _sp(stream)), "mlk_quant_to_planar")
+
+
+def linear_planar_workspace_bytes(rows, in_features, out_features):
+    """Bytes of the workspace of linear_planar (required up to 32 rows)."""
+    return int(lib.mlk_linear_planar_workspace_bytes(rows, in_features, out_features))
+
+
+_planar_ws = {}  # device id -> DeviceBuffer grown to the largest request
+
+
+def linear_planar(qtype, x, w_planar, y, rows, in_features, out_features, bias=None,
+                  stream=None, workspace="auto"):
+    """y[rows, out] = x[rows, in] @ dequant(W)^T (+ bias), W in the planar
+    layout; workspace: a DeviceBuffer, or "auto" (a per-device buffer kept by
+    this module, grown as needed)."""
+    if isinstance(workspace, str):
+        if workspace != "auto":
+            raise ValueError(f"workspace must be a DeviceBuffer or 'auto', not {workspace!r}")
+        need = max(linear_planar_workspace_bytes(rows, in_features, out_features), 16)
+        dev = C.c_int()
+        check(lib.mlk_get_device(C.byref(dev)))
+        buf = _planar_ws.get(dev.value)
+        if buf is None or buf.nbytes < need:
+            if buf is not None:
+                buf.close()
+            buf = _planar_ws[dev.value] = DeviceBuffer(need, np.uint8)
+        ws, ws_bytes = buf.ptr, buf.nbytes
+    elif workspace is None:
+        ws, ws_bytes = None, 0
+    else:
+        ws, ws_bytes = _p(workspace), workspace.nbytes
+    check(lib.mlk_linear_planar(QUANT[qtype], _p(x), _p(w_planar), _p(bias), _p(y), rows,
+                                in_features, out_features, ws, ws_bytes, _sp(stream)),
+          "mlk_linear_planar")
 
 
 def linear_f32(x, w, y, rows, in_features, out_features, bias=None, stream=None,

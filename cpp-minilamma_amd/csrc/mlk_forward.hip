@@ -30,6 +30,8 @@
 #include "mlk_common.h"
 #include "mlk_quant.h"
 
+#include <initializer_list>
+
 namespace mlk {
 namespace {
 
@@ -48,6 +50,10 @@ bool Contiguous(const int32_t* positions) { return positions == nullptr; }
 // quantized weights the layer fuses them as the one-token path does, with
 // the epilogues in the split-K reduction.
 bool FusedRows(int64_t T) { return T >= 8 && T <= 32; }
+
+// Token counts that take the planar weights when a layer has them (the
+// bf16 kernel, fused as FusedRows; one token keeps the block-layout GEMVs).
+bool PlanarRows(int64_t T) { return T >= 2 && T <= 32; }
 
 Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contiguous) {
     const int64_t D = c.dim, F = c.hidden_dim;
@@ -69,6 +75,14 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
         const int64_t fused[3][2] = {{D, QD + 2 * KD}, {D, 2 * F}, {F, D}};  // (in, all outputs)
         for (const auto& s : fused) {
             const int64_t b = SkinnyFusedWorkspaceBytes(MLK_Q8_0, T, s[0], s[1]);
+            if (b > p.lin_bytes) p.lin_bytes = b;
+        }
+    }
+    if (PlanarRows(T)) {  // the same groups (and wo) on planar weights
+        const int64_t groups[4][3] = {{D, QD + 2 * KD, 1}, {D, 2 * F, 1}, {F, D, 1}, {QD, D, 0}};
+        for (const auto& g : groups) {
+            if (g[0] % 256 != 0) continue;
+            const int64_t b = PlanarWorkspaceBytes(T, g[0], g[1], g[2] != 0);
             if (b > p.lin_bytes) p.lin_bytes = b;
         }
     }
@@ -104,6 +118,22 @@ StreamSeg Seg(const mlk_linear_weight& w, float* y, int64_t rows, const float* r
     return StreamSeg{static_cast<const uint8_t*>(w.data), w.bias, y, res, rows, 0};
 }
 
+// The weights of a group run planar: T in PlanarRows, all Q8_0 or all
+// Q4_0 with planar copies, in_features a multiple of 256.
+bool Planar(int64_t T, int64_t in, std::initializer_list<const mlk_linear_weight*> ws) {
+    const int t = (*ws.begin())->type;
+    if (!PlanarRows(T) || in % 256 != 0 || (t != MLK_Q8_0 && t != MLK_Q4_0)) return false;
+    for (const mlk_linear_weight* w : ws) {
+        if (w->type != t || w->planar == nullptr) return false;
+    }
+    return true;
+}
+
+StreamSeg PlanarSeg(const mlk_linear_weight& w, float* y, int64_t rows,
+                    const float* res = nullptr) {
+    return StreamSeg{static_cast<const uint8_t*>(w.planar), w.bias, y, res, rows, 0};
+}
+
 mlk_status CheckConfig(const char* fn, const mlk_layer_config* c) {
     if (c == nullptr) return Fail(MLK_ERR_INVALID, "%s: config must not be null", fn);
     if (c->dim <= 0 || c->hidden_dim <= 0 || c->n_heads <= 0 || c->n_kv_heads <= 0 ||
@@ -121,6 +151,12 @@ mlk_status CheckWeight(const char* fn, const char* name, const mlk_linear_weight
     if (w.data == nullptr) return Fail(MLK_ERR_INVALID, "%s: weight %s is null", fn, name);
     if (w.type != kLinearF32 && (w.type < MLK_Q8_0 || w.type > MLK_Q4_1)) {
         return Fail(MLK_ERR_INVALID, "%s: weight %s has unknown type %d", fn, name, w.type);
+    }
+    if (w.planar != nullptr &&
+        ((w.type != MLK_Q8_0 && w.type != MLK_Q4_0) || !Aligned(w.planar, 16))) {
+        return Fail(MLK_ERR_INVALID,
+                    "%s: weight %s: a planar copy needs Q8_0 or Q4_0 and 16-byte alignment", fn,
+                    name);
     }
     return MLK_OK;
 }
@@ -225,13 +261,19 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     const bool ffn1 = row && w->w_gate.type == w->w_up.type && RowStreamable(w->w_gate, D) &&
                       RowStreamable(w->w_up, D);
     const bool down1 = row && RowStreamable(w->w_down, F);
+    // 2..32 tokens on planar copies: the same three groups, plus wo
+    const bool qkvp = Planar(T, D, {&w->wq, &w->wk, &w->wv});
+    const bool ffnp = Planar(T, D, {&w->w_gate, &w->w_up});
+    const bool downp = Planar(T, F, {&w->w_down});
+    const bool wop = Planar(T, QD, {&w->wo});
     const bool mid = FusedRows(T);
-    const bool qkvm = mid && w->wq.type == w->wk.type && w->wq.type == w->wv.type &&
-                      w->wq.type != kLinearF32 && SkinnyFusedApplies(w->wq.type, T, D);
-    const bool ffnm = mid && w->w_gate.type == w->w_up.type && w->w_gate.type != kLinearF32 &&
-                      SkinnyFusedApplies(w->w_gate.type, T, D);
-    const bool downm = mid && w->w_down.type != kLinearF32 &&
-                       SkinnyFusedApplies(w->w_down.type, T, F);
+    const bool qkvm = qkvp || (mid && w->wq.type == w->wk.type && w->wq.type == w->wv.type &&
+                               w->wq.type != kLinearF32 && SkinnyFusedApplies(w->wq.type, T, D));
+    const bool ffnm = ffnp || (mid && w->w_gate.type == w->w_up.type &&
+                               w->w_gate.type != kLinearF32 &&
+                               SkinnyFusedApplies(w->w_gate.type, T, D));
+    const bool downm = downp || (mid && w->w_down.type != kLinearF32 &&
+                                 SkinnyFusedApplies(w->w_down.type, T, F));
     // The fused q/k/v launches also rotate q and k (normal-layout pairs) and
     // write k and v into the cache rows, in place of mlk_rope_f32 and
     // mlk_kv_write_f32; the NeoX layout keeps the separate launches.
@@ -245,16 +287,20 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     MLK_TRY(mlk_rmsnorm_f32(x, w->attention_norm, h, T, D, eps, stream));
     if (qkv1 || qkvm) {
         const int64_t slot = KD;
+        float* ky = rope_fused ? k_cache + layer * max_seq * slot : k;
+        float* vy = rope_fused ? v_cache + layer * max_seq * slot : v;
         StreamArgs a{};
-        a.seg[0] = Seg(w->wq, q, QD);
-        a.seg[1] = Seg(w->wk, rope_fused ? k_cache + layer * max_seq * slot : k, KD);
-        a.seg[2] = Seg(w->wv, rope_fused ? v_cache + layer * max_seq * slot : v, KD);
+        a.seg[0] = qkvp ? PlanarSeg(w->wq, q, QD) : Seg(w->wq, q, QD);
+        a.seg[1] = qkvp ? PlanarSeg(w->wk, ky, KD) : Seg(w->wk, ky, KD);
+        a.seg[2] = qkvp ? PlanarSeg(w->wv, vy, KD) : Seg(w->wv, vy, KD);
         a.n_seg = 3;
         a.rope = RopeArgs{positions, pos0, c.head_dim, slot, max_seq, err,
                           MakeRopeFreqs(c.rope_theta, c.head_dim)};
         const int mode = rope_fused ? kStreamQkvRope : kStreamPlain;
         if (qkv1) {
             MLK_TRY(LinearRowStream(w->wq.type, h, D, a, mode, hs));
+        } else if (qkvp) {
+            MLK_TRY(LinearPlanarFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs));
         } else {
             MLK_TRY(LinearSkinnyFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs));
         }
@@ -272,7 +318,12 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     MLK_TRY(mlk_attention_decode_f32(q, QD, k_cache, v_cache, n_layers, max_seq, c.n_heads,
                                      c.n_kv_heads, c.head_dim, layer, positions, pos0, T, max_ctx,
                                      a, att_ws, static_cast<size_t>(p.att_bytes), err, stream));
-    MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
+    if (wop) {
+        MLK_TRY(LinearPlanar(w->wo.type, a, w->wo.planar, w->wo.bias, proj, T, QD, D, lin_ws,
+                             lin_b, hs));
+    } else {
+        MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
+    }
     MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
     if (ffn1) {
         StreamArgs a{};
@@ -280,6 +331,12 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[1] = Seg(w->w_up, gate, F);
         a.n_seg = 2;
         MLK_TRY(LinearRowStream(w->w_gate.type, h, D, a, kStreamSwiGlu, hs));
+    } else if (ffnp) {
+        StreamArgs a{};
+        a.seg[0] = PlanarSeg(w->w_gate, gate, F);
+        a.seg[1] = PlanarSeg(w->w_up, gate, F);
+        a.n_seg = 2;
+        MLK_TRY(LinearPlanarFused(w->w_gate.type, h, T, D, a, kStreamSwiGlu, lin_ws, lin_b, hs));
     } else if (ffnm) {
         StreamArgs a{};
         a.seg[0] = Seg(w->w_gate, gate, F);
@@ -296,6 +353,11 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[0] = Seg(w->w_down, x, D, x);
         a.n_seg = 1;
         MLK_TRY(LinearRowStream(w->w_down.type, gate, F, a, kStreamAdd, hs));
+    } else if (downp) {
+        StreamArgs a{};
+        a.seg[0] = PlanarSeg(w->w_down, x, D, x);
+        a.n_seg = 1;
+        MLK_TRY(LinearPlanarFused(w->w_down.type, gate, T, F, a, kStreamAdd, lin_ws, lin_b, hs));
     } else if (downm) {
         StreamArgs a{};
         a.seg[0] = Seg(w->w_down, x, D, x);

@@ -160,11 +160,82 @@ struct QuantTile {
     }
 };
 
+// The same tile from the planar layout: thread tid takes inputs 16h ..
+// 16h + 15 (h = tid & 1) of block kb of row n0 + (tid >> 1), which lanes
+// 32h + r and 32h + 16 + r of the row's tile hold; the decoded values are
+// the block layout's (d * q, d * (code - 8)).
+template <int QT>
+struct PlanarTile {
+    uint32_t d;
+    uint32_t q[4];
+    uint32_t keep;
+    __device__ void Load(const uint8_t* w, int64_t O, int64_t K, int64_t n0, int64_t kb) {
+        const int64_t n = n0 + (threadIdx.x >> 1);
+        const int h = threadIdx.x & 1;
+        keep = n < O ? ~0u : 0u;
+        const int64_t row = n < O ? n : 0, rt = row / 16;
+        const int r = static_cast<int>(row % 16);
+        const int64_t tiles = (O + 15) / 16;
+        const int64_t code_tile = QT == MLK_Q8_0 ? 16 * K : 8 * K;
+        const uint8_t* scales = w + tiles * code_tile;
+        d = *reinterpret_cast<const uint16_t*>(scales + ((rt * (K / 256) + kb / 8) * 16 + r) * 16 +
+                                               (kb % 8) * 2);
+        if constexpr (QT == MLK_Q8_0) {
+            const uint8_t* c = w + rt * code_tile + ((kb / 2) * 64 + 32 * h + r) * 16 + (kb & 1) * 8;
+            const uint2 a = *reinterpret_cast<const uint2*>(c);
+            const uint2 b = *reinterpret_cast<const uint2*>(c + 16 * 16);
+            q[0] = a.x;
+            q[1] = a.y;
+            q[2] = b.x;
+            q[3] = b.y;
+        } else {
+            const uint8_t* c = w + rt * code_tile + ((kb / 4) * 64 + 32 * h + r) * 16 + (kb % 4) * 4;
+            q[0] = *reinterpret_cast<const uint32_t*>(c);
+            q[1] = *reinterpret_cast<const uint32_t*>(c + 16 * 16);
+        }
+    }
+    __device__ void Store(float* s) const {
+        const int h = threadIdx.x & 1;
+        float* dst = s + (threadIdx.x >> 1) * kLd + 16 * h;
+        const float sc = HalfHw(d);
+        float e[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int32_t code;
+            if constexpr (QT == MLK_Q8_0) {
+                code = static_cast<int32_t>(q[i / 4] << (24 - 8 * (i % 4))) >> 24;
+            } else {  // input 8g + e: nibble e (low half of byte e, then high)
+                const int e8 = i % 8;
+                const int sh = e8 < 4 ? 8 * e8 : 8 * (e8 - 4) + 4;
+                code = static_cast<int32_t>(q[i / 8] << (28 - sh)) >> 28;
+            }
+            e[i] = sc * static_cast<float>(code);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            *reinterpret_cast<float4*>(dst + 4 * i) =
+                Mask4(make_float4(e[4 * i], e[4 * i + 1], e[4 * i + 2], e[4 * i + 3]), keep);
+        }
+    }
+};
+
 template <int WT>
 struct WTile : QuantTile<WT> {
     __device__ void Load(const uint8_t* w, int64_t O, int64_t, int64_t row_bytes, int64_t n0,
                          int64_t k0) {
         QuantTile<WT>::Load(w, O, row_bytes, n0, k0 / kBK);
+    }
+};
+template <>
+struct WTile<kWPlanarQ8> : PlanarTile<MLK_Q8_0> {
+    __device__ void Load(const uint8_t* w, int64_t O, int64_t K, int64_t, int64_t n0, int64_t k0) {
+        PlanarTile<MLK_Q8_0>::Load(w, O, K, n0, k0 / kBK);
+    }
+};
+template <>
+struct WTile<kWPlanarQ4> : PlanarTile<MLK_Q4_0> {
+    __device__ void Load(const uint8_t* w, int64_t O, int64_t K, int64_t, int64_t n0, int64_t k0) {
+        PlanarTile<MLK_Q4_0>::Load(w, O, K, n0, k0 / kBK);
     }
 };
 template <>
@@ -303,6 +374,22 @@ __global__ __launch_bounds__(kGemmThreads) void GemmMfma(const float* __restrict
     }
 }
 
+// p[0] + p[stride] + ... + p[(splits - 1) * stride], added in that order;
+// the loads go out 8 at a time (a rolled loop would wait for each one).
+__device__ inline float SumSplits(const float* p, int splits, int64_t stride) {
+    float v = p[0];
+    int sp = 1;
+    for (; sp + 8 <= splits; sp += 8) {
+        float t[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = p[(sp + j) * stride];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v += t[j];
+    }
+    for (; sp < splits; ++sp) v += p[sp * stride];
+    return v;
+}
+
 // y = sum of the splits' partial sums, in split order, + bias.
 __global__ __launch_bounds__(kGemmThreads) void SplitKReduce(const float* __restrict__ partial,
                                                              int splits,
@@ -312,8 +399,7 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduce(const float* __rest
     const int64_t n = T * O;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        float v = partial[i];
-        for (int sp = 1; sp < splits; ++sp) v += partial[sp * n + i];
+        const float v = SumSplits(partial + i, splits, n);
         y[i] = bias != nullptr ? v + bias[i % O] : v;
     }
 }
@@ -577,6 +663,272 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
     }
 }
 
+// ------------------------------------------------------- planar weights, bf16 products
+// Q8_0 and Q4_0 weights on the bf16 matrix cores, with every product exact.
+// A code (q, or a Q4_0 code minus 8) is a small integer, exact in bf16, and
+// an fp32 x is the exact sum of three bf16 pieces: xh = x with its low 16
+// bits cleared, xm = the same of x - xh, xl = x - xh - xm (at most 8
+// significant bits left).  So each q * piece is exact in fp32, three
+// v_mfma_f32_16x16x32_bf16 (one per piece) give one block's
+// S = sum_i q_i x_i with fp32 summation only, and the block scale follows:
+// acc += d * S.  That is the reference's sum_k x_k * (d q_k) (d q is exact
+// in fp32) up to fp32 summation error, the bound every kernel here meets.
+// A bf16 instruction does 8x the work of an fp32 one in half the cycles,
+// so the matrix cores stop being the limit of the few-token projections.
+//
+// The weights come in the planar layout (mlk_quant_to_planar, below), in
+// which a wave's 16-byte loads of one row tile are 1 KB contiguous and each
+// lane's bytes are its MFMA operand: lane l = 16 g + r of row tile rt takes
+// row 16 rt + r and inputs 8g .. 8g + 7 of every block (A and B share the
+// assignment, so each product is formed once).  SplitXBf writes x once as
+// three bf16 planes per block, [piece][token][32 inputs].
+// GemmPlanar: workgroup = 4 waves = 128 output rows (wave: two 16-row
+// tiles) x T tokens (16 per tile) x one K range of 2 * NP blocks; the
+// ranges' partial sums are added by the split-K reductions, as
+// GemmSkinny's.  Every weight load of the range is issued first, the
+// range's x planes (token rows < T) are copied to LDS, and after one
+// barrier the waves run on their own.  Operands: x is A (lane l: token
+// l % 16), the weights are B, so the C registers of lane l are tokens
+// 4(l / 16) + r of the lane's own row, whose scale it holds.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPlTiles = 2;                  // 16-row weight tiles per wave
+constexpr int kPlRows = 4 * 16 * kPlTiles;   // output rows per workgroup
+
+// Two floats whose values are exact in bf16, as one dword of bf16 (a low).
+__device__ inline uint32_t PackBf(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
+// v = p[0] + p[1] + p[2] exactly, each p[i] exact in bf16.  Inf and NaN
+// go whole into p[0] (NaN as the quiet NaN, whose payload bit survives in
+// bf16), so a product with them is what the fp32 product would be.
+__device__ inline void SplitBf(float v, float (&p)[3]) {
+    if (!__builtin_isfinite(v)) {
+        p[0] = v != v ? __builtin_nanf("") : v;
+        p[1] = p[2] = 0.0f;
+        return;
+    }
+    p[0] = __uint_as_float(__float_as_uint(v) & 0xFFFF0000u);
+    const float r = v - p[0];  // exact: the low 16 bits of v's significand
+    p[1] = __uint_as_float(__float_as_uint(r) & 0xFFFF0000u);
+    p[2] = r - p[1];           // exact, at most 8 significant bits
+}
+
+// Bytes 2j, 2j + 1 of v as signed integers in bf16, in one dword.
+__device__ inline uint32_t BytesBf(uint32_t v, int j) {
+    return PackBf(static_cast<float>(static_cast<int8_t>(v >> (16 * j))),
+                  static_cast<float>(static_cast<int8_t>(v >> (16 * j + 8))));
+}
+
+// The x planes of tokens t < T: one thread per (block, token, input pair).
+__global__ __launch_bounds__(kGemmThreads) void SplitXBf(const float* __restrict__ x, int64_t T,
+                                                         int64_t K, int tokens,
+                                                         uint32_t* __restrict__ planes) {
+    const int64_t n = (K / 32) * T * 16;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int sp = static_cast<int>(i % 16);
+        const int64_t t = (i / 16) % T;
+        const int64_t b = i / (16 * T);
+        const float* src = x + t * K + 32 * b + 2 * sp;
+        float p0[3], p1[3];
+        SplitBf(src[0], p0);
+        SplitBf(src[1], p1);
+#pragma unroll
+        for (int p = 0; p < 3; ++p) planes[((b * 3 + p) * tokens + t) * 16 + sp] = PackBf(p0[p], p1[p]);
+    }
+}
+
+template <int QT, int TT, int NP>
+__global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restrict__ planes,
+                                                         SkinnyArgs a, int64_t T, int64_t K,
+                                                         float* __restrict__ partial) {
+    constexpr int kTok = 16 * TT;
+    constexpr int kBlockWords = 3 * kTok * 16;  // one block's x planes
+    constexpr int kCodeVecs = QT == MLK_Q8_0 ? NP : NP / 2;  // 16-byte code loads per tile
+    __shared__ __align__(16) uint32_t xs[2 * NP * kBlockWords];
+    const int rgall = static_cast<int>(blockIdx.x) % a.row_groups;
+    const int sp = static_cast<int>(blockIdx.x) / a.row_groups;
+    const int seg = (a.n_seg > 2 && rgall >= a.g0[2]) ? 2 : ((a.n_seg > 1 && rgall >= a.g0[1]) ? 1 : 0);
+    const int rg = rgall - (seg == 2 ? a.g0[2] : (seg == 1 ? a.g0[1] : 0));
+    const int64_t O = seg == 2 ? a.rows[2] : (seg == 1 ? a.rows[1] : a.rows[0]);
+    const uint8_t* w = seg == 2 ? a.w[2] : (seg == 1 ? a.w[1] : a.w[0]);
+    const int64_t col0 = seg == 2 ? a.col0[2] : (seg == 1 ? a.col0[1] : 0);
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int i16 = lane & 15, g = lane >> 4;
+    const int64_t tiles = (O + 15) / 16;
+    const int64_t tile0 = static_cast<int64_t>(rg) * (kPlRows / 16) + wave * kPlTiles;
+    const int64_t code_tile = QT == MLK_Q8_0 ? 16 * K : 8 * K;  // bytes per row tile
+    const uint8_t* scales = w + tiles * code_tile;
+
+    // every weight load of the range first (tiles past the last read it)
+    u32x4 cw[kPlTiles][kCodeVecs];
+    u32x4 sw[kPlTiles][NP / 4];
+#pragma unroll
+    for (int n = 0; n < kPlTiles; ++n) {
+        const int64_t tile = tile0 + n < tiles ? tile0 + n : tiles - 1;
+        const u32x4* c = reinterpret_cast<const u32x4*>(w + tile * code_tile) +
+                         static_cast<int64_t>(sp) * kCodeVecs * 64 + lane;
+#pragma unroll
+        for (int v = 0; v < kCodeVecs; ++v) cw[n][v] = __builtin_nontemporal_load(c + 64 * v);
+        const u32x4* sc = reinterpret_cast<const u32x4*>(scales + tile * (K / 32) * 32) +
+                          static_cast<int64_t>(sp) * (NP / 4) * 16 + i16;
+#pragma unroll
+        for (int v = 0; v < NP / 4; ++v) sw[n][v] = sc[16 * v];
+    }
+    // the range's x planes into LDS, (block, piece, token slot) rows of 16
+    // dwords: slots t < T copied (all loads before the stores), the rest zero
+    constexpr int kXIter = 2 * NP * 3 * kTok * 4 / kSkThreads;
+    static_assert(2 * NP * 3 * kTok * 4 % kSkThreads == 0, "whole copy rounds");
+    const u32x4* src = reinterpret_cast<const u32x4*>(planes) +
+                       static_cast<int64_t>(sp) * 2 * NP * 3 * T * 4;
+    u32x4 xv[kXIter];
+#pragma unroll
+    for (int k = 0; k < kXIter; ++k) {
+        const int i = static_cast<int>(threadIdx.x) + kSkThreads * k;
+        const int t = (i / 4) % kTok, bp = i / (4 * kTok);
+        xv[k] = u32x4{0u, 0u, 0u, 0u};
+        if (t < T) xv[k] = src[(bp * T + t) * 4 + i % 4];
+    }
+#pragma unroll
+    for (int k = 0; k < kXIter; ++k) {
+        reinterpret_cast<u32x4*>(xs)[static_cast<int>(threadIdx.x) + kSkThreads * k] = xv[k];
+    }
+    __syncthreads();
+
+    f32x4 acc[kPlTiles][TT];
+#pragma unroll
+    for (int n = 0; n < kPlTiles; ++n) {
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) acc[n][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int b = 0; b < 2 * NP; ++b) {
+        bf16x8 xa[TT][3];
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                xa[tt][p] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                    xs + ((b * 3 + p) * kTok + tt * 16 + i16) * 16 + 4 * g));
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < kPlTiles; ++n) {
+            u32x4 q;
+            float d;
+            const uint32_t sv = sw[n][b / 8][(b % 8) / 2];
+            const uint32_t h16 = (b & 1) ? sv >> 16 : sv & 0xFFFFu;
+            if constexpr (QT == MLK_Q8_0) {
+                const uint32_t lo = (b & 1) ? cw[n][b / 2][2] : cw[n][b / 2][0];
+                const uint32_t hi = (b & 1) ? cw[n][b / 2][3] : cw[n][b / 2][1];
+                q = u32x4{BytesBf(lo, 0), BytesBf(lo, 1), BytesBf(hi, 0), BytesBf(hi, 1)};
+                d = HalfHw(h16);
+            } else {
+                // nibbles (code - 8, two's complement) moved to the high half
+                // of each byte: signed bytes of 16 (code - 8), scale d / 16
+                const uint32_t v = cw[n][b / 4][b % 4];
+                const uint32_t lo = (v << 4) & 0xF0F0F0F0u, hi = v & 0xF0F0F0F0u;
+                q = u32x4{BytesBf(lo, 0), BytesBf(lo, 1), BytesBf(hi, 0), BytesBf(hi, 1)};
+                d = HalfHw(h16) * 0.0625f;
+            }
+            const bf16x8 wb = __builtin_bit_cast(bf16x8, q);
+#pragma unroll
+            for (int tt = 0; tt < TT; ++tt) {
+                f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][0], wb,
+                                                                  f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][1], wb, s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][2], wb, s, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[n][tt][r] = __builtin_fmaf(d, s[r], acc[n][tt][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < kPlTiles; ++n) {
+        const int64_t row = 16 * (tile0 + n) + i16;
+        if (row >= O) continue;
+        float* out = partial != nullptr ? partial + sp * T * a.cols + col0 + row : a.y + row;
+        const int64_t stride = partial != nullptr ? a.cols : O;
+        const float bias = partial == nullptr && a.bias != nullptr ? a.bias[row] : 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t t = tt * 16 + 4 * g + r;
+                if (t < T) out[t * stride] = acc[n][tt][r] + bias;
+            }
+        }
+    }
+}
+
+// Block layout -> planar layout (described at mlk_quant_to_planar): one
+// thread per 16 code bytes of a lane (a block pair of Q8_0, a block quad of
+// Q4_0), then one per row's 8 scales.  Rows past O get zero codes and scales.
+template <int QT>
+__global__ __launch_bounds__(kGemmThreads) void ToPlanar(const uint8_t* __restrict__ blocks,
+                                                         int64_t O, int64_t K,
+                                                         uint8_t* __restrict__ out) {
+    constexpr int kBB = QT == MLK_Q8_0 ? 34 : 18;
+    constexpr int kPer = QT == MLK_Q8_0 ? 2 : 4;  // blocks per 16-byte lane vector
+    const int64_t tiles = (O + 15) / 16, nb = K / 32, row_bytes = nb * kBB;
+    const int64_t code_vecs = tiles * (nb / kPer) * 64;
+    const int64_t n = code_vecs + tiles * (nb / 8) * 16;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        if (i < code_vecs) {
+            const int lane = static_cast<int>(i % 64), g = lane >> 4;
+            const int64_t v = (i / 64) % (nb / kPer), tile = i / (64 * (nb / kPer));
+            const int64_t row = 16 * tile + (lane & 15);
+            uint8_t bytes[16];
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const uint8_t* blk = blocks + row * row_bytes + (kPer * v + j) * kBB + 2;
+#pragma unroll
+                for (int e = 0; e < 16 / kPer; ++e) {
+                    uint8_t b = 0;
+                    if (row < O) {
+                        if constexpr (QT == MLK_Q8_0) {
+                            b = blk[8 * g + e];
+                        } else {  // input 8g + e (low nibble) and 8g + e + 4 (high), as code ^ 8
+                            const int c0 = 8 * g + e, c1 = c0 + 4;
+                            const uint32_t n0 = c0 < 16 ? blk[c0] & 15u : blk[c0 - 16] >> 4;
+                            const uint32_t n1 = c1 < 16 ? blk[c1] & 15u : blk[c1 - 16] >> 4;
+                            b = static_cast<uint8_t>((n0 ^ 8u) | ((n1 ^ 8u) << 4));
+                        }
+                    }
+                    bytes[(16 / kPer) * j + e] = b;
+                }
+            }
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                o[k] = bytes[4 * k] | (bytes[4 * k + 1] << 8) | (bytes[4 * k + 2] << 16) |
+                       (static_cast<uint32_t>(bytes[4 * k + 3]) << 24);
+            }
+            reinterpret_cast<u32x4*>(out)[i] = o;
+        } else {
+            const int64_t j = i - code_vecs;
+            const int r = static_cast<int>(j % 16);
+            const int64_t grp = (j / 16) % (nb / 8), tile = j / (16 * (nb / 8));
+            const int64_t row = 16 * tile + r;
+            uint32_t h[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint8_t* blk = blocks + row * row_bytes + (8 * grp + e) * kBB;
+                h[e] = row < O ? blk[0] | (static_cast<uint32_t>(blk[1]) << 8) : 0u;
+            }
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = h[2 * k] | (h[2 * k + 1] << 16);
+            const int64_t code_bytes = tiles * (QT == MLK_Q8_0 ? 16 : 8) * K;
+            reinterpret_cast<u32x4*>(out + code_bytes)[j] = o;
+        }
+    }
+}
+
 // The reduction of a fused skinny launch: each output's partial sums added in
 // chunk order (as SplitKReduce), then (+ bias) and the mode's epilogue:
 // plain y_s = v; add y_s = res_s + v; SwiGLU y_1 = SwiGlu(gate, up) with
@@ -589,12 +941,7 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int64_t t = i / out_cols, c = i % out_cols;
-        auto sum = [&](int64_t col) {
-            const float* pp = partial + t * cols + col;
-            float v = pp[0];
-            for (int sp = 1; sp < splits; ++sp) v += pp[sp * stride];
-            return v;
-        };
+        auto sum = [&](int64_t col) { return SumSplits(partial + t * cols + col, splits, stride); };
         if (mode == kStreamSwiGlu) {
             const int64_t F = a.seg[0].rows;
             float g = sum(c), u = sum(F + c);
@@ -671,7 +1018,7 @@ SplitPlan PlanSkinny(int wt, int64_t T, int64_t K) {
 // Where the skinny kernel measured faster than the tiled one on the 8B
 // layer's projections: the quantized types up to 32 rows (F32 stays tiled).
 bool SkinnyApplies(int wt, int64_t T, int64_t K) {
-    const bool rows = wt != kWF32 && T <= 32;
+    const bool rows = wt >= MLK_Q8_0 && wt <= MLK_Q4_1 && T <= 32;
     return rows && K % SkinnyChunk(wt) == 0 && K / SkinnyChunk(wt) <= 4096;
 }
 
@@ -736,6 +1083,14 @@ void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t
             break;
         case MLK_Q4_1:
             hipLaunchKernelGGL((GemmMfma<MLK_Q4_1, BM>), grid, dim3(kGemmThreads), 0, s, x, w,
+                               bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        case kWPlanarQ8:
+            hipLaunchKernelGGL((GemmMfma<kWPlanarQ8, BM>), grid, dim3(kGemmThreads), 0, s, x, w,
+                               bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        case kWPlanarQ4:
+            hipLaunchKernelGGL((GemmMfma<kWPlanarQ4, BM>), grid, dim3(kGemmThreads), 0, s, x, w,
                                bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
             break;
         default:
@@ -879,6 +1234,174 @@ mlk_status LinearSkinnyFused(int wt, const float* x, int64_t T, int64_t K, const
     hipLaunchKernelGGL(SplitKReduceFused, dim3(GridFor(T * out_cols, kGemmThreads, 8)),
                        dim3(kGemmThreads), 0, s, partial, plan.splits, T, cols, sa, mode,
                        out_cols);
+    return CheckLaunch("SplitKReduceFused");
+}
+
+// ------------------------------------------------------- planar launches
+int64_t PlanarBytes(int qt, int64_t O, int64_t K) {
+    if ((qt != MLK_Q8_0 && qt != MLK_Q4_0) || O <= 0 || K <= 0 || K % 256 != 0) return 0;
+    const int64_t tiles = (O + 15) / 16;
+    return tiles * (qt == MLK_Q8_0 ? 16 : 8) * K + tiles * (K / 32) * 32;
+}
+
+mlk_status LaunchToPlanar(int qt, const void* blocks, int64_t O, int64_t K, void* planar,
+                          hipStream_t s) {
+    const int64_t tiles = (O + 15) / 16, nb = K / 32;
+    const int64_t n = tiles * (nb / (qt == MLK_Q8_0 ? 2 : 4)) * 64 + tiles * (nb / 8) * 16;
+    const dim3 grid(GridFor(n, kGemmThreads, 8));
+    const uint8_t* b = static_cast<const uint8_t*>(blocks);
+    uint8_t* o = static_cast<uint8_t*>(planar);
+    if (qt == MLK_Q8_0) {
+        hipLaunchKernelGGL(ToPlanar<MLK_Q8_0>, grid, dim3(kGemmThreads), 0, s, b, O, K, o);
+    } else {
+        hipLaunchKernelGGL(ToPlanar<MLK_Q4_0>, grid, dim3(kGemmThreads), 0, s, b, O, K, o);
+    }
+    return CheckLaunch("ToPlanar");
+}
+
+namespace {
+
+// GemmPlanar's plan: token tiles, block pairs per K range, ranges (splits),
+// and the workspace: partial sums (splits > 1, or always with `partials`: a
+// fused launch's reduction applies its epilogue), then the x planes.
+struct PlanarPlan {
+    int tt = 1, np = 4, splits = 1;
+    int64_t partial_bytes = 0, plane_bytes = 0;
+    int64_t Bytes() const { return partial_bytes + plane_bytes; }
+};
+
+PlanarPlan PlanPlanar(int64_t T, int64_t K, int64_t cols, bool partials) {
+    PlanarPlan p;
+    p.tt = T <= 16 ? 1 : 2;
+    p.np = p.tt == 1 && K % 512 == 0 ? 8 : 4;
+    p.splits = static_cast<int>(K / (64 * p.np));
+    p.partial_bytes = p.splits > 1 || partials
+                          ? (static_cast<int64_t>(p.splits) * T * cols * 4 + 255) / 256 * 256
+                          : 0;
+    p.plane_bytes = (K / 32) * 3 * T * 64;
+    return p;
+}
+
+template <int QT>
+void LaunchPlanarT(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t* planes,
+                   const SkinnyArgs& a, int64_t T, int64_t K, float* partial) {
+    if (p.tt == 1 && p.np == 8) {
+        hipLaunchKernelGGL((GemmPlanar<QT, 1, 8>), grid, dim3(kSkThreads), 0, s, planes, a, T, K,
+                           partial);
+    } else if (p.tt == 1) {
+        hipLaunchKernelGGL((GemmPlanar<QT, 1, 4>), grid, dim3(kSkThreads), 0, s, planes, a, T, K,
+                           partial);
+    } else {
+        hipLaunchKernelGGL((GemmPlanar<QT, 2, 4>), grid, dim3(kSkThreads), 0, s, planes, a, T, K,
+                           partial);
+    }
+}
+
+// x split into planes (after the partial sums in the workspace), then
+// GemmPlanar over the segments' row groups x the plan's ranges.  a.w,
+// a.rows, a.n_seg set; the rest filled in here.  The caller reduces.
+mlk_status RunPlanar(int qt, const float* x, SkinnyArgs& a, int64_t T, int64_t K,
+                     bool partials, void* workspace, size_t workspace_bytes, int* splits,
+                     float** partial, hipStream_t s) {
+    int64_t cols = 0, groups = 0;
+    for (int i = 0; i < a.n_seg; ++i) {
+        if (!Aligned(a.w[i], 16)) return Fail(MLK_ERR_INVALID, "linear (planar): weights not 16-byte aligned");
+        a.col0[i] = cols;
+        a.g0[i] = static_cast<int>(groups);
+        cols += a.rows[i];
+        groups += (a.rows[i] + kPlRows - 1) / kPlRows;
+    }
+    const PlanarPlan p = PlanPlanar(T, K, cols, partials);
+    if (workspace == nullptr || !Aligned(workspace, 16) ||
+        static_cast<int64_t>(workspace_bytes) < p.Bytes()) {
+        return Fail(MLK_ERR_INVALID, "linear (planar): workspace of %lld bytes needed",
+                    static_cast<long long>(p.Bytes()));
+    }
+    if (groups * p.splits > 0x7FFFFFFF) {
+        return Fail(MLK_ERR_INVALID, "linear (planar): %lld output rows exceed one launch",
+                    static_cast<long long>(cols));
+    }
+    a.row_groups = static_cast<int>(groups);
+    a.cols = cols;
+    *splits = p.splits;
+    *partial = p.partial_bytes > 0 ? static_cast<float*>(workspace) : nullptr;
+    uint32_t* planes = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + p.partial_bytes);
+    hipLaunchKernelGGL(SplitXBf, dim3(GridFor((K / 32) * T * 16, kGemmThreads, 4)),
+                       dim3(kGemmThreads), 0, s, x, T, K, static_cast<int>(T), planes);
+    mlk_status st = CheckLaunch("SplitXBf");
+    if (st != MLK_OK) return st;
+    const dim3 grid(static_cast<unsigned>(groups * p.splits));
+    if (qt == MLK_Q8_0) {
+        LaunchPlanarT<MLK_Q8_0>(p, grid, s, planes, a, T, K, *partial);
+    } else {
+        LaunchPlanarT<MLK_Q4_0>(p, grid, s, planes, a, T, K, *partial);
+    }
+    return CheckLaunch("GemmPlanar");
+}
+
+}  // namespace
+
+bool PlanarApplies(int qt, int64_t T, int64_t K) {
+    return (qt == MLK_Q8_0 || qt == MLK_Q4_0) && T >= 1 && T <= 32 && K % 256 == 0;
+}
+
+int64_t PlanarWorkspaceBytes(int64_t T, int64_t K, int64_t cols, bool partials) {
+    return PlanPlanar(T, K, cols, partials).Bytes();
+}
+
+mlk_status LinearPlanar(int qt, const float* x, const void* w, const float* bias, float* y,
+                        int64_t T, int64_t K, int64_t O, void* workspace, size_t workspace_bytes,
+                        hipStream_t s) {
+    if (!PlanarApplies(qt, T, K)) {  // many rows: the tiled GEMM on the planar tiles
+        return LaunchGemm(qt == MLK_Q8_0 ? kWPlanarQ8 : kWPlanarQ4, x, w, bias, y, T, K, O, 0,
+                          workspace, workspace_bytes, s);
+    }
+    SkinnyArgs a{};
+    a.w[0] = static_cast<const uint8_t*>(w);
+    a.rows[0] = O;
+    a.n_seg = 1;
+    a.bias = bias;
+    a.y = y;
+    int splits = 1;
+    float* partial = nullptr;
+    mlk_status st = RunPlanar(qt, x, a, T, K, false, workspace, workspace_bytes, &splits,
+                              &partial, s);
+    if (st != MLK_OK || partial == nullptr) return st;
+    hipLaunchKernelGGL(SplitKReduce, dim3(GridFor(T * O, kGemmThreads, 8)), dim3(kGemmThreads), 0,
+                       s, partial, splits, bias, y, T, O);
+    return CheckLaunch("SplitKReduce");
+}
+
+mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const StreamArgs& sa,
+                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s) {
+    if (!PlanarApplies(qt, T, K) || sa.n_seg < 1 || sa.n_seg > 3 || !Aligned(x, 16) ||
+        (mode == kStreamSwiGlu && (sa.n_seg != 2 || sa.seg[0].rows != sa.seg[1].rows)) ||
+        (mode == kStreamQkvRope && !QkvRopeArgsOk(sa))) {
+        return Fail(MLK_ERR_INVALID, "linear (planar, fused rows): unsupported shape");
+    }
+    SkinnyArgs a{};
+    for (int i = 0; i < sa.n_seg; ++i) {
+        const StreamSeg& g = sa.seg[i];
+        if (g.w == nullptr || g.y == nullptr || g.rows <= 0 ||
+            (mode == kStreamAdd && g.res == nullptr)) {
+            return Fail(MLK_ERR_INVALID, "linear (planar, fused rows): bad segment %d", i);
+        }
+        a.w[i] = g.w;
+        a.rows[i] = g.rows;
+    }
+    a.n_seg = sa.n_seg;
+    int splits = 1;
+    float* partial = nullptr;
+    mlk_status st = RunPlanar(qt, x, a, T, K, true, workspace, workspace_bytes, &splits,
+                              &partial, s);
+    if (st != MLK_OK) return st;
+    const int64_t cols = a.cols;
+    const int64_t out_cols = mode == kStreamSwiGlu    ? sa.seg[0].rows
+                             : mode == kStreamQkvRope ? (sa.seg[0].rows + sa.seg[1].rows) / 2 +
+                                                            sa.seg[2].rows
+                                                      : cols;
+    hipLaunchKernelGGL(SplitKReduceFused, dim3(GridFor(T * out_cols, kGemmThreads, 8)),
+                       dim3(kGemmThreads), 0, s, partial, splits, T, cols, sa, mode, out_cols);
     return CheckLaunch("SplitKReduceFused");
 }
 

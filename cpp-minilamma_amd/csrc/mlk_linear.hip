@@ -1101,4 +1101,54 @@ mlk_status mlk_matmul_f32(const float* a, const float* b, float* c, int64_t m, i
     return CheckLaunch("MatmulKernel");
 }
 
+int64_t mlk_quant_planar_bytes(int32_t quant_type, int64_t rows, int64_t cols) {
+    return PlanarBytes(quant_type, rows, cols);
+}
+
+mlk_status mlk_quant_to_planar(int32_t quant_type, const void* blocks, int64_t rows,
+                               int64_t cols, void* planar, void* stream) {
+    if (PlanarBytes(quant_type, rows, cols) == 0) {
+        return Fail(MLK_ERR_INVALID,
+                    "mlk_quant_to_planar: no planar layout for type %d, %lld x %lld (Q8_0 or "
+                    "Q4_0, cols a positive multiple of 256)",
+                    quant_type, static_cast<long long>(rows), static_cast<long long>(cols));
+    }
+    if (blocks == nullptr || planar == nullptr) {
+        return Fail(MLK_ERR_INVALID, "mlk_quant_to_planar: null pointer");
+    }
+    if (!Aligned(planar, 16)) {
+        return Fail(MLK_ERR_INVALID, "mlk_quant_to_planar: the planar buffer must be 16-byte aligned");
+    }
+    return LaunchToPlanar(quant_type, blocks, rows, cols, planar, AsStream(stream));
+}
+
+int64_t mlk_linear_planar_workspace_bytes(int64_t rows, int64_t in_features,
+                                          int64_t out_features) {
+    if (rows <= 0 || in_features <= 0 || out_features <= 0 || in_features % 256 != 0) return 0;
+    if (!PlanarApplies(MLK_Q8_0, rows, in_features)) {
+        return GemmWorkspaceBytes(kWPlanarQ8, rows, in_features, out_features);
+    }
+    return PlanarWorkspaceBytes(rows, in_features, out_features, false);
+}
+
+mlk_status mlk_linear_planar(int32_t quant_type, const float* x, const void* w_planar,
+                             const float* bias, float* y, int64_t rows, int64_t in_features,
+                             int64_t out_features, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+    if (quant_type != MLK_Q8_0 && quant_type != MLK_Q4_0) {
+        return Fail(MLK_ERR_INVALID, "mlk_linear_planar: type %d has no planar layout",
+                    quant_type);
+    }
+    mlk_status st = CheckLinear("mlk_linear_planar", x, w_planar, y, rows, in_features,
+                                out_features);
+    if (st != MLK_OK) return st;
+    if (in_features % 256 != 0 || !Aligned(w_planar, 16) || !Aligned(x, 16)) {
+        return Fail(MLK_ERR_INVALID,
+                    "mlk_linear_planar: in_features must be a multiple of 256, the weights and x "
+                    "16-byte aligned");
+    }
+    return LinearPlanar(quant_type, x, w_planar, bias, y, rows, in_features, out_features,
+                        workspace, workspace_bytes, AsStream(stream));
+}
+
 }  // extern "C"

@@ -52,11 +52,14 @@ struct __align__(16) PrefillSmem {
 };
 
 // The next K and V tiles in registers: thread tid holds float4 tid + 256 i
-// of the [32][HD] tiles (positions past max_pos read max_pos's row).
+// of the [32][HD] tiles (positions past max_pos read max_pos's row).  The
+// registers are native 4-vectors: with HIP's float4 struct, each copy is an
+// aggregate memcpy, and the optimizer fuses load and LDS store into one
+// global-to-LDS copy at the store, so the prefetch would not happen.
 template <int HD>
 struct KvTile {
     static constexpr int NL = kPfTile * HD / 4 / kPfThreads;
-    float4 k[NL], v[NL];
+    f32x4 k[NL], v[NL];  // vectors, not float4 structs (see Load)
     const float* kb;
     const float* vb;
     int64_t slot, max_pos;
@@ -67,8 +70,8 @@ struct KvTile {
             const int64_t p = p0 + idx / (HD / 4);
             const int64_t pos = p <= max_pos ? p : max_pos;
             const int c4 = idx % (HD / 4);
-            k[i] = *reinterpret_cast<const float4*>(kb + pos * slot + 4 * c4);
-            v[i] = *reinterpret_cast<const float4*>(vb + pos * slot + 4 * c4);
+            k[i] = *reinterpret_cast<const f32x4*>(kb + pos * slot + 4 * c4);
+            v[i] = *reinterpret_cast<const f32x4*>(vb + pos * slot + 4 * c4);
         }
     }
     __device__ void Store(float* ks, float* vs) const {
@@ -76,8 +79,8 @@ struct KvTile {
         for (int i = 0; i < NL; ++i) {
             const int idx = static_cast<int>(threadIdx.x) + kPfThreads * i;
             const int o = (idx / (HD / 4)) * (HD + 4) + 4 * (idx % (HD / 4));
-            *reinterpret_cast<float4*>(ks + o) = k[i];
-            *reinterpret_cast<float4*>(vs + o) = v[i];
+            *reinterpret_cast<f32x4*>(ks + o) = k[i];
+            *reinterpret_cast<f32x4*>(vs + o) = v[i];
         }
     }
 };
@@ -180,6 +183,10 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
         const int buf = static_cast<int>(it & 1);
         const int64_t p0 = p_begin + it * kPfTile;
         load(p_begin + (it + 1 < n_tiles ? it + 1 : it) * kPfTile);
+        // Nothing crosses this point: without it the scheduler sinks the
+        // next tile's global loads to their LDS stores at the bottom of the
+        // loop, and every tile then waits out a full HBM round trip.
+        __builtin_amdgcn_sched_barrier(0);
         {  // idle waves (a head block past the group) compute too, unstored
             f32x4 s[2];
 #pragma unroll

@@ -135,4 +135,23 @@ mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, 
                       size_t workspace_bytes, hipStream_t s);
 int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O);
 
+// Planar Q8_0 / Q4_0 weights (layout at mlk_quant_to_planar, minilamma_hip.h;
+// mlk_gemm.hip).  wt values of LaunchGemm for them:
+constexpr int kWPlanarQ8 = 16, kWPlanarQ4 = 17;
+// bytes of the layout (0: unsupported shape) and the repack
+int64_t PlanarBytes(int qt, int64_t O, int64_t K);
+mlk_status LaunchToPlanar(int qt, const void* blocks, int64_t O, int64_t K, void* planar,
+                          hipStream_t s);
+// Up to 32 token rows on the bf16 matrix cores: one matrix, or up to three
+// with the same K fused as LinearSkinnyFused (modes and epilogues alike).
+// The workspace (16-byte aligned) holds PlanarWorkspaceBytes(T, K, rows of
+// all segments, fused) bytes: partial sums, then x split into bf16 planes.
+bool PlanarApplies(int qt, int64_t T, int64_t K);
+int64_t PlanarWorkspaceBytes(int64_t T, int64_t K, int64_t cols, bool fused);
+mlk_status LinearPlanar(int qt, const float* x, const void* w, const float* bias, float* y,
+                        int64_t T, int64_t K, int64_t O, void* workspace, size_t workspace_bytes,
+                        hipStream_t s);
+mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const StreamArgs& a,
+                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s);
+
 }  // namespace mlk

@@ -108,7 +108,7 @@ const char* mlk_status_string(int status) {
     }
 }
 
-int mlk_abi_version(void) { return 1; }
+int mlk_abi_version(void) { return 2; }
 
 mlk_status mlk_device_count(int* count) {
     if (count == nullptr) return Fail(MLK_ERR_INVALID, "mlk_device_count: null output");

@@ -26,8 +26,8 @@ import ctypes as C
 
 import numpy as np
 
-from . import (QUANT, DeviceBuffer, check, gather_f32, gather_quant, lib, linear_f32,
-               linear_quant, rmsnorm)
+from . import (DeviceBuffer, QUANT, check, gather_f32, gather_quant, lib, linear_f32,
+               linear_quant, quant_planar_bytes, quant_to_planar, rmsnorm)
 
 _i32, _i64, _vp = C.c_int32, C.c_int64, C.c_void_p
 WEIGHT_F32 = -1
@@ -43,7 +43,7 @@ class LayerConfig(C.Structure):
 
 class LinearWeight(C.Structure):
     """mlk_linear_weight."""
-    _fields_ = [("type", _i32), ("data", _vp), ("bias", _vp)]
+    _fields_ = [("type", _i32), ("data", _vp), ("bias", _vp), ("planar", _vp)]
 
 
 class LayerWeights(C.Structure):
@@ -92,9 +92,12 @@ class DeviceModel:
     Context does: a prompt chunk, then more chunks or single decode tokens
     at later positions."""
 
-    def __init__(self, model):
+    def __init__(self, model, planar=False):
+        """planar: also keep Q8_0 / Q4_0 weights (in_features a multiple of
+        256) in the planar layout, which batches of 2..32 tokens run on."""
         c = self.config = dict(model["config"])
         self._keep = []
+        self._planar = planar
         if "embedding_q" in model:
             qt, blocks = model["embedding_q"]
             self.embedding = (qt, self._up(np.ascontiguousarray(blocks, np.uint8)))
@@ -106,9 +109,13 @@ class DeviceModel:
             w = LayerWeights()
             w.attention_norm = self._up(lw["attention_norm"]).ptr
             w.ffn_norm = self._up(lw["ffn_norm"]).ptr
+            QD, KD = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+            shapes = {"wq": (QD, c["dim"]), "wk": (KD, c["dim"]), "wv": (KD, c["dim"]),
+                      "wo": (c["dim"], QD), "w_gate": (c["hidden_dim"], c["dim"]),
+                      "w_up": (c["hidden_dim"], c["dim"]), "w_down": (c["dim"], c["hidden_dim"])}
             for name in LINEAR_NAMES:
                 setattr(w, name, self._linear(lw[name], lw.get("b" + name[1]) if name in
-                                              ("wq", "wk", "wv") else None))
+                                              ("wq", "wk", "wv") else None, shapes[name]))
             self.layers.append(w)
         self.final_norm = self._up(model["final_norm"])
         kind, data = model["lm_head"]
@@ -128,13 +135,20 @@ class DeviceModel:
         self._keep.append(buf)
         return buf
 
-    def _linear(self, w, bias):
+    def _linear(self, w, bias, shape):
         kind, data = w
         lw = LinearWeight()
         lw.type = WEIGHT_F32 if kind == "f32" else QUANT[kind]
-        lw.data = self._up(np.asarray(data, np.float32) if kind == "f32" else
-                           np.asarray(data, np.uint8)).ptr
+        blocks = self._up(np.asarray(data, np.float32) if kind == "f32" else
+                          np.asarray(data, np.uint8))
+        lw.data = blocks.ptr
         lw.bias = None if bias is None else self._up(np.asarray(bias, np.float32)).ptr
+        n = quant_planar_bytes(kind, *shape) if self._planar and kind in ("q8_0", "q4_0") else 0
+        if n > 0:
+            planar = DeviceBuffer(n, np.uint8)
+            quant_to_planar(kind, blocks, shape[0], shape[1], planar)
+            self._keep.append(planar)
+            lw.planar = planar.ptr
         return lw
 
     def _workspace(self, n):

@@ -26,6 +26,7 @@ mlk_linear_weight ToC(const CudaLinearWeight& w, const char* name) {
     if (w.data == nullptr) Throw(std::string("weight ") + name + " is null");
     c.data = w.data;
     c.bias = w.bias;
+    c.planar = w.planar;
     return c;
 }
 

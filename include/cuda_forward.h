@@ -17,11 +17,14 @@
 namespace yan_lamma {
 
 // A device linear weight [out, in]: fp32 (kF32) or packed Q8_0 / Q4_0 /
-// Q4_1 blocks, borrowed; bias [out] (device) or null.
+// Q4_1 blocks, borrowed; bias [out] (device) or null; planar: null, or the
+// same Q8_0 / Q4_0 weight in the planar layout (mlk_quant_to_planar), which
+// calls of 2..32 tokens then use.
 struct CudaLinearWeight {
     QuantType type = QuantType::kF32;
     const void* data = nullptr;
     const float* bias = nullptr;
+    const void* planar = nullptr;
 };
 
 // The device weights of one layer (the reference's Layer, include/model.h).

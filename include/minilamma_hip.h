@@ -179,6 +179,42 @@ mlk_status mlk_linear_f32(const float* x, const float* w, const float* bias, flo
  * reference (cuBLAS keeps its own workspace). */
 int64_t mlk_linear_workspace_bytes(int64_t rows, int64_t in_features, int64_t out_features);
 
+/* Planar layout of Q8_0 / Q4_0 weights [out, in] (in % 256 == 0), made once
+ * at upload from the block layout by mlk_quant_to_planar.  The values are
+ * the blocks' (the same scale and codes per element); only their order
+ * differs, so that the few-token linear layers load each row tile's bytes
+ * 1 KB-contiguous per wave, already in matrix-core operand order:
+ *   codes: rows in tiles of 16 (the last tile padded with rows of zero
+ *     bytes, codes and scales alike); tile rt, lane l = 16 g + r (row
+ *     16 rt + r, inputs 8g .. 8g + 7 of each
+ *     block) holds 16 bytes per group of blocks: Q8_0 per block pair, bytes
+ *     0..7 the first block's codes, 8..15 the second's; Q4_0 per 4 blocks,
+ *     bytes 4j .. 4j + 3 block j, byte e holding input 8g + e in its low
+ *     nibble and 8g + e + 4 in its high one, each as (code - 8) in 4-bit
+ *     two's complement.  Order: [tile][group][lane][16 bytes];
+ *   scales: after the codes, [tile][in / 256][16 rows][8 blocks] fp16.
+ * No counterpart in the reference (its device weights keep the blocks,
+ * include/quantized_tensor.h:10-35); for callers that upload weights once
+ * and run few-token decode steps.  0: no planar layout for this shape (Q4_1,
+ * or in % 256 != 0). */
+int64_t mlk_quant_planar_bytes(int32_t quant_type, int64_t rows, int64_t cols);
+mlk_status mlk_quant_to_planar(int32_t quant_type, const void* blocks, int64_t rows,
+                               int64_t cols, void* planar, void* stream);
+
+/* y = x W^T (+ bias) with W in the planar layout (quant_type MLK_Q8_0 or
+ * MLK_Q4_0), the same sum bound as mlk_linear_quant.  Up to 32 rows run on
+ * the bf16 matrix cores with exact products (codes are exact in bf16 and x
+ * is split into three exact bf16 pieces), and need a workspace of
+ * mlk_linear_planar_workspace_bytes (16-byte aligned); more rows take the
+ * fp32 matrix-core GEMM, with the optional workspace of
+ * mlk_linear_workspace_bytes.  No counterpart in the reference. */
+mlk_status mlk_linear_planar(int32_t quant_type, const float* x, const void* w_planar,
+                             const float* bias, float* y, int64_t rows, int64_t in_features,
+                             int64_t out_features, void* workspace, size_t workspace_bytes,
+                             void* stream);
+int64_t mlk_linear_planar_workspace_bytes(int64_t rows, int64_t in_features,
+                                          int64_t out_features);
+
 /* c = a @ b for row-major a [m, k], b [k, n], c [m, n].  Replaces CudaMatmul
  * (include/cuda_matmul.h:7; src/cuda_matmul.cc:199-232). */
 mlk_status mlk_matmul_f32(const float* a, const float* b, float* c, int64_t m, int64_t k,
@@ -287,6 +323,9 @@ typedef struct {
     int32_t type;        /* MLK_WEIGHT_F32, MLK_Q8_0, MLK_Q4_0 or MLK_Q4_1 */
     const void* data;    /* [out, in]: fp32 row-major, or out rows of ceil(in / 32) blocks */
     const float* bias;   /* [out] or NULL */
+    const void* planar;  /* NULL, or the same Q8_0 / Q4_0 weight in the planar layout
+                            (mlk_quant_to_planar, 16-byte aligned): calls of 2..32 tokens
+                            then run on it.  No counterpart in the reference. */
 } mlk_linear_weight;
 
 /* A layer's device weights (the reference's Layer, include/model.h:41-55). */

@@ -262,3 +262,102 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
         # the rows of the other positions were written, the cache outside them kept
         kept = np.setdiff1d(np.arange(S), pv)
         np.testing.assert_array_equal(kc.download()[0, kept], kc0[0, kept])
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+@pytest.mark.parametrize("T", [2, 12, 24])
+@pytest.mark.parametrize("case", ["pos0", "positions", "bad_position", "neox"])
+def test_layer_planar_equals_op_by_op(mlk, fwd, wt, T, case):
+    """With planar copies of the weights, 2..32 tokens take the planar
+    launches: q/k/v in one (RoPE and the K/V cache rows in its reduction for
+    the normal layout), gate/up with SwiGLU, down adding into x, and wo.
+    Their per-element arithmetic is the separate entries' (mlk_linear_planar
+    per matrix, then the separate ops), so the layer equals that composition
+    bit for bit: residual stream, cache rows and error flag."""
+    S = 1024
+    cfg = dict(vocab=64, dim=512, hidden_dim=1536, layers=1, n_heads=8, n_kv_heads=2,
+               head_dim=64, max_seq=S, rope_type=1 if case == "neox" else 0, theta=10000.0,
+               eps=1e-5)
+    model = O.forward_model(cfg, seed=13, weight_type=wt, biases=True)
+    D, F, H, KV, hd = 512, 1536, 8, 2, 64
+    QD, KD, pos = H * hd, KV * hd, 600
+    lw = model["layers"][0]
+    dm = fwd.DeviceModel(model, planar=True)
+    rng = np.random.default_rng(7)
+    x0 = rng.standard_normal((T, D)).astype(np.float32)
+    kc0 = (rng.standard_normal((1, S, KV, hd)) * 0.5).astype(np.float32)
+    vc0 = rng.standard_normal((1, S, KV, hd)).astype(np.float32)
+    B = mlk.DeviceBuffer.from_array
+    positions = None
+    if case in ("positions", "bad_position"):
+        pv = np.sort(rng.choice(S, T, replace=False)).astype(np.int32)
+        if case == "bad_position":
+            pv[T // 2] = S
+        positions = B(pv)
+    contiguous = positions is None
+    flag, flag2 = B(np.zeros(1, np.int32)), B(np.zeros(1, np.int32))
+
+    x = B(x0)
+    kc, vc = B(kc0), B(vc0)
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, S, contiguous), np.uint8)
+    fwd.forward_layer_batch(cfg, dm.layers[0], x, T, kc, vc, 1, S, 0, S, ws, positions=positions,
+                            pos0=pos, err=flag)
+    got = x.download()
+
+    shapes = {"wq": (QD, D), "wk": (KD, D), "wv": (KD, D), "wo": (D, QD), "w_gate": (F, D),
+              "w_up": (F, D), "w_down": (D, F)}
+    pw = {}
+    for n, (o, i) in shapes.items():
+        blocks = B(np.ascontiguousarray(lw[n][1], np.uint8))
+        pw[n] = mlk.DeviceBuffer(mlk.quant_planar_bytes(wt, o, i), np.uint8)
+        mlk.quant_to_planar(wt, blocks, o, i, pw[n])
+    bias = {n: B(np.asarray(lw["b" + n[1]], np.float32)) for n in ("wq", "wk", "wv")}
+    an = B(np.asarray(lw["attention_norm"], np.float32))
+    fn = B(np.asarray(lw["ffn_norm"], np.float32))
+    x2, kc2, vc2 = B(x0), B(kc0), B(vc0)
+    e = mlk.DeviceBuffer.empty
+    h, q, k, v, a, proj = e((T, D)), e((T, QD)), e((T, KD)), e((T, KD)), e((T, QD)), e((T, D))
+    g, u = e((T, F)), e((T, F))
+    mlk.rmsnorm(x2, an, h, T, D, cfg["eps"])
+    mlk.linear_planar(wt, h, pw["wq"], q, T, D, QD, bias=bias["wq"])
+    mlk.linear_planar(wt, h, pw["wk"], k, T, D, KD, bias=bias["wk"])
+    mlk.linear_planar(wt, h, pw["wv"], v, T, D, KD, bias=bias["wv"])
+    mlk.rope(q, k, T, H, KV, hd, positions=positions, pos0=pos, theta=cfg["theta"],
+             rope_type=cfg["rope_type"], err=flag2)
+    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, positions=positions, pos0=pos, err=flag2)
+    nws = mlk.attention_workspace_bytes(T, H, KV, hd, S)
+    aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
+    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, positions=positions,
+                         pos0=pos, workspace=aws, workspace_bytes=aws.nbytes, err=flag2)
+    mlk.linear_planar(wt, a, pw["wo"], proj, T, QD, D)
+    mlk.add_rmsnorm(x2, proj, fn, h, T, D, cfg["eps"])
+    mlk.linear_planar(wt, h, pw["w_gate"], g, T, D, F)
+    mlk.linear_planar(wt, h, pw["w_up"], u, T, D, F)
+    mlk.swiglu(g, u, g, T * F)
+    mlk.linear_planar(wt, g, pw["w_down"], proj, T, F, D)
+    mlk.add(x2, proj, x2, T * D)
+    np.testing.assert_array_equal(got, x2.download())
+    np.testing.assert_array_equal(kc.download(), kc2.download())
+    np.testing.assert_array_equal(vc.download(), vc2.download())
+    assert int(flag.download()[0]) == int(flag2.download()[0]) == (1 if case == "bad_position" else 0)
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+def test_forward_planar_matches_oracle(orc, fwd, wt):
+    """A model with planar copies: decode batches of 2, 5, 16 and 32 tokens
+    (the planar kernels) after a 33-token prefill (the GEMM on the blocks),
+    against the reference's ForwardToken loop over the same tokens."""
+    cfg = dict(vocab=300, dim=512, hidden_dim=1024, layers=2, n_heads=8, n_kv_heads=2,
+               head_dim=64, max_seq=160, rope_type=0, theta=10000.0, eps=1e-5)
+    model = O.forward_model(cfg, seed=21, weight_type=wt, biases=True)
+    sizes = [33, 2, 5, 16, 32]
+    n = sum(sizes)
+    rng = np.random.default_rng(4)
+    tokens = rng.integers(0, cfg["vocab"], n).astype(np.int32)
+    want, _ = orc.forward_tokens(model, tokens, np.arange(n, dtype=np.int32))
+    dm = fwd.DeviceModel(model, planar=True)
+    at = 0
+    for T in sizes:
+        got = dm.forward(tokens[at:at + T], pos0=at, all_logits=True)
+        assert_forward_close(got, want[at:at + T], f"{wt} batch of {T} at {at}")
+        at += T

@@ -149,7 +149,7 @@ def test_quant_bytes_and_status_strings():
     assert mlk.quant_bytes("q4_1", 1, 32) == 20
     assert mlk.lib.mlk_quant_bytes(5, 1, 32) == 0
     assert mlk.lib.mlk_status_string(0) == b"success"
-    assert mlk.lib.mlk_abi_version() == 1
+    assert mlk.lib.mlk_abi_version() == 2
 
 
 def test_no_gpu_here_reports_zero_devices_or_a_hip_error():
