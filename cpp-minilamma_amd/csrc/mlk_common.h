@@ -203,6 +203,51 @@ __device__ inline void RopeRotate(float x0, float x1, double c, double s, float*
     *r1 = static_cast<float>(a0 * s + a1 * c);
 }
 
+// x for the planar bf16 linear layers (mlk_gemm.hip) as three bf16 planes:
+// v = p[0] + p[1] + p[2] exactly, each p[i] exact in bf16 (p[0] = v with its
+// low 16 bits cleared, p[1] the same of v - p[0], p[2] the rest, at most 8
+// significant bits).  Inf and NaN go whole into p[0] (NaN as the quiet NaN,
+// whose payload bit survives in bf16), so products with them are what fp32
+// products would be.
+__device__ inline void SplitBf(float v, float (&p)[3]) {
+    if (!__builtin_isfinite(v)) {
+        p[0] = v != v ? __builtin_nanf("") : v;
+        p[1] = p[2] = 0.0f;
+        return;
+    }
+    p[0] = __uint_as_float(__float_as_uint(v) & 0xFFFF0000u);
+    const float r = v - p[0];  // exact: the low 16 bits of v's significand
+    p[1] = __uint_as_float(__float_as_uint(r) & 0xFFFF0000u);
+    p[2] = r - p[1];
+}
+
+// Two floats whose values are exact in bf16, as one dword of bf16 (a low).
+__device__ inline uint32_t PackBf(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
+// Inputs k, k + 1 (k even) of token row t of a [T, K] x into its planes
+// ([K / 32 blocks][3 pieces][T tokens][16 dwords], dword j of a block
+// holding inputs 2j, 2j + 1).
+__device__ inline void StorePlanes(uint32_t* planes, int64_t T, int64_t t, int64_t k, float v0,
+                                   float v1) {
+    float p0[3], p1[3];
+    SplitBf(v0, p0);
+    SplitBf(v1, p1);
+    uint32_t* d = planes + ((k / 32) * 3 * T + t) * 16 + (k % 32) / 2;
+#pragma unroll
+    for (int p = 0; p < 3; ++p) d[p * T * 16] = PackBf(p0[p], p1[p]);
+}
+
+// Input k alone: its three bf16 halves of the planes' dwords.
+__device__ inline void StorePlanes1(uint32_t* planes, int64_t T, int64_t t, int64_t k, float v) {
+    float p[3];
+    SplitBf(v, p);
+    uint16_t* d = reinterpret_cast<uint16_t*>(planes + ((k / 32) * 3 * T + t) * 16) + k % 32;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) d[i * T * 32] = static_cast<uint16_t>(__float_as_uint(p[i]) >> 16);
+}
+
 // Raises a device-side error flag (the flag is only ever set, never read
 // back here, so any nonzero store is enough).
 __device__ inline void RaiseFlag(int32_t* err, int32_t code) {

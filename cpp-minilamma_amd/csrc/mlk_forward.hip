@@ -38,8 +38,8 @@ namespace {
 constexpr int kLinearF32 = MLK_WEIGHT_F32;
 
 struct Plan {
-    int64_t off[10];  // float offsets: h q k v a proj gate up | byte offsets: lin att
-    int64_t lin_bytes = 0, att_bytes = 0, total = 0;
+    int64_t off[11];  // float offsets: h q k v a proj gate up | byte offsets: lin att planes
+    int64_t lin_bytes = 0, att_bytes = 0, plane_bytes = 0, total = 0;
 };
 
 int64_t Align256(int64_t bytes) { return (bytes + 255) / 256 * 256; }
@@ -95,6 +95,10 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
                                                           max_ctx);
     p.off[9] = at;
     at += Align256(p.att_bytes);
+    // bf16 planes of the planar layers' x (h, then SwiGLU's output)
+    p.plane_bytes = PlanarRows(T) ? T * (D > F ? D : F) * 6 : 0;
+    p.off[10] = at;
+    at += Align256(p.plane_bytes);
     p.total = at;
     return p;
 }
@@ -240,6 +244,7 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
           *gate = buf(6), *up = buf(7);
     void* lin_ws = p.lin_bytes > 0 ? base + p.off[8] : nullptr;
     void* att_ws = p.att_bytes > 0 ? base + p.off[9] : nullptr;
+    uint32_t* planes = p.plane_bytes > 0 ? reinterpret_cast<uint32_t*>(base + p.off[10]) : nullptr;
     const size_t lin_b = static_cast<size_t>(p.lin_bytes);
     const float eps = c.rms_norm_eps;
 
@@ -284,7 +289,14 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         return Fail(MLK_ERR_RANGE, "%s: positions %d..%lld out of range [0, %lld)", fn, pos0,
                     static_cast<long long>(pos0 + T - 1), static_cast<long long>(max_seq));
     }
-    MLK_TRY(mlk_rmsnorm_f32(x, w->attention_norm, h, T, D, eps, stream));
+    // planar q/k/v: the norm also writes h's bf16 planes (no split launch)
+    const uint32_t* h_planes = nullptr;
+    if (qkvp && planes != nullptr && NormPlanesApplies(x, nullptr, w->attention_norm, h, D)) {
+        MLK_TRY(AddRmsNormPlanes(x, nullptr, w->attention_norm, h, planes, T, D, eps, hs));
+        h_planes = planes;
+    } else {
+        MLK_TRY(mlk_rmsnorm_f32(x, w->attention_norm, h, T, D, eps, stream));
+    }
     if (qkv1 || qkvm) {
         const int64_t slot = KD;
         float* ky = rope_fused ? k_cache + layer * max_seq * slot : k;
@@ -300,7 +312,7 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         if (qkv1) {
             MLK_TRY(LinearRowStream(w->wq.type, h, D, a, mode, hs));
         } else if (qkvp) {
-            MLK_TRY(LinearPlanarFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs));
+            MLK_TRY(LinearPlanarFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs, h_planes));
         } else {
             MLK_TRY(LinearSkinnyFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs));
         }
@@ -324,7 +336,14 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     } else {
         MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
     }
-    MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
+    h_planes = nullptr;
+    if (ffnp && planes != nullptr && NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
+        MLK_TRY(AddRmsNormPlanes(x, proj, w->ffn_norm, h, planes, T, D, eps, hs));
+        h_planes = planes;
+    } else {
+        MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
+    }
+    const uint32_t* g_planes = nullptr;
     if (ffn1) {
         StreamArgs a{};
         a.seg[0] = Seg(w->w_gate, gate, F);
@@ -332,11 +351,16 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.n_seg = 2;
         MLK_TRY(LinearRowStream(w->w_gate.type, h, D, a, kStreamSwiGlu, hs));
     } else if (ffnp) {
+        // the SwiGLU epilogue also writes the planes of its output for a
+        // planar down projection (over h's planes: the GEMM has read them)
         StreamArgs a{};
         a.seg[0] = PlanarSeg(w->w_gate, gate, F);
         a.seg[1] = PlanarSeg(w->w_up, gate, F);
         a.n_seg = 2;
-        MLK_TRY(LinearPlanarFused(w->w_gate.type, h, T, D, a, kStreamSwiGlu, lin_ws, lin_b, hs));
+        a.planes = downp && planes != nullptr && F % 32 == 0 ? planes : nullptr;
+        MLK_TRY(LinearPlanarFused(w->w_gate.type, h, T, D, a, kStreamSwiGlu, lin_ws, lin_b, hs,
+                                  h_planes));
+        g_planes = a.planes;
     } else if (ffnm) {
         StreamArgs a{};
         a.seg[0] = Seg(w->w_gate, gate, F);
@@ -357,7 +381,8 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         StreamArgs a{};
         a.seg[0] = PlanarSeg(w->w_down, x, D, x);
         a.n_seg = 1;
-        MLK_TRY(LinearPlanarFused(w->w_down.type, gate, T, F, a, kStreamAdd, lin_ws, lin_b, hs));
+        MLK_TRY(LinearPlanarFused(w->w_down.type, gate, T, F, a, kStreamAdd, lin_ws, lin_b, hs,
+                                  g_planes));
     } else if (downm) {
         StreamArgs a{};
         a.seg[0] = Seg(w->w_down, x, D, x);

@@ -696,26 +696,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kPlTiles = 2;                  // 16-row weight tiles per wave
 constexpr int kPlRows = 4 * 16 * kPlTiles;   // output rows per workgroup
 
-// Two floats whose values are exact in bf16, as one dword of bf16 (a low).
-__device__ inline uint32_t PackBf(float a, float b) {
-    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
-}
-
-// v = p[0] + p[1] + p[2] exactly, each p[i] exact in bf16.  Inf and NaN
-// go whole into p[0] (NaN as the quiet NaN, whose payload bit survives in
-// bf16), so a product with them is what the fp32 product would be.
-__device__ inline void SplitBf(float v, float (&p)[3]) {
-    if (!__builtin_isfinite(v)) {
-        p[0] = v != v ? __builtin_nanf("") : v;
-        p[1] = p[2] = 0.0f;
-        return;
-    }
-    p[0] = __uint_as_float(__float_as_uint(v) & 0xFFFF0000u);
-    const float r = v - p[0];  // exact: the low 16 bits of v's significand
-    p[1] = __uint_as_float(__float_as_uint(r) & 0xFFFF0000u);
-    p[2] = r - p[1];           // exact, at most 8 significant bits
-}
-
 // Bytes 2j, 2j + 1 of v as signed integers in bf16, in one dword.
 __device__ inline uint32_t BytesBf(uint32_t v, int j) {
     return PackBf(static_cast<float>(static_cast<int8_t>(v >> (16 * j))),
@@ -724,8 +704,7 @@ __device__ inline uint32_t BytesBf(uint32_t v, int j) {
 
 // The x planes of tokens t < T: one thread per (block, token, input pair).
 __global__ __launch_bounds__(kGemmThreads) void SplitXBf(const float* __restrict__ x, int64_t T,
-                                                         int64_t K, int tokens,
-                                                         uint32_t* __restrict__ planes) {
+                                                         int64_t K, uint32_t* __restrict__ planes) {
     const int64_t n = (K / 32) * T * 16;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
@@ -733,11 +712,7 @@ __global__ __launch_bounds__(kGemmThreads) void SplitXBf(const float* __restrict
         const int64_t t = (i / 16) % T;
         const int64_t b = i / (16 * T);
         const float* src = x + t * K + 32 * b + 2 * sp;
-        float p0[3], p1[3];
-        SplitBf(src[0], p0);
-        SplitBf(src[1], p1);
-#pragma unroll
-        for (int p = 0; p < 3; ++p) planes[((b * 3 + p) * tokens + t) * 16 + sp] = PackBf(p0[p], p1[p]);
+        StorePlanes(planes, T, t, 32 * b + 2 * sp, src[0], src[1]);
     }
 }
 
@@ -944,10 +919,15 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
         auto sum = [&](int64_t col) { return SumSplits(partial + t * cols + col, splits, stride); };
         if (mode == kStreamSwiGlu) {
             const int64_t F = a.seg[0].rows;
-            float g = sum(c), u = sum(F + c);
-            if (a.seg[0].bias != nullptr) g += a.seg[0].bias[c];
-            if (a.seg[1].bias != nullptr) u += a.seg[1].bias[c];
-            a.seg[1].y[t * F + c] = SwiGluF(g, u);
+            auto swiglu = [&](int64_t col) {
+                float g = sum(col), u = sum(F + col);
+                if (a.seg[0].bias != nullptr) g += a.seg[0].bias[col];
+                if (a.seg[1].bias != nullptr) u += a.seg[1].bias[col];
+                return SwiGluF(g, u);
+            };
+            const float yv = swiglu(c);
+            a.seg[1].y[t * F + c] = yv;
+            if (a.planes != nullptr) StorePlanes1(a.planes, T, t, c, yv);
             continue;
         }
         if (mode == kStreamQkvRope) {
@@ -1297,12 +1277,13 @@ void LaunchPlanarT(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t
     }
 }
 
-// x split into planes (after the partial sums in the workspace), then
-// GemmPlanar over the segments' row groups x the plan's ranges.  a.w,
-// a.rows, a.n_seg set; the rest filled in here.  The caller reduces.
-mlk_status RunPlanar(int qt, const float* x, SkinnyArgs& a, int64_t T, int64_t K,
-                     bool partials, void* workspace, size_t workspace_bytes, int* splits,
-                     float** partial, hipStream_t s) {
+// x split into planes (after the partial sums in the workspace; or the
+// caller's planes of x when planes_in is set), then GemmPlanar over the
+// segments' row groups x the plan's ranges.  a.w, a.rows, a.n_seg set; the
+// rest filled in here.  The caller reduces.
+mlk_status RunPlanar(int qt, const float* x, const uint32_t* planes_in, SkinnyArgs& a, int64_t T,
+                     int64_t K, bool partials, void* workspace, size_t workspace_bytes,
+                     int* splits, float** partial, hipStream_t s) {
     int64_t cols = 0, groups = 0;
     for (int i = 0; i < a.n_seg; ++i) {
         if (!Aligned(a.w[i], 16)) return Fail(MLK_ERR_INVALID, "linear (planar): weights not 16-byte aligned");
@@ -1321,15 +1302,22 @@ mlk_status RunPlanar(int qt, const float* x, SkinnyArgs& a, int64_t T, int64_t K
         return Fail(MLK_ERR_INVALID, "linear (planar): %lld output rows exceed one launch",
                     static_cast<long long>(cols));
     }
+    if (planes_in != nullptr && !Aligned(planes_in, 16)) {
+        return Fail(MLK_ERR_INVALID, "linear (planar): x planes not 16-byte aligned");
+    }
     a.row_groups = static_cast<int>(groups);
     a.cols = cols;
     *splits = p.splits;
     *partial = p.partial_bytes > 0 ? static_cast<float*>(workspace) : nullptr;
-    uint32_t* planes = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + p.partial_bytes);
-    hipLaunchKernelGGL(SplitXBf, dim3(GridFor((K / 32) * T * 16, kGemmThreads, 4)),
-                       dim3(kGemmThreads), 0, s, x, T, K, static_cast<int>(T), planes);
-    mlk_status st = CheckLaunch("SplitXBf");
-    if (st != MLK_OK) return st;
+    const uint32_t* planes = planes_in;
+    if (planes == nullptr) {
+        uint32_t* own = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + p.partial_bytes);
+        hipLaunchKernelGGL(SplitXBf, dim3(GridFor((K / 32) * T * 16, kGemmThreads, 4)),
+                           dim3(kGemmThreads), 0, s, x, T, K, own);
+        mlk_status st = CheckLaunch("SplitXBf");
+        if (st != MLK_OK) return st;
+        planes = own;
+    }
     const dim3 grid(static_cast<unsigned>(groups * p.splits));
     if (qt == MLK_Q8_0) {
         LaunchPlanarT<MLK_Q8_0>(p, grid, s, planes, a, T, K, *partial);
@@ -1351,7 +1339,7 @@ int64_t PlanarWorkspaceBytes(int64_t T, int64_t K, int64_t cols, bool partials) 
 
 mlk_status LinearPlanar(int qt, const float* x, const void* w, const float* bias, float* y,
                         int64_t T, int64_t K, int64_t O, void* workspace, size_t workspace_bytes,
-                        hipStream_t s) {
+                        hipStream_t s, const uint32_t* planes) {
     if (!PlanarApplies(qt, T, K)) {  // many rows: the tiled GEMM on the planar tiles
         return LaunchGemm(qt == MLK_Q8_0 ? kWPlanarQ8 : kWPlanarQ4, x, w, bias, y, T, K, O, 0,
                           workspace, workspace_bytes, s);
@@ -1364,8 +1352,8 @@ mlk_status LinearPlanar(int qt, const float* x, const void* w, const float* bias
     a.y = y;
     int splits = 1;
     float* partial = nullptr;
-    mlk_status st = RunPlanar(qt, x, a, T, K, false, workspace, workspace_bytes, &splits,
-                              &partial, s);
+    mlk_status st = RunPlanar(qt, x, planes, a, T, K, false, workspace, workspace_bytes,
+                              &splits, &partial, s);
     if (st != MLK_OK || partial == nullptr) return st;
     hipLaunchKernelGGL(SplitKReduce, dim3(GridFor(T * O, kGemmThreads, 8)), dim3(kGemmThreads), 0,
                        s, partial, splits, bias, y, T, O);
@@ -1373,7 +1361,12 @@ mlk_status LinearPlanar(int qt, const float* x, const void* w, const float* bias
 }
 
 mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const StreamArgs& sa,
-                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s) {
+                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s,
+                             const uint32_t* planes) {
+    if (sa.planes != nullptr &&
+        (mode != kStreamSwiGlu || sa.seg[0].rows % 32 != 0 || !Aligned(sa.planes, 16))) {
+        return Fail(MLK_ERR_INVALID, "linear (planar, fused rows): planes out only after SwiGLU");
+    }
     if (!PlanarApplies(qt, T, K) || sa.n_seg < 1 || sa.n_seg > 3 || !Aligned(x, 16) ||
         (mode == kStreamSwiGlu && (sa.n_seg != 2 || sa.seg[0].rows != sa.seg[1].rows)) ||
         (mode == kStreamQkvRope && !QkvRopeArgsOk(sa))) {
@@ -1392,7 +1385,7 @@ mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const
     a.n_seg = sa.n_seg;
     int splits = 1;
     float* partial = nullptr;
-    mlk_status st = RunPlanar(qt, x, a, T, K, true, workspace, workspace_bytes, &splits,
+    mlk_status st = RunPlanar(qt, x, planes, a, T, K, true, workspace, workspace_bytes, &splits,
                               &partial, s);
     if (st != MLK_OK) return st;
     const int64_t cols = a.cols;

@@ -18,6 +18,7 @@
 // all with non-temporal hints; w (4*dim) is shared by all rows and stays in
 // L2 (normal loads).  One workgroup per row, one row per workgroup.
 #include "mlk_common.h"
+#include "mlk_quant.h"
 
 #include <cmath>
 
@@ -32,12 +33,15 @@ constexpr int kWaves = kThreads / kWave;
 // 16 (1024 lanes: one float4 per lane at dim 4096).  Measured on MI355X at
 // [4096, 4096]: 16 waves x 1 float4 beats 1 wave x 16 float4 by 25%, and
 // non-temporal hints are worth another ~12%.
-template <int kWaves, int VPT, bool kDelta, bool kWriteBack>
+// kPlanes: y also goes to `planes`, split into the three bf16 planes the
+// planar linear layers read (StorePlanes; dim % 32 == 0).
+template <int kWaves, int VPT, bool kDelta, bool kWriteBack, bool kPlanes = false>
 __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(float* residual,
                                                                 const float* __restrict__ delta,
                                                                 const float* __restrict__ weight,
                                                                 float* y, int64_t n_rows,
-                                                                int64_t dim, float eps) {
+                                                                int64_t dim, float eps,
+                                                                uint32_t* planes) {
 #pragma clang fp contract(off)
     constexpr int lanes = kWave * kWaves;
     __shared__ double partial[2][kWaves];
@@ -103,6 +107,10 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(float* residual,
                 o.z = static_cast<float>(static_cast<double>(r[v].z) * static_cast<double>(w.z) * scale);
                 o.w = static_cast<float>(static_cast<double>(r[v].w) * static_cast<double>(w.w) * scale);
                 StoreNT(yr + i, o);
+                if (kPlanes) {
+                    StorePlanes(planes, n_rows, row, 4 * i, o.x, o.y);
+                    StorePlanes(planes, n_rows, row, 4 * i + 2, o.z, o.w);
+                }
             }
         }
     }
@@ -141,14 +149,20 @@ __global__ __launch_bounds__(kThreads) void AddRmsNormAny(float* residual,
     }
 }
 
-template <bool kDelta, bool kWriteBack>
+bool VecApplies(const float* residual, const float* delta, const float* weight, const float* y,
+                int64_t dim) {
+    return (dim % 4) == 0 && dim / 4 <= 1024 * 8 && Aligned(residual, 16) &&
+           Aligned(weight, 16) && Aligned(y, 16) && (delta == nullptr || Aligned(delta, 16));
+}
+
+template <bool kDelta, bool kWriteBack, bool kPlanes = false>
 mlk_status Launch(float* residual, const float* delta, const float* weight, float* y,
-                  int64_t n_rows, int64_t dim, float eps, hipStream_t stream) {
+                  int64_t n_rows, int64_t dim, float eps, hipStream_t stream,
+                  uint32_t* planes = nullptr) {
     const unsigned grid = FullGrid(n_rows, 1);
-    const bool vec = (dim % 4) == 0 && Aligned(residual, 16) && Aligned(weight, 16) &&
-                     Aligned(y, 16) && (!kDelta || Aligned(delta, 16));
+    const bool vec = VecApplies(residual, kDelta ? delta : nullptr, weight, y, dim);
     const int64_t dim4 = dim / 4;
-    if (vec && dim4 <= 1024 * 8) {  // beyond 8 float4 per lane the row would spill
+    if (vec) {  // beyond 8 float4 per lane the row would spill
         // waves: the smallest power of two covering the row one float4 per
         // lane, at most 16; then float4 per lane
         int64_t waves = 1;
@@ -156,9 +170,9 @@ mlk_status Launch(float* residual, const float* delta, const float* weight, floa
         const int64_t vpt = (dim4 + waves * kWave - 1) / (waves * kWave);
 #define MLK_NORM_CASE(W, V)                                                                    \
     if (waves == (W) && vpt <= (V)) {                                                         \
-        hipLaunchKernelGGL((AddRmsNormVec<W, V, kDelta, kWriteBack>), dim3(grid),              \
+        hipLaunchKernelGGL((AddRmsNormVec<W, V, kDelta, kWriteBack, kPlanes>), dim3(grid),     \
                            dim3(kWave * (W)), 0, stream, residual, delta, weight, y, n_rows,   \
-                           dim, eps);                                                          \
+                           dim, eps, planes);                                                  \
         return CheckLaunch("AddRmsNormVec");                                                   \
     }
         MLK_NORM_CASE(1, 1)
@@ -171,6 +185,7 @@ mlk_status Launch(float* residual, const float* delta, const float* weight, floa
         MLK_NORM_CASE(16, 8)
 #undef MLK_NORM_CASE
     }
+    if (kPlanes) return Fail(MLK_ERR_INVALID, "rmsnorm (planes): unsupported row layout");
     hipLaunchKernelGGL((AddRmsNormAny<kDelta, kWriteBack>), dim3(grid), dim3(kThreads), 0,
                        stream, residual, delta, weight, y, n_rows, dim, eps);
     return CheckLaunch("AddRmsNormAny");
@@ -193,6 +208,24 @@ mlk_status CheckNormArgs(const char* caller, const void* x, const void* weight, 
 }
 
 }  // namespace
+
+bool NormPlanesApplies(const float* residual, const float* delta, const float* weight,
+                       const float* y, int64_t dim) {
+    return dim % 32 == 0 && VecApplies(residual, delta, weight, y, dim);
+}
+
+mlk_status AddRmsNormPlanes(float* residual, const float* delta, const float* weight, float* y,
+                            uint32_t* planes, int64_t n_rows, int64_t dim, float eps,
+                            hipStream_t s) {
+    if (!NormPlanesApplies(residual, delta, weight, y, dim) || !Aligned(planes, 16)) {
+        return Fail(MLK_ERR_INVALID, "rmsnorm (planes): unsupported row layout");
+    }
+    if (delta == nullptr) {
+        return Launch<false, false, true>(residual, nullptr, weight, y, n_rows, dim, eps, s, planes);
+    }
+    return Launch<true, true, true>(residual, delta, weight, y, n_rows, dim, eps, s, planes);
+}
+
 }  // namespace mlk
 
 using namespace mlk;

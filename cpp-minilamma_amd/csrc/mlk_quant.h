@@ -102,6 +102,10 @@ struct StreamArgs {
     StreamSeg seg[3];
     int n_seg;
     RopeArgs rope;  // kStreamQkvRope only
+    // kStreamSwiGlu of the planar launches only: when set, the SwiGLU
+    // outputs also go here as bf16 planes (StorePlanes, mlk_common.h) for
+    // the next planar layer; F % 32 == 0
+    uint32_t* planes = nullptr;
 };
 
 // in_features % 64 == 0 and x (16-byte aligned) fits the kernel's LDS
@@ -146,12 +150,24 @@ mlk_status LaunchToPlanar(int qt, const void* blocks, int64_t O, int64_t K, void
 // with the same K fused as LinearSkinnyFused (modes and epilogues alike).
 // The workspace (16-byte aligned) holds PlanarWorkspaceBytes(T, K, rows of
 // all segments, fused) bytes: partial sums, then x split into bf16 planes.
+// planes: x's planes already made (StorePlanes layout, 16-byte aligned),
+// or null.
 bool PlanarApplies(int qt, int64_t T, int64_t K);
 int64_t PlanarWorkspaceBytes(int64_t T, int64_t K, int64_t cols, bool fused);
 mlk_status LinearPlanar(int qt, const float* x, const void* w, const float* bias, float* y,
                         int64_t T, int64_t K, int64_t O, void* workspace, size_t workspace_bytes,
-                        hipStream_t s);
+                        hipStream_t s, const uint32_t* planes = nullptr);
 mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const StreamArgs& a,
-                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s);
+                             int mode, void* workspace, size_t workspace_bytes, hipStream_t s,
+                             const uint32_t* planes = nullptr);
+
+// Residual add + RMSNorm (mlk_norm.hip; delta may be null: plain RMSNorm of
+// residual, which is then only read) that also writes y's bf16 planes for
+// the planar layers (StorePlanes, mlk_common.h), when NormPlanesApplies.
+bool NormPlanesApplies(const float* residual, const float* delta, const float* weight,
+                       const float* y, int64_t dim);
+mlk_status AddRmsNormPlanes(float* residual, const float* delta, const float* weight, float* y,
+                            uint32_t* planes, int64_t n_rows, int64_t dim, float eps,
+                            hipStream_t s);
 
 }  // namespace mlk
