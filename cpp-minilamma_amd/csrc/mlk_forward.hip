@@ -79,7 +79,7 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
         }
     }
     if (PlanarRows(T)) {  // the same groups (and wo) on planar weights
-        const int64_t groups[4][3] = {{D, QD + 2 * KD, 1}, {D, 2 * F, 1}, {F, D, 1}, {QD, D, 0}};
+        const int64_t groups[4][3] = {{D, QD + 2 * KD, 1}, {D, 2 * F, 1}, {F, D, 1}, {QD, D, 1}};
         for (const auto& g : groups) {
             if (g[0] % 256 != 0) continue;
             const int64_t b = PlanarWorkspaceBytes(T, g[0], g[1], g[2] != 0);
@@ -330,18 +330,34 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     MLK_TRY(mlk_attention_decode_f32(q, QD, k_cache, v_cache, n_layers, max_seq, c.n_heads,
                                      c.n_kv_heads, c.head_dim, layer, positions, pos0, T, max_ctx,
                                      a, att_ws, static_cast<size_t>(p.att_bytes), err, stream));
-    if (wop) {
-        MLK_TRY(LinearPlanar(w->wo.type, a, w->wo.planar, w->wo.bias, proj, T, QD, D, lin_ws,
-                             lin_b, hs));
-    } else {
-        MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
-    }
     h_planes = nullptr;
-    if (ffnp && planes != nullptr && NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
-        MLK_TRY(AddRmsNormPlanes(x, proj, w->ffn_norm, h, planes, T, D, eps, hs));
+    const bool wo_norm = wop && ffnp && planes != nullptr && lin_ws != nullptr &&
+                         NormPlanesApplies(x, static_cast<const float*>(lin_ws), w->ffn_norm, h,
+                                           D) &&
+                         (w->wo.bias == nullptr || Aligned(w->wo.bias, 16));
+    if (wo_norm) {
+        // wo's split-K partial sums reduced by the residual add + RMSNorm,
+        // which also writes h's planes for gate/up
+        float* partial = nullptr;
+        int splits = 1;
+        MLK_TRY(LinearPlanarPartials(w->wo.type, a, w->wo.planar, T, QD, D, lin_ws, lin_b, hs,
+                                     nullptr, &partial, &splits));
+        MLK_TRY(AddRmsNormPlanes(x, partial, w->ffn_norm, h, planes, T, D, eps, hs, splits,
+                                 w->wo.bias));
         h_planes = planes;
     } else {
-        MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
+        if (wop) {
+            MLK_TRY(LinearPlanar(w->wo.type, a, w->wo.planar, w->wo.bias, proj, T, QD, D, lin_ws,
+                                 lin_b, hs));
+        } else {
+            MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
+        }
+        if (ffnp && planes != nullptr && NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
+            MLK_TRY(AddRmsNormPlanes(x, proj, w->ffn_norm, h, planes, T, D, eps, hs));
+            h_planes = planes;
+        } else {
+            MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
+        }
     }
     const uint32_t* g_planes = nullptr;
     if (ffn1) {

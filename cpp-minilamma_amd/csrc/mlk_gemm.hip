@@ -1360,6 +1360,20 @@ mlk_status LinearPlanar(int qt, const float* x, const void* w, const float* bias
     return CheckLaunch("SplitKReduce");
 }
 
+mlk_status LinearPlanarPartials(int qt, const float* x, const void* w, int64_t T, int64_t K,
+                                int64_t O, void* workspace, size_t workspace_bytes,
+                                hipStream_t s, const uint32_t* planes, float** partial,
+                                int* splits) {
+    if (!PlanarApplies(qt, T, K) || !Aligned(x, 16)) {
+        return Fail(MLK_ERR_INVALID, "linear (planar): unsupported shape");
+    }
+    SkinnyArgs a{};
+    a.w[0] = static_cast<const uint8_t*>(w);
+    a.rows[0] = O;
+    a.n_seg = 1;
+    return RunPlanar(qt, x, planes, a, T, K, true, workspace, workspace_bytes, splits, partial, s);
+}
+
 mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const StreamArgs& sa,
                              int mode, void* workspace, size_t workspace_bytes, hipStream_t s,
                              const uint32_t* planes) {

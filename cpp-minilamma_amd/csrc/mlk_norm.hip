@@ -34,14 +34,15 @@ constexpr int kWaves = kThreads / kWave;
 // [4096, 4096]: 16 waves x 1 float4 beats 1 wave x 16 float4 by 25%, and
 // non-temporal hints are worth another ~12%.
 // kPlanes: y also goes to `planes`, split into the three bf16 planes the
-// planar linear layers read (StorePlanes; dim % 32 == 0).
+// planar linear layers read (StorePlanes; dim % 32 == 0).  splits > 1 or
+// dbias: delta is a linear layer's split-K partial sums ([splits][rows][dim],
+// split_stride floats apart), added in split order, then dbias: the
+// reduction SplitKReduce would do, fused here.
 template <int kWaves, int VPT, bool kDelta, bool kWriteBack, bool kPlanes = false>
-__global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(float* residual,
-                                                                const float* __restrict__ delta,
-                                                                const float* __restrict__ weight,
-                                                                float* y, int64_t n_rows,
-                                                                int64_t dim, float eps,
-                                                                uint32_t* planes) {
+__global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(
+    float* residual, const float* __restrict__ delta, const float* __restrict__ weight, float* y,
+    int64_t n_rows, int64_t dim, float eps, uint32_t* planes, int splits, int64_t split_stride,
+    const float* __restrict__ dbias) {
 #pragma clang fp contract(off)
     constexpr int lanes = kWave * kWaves;
     __shared__ double partial[2][kWaves];
@@ -72,7 +73,36 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(float* residual,
             for (int v = 0; v < VPT; ++v) {
                 const int64_t i = tid + static_cast<int64_t>(v) * lanes;
                 if (i < dim4) {
-                    const float4 d = LoadNT(dr + i);
+                    float4 d = LoadNT(dr + i);
+                    if (splits > 1) {
+                        float4 t[8];
+                        int sp = 1;
+                        for (; sp + 8 <= splits; sp += 8) {  // loads 8 at a time, adds in order
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) t[j] = LoadNT(dr + (sp + j) * (split_stride / 4) + i);
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                d.x += t[j].x;
+                                d.y += t[j].y;
+                                d.z += t[j].z;
+                                d.w += t[j].w;
+                            }
+                        }
+                        for (; sp < splits; ++sp) {
+                            const float4 e = LoadNT(dr + sp * (split_stride / 4) + i);
+                            d.x += e.x;
+                            d.y += e.y;
+                            d.z += e.z;
+                            d.w += e.w;
+                        }
+                    }
+                    if (dbias != nullptr) {
+                        const float4 b = reinterpret_cast<const float4*>(dbias)[i];
+                        d.x += b.x;
+                        d.y += b.y;
+                        d.z += b.z;
+                        d.w += b.w;
+                    }
                     r[v].x += d.x;
                     r[v].y += d.y;
                     r[v].z += d.z;
@@ -158,7 +188,7 @@ bool VecApplies(const float* residual, const float* delta, const float* weight, 
 template <bool kDelta, bool kWriteBack, bool kPlanes = false>
 mlk_status Launch(float* residual, const float* delta, const float* weight, float* y,
                   int64_t n_rows, int64_t dim, float eps, hipStream_t stream,
-                  uint32_t* planes = nullptr) {
+                  uint32_t* planes = nullptr, int splits = 1, const float* dbias = nullptr) {
     const unsigned grid = FullGrid(n_rows, 1);
     const bool vec = VecApplies(residual, kDelta ? delta : nullptr, weight, y, dim);
     const int64_t dim4 = dim / 4;
@@ -172,7 +202,7 @@ mlk_status Launch(float* residual, const float* delta, const float* weight, floa
     if (waves == (W) && vpt <= (V)) {                                                         \
         hipLaunchKernelGGL((AddRmsNormVec<W, V, kDelta, kWriteBack, kPlanes>), dim3(grid),     \
                            dim3(kWave * (W)), 0, stream, residual, delta, weight, y, n_rows,   \
-                           dim, eps, planes);                                                  \
+                           dim, eps, planes, splits, n_rows * dim, dbias);                     \
         return CheckLaunch("AddRmsNormVec");                                                   \
     }
         MLK_NORM_CASE(1, 1)
@@ -185,7 +215,9 @@ mlk_status Launch(float* residual, const float* delta, const float* weight, floa
         MLK_NORM_CASE(16, 8)
 #undef MLK_NORM_CASE
     }
-    if (kPlanes) return Fail(MLK_ERR_INVALID, "rmsnorm (planes): unsupported row layout");
+    if (kPlanes || splits > 1 || dbias != nullptr) {
+        return Fail(MLK_ERR_INVALID, "rmsnorm (planes / partial sums): unsupported row layout");
+    }
     hipLaunchKernelGGL((AddRmsNormAny<kDelta, kWriteBack>), dim3(grid), dim3(kThreads), 0,
                        stream, residual, delta, weight, y, n_rows, dim, eps);
     return CheckLaunch("AddRmsNormAny");
@@ -216,14 +248,16 @@ bool NormPlanesApplies(const float* residual, const float* delta, const float* w
 
 mlk_status AddRmsNormPlanes(float* residual, const float* delta, const float* weight, float* y,
                             uint32_t* planes, int64_t n_rows, int64_t dim, float eps,
-                            hipStream_t s) {
-    if (!NormPlanesApplies(residual, delta, weight, y, dim) || !Aligned(planes, 16)) {
+                            hipStream_t s, int splits, const float* dbias) {
+    if (!NormPlanesApplies(residual, delta, weight, y, dim) || !Aligned(planes, 16) ||
+        (dbias != nullptr && !Aligned(dbias, 16)) || splits < 1) {
         return Fail(MLK_ERR_INVALID, "rmsnorm (planes): unsupported row layout");
     }
     if (delta == nullptr) {
         return Launch<false, false, true>(residual, nullptr, weight, y, n_rows, dim, eps, s, planes);
     }
-    return Launch<true, true, true>(residual, delta, weight, y, n_rows, dim, eps, s, planes);
+    return Launch<true, true, true>(residual, delta, weight, y, n_rows, dim, eps, s, planes, splits,
+                                    dbias);
 }
 
 }  // namespace mlk

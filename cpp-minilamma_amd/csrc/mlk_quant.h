@@ -164,10 +164,19 @@ mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const
 // Residual add + RMSNorm (mlk_norm.hip; delta may be null: plain RMSNorm of
 // residual, which is then only read) that also writes y's bf16 planes for
 // the planar layers (StorePlanes, mlk_common.h), when NormPlanesApplies.
+// splits > 1 or dbias: delta holds a linear layer's split-K partial sums
+// ([splits][n_rows][dim]), reduced here in split order, then + dbias, as
+// SplitKReduce would.
 bool NormPlanesApplies(const float* residual, const float* delta, const float* weight,
                        const float* y, int64_t dim);
 mlk_status AddRmsNormPlanes(float* residual, const float* delta, const float* weight, float* y,
                             uint32_t* planes, int64_t n_rows, int64_t dim, float eps,
-                            hipStream_t s);
+                            hipStream_t s, int splits = 1, const float* dbias = nullptr);
+// The planar GEMM alone, partial sums always in the workspace: *partial,
+// *splits for the caller's reduction (e.g. AddRmsNormPlanes).
+mlk_status LinearPlanarPartials(int qt, const float* x, const void* w, int64_t T, int64_t K,
+                                int64_t O, void* workspace, size_t workspace_bytes,
+                                hipStream_t s, const uint32_t* planes, float** partial,
+                                int* splits);
 
 }  // namespace mlk
