@@ -38,7 +38,8 @@ constexpr int kWaves = kThreads / kWave;
 // dbias: delta is a linear layer's split-K partial sums ([splits][rows][dim],
 // split_stride floats apart), added in split order, then dbias: the
 // reduction SplitKReduce would do, fused here.
-template <int kWaves, int VPT, bool kDelta, bool kWriteBack, bool kPlanes = false>
+template <int kWaves, int VPT, bool kDelta, bool kWriteBack, bool kPlanes = false,
+          bool kPartials = false>
 __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(
     float* residual, const float* __restrict__ delta, const float* __restrict__ weight, float* y,
     int64_t n_rows, int64_t dim, float eps, uint32_t* planes, int splits, int64_t split_stride,
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(
                 const int64_t i = tid + static_cast<int64_t>(v) * lanes;
                 if (i < dim4) {
                     float4 d = LoadNT(dr + i);
-                    if (splits > 1) {
+                    if (kPartials && splits > 1) {
                         float4 t[8];
                         int sp = 1;
                         for (; sp + 8 <= splits; sp += 8) {  // loads 8 at a time, adds in order
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(
                             d.w += e.w;
                         }
                     }
-                    if (dbias != nullptr) {
+                    if (kPartials && dbias != nullptr) {
                         const float4 b = reinterpret_cast<const float4*>(dbias)[i];
                         d.x += b.x;
                         d.y += b.y;
@@ -185,7 +186,7 @@ bool VecApplies(const float* residual, const float* delta, const float* weight, 
            Aligned(weight, 16) && Aligned(y, 16) && (delta == nullptr || Aligned(delta, 16));
 }
 
-template <bool kDelta, bool kWriteBack, bool kPlanes = false>
+template <bool kDelta, bool kWriteBack, bool kPlanes = false, bool kPartials = false>
 mlk_status Launch(float* residual, const float* delta, const float* weight, float* y,
                   int64_t n_rows, int64_t dim, float eps, hipStream_t stream,
                   uint32_t* planes = nullptr, int splits = 1, const float* dbias = nullptr) {
@@ -200,7 +201,8 @@ mlk_status Launch(float* residual, const float* delta, const float* weight, floa
         const int64_t vpt = (dim4 + waves * kWave - 1) / (waves * kWave);
 #define MLK_NORM_CASE(W, V)                                                                    \
     if (waves == (W) && vpt <= (V)) {                                                         \
-        hipLaunchKernelGGL((AddRmsNormVec<W, V, kDelta, kWriteBack, kPlanes>), dim3(grid),     \
+        hipLaunchKernelGGL((AddRmsNormVec<W, V, kDelta, kWriteBack, kPlanes, kPartials>),      \
+                           dim3(grid),                                                         \
                            dim3(kWave * (W)), 0, stream, residual, delta, weight, y, n_rows,   \
                            dim, eps, planes, splits, n_rows * dim, dbias);                     \
         return CheckLaunch("AddRmsNormVec");                                                   \
@@ -256,8 +258,11 @@ mlk_status AddRmsNormPlanes(float* residual, const float* delta, const float* we
     if (delta == nullptr) {
         return Launch<false, false, true>(residual, nullptr, weight, y, n_rows, dim, eps, s, planes);
     }
-    return Launch<true, true, true>(residual, delta, weight, y, n_rows, dim, eps, s, planes, splits,
-                                    dbias);
+    if (splits > 1 || dbias != nullptr) {
+        return Launch<true, true, true, true>(residual, delta, weight, y, n_rows, dim, eps, s,
+                                              planes, splits, dbias);
+    }
+    return Launch<true, true, true>(residual, delta, weight, y, n_rows, dim, eps, s, planes);
 }
 
 }  // namespace mlk
