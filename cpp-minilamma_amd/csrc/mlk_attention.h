@@ -32,4 +32,16 @@ mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* k
                             int64_t max_ctx, float* out, float* ws_acc, float* ws_ml,
                             int32_t* err, hipStream_t s);
 
+// mlk_attention_decode_f32 with one more output: when the chunk merge runs
+// (more than one chunk of cache positions) and planes is not null, the merge
+// also writes out's bf16 planes (StorePlanes1 over rows of n_heads * head_dim,
+// which must be a multiple of 32) and sets *planes_written; otherwise planes
+// are untouched and *planes_written is false.
+mlk_status AttentionDecode(const float* q, int64_t q_row_stride, const float* k_cache,
+                           const float* v_cache, int64_t n_layers, int64_t max_seq,
+                           int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int64_t layer,
+                           const int32_t* positions, int32_t pos0, int64_t n_tokens,
+                           int64_t max_ctx, float* out, void* workspace, size_t workspace_bytes,
+                           int32_t* err, void* stream, uint32_t* planes, bool* planes_written);
+
 }  // namespace mlk

@@ -73,6 +73,7 @@ struct AttnParams {
     float* ws_acc;     // [T, H, n_chunks, hd]
     float* ws_ml;      // [T, H, n_chunks, 2]
     int32_t* err;
+    uint32_t* planes;  // AttnCombine: also out's bf16 planes (the [T, H * hd] rows)
 };
 
 __device__ inline int32_t TokenPos(const AttnParams& p, int64_t t) {
@@ -589,8 +590,13 @@ __global__ __launch_bounds__(kAttnThreads) void AttnCombine(AttnParams p) {
     const int64_t t = row / p.H;
     const int32_t pos = TokenPos(p, t);
     float* o = p.out + row * p.hd;
+    const int64_t k0 = (row - t * p.H) * p.hd;  // h * hd: the row's place in [H * hd]
+    const int64_t T = gridDim.x / p.H;
     if (pos < 0 || pos >= p.max_ctx) {
-        for (int d = threadIdx.x; d < p.hd; d += kAttnThreads) o[d] = 0.0f;
+        for (int d = threadIdx.x; d < p.hd; d += kAttnThreads) {
+            o[d] = 0.0f;
+            if (p.planes != nullptr) StorePlanes1(p.planes, T, t, k0 + d, 0.0f);
+        }
         return;
     }
     const int nc = pos / p.chunk + 1;
@@ -631,7 +637,11 @@ __global__ __launch_bounds__(kAttnThreads) void AttnCombine(AttnParams p) {
             for (; c < n; ++c) a = fmaf(ac[static_cast<int64_t>(c) * p.hd], wgt[c], a);
         }
     }
-    if (d < p.hd) o[d] = a / L;
+    if (d < p.hd) {
+        const float v = a / L;
+        o[d] = v;
+        if (p.planes != nullptr) StorePlanes1(p.planes, T, t, k0 + d, v);
+    }
 }
 
 template <int NQ, bool kFull>
@@ -812,14 +822,22 @@ int64_t mlk_attention_workspace_bytes(int64_t n_tokens, int32_t n_heads, int32_t
     return n_tokens * n_heads * nc * (head_dim + 2) * static_cast<int64_t>(sizeof(float));
 }
 
-mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const float* k_cache,
-                                    const float* v_cache, int64_t n_layers, int64_t max_seq,
-                                    int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
-                                    int64_t layer, const int32_t* positions, int32_t pos0,
-                                    int64_t n_tokens, int64_t max_ctx, float* out,
-                                    void* workspace, size_t workspace_bytes, int32_t* err,
-                                    void* stream) {
+}  // extern "C"
+
+namespace mlk {
+
+mlk_status AttentionDecode(const float* q, int64_t q_row_stride, const float* k_cache,
+                           const float* v_cache, int64_t n_layers, int64_t max_seq,
+                           int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int64_t layer,
+                           const int32_t* positions, int32_t pos0, int64_t n_tokens,
+                           int64_t max_ctx, float* out, void* workspace, size_t workspace_bytes,
+                           int32_t* err, void* stream, uint32_t* planes, bool* planes_written) {
     const char* fn = "mlk_attention_decode_f32";
+    if (planes_written != nullptr) *planes_written = false;
+    if (planes != nullptr &&
+        ((static_cast<int64_t>(n_heads) * head_dim) % 32 != 0 || !Aligned(planes, 16))) {
+        return Fail(MLK_ERR_INVALID, "%s: planes need n_heads * head_dim %% 32 == 0", fn);
+    }
     mlk_status st = CheckCache(fn, k_cache, v_cache, n_layers, max_seq, n_kv_heads, head_dim,
                                layer);
     if (st != MLK_OK) return st;
@@ -895,9 +913,12 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
         p.ws_acc = ws_acc;
         p.ws_ml = ws_ml;
         p.err = err;
+        p.planes = planes;
         hipLaunchKernelGGL(AttnCombine, dim3(static_cast<unsigned>(n_tokens * n_heads)),
                            dim3(kAttnThreads), 0, s, p);
-        return CheckLaunch("AttnCombine");
+        st = CheckLaunch("AttnCombine");
+        if (st == MLK_OK && planes_written != nullptr) *planes_written = planes != nullptr;
+        return st;
     }
     const int group = n_heads / n_kv_heads;
     const bool mf = MfSupported(head_dim) && Aligned(k_cache, 16);
@@ -918,7 +939,7 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
     if (n_tokens * nc > 0x7FFFFFFF || static_cast<int64_t>(n_kv_heads) * n_hblk > 65535) {
         return Fail(MLK_ERR_INVALID, "%s: launch too large", fn);
     }
-    AttnParams p;
+    AttnParams p{};
     p.q = q;
     p.q_stride = q_row_stride;
     p.kc = k_cache + layer * max_seq * slot;
@@ -959,11 +980,30 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
     }
     if (e != hipSuccess) return FromHip(e, mf ? "AttnDecodeMf" : "AttnSplit");
     if (nc > 1) {
+        p.planes = planes;
         hipLaunchKernelGGL(AttnCombine, dim3(static_cast<unsigned>(n_tokens * n_heads)),
                            dim3(kAttnThreads), 0, s, p);
-        return CheckLaunch("AttnCombine");
+        st = CheckLaunch("AttnCombine");
+        if (st == MLK_OK && planes_written != nullptr) *planes_written = planes != nullptr;
+        return st;
     }
     return MLK_OK;
+}
+
+}  // namespace mlk
+
+extern "C" {
+
+mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const float* k_cache,
+                                    const float* v_cache, int64_t n_layers, int64_t max_seq,
+                                    int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                    int64_t layer, const int32_t* positions, int32_t pos0,
+                                    int64_t n_tokens, int64_t max_ctx, float* out,
+                                    void* workspace, size_t workspace_bytes, int32_t* err,
+                                    void* stream) {
+    return AttentionDecode(q, q_row_stride, k_cache, v_cache, n_layers, max_seq, n_heads,
+                           n_kv_heads, head_dim, layer, positions, pos0, n_tokens, max_ctx, out,
+                           workspace, workspace_bytes, err, stream, nullptr, nullptr);
 }
 
 }  // extern "C"

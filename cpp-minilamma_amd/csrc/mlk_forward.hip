@@ -27,9 +27,11 @@
 // The intermediates live in the caller's workspace (no allocation here):
 // h, q, k, v, a, a Wo^T, gate, up, then the linear layers' split-K scratch
 // and the decode attention's chunk scratch, each 256-byte aligned.
+#include "mlk_attention.h"
 #include "mlk_common.h"
 #include "mlk_quant.h"
 
+#include <algorithm>
 #include <initializer_list>
 
 namespace mlk {
@@ -95,8 +97,10 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
                                                           max_ctx);
     p.off[9] = at;
     at += Align256(p.att_bytes);
-    // bf16 planes of the planar layers' x (h, then SwiGLU's output)
-    p.plane_bytes = PlanarRows(T) ? T * (D > F ? D : F) * 6 : 0;
+    // bf16 planes of the planar layers' x (h, attention's output, then
+    // SwiGLU's output)
+    const int64_t widest = std::max(D, std::max(F, QD));
+    p.plane_bytes = PlanarRows(T) ? T * widest * 6 : 0;
     p.off[10] = at;
     at += Align256(p.plane_bytes);
     p.total = at;
@@ -327,9 +331,13 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         MLK_TRY(mlk_kv_write_f32(k_cache, v_cache, n_layers, max_seq, c.n_kv_heads, c.head_dim,
                                  layer, k, KD, v, KD, positions, pos0, T, err, stream));
     }
-    MLK_TRY(mlk_attention_decode_f32(q, QD, k_cache, v_cache, n_layers, max_seq, c.n_heads,
-                                     c.n_kv_heads, c.head_dim, layer, positions, pos0, T, max_ctx,
-                                     a, att_ws, static_cast<size_t>(p.att_bytes), err, stream));
+    // the chunk merge also writes a's planes for a planar wo (over h's: the
+    // q/k/v GEMM has read them)
+    bool a_planes = false;
+    MLK_TRY(AttentionDecode(q, QD, k_cache, v_cache, n_layers, max_seq, c.n_heads, c.n_kv_heads,
+                            c.head_dim, layer, positions, pos0, T, max_ctx, a, att_ws,
+                            static_cast<size_t>(p.att_bytes), err, stream,
+                            wop && QD % 32 == 0 ? planes : nullptr, &a_planes));
     h_planes = nullptr;
     const bool wo_norm = wop && ffnp && planes != nullptr && lin_ws != nullptr &&
                          NormPlanesApplies(x, static_cast<const float*>(lin_ws), w->ffn_norm, h,
@@ -341,14 +349,14 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         float* partial = nullptr;
         int splits = 1;
         MLK_TRY(LinearPlanarPartials(w->wo.type, a, w->wo.planar, T, QD, D, lin_ws, lin_b, hs,
-                                     nullptr, &partial, &splits));
+                                     a_planes ? planes : nullptr, &partial, &splits));
         MLK_TRY(AddRmsNormPlanes(x, partial, w->ffn_norm, h, planes, T, D, eps, hs, splits,
                                  w->wo.bias));
         h_planes = planes;
     } else {
         if (wop) {
             MLK_TRY(LinearPlanar(w->wo.type, a, w->wo.planar, w->wo.bias, proj, T, QD, D, lin_ws,
-                                 lin_b, hs));
+                                 lin_b, hs, a_planes ? planes : nullptr));
         } else {
             MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
         }

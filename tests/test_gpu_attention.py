@@ -238,14 +238,16 @@ def test_attention_bad_positions_give_zero_rows_and_flag(mlk, T):
 
 @pytest.mark.parametrize("H,KV,hd,T,S", [(32, 8, 128, 21, 3000), (6, 2, 64, 5, 300),
                                          (8, 8, 64, 40, 700), (12, 2, 128, 17, 256),
-                                         (8, 8, 64, 1024, 600)])
+                                         (8, 8, 64, 1024, 600), (32, 8, 128, 16, 8192),
+                                         (64, 8, 128, 32, 1500), (8, 8, 128, 9, 100),
+                                         (32, 8, 64, 7, 64)])
 def test_attention_shared_tiles_any_positions(mlk, H, KV, hd, T, S):
     """5 or more decode tokens at arbitrary (unsorted, repeated) positions
     take the shared-tile kernel: 16 tokens per workgroup over chunks of the
-    cache, merged afterwards.  Shapes cover a partial token block, a GQA
-    group that is not a multiple of 4 (idle waves), one chunk (S = 256) and
-    many; 1024 tokens fill the GPU with one chunk spanning the whole
-    context (no merge)."""
+    cache, merged afterwards.  Shapes cover partial token blocks, GQA groups
+    of 4, 8, 6, 3 and 1 (idle waves where the group is not a multiple of 4),
+    one chunk (S = 256) and many; 1024 tokens fill the GPU with one chunk
+    spanning the whole context (no merge)."""
     rng = np.random.default_rng(T * 100 + hd)
     kc, vc = random_cache(rng, 2, S, KV, hd)
     cache = Cache(mlk, kc, vc)
