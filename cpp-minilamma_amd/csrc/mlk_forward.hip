@@ -293,9 +293,20 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         return Fail(MLK_ERR_RANGE, "%s: positions %d..%lld out of range [0, %lld)", fn, pos0,
                     static_cast<long long>(pos0 + T - 1), static_cast<long long>(max_seq));
     }
+    // one token: each norm folded into the streaming GEMV that reads its
+    // output (the same sums in the same order), where the norm kernel's
+    // block shape allows it; the ffn norm's residual x + proj then goes to
+    // h's buffer and the down projection adds into x from there
+    int nw = 0, nvpt = 0;
+    const bool norm_fold = NormShape(x, proj, w->attention_norm, h, D, &nw, &nvpt) &&
+                           Aligned(w->ffn_norm, 16) && (nw == 8 || nw == 16) && nvpt <= 2;
+    const bool attn_fold = qkv1 && norm_fold;
+    const bool ffn_fold = ffn1 && down1 && norm_fold;
     // planar q/k/v: the norm also writes h's bf16 planes (no split launch)
     const uint32_t* h_planes = nullptr;
-    if (qkvp && planes != nullptr && NormPlanesApplies(x, nullptr, w->attention_norm, h, D)) {
+    if (attn_fold) {
+        // in the q/k/v launch below
+    } else if (qkvp && planes != nullptr && NormPlanesApplies(x, nullptr, w->attention_norm, h, D)) {
         MLK_TRY(AddRmsNormPlanes(x, nullptr, w->attention_norm, h, planes, T, D, eps, hs));
         h_planes = planes;
     } else {
@@ -313,7 +324,10 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.rope = RopeArgs{positions, pos0, c.head_dim, slot, max_seq, err,
                           MakeRopeFreqs(c.rope_theta, c.head_dim)};
         const int mode = rope_fused ? kStreamQkvRope : kStreamPlain;
-        if (qkv1) {
+        if (qkv1 && attn_fold) {
+            a.norm = StreamNorm{w->attention_norm, nullptr, nullptr, eps, nw, nvpt};
+            MLK_TRY(LinearRowStream(w->wq.type, x, D, a, mode, hs));
+        } else if (qkv1) {
             MLK_TRY(LinearRowStream(w->wq.type, h, D, a, mode, hs));
         } else if (qkvp) {
             MLK_TRY(LinearPlanarFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs, h_planes));
@@ -363,7 +377,7 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         if (ffnp && planes != nullptr && NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
             MLK_TRY(AddRmsNormPlanes(x, proj, w->ffn_norm, h, planes, T, D, eps, hs));
             h_planes = planes;
-        } else {
+        } else if (!ffn_fold) {
             MLK_TRY(mlk_add_rmsnorm_f32(x, proj, w->ffn_norm, h, T, D, eps, stream));
         }
     }
@@ -373,7 +387,12 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[0] = Seg(w->w_gate, gate, F);
         a.seg[1] = Seg(w->w_up, gate, F);
         a.n_seg = 2;
-        MLK_TRY(LinearRowStream(w->w_gate.type, h, D, a, kStreamSwiGlu, hs));
+        if (ffn_fold) {  // RMSNorm(x + proj) staged in the launch; x + proj into h's buffer
+            a.norm = StreamNorm{w->ffn_norm, proj, h, eps, nw, nvpt};
+            MLK_TRY(LinearRowStream(w->w_gate.type, x, D, a, kStreamSwiGlu, hs));
+        } else {
+            MLK_TRY(LinearRowStream(w->w_gate.type, h, D, a, kStreamSwiGlu, hs));
+        }
     } else if (ffnp) {
         // the SwiGLU epilogue also writes the planes of its output for a
         // planar down projection (over h's planes: the GEMM has read them)
@@ -398,7 +417,7 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     }
     if (down1) {
         StreamArgs a{};
-        a.seg[0] = Seg(w->w_down, x, D, x);
+        a.seg[0] = Seg(w->w_down, x, D, ffn_fold ? h : x);  // x = (x + proj) + down
         a.n_seg = 1;
         MLK_TRY(LinearRowStream(w->w_down.type, gate, F, a, kStreamAdd, hs));
     } else if (downp) {

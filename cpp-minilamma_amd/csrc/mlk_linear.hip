@@ -708,6 +708,93 @@ __device__ inline void StreamFinish(float (&acc)[R][1], const StreamArgs& a, con
     }
 }
 
+// The RMSNorm of residual row x (+ delta) into xs (StreamNorm): the
+// separate norm kernel's threads are emulated here, virtual thread vt =
+// tid + 512 j of its 64 * waves (waves 8 or 16), each summing the squares
+// of its float4s vt, vt + 64 * waves (vpt of them, at most 2) in order, in
+// float64; each virtual wave's sum by the same butterfly, then the wave
+// sums in order; each float4 then scaled as that kernel scales it.  Every
+// load (x, delta, the norm weight) is issued before the reduction.
+constexpr int kNormVpt = 2;  // float4s per norm thread the staging handles
+
+__device__ void StageNorm(const StreamNorm& n, const float* x, int64_t K, float* xs,
+                          double* wsum) {
+#pragma clang fp contract(off)
+    constexpr int NJ = 1024 / kStreamThreads;  // virtual threads per thread, at most
+    const int nv = kWave * n.waves;
+    const int64_t dim4 = K / 4;
+    const int tid = threadIdx.x, lane = tid % kWave, rw = tid / kWave;
+    const bool writer = blockIdx.x == 0 && n.res_out != nullptr;
+    float4 r[NJ][kNormVpt], w[NJ][kNormVpt];
+    bool ok[NJ][kNormVpt];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+        for (int v = 0; v < kNormVpt; ++v) {
+            const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
+            ok[j][v] = j * kStreamThreads < nv && v < n.vpt && i < dim4;
+            r[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            w[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(n.weight)[i]
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    if (n.delta != nullptr) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+            for (int v = 0; v < kNormVpt; ++v) {
+                const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
+                if (ok[j][v]) {
+                    const float4 d = reinterpret_cast<const float4*>(n.delta)[i];
+                    r[j][v].x += d.x;
+                    r[j][v].y += d.y;
+                    r[j][v].z += d.z;
+                    r[j][v].w += d.w;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        if (j * kStreamThreads >= nv) break;
+        double ss = 0.0;
+#pragma unroll
+        for (int v = 0; v < kNormVpt; ++v) {
+            const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
+            if (ok[j][v]) {
+                if (writer) reinterpret_cast<float4*>(n.res_out)[i] = r[j][v];
+                const double a = r[j][v].x, b = r[j][v].y, c = r[j][v].z, d = r[j][v].w;
+                ss += a * a;
+                ss += b * b;
+                ss += c * c;
+                ss += d * d;
+            }
+        }
+        ss = WaveSum(ss);
+        if (lane == 0) wsum[rw + j * kStreamWaves] = ss;
+    }
+    __syncthreads();
+    double total = 0.0;
+    for (int k = 0; k < n.waves; ++k) total += wsum[k];
+    const double scale = 1.0 / sqrt(total / static_cast<double>(K) + static_cast<double>(n.eps));
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+        for (int v = 0; v < kNormVpt; ++v) {
+            const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
+            if (ok[j][v]) {
+                const float4 a = r[j][v], b = w[j][v];
+                float4 o;
+                o.x = static_cast<float>(static_cast<double>(a.x) * static_cast<double>(b.x) * scale);
+                o.y = static_cast<float>(static_cast<double>(a.y) * static_cast<double>(b.y) * scale);
+                o.z = static_cast<float>(static_cast<double>(a.z) * static_cast<double>(b.z) * scale);
+                o.w = static_cast<float>(static_cast<double>(a.w) * static_cast<double>(b.w) * scale);
+                *reinterpret_cast<float4*>(xs + XPad(4 * i)) = o;
+            }
+        }
+    }
+}
+
 // x and the weights are not __restrict__: loads through restrict-qualified
 // read-only pointers are marked invariant, and the compiler then sinks the
 // first steps' weight loads past the barrier to their first use.
@@ -766,8 +853,13 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, 
         ++next;
     }
     __builtin_amdgcn_sched_barrier(0);
-    for (int64_t i = threadIdx.x; i < K / 4; i += kStreamThreads) {
-        *reinterpret_cast<float4*>(xs + XPad(4 * i)) = reinterpret_cast<const float4*>(x)[i];
+    if (a.norm.weight != nullptr) {  // x's RMSNorm (the same thread stages and scales each float4)
+        __shared__ double wsum[16];
+        StageNorm(a.norm, x, K, xs, wsum);
+    } else {
+        for (int64_t i = threadIdx.x; i < K / 4; i += kStreamThreads) {
+            *reinterpret_cast<float4*>(xs + XPad(4 * i)) = reinterpret_cast<const float4*>(x)[i];
+        }
     }
     // q/k/v RoPE: the (cos, sin) of every pair index of a head, after x in
     // LDS, computed once per workgroup while the first steps load (the
@@ -975,6 +1067,13 @@ mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& 
     }
     if (mode == kStreamQkvRope && (!QkvRopeArgsOk(a) || !StreamRopeFits(K, a.rope.head_dim))) {
         return Fail(MLK_ERR_INVALID, "linear (one row): bad q/k/v RoPE segments");
+    }
+    const StreamNorm& n = a.norm;
+    if (n.weight != nullptr &&
+        ((n.waves != 8 && n.waves != 16) || n.vpt < 1 || n.vpt > kNormVpt ||
+         K / 4 > static_cast<int64_t>(n.vpt) * kWave * n.waves || !Aligned(n.weight, 16) ||
+         !Aligned(n.delta, 16) || !Aligned(n.res_out, 16) || !(n.eps > 0.0f))) {
+        return Fail(MLK_ERR_INVALID, "linear (one row): bad input RMSNorm");
     }
     const int64_t row_bytes = (K / 32) * BlockBytes(qt);
     switch (qt) {

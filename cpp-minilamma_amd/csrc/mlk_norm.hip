@@ -180,6 +180,16 @@ __global__ __launch_bounds__(kThreads) void AddRmsNormAny(float* residual,
     }
 }
 
+// AddRmsNormVec's block for rows of dim floats: waves doubled up to 16
+// while the row has more float4s than threads, then float4s per thread.
+void NormShapeOf(int64_t dim, int* waves, int* vpt) {
+    const int64_t dim4 = dim / 4;
+    int w = 1;
+    while (w < 16 && static_cast<int64_t>(w) * kWave < dim4) w *= 2;
+    *waves = w;
+    *vpt = static_cast<int>((dim4 + w * kWave - 1) / (w * kWave));
+}
+
 bool VecApplies(const float* residual, const float* delta, const float* weight, const float* y,
                 int64_t dim) {
     return (dim % 4) == 0 && dim / 4 <= 1024 * 8 && Aligned(residual, 16) &&
@@ -192,13 +202,9 @@ mlk_status Launch(float* residual, const float* delta, const float* weight, floa
                   uint32_t* planes = nullptr, int splits = 1, const float* dbias = nullptr) {
     const unsigned grid = FullGrid(n_rows, 1);
     const bool vec = VecApplies(residual, kDelta ? delta : nullptr, weight, y, dim);
-    const int64_t dim4 = dim / 4;
     if (vec) {  // beyond 8 float4 per lane the row would spill
-        // waves: the smallest power of two covering the row one float4 per
-        // lane, at most 16; then float4 per lane
-        int64_t waves = 1;
-        while (waves < 16 && waves * kWave < dim4) waves *= 2;
-        const int64_t vpt = (dim4 + waves * kWave - 1) / (waves * kWave);
+        int waves = 0, vpt = 0;
+        NormShapeOf(dim, &waves, &vpt);
 #define MLK_NORM_CASE(W, V)                                                                    \
     if (waves == (W) && vpt <= (V)) {                                                         \
         hipLaunchKernelGGL((AddRmsNormVec<W, V, kDelta, kWriteBack, kPlanes, kPartials>),      \
@@ -242,6 +248,13 @@ mlk_status CheckNormArgs(const char* caller, const void* x, const void* weight, 
 }
 
 }  // namespace
+
+bool NormShape(const float* residual, const float* delta, const float* weight, const float* y,
+               int64_t dim, int* waves, int* vpt) {
+    if (!VecApplies(residual, delta, weight, y, dim)) return false;
+    NormShapeOf(dim, waves, vpt);
+    return *vpt <= 8;
+}
 
 bool NormPlanesApplies(const float* residual, const float* delta, const float* weight,
                        const float* y, int64_t dim) {

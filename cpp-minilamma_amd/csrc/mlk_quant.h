@@ -98,9 +98,25 @@ struct RopeArgs {
     RopeFreqs freq;             // inverse frequencies of the head's pairs
 };
 
+// The one-token streaming GEMV can take its input as the RMSNorm of a
+// residual row (plus delta), staged straight into its LDS: the same float64
+// sums in the same order as AddRmsNormVec's block of `waves` waves with
+// `vpt` float4s per thread (NormShape), so the staged row equals that
+// kernel's output bit for bit.  res_out (when set) receives x + delta from
+// workgroup 0 (the residual stream's next value, which x itself cannot take
+// while other workgroups still read it).
+struct StreamNorm {
+    const float* weight = nullptr;  // null: no norm, the GEMV reads x as is
+    const float* delta = nullptr;
+    float* res_out = nullptr;
+    float eps = 0.0f;
+    int waves = 0, vpt = 0;
+};
+
 struct StreamArgs {
     StreamSeg seg[3];
     int n_seg;
+    StreamNorm norm;  // the input row's RMSNorm (LinearRowStream only)
     RopeArgs rope;  // kStreamQkvRope only
     // kStreamSwiGlu of the planar launches only: when set, the SwiGLU
     // outputs also go here as bf16 planes (StorePlanes, mlk_common.h) for
@@ -169,6 +185,10 @@ mlk_status LinearPlanarFused(int qt, const float* x, int64_t T, int64_t K, const
 // SplitKReduce would.
 bool NormPlanesApplies(const float* residual, const float* delta, const float* weight,
                        const float* y, int64_t dim);
+// AddRmsNormVec's block for rows of dim floats (false: another kernel takes
+// such rows, or a pointer is not 16-byte aligned)
+bool NormShape(const float* residual, const float* delta, const float* weight, const float* y,
+               int64_t dim, int* waves, int* vpt);
 mlk_status AddRmsNormPlanes(float* residual, const float* delta, const float* weight, float* y,
                             uint32_t* planes, int64_t n_rows, int64_t dim, float eps,
                             hipStream_t s, int splits = 1, const float* dbias = nullptr);

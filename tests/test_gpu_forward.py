@@ -265,6 +265,62 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
 
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+@pytest.mark.parametrize("D,F", [(2048, 1024), (4096, 1024), (6144, 512), (8192, 512)])
+def test_one_token_norms_folded_equal_op_by_op(mlk, fwd, wt, D, F):
+    """One token with dim 2048..8192: both RMSNorms are staged inside the
+    streaming q/k/v and gate/up launches (the norm kernel's block of 8 or 16
+    waves with one or two float4s per thread, the second partly used at
+    6144, emulated there: its float64 sums in the same order), and the
+    residual x + proj reaches the down projection through the h buffer.  The
+    layer equals the separate entry points bit for bit."""
+    S, H, KV, hd, pos = 256, 16, 4, 128, 200
+    cfg = dict(vocab=64, dim=D, hidden_dim=F, layers=1, n_heads=H, n_kv_heads=KV,
+               head_dim=hd, max_seq=S, rope_type=0, theta=500000.0, eps=1e-5)
+    model = O.forward_model(cfg, seed=D + F, weight_type=wt, biases=False)
+    QD, KD = H * hd, KV * hd
+    lw = model["layers"][0]
+    dm = fwd.DeviceModel(model)
+    rng = np.random.default_rng(D)
+    x0 = (rng.standard_normal((1, D)) * 3).astype(np.float32)
+    kc0 = (rng.standard_normal((1, S, KV, hd)) * 0.5).astype(np.float32)
+    vc0 = rng.standard_normal((1, S, KV, hd)).astype(np.float32)
+    B = mlk.DeviceBuffer.from_array
+    x, kc, vc = B(x0), B(kc0), B(vc0)
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, S, True), np.uint8)
+    fwd.forward_layer_batch(cfg, dm.layers[0], x, 1, kc, vc, 1, S, 0, S, ws, pos0=pos)
+    got = x.download()
+
+    def up(a):
+        return B(np.ascontiguousarray(a))
+    w = {n: up(np.asarray(lw[n][1], np.uint8)) for n in fwd.LINEAR_NAMES}
+    an, fn = up(np.asarray(lw["attention_norm"], np.float32)), up(np.asarray(lw["ffn_norm"], np.float32))
+    x2, kc2, vc2 = B(x0), B(kc0), B(vc0)
+    e = mlk.DeviceBuffer.empty
+    h, q, k, v, a, proj = e((1, D)), e((1, QD)), e((1, KD)), e((1, KD)), e((1, QD)), e((1, D))
+    g, u = e((1, F)), e((1, F))
+    mlk.rmsnorm(x2, an, h, 1, D, cfg["eps"])
+    mlk.linear_quant(wt, h, w["wq"], q, 1, D, QD)
+    mlk.linear_quant(wt, h, w["wk"], k, 1, D, KD)
+    mlk.linear_quant(wt, h, w["wv"], v, 1, D, KD)
+    mlk.rope(q, k, 1, H, KV, hd, pos0=pos, theta=cfg["theta"], rope_type=0)
+    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, 1, pos0=pos)
+    nws = mlk.attention_workspace_bytes(1, H, KV, hd, S)
+    aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
+    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, 1, a, S, pos0=pos, workspace=aws,
+                         workspace_bytes=aws.nbytes)
+    mlk.linear_quant(wt, a, w["wo"], proj, 1, QD, D)
+    mlk.add_rmsnorm(x2, proj, fn, h, 1, D, cfg["eps"])
+    mlk.linear_quant(wt, h, w["w_gate"], g, 1, D, F)
+    mlk.linear_quant(wt, h, w["w_up"], u, 1, D, F)
+    mlk.swiglu(g, u, g, F)
+    mlk.linear_quant(wt, g, w["w_down"], proj, 1, F, D)
+    mlk.add(x2, proj, x2, D)
+    np.testing.assert_array_equal(got, x2.download())
+    np.testing.assert_array_equal(kc.download(), kc2.download())
+    np.testing.assert_array_equal(vc.download(), vc2.download())
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
 @pytest.mark.parametrize("T", [2, 12, 24])
 @pytest.mark.parametrize("case", ["pos0", "positions", "bad_position", "neox"])
 def test_layer_planar_equals_op_by_op(mlk, fwd, wt, T, case):
