@@ -179,9 +179,12 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     load(p_begin);
     store(0);
     __syncthreads();
+    // positions fit in 32 bits (below max_seq); log2-unit score scale
+    const int32_t my_pos_32 = static_cast<int32_t>(my_pos);
+    const float scale2 = scale * 1.44269504088896340736f;
     for (int64_t it = 0; it < n_tiles; ++it) {
         const int buf = static_cast<int>(it & 1);
-        const int64_t p0 = p_begin + it * kPfTile;
+        const int32_t p0_32 = static_cast<int32_t>(p_begin + it * kPfTile);
         load(p_begin + (it + 1 < n_tiles ? it + 1 : it) * kPfTile);
         // Nothing crosses this point: without it the scheduler sinks the
         // next tile's global loads to their LDS stores at the bottom of the
@@ -209,8 +212,9 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
             for (int pt = 0; pt < 2; ++pt) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int64_t pos = p0 + pt * 16 + 4 * kq + r;
-                    const float x = pos <= my_pos ? s[pt][r] * scale : -INFINITY;
+                    // scores in log2 units (scale * log2(e)), for exp2 below
+                    const int32_t pos = p0_32 + pt * 16 + 4 * kq + r;
+                    const float x = pos <= my_pos_32 ? s[pt][r] * scale2 : -INFINITY;
                     sv[pt * 4 + r] = x;
                     tmax = fmaxf(tmax, x);
                 }
@@ -223,14 +227,18 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
             // reads that partial).
             const float mnew = fmaxf(m, tmax);
             const float mref = kChunked && mnew == -INFINITY ? 0.0f : mnew;
-            const float corr = expf(m - mref);
-            l *= corr;
+            // rescale only when some query's max moved (the factor is then
+            // exactly 1 for the others: skipping it changes nothing)
+            if (__builtin_amdgcn_ballot_w64(mnew != m) != 0) {
+                const float corr = __builtin_amdgcn_exp2f(m - mref);
+                l *= corr;
 #pragma unroll
-            for (int c = 0; c < NC; ++c) acc[c] *= corr;
+                for (int c = 0; c < NC; ++c) acc[c] *= corr;
+            }
             float pv[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                pv[i] = expf(sv[i] - mref);
+                pv[i] = __builtin_amdgcn_exp2f(sv[i] - mref);
                 l += pv[i];
             }
             m = mnew;
@@ -262,8 +270,8 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
                 *reinterpret_cast<float4*>(arow + 16 * cc) =
                     make_float4(acc[cc][0], acc[cc][1], acc[cc][2], acc[cc][3]);
             }
-            if (kq == 0) {
-                tc.ws_ml[(row * tc.n_chunks + ck) * 2] = m;
+            if (kq == 0) {  // the max back in natural-log units, as AttnCombine takes it
+                tc.ws_ml[(row * tc.n_chunks + ck) * 2] = m * 0.69314718055994530942f;
                 tc.ws_ml[(row * tc.n_chunks + ck) * 2 + 1] = l;
             }
             return;
