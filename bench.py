@@ -758,7 +758,9 @@ LAYER_LOOP_SAMPLE = 64  # tokens of the token-by-token comparison
 def _device_layer(mlk, fwd, cfg, wt, seed):
     """One Llama-3-8B-shaped layer's weights on the device (N(0, 0.02),
     quantized on the device; norm weights N(1, 0.1)) as LayerWeights, plus
-    the buffers that hold them."""
+    the buffers that hold them.  Q8_0 / Q4_0 weights also get a planar copy
+    (mlk_quant_to_planar), which calls of 2..32 tokens run on; one token
+    reads the blocks."""
     D, F = cfg["dim"], cfg["hidden_dim"]
     QD, KD = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
     shapes = {"wq": (QD, D), "wk": (KD, D), "wv": (KD, D), "wo": (D, QD), "w_gate": (F, D),
