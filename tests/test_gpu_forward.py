@@ -176,8 +176,8 @@ def test_forward_layer_rejects_cache_arguments(mlk, fwd):
         assert_bits_equal(x2.download(), before, f"x untouched (rope {rope_type}, {wt}, T {T})")
 
 
-@pytest.mark.parametrize("wt", ["q8_0", "q4_0", "q4_1"])
-@pytest.mark.parametrize("T", [1, 12, 24])
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0", "q4_1", "f32"])
+@pytest.mark.parametrize("T", [1, 12, 24, 40])
 @pytest.mark.parametrize("case", ["pos0", "positions", "bad_position", "neox"])
 def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
     """One token (streaming GEMVs) and 8..32 tokens (skinny GEMMs) through a
@@ -193,7 +193,8 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
     attention output zero); the NeoX layout (separate RoPE and K/V write).
     The cache spans several attention chunks, so the decode attention's
     in-kernel merge of them (after the fused q/k/v launch) is compared with
-    the separate merge launch."""
+    the separate merge launch.  40 tokens (and F32 weights from 8 rows) take
+    the matrix-core GEMM and the separate SwiGLU and residual-add launches."""
     S = 1024
     cfg = dict(vocab=64, dim=512, hidden_dim=1536, layers=1, n_heads=8, n_kv_heads=2,
                head_dim=64, max_seq=S, rope_type=1 if case == "neox" else 0, theta=10000.0,
@@ -228,17 +229,24 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
     # the same layer op by op
     def up(a):
         return B(np.ascontiguousarray(a))
-    w = {n: up(np.asarray(lw[n][1], np.uint8)) for n in fwd.LINEAR_NAMES}
+    w = {n: up(np.asarray(lw[n][1], np.float32 if wt == "f32" else np.uint8))
+         for n in fwd.LINEAR_NAMES}
     bias = {n: up(np.asarray(lw["b" + n[1]], np.float32)) for n in ("wq", "wk", "wv")}
     an, fn = up(np.asarray(lw["attention_norm"], np.float32)), up(np.asarray(lw["ffn_norm"], np.float32))
     x2, kc2, vc2 = B(x0), B(kc0), B(vc0)
+
+    def linear(name, x_in, y_out, rows, i, o, b=None):
+        if wt == "f32":
+            mlk.linear_f32(x_in, w[name], y_out, rows, i, o, bias=b)
+        else:
+            mlk.linear_quant(wt, x_in, w[name], y_out, rows, i, o, bias=b)
     e = mlk.DeviceBuffer.empty
     h, q, k, v, a, proj = e((T, D)), e((T, QD)), e((T, KD)), e((T, KD)), e((T, QD)), e((T, D))
     g, u = e((T, F)), e((T, F))
     mlk.rmsnorm(x2, an, h, T, D, cfg["eps"])
-    mlk.linear_quant(wt, h, w["wq"], q, T, D, QD, bias=bias["wq"])
-    mlk.linear_quant(wt, h, w["wk"], k, T, D, KD, bias=bias["wk"])
-    mlk.linear_quant(wt, h, w["wv"], v, T, D, KD, bias=bias["wv"])
+    linear("wq", h, q, T, D, QD, bias["wq"])
+    linear("wk", h, k, T, D, KD, bias["wk"])
+    linear("wv", h, v, T, D, KD, bias["wv"])
     mlk.rope(q, k, T, H, KV, hd, positions=positions, pos0=pos, theta=cfg["theta"],
              rope_type=cfg["rope_type"], err=flag2)
     mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, positions=positions, pos0=pos, err=flag2)
@@ -246,12 +254,12 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
     aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
     mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, positions=positions,
                          pos0=pos, workspace=aws, workspace_bytes=aws.nbytes, err=flag2)
-    mlk.linear_quant(wt, a, w["wo"], proj, T, QD, D)
+    linear("wo", a, proj, T, QD, D)
     mlk.add_rmsnorm(x2, proj, fn, h, T, D, cfg["eps"])
-    mlk.linear_quant(wt, h, w["w_gate"], g, T, D, F)
-    mlk.linear_quant(wt, h, w["w_up"], u, T, D, F)
+    linear("w_gate", h, g, T, D, F)
+    linear("w_up", h, u, T, D, F)
     mlk.swiglu(g, u, g, T * F)
-    mlk.linear_quant(wt, g, w["w_down"], proj, T, F, D)
+    linear("w_down", g, proj, T, F, D)
     mlk.add(x2, proj, x2, T * D)
     want = x2.download()
     np.testing.assert_array_equal(got, want)
