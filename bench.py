@@ -17,7 +17,10 @@ events recorded on the stream the kernels run on.
 The same run measures the other configs of BASELINE.json into "configs":
 configs[0] (the tiny chain), configs[1] (decode steps at T = 1..64, eager
 and graph-replayed), configs[3] (Q8_0/Q4_0/Q4_1 gathers) and configs[4]
-(the 70B chain), each beside the reference's CPU code timed on this host.
+(the 70B chain), each beside the reference's CPU code timed on this host;
+and "decode_layer_8b": one Llama-3-8B layer through mlk_forward_layer_batch
+as a decode step (one token at position 8191, and 16 tokens at positions in
+0..8191 on planar weights), Q8_0 / Q4_0 / F32, weights rotated over 4 layers.
 Before each measured section a ZeroKernel launch of 4096 * (100 + i) bytes
 marks section i in a rocprofv3 trace (bench.py --rocprof-report uses it).
 
@@ -872,7 +875,7 @@ DECODE_POS = 8191   # the token's position: it attends to 8192 cache rows
 DECODE_BATCH = 16   # tokens of the batched decode case (configs[1] positions)
 
 
-def decode_layer_bench(mlk, fwd, steps):
+def decode_layer_bench(mlk, fwd, steps, log=sys.stdout):
     """One decode step of one Llama-3-8B layer through mlk_forward_layer_batch:
     a single token at position 8191 (the top of configs[1]'s position
     range), and a batch of DECODE_BATCH tokens at positions uniform in
@@ -933,7 +936,7 @@ def decode_layer_bench(mlk, fwd, steps):
                         "tokens_per_s_32_layers": round(T * 1e6 / (32 * us), 1)}
             where = f"at position {DECODE_POS}" if T == 1 else "at positions uniform in 0..8191"
             print(f"decode layer {wt}, {T} token(s) {where}: {us:.1f} us ({gbs:.0f} GB/s, "
-                  f"{T * 1e6 / (32 * us):.0f} tokens/s over 32 layers)", flush=True)
+                  f"{T * 1e6 / (32 * us):.0f} tokens/s over 32 layers)", file=log, flush=True)
         del layers
     return res
 
@@ -1486,6 +1489,12 @@ def main():
     configs["c4_quant_gather"] = c4_gathers(mlk, args.steps, peak, marks, with_cpu)
     configs["c5_70b"] = c5_chain(mlk, args.steps, args.warmup, peak, marks, with_cpu)
     result["configs"] = configs
+    # beside the op chain: one 8B layer through mlk_forward_layer_batch as a
+    # decode step (one token at position 8191; 16 tokens at positions in
+    # 0..8191 on the planar weights), weights rotated over 4 layers
+    import importlib
+    fwd = importlib.import_module(mlk.__name__ + ".forward")
+    result["decode_layer_8b"] = decode_layer_bench(mlk, fwd, min(args.steps, 10), log=sys.stderr)
     print(json.dumps(result))
 
 
