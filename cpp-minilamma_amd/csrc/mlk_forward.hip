@@ -137,6 +137,18 @@ bool Planar(int64_t T, int64_t in, std::initializer_list<const mlk_linear_weight
     return true;
 }
 
+// One token over planar copies (LinearRowPlanar): all Q8_0 or all Q4_0 with
+// planar copies, in_features within the kernel's reach for `mode`.
+bool PlanarRow(int64_t in, std::initializer_list<const mlk_linear_weight*> ws,
+               int mode = kStreamPlain, bool norm = false) {
+    const int t = (*ws.begin())->type;
+    if ((t != MLK_Q8_0 && t != MLK_Q4_0) || !RowPlanarApplies(t, in, mode, norm)) return false;
+    for (const mlk_linear_weight* w : ws) {
+        if (w->type != t || w->planar == nullptr) return false;
+    }
+    return true;
+}
+
 StreamSeg PlanarSeg(const mlk_linear_weight& w, float* y, int64_t rows,
                     const float* res = nullptr) {
     return StreamSeg{static_cast<const uint8_t*>(w.planar), w.bias, y, res, rows, 0};
@@ -260,16 +272,23 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     // One token (the decode step) with quantized weights: q, k and v in one
     // launch, gate and up with SwiGLU in the epilogue, and the down
     // projection adding into x (the same per-element arithmetic as the
-    // separate kernels).  8..32 tokens: the same groups as skinny GEMM
-    // launches, with the epilogues in their split-K reductions.
+    // separate kernels), over the planar copies where a group has them
+    // (contiguous loads), else over the blocks.  8..32 tokens: the same
+    // groups as skinny GEMM launches, with the epilogues in their split-K
+    // reductions.
     const hipStream_t hs = AsStream(stream);
     const bool row = T == 1;
-    const bool qkv1 = row && w->wq.type == w->wk.type && w->wq.type == w->wv.type &&
-                      RowStreamable(w->wq, D) && RowStreamable(w->wk, D) &&
-                      RowStreamable(w->wv, D);
-    const bool ffn1 = row && w->w_gate.type == w->w_up.type && RowStreamable(w->w_gate, D) &&
-                      RowStreamable(w->w_up, D);
-    const bool down1 = row && RowStreamable(w->w_down, F);
+    // one token on planar copies: the same launches over the planar layout
+    const bool qkv1p = row && PlanarRow(D, {&w->wq, &w->wk, &w->wv}, kStreamQkvRope);
+    const bool ffn1p = row && PlanarRow(D, {&w->w_gate, &w->w_up}, kStreamSwiGlu);
+    const bool down1p = row && PlanarRow(F, {&w->w_down}, kStreamAdd);
+    const bool wo1p = row && PlanarRow(QD, {&w->wo});
+    const bool qkv1 = qkv1p || (row && w->wq.type == w->wk.type && w->wq.type == w->wv.type &&
+                                RowStreamable(w->wq, D) && RowStreamable(w->wk, D) &&
+                                RowStreamable(w->wv, D));
+    const bool ffn1 = ffn1p || (row && w->w_gate.type == w->w_up.type &&
+                                RowStreamable(w->w_gate, D) && RowStreamable(w->w_up, D));
+    const bool down1 = down1p || (row && RowStreamable(w->w_down, F));
     // 2..32 tokens on planar copies: the same three groups, plus wo
     const bool qkvp = Planar(T, D, {&w->wq, &w->wk, &w->wv});
     const bool ffnp = Planar(T, D, {&w->w_gate, &w->w_up});
@@ -286,7 +305,7 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     // The fused q/k/v launches also rotate q and k (normal-layout pairs) and
     // write k and v into the cache rows, in place of mlk_rope_f32 and
     // mlk_kv_write_f32; the NeoX layout keeps the separate launches.
-    const bool rope_fused = (qkvm || (qkv1 && StreamRopeFits(D, c.head_dim))) &&
+    const bool rope_fused = (qkvm || qkv1p || (qkv1 && StreamRopeFits(D, c.head_dim))) &&
                             c.rope_type == MLK_ROPE_NORMAL && c.head_dim % 2 == 0 &&
                             c.head_dim <= 2 * kRopePairs;
     if (rope_fused && positions == nullptr && (pos0 < 0 || pos0 + T > max_seq)) {
@@ -300,8 +319,12 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     int nw = 0, nvpt = 0;
     const bool norm_fold = NormShape(x, proj, w->attention_norm, h, D, &nw, &nvpt) &&
                            Aligned(w->ffn_norm, 16) && (nw == 8 || nw == 16) && nvpt <= 2;
-    const bool attn_fold = qkv1 && norm_fold;
-    const bool ffn_fold = ffn1 && down1 && norm_fold;
+    const bool attn_fold =
+        qkv1 && norm_fold &&
+        (!qkv1p || RowPlanarApplies(w->wq.type, D, rope_fused ? kStreamQkvRope : kStreamPlain,
+                                    true));
+    const bool ffn_fold = ffn1 && down1 && norm_fold &&
+                          (!ffn1p || RowPlanarApplies(w->w_gate.type, D, kStreamSwiGlu, true));
     // planar q/k/v: the norm also writes h's bf16 planes (no split launch)
     const uint32_t* h_planes = nullptr;
     if (attn_fold) {
@@ -317,18 +340,21 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         float* ky = rope_fused ? k_cache + layer * max_seq * slot : k;
         float* vy = rope_fused ? v_cache + layer * max_seq * slot : v;
         StreamArgs a{};
-        a.seg[0] = qkvp ? PlanarSeg(w->wq, q, QD) : Seg(w->wq, q, QD);
-        a.seg[1] = qkvp ? PlanarSeg(w->wk, ky, KD) : Seg(w->wk, ky, KD);
-        a.seg[2] = qkvp ? PlanarSeg(w->wv, vy, KD) : Seg(w->wv, vy, KD);
+        const bool pl = qkvp || qkv1p;
+        a.seg[0] = pl ? PlanarSeg(w->wq, q, QD) : Seg(w->wq, q, QD);
+        a.seg[1] = pl ? PlanarSeg(w->wk, ky, KD) : Seg(w->wk, ky, KD);
+        a.seg[2] = pl ? PlanarSeg(w->wv, vy, KD) : Seg(w->wv, vy, KD);
         a.n_seg = 3;
         a.rope = RopeArgs{positions, pos0, c.head_dim, slot, max_seq, err,
                           MakeRopeFreqs(c.rope_theta, c.head_dim)};
         const int mode = rope_fused ? kStreamQkvRope : kStreamPlain;
         if (qkv1 && attn_fold) {
             a.norm = StreamNorm{w->attention_norm, nullptr, nullptr, eps, nw, nvpt};
-            MLK_TRY(LinearRowStream(w->wq.type, x, D, a, mode, hs));
+            MLK_TRY(qkv1p ? LinearRowPlanar(w->wq.type, x, D, a, mode, hs)
+                          : LinearRowStream(w->wq.type, x, D, a, mode, hs));
         } else if (qkv1) {
-            MLK_TRY(LinearRowStream(w->wq.type, h, D, a, mode, hs));
+            MLK_TRY(qkv1p ? LinearRowPlanar(w->wq.type, h, D, a, mode, hs)
+                          : LinearRowStream(w->wq.type, h, D, a, mode, hs));
         } else if (qkvp) {
             MLK_TRY(LinearPlanarFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs, h_planes));
         } else {
@@ -371,6 +397,11 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         if (wop) {
             MLK_TRY(LinearPlanar(w->wo.type, a, w->wo.planar, w->wo.bias, proj, T, QD, D, lin_ws,
                                  lin_b, hs, a_planes ? planes : nullptr));
+        } else if (wo1p) {
+            StreamArgs sa{};
+            sa.seg[0] = PlanarSeg(w->wo, proj, D);
+            sa.n_seg = 1;
+            MLK_TRY(LinearRowPlanar(w->wo.type, a, QD, sa, kStreamPlain, hs));
         } else {
             MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
         }
@@ -384,15 +415,16 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     const uint32_t* g_planes = nullptr;
     if (ffn1) {
         StreamArgs a{};
-        a.seg[0] = Seg(w->w_gate, gate, F);
-        a.seg[1] = Seg(w->w_up, gate, F);
+        a.seg[0] = ffn1p ? PlanarSeg(w->w_gate, gate, F) : Seg(w->w_gate, gate, F);
+        a.seg[1] = ffn1p ? PlanarSeg(w->w_up, gate, F) : Seg(w->w_up, gate, F);
         a.n_seg = 2;
+        const float* in = h;
         if (ffn_fold) {  // RMSNorm(x + proj) staged in the launch; x + proj into h's buffer
             a.norm = StreamNorm{w->ffn_norm, proj, h, eps, nw, nvpt};
-            MLK_TRY(LinearRowStream(w->w_gate.type, x, D, a, kStreamSwiGlu, hs));
-        } else {
-            MLK_TRY(LinearRowStream(w->w_gate.type, h, D, a, kStreamSwiGlu, hs));
+            in = x;
         }
+        MLK_TRY(ffn1p ? LinearRowPlanar(w->w_gate.type, in, D, a, kStreamSwiGlu, hs)
+                      : LinearRowStream(w->w_gate.type, in, D, a, kStreamSwiGlu, hs));
     } else if (ffnp) {
         // the SwiGLU epilogue also writes the planes of its output for a
         // planar down projection (over h's planes: the GEMM has read them)
@@ -417,9 +449,11 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     }
     if (down1) {
         StreamArgs a{};
-        a.seg[0] = Seg(w->w_down, x, D, ffn_fold ? h : x);  // x = (x + proj) + down
+        const float* res = ffn_fold ? h : x;  // x = (x + proj) + down
+        a.seg[0] = down1p ? PlanarSeg(w->w_down, x, D, res) : Seg(w->w_down, x, D, res);
         a.n_seg = 1;
-        MLK_TRY(LinearRowStream(w->w_down.type, gate, F, a, kStreamAdd, hs));
+        MLK_TRY(down1p ? LinearRowPlanar(w->w_down.type, gate, F, a, kStreamAdd, hs)
+                       : LinearRowStream(w->w_down.type, gate, F, a, kStreamAdd, hs));
     } else if (downp) {
         StreamArgs a{};
         a.seg[0] = PlanarSeg(w->w_down, x, D, x);

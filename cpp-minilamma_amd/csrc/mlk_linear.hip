@@ -713,86 +713,105 @@ __device__ inline void StreamFinish(float (&acc)[R][1], const StreamArgs& a, con
 // tid + 512 j of its 64 * waves (waves 8 or 16), each summing the squares
 // of its float4s vt, vt + 64 * waves (vpt of them, at most 2) in order, in
 // float64; each virtual wave's sum by the same butterfly, then the wave
-// sums in order; each float4 then scaled as that kernel scales it.  Every
-// load (x, delta, the norm weight) is issued before the reduction.
+// sums in order; each float4 then scaled as that kernel scales it.  Load()
+// issues every load (x, delta, the norm weight); Finish() waits for them,
+// reduces (one barrier) and writes xs, so a caller can issue loads of its
+// own in between.  VPT: float4s per norm thread held (n.vpt <= VPT).
 constexpr int kNormVpt = 2;  // float4s per norm thread the staging handles
 
-__device__ void StageNorm(const StreamNorm& n, const float* x, int64_t K, float* xs,
-                          double* wsum) {
-#pragma clang fp contract(off)
-    constexpr int NJ = 1024 / kStreamThreads;  // virtual threads per thread, at most
-    const int nv = kWave * n.waves;
-    const int64_t dim4 = K / 4;
-    const int tid = threadIdx.x, lane = tid % kWave, rw = tid / kWave;
-    const bool writer = blockIdx.x == 0 && n.res_out != nullptr;
-    float4 r[NJ][kNormVpt], w[NJ][kNormVpt];
-    bool ok[NJ][kNormVpt];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-        for (int v = 0; v < kNormVpt; ++v) {
-            const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
-            ok[j][v] = j * kStreamThreads < nv && v < n.vpt && i < dim4;
-            r[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(x)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            w[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(n.weight)[i]
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+template <int VPT = kNormVpt>
+struct NormStager {
+    static constexpr int NJ = 1024 / kStreamThreads;  // virtual threads per thread, at most
+    float4 r[NJ][VPT], w[NJ][VPT], d[NJ][VPT];
+    bool ok[NJ][VPT];
+
+    __device__ int64_t Index(const StreamNorm& n, int j, int v) const {
+        return threadIdx.x + j * kStreamThreads + static_cast<int64_t>(v) * (kWave * n.waves);
     }
-    if (n.delta != nullptr) {
+
+    __device__ void Load(const StreamNorm& n, const float* x, int64_t K) {
+        const int nv = kWave * n.waves;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-            for (int v = 0; v < kNormVpt; ++v) {
-                const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
+            for (int v = 0; v < VPT; ++v) {
+                const int64_t i = Index(n, j, v);
+                ok[j][v] = j * kStreamThreads < nv && v < n.vpt && i < K / 4;
+                r[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(x)[i]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                w[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(n.weight)[i]
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                d[j][v] = ok[j][v] && n.delta != nullptr
+                              ? reinterpret_cast<const float4*>(n.delta)[i]
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    }
+
+    __device__ void Finish(const StreamNorm& n, int64_t K, float* xs, double* wsum) {
+#pragma clang fp contract(off)
+        const int nv = kWave * n.waves;
+        const int lane = threadIdx.x % kWave, rw = threadIdx.x / kWave;
+        const bool writer = blockIdx.x == 0 && n.res_out != nullptr;
+        if (n.delta != nullptr) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+                for (int v = 0; v < VPT; ++v) {
+                    r[j][v].x += d[j][v].x;
+                    r[j][v].y += d[j][v].y;
+                    r[j][v].z += d[j][v].z;
+                    r[j][v].w += d[j][v].w;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            if (j * kStreamThreads >= nv) break;
+            double ss = 0.0;
+#pragma unroll
+            for (int v = 0; v < VPT; ++v) {
                 if (ok[j][v]) {
-                    const float4 d = reinterpret_cast<const float4*>(n.delta)[i];
-                    r[j][v].x += d.x;
-                    r[j][v].y += d.y;
-                    r[j][v].z += d.z;
-                    r[j][v].w += d.w;
+                    if (writer) reinterpret_cast<float4*>(n.res_out)[Index(n, j, v)] = r[j][v];
+                    const double a = r[j][v].x, b = r[j][v].y, c = r[j][v].z, e = r[j][v].w;
+                    ss += a * a;
+                    ss += b * b;
+                    ss += c * c;
+                    ss += e * e;
+                }
+            }
+            ss = WaveSum(ss);
+            if (lane == 0) wsum[rw + j * kStreamWaves] = ss;
+        }
+        __syncthreads();
+        double total = 0.0;
+        for (int k = 0; k < n.waves; ++k) total += wsum[k];
+        const double scale =
+            1.0 / sqrt(total / static_cast<double>(K) + static_cast<double>(n.eps));
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+#pragma unroll
+            for (int v = 0; v < VPT; ++v) {
+                if (ok[j][v]) {
+                    const float4 a = r[j][v], b = w[j][v];
+                    float4 o;
+                    o.x = static_cast<float>(static_cast<double>(a.x) * static_cast<double>(b.x) * scale);
+                    o.y = static_cast<float>(static_cast<double>(a.y) * static_cast<double>(b.y) * scale);
+                    o.z = static_cast<float>(static_cast<double>(a.z) * static_cast<double>(b.z) * scale);
+                    o.w = static_cast<float>(static_cast<double>(a.w) * static_cast<double>(b.w) * scale);
+                    *reinterpret_cast<float4*>(xs + XPad(4 * Index(n, j, v))) = o;
                 }
             }
         }
     }
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        if (j * kStreamThreads >= nv) break;
-        double ss = 0.0;
-#pragma unroll
-        for (int v = 0; v < kNormVpt; ++v) {
-            const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
-            if (ok[j][v]) {
-                if (writer) reinterpret_cast<float4*>(n.res_out)[i] = r[j][v];
-                const double a = r[j][v].x, b = r[j][v].y, c = r[j][v].z, d = r[j][v].w;
-                ss += a * a;
-                ss += b * b;
-                ss += c * c;
-                ss += d * d;
-            }
-        }
-        ss = WaveSum(ss);
-        if (lane == 0) wsum[rw + j * kStreamWaves] = ss;
-    }
-    __syncthreads();
-    double total = 0.0;
-    for (int k = 0; k < n.waves; ++k) total += wsum[k];
-    const double scale = 1.0 / sqrt(total / static_cast<double>(K) + static_cast<double>(n.eps));
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-#pragma unroll
-        for (int v = 0; v < kNormVpt; ++v) {
-            const int64_t i = tid + j * kStreamThreads + static_cast<int64_t>(v) * nv;
-            if (ok[j][v]) {
-                const float4 a = r[j][v], b = w[j][v];
-                float4 o;
-                o.x = static_cast<float>(static_cast<double>(a.x) * static_cast<double>(b.x) * scale);
-                o.y = static_cast<float>(static_cast<double>(a.y) * static_cast<double>(b.y) * scale);
-                o.z = static_cast<float>(static_cast<double>(a.z) * static_cast<double>(b.z) * scale);
-                o.w = static_cast<float>(static_cast<double>(a.w) * static_cast<double>(b.w) * scale);
-                *reinterpret_cast<float4*>(xs + XPad(4 * i)) = o;
-            }
-        }
-    }
+};
+
+template <int VPT = kNormVpt>
+__device__ void StageNorm(const StreamNorm& n, const float* x, int64_t K, float* xs,
+                          double* wsum) {
+    NormStager<VPT> st;
+    st.Load(n, x, K);
+    st.Finish(n, K, xs, wsum);
 }
 
 // x and the weights are not __restrict__: loads through restrict-qualified
@@ -894,6 +913,353 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, 
                 cur.Advance<MODE>(a, passes, R);
             }
         }
+    }
+}
+
+// ------------------------------------------------ one token, planar weights
+// One token row over Q8_0 / Q4_0 weights in the planar layout
+// (mlk_quant_to_planar), with GemvStream's modes and epilogues (StreamArgs):
+//   - a workgroup owns one or two 16-row tiles (SwiGLU: the gate and the up
+//     tile of the same rows, waves [0, nwm) on gate and [nwm, 2 nwm) on up);
+//     its waves split each tile's K into 256-input chunks, ncw consecutive
+//     chunks per wave;
+//   - a chunk is 4 KB (Q8_0) or 2 KB (Q4_0) of codes, each load 1 KB
+//     contiguous per wave, plus 16 bytes of scales per lane (its row's 8
+//     blocks); lane l = 16 g + r takes row r and inputs 8g .. 8g + 7 of every
+//     block: per block s = sum code * x in input order, then acc += d * s,
+//     blocks in order;
+//   - a chunk's acc is summed over the lane groups, (g0 + g1) + (g2 + g3),
+//     into LDS, and a row's total adds the chunks in a fixed order: four
+//     running sums over chunks c = q (mod 4), c ascending, then (s0 + s1) +
+//     (s2 + s3).  The sums depend on K alone, not on how many waves a launch
+//     uses, so the fused launches (norm staged, q/k/v with RoPE, gate/up with
+//     SwiGLU) give the plain launch's sums bit for bit;
+//   - each wave requests its first chunk before x is staged (or its RMSNorm
+//     computed, whose operands are requested before it), then loads the
+//     next chunk while it computes one (a second chunk requested before the
+//     staging measured slower: the staging's wait covers every load before
+//     it, loads completing in order).
+// Every load is 16-byte aligned and contiguous across the wave, unlike the
+// block layout's 34- / 18-byte blocks; q/k/v RoPE's (cos, sin) are computed
+// by the finishing wave's lanes for their own rows while the loads are in
+// flight.
+constexpr int kRowPlanarMaxWaves = 16;
+
+template <int QT>
+constexpr int PlanarLoads() { return QT == MLK_Q8_0 ? 4 : 2; }
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int QT>
+struct PlanarChunk {
+    u32x4 c[PlanarLoads<QT>()];
+    u32x4 s;
+};
+
+__device__ inline float HalfOf(uint32_t w, int hi) {
+    return static_cast<float>(
+        __builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? w >> 16 : w & 0xFFFFu)));
+}
+
+__device__ inline float I8Of(uint32_t w, int byte) {
+    return static_cast<float>(static_cast<int8_t>(w >> (8 * byte)));
+}
+
+// the signed 4-bit value at bit `bit` of w
+__device__ inline float I4Of(uint32_t w, int bit) {
+    return static_cast<float>(static_cast<int32_t>(w << (28 - bit)) >> 28);
+}
+
+__device__ inline float4 XsAt(const float* xs, int k) {
+    return *reinterpret_cast<const float4*>(xs + XPad(k));
+}
+
+// codes: the tile's first chunk + 16 * lane; scales: the tile's scales of
+// row r (16 bytes a chunk)
+template <int QT>
+__device__ inline void LoadPlanarChunk(const uint8_t* codes, const uint8_t* scales, int c,
+                                       PlanarChunk<QT>& b) {
+    constexpr int L = PlanarLoads<QT>();
+    const u32x4* cp = reinterpret_cast<const u32x4*>(codes + static_cast<int64_t>(c) * L * 1024);
+#pragma unroll
+    for (int i = 0; i < L; ++i) b.c[i] = __builtin_nontemporal_load(cp + 64 * i);
+    b.s = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(scales + static_cast<int64_t>(c) * 256));
+}
+
+// The lane's part of one chunk: k0 = 256 * chunk + 8 g.
+template <int QT>
+__device__ inline float PlanarChunkDot(const PlanarChunk<QT>& b, const float* xs, int k0) {
+    float acc = 0.0f;
+    if constexpr (QT == MLK_Q8_0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // block pair i: blocks 2i, 2i + 1 of the chunk
+            const int k = k0 + 64 * i;
+            const float4 a0 = XsAt(xs, k), a1 = XsAt(xs, k + 4);
+            const float4 b0 = XsAt(xs, k + 32), b1 = XsAt(xs, k + 36);
+            const u32x4 c = b.c[i];
+            float s0 = I8Of(c.x, 0) * a0.x;
+            s0 = fmaf(I8Of(c.x, 1), a0.y, s0);
+            s0 = fmaf(I8Of(c.x, 2), a0.z, s0);
+            s0 = fmaf(I8Of(c.x, 3), a0.w, s0);
+            s0 = fmaf(I8Of(c.y, 0), a1.x, s0);
+            s0 = fmaf(I8Of(c.y, 1), a1.y, s0);
+            s0 = fmaf(I8Of(c.y, 2), a1.z, s0);
+            s0 = fmaf(I8Of(c.y, 3), a1.w, s0);
+            float s1 = I8Of(c.z, 0) * b0.x;
+            s1 = fmaf(I8Of(c.z, 1), b0.y, s1);
+            s1 = fmaf(I8Of(c.z, 2), b0.z, s1);
+            s1 = fmaf(I8Of(c.z, 3), b0.w, s1);
+            s1 = fmaf(I8Of(c.w, 0), b1.x, s1);
+            s1 = fmaf(I8Of(c.w, 1), b1.y, s1);
+            s1 = fmaf(I8Of(c.w, 2), b1.z, s1);
+            s1 = fmaf(I8Of(c.w, 3), b1.w, s1);
+            const uint32_t d = b.s[i];
+            acc = fmaf(HalfOf(d, 0), s0, acc);
+            acc = fmaf(HalfOf(d, 1), s1, acc);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {  // blocks 4i .. 4i + 3 of the chunk
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = k0 + 32 * (4 * i + j);
+                const float4 a0 = XsAt(xs, k), a1 = XsAt(xs, k + 4);
+                const uint32_t w = b.c[i][j];  // byte e: input e (low nibble), e + 4 (high)
+                float s = I4Of(w, 0) * a0.x;
+                s = fmaf(I4Of(w, 8), a0.y, s);
+                s = fmaf(I4Of(w, 16), a0.z, s);
+                s = fmaf(I4Of(w, 24), a0.w, s);
+                s = fmaf(I4Of(w, 4), a1.x, s);
+                s = fmaf(I4Of(w, 12), a1.y, s);
+                s = fmaf(I4Of(w, 20), a1.z, s);
+                s = fmaf(I4Of(w, 28), a1.w, s);
+                acc = fmaf(HalfOf(b.s[2 * i + j / 2], j & 1), s, acc);
+            }
+        }
+    }
+    return acc;
+}
+
+// Dynamic LDS: x (XPad(K) floats, 16-byte aligned), then the chunk sums
+// [tiles of the workgroup][matrices][K / 256][16].  A wave's work is the
+// flat sequence of steps s = (tile s / ncw of the workgroup, chunk c_lo +
+// s % ncw), two chunks in registers: while one is computed the other is
+// loading.  A prefetch past the last step (one step, or an odd count) reads
+// one line per load (the matrix's first bytes, the same for every lane), so
+// every weight load is issued unconditionally and each step waits only for
+// its own chunk.
+template <int QT, int MODE, int NVPT>
+__global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
+    const float* x, StreamArgs a, int64_t K, int nwm, int ncw, int tpw) {
+    extern __shared__ __align__(16) float xs[];
+    constexpr int L = PlanarLoads<QT>();
+    constexpr int kMats = MODE == kStreamSwiGlu ? 2 : 1;
+    constexpr int64_t kChunkBytes = L * 1024;
+    const int nch = static_cast<int>(K / 256);
+    float* part = xs + (XPad(K) + 3) / 4 * 4;
+    const int lane = threadIdx.x % kWave, g = lane / 16, r = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x / kWave));
+    // the workgroup's segment and first tile, the matrix this wave reads
+    int seg = 0, mat = 0, w_in = wave;
+    int64_t tile0 = static_cast<int64_t>(blockIdx.x) * tpw;
+    if constexpr (MODE == kStreamSwiGlu) {
+        mat = wave >= nwm ? 1 : 0;
+        w_in = wave - mat * nwm;
+    } else {
+        while (seg + 1 < a.n_seg && tile0 >= SegAt(a, seg).groups) {
+            tile0 -= SegAt(a, seg).groups;
+            ++seg;
+        }
+    }
+    const StreamSeg& ls = SegAt(a, MODE == kStreamSwiGlu ? mat : seg);
+    const int ntile = static_cast<int>(ls.groups - tile0 < tpw ? ls.groups - tile0 : tpw);
+    const int c_lo = w_in * ncw;
+    const int n_w = nch - c_lo < ncw ? nch - c_lo : ncw;  // <= 0: an idle wave
+    const int steps = ntile * ncw;
+    const int lg = 31 - __builtin_clz(ncw);  // ncw is a power of two
+    const uint8_t* scale0 = ls.w + ls.groups * nch * kChunkBytes + 16 * r;
+    auto load = [&](int st, PlanarChunk<QT>& b) {
+        const uint8_t* cp = ls.w;
+        const uint8_t* sp = ls.w;
+        if (st < steps) {
+            const int j = st & (ncw - 1);
+            const int64_t q = (tile0 + (st >> lg)) * nch + (c_lo + j < nch ? c_lo + j : nch - 1);
+            cp += q * kChunkBytes + 16 * lane;
+            sp = scale0 + q * 256;
+        }
+        LoadPlanarChunk<QT>(cp, sp, 0, b);
+    };
+    // the norm's operands first (x itself, without a norm, after the
+    // chunks: its loop would wait for every load before it either way)
+    NormStager<(NVPT > 0 ? NVPT : 1)> ns;
+    if constexpr (NVPT > 0) ns.Load(a.norm, x, K);
+    PlanarChunk<QT> b0, b1;
+    load(0, b0);
+    __builtin_amdgcn_sched_barrier(0);
+    // q/k/v RoPE (one tile a workgroup): the token's position and, in the
+    // finishing wave, the (cos, sin) of each lane's row
+    int32_t pos = 0;
+    double rc = 1.0, rs = 0.0;
+    if constexpr (MODE == kStreamQkvRope) {
+        pos = a.rope.positions != nullptr ? a.rope.positions[0] : a.rope.pos0;
+        if (wave == 0 && seg < 2 && pos >= 0) {
+            const int64_t row = tile0 * 16 + r;
+            RopeCosSin(pos, a.rope.freq.inv[static_cast<int>(row % a.rope.head_dim) / 2], &rc,
+                       &rs);
+        }
+        if (blockIdx.x == 0 && threadIdx.x == 0 && (pos < 0 || pos >= a.rope.max_seq)) {
+            RaiseFlag(a.rope.err, 1);
+        }
+    }
+    if constexpr (NVPT > 0) {  // the launcher sets kStreamThreads threads, a.norm.vpt <= NVPT
+        __shared__ double wsum[16];
+        ns.Finish(a.norm, K, xs, wsum);
+    } else {
+        for (int64_t i = threadIdx.x; i < K / 4; i += blockDim.x) {
+            *reinterpret_cast<float4*>(xs + XPad(4 * i)) = reinterpret_cast<const float4*>(x)[i];
+        }
+    }
+    __syncthreads();
+    auto compute = [&](const PlanarChunk<QT>& b, int st) {
+        const int j = st & (ncw - 1);
+        if (j >= n_w) return;
+        const int c = c_lo + j;
+        float v = PlanarChunkDot<QT>(b, xs, 256 * c + 8 * g);
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (g == 0) part[(((st >> lg) * kMats + mat) * nch + c) * 16 + r] = v;
+    };
+    // b0 and b1 hold steps st and st + 1; the last two steps take no further
+    // loads (a load still in flight would hold up the barrier below)
+    int st = 0;
+    load(1, b1);
+    for (; st + 2 < steps; st += 2) {
+        compute(b0, st);
+        load(st + 2, b0);
+        compute(b1, st + 1);
+        load(st + 3, b1);
+    }
+    compute(b0, st);
+    if (st + 1 < steps) compute(b1, st + 1);
+    __syncthreads();
+    if (wave >= ntile) return;  // wave t finishes tile t
+    const int64_t tile = tile0 + wave;
+    auto total = [&](int m) {
+        const float* p = part + (wave * kMats + m) * nch * 16 + r;
+        float v[16];  // chunks g, g + 4, ... (at most 64 chunks fit the LDS)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int c = g + 4 * i;
+            v[i] = c < nch ? p[c * 16] : 0.0f;
+        }
+        float t = v[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) t += v[i];
+        t += __shfl_xor(t, 16);
+        t += __shfl_xor(t, 32);
+        return t;
+    };
+    const int64_t row = tile * 16 + r;
+    if constexpr (MODE == kStreamSwiGlu) {
+        const float tg = total(0), tu = total(1);
+        const StreamSeg& gs = a.seg[0];
+        const StreamSeg& us = a.seg[1];
+        if (g != 0 || row >= us.rows) return;
+        const float gv = gs.bias != nullptr ? tg + gs.bias[row] : tg;
+        const float uv = us.bias != nullptr ? tu + us.bias[row] : tu;
+        us.y[row] = SwiGluF(gv, uv);
+        return;
+    }
+    const float tot = total(0);
+    const StreamSeg& sg = SegAt(a, seg);
+    const bool valid = row < sg.rows;
+    const float val = valid && sg.bias != nullptr ? tot + sg.bias[row] : tot;
+    if constexpr (MODE == kStreamQkvRope) {
+        const bool cache_ok = pos >= 0 && pos < a.rope.max_seq;
+        if (seg == 2) {
+            if (g == 0 && valid && cache_ok) sg.y[pos * a.rope.kv_stride + row] = val;
+            return;
+        }
+        const float other = __shfl_xor(val, 1);
+        const float x0 = (r & 1) ? other : val, x1 = (r & 1) ? val : other;
+        float r0 = x0, r1 = x1;
+        if (pos >= 0) RopeRotate(x0, x1, rc, rs, &r0, &r1);
+        if (g != 0 || !valid || (seg == 1 && !cache_ok)) return;
+        float* y = seg == 1 ? sg.y + pos * a.rope.kv_stride : sg.y;
+        y[row] = (r & 1) ? r1 : r0;
+        return;
+    }
+    if (g != 0 || !valid) return;
+    if constexpr (MODE == kStreamAdd) {
+        sg.y[row] = sg.res[row] + val;
+    } else {
+        sg.y[row] = val;
+    }
+}
+
+// The shape of a one-token planar launch: waves per matrix (nwm), chunks
+// per wave (ncw) and tiles per workgroup (tpw).  With a staged norm the
+// workgroup is kStreamThreads threads (StageNorm's shape), else the fewest
+// chunks per wave (1, 2, 4 or 8) that keep the waves within 8 a workgroup,
+// or within kRowPlanarMaxWaves when there are fewer than two tiles per
+// compute unit (the kernel holds 76 registers, so a compute unit runs 24
+// waves: three 8-wave workgroups, or one of 16; few tiles need the larger
+// workgroups to fill it).  Workgroups take two tiles (one segment, or
+// SwiGLU's pairs) when that still leaves a workgroup per compute unit,
+// halving the copies of x (and of its norm) staged.  False: K has more
+// chunks than the waves cover.
+struct RowPlanarPlan {
+    int nwm = 0, ncw = 0, tpw = 1;
+};
+
+bool RowPlanarShape(int64_t K, int mode, bool norm, int64_t tiles, RowPlanarPlan* p) {
+    const int64_t nch = K / 256;
+    const int mats = mode == kStreamSwiGlu ? 2 : 1;
+    const int wg = norm ? kStreamWaves
+                        : (tiles < 2 * ComputeUnits() ? kRowPlanarMaxWaves : kStreamWaves);
+    const int most = wg / mats;
+    for (const int c : {1, 2, 4, 8}) {
+        const int64_t w = (nch + c - 1) / c;
+        if (w <= most) {
+            p->nwm = norm ? most : static_cast<int>(w);
+            p->ncw = c;
+            return true;
+        }
+    }
+    return false;
+}
+
+size_t RowPlanarLds(int64_t K, int mode, int tpw) {
+    const int mats = mode == kStreamSwiGlu ? 2 : 1;
+    return static_cast<size_t>((XPad(K) + 3) / 4 * 4 + tpw * mats * (K / 256) * 16) * 4;
+}
+
+constexpr size_t kRowPlanarLdsMax = 64 * 1024 - 16 * sizeof(double);  // StageNorm's sums
+
+template <int QT, int MODE>
+void LaunchRowPlanar(unsigned grid, int threads, size_t lds, hipStream_t s, const float* x,
+                     const StreamArgs& a, int64_t K, const RowPlanarPlan& p) {
+    if (a.norm.weight == nullptr) {
+        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 0>), dim3(grid), dim3(threads), lds, s, x, a,
+                           K, p.nwm, p.ncw, p.tpw);
+    } else if (a.norm.vpt == 1) {
+        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 1>), dim3(grid), dim3(threads), lds, s, x, a,
+                           K, p.nwm, p.ncw, p.tpw);
+    } else {
+        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 2>), dim3(grid), dim3(threads), lds, s, x, a,
+                           K, p.nwm, p.ncw, p.tpw);
+    }
+}
+
+template <int QT>
+void LaunchRowPlanarMode(int mode, unsigned grid, int threads, size_t lds, hipStream_t s,
+                         const float* x, const StreamArgs& a, int64_t K, const RowPlanarPlan& p) {
+    switch (mode) {
+        case kStreamAdd: LaunchRowPlanar<QT, kStreamAdd>(grid, threads, lds, s, x, a, K, p); break;
+        case kStreamSwiGlu: LaunchRowPlanar<QT, kStreamSwiGlu>(grid, threads, lds, s, x, a, K, p); break;
+        case kStreamQkvRope: LaunchRowPlanar<QT, kStreamQkvRope>(grid, threads, lds, s, x, a, K, p); break;
+        default: LaunchRowPlanar<QT, kStreamPlain>(grid, threads, lds, s, x, a, K, p); break;
     }
 }
 
@@ -1053,6 +1419,15 @@ bool StreamRopeFits(int64_t K, int64_t head_dim) {
     return StreamFits(K) && head_dim > 0 && XPad(K) * 4 + head_dim / 2 * 16 <= 64 * 1024;
 }
 
+// no norm, or one StageNorm can stage (the norm kernel's 8 or 16 waves, at
+// most kNormVpt float4s per thread covering K)
+bool NormArgsOk(const StreamNorm& n, int64_t K) {
+    return n.weight == nullptr ||
+           ((n.waves == 8 || n.waves == 16) && n.vpt >= 1 && n.vpt <= kNormVpt &&
+            K / 4 <= static_cast<int64_t>(n.vpt) * kWave * n.waves && Aligned(n.weight, 16) &&
+            Aligned(n.delta, 16) && Aligned(n.res_out, 16) && n.eps > 0.0f);
+}
+
 mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
                            hipStream_t s) {
     if (qt < MLK_Q8_0 || qt > MLK_Q4_1 || !StreamFits(K) || !Aligned(x, 16) || a.n_seg < 1 ||
@@ -1068,11 +1443,7 @@ mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& 
     if (mode == kStreamQkvRope && (!QkvRopeArgsOk(a) || !StreamRopeFits(K, a.rope.head_dim))) {
         return Fail(MLK_ERR_INVALID, "linear (one row): bad q/k/v RoPE segments");
     }
-    const StreamNorm& n = a.norm;
-    if (n.weight != nullptr &&
-        ((n.waves != 8 && n.waves != 16) || n.vpt < 1 || n.vpt > kNormVpt ||
-         K / 4 > static_cast<int64_t>(n.vpt) * kWave * n.waves || !Aligned(n.weight, 16) ||
-         !Aligned(n.delta, 16) || !Aligned(n.res_out, 16) || !(n.eps > 0.0f))) {
+    if (!NormArgsOk(a.norm, K)) {
         return Fail(MLK_ERR_INVALID, "linear (one row): bad input RMSNorm");
     }
     const int64_t row_bytes = (K / 32) * BlockBytes(qt);
@@ -1081,6 +1452,59 @@ mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& 
         case MLK_Q4_0: return StreamLaunch<MLK_Q4_0>(x, a, mode, K, row_bytes, s);
         default: return StreamLaunch<MLK_Q4_1>(x, a, mode, K, row_bytes, s);
     }
+}
+
+bool RowPlanarApplies(int qt, int64_t K, int mode, bool norm) {
+    RowPlanarPlan p;  // the 8-wave shape covers fewer chunks than the 16-wave one
+    return (qt == MLK_Q8_0 || qt == MLK_Q4_0) && K > 0 && K % 256 == 0 &&
+           RowPlanarLds(K, mode, 1) <= kRowPlanarLdsMax &&
+           RowPlanarShape(K, mode, norm, int64_t{1} << 40, &p);
+}
+
+mlk_status LinearRowPlanar(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
+                           hipStream_t s) {
+    const bool norm = a.norm.weight != nullptr;
+    if (!RowPlanarApplies(qt, K, mode, norm) || !Aligned(x, 16) || a.n_seg < 1 || a.n_seg > 3 ||
+        a.planes != nullptr ||
+        (mode == kStreamSwiGlu && (a.n_seg != 2 || a.seg[0].rows != a.seg[1].rows))) {
+        return Fail(MLK_ERR_INVALID, "linear (one row, planar): unsupported shape");
+    }
+    StreamArgs b = a;
+    int64_t tiles = 0;
+    for (int i = 0; i < b.n_seg; ++i) {
+        StreamSeg& g = b.seg[i];
+        if (g.w == nullptr || !Aligned(g.w, 16) || g.y == nullptr || g.rows <= 0 ||
+            (mode == kStreamAdd && g.res == nullptr)) {
+            return Fail(MLK_ERR_INVALID, "linear (one row, planar): bad segment %d", i);
+        }
+        g.groups = (g.rows + 15) / 16;
+        tiles += g.groups;
+    }
+    if (mode == kStreamSwiGlu) tiles = b.seg[0].groups;
+    if (mode == kStreamQkvRope && !QkvRopeArgsOk(b)) {
+        return Fail(MLK_ERR_INVALID, "linear (one row, planar): bad q/k/v RoPE segments");
+    }
+    if (!NormArgsOk(b.norm, K)) {
+        return Fail(MLK_ERR_INVALID, "linear (one row, planar): bad input RMSNorm");
+    }
+    RowPlanarPlan p;
+    RowPlanarShape(K, mode, norm, tiles, &p);
+    const int waves = p.nwm * (mode == kStreamSwiGlu ? 2 : 1);
+    if ((b.n_seg == 1 || mode == kStreamSwiGlu) && tiles >= 2 * ComputeUnits() &&
+        waves >= 2 && RowPlanarLds(K, mode, 2) <= kRowPlanarLdsMax) {
+        p.tpw = 2;
+    }
+    const int64_t grid = (tiles + p.tpw - 1) / p.tpw;
+    if (grid > 0x7FFFFFFF) return Fail(MLK_ERR_INVALID, "linear (one row, planar): too many rows");
+    const size_t lds = RowPlanarLds(K, mode, p.tpw);
+    if (qt == MLK_Q8_0) {
+        LaunchRowPlanarMode<MLK_Q8_0>(mode, static_cast<unsigned>(grid), waves * kWave, lds, s, x,
+                                      b, K, p);
+    } else {
+        LaunchRowPlanarMode<MLK_Q4_0>(mode, static_cast<unsigned>(grid), waves * kWave, lds, s, x,
+                                      b, K, p);
+    }
+    return CheckLaunch("GemvRowPlanar");
 }
 
 }  // namespace mlk
@@ -1224,6 +1648,7 @@ mlk_status mlk_quant_to_planar(int32_t quant_type, const void* blocks, int64_t r
 int64_t mlk_linear_planar_workspace_bytes(int64_t rows, int64_t in_features,
                                           int64_t out_features) {
     if (rows <= 0 || in_features <= 0 || out_features <= 0 || in_features % 256 != 0) return 0;
+    if (rows == 1 && RowPlanarApplies(MLK_Q8_0, in_features, kStreamPlain, false)) return 0;
     if (!PlanarApplies(MLK_Q8_0, rows, in_features)) {
         return GemmWorkspaceBytes(kWPlanarQ8, rows, in_features, out_features);
     }
@@ -1245,6 +1670,13 @@ mlk_status mlk_linear_planar(int32_t quant_type, const float* x, const void* w_p
         return Fail(MLK_ERR_INVALID,
                     "mlk_linear_planar: in_features must be a multiple of 256, the weights and x "
                     "16-byte aligned");
+    }
+    if (rows == 1 && RowPlanarApplies(quant_type, in_features, kStreamPlain, false)) {
+        StreamArgs a{};
+        a.seg[0] = StreamSeg{static_cast<const uint8_t*>(w_planar), bias, y, nullptr,
+                             out_features, 0};
+        a.n_seg = 1;
+        return LinearRowPlanar(quant_type, x, in_features, a, kStreamPlain, AsStream(stream));
     }
     return LinearPlanar(quant_type, x, w_planar, bias, y, rows, in_features, out_features,
                         workspace, workspace_bytes, AsStream(stream));

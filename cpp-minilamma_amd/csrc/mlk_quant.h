@@ -116,7 +116,7 @@ struct StreamNorm {
 struct StreamArgs {
     StreamSeg seg[3];
     int n_seg;
-    StreamNorm norm;  // the input row's RMSNorm (LinearRowStream only)
+    StreamNorm norm;  // the input row's RMSNorm (LinearRowStream, LinearRowPlanar)
     RopeArgs rope;  // kStreamQkvRope only
     // kStreamSwiGlu of the planar launches only: when set, the SwiGLU
     // outputs also go here as bf16 planes (StorePlanes, mlk_common.h) for
@@ -131,6 +131,15 @@ bool StreamFits(int64_t K);
 bool QkvRopeArgsOk(const StreamArgs& a);
 bool StreamRopeFits(int64_t K, int64_t head_dim);
 mlk_status LinearRowStream(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
+                           hipStream_t s);
+// The same for one token over planar Q8_0 / Q4_0 weights (segments' w in
+// the layout at mlk_quant_to_planar, 16-byte aligned; no `planes` out):
+// contiguous 1 KB loads per wave, sums that depend on K only, so every mode
+// and a staged norm give the plain launch's sums bit for bit.  Applies when
+// K % 256 == 0 and x plus the chunk sums fit the kernel's LDS (K up to
+// about 14.5 K inputs).
+bool RowPlanarApplies(int qt, int64_t K, int mode, bool norm);
+mlk_status LinearRowPlanar(int qt, const float* x, int64_t K, const StreamArgs& a, int mode,
                            hipStream_t s);
 
 // T token rows (up to 32) through up to three quantized weight matrices with

@@ -94,7 +94,7 @@ class DeviceModel:
 
     def __init__(self, model, planar=False):
         """planar: also keep Q8_0 / Q4_0 weights (in_features a multiple of
-        256) in the planar layout, which batches of 2..32 tokens run on."""
+        256) in the planar layout, which batches of 1..32 tokens run on."""
         c = self.config = dict(model["config"])
         self._keep = []
         self._planar = planar

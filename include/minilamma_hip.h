@@ -202,9 +202,11 @@ mlk_status mlk_quant_to_planar(int32_t quant_type, const void* blocks, int64_t r
                                int64_t cols, void* planar, void* stream);
 
 /* y = x W^T (+ bias) with W in the planar layout (quant_type MLK_Q8_0 or
- * MLK_Q4_0), the same sum bound as mlk_linear_quant.  Up to 32 rows run on
- * the bf16 matrix cores with exact products (codes are exact in bf16 and x
- * is split into three exact bf16 pieces), and need a workspace of
+ * MLK_Q4_0), the same sum bound as mlk_linear_quant.  One row with
+ * in_features up to 14336 takes a streaming GEMV in fp32 (no workspace:
+ * mlk_linear_planar_workspace_bytes is 0); up to 32 rows run on the bf16
+ * matrix cores with exact products (codes are exact in bf16 and x is split
+ * into three exact bf16 pieces), and need a workspace of
  * mlk_linear_planar_workspace_bytes (16-byte aligned); more rows take the
  * fp32 matrix-core GEMM, with the optional workspace of
  * mlk_linear_workspace_bytes.  No counterpart in the reference. */
@@ -324,7 +326,7 @@ typedef struct {
     const void* data;    /* [out, in]: fp32 row-major, or out rows of ceil(in / 32) blocks */
     const float* bias;   /* [out] or NULL */
     const void* planar;  /* NULL, or the same Q8_0 / Q4_0 weight in the planar layout
-                            (mlk_quant_to_planar, 16-byte aligned): calls of 2..32 tokens
+                            (mlk_quant_to_planar, 16-byte aligned): calls of 1..32 tokens
                             then run on it.  No counterpart in the reference. */
 } mlk_linear_weight;
 

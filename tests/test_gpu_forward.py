@@ -274,20 +274,22 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
 @pytest.mark.parametrize("D,F", [(2048, 1024), (4096, 1024), (6144, 512), (8192, 512)])
-def test_one_token_norms_folded_equal_op_by_op(mlk, fwd, wt, D, F):
+@pytest.mark.parametrize("planar", [False, True])
+def test_one_token_norms_folded_equal_op_by_op(mlk, fwd, wt, D, F, planar):
     """One token with dim 2048..8192: both RMSNorms are staged inside the
     streaming q/k/v and gate/up launches (the norm kernel's block of 8 or 16
     waves with one or two float4s per thread, the second partly used at
     6144, emulated there: its float64 sums in the same order), and the
     residual x + proj reaches the down projection through the h buffer.  The
-    layer equals the separate entry points bit for bit."""
+    layer equals the separate entry points bit for bit, over the blocks and
+    over planar copies (then each matrix through mlk_linear_planar)."""
     S, H, KV, hd, pos = 256, 16, 4, 128, 200
     cfg = dict(vocab=64, dim=D, hidden_dim=F, layers=1, n_heads=H, n_kv_heads=KV,
                head_dim=hd, max_seq=S, rope_type=0, theta=500000.0, eps=1e-5)
     model = O.forward_model(cfg, seed=D + F, weight_type=wt, biases=False)
     QD, KD = H * hd, KV * hd
     lw = model["layers"][0]
-    dm = fwd.DeviceModel(model)
+    dm = fwd.DeviceModel(model, planar=planar)
     rng = np.random.default_rng(D)
     x0 = (rng.standard_normal((1, D)) * 3).astype(np.float32)
     kc0 = (rng.standard_normal((1, S, KV, hd)) * 0.5).astype(np.float32)
@@ -301,27 +303,41 @@ def test_one_token_norms_folded_equal_op_by_op(mlk, fwd, wt, D, F):
     def up(a):
         return B(np.ascontiguousarray(a))
     w = {n: up(np.asarray(lw[n][1], np.uint8)) for n in fwd.LINEAR_NAMES}
+    shapes = {"wq": (QD, D), "wk": (KD, D), "wv": (KD, D), "wo": (D, QD), "w_gate": (F, D),
+              "w_up": (F, D), "w_down": (D, F)}
+    if planar:
+        for n, (o, i) in shapes.items():
+            pw = mlk.DeviceBuffer(mlk.quant_planar_bytes(wt, o, i), np.uint8)
+            mlk.quant_to_planar(wt, w[n], o, i, pw)
+            w[n] = pw
+
+    def linear(name, x_in, y_out):
+        o, i = shapes[name]
+        if planar:
+            mlk.linear_planar(wt, x_in, w[name], y_out, 1, i, o, workspace=None)
+        else:
+            mlk.linear_quant(wt, x_in, w[name], y_out, 1, i, o)
     an, fn = up(np.asarray(lw["attention_norm"], np.float32)), up(np.asarray(lw["ffn_norm"], np.float32))
     x2, kc2, vc2 = B(x0), B(kc0), B(vc0)
     e = mlk.DeviceBuffer.empty
     h, q, k, v, a, proj = e((1, D)), e((1, QD)), e((1, KD)), e((1, KD)), e((1, QD)), e((1, D))
     g, u = e((1, F)), e((1, F))
     mlk.rmsnorm(x2, an, h, 1, D, cfg["eps"])
-    mlk.linear_quant(wt, h, w["wq"], q, 1, D, QD)
-    mlk.linear_quant(wt, h, w["wk"], k, 1, D, KD)
-    mlk.linear_quant(wt, h, w["wv"], v, 1, D, KD)
+    linear("wq", h, q)
+    linear("wk", h, k)
+    linear("wv", h, v)
     mlk.rope(q, k, 1, H, KV, hd, pos0=pos, theta=cfg["theta"], rope_type=0)
     mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, 1, pos0=pos)
     nws = mlk.attention_workspace_bytes(1, H, KV, hd, S)
     aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
     mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, 1, a, S, pos0=pos, workspace=aws,
                          workspace_bytes=aws.nbytes)
-    mlk.linear_quant(wt, a, w["wo"], proj, 1, QD, D)
+    linear("wo", a, proj)
     mlk.add_rmsnorm(x2, proj, fn, h, 1, D, cfg["eps"])
-    mlk.linear_quant(wt, h, w["w_gate"], g, 1, D, F)
-    mlk.linear_quant(wt, h, w["w_up"], u, 1, D, F)
+    linear("w_gate", h, g)
+    linear("w_up", h, u)
     mlk.swiglu(g, u, g, F)
-    mlk.linear_quant(wt, g, w["w_down"], proj, 1, F, D)
+    linear("w_down", g, proj)
     mlk.add(x2, proj, x2, D)
     np.testing.assert_array_equal(got, x2.download())
     np.testing.assert_array_equal(kc.download(), kc2.download())
@@ -329,12 +345,13 @@ def test_one_token_norms_folded_equal_op_by_op(mlk, fwd, wt, D, F):
 
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
-@pytest.mark.parametrize("T", [2, 12, 24])
+@pytest.mark.parametrize("T", [1, 2, 12, 24])
 @pytest.mark.parametrize("case", ["pos0", "positions", "bad_position", "neox"])
 def test_layer_planar_equals_op_by_op(mlk, fwd, wt, T, case):
-    """With planar copies of the weights, 2..32 tokens take the planar
-    launches: q/k/v in one (RoPE and the K/V cache rows in its reduction for
-    the normal layout), gate/up with SwiGLU, down adding into x, and wo.
+    """With planar copies of the weights, 1..32 tokens take the planar
+    launches: q/k/v in one (RoPE and the K/V cache rows in its epilogue or
+    reduction for the normal layout; one token also stages the RMSNorm),
+    gate/up with SwiGLU, down adding into x, and wo.
     Their per-element arithmetic is the separate entries' (mlk_linear_planar
     per matrix, then the separate ops), so the layer equals that composition
     bit for bit: residual stream, cache rows and error flag."""
@@ -408,13 +425,14 @@ def test_layer_planar_equals_op_by_op(mlk, fwd, wt, T, case):
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
 def test_forward_planar_matches_oracle(orc, fwd, wt):
-    """A model with planar copies: decode batches of 2, 5, 16 and 32 tokens
-    (the planar kernels) after a 33-token prefill (the GEMM on the blocks),
+    """A model with planar copies: decode steps of 1 token and batches of 2,
+    5, 16 and 32 tokens (the planar kernels) after a 33-token prefill (the
+    GEMM on the blocks),
     against the reference's ForwardToken loop over the same tokens."""
     cfg = dict(vocab=300, dim=512, hidden_dim=1024, layers=2, n_heads=8, n_kv_heads=2,
                head_dim=64, max_seq=160, rope_type=0, theta=10000.0, eps=1e-5)
     model = O.forward_model(cfg, seed=21, weight_type=wt, biases=True)
-    sizes = [33, 2, 5, 16, 32]
+    sizes = [33, 1, 2, 5, 1, 16, 32]
     n = sum(sizes)
     rng = np.random.default_rng(4)
     tokens = rng.integers(0, cfg["vocab"], n).astype(np.int32)

@@ -80,8 +80,12 @@ def test_planar_layout_bytes(mlk, orc, qt, rows, cols):
     np.testing.assert_array_equal(got, want)
 
 
-PLANAR_SHAPES = [  # (out, in, rows): 1..32 rows take the bf16 kernel, more the GEMM
-    (131, 256, 1), (4099, 4096, 1), (64, 512, 3), (4096, 4096, 7), (100, 256, 16),
+PLANAR_SHAPES = [  # (out, in, rows): one row takes the streaming GEMV (in_features up to
+    # 14336; 1, 2, 4 or 8 chunks of 256 inputs per wave, idle waves, partial
+    # tiles), 2..32 rows the bf16 kernel (one row too past 14336), more the GEMM
+    (131, 256, 1), (4099, 4096, 1), (4096, 14336, 1), (300, 2816, 1), (1000, 11008, 1),
+    (8192, 8192, 1), (17, 14592, 1),
+    (64, 512, 3), (4096, 4096, 7), (100, 256, 16),
     (4097, 512, 17), (64, 4096, 31), (14336, 4096, 32), (4096, 14336, 12), (130, 768, 25),
     (1024, 4096, 33), (257, 512, 64), (200, 1024, 130)]
 
@@ -91,7 +95,7 @@ PLANAR_SHAPES = [  # (out, in, rows): 1..32 rows take the bf16 kernel, more the 
 def test_planar_linear_shapes(mlk, orc, qt, shape):
     """Token counts 1..32 (one and two 16-token tiles, partial tiles),
     output counts that end inside a 16-row tile or a 128-row workgroup, one
-    to 56 K ranges; 33+ rows on the tiled GEMM (partial 128 x 128 tiles,
+    to 57 K ranges; 33+ rows on the tiled GEMM (partial 128 x 128 tiles,
     split K); with a bias."""
     O, K, T = shape
     rng = np.random.default_rng(O + 7 * K + T)
@@ -127,7 +131,8 @@ def test_planar_equals_block_layout_bound(mlk, orc, qt):
 def test_planar_non_finite_inputs(mlk, orc, qt):
     """x with inf and NaN: every output whose sum meets them is what fp32
     products give (NaN, or inf of the sign the products force), the rest
-    finite and within the bound."""
+    finite and within the bound; four rows (bf16 kernel) and each row alone
+    (the one-row GEMV)."""
     O, K, T = 64, 512, 4
     rng = np.random.default_rng(3)
     blocks = orc.quantize(qt, normal(rng, (O, K), 0.02))
@@ -135,17 +140,38 @@ def test_planar_non_finite_inputs(mlk, orc, qt):
     x = normal(rng, (T, K))
     x[1, 5] = np.inf
     x[2, 300] = np.nan
-    got = run_planar(mlk, qt, x, to_planar(mlk, qt, blocks, O, K), O)
+    planar = to_planar(mlk, qt, blocks, O, K)
     with np.errstate(invalid="ignore", over="ignore"):
         want = x.astype(np.float64) @ wd.astype(np.float64).T
-    for t in (1, 2):
-        np.testing.assert_array_equal(np.isnan(got[t]), np.isnan(want[t]))
-        fin = np.isfinite(want[t])
-        np.testing.assert_array_equal(got[t][~fin & ~np.isnan(want[t])],
-                                      want[t][~fin & ~np.isnan(want[t])])
-    ok = [0, 3]
-    ex, s = dot_exact(x[ok], wd)
-    assert_dot_close(got[ok], ex, s, K, f"{qt} finite rows")
+    for got in (run_planar(mlk, qt, x, planar, O),
+                np.concatenate([run_planar(mlk, qt, x[t], planar, O) for t in range(T)])):
+        for t in (1, 2):
+            np.testing.assert_array_equal(np.isnan(got[t]), np.isnan(want[t]))
+            fin = np.isfinite(want[t])
+            np.testing.assert_array_equal(got[t][~fin & ~np.isnan(want[t])],
+                                          want[t][~fin & ~np.isnan(want[t])])
+        ok = [0, 3]
+        ex, s = dot_exact(x[ok], wd)
+        assert_dot_close(got[ok], ex, s, K, f"{qt} finite rows")
+
+
+@pytest.mark.parametrize("qt", QT)
+def test_planar_one_row_equals_block_layout_bound(mlk, orc, qt):
+    """One row at the 8B shapes (q/k/v, wo, gate and down): the planar GEMV
+    and the block-layout streaming GEMV on the same blocks, both within the
+    bound of the exact sums; the planar one needs no workspace."""
+    rng = np.random.default_rng(23)
+    for O, K in ((6144, 4096), (4096, 4096), (14336, 4096), (4096, 14336)):
+        assert mlk.linear_planar_workspace_bytes(1, K, O) == 0
+        blocks = orc.quantize(qt, normal(rng, (O, K), 0.02))
+        x = normal(rng, (1, K))
+        ex, s = dot_exact(x, orc.dequantize(qt, blocks, O, K))
+        got_p = run_planar(mlk, qt, x, to_planar(mlk, qt, blocks, O, K), O, workspace=None)
+        d_x, d_w = mlk.DeviceBuffer.from_array(x), mlk.DeviceBuffer.from_array(blocks)
+        d_y = mlk.DeviceBuffer.empty((1, O))
+        mlk.linear_quant(qt, d_x, d_w, d_y, 1, K, O)
+        assert_dot_close(got_p, ex, s, K, f"{qt} {O}x{K} planar")
+        assert_dot_close(d_y.download(), ex, s, K, f"{qt} {O}x{K} blocks")
 
 
 def test_planar_rejects(mlk, orc):
