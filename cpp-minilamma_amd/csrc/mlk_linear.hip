@@ -965,14 +965,7 @@ __device__ inline float I8Of(uint32_t w, int byte) {
     return static_cast<float>(static_cast<int8_t>(w >> (8 * byte)));
 }
 
-// the signed 4-bit value at bit `bit` of w
-__device__ inline float I4Of(uint32_t w, int bit) {
-    return static_cast<float>(static_cast<int32_t>(w << (28 - bit)) >> 28);
-}
-
-__device__ inline float4 XsAt(const float* xs, int k) {
-    return *reinterpret_cast<const float4*>(xs + XPad(k));
-}
+__device__ inline float4 XsAt(const float* p) { return *reinterpret_cast<const float4*>(p); }
 
 // codes: the tile's first chunk + 16 * lane; scales: the tile's scales of
 // row r (16 bytes a chunk)
@@ -987,16 +980,24 @@ __device__ inline void LoadPlanarChunk(const uint8_t* codes, const uint8_t* scal
         reinterpret_cast<const u32x4*>(scales + static_cast<int64_t>(c) * 256));
 }
 
-// The lane's part of one chunk: k0 = 256 * chunk + 8 g.
+// The lane's part of one chunk, from xc = xs + XPad(256 * chunk) + 8 g
+// (= xs + 272 * chunk + 8 g): a 256-input chunk starts 64-aligned, so input
+// 32 b + 8 g + e of it sits at xc + 32 b + 4 (b / 2) + e, an immediate
+// offset per block.  Q4_0: each code word spreads into two words of
+// sign-extended bytes holding 16 * the code's value (low nibbles shifted
+// up, high nibbles in place), converted one instruction a byte as Q8_0's
+// are; the chunk's sums then carry a factor 16, exact in binary floating
+// point, taken out once at the end, so the result is that of the values
+// themselves bit for bit.
 template <int QT>
-__device__ inline float PlanarChunkDot(const PlanarChunk<QT>& b, const float* xs, int k0) {
+__device__ inline float PlanarChunkDot(const PlanarChunk<QT>& b, const float* xc) {
     float acc = 0.0f;
     if constexpr (QT == MLK_Q8_0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {  // block pair i: blocks 2i, 2i + 1 of the chunk
-            const int k = k0 + 64 * i;
-            const float4 a0 = XsAt(xs, k), a1 = XsAt(xs, k + 4);
-            const float4 b0 = XsAt(xs, k + 32), b1 = XsAt(xs, k + 36);
+            const float* q = xc + 68 * i;
+            const float4 a0 = XsAt(q), a1 = XsAt(q + 4);
+            const float4 b0 = XsAt(q + 32), b1 = XsAt(q + 36);
             const u32x4 c = b.c[i];
             float s0 = I8Of(c.x, 0) * a0.x;
             s0 = fmaf(I8Of(c.x, 1), a0.y, s0);
@@ -1023,20 +1024,23 @@ __device__ inline float PlanarChunkDot(const PlanarChunk<QT>& b, const float* xs
         for (int i = 0; i < 2; ++i) {  // blocks 4i .. 4i + 3 of the chunk
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int k = k0 + 32 * (4 * i + j);
-                const float4 a0 = XsAt(xs, k), a1 = XsAt(xs, k + 4);
+                const int blk = 4 * i + j;
+                const float* q = xc + 32 * blk + 4 * (blk / 2);
+                const float4 a0 = XsAt(q), a1 = XsAt(q + 4);
                 const uint32_t w = b.c[i][j];  // byte e: input e (low nibble), e + 4 (high)
-                float s = I4Of(w, 0) * a0.x;
-                s = fmaf(I4Of(w, 8), a0.y, s);
-                s = fmaf(I4Of(w, 16), a0.z, s);
-                s = fmaf(I4Of(w, 24), a0.w, s);
-                s = fmaf(I4Of(w, 4), a1.x, s);
-                s = fmaf(I4Of(w, 12), a1.y, s);
-                s = fmaf(I4Of(w, 20), a1.z, s);
-                s = fmaf(I4Of(w, 28), a1.w, s);
+                const uint32_t lo = (w << 4) & 0xF0F0F0F0u, hi = w & 0xF0F0F0F0u;
+                float s = I8Of(lo, 0) * a0.x;
+                s = fmaf(I8Of(lo, 1), a0.y, s);
+                s = fmaf(I8Of(lo, 2), a0.z, s);
+                s = fmaf(I8Of(lo, 3), a0.w, s);
+                s = fmaf(I8Of(hi, 0), a1.x, s);
+                s = fmaf(I8Of(hi, 1), a1.y, s);
+                s = fmaf(I8Of(hi, 2), a1.z, s);
+                s = fmaf(I8Of(hi, 3), a1.w, s);
                 acc = fmaf(HalfOf(b.s[2 * i + j / 2], j & 1), s, acc);
             }
         }
+        acc *= 0.0625f;
     }
     return acc;
 }
@@ -1125,7 +1129,7 @@ __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
         const int j = st & (ncw - 1);
         if (j >= n_w) return;
         const int c = c_lo + j;
-        float v = PlanarChunkDot<QT>(b, xs, 256 * c + 8 * g);
+        float v = PlanarChunkDot<QT>(b, xs + 272 * c + 8 * g);
         v += __shfl_xor(v, 16);
         v += __shfl_xor(v, 32);
         if (g == 0) part[(((st >> lg) * kMats + mat) * nch + c) * 16 + r] = v;
