@@ -729,21 +729,24 @@ struct NormStager {
         return threadIdx.x + j * kStreamThreads + static_cast<int64_t>(v) * (kWave * n.waves);
     }
 
+    // Every load is issued (lanes past the row read its first float4, and
+    // without a delta x stands in for it), so no branch joins after a load
+    // and the caller's own loads issued next are not waited for early.
     __device__ void Load(const StreamNorm& n, const float* x, int64_t K) {
         const int nv = kWave * n.waves;
+        const float4* xs4 = reinterpret_cast<const float4*>(x);
+        const float4* ws4 = reinterpret_cast<const float4*>(n.weight);
+        const float4* ds4 = reinterpret_cast<const float4*>(n.delta != nullptr ? n.delta : x);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) {
 #pragma unroll
             for (int v = 0; v < VPT; ++v) {
                 const int64_t i = Index(n, j, v);
                 ok[j][v] = j * kStreamThreads < nv && v < n.vpt && i < K / 4;
-                r[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(x)[i]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                w[j][v] = ok[j][v] ? reinterpret_cast<const float4*>(n.weight)[i]
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                d[j][v] = ok[j][v] && n.delta != nullptr
-                              ? reinterpret_cast<const float4*>(n.delta)[i]
-                              : make_float4(0.f, 0.f, 0.f, 0.f);
+                const int64_t ic = ok[j][v] ? i : 0;
+                r[j][v] = xs4[ic];
+                w[j][v] = ws4[ic];
+                d[j][v] = ds4[ic];
             }
         }
     }
@@ -934,11 +937,11 @@ __global__ __launch_bounds__(kStreamThreads, 4) void GemvStream(const float* x, 
 //     (s2 + s3).  The sums depend on K alone, not on how many waves a launch
 //     uses, so the fused launches (norm staged, q/k/v with RoPE, gate/up with
 //     SwiGLU) give the plain launch's sums bit for bit;
-//   - each wave requests its first chunk before x is staged (or its RMSNorm
-//     computed, whose operands are requested before it), then loads the
-//     next chunk while it computes one (a second chunk requested before the
-//     staging measured slower: the staging's wait covers every load before
-//     it, loads completing in order).
+//   - each thread requests its float4s of x (or of its RMSNorm's operands)
+//     first, then its wave's first two chunks, then stages x: loads complete
+//     in order, so the staging waits for x alone while the chunks are in
+//     flight; from there each wave loads the next chunk while it computes
+//     one.
 // Every load is 16-byte aligned and contiguous across the wave, unlike the
 // block layout's 34- / 18-byte blocks; q/k/v RoPE's (cos, sin) are computed
 // by the finishing wave's lanes for their own rows while the loads are in
@@ -1096,22 +1099,49 @@ __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
     };
     // the norm's operands first (x itself, without a norm, after the
     // chunks: its loop would wait for every load before it either way)
+    // q/k/v RoPE (one tile a workgroup): the token's position and, in the
+    // finishing wave, each lane's inverse frequency, requested before the
+    // weights (loads complete in order, so a wait for them later would
+    // also wait for every chunk requested before)
+    int32_t pos = 0;
+    double inv = 0.0;
+    const bool rope_rows = MODE == kStreamQkvRope && wave == 0 && seg < 2;
+    if constexpr (MODE == kStreamQkvRope) {
+        // every lane loads (no branch joins after a load), through a global
+        // pointer (a generic one would make a flat load, which every later
+        // wait must cover); without positions the weights stand in
+        typedef const int32_t __attribute__((address_space(1)))* GlobalI32;
+        const int32_t* pp = a.rope.positions != nullptr
+                                ? a.rope.positions : reinterpret_cast<const int32_t*>(ls.w);
+        const int32_t p0 = *(GlobalI32)pp;
+        pos = a.rope.positions != nullptr ? p0 : a.rope.pos0;
+        inv = a.rope.freq.inv[static_cast<int>((tile0 * 16 + r) % a.rope.head_dim) / 2];
+    }
     NormStager<(NVPT > 0 ? NVPT : 1)> ns;
-    if constexpr (NVPT > 0) ns.Load(a.norm, x, K);
+    // no norm: x's float4s tid + i * threads, i < 4 (named, not an array,
+    // which the compiler would keep in scratch memory)
+    float4 xq0, xq1, xq2, xq3;
+    const int64_t k4 = K / 4;
+    auto x_at = [&](int i) {  // unconditional (past x: its last float4)
+        const int64_t e = threadIdx.x + static_cast<int64_t>(i) * blockDim.x;
+        return reinterpret_cast<const float4*>(x)[e < k4 ? e : k4 - 1];
+    };
+    if constexpr (NVPT > 0) {
+        ns.Load(a.norm, x, K);
+    } else {
+        xq0 = x_at(0);
+        xq1 = x_at(1);
+        xq2 = x_at(2);
+        xq3 = x_at(3);
+    }
     PlanarChunk<QT> b0, b1;
     load(0, b0);
+    load(1, b1);
     __builtin_amdgcn_sched_barrier(0);
-    // q/k/v RoPE (one tile a workgroup): the token's position and, in the
-    // finishing wave, the (cos, sin) of each lane's row
-    int32_t pos = 0;
+    // the (cos, sin) of each finishing lane's row, while the chunks load
     double rc = 1.0, rs = 0.0;
     if constexpr (MODE == kStreamQkvRope) {
-        pos = a.rope.positions != nullptr ? a.rope.positions[0] : a.rope.pos0;
-        if (wave == 0 && seg < 2 && pos >= 0) {
-            const int64_t row = tile0 * 16 + r;
-            RopeCosSin(pos, a.rope.freq.inv[static_cast<int>(row % a.rope.head_dim) / 2], &rc,
-                       &rs);
-        }
+        if (rope_rows && pos >= 0) RopeCosSin(pos, inv, &rc, &rs);
         if (blockIdx.x == 0 && threadIdx.x == 0 && (pos < 0 || pos >= a.rope.max_seq)) {
             RaiseFlag(a.rope.err, 1);
         }
@@ -1120,8 +1150,18 @@ __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
         __shared__ double wsum[16];
         ns.Finish(a.norm, K, xs, wsum);
     } else {
-        for (int64_t i = threadIdx.x; i < K / 4; i += blockDim.x) {
-            *reinterpret_cast<float4*>(xs + XPad(4 * i)) = reinterpret_cast<const float4*>(x)[i];
+        auto put = [&](int i, const float4& v) {
+            const int64_t e = threadIdx.x + static_cast<int64_t>(i) * blockDim.x;
+            if (e < k4) *reinterpret_cast<float4*>(xs + XPad(4 * e)) = v;
+        };
+        put(0, xq0);
+        put(1, xq1);
+        put(2, xq2);
+        put(3, xq3);
+        // x past four float4s a thread (K beyond 16 * threads)
+        for (int64_t e = threadIdx.x + 4 * static_cast<int64_t>(blockDim.x); e < k4;
+             e += blockDim.x) {
+            *reinterpret_cast<float4*>(xs + XPad(4 * e)) = reinterpret_cast<const float4*>(x)[e];
         }
     }
     __syncthreads();
@@ -1137,7 +1177,6 @@ __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
     // b0 and b1 hold steps st and st + 1; the last two steps take no further
     // loads (a load still in flight would hold up the barrier below)
     int st = 0;
-    load(1, b1);
     for (; st + 2 < steps; st += 2) {
         compute(b0, st);
         load(st + 2, b0);
@@ -1205,7 +1244,9 @@ __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
 // The shape of a one-token planar launch: waves per matrix (nwm), chunks
 // per wave (ncw) and tiles per workgroup (tpw).  With a staged norm the
 // workgroup is kStreamThreads threads (StageNorm's shape), else the fewest
-// chunks per wave (1, 2, 4 or 8) that keep the waves within 8 a workgroup,
+// chunks per wave (2, 4 or 8; 1 only for K = 256: a wave with one chunk
+// has nothing to overlap its load with) that keep the waves within 8 a
+// workgroup,
 // or within kRowPlanarMaxWaves when there are fewer than two tiles per
 // compute unit (the kernel holds 76 registers, so a compute unit runs 24
 // waves: three 8-wave workgroups, or one of 16; few tiles need the larger
@@ -1225,7 +1266,7 @@ bool RowPlanarShape(int64_t K, int mode, bool norm, int64_t tiles, RowPlanarPlan
     const int most = wg / mats;
     for (const int c : {1, 2, 4, 8}) {
         const int64_t w = (nch + c - 1) / c;
-        if (w <= most) {
+        if (w <= most && (c > 1 || nch == 1 || norm)) {
             p->nwm = norm ? most : static_cast<int>(w);
             p->ncw = c;
             return true;
