@@ -584,6 +584,14 @@ def c5_chain(mlk, steps, warmup, peak, marks, with_cpu):
 # ------------------------------------------------------------ linear layers
 
 LINEAR_TYPES = ("q8_0", "q4_0", "q4_1", "f32")
+# the decode GEMV bench also runs the planar copies (mlk_linear_planar)
+LINEAR_DECODE_TYPES = LINEAR_TYPES + ("q8_0_planar", "q4_0_planar")
+
+
+def base_type(qtype):
+    """The block format of a weight type name ("q8_0_planar" -> "q8_0"):
+    a planar copy holds the same bytes in another order."""
+    return qtype[:-len("_planar")] if qtype.endswith("_planar") else qtype
 LINEAR_TOKENS = (1, 4, 16)
 LINEAR_WORKING_SET = 768 << 20  # rotate layer copies until the weights exceed 3x the MALL
 
@@ -597,19 +605,28 @@ class LinearLayers:
 
     def __init__(self, mlk, cfg, qtype, seed, working_set=LINEAR_WORKING_SET):
         self.mlk, self.qtype = mlk, qtype
+        self.base = base_type(qtype)
+        self.planar = qtype != self.base
         self.shapes = workloads.layer_linears(cfg)
         biggest = max(k * o for _, k, o in self.shapes)
         tmp = mlk.DeviceBuffer.empty((biggest,)) if qtype != "f32" else None
+        blk = (mlk.DeviceBuffer(max(mlk.quant_bytes(self.base, o, k) for _, k, o in self.shapes),
+                                np.uint8) if self.planar else None)
         self.copies = {}
         for j, (name, k, o) in enumerate(self.shapes):
             n = max(1 if working_set == 0 else 2,
-                    -(-working_set // workloads.weight_bytes(qtype, k, o)))
+                    -(-working_set // workloads.weight_bytes(self.base, k, o)))
             mats = []
             for c in range(n):
                 sd = seed + 97 * c + j
                 if qtype == "f32":
                     w = mlk.DeviceBuffer.empty((o, k))
                     mlk.fill_normal(w, o * k, 0.0, 0.02, sd)
+                elif self.planar:  # the same blocks, repacked
+                    mlk.fill_normal(tmp, o * k, 0.0, 0.02, sd)
+                    mlk.quantize(self.base, tmp, o, k, blk)
+                    w = mlk.DeviceBuffer(mlk.quant_planar_bytes(self.base, o, k), np.uint8)
+                    mlk.quant_to_planar(self.base, blk, o, k, w)
                 else:
                     mlk.fill_normal(tmp, o * k, 0.0, 0.02, sd)
                     w = mlk.DeviceBuffer(mlk.quant_bytes(qtype, o, k), np.uint8)
@@ -617,8 +634,9 @@ class LinearLayers:
                 mats.append(w)
             self.copies[name] = mats
         mlk.synchronize()
-        if tmp is not None:
-            tmp.close()
+        for b in (tmp, blk):
+            if b is not None:
+                b.close()
 
     def n_copies(self, name):
         return len(self.copies[name])
@@ -628,6 +646,8 @@ class LinearLayers:
         w = mats[i % len(mats)]
         if self.qtype == "f32":
             self.mlk.linear_f32(x, w, y, T, k, o, stream=stream)
+        elif self.planar:
+            self.mlk.linear_planar(self.base, x, w, y, T, k, o, stream=stream)
         else:
             self.mlk.linear_quant(self.qtype, x, w, y, T, k, o, stream=stream)
 
@@ -646,7 +666,7 @@ def linear_bench(mlk, steps, peak, path):
     out = {"workload": "Llama-3-8B layer projections (configs[1] shapes), weights N(0,0.02) "
                        "quantized on the device; x N(0,1)",
            "peak_GBps": peak}
-    for qt in LINEAR_TYPES:
+    for qt in LINEAR_DECODE_TYPES:
         layers = LinearLayers(mlk, cfg, qt, seed=300)
         res = {"weight_copies": {n: layers.n_copies(n) for n, _, _ in layers.shapes}}
         for T in LINEAR_TOKENS:
@@ -662,7 +682,7 @@ def linear_bench(mlk, steps, peak, path):
                 e1.record(st)
                 e1.synchronize()
                 ms = e0.elapsed_ms(e1) / steps
-                nb = workloads.bytes_linear(qt, T, k, o)
+                nb = workloads.bytes_linear(base_type(qt), T, k, o)
                 gbs = nb / (ms * 1e-3) / 1e9
                 per[name] = {"in": k, "out": o, "us": round(ms * 1e3, 2), "bytes": nb,
                              "GBps": round(gbs, 1), "frac_of_peak": round(gbs / peak, 4)}
@@ -674,7 +694,7 @@ def linear_bench(mlk, steps, peak, path):
             e1.record(st)
             e1.synchronize()
             ms = e0.elapsed_ms(e1) / steps
-            nb = sum(workloads.bytes_linear(qt, T, k, o) for _, k, o in layers.shapes)
+            nb = sum(workloads.bytes_linear(base_type(qt), T, k, o) for _, k, o in layers.shapes)
             gbs = nb / (ms * 1e-3) / 1e9
             res[str(T)] = {"layer_us": round(ms * 1e3, 2), "layer_bytes": nb,
                            "layer_GBps": round(gbs, 1), "layer_frac_of_peak": round(gbs / peak, 4),
