@@ -683,7 +683,8 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
 // assignment, so each product is formed once).  SplitXBf writes x once as
 // three bf16 planes per block, [piece][token][32 inputs].
 // GemmPlanar: workgroup = 4 waves = 128 output rows (wave: two 16-row
-// tiles) x T tokens (16 per tile) x one K range of 2 * NP blocks; the
+// tiles; one, 64 rows, when that leaves too few workgroups) x T tokens
+// (16 per tile) x one K range of 2 * NP blocks; the
 // ranges' partial sums are added by the split-K reductions, as
 // GemmSkinny's.  Every weight load of the range is issued first, the
 // range's x planes (token rows < T) are copied to LDS, and after one
@@ -693,8 +694,9 @@ __global__ __launch_bounds__(kSkThreads) void GemmSkinny(const float* __restrict
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kPlTiles = 2;                  // 16-row weight tiles per wave
-constexpr int kPlRows = 4 * 16 * kPlTiles;   // output rows per workgroup
+// PT: 16-row weight tiles per wave (2, or 1 for the shapes whose two-tile
+// workgroups would be fewer than two per compute unit); a workgroup covers
+// 4 * 16 * PT output rows.
 
 // Bytes 2j, 2j + 1 of v as signed integers in bf16, in one dword.
 __device__ inline uint32_t BytesBf(uint32_t v, int j) {
@@ -716,7 +718,7 @@ __global__ __launch_bounds__(kGemmThreads) void SplitXBf(const float* __restrict
     }
 }
 
-template <int QT, int TT, int NP>
+template <int QT, int TT, int NP, int PT>
 __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restrict__ planes,
                                                          SkinnyArgs a, int64_t T, int64_t K,
                                                          float* __restrict__ partial) {
@@ -734,15 +736,15 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int i16 = lane & 15, g = lane >> 4;
     const int64_t tiles = (O + 15) / 16;
-    const int64_t tile0 = static_cast<int64_t>(rg) * (kPlRows / 16) + wave * kPlTiles;
+    const int64_t tile0 = static_cast<int64_t>(rg) * (4 * PT) + wave * PT;
     const int64_t code_tile = QT == MLK_Q8_0 ? 16 * K : 8 * K;  // bytes per row tile
     const uint8_t* scales = w + tiles * code_tile;
 
     // every weight load of the range first (tiles past the last read it)
-    u32x4 cw[kPlTiles][kCodeVecs];
-    u32x4 sw[kPlTiles][NP / 4];
+    u32x4 cw[PT][kCodeVecs];
+    u32x4 sw[PT][NP / 4];
 #pragma unroll
-    for (int n = 0; n < kPlTiles; ++n) {
+    for (int n = 0; n < PT; ++n) {
         const int64_t tile = tile0 + n < tiles ? tile0 + n : tiles - 1;
         const u32x4* c = reinterpret_cast<const u32x4*>(w + tile * code_tile) +
                          static_cast<int64_t>(sp) * kCodeVecs * 64 + lane;
@@ -773,9 +775,9 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
     }
     __syncthreads();
 
-    f32x4 acc[kPlTiles][TT];
+    f32x4 acc[PT][TT];
 #pragma unroll
-    for (int n = 0; n < kPlTiles; ++n) {
+    for (int n = 0; n < PT; ++n) {
 #pragma unroll
         for (int tt = 0; tt < TT; ++tt) acc[n][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
@@ -791,7 +793,7 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
             }
         }
 #pragma unroll
-        for (int n = 0; n < kPlTiles; ++n) {
+        for (int n = 0; n < PT; ++n) {
             u32x4 q;
             float d;
             const uint32_t sv = sw[n][b / 8][(b % 8) / 2];
@@ -822,7 +824,7 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
         }
     }
 #pragma unroll
-    for (int n = 0; n < kPlTiles; ++n) {
+    for (int n = 0; n < PT; ++n) {
         const int64_t row = 16 * (tile0 + n) + i16;
         if (row >= O) continue;
         float* out = partial != nullptr ? partial + sp * T * a.cols + col0 + row : a.y + row;
@@ -1245,7 +1247,7 @@ namespace {
 // and the workspace: partial sums (splits > 1, or always with `partials`: a
 // fused launch's reduction applies its epilogue), then the x planes.
 struct PlanarPlan {
-    int tt = 1, np = 4, splits = 1;
+    int tt = 1, np = 4, splits = 1, pt = 2;
     int64_t partial_bytes = 0, plane_bytes = 0;
     int64_t Bytes() const { return partial_bytes + plane_bytes; }
 };
@@ -1262,18 +1264,28 @@ PlanarPlan PlanPlanar(int64_t T, int64_t K, int64_t cols, bool partials) {
     return p;
 }
 
+template <int QT, int PT>
+void LaunchPlanarPt(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t* planes,
+                    const SkinnyArgs& a, int64_t T, int64_t K, float* partial) {
+    if (p.tt == 1 && p.np == 8) {
+        hipLaunchKernelGGL((GemmPlanar<QT, 1, 8, PT>), grid, dim3(kSkThreads), 0, s, planes, a,
+                           T, K, partial);
+    } else if (p.tt == 1) {
+        hipLaunchKernelGGL((GemmPlanar<QT, 1, 4, PT>), grid, dim3(kSkThreads), 0, s, planes, a,
+                           T, K, partial);
+    } else {
+        hipLaunchKernelGGL((GemmPlanar<QT, 2, 4, PT>), grid, dim3(kSkThreads), 0, s, planes, a,
+                           T, K, partial);
+    }
+}
+
 template <int QT>
 void LaunchPlanarT(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t* planes,
                    const SkinnyArgs& a, int64_t T, int64_t K, float* partial) {
-    if (p.tt == 1 && p.np == 8) {
-        hipLaunchKernelGGL((GemmPlanar<QT, 1, 8>), grid, dim3(kSkThreads), 0, s, planes, a, T, K,
-                           partial);
-    } else if (p.tt == 1) {
-        hipLaunchKernelGGL((GemmPlanar<QT, 1, 4>), grid, dim3(kSkThreads), 0, s, planes, a, T, K,
-                           partial);
+    if (p.pt == 1) {
+        LaunchPlanarPt<QT, 1>(p, grid, s, planes, a, T, K, partial);
     } else {
-        hipLaunchKernelGGL((GemmPlanar<QT, 2, 4>), grid, dim3(kSkThreads), 0, s, planes, a, T, K,
-                           partial);
+        LaunchPlanarPt<QT, 2>(p, grid, s, planes, a, T, K, partial);
     }
 }
 
@@ -1284,15 +1296,26 @@ void LaunchPlanarT(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t
 mlk_status RunPlanar(int qt, const float* x, const uint32_t* planes_in, SkinnyArgs& a, int64_t T,
                      int64_t K, bool partials, void* workspace, size_t workspace_bytes,
                      int* splits, float** partial, hipStream_t s) {
-    int64_t cols = 0, groups = 0;
+    int64_t cols = 0;
     for (int i = 0; i < a.n_seg; ++i) {
         if (!Aligned(a.w[i], 16)) return Fail(MLK_ERR_INVALID, "linear (planar): weights not 16-byte aligned");
         a.col0[i] = cols;
-        a.g0[i] = static_cast<int>(groups);
         cols += a.rows[i];
-        groups += (a.rows[i] + kPlRows - 1) / kPlRows;
     }
-    const PlanarPlan p = PlanPlanar(T, K, cols, partials);
+    PlanarPlan p = PlanPlanar(T, K, cols, partials);
+    // row groups of 4 waves x pt tiles: one tile per wave when two would
+    // leave fewer than two workgroups per compute unit
+    auto count_groups = [&](int pt) {
+        int64_t g = 0;
+        for (int i = 0; i < a.n_seg; ++i) g += (a.rows[i] + 64 * pt - 1) / (64 * pt);
+        return g;
+    };
+    if (count_groups(2) * p.splits < 2 * ComputeUnits()) p.pt = 1;
+    int64_t groups = 0;
+    for (int i = 0; i < a.n_seg; ++i) {
+        a.g0[i] = static_cast<int>(groups);
+        groups += (a.rows[i] + 64 * p.pt - 1) / (64 * p.pt);
+    }
     if (workspace == nullptr || !Aligned(workspace, 16) ||
         static_cast<int64_t>(workspace_bytes) < p.Bytes()) {
         return Fail(MLK_ERR_INVALID, "linear (planar): workspace of %lld bytes needed",
