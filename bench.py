@@ -20,7 +20,8 @@ and graph-replayed), configs[3] (Q8_0/Q4_0/Q4_1 gathers) and configs[4]
 (the 70B chain), each beside the reference's CPU code timed on this host;
 and "decode_layer_8b": one Llama-3-8B layer through mlk_forward_layer_batch
 as a decode step (one token at position 8191, and 16 tokens at positions in
-0..8191 on planar weights), Q8_0 / Q4_0 / F32, weights rotated over 4 layers.
+0..8191; Q8_0 / Q4_0 on their planar copies), Q8_0 / Q4_0 / F32, weights
+rotated over 4 layers.
 Before each measured section a ZeroKernel launch of 4096 * (100 + i) bytes
 marks section i in a rocprofv3 trace (bench.py --rocprof-report uses it).
 
@@ -782,8 +783,7 @@ def _device_layer(mlk, fwd, cfg, wt, seed):
     """One Llama-3-8B-shaped layer's weights on the device (N(0, 0.02),
     quantized on the device; norm weights N(1, 0.1)) as LayerWeights, plus
     the buffers that hold them.  Q8_0 / Q4_0 weights also get a planar copy
-    (mlk_quant_to_planar), which calls of 2..32 tokens run on; one token
-    reads the blocks."""
+    (mlk_quant_to_planar), which calls of 1..32 tokens run on."""
     D, F = cfg["dim"], cfg["hidden_dim"]
     QD, KD = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
     shapes = {"wq": (QD, D), "wk": (KD, D), "wv": (KD, D), "wo": (D, QD), "w_gate": (F, D),
@@ -803,7 +803,7 @@ def _device_layer(mlk, fwd, cfg, wt, seed):
             mlk.quantize(wt, tmp, o, i, buf)
             lw.type = mlk.QUANT[wt]
             n_planar = mlk.quant_planar_bytes(wt, o, i)
-            if n_planar > 0:  # the planar copy the 2..32-token calls run on
+            if n_planar > 0:  # the planar copy the 1..32-token calls run on
                 pl = mlk.DeviceBuffer(n_planar, np.uint8)
                 mlk.quant_to_planar(wt, buf, o, i, pl)
                 lw.planar = pl.ptr
