@@ -410,7 +410,8 @@ def gather_fractions(entry):
 # to (the chain kernels run at several shapes in one command).
 
 PHASE_BASE = 100
-PHASES = ("c3_chain", "c3_ops", "c2_decode", "c1_tiny", "c4_gather", "c5_chain", "c5_ops")
+PHASES = ("c3_chain", "c3_ops", "c2_decode", "c1_tiny", "c4_gather", "c5_chain", "c5_ops",
+          "c2_decode_graph", "c1_tiny_graph")
 
 
 class Marks:
@@ -443,6 +444,7 @@ def c1_tiny(mlk, steps, warmup, marks):
     n = max(steps, 200)
     marks("c1_tiny", ch.stream)
     eager = ch.run(n, warmup) / n
+    marks("c1_tiny_graph", ch.stream)
     graph = ch.run_graph(n)
     out = {"tokens": T, "us_per_chain_eager": round(eager * 1e3, 2),
            "us_per_chain_graph": round(graph * 1e3, 2),
@@ -473,15 +475,13 @@ def c2_decode(mlk, steps, warmup, marks, table):
     launches and one HIP graph replay per step."""
     c2 = workloads.CONFIGS["c2_decode_8b"]
     out = {}
-    first = True
     for t in c2["tokens"]:
         pos = workloads.decode_positions(t, c2["max_pos"], c2["seed"])
         dch = Chain(mlk, c2, t, seed=c2["seed"], n_sets=2, positions=pos, table=table)
-        if first:
-            marks("c2_decode", dch.stream)
-            first = False
+        marks("c2_decode", dch.stream)
         n = max(steps, 100)
         eager = dch.run(n, warmup) / n
+        marks("c2_decode_graph", dch.stream)
         graph = dch.run_graph(n)
         out[str(t)] = {"us_per_chain_eager": round(eager * 1e3, 2),
                        "us_per_chain_graph": round(graph * 1e3, 2),
@@ -1318,8 +1318,10 @@ def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
     # decode and tiny: latency-bound; every launch of the sections by kernel and grid
     lines = ["# Decode steps, configs[1], and the tiny chain, configs[0]: rocprofv3 summary",
              ""] + preamble
-    for sec, title in (("c2_decode", "configs[1]: 8B chain at T = 1..64 (eager and graph-replayed launches)"),
-                       ("c1_tiny", "configs[0]: tiny chain, 6 tokens")):
+    for sec, title in (("c2_decode", "configs[1]: 8B chain at T = 1..64, eager launches"),
+                       ("c2_decode_graph", "configs[1]: 8B chain at T = 1..64, graph-replayed launches"),
+                       ("c1_tiny", "configs[0]: tiny chain, 6 tokens, eager launches"),
+                       ("c1_tiny_graph", "configs[0]: tiny chain, 6 tokens, graph-replayed launches")):
         lines += [f"## {title}", "", "| op | kernel | grid (work-items) | launches | avg us | min us |",
                   "|---|---|---|---|---|---|"]
         groups = {}
