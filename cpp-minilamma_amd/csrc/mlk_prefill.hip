@@ -31,9 +31,23 @@
 // (-inf score) per query.  A wave whose head is past its group (head counts
 // per KV head that are not a multiple of 4) computes on head 0's query and
 // stores nothing: no branch around the loop body.  FLOPs: 4 * hd * H * sum_t (pos0 + t + 1).
+//
+// bf16 products (kBf, decode tiles at head_dim 128 whose grid fits one
+// workgroup per compute unit): K, V, q and p are each the exact sum of
+// three bf16 pieces (x with its low 16 bits cleared, the same of the rest,
+// the rest: at most 8 significant bits each), staged once per tile by the
+// thread that loaded them.  v_mfma_f32_16x16x32_bf16 takes 32 dims (scores)
+// or the tile's 32 positions (values) per instruction in half the cycles of
+// the fp32 instruction's 4.  Scores keep the 6 piece products above
+// 2^-21 relative (|dropped| < 2^-20 |q_d k_d|, 16 u: within the gamma_{hd+1}
+// score bound with the fp32 sums); values keep all 9, so their products are
+// exact and only fp32 summation rounds.  The value MFMA's k index is the
+// lane's own 8 probabilities: slot 8 kq + j is position 16 (j / 4) + 4 kq +
+// j % 4 of the tile, the order V^T is staged in.
 #include "mlk_attention.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace mlk {
 namespace {
@@ -85,6 +99,108 @@ struct KvTile {
     }
 };
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+constexpr int kBfKLd = 8;  // bf16 padding per K plane row (rows 16 bytes apart in bank terms)
+constexpr int kBfVLd = kPfTile + 8;  // V^T plane row: 32 slots + 8 padding
+
+// K planes [piece][32 positions][HD + 8] and V^T planes [piece][HD][40] of
+// a tile, bf16 (two buffers).
+template <int HD>
+struct __align__(16) PrefillSmemBf {
+    uint16_t k[2][3 * kPfTile * (HD + kBfKLd)];
+    uint16_t v[2][3 * HD * kBfVLd];
+};
+
+// The three bf16 pieces of 4 floats, 4 per dword pair (low half first).
+__device__ inline void SplitPieces4(f32x4 x, uint2 (&o)[3]) {
+    uint32_t h[4], m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t u = __float_as_uint(x[i]);
+        const float r = x[i] - __uint_as_float(u & 0xFFFF0000u);
+        const uint32_t ru = __float_as_uint(r);
+        h[i] = u;
+        m[i] = ru;
+        l[i] = __float_as_uint(r - __uint_as_float(ru & 0xFFFF0000u));
+    }
+    o[0] = make_uint2(__builtin_amdgcn_perm(h[1], h[0], 0x07060302u),
+                      __builtin_amdgcn_perm(h[3], h[2], 0x07060302u));
+    o[1] = make_uint2(__builtin_amdgcn_perm(m[1], m[0], 0x07060302u),
+                      __builtin_amdgcn_perm(m[3], m[2], 0x07060302u));
+    o[2] = make_uint2(__builtin_amdgcn_perm(l[1], l[0], 0x07060302u),
+                      __builtin_amdgcn_perm(l[3], l[2], 0x07060302u));
+}
+
+// The three pieces of 8 floats as bf16x8 operands.
+__device__ inline void SplitPieces8(f32x4 a, f32x4 b, bf16x8 (&o)[3]) {
+    uint2 pa[3], pb[3];
+    SplitPieces4(a, pa);
+    SplitPieces4(b, pb);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        const uint4 w = make_uint4(pa[p].x, pa[p].y, pb[p].x, pb[p].y);
+        o[p] = __builtin_bit_cast(bf16x8, w);
+    }
+}
+
+// The next tile for the bf16 kernel: thread tid holds one 4 x 4 block of K
+// and one of V, at positions 4 a .. 4 a + 3 and dims 4 c4 .. 4 c4 + 3
+// (head_dim 128), positions past max_pos reading max_pos's row.  K takes
+// a = tid / 32, c4 = tid % 32 (a 16-lane group writes 128 contiguous bytes
+// of a plane row); V takes a = tid % 8, c4 = tid / 8, so a group's V^T
+// writes (8 position groups x 2 dim rows, 80 bytes apart) meet each LDS
+// bank once.
+struct KvBlockBf {
+    f32x4 k[4], v[4];
+    const float* kb;
+    const float* vb;
+    int64_t slot, max_pos;
+    __device__ void Load(int64_t p0) {
+        const int tid = static_cast<int>(threadIdx.x);
+        const int ak = tid / 32, ck = tid % 32, av = tid % 8, cv = tid / 8;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t p = p0 + 4 * ak + r;
+            const int64_t pos = p <= max_pos ? p : max_pos;
+            k[r] = *reinterpret_cast<const f32x4*>(kb + pos * slot + 4 * ck);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t p = p0 + 4 * av + r;
+            const int64_t pos = p <= max_pos ? p : max_pos;
+            v[r] = *reinterpret_cast<const f32x4*>(vb + pos * slot + 4 * cv);
+        }
+    }
+    // K rows 4 a + r; V^T rows 4 c4 + e at slots s0 .. s0 + 3, where
+    // positions 4 a .. 4 a + 3 sit (slot 8 kq + j: position 16 (j / 4) +
+    // 4 kq + j % 4)
+    __device__ void Store(uint16_t* ks, uint16_t* vs) const {
+        constexpr int HD = 128;
+        constexpr int KL = HD + kBfKLd;
+        const int tid = static_cast<int>(threadIdx.x);
+        const int a = tid / 32, c4 = tid % 32, av = tid % 8, cv = tid / 8;
+        const int s0 = av < 4 ? 8 * av : 8 * (av - 4) + 4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint2 pc[3];
+            SplitPieces4(k[r], pc);
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                *reinterpret_cast<uint2*>(ks + (p * kPfTile + 4 * a + r) * KL + 4 * c4) = pc[p];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint2 pc[3];
+            SplitPieces4(f32x4{v[0][e], v[1][e], v[2][e], v[3][e]}, pc);
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                *reinterpret_cast<uint2*>(vs + (p * HD + 4 * cv + e) * kBfVLd + s0) = pc[p];
+            }
+        }
+    }
+};
+
 // kChunked (decode tokens at any positions, AttnDecodeTile below): the
 // token's position comes from `positions`, and the workgroup covers one
 // chunk of cache positions, writing partials for AttnCombine.
@@ -97,15 +213,17 @@ struct TileChunks {
     int32_t* err;
 };
 
-template <int HD, bool kChunked>
+template <int HD, bool kChunked, bool kBf>
 __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const float* __restrict__ q, int64_t q_stride, const float* __restrict__ kc,
     const float* __restrict__ vc, int64_t slot, int KV, int H, int32_t pos0, int64_t T,
     float scale, float* __restrict__ out, int head_blocks, TileChunks tc) {
 #pragma clang fp contract(off)
+    static_assert(!kBf || (HD == 128 && kChunked), "bf16 products: decode tiles, head_dim 128");
     constexpr int LD = HD + 4;
     constexpr int NC = HD / 16;                          // 16-dim chunks
-    __shared__ PrefillSmem<HD> sm;
+    constexpr int KL = HD + kBfKLd;                      // K plane row (bf16)
+    __shared__ typename std::conditional<kBf, PrefillSmemBf<HD>, PrefillSmem<HD>>::type sm;
     const int group = H / KV;
     const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
     int64_t bid = blockIdx.x;
@@ -156,12 +274,25 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
         }
     }
 
-    f32x4 qv[NC];
-    const float* qrow = q + t * q_stride + static_cast<int64_t>(h) * HD + 4 * kq;
+    f32x4 qv[NC];         // fp32: dims 16 c + 4 kq .. + 3
+    bf16x8 qp[3][HD / 32];  // bf16: pieces of dims 32 c + 8 kq .. + 7
+    if constexpr (kBf) {
+        const float* qrow = q + t * q_stride + static_cast<int64_t>(h) * HD + 8 * kq;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c);
+        for (int c = 0; c < HD / 32; ++c) {
+            bf16x8 pc[3];
+            SplitPieces8(*reinterpret_cast<const f32x4*>(qrow + 32 * c),
+                         *reinterpret_cast<const f32x4*>(qrow + 32 * c + 4), pc);
+#pragma unroll
+            for (int p = 0; p < 3; ++p) qp[p][c] = pc[p];
+        }
+    } else {
+        const float* qrow = q + t * q_stride + static_cast<int64_t>(h) * HD + 4 * kq;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c);
+    }
 
-    KvTile<HD> tile;
+    typename std::conditional<kBf, KvBlockBf, KvTile<HD>>::type tile;
     tile.kb = kc + static_cast<int64_t>(g) * HD;
     tile.vb = vc + static_cast<int64_t>(g) * HD;
     tile.slot = slot;
@@ -195,14 +326,33 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
 #pragma unroll
             for (int pt = 0; pt < 2; ++pt) {
                 s[pt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                const float* krow = &sm.k[buf][(pt * 16 + i16) * LD + 4 * kq];
+                if constexpr (kBf) {
+                    const uint16_t* krow = &sm.k[buf][(pt * 16 + i16) * KL + 8 * kq];
 #pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    const f32x4 kk = *reinterpret_cast<const f32x4*>(krow + 16 * c);
+                    for (int c = 0; c < HD / 32; ++c) {
+                        bf16x8 kp[3];
 #pragma unroll
-                    for (int st = 0; st < 4; ++st) {
-                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[st], qv[c][st], s[pt], 0,
-                                                                     0, 0);
+                        for (int p = 0; p < 3; ++p) {
+                            kp[p] = *reinterpret_cast<const bf16x8*>(krow + p * kPfTile * KL + 32 * c);
+                        }
+                        // the 6 largest piece products, smallest first
+                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp[2], qp[0][c], s[pt], 0, 0, 0);
+                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp[0], qp[2][c], s[pt], 0, 0, 0);
+                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp[1], qp[1][c], s[pt], 0, 0, 0);
+                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp[1], qp[0][c], s[pt], 0, 0, 0);
+                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp[0], qp[1][c], s[pt], 0, 0, 0);
+                        s[pt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kp[0], qp[0][c], s[pt], 0, 0, 0);
+                    }
+                } else {
+                    const float* krow = &sm.k[buf][(pt * 16 + i16) * LD + 4 * kq];
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) {
+                        const f32x4 kk = *reinterpret_cast<const f32x4*>(krow + 16 * c);
+#pragma unroll
+                        for (int st = 0; st < 4; ++st) {
+                            s[pt] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[st], qv[c][st], s[pt],
+                                                                         0, 0, 0);
+                        }
                     }
                 }
             }
@@ -242,15 +392,40 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
                 l += pv[i];
             }
             m = mnew;
+            if constexpr (kBf) {
+                // B: this lane's probabilities, slot j = position 16 (j / 4) + 4 kq + j % 4
+                bf16x8 pp[3];
+                SplitPieces8(f32x4{pv[0], pv[1], pv[2], pv[3]}, f32x4{pv[4], pv[5], pv[6], pv[7]}, pp);
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
+                for (int c = 0; c < NC; ++c) {
+                    const uint16_t* vrow = &sm.v[buf][(16 * c + i16) * kBfVLd + 8 * kq];
+                    bf16x8 vp[3];
 #pragma unroll
-                for (int pt = 0; pt < 2; ++pt) {
+                    for (int p = 0; p < 3; ++p) {
+                        vp[p] = *reinterpret_cast<const bf16x8*>(vrow + p * HD * kBfVLd);
+                    }
+                    // all 9 piece products (exact), smallest first
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[2], pp[2], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[2], pp[1], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[1], pp[2], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[2], pp[0], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[0], pp[2], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[1], pp[1], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[1], pp[0], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[0], pp[1], acc[c], 0, 0, 0);
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[0], pp[0], acc[c], 0, 0, 0);
+                }
+            } else {
 #pragma unroll
-                    for (int st = 0; st < 4; ++st) {
-                        const float vv = sm.v[buf][(pt * 16 + 4 * kq + st) * LD + 16 * c + i16];
-                        acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv, pv[pt * 4 + st], acc[c],
-                                                                      0, 0, 0);
+                for (int c = 0; c < NC; ++c) {
+#pragma unroll
+                    for (int pt = 0; pt < 2; ++pt) {
+#pragma unroll
+                        for (int st = 0; st < 4; ++st) {
+                            const float vv = sm.v[buf][(pt * 16 + 4 * kq + st) * LD + 16 * c + i16];
+                            acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv, pv[pt * 4 + st],
+                                                                          acc[c], 0, 0, 0);
+                        }
                     }
                 }
             }
@@ -314,10 +489,11 @@ mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, 
     const dim3 grid(static_cast<unsigned>(blocks));
     const TileChunks none{};
     if (head_dim == 64) {
-        hipLaunchKernelGGL((AttnPrefill<64, false>), grid, dim3(kPfThreads), 0, s, q, q_row_stride,
-                           kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks, none);
+        hipLaunchKernelGGL((AttnPrefill<64, false, false>), grid, dim3(kPfThreads), 0, s, q,
+                           q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
+                           none);
     } else {
-        hipLaunchKernelGGL((AttnPrefill<128, false>), grid, dim3(kPfThreads), 0, s, q,
+        hipLaunchKernelGGL((AttnPrefill<128, false, false>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
                            none);
     }
@@ -352,10 +528,17 @@ mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* k
     const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
     const dim3 grid(static_cast<unsigned>(blocks));
     if (head_dim == 64) {
-        hipLaunchKernelGGL((AttnPrefill<64, true>), grid, dim3(kPfThreads), 0, s, q, q_row_stride,
-                           kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks, tc);
+        hipLaunchKernelGGL((AttnPrefill<64, true, false>), grid, dim3(kPfThreads), 0, s, q,
+                           q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
+                           tc);
+    } else if (blocks <= ComputeUnits()) {
+        // bf16 products: their 111 KB of LDS leave one workgroup per unit,
+        // which a grid this small uses anyway
+        hipLaunchKernelGGL((AttnPrefill<128, true, true>), grid, dim3(kPfThreads), 0, s, q,
+                           q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
+                           tc);
     } else {
-        hipLaunchKernelGGL((AttnPrefill<128, true>), grid, dim3(kPfThreads), 0, s, q,
+        hipLaunchKernelGGL((AttnPrefill<128, true, false>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
                            tc);
     }
