@@ -104,11 +104,11 @@ constexpr int kBfKLd = 8;  // bf16 padding per K plane row (rows 16 bytes apart 
 constexpr int kBfVLd = kPfTile + 8;  // V^T plane row: 32 slots + 8 padding
 
 // K planes [piece][32 positions][HD + 8] and V^T planes [piece][HD][40] of
-// a tile, bf16 (two buffers).
-template <int HD>
+// a tile, bf16: NBUF buffers (one: 56.8 KB, two workgroups per compute unit).
+template <int HD, int NBUF>
 struct __align__(16) PrefillSmemBf {
-    uint16_t k[2][3 * kPfTile * (HD + kBfKLd)];
-    uint16_t v[2][3 * HD * kBfVLd];
+    uint16_t k[NBUF][3 * kPfTile * (HD + kBfKLd)];
+    uint16_t v[NBUF][3 * HD * kBfVLd];
 };
 
 // The three bf16 pieces of 4 floats, 4 per dword pair (low half first).
@@ -213,17 +213,18 @@ struct TileChunks {
     int32_t* err;
 };
 
-template <int HD, bool kChunked, bool kBf>
+template <int HD, bool kChunked, bool kBf, int NBUF = 2>
 __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const float* __restrict__ q, int64_t q_stride, const float* __restrict__ kc,
     const float* __restrict__ vc, int64_t slot, int KV, int H, int32_t pos0, int64_t T,
     float scale, float* __restrict__ out, int head_blocks, TileChunks tc) {
 #pragma clang fp contract(off)
-    static_assert(!kBf || (HD == 128 && kChunked), "bf16 products: decode tiles, head_dim 128");
+    static_assert(!kBf || HD == 128, "bf16 products: head_dim 128");
+    static_assert(NBUF == 2 || (NBUF == 1 && kBf), "one tile buffer: bf16 products only");
     constexpr int LD = HD + 4;
     constexpr int NC = HD / 16;                          // 16-dim chunks
     constexpr int KL = HD + kBfKLd;                      // K plane row (bf16)
-    __shared__ typename std::conditional<kBf, PrefillSmemBf<HD>, PrefillSmem<HD>>::type sm;
+    __shared__ typename std::conditional<kBf, PrefillSmemBf<HD, NBUF>, PrefillSmem<HD>>::type sm;
     const int group = H / KV;
     const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
     int64_t bid = blockIdx.x;
@@ -314,7 +315,7 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const int32_t my_pos_32 = static_cast<int32_t>(my_pos);
     const float scale2 = scale * 1.44269504088896340736f;
     for (int64_t it = 0; it < n_tiles; ++it) {
-        const int buf = static_cast<int>(it & 1);
+        const int buf = NBUF == 2 ? static_cast<int>(it & 1) : 0;
         const int32_t p0_32 = static_cast<int32_t>(p_begin + it * kPfTile);
         load(p_begin + (it + 1 < n_tiles ? it + 1 : it) * kPfTile);
         // Nothing crosses this point: without it the scheduler sinks the
@@ -430,7 +431,12 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
                 }
             }
         }
-        store(buf ^ 1);
+        if constexpr (NBUF == 1) {
+            __syncthreads();  // every wave is done with the tile before it is replaced
+            store(0);
+        } else {
+            store(buf ^ 1);
+        }
         __syncthreads();
     }
     l += __shfl_xor(l, 16, kWave);
@@ -493,7 +499,7 @@ mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, 
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
                            none);
     } else {
-        hipLaunchKernelGGL((AttnPrefill<128, false, false>), grid, dim3(kPfThreads), 0, s, q,
+        hipLaunchKernelGGL((AttnPrefill<128, false, true, 1>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
                            none);
     }
@@ -538,7 +544,7 @@ mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* k
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
                            tc);
     } else {
-        hipLaunchKernelGGL((AttnPrefill<128, true, false>), grid, dim3(kPfThreads), 0, s, q,
+        hipLaunchKernelGGL((AttnPrefill<128, true, true, 1>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
                            tc);
     }
