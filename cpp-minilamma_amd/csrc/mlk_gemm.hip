@@ -374,20 +374,38 @@ __global__ __launch_bounds__(kGemmThreads) void GemmMfma(const float* __restrict
     }
 }
 
-// p[0] + p[stride] + ... + p[(splits - 1) * stride], added in that order;
-// the loads go out 8 at a time (a rolled loop would wait for each one).
-__device__ inline float SumSplits(const float* p, int splits, int64_t stride) {
-    float v = p[0];
-    int sp = 1;
-    for (; sp + 8 <= splits; sp += 8) {
-        float t[8];
+// For each n: p[n][0] + p[n][stride] + ... + p[n][(splits - 1) * stride],
+// added in that order (splits >= 1).  The loads of all N sums go out 8
+// splits at a time, a group's indices past the last split reading the last
+// one (not added): a rolled remainder loop would wait for each load.
+template <int N>
+__device__ inline void SumSplitsN(const float* const (&p)[N], int splits, int64_t stride,
+                                  float (&v)[N]) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) t[j] = p[(sp + j) * stride];
+    for (int n = 0; n < N; ++n) v[n] = 0.0f;
+    for (int sp = 0; sp < splits; sp += 8) {
+        float t[N][8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v += t[j];
+        for (int j = 0; j < 8; ++j) {
+            const int64_t at = static_cast<int64_t>(sp + j < splits ? sp + j : splits - 1) * stride;
+#pragma unroll
+            for (int n = 0; n < N; ++n) t[n][j] = p[n][at];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (sp + j < splits) {
+#pragma unroll
+                for (int n = 0; n < N; ++n) v[n] = sp + j == 0 ? t[n][j] : v[n] + t[n][j];
+            }
+        }
     }
-    for (; sp < splits; ++sp) v += p[sp * stride];
-    return v;
+}
+
+__device__ inline float SumSplits(const float* p, int splits, int64_t stride) {
+    const float* q[1] = {p};
+    float v[1];
+    SumSplitsN<1>(q, splits, stride, v);
+    return v[0];
 }
 
 // y = sum of the splits' partial sums, in split order, + bias.
@@ -918,11 +936,20 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int64_t t = i / out_cols, c = i % out_cols;
-        auto sum = [&](int64_t col) { return SumSplits(partial + t * cols + col, splits, stride); };
+        const float* row = partial + t * cols;
+        auto sum = [&](int64_t col) { return SumSplits(row + col, splits, stride); };
+        auto sum2 = [&](int64_t c0, int64_t c1, float* a0, float* a1) {
+            const float* q[2] = {row + c0, row + c1};
+            float v[2];
+            SumSplitsN<2>(q, splits, stride, v);
+            *a0 = v[0];
+            *a1 = v[1];
+        };
         if (mode == kStreamSwiGlu) {
             const int64_t F = a.seg[0].rows;
             auto swiglu = [&](int64_t col) {
-                float g = sum(col), u = sum(F + col);
+                float g, u;
+                sum2(col, F + col, &g, &u);
                 if (a.seg[0].bias != nullptr) g += a.seg[0].bias[col];
                 if (a.seg[1].bias != nullptr) u += a.seg[1].bias[col];
                 return SwiGluF(g, u);
@@ -951,7 +978,8 @@ __global__ __launch_bounds__(kGemmThreads) void SplitKReduceFused(const float* _
             const bool is_k = col >= QD;
             const StreamSeg& sg = is_k ? a.seg[1] : a.seg[0];
             const int64_t local = is_k ? col - QD : col;
-            float x0 = sum(col), x1 = sum(col + 1);
+            float x0, x1;
+            sum2(col, col + 1, &x0, &x1);
             if (sg.bias != nullptr) {
                 x0 += sg.bias[local];
                 x1 += sg.bias[local + 1];

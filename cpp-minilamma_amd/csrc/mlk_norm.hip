@@ -76,25 +76,24 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(
                 if (i < dim4) {
                     float4 d = LoadNT(dr + i);
                     if (kPartials && splits > 1) {
-                        float4 t[8];
-                        int sp = 1;
-                        for (; sp + 8 <= splits; sp += 8) {  // loads 8 at a time, adds in order
-#pragma unroll
-                            for (int j = 0; j < 8; ++j) t[j] = LoadNT(dr + (sp + j) * (split_stride / 4) + i);
+                        // splits 1.. added in order; loads 8 at a time, indices
+                        // past the last split reading the last one (not added)
+                        for (int sp = 1; sp < splits; sp += 8) {
+                            float4 t[8];
 #pragma unroll
                             for (int j = 0; j < 8; ++j) {
-                                d.x += t[j].x;
-                                d.y += t[j].y;
-                                d.z += t[j].z;
-                                d.w += t[j].w;
+                                const int64_t at = sp + j < splits ? sp + j : splits - 1;
+                                t[j] = LoadNT(dr + at * (split_stride / 4) + i);
                             }
-                        }
-                        for (; sp < splits; ++sp) {
-                            const float4 e = LoadNT(dr + sp * (split_stride / 4) + i);
-                            d.x += e.x;
-                            d.y += e.y;
-                            d.z += e.z;
-                            d.w += e.w;
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                if (sp + j < splits) {
+                                    d.x += t[j].x;
+                                    d.y += t[j].y;
+                                    d.z += t[j].z;
+                                    d.w += t[j].w;
+                                }
+                            }
                         }
                     }
                     if (kPartials && dbias != nullptr) {
