@@ -374,6 +374,200 @@ __global__ __launch_bounds__(kGemmThreads) void GemmMfma(const float* __restrict
     }
 }
 
+// ------------------------------------------------ tiles on bf16 piece products
+// The tiled GEMM for Q8_0 / Q4_0 weights (block or planar layout) with every
+// product exact, as in GemmPlanar below: a code is a small integer, exact in
+// bf16, and x is the exact sum of three bf16 pieces, so for each block
+//   S = sum_i code_i x_i  (3 v_mfma_f32_16x16x32_bf16, fp32 sums only),
+//   acc += d * S.
+// Same tiling and split-K protocol as GemmMfma (128 token rows x 128
+// outputs, one 32-input block per stage, wave w: rows (w / 2) * 64, outputs
+// (w % 2) * 64, 4 x 4 MFMA tiles), 8x less matrix-core time per stage.  The
+// thread that loads an x float4 splits it into pieces once per stage; x
+// planes are [piece][128 rows][32 bf16] with the 16-byte group g of row r
+// at g ^ ((r / 2) % 4), and W codes [128 rows][32 bf16 + 8] (80-byte rows),
+// so the operand reads of 8 lanes meet 8 distinct bank quads.  Two stage
+// buffers, 69 KB: two workgroups per compute unit.
+typedef __bf16 bf16x8g __attribute__((ext_vector_type(8)));
+constexpr int kPcWRow = 20;  // W code row, dwords
+
+struct __align__(16) PiecesSmem {
+    uint32_t x[2][3 * 128 * 16];
+    uint32_t w[2][kBN * kPcWRow];
+    float d[2][kBN];
+};
+
+// The pieces of 4 floats, two per dword: o[0] high, o[1] middle, o[2] low.
+// Finite values: mask and subtract; a wave with any inf or NaN takes
+// SplitBf's form (the value whole in the high piece), so products with them
+// are what fp32 products would be.
+__device__ inline void PiecesOf4(float4 v, uint2 (&o)[3]) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h[4], m[4], l[4];
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t u = __float_as_uint(x[i]);
+        const float r = x[i] - __uint_as_float(u & 0xFFFF0000u);
+        h[i] = u;
+        m[i] = __float_as_uint(r);
+        l[i] = __float_as_uint(r - __uint_as_float(m[i] & 0xFFFF0000u));
+        bad |= !__builtin_isfinite(x[i]);
+    }
+    if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float p[3];
+            SplitBf(x[i], p);
+            h[i] = __float_as_uint(p[0]);
+            m[i] = __float_as_uint(p[1]);
+            l[i] = __float_as_uint(p[2]);
+        }
+    }
+    o[0] = make_uint2(__builtin_amdgcn_perm(h[1], h[0], 0x07060302u),
+                      __builtin_amdgcn_perm(h[3], h[2], 0x07060302u));
+    o[1] = make_uint2(__builtin_amdgcn_perm(m[1], m[0], 0x07060302u),
+                      __builtin_amdgcn_perm(m[3], m[2], 0x07060302u));
+    o[2] = make_uint2(__builtin_amdgcn_perm(l[1], l[0], 0x07060302u),
+                      __builtin_amdgcn_perm(l[3], l[2], 0x07060302u));
+}
+
+// The 16 signed codes a weight tile thread holds (inputs 16h .. 16h + 15 of
+// its row's block), as the tiles' Store decodes them.
+template <int WT>
+__device__ inline void TileCodes(const WTile<WT>& t, int32_t (&c)[16]) {
+    const int h = threadIdx.x & 1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if constexpr (WT == MLK_Q8_0 || WT == kWPlanarQ8) {
+            c[i] = static_cast<int32_t>(t.q[i / 4] << (24 - 8 * (i % 4))) >> 24;
+        } else if constexpr (WT == MLK_Q4_0) {
+            const uint32_t byte = (t.q[i / 4] >> (8 * (i % 4))) & 0xFFu;
+            c[i] = static_cast<int32_t>(h ? byte >> 4 : byte & 15u) - 8;
+        } else {  // planar Q4_0: input 8g + e is nibble e (low half of byte e, then high)
+            const int e8 = i % 8;
+            const int sh = e8 < 4 ? 8 * e8 : 8 * (e8 - 4) + 4;
+            c[i] = static_cast<int32_t>(t.q[i / 8] << (28 - sh)) >> 28;
+        }
+    }
+}
+
+template <int WT>
+__global__ __launch_bounds__(kGemmThreads) void GemmPieces(const float* __restrict__ x,
+                                                           const uint8_t* __restrict__ w,
+                                                           const float* __restrict__ bias,
+                                                           float* __restrict__ y, int64_t T,
+                                                           int64_t K, int64_t O,
+                                                           int64_t row_bytes, int tiles_m,
+                                                           int tiles, int64_t per_split,
+                                                           float* __restrict__ partial) {
+    constexpr int BM = 128;
+    __shared__ PiecesSmem sm;
+    const int tile = static_cast<int>(blockIdx.x) % tiles;
+    const int sp = static_cast<int>(blockIdx.x) / tiles;
+    const int tm = tile % tiles_m;
+    const int tn = tile / tiles_m;
+    const int64_t m0 = static_cast<int64_t>(tm) * BM;
+    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int i16 = lane & 15, kq = lane >> 4;
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    const int64_t all_stages = (K + kBK - 1) / kBK;
+    const int64_t s0 = sp * per_split;
+    const int64_t s1 = s0 + per_split < all_stages ? s0 + per_split : all_stages;
+    F32Tile<BM> xt;
+    WTile<WT> wt;
+    // one stage into LDS buffer b: x pieces, W codes as bf16, scales
+    auto store = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < F32Tile<BM>::kN; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kGemmThreads * i;
+            const int r = idx >> 3, c8 = idx & 7;
+            uint2 pc[3];
+            PiecesOf4(Mask4(xt.v[i], ((xt.keep >> i) & 1u) ? ~0u : 0u), pc);
+            const int at = r * 16 + (((c8 >> 1) ^ ((r >> 1) & 3)) << 2) + 2 * (c8 & 1);
+#pragma unroll
+            for (int p = 0; p < 3; ++p) *reinterpret_cast<uint2*>(&sm.x[b][p * 128 * 16 + at]) = pc[p];
+        }
+        int32_t c[16];
+        TileCodes<WT>(wt, c);
+        uint32_t pk[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            pk[i] = wt.keep ? PackBf(static_cast<float>(c[2 * i]), static_cast<float>(c[2 * i + 1]))
+                            : 0u;
+        }
+        const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
+        uint4* dst = reinterpret_cast<uint4*>(&sm.w[b][row * kPcWRow + 8 * h]);
+        dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+        if (h == 0) sm.d[b][row] = wt.keep ? HalfHw(wt.d & 0xFFFFu) : 0.0f;
+    };
+    xt.Load(x, T, K, m0, s0 * kBK);
+    wt.Load(w, O, K, row_bytes, n0, s0 * kBK);
+    store(0);
+    __syncthreads();
+    for (int64_t s = s0; s < s1; ++s) {
+        const int buf = static_cast<int>((s - s0) & 1);
+        const int64_t k_next = (s + 1 < s1 ? s + 1 : s) * kBK;
+        xt.Load(x, T, K, m0, k_next);
+        wt.Load(w, O, K, row_bytes, n0, k_next);
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8g b[4];
+        float dj[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = wn * 64 + 16 * j + i16;
+            b[j] = *reinterpret_cast<const bf16x8g*>(&sm.w[buf][row * kPcWRow + 4 * kq]);
+            dj[j] = sm.d[buf][row];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = wm * 64 + 16 * i + i16;
+            const int at = r * 16 + ((kq ^ ((r >> 1) & 3)) << 2);
+            bf16x8g a[3];
+#pragma unroll
+            for (int p = 0; p < 3; ++p) a[p] = *reinterpret_cast<const bf16x8g*>(&sm.x[buf][p * 128 * 16 + at]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f32x4 S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[2], b[j], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[1], b[j], S, 0, 0, 0);
+                S = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[0], b[j], S, 0, 0, 0);
+#pragma unroll
+                for (int r4 = 0; r4 < 4; ++r4) acc[i][j][r4] += dj[j] * S[r4];
+            }
+        }
+        store(buf ^ 1);
+        __syncthreads();
+    }
+
+    float* out = partial != nullptr ? partial + sp * T * O : y;
+    const float* add = partial != nullptr ? nullptr : bias;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t col = n0 + wn * 64 + 16 * j + i16;
+        if (col >= O) continue;
+        const float bb = add != nullptr ? add[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = m0 + wm * 64 + 16 * i + 4 * kq + r;
+                if (row < T) out[row * O + col] = acc[i][j][r] + bb;
+            }
+        }
+    }
+}
+
 // For each n: p[n][0] + p[n][stride] + ... + p[n][(splits - 1) * stride],
 // added in that order (splits >= 1).  The loads of all N sums go out 8
 // splits at a time, a group's indices past the last split reading the last
@@ -1082,6 +1276,31 @@ template <int BM>
 void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
                  const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
                  int tiles_m, int tiles, int64_t per_split, float* partial) {
+    // 128-row tiles of Q8_0 / Q4_0 on bf16 piece products; K % 256 == 0 keeps
+    // each product's fp32 roundings (block sum, scale, K / 32 block adds)
+    // under the K of the fp32 kernel's bound
+    if (BM == 128 && K % 256 == 0) {
+        switch (wt) {
+            case MLK_Q8_0:
+                hipLaunchKernelGGL((GemmPieces<MLK_Q8_0>), grid, dim3(kGemmThreads), 0, s, x, w,
+                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+                return;
+            case MLK_Q4_0:
+                hipLaunchKernelGGL((GemmPieces<MLK_Q4_0>), grid, dim3(kGemmThreads), 0, s, x, w,
+                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+                return;
+            case kWPlanarQ8:
+                hipLaunchKernelGGL((GemmPieces<kWPlanarQ8>), grid, dim3(kGemmThreads), 0, s, x, w,
+                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+                return;
+            case kWPlanarQ4:
+                hipLaunchKernelGGL((GemmPieces<kWPlanarQ4>), grid, dim3(kGemmThreads), 0, s, x, w,
+                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
+                return;
+            default:
+                break;
+        }
+    }
     switch (wt) {
         case MLK_Q8_0:
             hipLaunchKernelGGL((GemmMfma<MLK_Q8_0, BM>), grid, dim3(kGemmThreads), 0, s, x, w,
