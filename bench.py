@@ -711,6 +711,28 @@ def linear_bench(mlk, steps, peak, path):
 
 GEMM_TOKENS = (8, 16, 32, 64, 128, 512, 4096)
 MFMA_FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix-core peak
+# Q8_0 / Q4_0 tiles of more than 64 token rows (and the attention at head_dim
+# 128) form each product from three exact bf16 pieces: three bf16 MACs per
+# useful MAC, so their ceiling in useful TFLOP/s is a third of the bf16 peak.
+PIECES_PEAK_TFLOPS = MFMA_BF16_PEAK_TFLOPS / 3
+
+
+def attention_peak(hd):
+    """(peak TFLOP/s of useful MACs, basis) of the tile attention: at
+    head_dim 128 the scores take 6 and the values 9 bf16 piece products per
+    useful MAC (7.5 on average), at 64 the fp32 instruction."""
+    if hd == 128:
+        return MFMA_BF16_PEAK_TFLOPS / 7.5, "bf16 MFMA / 7.5 (piece products)"
+    return MFMA_FP32_PEAK_TFLOPS, "fp32 MFMA"
+
+
+def gemm_peak(wt, T):
+    """(peak TFLOP/s of useful MACs, basis) of the kernel the tiled GEMM
+    runs for weight type `wt` at T token rows (K a multiple of 256)."""
+    if wt in ("q8_0", "q4_0") and T > 64:
+        return PIECES_PEAK_TFLOPS, "bf16 MFMA / 3 (three-piece products)"
+    return MFMA_FP32_PEAK_TFLOPS, "fp32 MFMA"
 
 
 def gemm_bench(mlk, steps, path):
@@ -718,7 +740,7 @@ def gemm_bench(mlk, steps, path):
     (the matrix-core GEMM path): per-projection launch time, each launched
     `steps` times back to back between two events on its stream, and one
     whole layer's seven projections; TFLOP/s = 2 T K O / time against the
-    fp32 MFMA peak.  One weight copy per projection: from 128 rows on these
+    peak of the instruction the kernel uses (gemm_peak).  One weight copy per projection: from 128 rows on these
     shapes are compute-bound, and below that the split-K launches read each
     weight byte once per call either way."""
     cfg = workloads.CONFIGS["c3_prefill_8b"]
@@ -749,8 +771,9 @@ def gemm_bench(mlk, steps, path):
                 e1.synchronize()
                 ms = e0.elapsed_ms(e1) / steps
                 tf = workloads.flops_linear(T, k, o) / (ms * 1e-3) / 1e12
+                peak, _ = gemm_peak(qt, T)
                 per[name] = {"in": k, "out": o, "us": round(ms * 1e3, 2),
-                             "TFLOPs": round(tf, 2), "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+                             "TFLOPs": round(tf, 2), "frac_of_peak": round(tf / peak, 4)}
             e0, e1 = mlk.Event(), mlk.Event()
             e0.record(st)
             for i in range(steps):
@@ -761,11 +784,13 @@ def gemm_bench(mlk, steps, path):
             ms = e0.elapsed_ms(e1) / steps
             fl = sum(workloads.flops_linear(T, k, o) for _, k, o in shapes)
             tf = fl / (ms * 1e-3) / 1e12
+            peak, basis = gemm_peak(qt, T)
             res[str(T)] = {"layer_us": round(ms * 1e3, 2), "layer_flops": fl,
-                           "layer_TFLOPs": round(tf, 2),
-                           "layer_frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4), "ops": per}
+                           "layer_TFLOPs": round(tf, 2), "peak_TFLOPs": round(peak, 1),
+                           "peak_basis": basis,
+                           "layer_frac_of_peak": round(tf / peak, 4), "ops": per}
             print(f"gemm {qt} T={T}: layer {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s "
-                  f"({100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}%) "
+                  f"({100 * tf / peak:.1f}% of {basis}) "
                   + " ".join(f"{n}={v['TFLOPs']}" for n, v in per.items()), flush=True)
         out[qt] = res
         del layers
@@ -874,9 +899,11 @@ def layer_bench(mlk, steps, path):
         e3.synchronize()
         loop_us = e2.elapsed_ms(e3) / n * 1e3
         tf = (fl_lin + fl_att) / (ms * 1e-3) / 1e12
+        peak, basis = gemm_peak(wt, T)
         out[wt] = {"us": round(ms * 1e3, 1), "layer_ms": round(ms, 3),
                    "tokens_per_s": round(T / (ms * 1e-3), 1),
-                   "TFLOPs": round(tf, 2), "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4),
+                   "TFLOPs": round(tf, 2), "peak_TFLOPs": round(peak, 1), "peak_basis": basis,
+                   "frac_of_peak": round(tf / peak, 4),
                    "token_loop_us_per_token": round(loop_us, 1),
                    "token_loop_tokens_per_s": round(1e6 / loop_us, 1),
                    "batch_speedup_over_token_loop": round(loop_us * T / (ms * 1e3), 1)}
@@ -1043,12 +1070,14 @@ def attention_bench(mlk, steps, peak, path):
             else:  # tokens share each K/V tile on the matrix cores: against the MFMA peak
                 fl = workloads.flops_decode_attention(pos, H, hd)
                 tf = fl / (ms * 1e-3) / 1e12
+                apk, abasis = attention_peak(hd)
                 rows[case] = {"us": round(ms * 1e3, 2), "flops": fl, "TFLOPs": round(tf, 2),
-                              "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4),
+                              "peak_TFLOPs": round(apk, 1), "peak_basis": abasis,
+                              "frac_of_peak": round(tf / apk, 4),
                               "token_prefix_bytes": nb, "token_prefix_GBps": round(gbs, 1),
                               "workspace_bytes": wsb}
                 print(f"attention {name} {case}: {ms * 1e3:.2f} us, {tf:.1f} TFLOP/s "
-                      f"({100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}% of fp32 MFMA; per-token prefixes "
+                      f"({100 * tf / apk:.1f}% of {abasis}; per-token prefixes "
                       f"{gbs:.0f} GB/s)", flush=True)
         # causal prefill of a prompt chunk at positions 0..T-1 (matrix cores)
         for T in PREFILL_TOKENS:
@@ -1072,11 +1101,12 @@ def attention_bench(mlk, steps, peak, path):
             ms = e0.elapsed_ms(e1) / n_pf
             fl = workloads.flops_prefill_attention(T, H, hd)
             tf = fl / (ms * 1e-3) / 1e12
+            apk, abasis = attention_peak(hd)
             rows["prefill_T%d" % T] = {"us": round(ms * 1e3, 2), "flops": fl,
-                                       "TFLOPs": round(tf, 2),
-                                       "frac_of_peak": round(tf / MFMA_FP32_PEAK_TFLOPS, 4)}
+                                       "TFLOPs": round(tf, 2), "peak_TFLOPs": round(apk, 1),
+                                       "peak_basis": abasis, "frac_of_peak": round(tf / apk, 4)}
             print(f"attention {name} prefill T={T}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s "
-                  f"({100 * tf / MFMA_FP32_PEAK_TFLOPS:.1f}% of fp32 MFMA)", flush=True)
+                  f"({100 * tf / apk:.1f}% of {abasis})", flush=True)
         out[name] = {"n_heads": H, "n_kv_heads": KV, "head_dim": hd, "cases": rows}
         del kc, vc
     with open(path, "w") as f:
@@ -1388,7 +1418,7 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
         md.append(row)
     md += ["", "Results of the same command (bench.py JSON, events around back-to-back "
            "launches; HBM-bound cases on rotating cold copies, against 8 TB/s; "
-           "matrix-core cases against the 157.3 TFLOP/s fp32 MFMA peak):", "",
+           "matrix-core cases against the peak of the instruction they run: 157.3 TFLOP/s fp32 MFMA, or for bf16 piece products the 2.5 PFLOP/s bf16 peak over the bf16 MACs per useful MAC, 3 in the GEMM and 7.5 in the attention):", "",
            "| case | us | throughput | fraction of peak |", "|---|---|---|---|"]
 
     def rate(node, prefix=""):
