@@ -208,7 +208,8 @@ mlk_status mlk_quant_to_planar(int32_t quant_type, const void* blocks, int64_t r
  * matrix cores with exact products (codes are exact in bf16 and x is split
  * into three exact bf16 pieces), and need a workspace of
  * mlk_linear_planar_workspace_bytes (16-byte aligned); more rows take the
- * fp32 matrix-core GEMM, with the optional workspace of
+ * tiled matrix-core GEMM (from 65 rows with in_features a multiple of 256,
+ * on the same exact bf16 products), with the optional workspace of
  * mlk_linear_workspace_bytes.  No counterpart in the reference. */
 mlk_status mlk_linear_planar(int32_t quant_type, const float* x, const void* w_planar,
                              const float* bias, float* y, int64_t rows, int64_t in_features,
