@@ -387,14 +387,18 @@ __global__ __launch_bounds__(kGemmThreads) void GemmMfma(const float* __restrict
 // planes are [piece][128 rows][32 bf16] with the 16-byte group g of row r
 // at g ^ ((r / 2) % 4), and W codes [128 rows][32 bf16 + 8] (80-byte rows),
 // so the operand reads of 8 lanes meet 8 distinct bank quads.  Two stage
-// buffers, 69 KB: two workgroups per compute unit.
+// buffers, 69 KB: two workgroups per compute unit.  NW = 8 waves take 256
+// outputs per tile (90 KB, one workgroup per unit): each x split then
+// serves twice the outputs, which halves the split work per product, the
+// stage's largest VALU cost.
 typedef __bf16 bf16x8g __attribute__((ext_vector_type(8)));
 constexpr int kPcWRow = 20;  // W code row, dwords
 
+template <int BNT>
 struct __align__(16) PiecesSmem {
     uint32_t x[2][3 * 128 * 16];
-    uint32_t w[2][kBN * kPcWRow];
-    float d[2][kBN];
+    uint32_t w[2][BNT * kPcWRow];
+    float d[2][BNT];
 };
 
 // The pieces of 4 floats, two per dword: o[0] high, o[1] middle, o[2] low.
@@ -452,8 +456,8 @@ __device__ inline void TileCodes(const WTile<WT>& t, int32_t (&c)[16]) {
     }
 }
 
-template <int WT>
-__global__ __launch_bounds__(kGemmThreads) void GemmPieces(const float* __restrict__ x,
+template <int WT, int NW>
+__global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ x,
                                                            const uint8_t* __restrict__ w,
                                                            const float* __restrict__ bias,
                                                            float* __restrict__ y, int64_t T,
@@ -462,16 +466,19 @@ __global__ __launch_bounds__(kGemmThreads) void GemmPieces(const float* __restri
                                                            int tiles, int64_t per_split,
                                                            float* __restrict__ partial) {
     constexpr int BM = 128;
-    __shared__ PiecesSmem sm;
+    constexpr int kThreads = 64 * NW;
+    constexpr int BNT = 32 * NW;               // outputs per tile
+    constexpr int kXN = BM * kBK / 4 / kThreads;  // x float4s per thread and stage
+    __shared__ PiecesSmem<BNT> sm;
     const int tile = static_cast<int>(blockIdx.x) % tiles;
     const int sp = static_cast<int>(blockIdx.x) / tiles;
     const int tm = tile % tiles_m;
     const int tn = tile / tiles_m;
     const int64_t m0 = static_cast<int64_t>(tm) * BM;
-    const int64_t n0 = static_cast<int64_t>(tn) * kBN;
+    const int64_t n0 = static_cast<int64_t>(tn) * BNT;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave & 1, wn = wave >> 1;  // 64 token rows x 64 outputs per wave
     const int i16 = lane & 15, kq = lane >> 4;
 
     f32x4 acc[4][4];
@@ -484,16 +491,31 @@ __global__ __launch_bounds__(kGemmThreads) void GemmPieces(const float* __restri
     const int64_t all_stages = (K + kBK - 1) / kBK;
     const int64_t s0 = sp * per_split;
     const int64_t s1 = s0 + per_split < all_stages ? s0 + per_split : all_stages;
-    F32Tile<BM> xt;
+    // x: thread tid holds float4 tid + kThreads i of the [128][32] stage, 8
+    // per row (rows past T read row 0 and are zeroed at the split)
+    float4 xv[kXN];
+    uint32_t xkeep = 0;
+    auto load_x = [&](int64_t k0) {
+        xkeep = 0;
+#pragma unroll
+        for (int i = 0; i < kXN; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
+            const int64_t r = m0 + (idx >> 3);
+            const int64_t c = k0 + 4 * (idx & 7);
+            const bool ok = r < T && c < K;
+            xkeep |= static_cast<uint32_t>(ok) << i;
+            xv[i] = *reinterpret_cast<const float4*>(x + (ok ? r * K + c : 0));
+        }
+    };
     WTile<WT> wt;
     // one stage into LDS buffer b: x pieces, W codes as bf16, scales
     auto store = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < F32Tile<BM>::kN; ++i) {
-            const int idx = static_cast<int>(threadIdx.x) + kGemmThreads * i;
+        for (int i = 0; i < kXN; ++i) {
+            const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
             const int r = idx >> 3, c8 = idx & 7;
             uint2 pc[3];
-            PiecesOf4(Mask4(xt.v[i], ((xt.keep >> i) & 1u) ? ~0u : 0u), pc);
+            PiecesOf4(Mask4(xv[i], ((xkeep >> i) & 1u) ? ~0u : 0u), pc);
             const int at = r * 16 + (((c8 >> 1) ^ ((r >> 1) & 3)) << 2) + 2 * (c8 & 1);
 #pragma unroll
             for (int p = 0; p < 3; ++p) *reinterpret_cast<uint2*>(&sm.x[b][p * 128 * 16 + at]) = pc[p];
@@ -512,14 +534,14 @@ __global__ __launch_bounds__(kGemmThreads) void GemmPieces(const float* __restri
         dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
         if (h == 0) sm.d[b][row] = wt.keep ? HalfHw(wt.d & 0xFFFFu) : 0.0f;
     };
-    xt.Load(x, T, K, m0, s0 * kBK);
+    load_x(s0 * kBK);
     wt.Load(w, O, K, row_bytes, n0, s0 * kBK);
     store(0);
     __syncthreads();
     for (int64_t s = s0; s < s1; ++s) {
         const int buf = static_cast<int>((s - s0) & 1);
         const int64_t k_next = (s + 1 < s1 ? s + 1 : s) * kBK;
-        xt.Load(x, T, K, m0, k_next);
+        load_x(k_next);
         wt.Load(w, O, K, row_bytes, n0, k_next);
         __builtin_amdgcn_sched_barrier(0);
         bf16x8g b[4];
@@ -1272,6 +1294,31 @@ mlk_status LaunchSkinny(int wt, const float* x, const SkinnyArgs& a, int64_t T, 
     return CheckLaunch("GemmSkinny");
 }
 
+template <int NW>
+void LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
+                  const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
+                  int tiles_m, int tiles, int64_t per_split, float* partial) {
+    const dim3 block(64 * NW);
+    switch (wt) {
+        case MLK_Q8_0:
+            hipLaunchKernelGGL((GemmPieces<MLK_Q8_0, NW>), grid, block, 0, s, x, w, bias, y, T, K,
+                               O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        case MLK_Q4_0:
+            hipLaunchKernelGGL((GemmPieces<MLK_Q4_0, NW>), grid, block, 0, s, x, w, bias, y, T, K,
+                               O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        case kWPlanarQ8:
+            hipLaunchKernelGGL((GemmPieces<kWPlanarQ8, NW>), grid, block, 0, s, x, w, bias, y, T,
+                               K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+        default:
+            hipLaunchKernelGGL((GemmPieces<kWPlanarQ4, NW>), grid, block, 0, s, x, w, bias, y, T,
+                               K, O, row_bytes, tiles_m, tiles, per_split, partial);
+            break;
+    }
+}
+
 template <int BM>
 void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
                  const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
@@ -1279,27 +1326,19 @@ void LaunchTiles(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t
     // 128-row tiles of Q8_0 / Q4_0 on bf16 piece products; K % 256 == 0 keeps
     // each product's fp32 roundings (block sum, scale, K / 32 block adds)
     // under the K of the fp32 kernel's bound
-    if (BM == 128 && K % 256 == 0) {
-        switch (wt) {
-            case MLK_Q8_0:
-                hipLaunchKernelGGL((GemmPieces<MLK_Q8_0>), grid, dim3(kGemmThreads), 0, s, x, w,
-                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
-                return;
-            case MLK_Q4_0:
-                hipLaunchKernelGGL((GemmPieces<MLK_Q4_0>), grid, dim3(kGemmThreads), 0, s, x, w,
-                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
-                return;
-            case kWPlanarQ8:
-                hipLaunchKernelGGL((GemmPieces<kWPlanarQ8>), grid, dim3(kGemmThreads), 0, s, x, w,
-                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
-                return;
-            case kWPlanarQ4:
-                hipLaunchKernelGGL((GemmPieces<kWPlanarQ4>), grid, dim3(kGemmThreads), 0, s, x, w,
-                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split, partial);
-                return;
-            default:
-                break;
+    if (BM == 128 && K % 256 == 0 &&
+        (wt == MLK_Q8_0 || wt == MLK_Q4_0 || wt == kWPlanarQ8 || wt == kWPlanarQ4)) {
+        // 256-output tiles when they still fill two workgroups per CU and K
+        // is not split; else 128
+        const int64_t tiles8 = static_cast<int64_t>(tiles_m) * ((O + 255) / 256);
+        if (per_split >= (K + kBK - 1) / kBK && tiles8 >= 2 * static_cast<int64_t>(ComputeUnits())) {
+            LaunchPieces<8>(wt, dim3(static_cast<unsigned>(tiles8)), s, x, w, bias, y, T, K, O,
+                            row_bytes, tiles_m, static_cast<int>(tiles8), per_split, partial);
+        } else {
+            LaunchPieces<4>(wt, grid, s, x, w, bias, y, T, K, O, row_bytes, tiles_m, tiles,
+                            per_split, partial);
         }
+        return;
     }
     switch (wt) {
         case MLK_Q8_0:
