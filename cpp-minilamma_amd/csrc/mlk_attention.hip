@@ -611,17 +611,39 @@ __global__ __launch_bounds__(kAttnThreads) void AttnCombine(AttnParams p) {
         const int cc = c < nc ? c : nc - 1;
         pre[c] = acc[static_cast<int64_t>(cc) * p.hd + (d < p.hd ? d : 0)];
     }
+    // at most one chunk per thread (every context up to kAttnThreads chunks):
+    // its (m, l) stay in registers for the max, the sum and the weight, in
+    // place of two more dependent reads after each reduction
+    const bool one = nc <= kAttnThreads;
+    const int c1 = one && static_cast<int>(threadIdx.x) < nc ? static_cast<int>(threadIdx.x) : 0;
+    const float m1 = mlr[2 * c1], l1 = mlr[2 * c1 + 1];
     float mloc = -INFINITY;
-    for (int c = threadIdx.x; c < nc; c += kAttnThreads) mloc = fmaxf(mloc, mlr[2 * c]);
+    if (one) {
+        if (static_cast<int>(threadIdx.x) < nc) mloc = fmaxf(mloc, m1);
+    } else {
+        for (int c = threadIdx.x; c < nc; c += kAttnThreads) mloc = fmaxf(mloc, mlr[2 * c]);
+    }
     const float M = BlockMax<kAttnWaves>(mloc, redf);
     float lloc = 0.0f;
-    for (int c = threadIdx.x; c < nc; c += kAttnThreads) lloc += mlr[2 * c + 1] * expf(mlr[2 * c] - M);
+    float w1 = 0.0f;  // this thread's chunk weight exp(m - M) (one chunk per thread)
+    if (one) {
+        if (static_cast<int>(threadIdx.x) < nc) {
+            w1 = expf(m1 - M);
+            lloc += l1 * w1;
+        }
+    } else {
+        for (int c = threadIdx.x; c < nc; c += kAttnThreads) lloc += mlr[2 * c + 1] * expf(mlr[2 * c] - M);
+    }
     const float L = static_cast<float>(BlockSum<kAttnWaves>(static_cast<double>(lloc), red));
     float a = 0.0f;
     for (int c0 = 0; c0 < nc; c0 += kCombineTile) {
         const int n = min(kCombineTile, nc - c0);
         __syncthreads();
-        for (int c = threadIdx.x; c < n; c += kAttnThreads) wgt[c] = expf(mlr[2 * (c0 + c)] - M);
+        if (one) {
+            if (static_cast<int>(threadIdx.x) < n) wgt[threadIdx.x] = w1;
+        } else {
+            for (int c = threadIdx.x; c < n; c += kAttnThreads) wgt[c] = expf(mlr[2 * (c0 + c)] - M);
+        }
         __syncthreads();
         if (d < p.hd) {
             int c = 0;
