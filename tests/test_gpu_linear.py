@@ -157,6 +157,24 @@ def test_linear_gemm_shapes(mlk, orc, wt, shape):
         np.testing.assert_array_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("wt", ("q8_0", "q4_0"))
+def test_linear_gemm_wide_tiles(mlk, orc, wt):
+    """Q8_0 / Q4_0 tiles on bf16 piece products with 256 outputs per
+    workgroup: 4059 rows x 4300 outputs is 32 x 17 = 544 such tiles, at least
+    two per compute unit on the 256 of an MI355X, so the launch takes them
+    (no split of K = 256). The last row tile and the last output tile are
+    partial. Same bar as the other GEMM shapes, with a bias."""
+    O, K, T = 4300, 256, 4059
+    rng = np.random.default_rng(41)
+    w = normal(rng, (O, K), 0.02)
+    x = normal(rng, (T, K))
+    bias = normal(rng, (O,), 0.1)
+    blocks = orc.quantize(wt, w)
+    ex, s = dot_exact(x, orc.dequantize(wt, blocks, O, K), bias)
+    got = run_quant(mlk, wt, x, blocks, O, bias=bias)
+    assert_dot_close(got, ex, s, K + 1, f"{wt} wide tiles")
+
+
 SKINNY_SHAPES = [  # (out, in, rows): quantized weights with 8..32 rows, in a multiple of 256, take
     # the skinny kernel (F32 runs the tiled GEMM on the same shapes)
     (4096, 4096, 8), (1024, 4096, 9), (100, 256, 16), (4097, 512, 17), (64, 4096, 31),
