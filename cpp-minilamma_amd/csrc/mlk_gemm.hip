@@ -404,21 +404,24 @@ struct __align__(16) PiecesSmem {
 // The pieces of 4 floats, two per dword: o[0] high, o[1] middle, o[2] low.
 // Finite values: mask and subtract; a wave with any inf or NaN takes
 // SplitBf's form (the value whole in the high piece), so products with them
-// are what fp32 products would be.
+// are what fp32 products would be.  The low pieces of finite values are
+// finite and below 2^-14 of them, so their sum is NaN exactly when some
+// value is inf or NaN (inf - inf, NaN propagating): one test for four.
 __device__ inline void PiecesOf4(float4 v, uint2 (&o)[3]) {
     const float x[4] = {v.x, v.y, v.z, v.w};
     uint32_t h[4], m[4], l[4];
-    bool bad = false;
+    float lf[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t u = __float_as_uint(x[i]);
         const float r = x[i] - __uint_as_float(u & 0xFFFF0000u);
         h[i] = u;
         m[i] = __float_as_uint(r);
-        l[i] = __float_as_uint(r - __uint_as_float(m[i] & 0xFFFF0000u));
-        bad |= !__builtin_isfinite(x[i]);
+        lf[i] = r - __uint_as_float(m[i] & 0xFFFF0000u);
+        l[i] = __float_as_uint(lf[i]);
     }
-    if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+    const float chk = (lf[0] + lf[1]) + (lf[2] + lf[3]);
+    if (__builtin_amdgcn_ballot_w64(chk != chk) != 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float p[3];
@@ -492,19 +495,17 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
     const int64_t s0 = sp * per_split;
     const int64_t s1 = s0 + per_split < all_stages ? s0 + per_split : all_stages;
     // x: thread tid holds float4 tid + kThreads i of the [128][32] stage, 8
-    // per row (rows past T read row 0 and are zeroed at the split)
+    // per row.  Rows past T read row 0 and W rows past O their tile's row 0,
+    // unmasked: the outputs they meet are never stored (K is a multiple of
+    // 256, so no stage reads past K).
     float4 xv[kXN];
-    uint32_t xkeep = 0;
     auto load_x = [&](int64_t k0) {
-        xkeep = 0;
 #pragma unroll
         for (int i = 0; i < kXN; ++i) {
             const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
             const int64_t r = m0 + (idx >> 3);
             const int64_t c = k0 + 4 * (idx & 7);
-            const bool ok = r < T && c < K;
-            xkeep |= static_cast<uint32_t>(ok) << i;
-            xv[i] = *reinterpret_cast<const float4*>(x + (ok ? r * K + c : 0));
+            xv[i] = *reinterpret_cast<const float4*>(x + (r < T ? r * K + c : c));
         }
     };
     WTile<WT> wt;
@@ -515,7 +516,7 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
             const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
             const int r = idx >> 3, c8 = idx & 7;
             uint2 pc[3];
-            PiecesOf4(Mask4(xv[i], ((xkeep >> i) & 1u) ? ~0u : 0u), pc);
+            PiecesOf4(xv[i], pc);
             const int at = r * 16 + (((c8 >> 1) ^ ((r >> 1) & 3)) << 2) + 2 * (c8 & 1);
 #pragma unroll
             for (int p = 0; p < 3; ++p) *reinterpret_cast<uint2*>(&sm.x[b][p * 128 * 16 + at]) = pc[p];
@@ -524,15 +525,12 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
         TileCodes<WT>(wt, c);
         uint32_t pk[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            pk[i] = wt.keep ? PackBf(static_cast<float>(c[2 * i]), static_cast<float>(c[2 * i + 1]))
-                            : 0u;
-        }
+        for (int i = 0; i < 8; ++i) pk[i] = PackBf(static_cast<float>(c[2 * i]), static_cast<float>(c[2 * i + 1]));
         const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
         uint4* dst = reinterpret_cast<uint4*>(&sm.w[b][row * kPcWRow + 8 * h]);
         dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-        if (h == 0) sm.d[b][row] = wt.keep ? HalfHw(wt.d & 0xFFFFu) : 0.0f;
+        if (h == 0) sm.d[b][row] = HalfHw(wt.d & 0xFFFFu);
     };
     load_x(s0 * kBK);
     wt.Load(w, O, K, row_bytes, n0, s0 * kBK);
