@@ -440,17 +440,28 @@ __device__ inline void PiecesOf4(float4 v, uint2 (&o)[3]) {
 }
 
 // The 16 signed codes a weight tile thread holds (inputs 16h .. 16h + 15 of
-// its row's block), as the tiles' Store decodes them.
+// its row's block), as the tiles' Store decodes them; block-layout Q4_0
+// codes come as 16 x (nibble - 8) (CodeScale<WT>() undoes the 16 in the
+// scale, exactly): each dword's nibbles of half h, XOR 8, moved to the high
+// half of their bytes are those values as signed bytes, with no per-code
+// select on h.
+template <int WT>
+__device__ constexpr float CodeScale() { return WT == MLK_Q4_0 ? 0.0625f : 1.0f; }
+
 template <int WT>
 __device__ inline void TileCodes(const WTile<WT>& t, int32_t (&c)[16]) {
     const int h = threadIdx.x & 1;
+    uint32_t sb[4];
+    if constexpr (WT == MLK_Q4_0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sb[j] = (((t.q[j] >> (4 * h)) & 0x0F0F0F0Fu) ^ 0x08080808u) << 4;
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         if constexpr (WT == MLK_Q8_0 || WT == kWPlanarQ8) {
             c[i] = static_cast<int32_t>(t.q[i / 4] << (24 - 8 * (i % 4))) >> 24;
         } else if constexpr (WT == MLK_Q4_0) {
-            const uint32_t byte = (t.q[i / 4] >> (8 * (i % 4))) & 0xFFu;
-            c[i] = static_cast<int32_t>(h ? byte >> 4 : byte & 15u) - 8;
+            c[i] = static_cast<int32_t>(sb[i / 4] << (24 - 8 * (i % 4))) >> 24;
         } else {  // planar Q4_0: input 8g + e is nibble e (low half of byte e, then high)
             const int e8 = i % 8;
             const int sh = e8 < 4 ? 8 * e8 : 8 * (e8 - 4) + 4;
@@ -530,7 +541,7 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
         uint4* dst = reinterpret_cast<uint4*>(&sm.w[b][row * kPcWRow + 8 * h]);
         dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-        if (h == 0) sm.d[b][row] = HalfHw(wt.d & 0xFFFFu);
+        if (h == 0) sm.d[b][row] = HalfHw(wt.d & 0xFFFFu) * CodeScale<WT>();
     };
     load_x(s0 * kBK);
     wt.Load(w, O, K, row_bytes, n0, s0 * kBK);
