@@ -261,6 +261,57 @@ class _Oracle:
             return self.linear_f32(x, data, bias)
         return self.linear_quant(kind, x, data, out_features, bias)
 
+    def layer_token(self, c, lw, x, kc, vc, li, pos, mistake=None, keep=None):
+        """One layer of ForwardLayer (src/forward.cc:385-414) for one token
+        at `pos`: x [dim] in, the layer's output out; its K/V row is written
+        to slot (li, pos) of kc / vc [layers, max_seq, KV, hd] first, and
+        the token attends to slots 0..pos.  keep: a dict that receives the
+        intermediates (h, q, k, v after RoPE, a, r, h2, f)."""
+        D, H, KV, hd = c["dim"], c["n_heads"], c["n_kv_heads"], c["head_dim"]
+        F = c["hidden_dim"]
+        h = self.rmsnorm(x, lw["ffn_norm" if mistake == "swap_norms" else "attention_norm"],
+                         c["eps"])
+        q = self.linear(lw["wq"], h, H * hd, lw.get("bq"))
+        k = self.linear(lw["wk"], h, KV * hd, lw.get("bk"))
+        v = self.linear(lw["wv"], h, KV * hd, lw.get("bv"))
+        if mistake != "no_rope_on_k":
+            q, k = self.rope(q[None], k[None], H, KV, hd, positions=[pos],
+                             theta=c["theta"], rope_type=c["rope_type"])
+        else:
+            q, _ = self.rope(q[None], k[None], H, KV, hd, positions=[pos],
+                             theta=c["theta"], rope_type=c["rope_type"])
+            k = k[None]
+        self.kv_write(kc, vc, li, [pos], k.reshape(1, KV, hd), v.reshape(1, KV, hd))
+        a = self.attention(q.reshape(1, H, hd), kc, vc, li,
+                           [pos - 1 if mistake == "exclusive_attention" and pos > 0 else pos])
+        o = self.linear(lw["wo"], a.reshape(-1), D)
+        r = x if mistake == "no_attention_residual" else self.add(x, o)
+        if mistake == "no_attention_residual":
+            r = o
+        h2 = self.rmsnorm(r, lw["ffn_norm"], c["eps"])
+        g = self.linear(lw["w_gate"], h2, F)
+        u = self.linear(lw["w_up"], h2, F)
+        f = self.swiglu(u, g) if mistake == "swap_gate_up" else self.swiglu(g, u)
+        if keep is not None:
+            keep.update(h=h, q=np.ravel(q), k=np.ravel(k), v=np.ravel(v), a=np.ravel(a), r=r,
+                        h2=h2, f=f)
+        return self.add(r, self.linear(lw["w_down"], f, D))
+
+    def layer_tokens(self, c, lw, x, kc, vc, li, positions, keep=None):
+        """ForwardBatch's token loop (src/forward.cc:482-486) restricted to
+        one layer: rows t of x [T, dim] in order, token t at positions[t]
+        over the caches as they stand (already-filled slots included);
+        returns the layer's outputs [T, dim] and updates the caches.  keep:
+        a list that receives each token's intermediates (layer_token)."""
+        x = np.asarray(x, np.float32)
+        out = []
+        for t in range(x.shape[0]):
+            d = {} if keep is not None else None
+            out.append(self.layer_token(c, lw, x[t], kc, vc, li, int(positions[t]), keep=d))
+            if keep is not None:
+                keep.append(d)
+        return np.stack(out)
+
     def forward_tokens(self, model, tokens, positions, mistake=None):
         """The reference's CPU forward pass restated over the ops above:
         ForwardBatch's loop (src/forward.cc:473-488) of ForwardToken
@@ -297,31 +348,7 @@ class _Oracle:
                 x = self.gather_quant(qt, blocks, V, D, np.array([tokens[t]], np.int32))[0]
             for li, lw in enumerate(model["layers"]):
                 hidden[t, li] = x
-                h = self.rmsnorm(x, lw["ffn_norm" if mistake == "swap_norms" else "attention_norm"],
-                                 c["eps"])
-                q = self.linear(lw["wq"], h, H * hd, lw.get("bq"))
-                k = self.linear(lw["wk"], h, KV * hd, lw.get("bk"))
-                v = self.linear(lw["wv"], h, KV * hd, lw.get("bv"))
-                if mistake != "no_rope_on_k":
-                    q, k = self.rope(q[None], k[None], H, KV, hd, positions=[pos],
-                                     theta=c["theta"], rope_type=c["rope_type"])
-                else:
-                    q, _ = self.rope(q[None], k[None], H, KV, hd, positions=[pos],
-                                     theta=c["theta"], rope_type=c["rope_type"])
-                    k = k[None]
-                self.kv_write(kc, vc, li, [pos], k.reshape(1, KV, hd), v.reshape(1, KV, hd))
-                a = self.attention(q.reshape(1, H, hd), kc, vc, li,
-                                   [pos - 1 if mistake == "exclusive_attention" and pos > 0
-                                    else pos])
-                o = self.linear(lw["wo"], a.reshape(-1), D)
-                r = x if mistake == "no_attention_residual" else self.add(x, o)
-                if mistake == "no_attention_residual":
-                    r = o
-                h2 = self.rmsnorm(r, lw["ffn_norm"], c["eps"])
-                g = self.linear(lw["w_gate"], h2, F)
-                u = self.linear(lw["w_up"], h2, F)
-                f = self.swiglu(u, g) if mistake == "swap_gate_up" else self.swiglu(g, u)
-                x = self.add(r, self.linear(lw["w_down"], f, D))
+                x = self.layer_token(c, lw, x, kc, vc, li, pos, mistake)
             hidden[t, L] = x
             logits[t] = self.linear(model["lm_head"], self.rmsnorm(x, model["final_norm"],
                                                                    c["eps"]), V)

@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from conftest import assert_bits_equal, tiny_model
+from conftest import U32, assert_bits_equal, tiny_model
 
 pytestmark = pytest.mark.gpu
 
@@ -443,3 +443,135 @@ def test_forward_planar_matches_oracle(orc, fwd, wt):
         got = dm.forward(tokens[at:at + T], pos0=at, all_logits=True)
         assert_forward_close(got, want[at:at + T], f"{wt} batch of {T} at {at}")
         at += T
+
+
+LAYER_8B = dict(dim=4096, hidden_dim=14336, n_heads=32, n_kv_heads=8, head_dim=128, layers=1,
+                rope_type=0, theta=500000.0, eps=1e-5)
+S_8B = 8192
+
+
+def host_layer_8b(orc, qt, seed):
+    """One Llama-3-8B-shaped layer on the host: norm weights N(1, 0.1),
+    projections N(0, 0.02) quantized by the oracle (the reference's
+    quantizer, bit for bit)."""
+    c = LAYER_8B
+    D, F = c["dim"], c["hidden_dim"]
+    QD, KD = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    rng = np.random.default_rng(seed)
+    lw = {"attention_norm": (1 + 0.1 * rng.standard_normal(D)).astype(np.float32),
+          "ffn_norm": (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)}
+    for name, (o, i) in {"wq": (QD, D), "wk": (KD, D), "wv": (KD, D), "wo": (D, QD),
+                         "w_gate": (F, D), "w_up": (F, D), "w_down": (D, F)}.items():
+        w = (0.02 * rng.standard_normal((o, i), dtype=np.float32))
+        lw[name] = (qt, orc.quantize(qt, w))
+        lw[name + "_shape"] = (o, i)
+    return lw
+
+
+def gamma(n):
+    return n * U32 / (1 - n * U32)
+
+
+@pytest.mark.parametrize("qt", ["q8_0", "q4_0"])
+def test_layer_8b_decode_planar_matches_oracle(mlk, orc, fwd, qt):
+    """The decode steps the bench times, at the Llama-3-8B layer shape on
+    planar Q8_0 / Q4_0 weights (the path of 1..32 tokens) over a cache
+    pre-filled at every position 0..8191: one token at position 8191
+    (streaming GEMVs, attention over 8192 rows), and 16 tokens at distinct
+    positions uniform in 0..8191 (planar matrix-core linears, shared-tile
+    attention).  Against the oracle's op-by-op composition of the same step
+    (ForwardBatch's token loop over one layer, src/forward.cc:482-486 and
+    ForwardLayer :385-414) with the same weights and cache.
+
+    The bars.  The reference's forward bar 1e-5 + 1e-4|x| was set on its
+    tiny model (dim 32); at this shape the last op sums 14336 fp32 terms of
+    size ~1e-2, and an fp32 sum in any order is only within
+    gamma_K * sum|terms| of the exact one: measured here, both the oracle's
+    serial sum and the device's split sums land up to ~2-3e-5 from the exact
+    value near x = 0, beyond 1e-5.  So the forward bar gets the summation
+    bound of the down projection added (f = the oracle's SwiGLU output,
+    S_j = sum_k |f_k w_jk|):
+      - the layer output against the oracle's own fp32 result: the forward
+        bar + 2 gamma_F S (both sums);
+      - the layer output against r + f W_down^T evaluated in float64 over
+        the oracle's own residual r and f: the forward bar + gamma_F S (the
+        device's sum alone);
+      - the K / V rows each token wrote against the oracle's: 1e-5 + 1e-4|k|
+        plus 2 gamma_D sum_i |h_i w_ji| (over both rows of a rotated pair
+        for K).
+    Each case prints its largest error as a multiple of the plain forward
+    bar."""
+    c = LAYER_8B
+    D, F, KV, hd = c["dim"], c["hidden_dim"], c["n_kv_heads"], c["head_dim"]
+    lw = host_layer_8b(orc, qt, seed=17 if qt == "q8_0" else 18)
+    keep = []
+
+    def up(a):
+        buf = mlk.DeviceBuffer.from_array(np.ascontiguousarray(a))
+        keep.append(buf)
+        return buf
+
+    w = fwd.LayerWeights()
+    w.attention_norm = up(lw["attention_norm"]).ptr
+    w.ffn_norm = up(lw["ffn_norm"]).ptr
+    for name in fwd.LINEAR_NAMES:
+        o, i = lw[name + "_shape"]
+        blocks = up(lw[name][1])
+        pl = mlk.DeviceBuffer(mlk.quant_planar_bytes(qt, o, i), np.uint8)
+        mlk.quant_to_planar(qt, blocks, o, i, pl)
+        keep.append(pl)
+        lin = fwd.LinearWeight()
+        lin.type, lin.data, lin.bias, lin.planar = mlk.QUANT[qt], blocks.ptr, None, pl.ptr
+        setattr(w, name, lin)
+    wd = orc.dequantize(qt, lw["w_down"][1], D, F).astype(np.float64)
+    wk = np.abs(orc.dequantize(qt, lw["wk"][1], KV * hd, D).astype(np.float64))
+    wv = np.abs(orc.dequantize(qt, lw["wv"][1], KV * hd, D).astype(np.float64))
+    rng = np.random.default_rng(5)
+    kc0 = rng.standard_normal((1, S_8B, KV, hd), dtype=np.float32)
+    vc0 = rng.standard_normal((1, S_8B, KV, hd), dtype=np.float32)
+    spos = np.sort(rng.choice(S_8B, 16, replace=False)).astype(np.int32)
+    for T, positions in ((1, np.array([S_8B - 1], np.int32)), (16, spos)):
+        print(f"8B layer {qt}: T={T} positions {positions[:4]}...{positions[-1]}", flush=True)
+        x = rng.standard_normal((T, D), dtype=np.float32)
+        kc, vc = kc0.copy(), vc0.copy()
+        inter = []
+        want = orc.layer_tokens(c, lw, x, kc, vc, 0, positions, keep=inter).astype(np.float64)
+        f = np.stack([d["f"] for d in inter]).astype(np.float64)
+        r = np.stack([d["r"] for d in inter]).astype(np.float64)
+        h = np.abs(np.stack([d["h"] for d in inter]).astype(np.float64))
+        d_x, d_k, d_v = up(x), up(kc0), up(vc0)
+        consecutive = T == 1
+        max_ctx = int(positions.max()) + 1
+        ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(c, T, max_ctx, consecutive), np.uint8)
+        d_pos = None if consecutive else up(positions)
+        fwd.forward_layer_batch(c, w, d_x, T, d_k, d_v, 1, S_8B, 0, max_ctx, ws,
+                                positions=d_pos, pos0=int(positions[0]))
+        mlk.synchronize()
+        got = d_x.download().astype(np.float64)
+        assert np.isfinite(got).all()
+        err = np.abs(got - want)
+        bar = 1e-5 + 1e-4 * np.abs(want)
+        sum_bound = gamma(F) * (np.abs(f) @ np.abs(wd).T)
+        assert (err <= bar + 2 * sum_bound).all(), (
+            f"{qt} T={T}: {int((err > bar + 2 * sum_bound).sum())} outputs beyond the forward "
+            "bar + both sums' bound")
+        exact = r + f @ wd.T
+        err64 = np.abs(got - exact)
+        bar64 = 1e-5 + 1e-4 * np.abs(exact)
+        assert (err64 <= bar64 + sum_bound).all(), (
+            f"{qt} T={T}: {int((err64 > bar64 + sum_bound).sum())} outputs beyond the forward "
+            "bar + the device sum's bound, against float64")
+        print(f"8B layer {qt} T={T}: vs the oracle max |err| {float(err.max()):.2e} "
+              f"({float((err / bar).max()):.2f} x the plain forward bar, "
+              f"{int((err > bar).sum())} beyond it); vs the float64 down projection "
+              f"{float(err64.max()):.2e} ({float((err64 / bar64).max()):.2f} x, "
+              f"{int((err64 > bar64).sum())} beyond it); of {err.size}")
+        s_k = h @ wk.T  # [T, KV*hd]
+        s_k = s_k + s_k.reshape(T, -1, 2)[:, :, ::-1].reshape(T, -1)  # both rows of a pair
+        s_v = h @ wv.T
+        for cache_d, cache_h, s, what in ((d_k, kc, s_k, "K"), (d_v, vc, s_v, "V")):
+            g_rows = cache_d.download()[0, positions].reshape(T, -1).astype(np.float64)
+            w_rows = cache_h[0, positions].reshape(T, -1).astype(np.float64)
+            e = np.abs(g_rows - w_rows)
+            lim = 1e-5 + 1e-4 * np.abs(w_rows) + 2 * gamma(D) * s
+            assert (e <= lim).all(), f"{qt} T={T} {what} rows: {int((e > lim).sum())} beyond"

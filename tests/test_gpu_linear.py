@@ -175,6 +175,77 @@ def test_linear_gemm_wide_tiles(mlk, orc, wt):
     assert_dot_close(got, ex, s, K + 1, f"{wt} wide tiles")
 
 
+BENCH_GEMM_SHAPES = [(4096, 14336, 4096), (14336, 4096, 4096)]  # (out, in, rows)
+
+
+def sample_rows(T, tile=128):
+    """Rows spread over every 128-row tile: its first, a middle and its last
+    row (the last tile's rows may be fewer)."""
+    rows = set()
+    for r0 in range(0, T, tile):
+        r1 = min(T, r0 + tile) - 1
+        rows.update((r0, (r0 + r1) // 2 + 1 if r1 > r0 else r0, r1))
+    return np.array(sorted(rows))
+
+
+@pytest.mark.parametrize("wt", ("q8_0", "q4_0"))
+@pytest.mark.parametrize("shape", BENCH_GEMM_SHAPES, ids=["down_4096x14336", "gate_14336x4096"])
+def test_linear_gemm_bench_shapes(mlk, orc, wt, shape):
+    """The prefill layer's GEMM at the shapes the bench times (T = 4096
+    tokens; w_down: 4096 outputs over 14336 inputs, w_gate / w_up: 14336
+    outputs over 4096): 32 row tiles x 16 or 56 output tiles of 256 is at
+    least two workgroups per compute unit, so these take the 8-wave
+    piece-product tiles.  Every output of 96 rows (first, middle and last of
+    each of the 32 row tiles) against the gamma_K bound of the float64
+    products with the dequantized weights."""
+    O, K, T = shape
+    rng = np.random.default_rng(O + 2 * K)
+    w = normal(rng, (O, K), 0.02)
+    blocks = orc.quantize(wt, w)
+    del w
+    x = normal(rng, (T, K))
+    got = run_quant(mlk, wt, x, blocks, O)
+    rows = sample_rows(T)
+    assert rows.size >= 64
+    ex, s = dot_exact(x[rows], orc.dequantize(wt, blocks, O, K))
+    assert_dot_close(got[rows], ex, s, K, f"{wt} {shape} sampled rows")
+    assert np.isfinite(got).all()
+    print(f"gemm {wt} {shape}: {rows.size} rows x {O} outputs checked; "
+          f"max |err| / sum|terms| = {float((np.abs(got[rows] - ex) / s).max()):.2e}")
+
+
+@pytest.mark.parametrize("wt", ("q8_0", "q4_0"))
+@pytest.mark.parametrize("shape", [(300, 512, 130), (4300, 256, 4059)],
+                         ids=["128_output_tiles", "256_output_tiles"])
+def test_linear_gemm_non_finite_inputs(mlk, orc, wt, shape):
+    """The piece-product GEMM (Q8_0 / Q4_0, more than 64 rows, in a multiple
+    of 256) with inf and NaN in x: row 0, a middle row and a row of the
+    partial last row tile.  Every output those rows reach is what the
+    products give (the same NaN pattern, infinities of the same sign); every
+    other row stays finite and within the bound.  Both tile widths: 300
+    outputs over 130 rows (128-output tiles), and 4300 outputs over 4059
+    rows (enough tiles for the 256-output ones)."""
+    O, K, T = shape
+    rng = np.random.default_rng(O + K + T)
+    blocks = orc.quantize(wt, normal(rng, (O, K), 0.02))
+    wd = orc.dequantize(wt, blocks, O, K)
+    x = normal(rng, (T, K))
+    bad_rows = [0, T // 2, T - 1]
+    x[0, 7] = np.nan
+    x[T // 2, 3] = -np.inf
+    x[T - 1, K - 1] = np.inf
+    got = run_quant(mlk, wt, x, blocks, O)
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = x[bad_rows].astype(np.float64) @ wd.astype(np.float64).T
+    for i, t in enumerate(bad_rows):
+        np.testing.assert_array_equal(np.isnan(got[t]), np.isnan(want[i]), err_msg=f"row {t}")
+        inf = np.isinf(want[i])
+        np.testing.assert_array_equal(got[t][inf], want[i][inf], err_msg=f"row {t}")
+    ok = np.setdiff1d(sample_rows(T), bad_rows)
+    ex, s = dot_exact(x[ok], wd)
+    assert_dot_close(got[ok], ex, s, K, f"{wt} {shape} finite rows")
+
+
 SKINNY_SHAPES = [  # (out, in, rows): quantized weights with 8..32 rows, in a multiple of 256, take
     # the skinny kernel (F32 runs the tiled GEMM on the same shapes)
     (4096, 4096, 8), (1024, 4096, 9), (100, 256, 16), (4097, 512, 17), (64, 4096, 31),
