@@ -413,12 +413,14 @@ CudaTensor CudaEmbeddingBatchDevice(const void* embedding_data, const std::vecto
     RequireTable(embedding_data, shape, caller);
     RequireIds(token_ids, shape[0], caller);
     SetCudaService(device_id);
-    CudaDeviceBuffer ids = UploadInts(token_ids, device_id);
+    // one id travels as a kernel argument (no copy, as CudaEmbeddingDevice);
+    // more are copied to the device once
     const int n = static_cast<int>(token_ids.size());
+    CudaDeviceBuffer ids = n > 1 ? UploadInts(token_ids, device_id) : CudaDeviceBuffer();
     CudaTensor y({n, shape[1]}, device_id);
     Launched(mlk_gather_f32(static_cast<const float*>(embedding_data), shape[0], shape[1],
-                            static_cast<const int32_t*>(ids.GetData()), 0, n, F(y), nullptr,
-                            nullptr),
+                            static_cast<const int32_t*>(ids.GetData()), token_ids[0], n, F(y),
+                            nullptr, nullptr),
              caller);
     return y;
 }
@@ -431,12 +433,12 @@ CudaTensor CudaEmbeddingQuantDevice(const void* blocks, QuantType type,
     RequireTable(blocks, shape, caller);
     RequireIds(token_ids, shape[0], caller);
     SetCudaService(device_id);
-    CudaDeviceBuffer ids = UploadInts(token_ids, device_id);
     const int n = static_cast<int>(token_ids.size());
+    CudaDeviceBuffer ids = n > 1 ? UploadInts(token_ids, device_id) : CudaDeviceBuffer();
     CudaTensor y({n, shape[1]}, device_id);
     Launched(mlk_gather_quant(code, blocks, shape[0], shape[1],
-                              static_cast<const int32_t*>(ids.GetData()), 0, n, F(y), nullptr,
-                              nullptr),
+                              static_cast<const int32_t*>(ids.GetData()), token_ids[0], n, F(y),
+                              nullptr, nullptr),
              caller);
     return y;
 }

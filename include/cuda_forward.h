@@ -19,7 +19,8 @@ namespace yan_lamma {
 // A device linear weight [out, in]: fp32 (kF32) or packed Q8_0 / Q4_0 /
 // Q4_1 blocks, borrowed; bias [out] (device) or null; planar: null, or the
 // same Q8_0 / Q4_0 weight in the planar layout (mlk_quant_to_planar), which
-// calls of 2..32 tokens then use.
+// calls of 1..32 tokens then use (one token: the planar streaming GEMV;
+// 2..32: the planar matrix-core kernel).
 struct CudaLinearWeight {
     QuantType type = QuantType::kF32;
     const void* data = nullptr;
@@ -55,5 +56,16 @@ struct CudaLayerConfig {
 void CudaForwardLayerBatchDevice(const CudaLayerConfig& config, const CudaLayerWeights& weights,
                                  CudaTensor& x, CudaCache& cache, int layer, int pos0,
                                  int device_id = 0);
+
+// The same for tokens at positions[t] (the reference's Batch::poss,
+// include/batch.h:5-8), positions.size() == T, strictly increasing and in
+// [0, max_seq_len): all K/V rows are written before any token attends,
+// which equals the reference's token loop only when each token's
+// predecessors sit at lower positions.  Consecutive positions run as the
+// pos0 overload (nothing copied); otherwise the positions are copied to the
+// device once per call (one counted host-to-device copy of 4 T bytes).
+void CudaForwardLayerBatchDevice(const CudaLayerConfig& config, const CudaLayerWeights& weights,
+                                 CudaTensor& x, CudaCache& cache, int layer,
+                                 const std::vector<int>& positions, int device_id = 0);
 
 }  // namespace yan_lamma

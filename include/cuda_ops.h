@@ -79,6 +79,8 @@ void CudaRopeRangeDevice(CudaTensor& q, CudaTensor& k, int pos0, int n_heads, in
                          int head_dim, float theta, RopeType rope_type = RopeType::kNormal,
                          int device_id = 0);
 // Embedding rows of token_ids from an F32 table [vocab, dim] -> [T, dim].
+// One id is passed to the kernel as an argument; more are copied to the
+// device (one counted host-to-device copy of 4 T bytes).  Likewise below.
 CudaTensor CudaEmbeddingBatchDevice(const void* embedding_data, const std::vector<int>& shape,
                                     const std::vector<int>& token_ids, int device_id = 0);
 // Embedding rows of token_ids from a block-quantized table (type kQ80, kQ40

@@ -192,6 +192,24 @@ void GpuEmbedding() {
                            expected.data.data()) == ORC_OK,
             "oracle gather");
     RequireTensor(rows.Download(), expected, "batched embedding", 0.0);
+    // one id goes to the kernel as an argument: no host-to-device copy; more
+    // ids take one copy of 4 T bytes
+    for (const std::vector<int>& few : {std::vector<int>{130}, std::vector<int>{5, 9}}) {
+        CudaTransferStats stats;
+        CudaTensor got;
+        {
+            CudaStatsScope scope(&stats);
+            got = CudaEmbeddingBatchDevice(d.GetData(), table.shape, few);
+        }
+        const bool one = few.size() == 1;
+        Require(stats.host_to_device_copies == (one ? 0u : 1u) &&
+                    stats.host_to_device_bytes == (one ? 0u : 4 * few.size()),
+                "batched embedding host-to-device copies");
+        Tensor want({static_cast<int>(few.size()), 64});
+        Require(orc_gather_f32(table.data.data(), 131, 64, few.data(), few.size(),
+                               want.data.data()) == ORC_OK, "oracle gather");
+        RequireTensor(got.Download(), want, "batched embedding of few ids", 0.0);
+    }
 }
 
 // test/cuda_ops_test.cc:105-126.
@@ -373,6 +391,16 @@ void GpuQuantized() {
                                      ids.size(), expected.data.data()) == ORC_OK,
                     "oracle quant gather");
             RequireTensor(rows.Download(), expected, "quantized gather", 0.0);
+            CudaTransferStats stats;
+            CudaTensor one;
+            {
+                CudaStatsScope scope(&stats);
+                one = CudaEmbeddingQuantDevice(blocks.GetData(), t, shape, {shape[0] - 1});
+            }
+            Require(stats.host_to_device_copies == 0, "one id: no host-to-device copy");
+            Tensor last({1, shape[1]});
+            std::copy_n(expected.data.begin() + shape[1], shape[1], last.data.begin());
+            RequireTensor(one.Download(), last, "quantized gather of one id", 0.0);
         }
     }
 }

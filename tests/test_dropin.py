@@ -73,9 +73,13 @@ def test_layouts_agree_with_the_reference_headers(built):
 
 def test_reference_test_programs_reach_this_library(built):
     # without a GPU the programs get as far as this library's device count:
-    # CudaRuntimeBuilt() is true and DeviceCount() reports no device
-    for part in ("runtime", "ops", "forward"):
-        proc = subprocess.run([os.path.join(built, "bin", f"test_cuda_{part}")],
+    # CudaRuntimeBuilt() is true and DeviceCount() reports no device.
+    # test_forward_batch is the reference-side binding of the batched layer
+    # (tests/dropin/forward_batch_device.cc) with its test, built against the
+    # reference's headers and linked with its library
+    for prog in ("test_cuda_runtime", "test_cuda_ops", "test_cuda_forward",
+                 "test_forward_batch"):
+        proc = subprocess.run([os.path.join(built, "bin", prog)],
                               capture_output=True, text=True, timeout=60, cwd=built)
         if proc.returncode == 0:  # a machine with a GPU: the program passed
             assert "PASS" in proc.stdout

@@ -46,6 +46,16 @@ CASES = [
     ("strict-bench-counters", "test_bench_counters", None),
 ]
 
+# The reference-side binding of the batched layer and of the device token
+# table (tests/dropin/forward_batch_device.cc), held to the reference's
+# device-forward bar against its CPU ForwardBatch with the transfer counters
+# (tests/dropin/test_forward_batch.cc): linears F32 / Q8_0 / Q4_0 with the F32
+# table, the token table as Q8_0 / Q4_0 / Q4_1 blocks, the token-loop
+# fallback for positions that do not increase, and the rejected calls.
+BINDING_MODES = ["f32", "q8_0", "q4_0", "table_q8_0", "table_q4_0", "table_q4_1", "fallback",
+                 "rejects"]
+CASES += [(f"forward_batch_device_{m}", "test_forward_batch", m) for m in BINDING_MODES]
+
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,program,mode", CASES, ids=[c[0] for c in CASES])
