@@ -108,13 +108,14 @@ class ChainSet:
         shapes = {"x": (T, D), "delta": (T, D), "y": (T, D), "q": (T, H * hd),
                   "k": (T, KV * hd), "gate": (T, F), "up": (T, F), "out": (T, F)}
         filled = {"x": 0, "delta": 1, "q": 2, "k": 3, "gate": 4, "up": 5}
+        std = cfg.get("act_std", 0.02)  # activations: N(0, 1) for configs[0], else N(0, 0.02)
         self.nbytes = 0
         for name in fields or shapes:
             buf = mlk.DeviceBuffer.empty(shapes[name])
             setattr(self, name, buf)
             self.nbytes += buf.nbytes
             if name in filled and (fields is not None or fill_x or name != "x"):
-                mlk.fill_normal(buf, buf.nbytes // 4, 0.0, 0.02, seed + filled[name])
+                mlk.fill_normal(buf, buf.nbytes // 4, 0.0, std, seed + filled[name])
 
 
 class Chain:
@@ -311,9 +312,10 @@ def _cpu_model():
     return "unknown"
 
 
-def chain_host_bufs(chain, cfg, rows):
+def chain_host_bufs(chain, cfg, rows, table_host=None):
     """Host copies of the first `rows` token rows of a chain's set 0 (the
-    CPU baseline's inputs) and its output arrays."""
+    CPU baseline's inputs) and its output arrays; table_host: a host copy of
+    the chain's token table already downloaded (else it is downloaded)."""
     D, H, KV, hd, F = cfg["dim"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"], cfg["ffn"]
     s = chain.sets[0]
     pos = (chain.positions_host[:rows] if chain.positions_host is not None
@@ -326,7 +328,7 @@ def chain_host_bufs(chain, cfg, rows):
                 theta=cfg["theta"], gate=s.gate.download((rows, F)), up=s.up.download((rows, F)),
                 ffn_out=np.empty((rows, F), np.float32), ffn_dim=F)
     if chain.table is not None:
-        bufs["table"] = chain.table.download()
+        bufs["table"] = table_host if table_host is not None else chain.table.download()
         bufs["ids"] = np.ascontiguousarray(chain.ids_host[:rows], np.int32)
     else:
         bufs["x_in"] = s.x.download((rows, D))
@@ -411,7 +413,7 @@ def gather_fractions(entry):
 
 PHASE_BASE = 100
 PHASES = ("c3_chain", "c3_ops", "c2_decode", "c1_tiny", "c4_gather", "c5_chain", "c5_ops",
-          "c2_decode_graph", "c1_tiny_graph")
+          "c2_decode_graph", "c1_tiny_graph", "decode_layer_8b")
 
 
 class Marks:
@@ -469,12 +471,44 @@ def c1_tiny(mlk, steps, warmup, marks):
     return out
 
 
-def c2_decode(mlk, steps, warmup, marks, table):
+C2_CPU_TOKENS = {1: 200, 64: 20}  # decode sizes timed on the CPU: calls per median
+
+
+def cpu_decode_baseline(impl, kind, build, bufs, rows, reps):
+    """The configs[1] chain on the CPU for one decode step of `rows` tokens,
+    one token at a time as ForwardBatch runs it (src/forward.cc:482-486):
+    µs per step, spread over tokens with the reference's ParallelFor and on
+    one thread; bufs["model"] holds the reference's token table."""
+    threads = _cpu_threads()
+
+    def run(n_threads):
+        rc = impl.chain(bufs, rows, n_threads)
+        if rc != 0:
+            raise RuntimeError(f"CPU baseline failed (status {rc})")
+
+    t_mt = _median_s(lambda: run(threads), reps)
+    t_st = _median_s(lambda: run(1), reps)
+    return {"value": round(t_mt * 1e6, 2), "unit": "us per chain", "cores": threads,
+            "kind": kind,
+            "sample": f"the whole configs[1] chain at T={rows} (gather, add+RMSNorm, RoPE at "
+                      f"the step's positions, SwiGLU; Llama-3-8B shapes); {build}, ParallelFor "
+                      f"over tokens; median of {reps} calls after 1 warmup, each call's Python "
+                      "overhead (a few us) included",
+            "single_thread_value": round(t_st * 1e6, 2), **_host_facts()}
+
+
+def c2_decode(mlk, steps, warmup, marks, table, table_host=None):
     """the 8B chain as a decode step at T = 1..64 tokens at
     positions uniform in [0, 8191]: latency-bound, µs per chain, eager
-    launches and one HIP graph replay per step."""
+    launches and one HIP graph replay per step; with table_host (a host copy
+    of `table`), the reference's CPU chain at T = 1 and T = 64 beside it."""
     c2 = workloads.CONFIGS["c2_decode_8b"]
     out = {}
+    impl = model = None
+    if table_host is not None:
+        impl, kind, build = _cpu_impl()
+        if kind == "reference":
+            model = impl.embedding_model(table_host)
     for t in c2["tokens"]:
         pos = workloads.decode_positions(t, c2["max_pos"], c2["seed"])
         dch = Chain(mlk, c2, t, seed=c2["seed"], n_sets=2, positions=pos, table=table)
@@ -486,7 +520,15 @@ def c2_decode(mlk, steps, warmup, marks, table):
         out[str(t)] = {"us_per_chain_eager": round(eager * 1e3, 2),
                        "us_per_chain_graph": round(graph * 1e3, 2),
                        "chain_bytes": workloads.bytes_chain(c2, t)}
+        if impl is not None and t in C2_CPU_TOKENS:
+            bufs = chain_host_bufs(dch, c2, t, table_host)
+            if model is not None:
+                bufs["model"] = model
+            out[str(t)]["cpu_baseline"] = cpu_decode_baseline(impl, kind, build, bufs, t,
+                                                              C2_CPU_TOKENS[t])
         del dch
+    if model is not None:
+        impl.free_model(model)
     return out
 
 
@@ -653,10 +695,36 @@ class LinearLayers:
             self.mlk.linear_quant(self.qtype, x, w, y, T, k, o, stream=stream)
 
 
+def _graph_ms(mlk, st, launches, n):
+    """ms per item of `launches(i)` for i < n, issued as one captured HIP
+    graph and timed over one replay between two events on `st` (after one
+    untimed replay): the host dispatches one graph instead of n ctypes calls
+    and their HIP launches, so the time is the kernels' and the gaps the GPU
+    leaves between graph nodes."""
+    with mlk.Graph.capture(st) as graph:
+        for i in range(n):
+            launches(i)
+    try:
+        graph.launch()
+        st.synchronize()
+        e0, e1 = mlk.Event(), mlk.Event()
+        e0.record(st)
+        graph.launch()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / n
+    finally:
+        graph.close()
+
+
 def linear_bench(mlk, steps, peak, path):
-    """Per-projection launch time (each launched `steps` times back to back
-    over the rotating weight copies, between two events on its stream) and
-    the time of one whole layer's seven projections."""
+    """Per-projection launch time and the time of one whole layer's seven
+    projections.  Each projection's `steps` calls (over its rotating weight
+    copies) are captured into one HIP graph and timed over a replay, so the
+    figure is the kernels' time on the GPU, not Python's dispatch of the
+    calls (a planar call of 2..32 rows is three kernels: x split, the
+    matrix-core GEMV and the split-K sum).  Workspaces are sized by one eager
+    call of each shape before its capture."""
     cfg = workloads.CONFIGS["c2_decode_8b"]
     big = max(max(k, o) for _, k, o in workloads.layer_linears(cfg))
     T_max = max(LINEAR_TOKENS)
@@ -666,6 +734,8 @@ def linear_bench(mlk, steps, peak, path):
     st = mlk.Stream()
     out = {"workload": "Llama-3-8B layer projections (configs[1] shapes), weights N(0,0.02) "
                        "quantized on the device; x N(0,1)",
+           "timing": f"each projection's {steps} calls captured into one HIP graph over the "
+                     "rotating weight copies, one replay timed between two events",
            "peak_GBps": peak}
     for qt in LINEAR_DECODE_TYPES:
         layers = LinearLayers(mlk, cfg, qt, seed=300)
@@ -673,34 +743,27 @@ def linear_bench(mlk, steps, peak, path):
         for T in LINEAR_TOKENS:
             per = {}
             for name, k, o in layers.shapes:
-                for i in range(3):
+                for i in range(3):  # eager: sizes the auto workspace before the capture
                     layers.launch(i, name, k, o, x, y, T, st)
                 st.synchronize()
-                e0, e1 = mlk.Event(), mlk.Event()
-                e0.record(st)
-                for i in range(3, 3 + steps):  # copies not touched by the warmup
-                    layers.launch(i, name, k, o, x, y, T, st)
-                e1.record(st)
-                e1.synchronize()
-                ms = e0.elapsed_ms(e1) / steps
+                ms = _graph_ms(mlk, st, lambda i: layers.launch(3 + i, name, k, o, x, y, T, st),
+                               steps)
                 nb = workloads.bytes_linear(base_type(qt), T, k, o)
                 gbs = nb / (ms * 1e-3) / 1e9
                 per[name] = {"in": k, "out": o, "us": round(ms * 1e3, 2), "bytes": nb,
                              "GBps": round(gbs, 1), "frac_of_peak": round(gbs / peak, 4)}
-            e0, e1 = mlk.Event(), mlk.Event()
-            e0.record(st)
-            for i in range(3 + steps, 3 + 2 * steps):
+
+            def layer_call(i):
                 for name, k, o in layers.shapes:
-                    layers.launch(i, name, k, o, x, y, T, st)
-            e1.record(st)
-            e1.synchronize()
-            ms = e0.elapsed_ms(e1) / steps
+                    layers.launch(3 + steps + i, name, k, o, x, y, T, st)
+            ms = _graph_ms(mlk, st, layer_call, steps)
             nb = sum(workloads.bytes_linear(base_type(qt), T, k, o) for _, k, o in layers.shapes)
             gbs = nb / (ms * 1e-3) / 1e9
             res[str(T)] = {"layer_us": round(ms * 1e3, 2), "layer_bytes": nb,
                            "layer_GBps": round(gbs, 1), "layer_frac_of_peak": round(gbs / peak, 4),
                            "ops": per}
-            print(f"linear {qt} T={T}: layer {ms * 1e3:.1f} us, {gbs:.0f} GB/s", flush=True)
+            print(f"linear {qt} T={T}: layer {ms * 1e3:.1f} us, {gbs:.0f} GB/s; "
+                  + " ".join(f"{n}={v['us']}" for n, v in per.items()), flush=True)
         out[qt] = res
         del layers
     with open(path, "w") as f:
@@ -922,7 +985,7 @@ DECODE_POS = 8191   # the token's position: it attends to 8192 cache rows
 DECODE_BATCH = 16   # tokens of the batched decode case (configs[1] positions)
 
 
-def decode_layer_bench(mlk, fwd, steps, log=sys.stdout):
+def decode_layer_bench(mlk, fwd, steps, log=sys.stdout, marks=None):
     """One decode step of one Llama-3-8B layer through mlk_forward_layer_batch:
     a single token at position 8191 (the top of configs[1]'s position
     range), and a batch of DECODE_BATCH tokens at positions uniform in
@@ -935,6 +998,8 @@ def decode_layer_bench(mlk, fwd, steps, log=sys.stdout):
     cfg.update(hidden_dim=cfg["ffn"], max_seq=S)
     D, KV, hd = cfg["dim"], cfg["n_kv_heads"], cfg["head_dim"]
     st = mlk.Stream()
+    if marks is not None:
+        marks("decode_layer_8b", st)
     L = DECODE_COPIES
     kc = mlk.DeviceBuffer.empty((L, S, KV, hd))
     vc = mlk.DeviceBuffer.empty((L, S, KV, hd))
@@ -1362,6 +1427,30 @@ def rocprof_report(kt_dir, fetch_dir, write_dir, cfetch_dir, cwrite_dir):
         lines.append("")
     with open(os.path.join(out_dir, "chain_decode_tiny_rocprof.md"), "w") as f:
         f.write("\n".join(lines))
+    # the 8B decode layer (decode_layer_8b): every kernel of the section by
+    # name and grid, with the counters' HBM bytes
+    fsec, wsec = fetch.get("decode_layer_8b", []), write.get("decode_layer_8b", [])
+    lines = ["# One Llama-3-8B layer as a decode step (bench.py decode_layer_8b): rocprofv3 "
+             "summary", ""] + preamble
+    lines += ["The section runs, in this order, Q8_0, Q4_0 and F32 weights (Q8_0 / Q4_0 on "
+              "their planar copies), each for one token at position 8191 and for 16 tokens at "
+              "positions in 0..8191, over 4 rotated layers.  Weight preparation (quantization, "
+              "planar repacking) is left out.", "",
+              "| kernel | grid (work-items) | launches | avg us | min us | HBM bytes / launch |",
+              "|---|---|---|---|---|---|"]
+    groups = {}
+    for op, k, g, v in durations.get("decode_layer_8b", []):
+        if _base(k) in ("QuantizeKernel", "ToPlanar"):
+            continue
+        groups.setdefault((k, g), []).append(v)
+    for (k, g), d in groups.items():
+        fk = mean([v for _, kk, gg, v in fsec if kk == k and gg == g])
+        wk = mean([v for _, kk, gg, v in wsec if kk == k and gg == g])
+        hbm = "%.0f" % ((fk / f_factor + wk / w_factor) * 1024) if fk is not None and wk is not None else "n/a"
+        lines.append("| %s | %d | %d | %.2f | %.2f | %s |" % (k, g, len(d), mean(d), min(d), hbm))
+    lines.append("")
+    with open(os.path.join(out_dir, "decode_layer_8b_rocprof.md"), "w") as f:
+        f.write("\n".join(lines))
     sw = [r for r in c3_rows if r[0] == "swiglu"][0]
     with open(PMC_FILE, "w") as f:
         json.dump({"kernel": "StreamKernel<SwiGluOp> (swiglu)", "workload": "c3_prefill_8b",
@@ -1448,6 +1537,11 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
     print("\n".join(md[:40]))
 
 
+def progress(msg):
+    """A progress line on stderr (the JSON result is the only stdout line)."""
+    print(f"bench.py: {msg}", file=sys.stderr, flush=True)
+
+
 def main():
     args = parse_args()
     if args.kernel_summary:
@@ -1530,23 +1624,30 @@ def main():
         "device": mlk.device_info(0),
     }
     with_cpu = not args.no_cpu_baseline
+    table_host = chain.table.download() if with_cpu else None  # shared by C3 and C2
     if with_cpu:
         result["cpu_baseline"] = cpu_chain_baseline(
-            chain_host_bufs(chain, cfg, T), T, chain_bytes,
+            chain_host_bufs(chain, cfg, T, table_host), T, chain_bytes,
             f"the whole configs[2] chain (T={T}, Llama-3-8B shapes)")
+    progress("configs[2] chain and its CPU baseline done")
     configs = {"c1_tiny": None, "c2_decode_8b": c2_decode(mlk, args.steps, args.warmup, marks,
-                                                          chain.table)}
-    del chain
+                                                          chain.table, table_host)}
+    del chain, table_host
+    progress("configs[1] decode steps done")
     configs["c1_tiny"] = c1_tiny(mlk, args.steps, args.warmup, marks)
+    progress("configs[0] tiny chain done")
     configs["c4_quant_gather"] = c4_gathers(mlk, args.steps, peak, marks, with_cpu)
+    progress("configs[3] quantized gathers done")
     configs["c5_70b"] = c5_chain(mlk, args.steps, args.warmup, peak, marks, with_cpu)
+    progress("configs[4] 70B chain done")
     result["configs"] = configs
     # beside the op chain: one 8B layer through mlk_forward_layer_batch as a
     # decode step (one token at position 8191; 16 tokens at positions in
     # 0..8191 on the planar weights), weights rotated over 4 layers
     import importlib
     fwd = importlib.import_module(mlk.__name__ + ".forward")
-    result["decode_layer_8b"] = decode_layer_bench(mlk, fwd, min(args.steps, 10), log=sys.stderr)
+    result["decode_layer_8b"] = decode_layer_bench(mlk, fwd, min(args.steps, 10), log=sys.stderr,
+                                                   marks=marks)
     print(json.dumps(result))
 
 

@@ -176,7 +176,10 @@ def set_device(device_id):
 def device_info(device_id=0):
     info = DeviceInfo()
     check(lib.mlk_get_device_info(device_id, C.byref(info)))
-    return {"name": info.name.decode(), "arch": info.arch.decode(),
+    arch = info.arch.decode()
+    # the runtime leaves the marketing name empty on some boxes: fall back to
+    # the architecture name, as GetCudaInfo does
+    return {"name": info.name.decode() or arch, "arch": arch,
             "compute_units": info.multiprocessors, "total_bytes": info.total_bytes,
             "clock_khz": info.clock_khz, "memory_clock_khz": info.memory_clock_khz,
             "memory_bus_bits": info.memory_bus_bits, "runtime_version": info.runtime_version,

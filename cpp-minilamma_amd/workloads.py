@@ -17,8 +17,11 @@ LLAMA3_70B = dict(dim=8192, n_heads=64, n_kv_heads=8, head_dim=128, ffn=28672, t
 
 CONFIGS = {
     # tiny-model op chain (the reference's CPU-runnable case)
+    # (table N(0, 0.02), norm weight N(1, 0.1), activations and the residual
+    # delta N(0, 1): act_std; the 8B and 70B configs scale activations by 0.02)
     "c1_tiny": dict(vocab=131, dim=64, n_heads=4, n_kv_heads=2, head_dim=16, ffn=172,
-                    eps=1e-5, theta=10000.0, ids=[128, 104, 101, 108, 108, 111], seed=42),
+                    eps=1e-5, theta=10000.0, ids=[128, 104, 101, 108, 108, 111], seed=42,
+                    act_std=1.0),
     # 8B decode step, T = 1..64, positions uniform in [0, 8191]
     "c2_decode_8b": dict(LLAMA3_8B, tokens=(1, 2, 4, 8, 16, 32, 64), max_pos=8191, seed=42),
     # 8B prefill, T = 4096 at positions 0..4095

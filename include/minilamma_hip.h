@@ -277,8 +277,11 @@ mlk_status mlk_attention_decode_f32(const float* q, int64_t q_row_stride, const 
  * hipMalloc).  No counterpart in the reference.  Same arguments, semantics
  * and results as mlk_attention_decode_f32 without the workspace: the chunk
  * partials go to a fixed device array of the library, one per GPU, of
- * mlk_attention_noalloc_scratch_bytes() bytes (64 MiB), held from the first
- * call on that GPU until the process ends.  Calls needing more than that
+ * mlk_attention_noalloc_scratch_bytes() bytes (64 MiB).  The array is part of
+ * the library's code object, so it is reserved on a GPU as soon as any
+ * kernel of the library loads there (for every user of the library, whether
+ * or not it calls this entry) and is held until the process ends.  Calls
+ * needing more than that
  * (mlk_attention_workspace_bytes() of the shape) are rejected with
  * MLK_ERR_INVALID before any launch; at max_ctx 8192 every batch up to 256
  * tokens of the 8B and 70B head shapes fits.  Nothing is allocated and no

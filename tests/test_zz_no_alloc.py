@@ -61,7 +61,9 @@ def test_noalloc_rejects_more_than_the_scratch(mlk):
     assert limit == 64 << 20
     T, max_ctx = 1024, 1 << 17
     assert mlk.attention_workspace_bytes(T, 64, 8, 128, max_ctx) > limit
-    fake = 1 << 20  # never dereferenced: the size check comes first
-    with pytest.raises(mlk.MlkError, match="scratch"):
-        mlk.attention_decode_noalloc(fake, fake, fake + 4096, 1, max_ctx, 64, 8, 128, 0, T,
-                                     fake + 8192, max_ctx, pos0=0)
+    # null operands: the size check comes first and names the scratch; were it
+    # ever moved after the operand checks, those would reject the nulls with
+    # another message (a clean failure here, never a launch)
+    with pytest.raises(mlk.MlkError, match="exceed the .*-byte scratch"):
+        mlk.attention_decode_noalloc(None, None, None, 1, max_ctx, 64, 8, 128, 0, T,
+                                     None, max_ctx, pos0=0)
