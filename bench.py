@@ -67,6 +67,11 @@ def parse_args():
                    help="only measure one Llama-3-8B layer over a 4096-token prompt chunk "
                         "(mlk_forward_layer_batch), with a token-by-token comparison, into "
                         "this JSON file")
+    p.add_argument("--decode-layer", default=None,
+                   help="only measure one Llama-3-8B layer as a decode step (one token at "
+                        "position 8191; 16 tokens at positions in 0..8191; Q8_0 / Q4_0 on "
+                        "planar copies, F32), the default run's decode_layer_8b section, into "
+                        "this JSON file")
     p.add_argument("--attention", default=None,
                    help="only measure decode attention (Llama-3-8B and 70B head shapes, one "
                         "token at several context lengths and configs[1]'s 64 tokens) into "
@@ -1571,6 +1576,13 @@ def main():
         return
     if args.layer:
         layer_bench(mlk, args.steps, args.layer)
+        return
+    if args.decode_layer:
+        import importlib
+        fwd = importlib.import_module(mlk.__name__ + ".forward")
+        res = decode_layer_bench(mlk, fwd, args.steps, log=sys.stderr)
+        with open(args.decode_layer, "w") as f:
+            json.dump(res, f, indent=1)
         return
     peak = workloads.HBM_PEAK_GBS
     cfg = workloads.CONFIGS["c3_prefill_8b"]

@@ -1056,7 +1056,7 @@ __device__ inline float PlanarChunkDot(const PlanarChunk<QT>& b, const float* xc
 // one line per load (the matrix's first bytes, the same for every lane), so
 // every weight load is issued unconditionally and each step waits only for
 // its own chunk.
-template <int QT, int MODE, int NVPT>
+template <int QT, int MODE, int NVPT, int NB>
 __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
     const float* x, StreamArgs a, int64_t K, int nwm, int ncw, int tpw) {
     extern __shared__ __align__(16) float xs[];
@@ -1134,9 +1134,9 @@ __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
         xq2 = x_at(2);
         xq3 = x_at(3);
     }
-    PlanarChunk<QT> b0, b1;
-    load(0, b0);
-    load(1, b1);
+    PlanarChunk<QT> b[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) load(i, b[i]);
     __builtin_amdgcn_sched_barrier(0);
     // the (cos, sin) of each finishing lane's row, while the chunks load
     double rc = 1.0, rs = 0.0;
@@ -1174,17 +1174,21 @@ __global__ __launch_bounds__(kRowPlanarMaxWaves* kWave) void GemvRowPlanar(
         v += __shfl_xor(v, 32);
         if (g == 0) part[(((st >> lg) * kMats + mat) * nch + c) * 16 + r] = v;
     };
-    // b0 and b1 hold steps st and st + 1; the last two steps take no further
-    // loads (a load still in flight would hold up the barrier below)
+    // b[i] holds step st + i; each computed buffer takes the step NB ahead,
+    // and the last NB steps take no further loads (a load still in flight
+    // would hold up the barrier below)
     int st = 0;
-    for (; st + 2 < steps; st += 2) {
-        compute(b0, st);
-        load(st + 2, b0);
-        compute(b1, st + 1);
-        load(st + 3, b1);
+    for (; st + NB < steps; st += NB) {
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            compute(b[i], st + i);
+            load(st + i + NB, b[i]);
+        }
     }
-    compute(b0, st);
-    if (st + 1 < steps) compute(b1, st + 1);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if (st + i < steps) compute(b[i], st + i);
+    }
     __syncthreads();
     if (wave >= ntile) return;  // wave t finishes tile t
     const int64_t tile = tile0 + wave;
@@ -1282,19 +1286,28 @@ size_t RowPlanarLds(int64_t K, int mode, int tpw) {
 
 constexpr size_t kRowPlanarLdsMax = 64 * 1024 - 16 * sizeof(double);  // StageNorm's sums
 
+template <int QT, int MODE, int NB>
+void LaunchRowPlanarNb(unsigned grid, int threads, size_t lds, hipStream_t s, const float* x,
+                       const StreamArgs& a, int64_t K, const RowPlanarPlan& p) {
+    if (a.norm.weight == nullptr) {
+        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 0, NB>), dim3(grid), dim3(threads), lds, s, x,
+                           a, K, p.nwm, p.ncw, p.tpw);
+    } else if (a.norm.vpt == 1) {
+        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 1, NB>), dim3(grid), dim3(threads), lds, s, x,
+                           a, K, p.nwm, p.ncw, p.tpw);
+    } else {
+        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 2, NB>), dim3(grid), dim3(threads), lds, s, x,
+                           a, K, p.nwm, p.ncw, p.tpw);
+    }
+}
+
+// Two chunks in flight per wave.  Four (16 KB of Q8_0 weights requested per
+// wave) measured slower on the 8B decode layer (Q8_0 77.4 -> 80.6 us): the
+// extra registers cost a wave per SIMD, and the weights streamed no faster.
 template <int QT, int MODE>
 void LaunchRowPlanar(unsigned grid, int threads, size_t lds, hipStream_t s, const float* x,
                      const StreamArgs& a, int64_t K, const RowPlanarPlan& p) {
-    if (a.norm.weight == nullptr) {
-        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 0>), dim3(grid), dim3(threads), lds, s, x, a,
-                           K, p.nwm, p.ncw, p.tpw);
-    } else if (a.norm.vpt == 1) {
-        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 1>), dim3(grid), dim3(threads), lds, s, x, a,
-                           K, p.nwm, p.ncw, p.tpw);
-    } else {
-        hipLaunchKernelGGL((GemvRowPlanar<QT, MODE, 2>), dim3(grid), dim3(threads), lds, s, x, a,
-                           K, p.nwm, p.ncw, p.tpw);
-    }
+    LaunchRowPlanarNb<QT, MODE, 2>(grid, threads, lds, s, x, a, K, p);
 }
 
 template <int QT>

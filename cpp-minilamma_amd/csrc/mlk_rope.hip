@@ -238,9 +238,17 @@ __global__ __launch_bounds__(kThreads) void RopeKernel(float* q, float* k, int64
 // run (two register sets, loop unrolled by two with the last one or two
 // tokens peeled, so no load sits under a branch and no token is loaded
 // twice: a reload would come from HBM, the loads being non-temporal).
-// Same arithmetic as RopeKernel.
+// Same arithmetic as RopeKernel.  The Llama path (normal layout, two pairs
+// a lane) fits 128 registers and takes workgroups of up to 1024 threads;
+// the NeoX and one-pair forms need a few more registers than that (their
+// two register sets of 2 x 5 heads, and the extra address of NeoX's second
+// half), so they are built for at most 512 threads (up to 256 registers,
+// no scratch) -- every Llama / Qwen head shape fits 512.
 template <int PV, bool kNeoX>
-__global__ __launch_bounds__(1024) void RopePipe(float* q, float* k, int64_t n_tokens,
+constexpr int PipeMaxThreads() { return PV == 2 && !kNeoX ? 1024 : 512; }
+
+template <int PV, bool kNeoX>
+__global__ __launch_bounds__((PipeMaxThreads<PV, kNeoX>())) void RopePipe(float* q, float* k, int64_t n_tokens,
                                                  int n_heads, int n_kv_heads, int head_dim,
                                                  int64_t q_stride, int64_t k_stride,
                                                  const int32_t* positions, int32_t pos0,
@@ -317,9 +325,10 @@ __global__ __launch_bounds__(1024) void RopePipe(float* q, float* k, int64_t n_t
 }
 
 // Smallest row count whose Q and K slots fit kBatch, or 0 when the rows
-// would need more than 1024 threads.
-inline int PipeRows(int n_heads, int n_kv_heads, int lanes) {
-    for (int rows = (n_heads + n_kv_heads + kBatch - 1) / kBatch; rows * lanes <= 1024; ++rows) {
+// would need more than max_threads threads.
+inline int PipeRows(int n_heads, int n_kv_heads, int lanes, int max_threads) {
+    for (int rows = (n_heads + n_kv_heads + kBatch - 1) / kBatch; rows * lanes <= max_threads;
+         ++rows) {
         if ((n_heads + rows - 1) / rows + (n_kv_heads + rows - 1) / rows <= kBatch) return rows;
     }
     return 0;
@@ -332,7 +341,7 @@ mlk_status LaunchRope(float* q, float* k, int64_t n_tokens, int n_heads, int n_k
     const int lanes = head_dim / 2 / PV;
     const bool table = head_dim / 2 <= kRopePairs;
     const RopeFreqs f = MakeRopeFreqs(theta, table ? head_dim : 2);
-    const int rows = table ? PipeRows(n_heads, n_kv_heads, lanes) : 0;
+    const int rows = table ? PipeRows(n_heads, n_kv_heads, lanes, PipeMaxThreads<PV, kNeoX>()) : 0;
     // byte offsets within a token's Q or K row are 32-bit
     const bool offsets_fit =
         4 * static_cast<int64_t>(n_heads > n_kv_heads ? n_heads : n_kv_heads) * head_dim <= UINT32_MAX;
