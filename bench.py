@@ -60,6 +60,11 @@ def parse_args():
                    help="only measure the seven linear projections of one Llama-3-8B layer "
                         "(F32, Q8_0, Q4_0, Q4_1 weights; T = 1, 4, 16 token rows) into this "
                         "JSON file")
+    p.add_argument("--linear-eager", action="store_true",
+                   help="with --linear: issue each projection's calls as eager launches "
+                        "instead of one replayed HIP graph (for a rocprofv3 kernel trace: "
+                        "rocprofv3 7.2 faults tracing replays of the three-kernel planar calls); "
+                        "the same marker kernels bracket the timed calls")
     p.add_argument("--gemm", default=None,
                    help="only measure the seven Llama-3-8B layer projections at prefill row counts "
                         "(32 to 4096; the matrix-core GEMM) into this JSON file")
@@ -90,6 +95,10 @@ def parse_args():
                         "--linear or --attention run, with that run's JSON results, into OUT_MD; "
                         "the commands that produced the inputs are read from the environment "
                         "variable PROFILE_COMMANDS (one per line)")
+    p.add_argument("--pmc-summary", nargs=3, default=None,
+                   metavar=("OUT_MD", "TITLE", "COUNTER_DIR"),
+                   help="write the mean of every counter of a rocprofv3 --pmc run per kernel and "
+                        "grid into OUT_MD (the commands from PROFILE_COMMANDS, one per line)")
     p.add_argument("--calibrate", action="store_true",
                    help="only run the counter-calibration kernel (SiLU over 256 MiB: "
                         "reads 256 MiB, writes 256 MiB per launch)")
@@ -700,29 +709,67 @@ class LinearLayers:
             self.mlk.linear_quant(self.qtype, x, w, y, T, k, o, stream=stream)
 
 
-def _graph_ms(mlk, st, launches, n):
+# marker grids 256 * (LINEAR_MARK_BASE + i): timed calls i of --linear; 256 *
+# LINEAR_MARK_END: their end.  Below 1024 workgroups, the most a zero fill
+# launches on a 256-CU GPU (4 a CU), so the grid is the marker's own.
+LINEAR_MARK_BASE = 600
+LINEAR_MARK_END = 599
+
+
+def _linear_mark(mlk, buf, k, st):
+    """A ZeroKernel of grid 256 * k work-items on `st`: a rocprofv3 trace of
+    --linear tells the timed replays' kernels apart by these."""
+    mlk.check(mlk.lib.mlk_zero_async(buf.ptr, 4096 * k, st.handle), "mark")
+
+
+def _eager_ms(mlk, st, launches, n, mark=None):
+    """_graph_ms with the n calls issued as eager launches (Python dispatch
+    included in the event time; a kernel trace of this run gives the
+    kernels' own durations)."""
+    for i in range(min(n, 3)):
+        launches(i)
+    st.synchronize()
+    if mark is not None:
+        _linear_mark(mlk, mark[0], LINEAR_MARK_BASE + mark[1], st)
+    e0, e1 = mlk.Event(), mlk.Event()
+    e0.record(st)
+    for i in range(n):
+        launches(i)
+    e1.record(st)
+    if mark is not None:
+        _linear_mark(mlk, mark[0], LINEAR_MARK_END, st)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / n
+
+
+def _graph_ms(mlk, st, launches, n, mark=None):
     """ms per item of `launches(i)` for i < n, issued as one captured HIP
     graph and timed over one replay between two events on `st` (after one
     untimed replay): the host dispatches one graph instead of n ctypes calls
     and their HIP launches, so the time is the kernels' and the gaps the GPU
-    leaves between graph nodes."""
+    leaves between graph nodes.  mark: (buffer, index) -- marker kernels
+    bracket the timed replay (outside the events)."""
     with mlk.Graph.capture(st) as graph:
         for i in range(n):
             launches(i)
     try:
         graph.launch()
         st.synchronize()
+        if mark is not None:
+            _linear_mark(mlk, mark[0], LINEAR_MARK_BASE + mark[1], st)
         e0, e1 = mlk.Event(), mlk.Event()
         e0.record(st)
         graph.launch()
         e1.record(st)
+        if mark is not None:
+            _linear_mark(mlk, mark[0], LINEAR_MARK_END, st)
         e1.synchronize()
         return e0.elapsed_ms(e1) / n
     finally:
         graph.close()
 
 
-def linear_bench(mlk, steps, peak, path):
+def linear_bench(mlk, steps, peak, path, eager=False):
     """Per-projection launch time and the time of one whole layer's seven
     projections.  Each projection's `steps` calls (over its rotating weight
     copies) are captured into one HIP graph and timed over a replay, so the
@@ -739,9 +786,18 @@ def linear_bench(mlk, steps, peak, path):
     st = mlk.Stream()
     out = {"workload": "Llama-3-8B layer projections (configs[1] shapes), weights N(0,0.02) "
                        "quantized on the device; x N(0,1)",
-           "timing": f"each projection's {steps} calls captured into one HIP graph over the "
-                     "rotating weight copies, one replay timed between two events",
-           "peak_GBps": peak}
+           "timing": (f"each projection's {steps} calls as eager launches between two events"
+                      if eager else
+                      f"each projection's {steps} calls captured into one HIP graph over the "
+                      "rotating weight copies, one replay timed between two events"),
+           "peak_GBps": peak, "calls_per_replay": steps, "markers": {}}
+    mark_buf = mlk.DeviceBuffer(4096 * 1024, np.uint8)
+    timed = _eager_ms if eager else _graph_ms
+    marks = out["markers"]
+
+    def mark(label):
+        marks[len(marks)] = label
+        return (mark_buf, len(marks) - 1)
     for qt in LINEAR_DECODE_TYPES:
         layers = LinearLayers(mlk, cfg, qt, seed=300)
         res = {"weight_copies": {n: layers.n_copies(n) for n, _, _ in layers.shapes}}
@@ -751,8 +807,8 @@ def linear_bench(mlk, steps, peak, path):
                 for i in range(3):  # eager: sizes the auto workspace before the capture
                     layers.launch(i, name, k, o, x, y, T, st)
                 st.synchronize()
-                ms = _graph_ms(mlk, st, lambda i: layers.launch(3 + i, name, k, o, x, y, T, st),
-                               steps)
+                ms = timed(mlk, st, lambda i: layers.launch(3 + i, name, k, o, x, y, T, st),
+                           steps, mark(f"{qt} / {T} / {name}"))
                 nb = workloads.bytes_linear(base_type(qt), T, k, o)
                 gbs = nb / (ms * 1e-3) / 1e9
                 per[name] = {"in": k, "out": o, "us": round(ms * 1e3, 2), "bytes": nb,
@@ -761,7 +817,7 @@ def linear_bench(mlk, steps, peak, path):
             def layer_call(i):
                 for name, k, o in layers.shapes:
                     layers.launch(3 + steps + i, name, k, o, x, y, T, st)
-            ms = _graph_ms(mlk, st, layer_call, steps)
+            ms = timed(mlk, st, layer_call, steps, mark(f"{qt} / {T} / layer"))
             nb = sum(workloads.bytes_linear(base_type(qt), T, k, o) for _, k, o in layers.shapes)
             gbs = nb / (ms * 1e-3) / 1e9
             res[str(T)] = {"layer_us": round(ms * 1e3, 2), "layer_bytes": nb,
@@ -1501,7 +1557,7 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
         return m.group(1) if m else name
 
     for (name, grid), d in sorted(launches.items(), key=lambda kv: (short(kv[0][0]), kv[0][1])):
-        if name.startswith("__amd") or "Fill" in name or "Quantize" in name:
+        if name.startswith("__amd") or "Fill" in name or "Quantize" in name or "ZeroKernel" in name:
             continue
         row = "| %s | %d | %d | %.2f | %.2f |" % (short(name), grid, len(d), sum(d) / len(d),
                                                   min(d))
@@ -1511,7 +1567,9 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
             row += " %s |" % (("%.0f" % ((fk[0] / ff + wk[0] / wf) * 1024)) if fk and wk else "n/a")
         md.append(row)
     md += ["", "Results of the same command (bench.py JSON, events around back-to-back "
-           "launches; HBM-bound cases on rotating cold copies, against 8 TB/s; "
+           "launches -- for --linear, around one replay of a HIP graph holding each "
+           "projection's calls, so the figure is kernel time, not Python dispatch; HBM-bound "
+           "cases on rotating cold copies, against 8 TB/s; "
            "matrix-core cases against the peak of the instruction they run: 157.3 TFLOP/s fp32 MFMA, or for bf16 piece products the 2.5 PFLOP/s bf16 peak over the bf16 MACs per useful MAC, 3 in the GEMM and 7.5 in the attention):", "",
            "| case | us | throughput | fraction of peak |", "|---|---|---|---|"]
 
@@ -1536,7 +1594,50 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
                 if k not in ("ops",) or isinstance(v, dict):
                     walk(v, path + ([k] if k not in ("ops", "cases") else []))
 
-    walk(json.load(open(bench_json)), [])
+    res = json.load(open(bench_json))
+    walk(res, [])
+    if res.get("markers"):
+        # --linear: each timed graph replay sits between a start marker
+        # (grid 256 * (LINEAR_MARK_BASE + i)) and an end marker; the
+        # kernels in between are that replay's, calls_per_replay calls
+        rows = sorted(csv.DictReader(open(_one_csv(kt_dir, "kernel_trace.csv"))),
+                      key=lambda r: int(r["Dispatch_Id"]))
+        sums, spans, cur = {}, {}, None
+        for r in rows:
+            g = int(r["Grid_Size_X"]) * int(r.get("Grid_Size_Y", 1) or 1) * int(r.get("Grid_Size_Z", 1) or 1)
+            t0, t1 = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+            if _base(r["Kernel_Name"]) == "ZeroKernel" and g % 256 == 0:
+                k = g // 256
+                if k == LINEAR_MARK_END:
+                    cur = None
+                    continue
+                if k >= LINEAR_MARK_BASE:
+                    cur = k - LINEAR_MARK_BASE
+                    continue
+            if cur is None:
+                continue
+            sums[cur] = sums.get(cur, 0.0) + (t1 - t0) / 1e3
+            lo, hi = spans.get(cur, (t0, t1))
+            spans[cur] = (min(lo, t0), max(hi, t1))
+        n = res["calls_per_replay"]
+
+        def event_us(label):
+            qt, t, name = label.split(" / ")
+            node = res[qt][t]
+            return node["layer_us"] if name == "layer" else node["ops"][name]["us"]
+        md += ["", "Event time per call (the bench JSON's run: one replayed HIP graph per "
+               "projection) against the kernels of the same calls in the kernel trace (kernel "
+               "sum: the durations of their kernels; span: first start to last end, the gaps "
+               "between launches included; both per call):", "",
+               "| case | event us / call | trace kernel sum us / call | trace span us / call | "
+               "event / kernel sum |", "|---|---|---|---|---|"]
+        for i, label in sorted(((int(k), v) for k, v in res["markers"].items())):
+            if i not in sums:
+                continue
+            ev = event_us(label)
+            ks = sums[i] / n
+            sp = (spans[i][1] - spans[i][0]) / 1e3 / n
+            md.append("| %s | %.2f | %.2f | %.2f | %.3f |" % (label, ev, ks, sp, ev / ks))
     with open(out_md, "w") as f:
         f.write("\n".join(md) + "\n")
     print("\n".join(md[:40]))
@@ -1547,8 +1648,37 @@ def progress(msg):
     print(f"bench.py: {msg}", file=sys.stderr, flush=True)
 
 
+def pmc_summary(out_md, title, d):
+    """Mean counter values per dispatch, by kernel and grid, of a --pmc run
+    (input generation, quantization, repacking and markers left out)."""
+    import csv
+    acc = {}
+    for r in csv.DictReader(open(_one_csv(d, "counter_collection.csv"))):
+        if _base(r["Kernel_Name"]) in ("FillNormalKernel", "QuantizeKernel", "ToPlanar",
+                                       "ZeroKernel") or r["Kernel_Name"].startswith("__amd"):
+            continue
+        key = (_short(r["Kernel_Name"]), int(r["Grid_Size"]))
+        acc.setdefault(key, {}).setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    names = sorted({c for v in acc.values() for c in v})
+    cmds = [c for c in os.environ.get("PROFILE_COMMANDS", "").split("\n") if c.strip()]
+    md = [f"# {title}: rocprofv3 counters", "", "Commands (repo root, one MI355X):", ""]
+    md += ["    " + c for c in cmds]
+    md += ["", "Mean value per dispatch (the SQ counters summed over the GPU), by kernel and grid "
+           "(total work-items):", "",
+           "| kernel | grid | " + " | ".join(names) + " |", "|---|---|" + "---|" * len(names)]
+    for (k, g), v in acc.items():
+        md.append("| %s | %d | " % (k, g) + " | ".join(
+            "%.0f" % (sum(v[n]) / len(v[n])) if n in v else "n/a" for n in names) + " |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(md) + "\n")
+    print("\n".join(md))
+
+
 def main():
     args = parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary)
+        return
     if args.kernel_summary:
         kernel_summary(*args.kernel_summary)
         return
@@ -1566,7 +1696,7 @@ def main():
         calibrate(mlk, args.steps)
         return
     if args.linear:
-        linear_bench(mlk, args.steps, workloads.HBM_PEAK_GBS, args.linear)
+        linear_bench(mlk, args.steps, workloads.HBM_PEAK_GBS, args.linear, eager=args.linear_eager)
         return
     if args.attention:
         attention_bench(mlk, args.steps, workloads.HBM_PEAK_GBS, args.attention)
