@@ -947,6 +947,47 @@ __device__ inline uint32_t BytesBf(uint32_t v, int j) {
                   static_cast<float>(static_cast<int8_t>(v >> (16 * j + 8))));
 }
 
+// Block b of a lane's planar codes (cw: the range's 16-byte code loads of one
+// row tile, sw: its scale loads) as the MFMA's bf16 weight operand, and the
+// block's scale.
+template <int QT, int NP>
+__device__ inline bf16x8 PlanarBlockOperand(const u32x4 (&cw)[QT == MLK_Q8_0 ? NP : NP / 2],
+                                            const u32x4 (&sw)[NP / 4], int b, float* d) {
+    const uint32_t sv = sw[b / 8][(b % 8) / 2];
+    const uint32_t h16 = (b & 1) ? sv >> 16 : sv & 0xFFFFu;
+    u32x4 q;
+    if constexpr (QT == MLK_Q8_0) {
+        const uint32_t lo = (b & 1) ? cw[b / 2][2] : cw[b / 2][0];
+        const uint32_t hi = (b & 1) ? cw[b / 2][3] : cw[b / 2][1];
+        q = u32x4{BytesBf(lo, 0), BytesBf(lo, 1), BytesBf(hi, 0), BytesBf(hi, 1)};
+        *d = HalfHw(h16);
+    } else {
+        // nibbles (code - 8, two's complement) moved to the high half of each
+        // byte: signed bytes of 16 (code - 8), scale d / 16
+        const uint32_t v = cw[b / 4][b % 4];
+        const uint32_t lo = (v << 4) & 0xF0F0F0F0u, hi = v & 0xF0F0F0F0u;
+        q = u32x4{BytesBf(lo, 0), BytesBf(lo, 1), BytesBf(hi, 0), BytesBf(hi, 1)};
+        *d = HalfHw(h16) * 0.0625f;
+    }
+    return __builtin_bit_cast(bf16x8, q);
+}
+
+// acc += d * (the block's three piece products): the exact products summed
+// on the matrix cores, then one fp32 FMA with the block's scale.
+template <int TT>
+__device__ inline void PlanarBlockProducts(const bf16x8 (&xa)[TT][3], bf16x8 wb, float d,
+                                           f32x4 (&acc)[TT]) {
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+        f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][0], wb, f32x4{0.f, 0.f, 0.f, 0.f},
+                                                          0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][1], wb, s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][2], wb, s, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[tt][r] = __builtin_fmaf(d, s[r], acc[tt][r]);
+    }
+}
+
 // The x planes of tokens t < T: one thread per (block, token, input pair).
 __global__ __launch_bounds__(kGemmThreads) void SplitXBf(const float* __restrict__ x, int64_t T,
                                                          int64_t K, uint32_t* __restrict__ planes) {
@@ -961,14 +1002,59 @@ __global__ __launch_bounds__(kGemmThreads) void SplitXBf(const float* __restrict
     }
 }
 
+// One K range's x planes in LDS: (block, piece, token slot) rows of 16
+// dwords, kTok = 16 TT slots; slots t < T copied, the rest zero.  (Rows
+// padded to 20 dwords measured no faster, with slightly more bank-conflict
+// cycles.)
+template <int TT, int NP>
+struct PlanarX {
+    static constexpr int kTok = 16 * TT;
+    static constexpr int kRowWords = 16;
+    static constexpr int kRows = 2 * NP * 3 * kTok;
+    static constexpr int kWords = kRows * kRowWords;  // the LDS array
+    static constexpr int kIter = kRows * 4 / kSkThreads;  // 16-byte copies per thread
+    static_assert(kRows * 4 % kSkThreads == 0, "whole copy rounds");
+    u32x4 v[kIter];
+    __device__ void Load(const uint32_t* planes, int sp, int64_t T) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(planes) +
+                           static_cast<int64_t>(sp) * 2 * NP * 3 * T * 4;
+#pragma unroll
+        for (int k = 0; k < kIter; ++k) {
+            const int i = static_cast<int>(threadIdx.x) + kSkThreads * k;
+            const int t = (i / 4) % kTok, bp = i / (4 * kTok);
+            v[k] = u32x4{0u, 0u, 0u, 0u};
+            if (t < T) v[k] = src[(bp * T + t) * 4 + i % 4];
+        }
+    }
+    __device__ void Store(uint32_t* xs) const {
+#pragma unroll
+        for (int k = 0; k < kIter; ++k) {
+            const int i = static_cast<int>(threadIdx.x) + kSkThreads * k;
+            *reinterpret_cast<u32x4*>(xs + (i / 4) * kRowWords + 4 * (i % 4)) = v[k];
+        }
+    }
+    // block b's three pieces as the A operands of the lane (token i16 of
+    // each 16-token tile, inputs 8g .. 8g + 7)
+    // (lo: the lane's offset in dwords, LaneOffset)
+    __device__ static int LaneOffset(int i16, int g) { return i16 * kRowWords + 4 * g; }
+    __device__ static void Read(const uint32_t* xs, int lo, int b, bf16x8 (&xa)[TT][3]) {
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                xa[tt][p] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                    xs + lo + ((b * 3 + p) * kTok + tt * 16) * kRowWords));
+            }
+        }
+    }
+};
+
 template <int QT, int TT, int NP, int PT>
 __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restrict__ planes,
                                                          SkinnyArgs a, int64_t T, int64_t K,
                                                          float* __restrict__ partial) {
-    constexpr int kTok = 16 * TT;
-    constexpr int kBlockWords = 3 * kTok * 16;  // one block's x planes
     constexpr int kCodeVecs = QT == MLK_Q8_0 ? NP : NP / 2;  // 16-byte code loads per tile
-    __shared__ __align__(16) uint32_t xs[2 * NP * kBlockWords];
+    __shared__ __align__(16) uint32_t xs[PlanarX<TT, NP>::kWords];
     const int rgall = static_cast<int>(blockIdx.x) % a.row_groups;
     const int sp = static_cast<int>(blockIdx.x) / a.row_groups;
     const int seg = (a.n_seg > 2 && rgall >= a.g0[2]) ? 2 : ((a.n_seg > 1 && rgall >= a.g0[1]) ? 1 : 0);
@@ -998,24 +1084,10 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
 #pragma unroll
         for (int v = 0; v < NP / 4; ++v) sw[n][v] = sc[16 * v];
     }
-    // the range's x planes into LDS, (block, piece, token slot) rows of 16
-    // dwords: slots t < T copied (all loads before the stores), the rest zero
-    constexpr int kXIter = 2 * NP * 3 * kTok * 4 / kSkThreads;
-    static_assert(2 * NP * 3 * kTok * 4 % kSkThreads == 0, "whole copy rounds");
-    const u32x4* src = reinterpret_cast<const u32x4*>(planes) +
-                       static_cast<int64_t>(sp) * 2 * NP * 3 * T * 4;
-    u32x4 xv[kXIter];
-#pragma unroll
-    for (int k = 0; k < kXIter; ++k) {
-        const int i = static_cast<int>(threadIdx.x) + kSkThreads * k;
-        const int t = (i / 4) % kTok, bp = i / (4 * kTok);
-        xv[k] = u32x4{0u, 0u, 0u, 0u};
-        if (t < T) xv[k] = src[(bp * T + t) * 4 + i % 4];
-    }
-#pragma unroll
-    for (int k = 0; k < kXIter; ++k) {
-        reinterpret_cast<u32x4*>(xs)[static_cast<int>(threadIdx.x) + kSkThreads * k] = xv[k];
-    }
+    // the range's x planes into LDS (all loads before the stores)
+    PlanarX<TT, NP> xv;
+    xv.Load(planes, sp, T);
+    xv.Store(xs);
     __syncthreads();
 
     f32x4 acc[PT][TT];
@@ -1027,43 +1099,12 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
 #pragma unroll
     for (int b = 0; b < 2 * NP; ++b) {
         bf16x8 xa[TT][3];
-#pragma unroll
-        for (int tt = 0; tt < TT; ++tt) {
-#pragma unroll
-            for (int p = 0; p < 3; ++p) {
-                xa[tt][p] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
-                    xs + ((b * 3 + p) * kTok + tt * 16 + i16) * 16 + 4 * g));
-            }
-        }
+        PlanarX<TT, NP>::Read(xs, PlanarX<TT, NP>::LaneOffset(i16, g), b, xa);
 #pragma unroll
         for (int n = 0; n < PT; ++n) {
-            u32x4 q;
             float d;
-            const uint32_t sv = sw[n][b / 8][(b % 8) / 2];
-            const uint32_t h16 = (b & 1) ? sv >> 16 : sv & 0xFFFFu;
-            if constexpr (QT == MLK_Q8_0) {
-                const uint32_t lo = (b & 1) ? cw[n][b / 2][2] : cw[n][b / 2][0];
-                const uint32_t hi = (b & 1) ? cw[n][b / 2][3] : cw[n][b / 2][1];
-                q = u32x4{BytesBf(lo, 0), BytesBf(lo, 1), BytesBf(hi, 0), BytesBf(hi, 1)};
-                d = HalfHw(h16);
-            } else {
-                // nibbles (code - 8, two's complement) moved to the high half
-                // of each byte: signed bytes of 16 (code - 8), scale d / 16
-                const uint32_t v = cw[n][b / 4][b % 4];
-                const uint32_t lo = (v << 4) & 0xF0F0F0F0u, hi = v & 0xF0F0F0F0u;
-                q = u32x4{BytesBf(lo, 0), BytesBf(lo, 1), BytesBf(hi, 0), BytesBf(hi, 1)};
-                d = HalfHw(h16) * 0.0625f;
-            }
-            const bf16x8 wb = __builtin_bit_cast(bf16x8, q);
-#pragma unroll
-            for (int tt = 0; tt < TT; ++tt) {
-                f32x4 s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][0], wb,
-                                                                  f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][1], wb, s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[tt][2], wb, s, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) acc[n][tt][r] = __builtin_fmaf(d, s[r], acc[n][tt][r]);
-            }
+            const bf16x8 wb = PlanarBlockOperand<QT, NP>(cw[n], sw[n], b, &d);
+            PlanarBlockProducts<TT>(xa, wb, d, acc[n]);
         }
     }
 #pragma unroll
@@ -1080,6 +1121,164 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
                 const int64_t t = tt * 16 + 4 * g + r;
                 if (t < T) out[t * stride] = acc[n][tt][r] + bias;
             }
+        }
+    }
+}
+
+// GemmPlanarStream: GemmPlanar's products, in its order, by workgroups that
+// stay on one K range.  The range's x planes go to LDS once; then each wave
+// streams steps (PT 16-row tiles of one segment) gw, gw + S, gw + 2S, ...
+// (gw: the wave among the range's S = 4 wgs waves), computing one step
+// while the codes and scales of the next D are in flight.  Weight loads
+// are buffer loads against the segment's bytes; a tile past the segment's
+// last, or a step past the launch's last, has an empty range and reads
+// zeros without a memory access.  a.g0 / a.row_groups count steps here.
+// Needs each segment's planar bytes below 2^31 and T x a partial row (or
+// T x O) below 2^30 bytes (the offsets are 32-bit); no bias (partial sums get theirs in
+// the reduction; a direct output with a bias runs GemmPlanar).
+// A segment's field (selects: the arguments are not indexed dynamically).
+template <typename V>
+__device__ inline V Seg3(int seg, V v0, V v1, V v2) {
+    return seg == 2 ? v2 : (seg == 1 ? v1 : v0);
+}
+
+template <int QT, int NP, int PT>
+struct PlanarStep {
+    static constexpr int kCodeVecs = QT == MLK_Q8_0 ? NP : NP / 2;
+    u32x4 cw[PT][kCodeVecs];
+    u32x4 sw[PT][NP / 4];
+};
+
+template <int QT, int TT, int NP, int PT, int D>
+__global__ __launch_bounds__(kSkThreads) void GemmPlanarStream(const uint32_t* __restrict__ planes,
+                                                               SkinnyArgs a, int64_t T, int64_t K,
+                                                               float* __restrict__ partial,
+                                                               int wgs) {
+    using Step = PlanarStep<QT, NP, PT>;
+    constexpr int kCodeVecs = Step::kCodeVecs;
+    __shared__ __align__(16) uint32_t xs[PlanarX<TT, NP>::kWords];
+    const int sp = static_cast<int>(blockIdx.x) / wgs;
+    const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    const int lane = threadIdx.x % kWave;
+    const int i16 = lane & 15, g = lane >> 4;
+    const int waves = 4 * wgs;
+    const int first = (static_cast<int>(blockIdx.x) % wgs) * 4 + wave;
+    const uint32_t code_tile = static_cast<uint32_t>(QT == MLK_Q8_0 ? 16 * K : 8 * K);
+    const uint32_t code_lane = static_cast<uint32_t>(sp * kCodeVecs * 1024 + lane * 16);
+    const uint32_t scale_lane = static_cast<uint32_t>(sp * (NP / 4) * 256 + i16 * 16);
+
+    // the segment of step s, and its first tile
+    auto locate = [&](int s, int* seg, int64_t* tile0) {
+        *seg = (a.n_seg > 2 && s >= a.g0[2]) ? 2 : ((a.n_seg > 1 && s >= a.g0[1]) ? 1 : 0);
+        *tile0 = static_cast<int64_t>(s - Seg3(*seg, 0, a.g0[1], a.g0[2])) * PT;
+    };
+    auto load = [&](int s, Step& st) {
+        int seg;
+        int64_t tile0;
+        locate(s, &seg, &tile0);
+        const int64_t tiles = (Seg3(seg, a.rows[0], a.rows[1], a.rows[2]) + 15) / 16;
+        const uint32_t bytes = static_cast<uint32_t>(tiles * (code_tile + K));
+#pragma unroll
+        for (int n = 0; n < PT; ++n) {
+            const bool live = s < a.row_groups && tile0 + n < tiles;
+            const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t*>(Seg3(seg, a.w[0], a.w[1], a.w[2])), 0, live ? bytes : 0u, 0x00020000);
+            const uint32_t tile = static_cast<uint32_t>(live ? tile0 + n : 0);
+            const uint32_t c = tile * code_tile + code_lane;
+            const uint32_t sc = static_cast<uint32_t>(tiles) * code_tile +
+                                tile * static_cast<uint32_t>(K) + scale_lane;
+#pragma unroll
+            for (int v = 0; v < kCodeVecs; ++v) {
+                st.cw[n][v] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, c + 1024 * v, 0, 2));
+            }
+#pragma unroll
+            for (int v = 0; v < NP / 4; ++v) {
+                st.sw[n][v] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, sc + 256 * v, 0, 0));
+            }
+        }
+    };
+
+    // x loads first, then the first step's weights; the x planes stored to
+    // LDS; then the other steps of the ring
+    Step ring[D];
+    {
+        PlanarX<TT, NP> xv;
+        xv.Load(planes, sp, T);
+        load(first, ring[0]);
+        xv.Store(xs);
+    }
+#pragma unroll
+    for (int d = 1; d < D; ++d) load(first + d * waves, ring[d]);
+    __syncthreads();
+
+    // the output: this range's partial rows, or y; buffer stores, so rows
+    // t >= T fall outside the range and are dropped (as are rows past a
+    // segment's last, sent past it)
+    const int64_t stride = partial != nullptr ? a.cols : a.rows[0];
+    float* const out_base = partial != nullptr ? partial + sp * T * a.cols : a.y;
+    const __amdgpu_buffer_rsrc_t out_r = __builtin_amdgcn_make_buffer_rsrc(
+        out_base, 0, static_cast<uint32_t>(T * stride * 4), 0x00020000);
+
+    // Every path through a step issues the slot's next loads, and the loop
+    // exits only at its head: the memory counter then holds the same loads on
+    // every path into the head, so each wait there is for one step's loads.
+    for (int s0 = first; s0 < a.row_groups; s0 += D * waves) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            const int s = s0 + d * waves;
+            if (s < a.row_groups) {
+                f32x4 acc[PT][TT];
+#pragma unroll
+                for (int n = 0; n < PT; ++n) {
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt) acc[n][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+                // the x reads stay in the step (an opaque offset): hoisted
+                // out of the loop, all blocks' pieces would take 192 registers
+                int lo = PlanarX<TT, NP>::LaneOffset(i16, g);
+                asm volatile("" : "+v"(lo));
+#pragma unroll
+                for (int b = 0; b < 2 * NP; ++b) {
+                    bf16x8 xa[TT][3];
+                    PlanarX<TT, NP>::Read(xs, lo, b, xa);
+#pragma unroll
+                    for (int n = 0; n < PT; ++n) {
+                        float dd;
+                        const bf16x8 wb =
+                            PlanarBlockOperand<QT, NP>(ring[d].cw[n], ring[d].sw[n], b, &dd);
+                        PlanarBlockProducts<TT>(xa, wb, dd, acc[n]);
+                    }
+                }
+                int seg;
+                int64_t tile0;
+                locate(s, &seg, &tile0);
+                const int64_t O = Seg3(seg, a.rows[0], a.rows[1], a.rows[2]);
+                const int64_t col0 = Seg3(seg, a.col0[0], a.col0[1], a.col0[2]);
+#pragma unroll
+                for (int n = 0; n < PT; ++n) {
+                    const int64_t row = 16 * (tile0 + n) + i16;
+                    const uint32_t o0 = static_cast<uint32_t>((col0 + row) * 4);
+#pragma unroll
+                    for (int tt = 0; tt < TT; ++tt) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int64_t t = tt * 16 + 4 * g + r;
+                            const uint32_t off =
+                                row < O ? o0 + static_cast<uint32_t>(t * stride * 4) : 0x7FFFFFF0u;
+                            // (__float_as_uint: this compiler's __builtin_bit_cast
+                            // of a vector element reads element 0)
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[n][tt][r]),
+                                                                  out_r, off, 0, 0);
+                        }
+                    }
+                }
+            }
+            // then the slot's next step (after the last use of the slot, so
+            // the new values take the same registers: no copies at the loop's
+            // back edge, which would wait for these loads)
+            load(s + D * waves, ring[d]);
         }
     }
 }
@@ -1543,6 +1742,7 @@ namespace {
 // fused launch's reduction applies its epilogue), then the x planes.
 struct PlanarPlan {
     int tt = 1, np = 4, splits = 1, pt = 2;
+    int wgs = 0;  // > 0: GemmPlanarStream, with this many workgroups per K range
     int64_t partial_bytes = 0, plane_bytes = 0;
     int64_t Bytes() const { return partial_bytes + plane_bytes; }
 };
@@ -1574,10 +1774,35 @@ void LaunchPlanarPt(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_
     }
 }
 
+// GemmPlanarStream's shape: steps of kStreamPt tiles, a ring of kStreamD
+// steps per wave, about kStreamWgsPerCu workgroups per compute unit.
+constexpr int kStreamPt = 1;
+constexpr int kStreamD = 3;
+constexpr int kStreamWgsPerCu = 2;
+constexpr int kStreamMinWgsPerCu = 4;
+
+template <int QT>
+void LaunchPlanarStream(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t* planes,
+                        const SkinnyArgs& a, int64_t T, int64_t K, float* partial) {
+    constexpr int P = kStreamPt, D = kStreamD;
+    if (p.tt == 1 && p.np == 8) {
+        hipLaunchKernelGGL((GemmPlanarStream<QT, 1, 8, P, D>), grid, dim3(kSkThreads), 0, s,
+                           planes, a, T, K, partial, p.wgs);
+    } else if (p.tt == 1) {
+        hipLaunchKernelGGL((GemmPlanarStream<QT, 1, 4, P, D>), grid, dim3(kSkThreads), 0, s,
+                           planes, a, T, K, partial, p.wgs);
+    } else {
+        hipLaunchKernelGGL((GemmPlanarStream<QT, 2, 4, P, D>), grid, dim3(kSkThreads), 0, s,
+                           planes, a, T, K, partial, p.wgs);
+    }
+}
+
 template <int QT>
 void LaunchPlanarT(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t* planes,
                    const SkinnyArgs& a, int64_t T, int64_t K, float* partial) {
-    if (p.pt == 1) {
+    if (p.wgs > 0) {
+        LaunchPlanarStream<QT>(p, grid, s, planes, a, T, K, partial);
+    } else if (p.pt == 1) {
         LaunchPlanarPt<QT, 1>(p, grid, s, planes, a, T, K, partial);
     } else {
         LaunchPlanarPt<QT, 2>(p, grid, s, planes, a, T, K, partial);
@@ -1605,18 +1830,45 @@ mlk_status RunPlanar(int qt, const float* x, const uint32_t* planes_in, SkinnyAr
         for (int i = 0; i < a.n_seg; ++i) g += (a.rows[i] + 64 * pt - 1) / (64 * pt);
         return g;
     };
-    if (count_groups(2) * p.splits < 2 * ComputeUnits()) p.pt = 1;
-    int64_t groups = 0;
+    // The streaming kernel where GemmPlanar's grid would take more than
+    // kStreamMinWgsPerCu workgroups per compute unit (the 8B gate/up with
+    // 16 tokens, 7: measured 34.3 -> 27.6 us; at 1-4 per unit GemmPlanar's
+    // one round of loads per workgroup measured as fast or faster: the 8B
+    // q/k/v 11.6 vs 12.7 us, wo 9 vs 11, down 20 vs 20.4), and where its
+    // offsets fit 31 bits, unless y takes a bias.
+    const int64_t out_row = p.partial_bytes > 0 ? cols : a.rows[0];
+    bool stream = count_groups(2) * p.splits > kStreamMinWgsPerCu * ComputeUnits() &&
+                  !(p.partial_bytes == 0 && a.bias != nullptr) &&
+                  T * out_row * 4 < (int64_t{1} << 30);
     for (int i = 0; i < a.n_seg; ++i) {
-        a.g0[i] = static_cast<int>(groups);
-        groups += (a.rows[i] + 64 * p.pt - 1) / (64 * p.pt);
+        const int64_t tiles = (a.rows[i] + 15) / 16;
+        stream = stream && tiles * ((qt == MLK_Q8_0 ? 16 : 8) * K + K) < (int64_t{1} << 31);
+    }
+    int64_t groups = 0;
+    if (stream) {
+        // steps of kStreamPt tiles per segment; per K range as many
+        // workgroups as give each wave the same count of steps, within
+        // kStreamWgsPerCu per compute unit over all ranges
+        for (int i = 0; i < a.n_seg; ++i) {
+            a.g0[i] = static_cast<int>(groups);
+            groups += ((a.rows[i] + 15) / 16 + kStreamPt - 1) / kStreamPt;
+        }
+        const int64_t cap = std::max<int64_t>(1, kStreamWgsPerCu * ComputeUnits() / p.splits);
+        const int64_t per_wave = std::max<int64_t>(1, (groups + 4 * cap - 1) / (4 * cap));
+        p.wgs = static_cast<int>((groups + 4 * per_wave - 1) / (4 * per_wave));
+    } else {
+        if (count_groups(2) * p.splits < 2 * ComputeUnits()) p.pt = 1;
+        for (int i = 0; i < a.n_seg; ++i) {
+            a.g0[i] = static_cast<int>(groups);
+            groups += (a.rows[i] + 64 * p.pt - 1) / (64 * p.pt);
+        }
     }
     if (workspace == nullptr || !Aligned(workspace, 16) ||
         static_cast<int64_t>(workspace_bytes) < p.Bytes()) {
         return Fail(MLK_ERR_INVALID, "linear (planar): workspace of %lld bytes needed",
                     static_cast<long long>(p.Bytes()));
     }
-    if (groups * p.splits > 0x7FFFFFFF) {
+    if ((p.wgs > 0 ? p.wgs : groups) * p.splits > 0x7FFFFFFF) {
         return Fail(MLK_ERR_INVALID, "linear (planar): %lld output rows exceed one launch",
                     static_cast<long long>(cols));
     }
@@ -1636,7 +1888,7 @@ mlk_status RunPlanar(int qt, const float* x, const uint32_t* planes_in, SkinnyAr
         if (st != MLK_OK) return st;
         planes = own;
     }
-    const dim3 grid(static_cast<unsigned>(groups * p.splits));
+    const dim3 grid(static_cast<unsigned>((p.wgs > 0 ? p.wgs : groups) * p.splits));
     if (qt == MLK_Q8_0) {
         LaunchPlanarT<MLK_Q8_0>(p, grid, s, planes, a, T, K, *partial);
     } else {

@@ -174,6 +174,44 @@ def test_planar_one_row_equals_block_layout_bound(mlk, orc, qt):
         assert_dot_close(d_y.download(), ex, s, K, f"{qt} {O}x{K} blocks")
 
 
+STREAM_SHAPES = [  # (out, in, rows, chunk): one call over `out` rows takes more workgroups
+    # than the one-shot kernel spreads well (the 8B gate and up as one matrix,
+    # 16 tokens, a ragged 5, two token tiles with 24), or one K range with
+    # direct output (131088 rows, no split-K partials); `chunk` rows per call
+    # stay within the one-shot kernel
+    (28672, 4096, 16, 7168), (28672, 4096, 5, 7168), (28672, 4096, 24, 7168),
+    (131088, 512, 5, 16384)]
+
+
+@pytest.mark.parametrize("qt", QT)
+@pytest.mark.parametrize("shape", STREAM_SHAPES, ids=["gateup_16", "gateup_5", "gateup_24",
+                                                      "direct_5"])
+def test_planar_stream_equals_one_shot(mlk, orc, qt, shape):
+    """Many row tiles per K range: the streaming launch (each workgroup's
+    waves walk the row tiles of one K range, the next tiles' loads in
+    flight) forms the same products in the same order as the one-shot
+    launch (one workgroup per row group and K range), so one call over all
+    rows equals calls over row chunks bit for bit.  The whole result is
+    also held to the bound of the exact sums, on a sample of rows."""
+    O, K, T, chunk = shape
+    rng = np.random.default_rng(O + K + T)
+    w = normal(rng, (O, K), 0.02)
+    x = normal(rng, (T, K))
+    blocks = orc.quantize(qt, w)
+    got = run_planar(mlk, qt, x, to_planar(mlk, qt, blocks, O, K), O)
+    per_row = blocks.size // O
+    parts = []
+    for r0 in range(0, O, chunk):
+        n = min(chunk, O - r0)
+        sub = blocks.reshape(O, per_row)[r0:r0 + n]
+        parts.append(run_planar(mlk, qt, x, to_planar(mlk, qt, sub, n, K), n))
+    np.testing.assert_array_equal(got, np.concatenate(parts, axis=1))
+    rows = np.unique(np.r_[0:64, O // 2 - 32:O // 2 + 32, O - 64:O,
+                           rng.choice(O, 256, replace=False)])
+    ex, s = dot_exact(x, orc.dequantize(qt, blocks.reshape(O, per_row)[rows], len(rows), K))
+    assert_dot_close(got[:, rows], ex, s, K, f"{qt} {shape}")
+
+
 def test_planar_rejects(mlk, orc):
     """Q4_1 and in_features that are not a multiple of 256 have no planar
     layout; the few-row path needs its workspace."""
