@@ -509,8 +509,12 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
     // per row.  Rows past T read row 0 and W rows past O their tile's row 0,
     // unmasked: the outputs they meet are never stored (K is a multiple of
     // 256, so no stage reads past K).
-    float4 xv[kXN];
-    auto load_x = [&](int64_t k0) {
+    // Stages are requested two ahead: registers A / B alternate, so the
+    // stage stored at the end of stage s was requested at the start of
+    // stage s - 1 and is in registers by then (requested one ahead, the
+    // scheduler moved its split next to its request and every stage waited
+    // out the load latency).
+    auto load_x = [&](int64_t k0, float4 (&xv)[kXN]) {
 #pragma unroll
         for (int i = 0; i < kXN; ++i) {
             const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
@@ -519,9 +523,8 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
             xv[i] = *reinterpret_cast<const float4*>(x + (r < T ? r * K + c : c));
         }
     };
-    WTile<WT> wt;
     // one stage into LDS buffer b: x pieces, W codes as bf16, scales
-    auto store = [&](int b) {
+    auto store = [&](int b, const float4 (&xv)[kXN], const WTile<WT>& wt) {
 #pragma unroll
         for (int i = 0; i < kXN; ++i) {
             const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
@@ -543,15 +546,15 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
         dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
         if (h == 0) sm.d[b][row] = HalfHw(wt.d & 0xFFFFu) * CodeScale<WT>();
     };
-    load_x(s0 * kBK);
-    wt.Load(w, O, K, row_bytes, n0, s0 * kBK);
-    store(0);
-    __syncthreads();
-    for (int64_t s = s0; s < s1; ++s) {
+    // stage s in LDS buffer (s - s0) & 1, stage s + 1 in registers `held`;
+    // stage s + 2 requested into `next` (past the last stage: the last again,
+    // never stored where it is read)
+    auto step = [&](int64_t s, const float4 (&held_x)[kXN], const WTile<WT>& held_w,
+                    float4 (&next_x)[kXN], WTile<WT>& next_w) {
         const int buf = static_cast<int>((s - s0) & 1);
-        const int64_t k_next = (s + 1 < s1 ? s + 1 : s) * kBK;
-        load_x(k_next);
-        wt.Load(w, O, K, row_bytes, n0, k_next);
+        const int64_t k2 = (s + 2 < s1 ? s + 2 : s1 - 1) * kBK;
+        load_x(k2, next_x);
+        next_w.Load(w, O, K, row_bytes, n0, k2);
         __builtin_amdgcn_sched_barrier(0);
         bf16x8g b[4];
         float dj[4];
@@ -577,8 +580,24 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
                 for (int r4 = 0; r4 < 4; ++r4) acc[i][j][r4] += dj[j] * S[r4];
             }
         }
-        store(buf ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        store(buf ^ 1, held_x, held_w);
         __syncthreads();
+    };
+    float4 xa[kXN], xb[kXN];
+    WTile<WT> wa, wb;
+    load_x(s0 * kBK, xa);
+    wa.Load(w, O, K, row_bytes, n0, s0 * kBK);
+    {
+        const int64_t k1 = (s0 + 1 < s1 ? s0 + 1 : s0) * kBK;
+        load_x(k1, xb);
+        wb.Load(w, O, K, row_bytes, n0, k1);
+    }
+    store(0, xa, wa);
+    __syncthreads();
+    for (int64_t s = s0; s < s1; s += 2) {
+        step(s, xb, wb, xa, wa);
+        if (s + 1 < s1) step(s + 1, xa, wa, xb, wb);
     }
 
     float* out = partial != nullptr ? partial + sp * T * O : y;
