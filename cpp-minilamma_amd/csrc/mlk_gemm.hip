@@ -1152,8 +1152,8 @@ __global__ __launch_bounds__(kSkThreads) void GemmPlanar(const uint32_t* __restr
 // are buffer loads against the segment's bytes; a tile past the segment's
 // last, or a step past the launch's last, has an empty range and reads
 // zeros without a memory access.  a.g0 / a.row_groups count steps here.
-// Needs each segment's planar bytes below 2^31 and T x a partial row (or
-// T x O) below 2^30 bytes (the offsets are 32-bit); no bias (partial sums get theirs in
+// Needs each segment's planar bytes below 2^31 and 16 TT x a partial row
+// (or x O) below 2^30 bytes (the offsets are 32-bit); no bias (partial sums get theirs in
 // the reduction; a direct output with a bias runs GemmPlanar).
 // A segment's field (selects: the arguments are not indexed dynamically).
 template <typename V>
@@ -1856,9 +1856,11 @@ mlk_status RunPlanar(int qt, const float* x, const uint32_t* planes_in, SkinnyAr
     // q/k/v 11.6 vs 12.7 us, wo 9 vs 11, down 20 vs 20.4), and where its
     // offsets fit 31 bits, unless y takes a bias.
     const int64_t out_row = p.partial_bytes > 0 ? cols : a.rows[0];
+    // (every token slot of the tiles, t < 16 tt, not only t < T: the stores
+    // of slots past T must land past the output's range, unwrapped)
     bool stream = count_groups(2) * p.splits > kStreamMinWgsPerCu * ComputeUnits() &&
                   !(p.partial_bytes == 0 && a.bias != nullptr) &&
-                  T * out_row * 4 < (int64_t{1} << 30);
+                  16 * p.tt * out_row * 4 < (int64_t{1} << 30);
     for (int i = 0; i < a.n_seg; ++i) {
         const int64_t tiles = (a.rows[i] + 15) / 16;
         stream = stream && tiles * ((qt == MLK_Q8_0 ? 16 : 8) * K + K) < (int64_t{1} << 31);
