@@ -355,12 +355,32 @@ def test_layer_planar_equals_op_by_op(mlk, fwd, wt, T, case):
     Their per-element arithmetic is the separate entries' (mlk_linear_planar
     per matrix, then the separate ops), so the layer equals that composition
     bit for bit: residual stream, cache rows and error flag."""
-    S = 1024
     cfg = dict(vocab=64, dim=512, hidden_dim=1536, layers=1, n_heads=8, n_kv_heads=2,
-               head_dim=64, max_seq=S, rope_type=1 if case == "neox" else 0, theta=10000.0,
+               head_dim=64, max_seq=1024, rope_type=1 if case == "neox" else 0, theta=10000.0,
                eps=1e-5)
+    layer_planar_vs_op_by_op(mlk, fwd, wt, T, case, cfg)
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+def test_layer_planar_equals_op_by_op_70b(mlk, fwd, wt):
+    """The same at Llama-3-70B's layer shape with 16 tokens, where the fused
+    launches take the streaming planar GEMM (more row groups than the
+    one-shot grid spreads well): q/k/v as three segments of one launch (RoPE
+    and the cache rows in its reduction), gate/up as two (SwiGLU), down with
+    its split-K partials (the residual add).  Separately, q, k and v each
+    take the one-shot kernel and gate, up and down the streaming one on a
+    single segment.  Equal bit for bit."""
+    cfg = dict(vocab=64, dim=8192, hidden_dim=28672, layers=1, n_heads=64, n_kv_heads=8,
+               head_dim=128, max_seq=1024, rope_type=0, theta=500000.0, eps=1e-5)
+    layer_planar_vs_op_by_op(mlk, fwd, wt, 16, "pos0", cfg)
+
+
+def layer_planar_vs_op_by_op(mlk, fwd, wt, T, case, cfg):
+    """One layer through forward_layer_batch on planar copies against the
+    separate entries on the same blocks (see the tests above)."""
+    S = cfg["max_seq"]
     model = O.forward_model(cfg, seed=13, weight_type=wt, biases=True)
-    D, F, H, KV, hd = 512, 1536, 8, 2, 64
+    D, F, H, KV, hd = (cfg[k] for k in ("dim", "hidden_dim", "n_heads", "n_kv_heads", "head_dim"))
     QD, KD, pos = H * hd, KV * hd, 600
     lw = model["layers"][0]
     dm = fwd.DeviceModel(model, planar=True)
