@@ -1835,6 +1835,11 @@ void LaunchPlanarT(const PlanarPlan& p, dim3 grid, hipStream_t s, const uint32_t
 mlk_status RunPlanar(int qt, const float* x, const uint32_t* planes_in, SkinnyArgs& a, int64_t T,
                      int64_t K, bool partials, void* workspace, size_t workspace_bytes,
                      int* splits, float** partial, hipStream_t s) {
+    // a direct output is one [T, rows] matrix: several segments go through
+    // partial sums (the fused launches' reductions place each segment)
+    if (a.n_seg > 1 && !partials) {
+        return Fail(MLK_ERR_INVALID, "linear (planar): several segments need partial sums");
+    }
     int64_t cols = 0;
     for (int i = 0; i < a.n_seg; ++i) {
         if (!Aligned(a.w[i], 16)) return Fail(MLK_ERR_INVALID, "linear (planar): weights not 16-byte aligned");
