@@ -43,10 +43,12 @@
 // matrix work: 8B prefill of 4096 tokens 1339 -> 1107 us, 64 decode tokens
 // 100 -> 79 us.  v_mfma_f32_16x16x32_bf16 takes 32 dims (scores)
 // or the tile's 32 positions (values) per instruction in half the cycles of
-// the fp32 instruction's 4.  Scores keep the 6 piece products above
-// 2^-21 relative (|dropped| < 2^-20 |q_d k_d|, 16 u: within the gamma_{hd+1}
-// score bound with the fp32 sums); values keep all 9, so their products are
-// exact and only fp32 summation rounds.  The value MFMA's k index is the
+// the fp32 instruction's 4.  Scores and values each keep the 6 piece
+// products above 2^-21 relative: with pieces below 2^-7 and 2^-14 of the
+// value, the dropped three are below 2^-20 |a b| (16 u) a product; for
+// scores within the gamma_{hd+1} score bound with the fp32 sums, for values
+// 16 u of sum_j p_j |v_jd| on top of the fp32 sums' (n + 6) u (the
+// (n + 22) u the tests hold the tiles to).  The value MFMA's k index is the
 // lane's own 8 probabilities: slot 8 kq + j is position 16 (j / 4) + 4 kq +
 // j % 4 of the tile, the order V^T is staged in.
 #include "mlk_attention.h"
@@ -410,10 +412,7 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
                     for (int p = 0; p < 3; ++p) {
                         vp[p] = *reinterpret_cast<const bf16x8*>(vrow + p * HD * kBfVLd);
                     }
-                    // all 9 piece products (exact), smallest first
-                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[2], pp[2], acc[c], 0, 0, 0);
-                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[2], pp[1], acc[c], 0, 0, 0);
-                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[1], pp[2], acc[c], 0, 0, 0);
+                    // the 6 piece products above 2^-21 relative, smallest first
                     acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[2], pp[0], acc[c], 0, 0, 0);
                     acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[0], pp[2], acc[c], 0, 0, 0);
                     acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vp[1], pp[1], acc[c], 0, 0, 0);

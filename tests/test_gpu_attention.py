@@ -1,13 +1,17 @@
 """GPU parity of decode attention and the KV cache write, through the C ABI.
 
 The bar (attention_bound): for output element (h, d),
-    |got - exact| <= (2 * D + (n + 6) * u) * sum_j p_j |v_jd|,
+    |got - exact| <= (2 * D + (n + 6 + e) * u) * sum_j p_j |v_jd|,
 with exact the float64 value, n = pos + 1 attended positions, u = 2^-24,
 and D = gamma_{hd+1} * scale * max_j sum_d |q_d k_jd| the rounding bound of
 one fp32 score: a score error moves p_j by at most 2D relatively, the exp,
 the sum of n terms and the final division add (n + 6) u.  Any fp32
-evaluation order meets it, the reference's serial loops included (the
-oracle is held to the same bound).  On the reference's own test inputs its
+evaluation order meets it with e = 0, the reference's serial loops included
+(the oracle is held to the same bound).  The head_dim-128 tiles (prefill,
+and decode batches of 5 or more tokens) form each p_j v_jd from the 6 bf16
+piece products above 2^-21 relative (pieces below 2^-7 and 2^-14 of the
+value); the three dropped are below 2^-20 = 16 u of it, so those cases are
+held to e = 16 (`pieces`).  On the reference's own test inputs its
 tolerance, 2e-5 against float64 (test/cuda_attention_test.cc:108-109), is
 checked too.  At long contexts the n u term is loose, so structured inputs
 (equal keys with position-coded values; one dominant key in a chosen chunk)
@@ -54,8 +58,8 @@ def attention_exact(q, kc, vc, layer, pos):
     return out, pav, dmax, n
 
 
-def assert_attention_close(got, exact, pav, dmax, n, what):
-    bound = (2 * dmax + (n + 6) * U) * pav + 1e-30
+def assert_attention_close(got, exact, pav, dmax, n, what, pieces=False):
+    bound = (2 * dmax + (n + 6 + (16 if pieces else 0)) * U) * pav + 1e-30
     err = np.abs(np.asarray(got, np.float64) - exact)
     bad = err > bound
     assert np.isfinite(got).all(), f"{what}: non-finite output"
@@ -152,12 +156,12 @@ def test_attention_many_tokens_8b_decode(mlk):
     got = cache.attend(q, 0, pos)
     for t in range(64):
         ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, int(pos[t]))
-        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t} pos {pos[t]}")
+        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t} pos {pos[t]}", pieces=True)
     # consecutive positions pos0 .. pos0 + T - 1 (no positions array)
     got2 = cache.attend(q[:5], 0, None, pos0=8000)
     for t in range(5):
         ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, 8000 + t)
-        assert_attention_close(got2[t], ex, pav, dmax, n, f"pos0 token {t}")
+        assert_attention_close(got2[t], ex, pav, dmax, n, f"pos0 token {t}", pieces=True)
 
 
 @pytest.mark.parametrize("S", [64, 700, 8192])
@@ -260,7 +264,8 @@ def test_attention_shared_tiles_any_positions(mlk, H, KV, hd, T, S):
     got = cache.attend(q, 1, pos)
     for t in range(T):
         ex, pav, dmax, n = attention_exact(q[t], kc, vc, 1, int(pos[t]))
-        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t} pos {pos[t]}")
+        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t} pos {pos[t]}",
+                               pieces=hd == 128)
 
 
 def test_attention_shared_tiles_all_invalid_one_chunk(mlk):
@@ -409,8 +414,9 @@ def prefill_exact(q, kc, vc, layer, pos0):
     return out, pav, dmax, pos + 1
 
 
-def assert_prefill_close(got, exact, pav, dmax, n, what):
-    bound = (2 * dmax[:, :, None] + (n[:, None, None] + 6) * U) * pav + 1e-30
+def assert_prefill_close(got, exact, pav, dmax, n, what, pieces=False):
+    extra = 16 if pieces else 0
+    bound = (2 * dmax[:, :, None] + (n[:, None, None] + 6 + extra) * U) * pav + 1e-30
     err = np.abs(np.asarray(got, np.float64) - exact)
     assert np.isfinite(got).all(), f"{what}: non-finite output"
     bad = err > bound
@@ -460,7 +466,8 @@ def test_attention_prefill_shapes(mlk, H, KV, hd, T, pos0):
     q = rng.standard_normal((T, H, hd)).astype(np.float32)
     got = run_prefill(mlk, cache, q, 1, pos0)
     ex, pav, dmax, n = prefill_exact(q, kc, vc, 1, pos0)
-    assert_prefill_close(got, ex, pav, dmax, n, f"prefill H{H} KV{KV} hd{hd} T{T} pos0 {pos0}")
+    assert_prefill_close(got, ex, pav, dmax, n, f"prefill H{H} KV{KV} hd{hd} T{T} pos0 {pos0}",
+                         pieces=hd == 128)
     np.testing.assert_array_equal(run_prefill(mlk, cache, q, 1, pos0, via_decode=True), got)
 
 
@@ -502,7 +509,7 @@ def test_attention_prefill_after_kv_write(mlk, orc):
         q = rng.standard_normal((T, H, hd)).astype(np.float32)
         got = run_prefill(mlk, cache, q, 1, pos0)
         ex, pav, dmax, n = prefill_exact(q, kc, vc, 1, pos0)
-        assert_prefill_close(got, ex, pav, dmax, n, f"chunk at {pos0}")
+        assert_prefill_close(got, ex, pav, dmax, n, f"chunk at {pos0}", pieces=True)
         sample = [0, T // 2, T - 1]
         ora = orc.attention(q[sample], kc, vc, 1, [pos0 + t for t in sample])
         for i, t in enumerate(sample):
