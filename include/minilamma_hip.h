@@ -256,7 +256,10 @@ int64_t mlk_attention_workspace_bytes(int64_t n_tokens, int32_t n_heads, int32_t
  * mlk_attention_workspace_bytes() is nonzero, `workspace` must hold that many
  * bytes (chunk partials); out must not alias q.  Sums are fp32 in the
  * kernel's order (the reference's tolerance: 2e-5 against float64,
- * test/cuda_attention_test.cc:108-109).  With positions == NULL, 16 or more
+ * test/cuda_attention_test.cc:108-109); with head_dim 128, batches of 5 or
+ * more tokens and the prefill kernel form each q.k and p.v product from the
+ * six bf16 piece products above 2^-21 relative, so each product is within
+ * 2^-20 of its exact value (fp32 rounds at 2^-24).  With positions == NULL, 16 or more
  * tokens, head_dim 64 or 128 and 16-byte aligned q rows, out and caches, the
  * call runs mlk_attention_prefill_f32's kernel and uses no workspace.
  * Replaces CudaAttentionDevice (include/cuda_attention.h:12-13;
