@@ -844,10 +844,10 @@ PIECES_PEAK_TFLOPS = MFMA_BF16_PEAK_TFLOPS / 3
 
 def attention_peak(hd):
     """(peak TFLOP/s of useful MACs, basis) of the tile attention: at
-    head_dim 128 the scores take 6 and the values 9 bf16 piece products per
-    useful MAC (7.5 on average), at 64 the fp32 instruction."""
+    head_dim 128 the scores and the values each take 6 bf16 piece products
+    per useful MAC, at 64 the fp32 instruction."""
     if hd == 128:
-        return MFMA_BF16_PEAK_TFLOPS / 7.5, "bf16 MFMA / 7.5 (piece products)"
+        return MFMA_BF16_PEAK_TFLOPS / 6, "bf16 MFMA / 6 (piece products)"
     return MFMA_FP32_PEAK_TFLOPS, "fp32 MFMA"
 
 
@@ -1570,7 +1570,7 @@ def kernel_summary(out_md, title, bench_json, kt_dir, fetch_dir=None, write_dir=
            "launches -- for --linear, around one replay of a HIP graph holding each "
            "projection's calls, so the figure is kernel time, not Python dispatch; HBM-bound "
            "cases on rotating cold copies, against 8 TB/s; "
-           "matrix-core cases against the peak of the instruction they run: 157.3 TFLOP/s fp32 MFMA, or for bf16 piece products the 2.5 PFLOP/s bf16 peak over the bf16 MACs per useful MAC, 3 in the GEMM and 7.5 in the attention):", "",
+           "matrix-core cases against the peak of the instruction they run: 157.3 TFLOP/s fp32 MFMA, or for bf16 piece products the 2.5 PFLOP/s bf16 peak over the bf16 MACs per useful MAC, 3 in the GEMM and 6 in the attention):", "",
            "| case | us | throughput | fraction of peak |", "|---|---|---|---|"]
 
     def rate(node, prefix=""):
