@@ -516,6 +516,42 @@ def test_attention_prefill_after_kv_write(mlk, orc):
             assert_attention_close(ora[i], ex[t], pav[t], float(dmax[t].max()), n[t], "oracle")
 
 
+def full_significand(rng, shape):
+    """fp32 values with every significand bit set (1.99999988 * 2^e, random
+    sign, e in [-2, 2]): their middle and low bf16 pieces are as large as the
+    split allows, so each value product the head_dim-128 tiles drop is close
+    to its 2^-20 bound."""
+    e = rng.integers(-2, 3, size=shape)
+    sign = np.where(rng.random(shape) < 0.5, -1.0, 1.0)
+    return (sign * np.ldexp(2.0 - 2.0 ** -23, e)).astype(np.float32)
+
+
+def test_attention_tiles_dropped_pieces_within_bound(mlk):
+    """The tiles' six-of-nine value products against the bound they are held
+    to, (n + 22) u (16 u a product for the three dropped): V with every
+    significand bit set and keys spread enough that the probabilities carry
+    full significands too, through the prefill kernel (a 64-token chunk after
+    a 40-token prefix) and the shared decode tiles (16 tokens at scattered
+    positions)."""
+    rng = np.random.default_rng(21)
+    H, KV, hd, S = 8, 2, 128, 160
+    kc = (rng.standard_normal((2, S, KV, hd)) * 0.3).astype(np.float32)
+    vc = full_significand(rng, (2, S, KV, hd))
+    cache = Cache(mlk, kc, vc)
+    T, pos0 = 64, 40
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    got = run_prefill(mlk, cache, q, 1, pos0)
+    ex, pav, dmax, n = prefill_exact(q, kc, vc, 1, pos0)
+    assert_prefill_close(got, ex, pav, dmax, n, "prefill, full-significand values", pieces=True)
+    pos = rng.choice(S, 16, replace=False).astype(np.int32)
+    qd = rng.standard_normal((16, H, hd)).astype(np.float32)
+    gotd = cache.attend(qd, 1, pos)
+    for t in range(16):
+        ex, pav, dmax, n = attention_exact(qd[t], kc, vc, 1, int(pos[t]))
+        assert_attention_close(gotd[t], ex, pav, dmax, n, f"decode tiles token {t} pos {pos[t]}",
+                               pieces=True)
+
+
 def test_attention_prefill_rejects(mlk):
     kc = mlk.DeviceBuffer.empty((2, 64, 2, 128))
     vc = mlk.DeviceBuffer.empty((2, 64, 2, 128))
