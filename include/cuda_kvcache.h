@@ -1,7 +1,7 @@
 // cuda_kvcache.h -- the device KV cache, on MI355X.
 //
 // Same declarations and member layout as the reference's device KV cache
-// (include/cuda_kvcache.h:1-60 of the reference tree; src/cuda_kvcache.cc):
+// (include/cuda_kvcache.h:1-57 of the reference tree; src/cuda_kvcache.cc):
 //   keys:   [n_layers, max_seq_len, n_kv_heads, head_dim] fp32
 //   values: [n_layers, max_seq_len, n_kv_heads, head_dim] fp32
 // Validation and messages follow the reference.  Differences a caller can

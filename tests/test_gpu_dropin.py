@@ -6,8 +6,8 @@ against libminilamma_ops.so + libminilamma_hip.so in place of the
 reference's device layer (tests/dropin/Makefile, built in the container that
 holds the reference tree; the GPU box runs the prebuilt programs).  The
 cases and their modes are the reference's CTest list
-(tests/CMakeLists.txt:14-31), run from a directory that holds the tiny model
-where its tests look for it (models/tiny, cuda_test_support.h:44).  Each
+(tests/CMakeLists.txt:14-29, 46), run from a directory that holds the tiny
+model where its tests look for it (models/tiny, tests/cuda_test_support.h:49).  Each
 program prints "PASS <mode> CUDA" per case and exits 0 only if every check
 passed; the forward cases compare the device logits with the CPU forward
 pass token by token and check the transfer counters: no host-to-device
