@@ -516,6 +516,23 @@ def test_attention_prefill_after_kv_write(mlk, orc):
             assert_attention_close(ora[i], ex[t], pav[t], float(dmax[t].max()), n[t], "oracle")
 
 
+def test_attention_prefill_bench_shape(mlk):
+    """The bench's prefill case at its full size: 8B heads (32 / 8, head_dim
+    128), T = 4096 tokens at positions 0..4095 in one launch (256 token blocks
+    x 8 KV heads), N(0, 1) queries and cache so the softmax is far from
+    uniform; tokens sampled across the blocks (first and last of a block, the
+    two ends of the chunk) against float64."""
+    rng = np.random.default_rng(31)
+    H, KV, hd, T = 32, 8, 128, 4096
+    kc, vc = random_cache(rng, 1, T, KV, hd)
+    cache = Cache(mlk, kc, vc)
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    got = run_prefill(mlk, cache, q, 0, 0)
+    for t in (0, 1, 15, 16, 17, 255, 1000, 2047, 2048, 3071, 4094, 4095):
+        ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, t)
+        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t}", pieces=True)
+
+
 def full_significand(rng, shape):
     """fp32 values with every significand bit set (1.99999988 * 2^e, random
     sign, e in [-2, 2]): their middle and low bf16 pieces are as large as the
