@@ -4,8 +4,10 @@
 // loop of ForwardBatch (:473-488) layer by layer.
 //
 // Per layer, on one stream (x [T, dim] is the residual stream, in place;
-// for 1 and for 8..32 tokens with quantized weights q/k/v are one launch,
-// gate/up carry the SwiGLU and the down projection adds into x, see below):
+// for 1 and for 2..32 tokens with quantized weights q/k/v are one launch,
+// gate/up carry the SwiGLU and the down projection adds into x; for many
+// tokens over Q8_0 / Q4_0 blocks gate/up carry the SwiGLU and wo and down
+// add into x, see below):
 //   h = RmsNorm(x, attention_norm)                    mlk_rmsnorm_f32
 //   q, k, v = h W^T (+ bias)                          mlk_linear_* (GEMM from 8 rows)
 //   RoPE(q, k) at each token's position               mlk_rope_f32
@@ -302,6 +304,17 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
                                SkinnyFusedApplies(w->w_gate.type, T, D));
     const bool downm = downp || (mid && w->w_down.type != kLinearF32 &&
                                  SkinnyFusedApplies(w->w_down.type, T, F));
+    // Many tokens (128-row tiles, K in one pass): the same groups' epilogues
+    // in the GEMM itself, gate/up as one launch with SwiGLU, wo and down
+    // adding into x (the plain GEMM's sums, so the separate kernels' values)
+    const bool wo_add = !wop && !wo1p && TiledFusedApplies(w->wo.type, T, QD, D, kStreamAdd) &&
+                        Aligned(w->wo.data, 2);
+    const bool ffn_tiled = !ffn1 && !ffnp && !ffnm && w->w_gate.type == w->w_up.type &&
+                           TiledFusedApplies(w->w_gate.type, T, D, F, kStreamSwiGlu) &&
+                           Aligned(w->w_gate.data, 2) && Aligned(w->w_up.data, 2);
+    const bool down_tiled = !down1 && !downp && !downm &&
+                            TiledFusedApplies(w->w_down.type, T, F, D, kStreamAdd) &&
+                            Aligned(w->w_down.data, 2);
     // The fused q/k/v launches also rotate q and k (normal-layout pairs) and
     // write k and v into the cache rows, in place of mlk_rope_f32 and
     // mlk_kv_write_f32; the NeoX layout keeps the separate launches.
@@ -402,10 +415,17 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
             sa.seg[0] = PlanarSeg(w->wo, proj, D);
             sa.n_seg = 1;
             MLK_TRY(LinearRowPlanar(w->wo.type, a, QD, sa, kStreamPlain, hs));
+        } else if (wo_add) {
+            StreamArgs sa{};
+            sa.seg[0] = Seg(w->wo, x, D, x);
+            sa.n_seg = 1;
+            MLK_TRY(LinearTiledFused(w->wo.type, a, T, QD, sa, kStreamAdd, hs));
         } else {
             MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
         }
-        if (ffnp && planes != nullptr && NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
+        if (wo_add) {  // x already holds x + proj
+            MLK_TRY(mlk_rmsnorm_f32(x, w->ffn_norm, h, T, D, eps, stream));
+        } else if (ffnp && planes != nullptr && NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
             MLK_TRY(AddRmsNormPlanes(x, proj, w->ffn_norm, h, planes, T, D, eps, hs));
             h_planes = planes;
         } else if (!ffn_fold) {
@@ -442,6 +462,12 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[1] = Seg(w->w_up, gate, F);
         a.n_seg = 2;
         MLK_TRY(LinearSkinnyFused(w->w_gate.type, h, T, D, a, kStreamSwiGlu, lin_ws, lin_b, hs));
+    } else if (ffn_tiled) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->w_gate, gate, F);
+        a.seg[1] = Seg(w->w_up, gate, F);
+        a.n_seg = 2;
+        MLK_TRY(LinearTiledFused(w->w_gate.type, h, T, D, a, kStreamSwiGlu, hs));
     } else {
         MLK_TRY(Linear(w->w_gate, h, gate, T, D, F, lin_ws, lin_b, stream));
         MLK_TRY(Linear(w->w_up, h, up, T, D, F, lin_ws, lin_b, stream));
@@ -465,6 +491,11 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[0] = Seg(w->w_down, x, D, x);
         a.n_seg = 1;
         MLK_TRY(LinearSkinnyFused(w->w_down.type, gate, T, F, a, kStreamAdd, lin_ws, lin_b, hs));
+    } else if (down_tiled) {
+        StreamArgs a{};
+        a.seg[0] = Seg(w->w_down, x, D, x);
+        a.n_seg = 1;
+        MLK_TRY(LinearTiledFused(w->w_down.type, gate, T, F, a, kStreamAdd, hs));
     } else {
         MLK_TRY(Linear(w->w_down, gate, proj, T, F, D, lin_ws, lin_b, stream));
         MLK_TRY(mlk_add_f32(x, proj, x, T * D, stream));

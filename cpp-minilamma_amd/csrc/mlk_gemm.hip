@@ -470,7 +470,18 @@ __device__ inline void TileCodes(const WTile<WT>& t, int32_t (&c)[16]) {
     }
 }
 
-template <int WT, int NW>
+// Epilogues of GemmPieces (one K pass, no partial sums for the last two):
+//   kPcStore   y = sum + bias, or the split's partial sums;
+//   kPcAdd     y = y + (sum + bias), the residual add of the layer;
+//   kPcSwiGlu  gate and up in one tile (NW = 8): W rows n0 .. n0 + 127 of
+//              w (gate, waves with wn 0, 1) and of w2 (up, wn 2, 3); the gate
+//              waves hand their sums + bias through LDS to the up waves that
+//              hold the same outputs, which store SwiGlu(gate, up + bias2).
+// Each output's sum is the same as kPcStore's, so every epilogue gives the
+// separate kernels' values (mlk_add_f32, mlk_swiglu_f32) bit for bit.
+enum PiecesEpi { kPcStore = 0, kPcAdd = 1, kPcSwiGlu = 2 };
+
+template <int WT, int NW, int EPI = kPcStore>
 __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ x,
                                                            const uint8_t* __restrict__ w,
                                                            const float* __restrict__ bias,
@@ -478,18 +489,27 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
                                                            int64_t K, int64_t O,
                                                            int64_t row_bytes, int tiles_m,
                                                            int tiles, int64_t per_split,
-                                                           float* __restrict__ partial) {
+                                                           float* __restrict__ partial,
+                                                           const uint8_t* __restrict__ w2,
+                                                           const float* __restrict__ bias2) {
     constexpr int BM = 128;
     constexpr int kThreads = 64 * NW;
-    constexpr int BNT = 32 * NW;               // outputs per tile
+    constexpr int BNT = 32 * NW;               // W rows per tile
     constexpr int kXN = BM * kBK / 4 / kThreads;  // x float4s per thread and stage
+    constexpr bool kDual = EPI == kPcSwiGlu;
+    static_assert(!kDual || NW == 8, "gate / up tiles take 8 waves");
     __shared__ PiecesSmem<BNT> sm;
     const int tile = static_cast<int>(blockIdx.x) % tiles;
     const int sp = static_cast<int>(blockIdx.x) / tiles;
     const int tm = tile % tiles_m;
     const int tn = tile / tiles_m;
     const int64_t m0 = static_cast<int64_t>(tm) * BM;
-    const int64_t n0 = static_cast<int64_t>(tn) * BNT;
+    const int64_t n0 = static_cast<int64_t>(tn) * (kDual ? BNT / 2 : BNT);
+    // the W rows this thread loads: gate rows n0 .. for the tile's first
+    // half, up rows n0 .. (from w2) for the second when kDual
+    const bool w_second = kDual && static_cast<int>(threadIdx.x >> 1) >= BNT / 2;
+    const uint8_t* const wsrc = w_second ? w2 : w;
+    const int64_t n0w = w_second ? n0 - BNT / 2 : n0;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int wm = wave & 1, wn = wave >> 1;  // 64 token rows x 64 outputs per wave
@@ -554,7 +574,7 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
         const int buf = static_cast<int>((s - s0) & 1);
         const int64_t k2 = (s + 2 < s1 ? s + 2 : s1 - 1) * kBK;
         load_x(k2, next_x);
-        next_w.Load(w, O, K, row_bytes, n0, k2);
+        next_w.Load(wsrc, O, K, row_bytes, n0w, k2);
         __builtin_amdgcn_sched_barrier(0);
         bf16x8g b[4];
         float dj[4];
@@ -587,11 +607,11 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
     float4 xa[kXN], xb[kXN];
     WTile<WT> wa, wb;
     load_x(s0 * kBK, xa);
-    wa.Load(w, O, K, row_bytes, n0, s0 * kBK);
+    wa.Load(wsrc, O, K, row_bytes, n0w, s0 * kBK);
     {
         const int64_t k1 = (s0 + 1 < s1 ? s0 + 1 : s0) * kBK;
         load_x(k1, xb);
-        wb.Load(w, O, K, row_bytes, n0, k1);
+        wb.Load(wsrc, O, K, row_bytes, n0w, k1);
     }
     store(0, xa, wa);
     __syncthreads();
@@ -600,6 +620,48 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
         if (s + 1 < s1) step(s + 1, xa, wa, xb, wb);
     }
 
+    if constexpr (kDual) {
+        // The stage buffers are free (the last stage's reads are behind the
+        // loop's last barrier).  Gate wave (wm, wn) and up wave (wm, wn + 2)
+        // hold the same outputs in the same registers, so lane l of one
+        // hands lane l of the other its 64 sums, 16 float4s at a stride of
+        // 64 lanes (1 KB per instruction, no bank conflicts).
+        static_assert(sizeof(PiecesSmem<BNT>) >= 4 * 16 * 64 * sizeof(float4),
+                      "the gate sums fit the stage buffers");
+        float4* const xch = reinterpret_cast<float4*>(&sm) + (wm * 2 + (wn & 1)) * 16 * 64 + lane;
+        if (wn < 2) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = n0 + wn * 64 + 16 * j + i16;
+                const float bg = bias != nullptr && col < O ? bias[col] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    xch[(4 * i + j) * 64] = make_float4(acc[i][j][0] + bg, acc[i][j][1] + bg,
+                                                        acc[i][j][2] + bg, acc[i][j][3] + bg);
+                }
+            }
+        }
+        __syncthreads();
+        if (wn >= 2) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = n0 + (wn - 2) * 64 + 16 * j + i16;
+                if (col >= O) continue;
+                const float bu = bias2 != nullptr ? bias2[col] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 g4 = xch[(4 * i + j) * 64];
+                    const float g[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = m0 + wm * 64 + 16 * i + 4 * kq + r;
+                        if (row < T) y[row * O + col] = SwiGluF(g[r], acc[i][j][r] + bu);
+                    }
+                }
+            }
+        }
+        return;
+    }
     float* out = partial != nullptr ? partial + sp * T * O : y;
     const float* add = partial != nullptr ? nullptr : bias;
 #pragma unroll
@@ -612,7 +674,12 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = m0 + wm * 64 + 16 * i + 4 * kq + r;
-                if (row < T) out[row * O + col] = acc[i][j][r] + bb;
+                if (row >= T) continue;
+                if constexpr (EPI == kPcAdd) {
+                    out[row * O + col] = out[row * O + col] + (acc[i][j][r] + bb);
+                } else {
+                    out[row * O + col] = acc[i][j][r] + bb;
+                }
             }
         }
     }
@@ -1521,29 +1588,39 @@ mlk_status LaunchSkinny(int wt, const float* x, const SkinnyArgs& a, int64_t T, 
     return CheckLaunch("GemmSkinny");
 }
 
-template <int NW>
-void LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
+// false: no kernel of this epilogue for wt (the fused epilogues are built
+// for block-layout Q8_0 / Q4_0 only)
+template <int NW, int EPI = kPcStore>
+bool LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
                   const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
-                  int tiles_m, int tiles, int64_t per_split, float* partial) {
+                  int tiles_m, int tiles, int64_t per_split, float* partial,
+                  const uint8_t* w2 = nullptr, const float* bias2 = nullptr) {
     const dim3 block(64 * NW);
     switch (wt) {
         case MLK_Q8_0:
-            hipLaunchKernelGGL((GemmPieces<MLK_Q8_0, NW>), grid, block, 0, s, x, w, bias, y, T, K,
-                               O, row_bytes, tiles_m, tiles, per_split, partial);
-            break;
+            hipLaunchKernelGGL((GemmPieces<MLK_Q8_0, NW, EPI>), grid, block, 0, s, x, w, bias, y,
+                               T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+            return true;
         case MLK_Q4_0:
-            hipLaunchKernelGGL((GemmPieces<MLK_Q4_0, NW>), grid, block, 0, s, x, w, bias, y, T, K,
-                               O, row_bytes, tiles_m, tiles, per_split, partial);
-            break;
-        case kWPlanarQ8:
-            hipLaunchKernelGGL((GemmPieces<kWPlanarQ8, NW>), grid, block, 0, s, x, w, bias, y, T,
-                               K, O, row_bytes, tiles_m, tiles, per_split, partial);
-            break;
+            hipLaunchKernelGGL((GemmPieces<MLK_Q4_0, NW, EPI>), grid, block, 0, s, x, w, bias, y,
+                               T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+            return true;
         default:
-            hipLaunchKernelGGL((GemmPieces<kWPlanarQ4, NW>), grid, block, 0, s, x, w, bias, y, T,
-                               K, O, row_bytes, tiles_m, tiles, per_split, partial);
             break;
     }
+    if constexpr (EPI == kPcStore) {
+        if (wt == kWPlanarQ8) {
+            hipLaunchKernelGGL((GemmPieces<kWPlanarQ8, NW>), grid, block, 0, s, x, w, bias, y, T,
+                               K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+            return true;
+        }
+        if (wt == kWPlanarQ4) {
+            hipLaunchKernelGGL((GemmPieces<kWPlanarQ4, NW>), grid, block, 0, s, x, w, bias, y, T,
+                               K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+            return true;
+        }
+    }
+    return false;
 }
 
 template <int BM>
@@ -1673,6 +1750,65 @@ mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, 
     hipLaunchKernelGGL(SplitKReduce, dim3(GridFor(T * O, kGemmThreads, 8)), dim3(kGemmThreads), 0,
                        s, partial, plan.splits, bias, y, T, O);
     return CheckLaunch("SplitKReduce");
+}
+
+bool TiledFusedApplies(int wt, int64_t T, int64_t K, int64_t O, int mode) {
+    if ((wt != MLK_Q8_0 && wt != MLK_Q4_0) || K % 256 != 0 || TileRows(T) != 128 ||
+        O <= 0 || PlanSplits(T, K, O).splits != 1) {
+        return false;
+    }
+    const int64_t tiles_m = (T + 127) / 128;
+    if (mode == kStreamSwiGlu) {
+        const int64_t tiles = tiles_m * ((O + 127) / 128);
+        return tiles >= 2 * static_cast<int64_t>(ComputeUnits()) && tiles <= 0x7FFFFFFF;
+    }
+    return mode == kStreamAdd && tiles_m * ((O + 127) / 128) <= 0x7FFFFFFF;
+}
+
+mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& sa,
+                            int mode, hipStream_t s) {
+    const StreamSeg& g0 = sa.seg[0];
+    const int64_t O = g0.rows;
+    if (!TiledFusedApplies(wt, T, K, O, mode) || !Aligned(x, 16)) {
+        return Fail(MLK_ERR_INVALID, "linear (tiled, fused): unsupported shape");
+    }
+    if (mode == kStreamSwiGlu) {
+        const StreamSeg& g1 = sa.seg[1];
+        if (sa.n_seg != 2 || g1.rows != O || g0.w == nullptr || g1.w == nullptr ||
+            g1.y == nullptr || !Aligned(g0.w, 2) || !Aligned(g1.w, 2)) {
+            return Fail(MLK_ERR_INVALID, "linear (tiled, fused): bad gate / up segments");
+        }
+    } else if (sa.n_seg != 1 || g0.w == nullptr || g0.y == nullptr || g0.res != g0.y ||
+               !Aligned(g0.w, 2)) {
+        // the residual add runs in place: y = y + sum
+        return Fail(MLK_ERR_INVALID, "linear (tiled, fused): the residual must be y");
+    }
+    const int64_t row_bytes = (K / 32) * BlockBytes(wt);
+    const int64_t stages = K / kBK;
+    const int tm = static_cast<int>((T + 127) / 128);
+    bool ok = false;
+    if (mode == kStreamSwiGlu) {
+        const int tiles = static_cast<int>(tm * ((O + 127) / 128));
+        ok = LaunchPieces<8, kPcSwiGlu>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w, g0.bias,
+                                        sa.seg[1].y, T, K, O, row_bytes, tm, tiles, stages,
+                                        nullptr, sa.seg[1].w, sa.seg[1].bias);
+    } else {
+        // the tile width LaunchTiles takes for the plain product
+        const int64_t tiles8 = static_cast<int64_t>(tm) * ((O + 255) / 256);
+        if (tiles8 >= 2 * static_cast<int64_t>(ComputeUnits())) {
+            const int tiles = static_cast<int>(tiles8);
+            ok = LaunchPieces<8, kPcAdd>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w,
+                                         g0.bias, g0.y, T, K, O, row_bytes, tm, tiles, stages,
+                                         nullptr);
+        } else {
+            const int tiles = static_cast<int>(tm * ((O + 127) / 128));
+            ok = LaunchPieces<4, kPcAdd>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w,
+                                         g0.bias, g0.y, T, K, O, row_bytes, tm, tiles, stages,
+                                         nullptr);
+        }
+    }
+    if (!ok) return Fail(MLK_ERR_INVALID, "linear (tiled, fused): weight type %d", wt);
+    return CheckLaunch("GemmPieces (fused)");
 }
 
 bool SkinnyFusedApplies(int wt, int64_t T, int64_t K) {

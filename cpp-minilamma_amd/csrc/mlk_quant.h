@@ -163,6 +163,17 @@ mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, 
                       int64_t T, int64_t K, int64_t O, int64_t row_bytes, void* workspace,
                       size_t workspace_bytes, hipStream_t s);
 int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O);
+// The same tiled product with the layer's epilogue in one launch (no
+// workspace) for many token rows: block-layout Q8_0 / Q4_0, K % 256 == 0,
+// T > 64, O rows per matrix, and only where LaunchGemm would not split K
+// either, so each output's sum is LaunchGemm's.  kStreamAdd: one segment
+// with res == y (y = y + (sum + bias), mlk_add_f32's value).  kStreamSwiGlu:
+// gate and up segments of O rows each, seg[1].y = SwiGlu(gate, up) as
+// mlk_swiglu_f32 computes it, when the gate / up tiles fill two workgroups
+// per CU.  x 16-byte aligned, W 2-byte aligned.
+bool TiledFusedApplies(int wt, int64_t T, int64_t K, int64_t O, int mode);
+mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& a,
+                            int mode, hipStream_t s);
 
 // Planar Q8_0 / Q4_0 weights (layout at mlk_quant_to_planar, minilamma_hip.h;
 // mlk_gemm.hip).  wt values of LaunchGemm for them:

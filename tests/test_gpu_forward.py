@@ -273,6 +273,76 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
 
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
+@pytest.mark.parametrize("T", [4096, 4000])
+@pytest.mark.parametrize("biases", [False, True])
+def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, T, biases):
+    """A prompt chunk large enough that wo, gate/up and down each take the
+    128-row tile GEMM in one K pass (dim 2048, hidden 3072: 512 and more
+    tiles) carries their epilogues in that GEMM: wo and down add into the
+    residual stream (then plain RMSNorm for the ffn input), gate and up run
+    as one launch that writes SwiGLU(gate, up).  The sums are the plain
+    GEMM's, so the layer equals the separate entry points bit for bit,
+    with biases on all four matrices too (T = 4000: a partial last tile).
+    k and v (1024 tiles' worth of fewer outputs) still split K."""
+    S = 4096
+    cfg = dict(vocab=64, dim=2048, hidden_dim=3072, layers=1, n_heads=16, n_kv_heads=4,
+               head_dim=128, max_seq=S, rope_type=0, theta=500000.0, eps=1e-5)
+    model = O.forward_model(cfg, seed=17, weight_type=wt, biases=True)
+    D, F, H, KV, hd = 2048, 3072, 16, 4, 128
+    QD, KD = H * hd, KV * hd
+    lw = model["layers"][0]
+    dm = fwd.DeviceModel(model)
+    rng = np.random.default_rng(9)
+    B = mlk.DeviceBuffer.from_array
+    extra = {}
+    if biases:
+        for n, o in (("wo", D), ("w_gate", F), ("w_up", F), ("w_down", D)):
+            extra[n] = B((rng.standard_normal(o) * 0.1).astype(np.float32))
+            getattr(dm.layers[0], n).bias = extra[n].ptr
+    x0 = rng.standard_normal((T, D)).astype(np.float32)
+    kc0 = np.zeros((1, S, KV, hd), np.float32)
+    vc0 = np.zeros((1, S, KV, hd), np.float32)
+
+    x, kc, vc = B(x0), B(kc0), B(vc0)
+    ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, S, True), np.uint8)
+    fwd.forward_layer_batch(cfg, dm.layers[0], x, T, kc, vc, 1, S, 0, S, ws, pos0=0)
+    got = x.download()
+
+    w = {n: B(np.ascontiguousarray(lw[n][1], np.uint8)) for n in fwd.LINEAR_NAMES}
+    bias = {n: B(np.asarray(lw["b" + n[1]], np.float32)) for n in ("wq", "wk", "wv")}
+    bias.update(extra)
+    an = B(np.asarray(lw["attention_norm"], np.float32))
+    fn = B(np.asarray(lw["ffn_norm"], np.float32))
+    x2, kc2, vc2 = B(x0), B(kc0), B(vc0)
+    e = mlk.DeviceBuffer.empty
+    h, q, k, v, a, proj = e((T, D)), e((T, QD)), e((T, KD)), e((T, KD)), e((T, QD)), e((T, D))
+    g, u = e((T, F)), e((T, F))
+
+    def linear(name, x_in, y_out, i, o):
+        mlk.linear_quant(wt, x_in, w[name], y_out, T, i, o, bias=bias.get(name))
+    mlk.rmsnorm(x2, an, h, T, D, cfg["eps"])
+    linear("wq", h, q, D, QD)
+    linear("wk", h, k, D, KD)
+    linear("wv", h, v, D, KD)
+    mlk.rope(q, k, T, H, KV, hd, pos0=0, theta=cfg["theta"], rope_type=0)
+    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, pos0=0)
+    nws = mlk.attention_workspace_bytes(T, H, KV, hd, S)
+    aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
+    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, pos0=0, workspace=aws,
+                         workspace_bytes=aws.nbytes)
+    linear("wo", a, proj, QD, D)
+    mlk.add_rmsnorm(x2, proj, fn, h, T, D, cfg["eps"])
+    linear("w_gate", h, g, D, F)
+    linear("w_up", h, u, D, F)
+    mlk.swiglu(g, u, g, T * F)
+    linear("w_down", g, proj, F, D)
+    mlk.add(x2, proj, x2, T * D)
+    np.testing.assert_array_equal(got, x2.download())
+    np.testing.assert_array_equal(kc.download(), kc2.download())
+    np.testing.assert_array_equal(vc.download(), vc2.download())
+
+
+@pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
 @pytest.mark.parametrize("D,F", [(2048, 1024), (4096, 1024), (6144, 512), (8192, 512)])
 @pytest.mark.parametrize("planar", [False, True])
 def test_one_token_norms_folded_equal_op_by_op(mlk, fwd, wt, D, F, planar):
