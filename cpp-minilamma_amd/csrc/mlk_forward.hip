@@ -6,8 +6,10 @@
 // Per layer, on one stream (x [T, dim] is the residual stream, in place;
 // for 1 and for 2..32 tokens with quantized weights q/k/v are one launch,
 // gate/up carry the SwiGLU and the down projection adds into x; for many
-// tokens over Q8_0 / Q4_0 blocks gate/up carry the SwiGLU and wo and down
-// add into x, see below):
+// tokens over Q8_0 / Q4_0 blocks gate/up carry the SwiGLU, wo and down add
+// into x and k, v may share one launch; with separate q/k/v launches at
+// consecutive positions k and v are written to their cache rows and
+// rotated there, with no copy; see below):
 //   h = RmsNorm(x, attention_norm)                    mlk_rmsnorm_f32
 //   q, k, v = h W^T (+ bias)                          mlk_linear_* (GEMM from 8 rows)
 //   RoPE(q, k) at each token's position               mlk_rope_f32
@@ -304,6 +306,17 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
                                SkinnyFusedApplies(w->w_gate.type, T, D));
     const bool downm = downp || (mid && w->w_down.type != kLinearF32 &&
                                  SkinnyFusedApplies(w->w_down.type, T, F));
+    // The separate q/k/v launches at consecutive positions (pos0 + T <=
+    // max_ctx <= max_seq, checked above): k and v go straight to their cache
+    // rows, which RoPE then rotates in place, so no copy launch; for many
+    // tokens k and v run as one launch where that fills the GPU without a K
+    // split (each split alone)
+    const bool kv_direct = !(qkv1 || qkvm) && contiguous;
+    float* const k_rows = kv_direct ? k_cache + (layer * max_seq + pos0) * KD : k;
+    float* const v_rows = kv_direct ? v_cache + (layer * max_seq + pos0) * KD : v;
+    const bool kv_pair = !(qkv1 || qkvm) && w->wk.type == w->wv.type &&
+                         TiledFusedApplies(w->wk.type, T, D, KD, kStreamPlain) &&
+                         Aligned(w->wk.data, 2) && Aligned(w->wv.data, 2);
     // Many tokens (128-row tiles, K in one pass): the same groups' epilogues
     // in the GEMM itself, gate/up as one launch with SwiGLU, wo and down
     // adding into x (the plain GEMM's sums, so the separate kernels' values)
@@ -375,14 +388,25 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         }
     } else {
         MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
-        MLK_TRY(Linear(w->wk, h, k, T, D, KD, lin_ws, lin_b, stream));
-        MLK_TRY(Linear(w->wv, h, v, T, D, KD, lin_ws, lin_b, stream));
+        if (kv_pair) {
+            StreamArgs a{};
+            a.seg[0] = Seg(w->wk, k_rows, KD);
+            a.seg[1] = Seg(w->wv, v_rows, KD);
+            a.n_seg = 2;
+            MLK_TRY(LinearTiledFused(w->wk.type, h, T, D, a, kStreamPlain, hs));
+        } else {
+            MLK_TRY(Linear(w->wk, h, k_rows, T, D, KD, lin_ws, lin_b, stream));
+            MLK_TRY(Linear(w->wv, h, v_rows, T, D, KD, lin_ws, lin_b, stream));
+        }
     }
     if (!rope_fused) {
-        MLK_TRY(mlk_rope_f32(q, k, T, c.n_heads, c.n_kv_heads, c.head_dim, QD, KD, positions,
+        MLK_TRY(mlk_rope_f32(q, k_rows, T, c.n_heads, c.n_kv_heads, c.head_dim, QD, KD, positions,
                              pos0, c.rope_theta, c.rope_type, err, stream));
-        MLK_TRY(mlk_kv_write_f32(k_cache, v_cache, n_layers, max_seq, c.n_kv_heads, c.head_dim,
-                                 layer, k, KD, v, KD, positions, pos0, T, err, stream));
+        if (!kv_direct) {
+            MLK_TRY(mlk_kv_write_f32(k_cache, v_cache, n_layers, max_seq, c.n_kv_heads,
+                                     c.head_dim, layer, k, KD, v, KD, positions, pos0, T, err,
+                                     stream));
+        }
     }
     // the chunk merge also writes a's planes for a planar wo (over h's: the
     // q/k/v GEMM has read them)

@@ -477,9 +477,12 @@ __device__ inline void TileCodes(const WTile<WT>& t, int32_t (&c)[16]) {
 //              w (gate, waves with wn 0, 1) and of w2 (up, wn 2, 3); the gate
 //              waves hand their sums + bias through LDS to the up waves that
 //              hold the same outputs, which store SwiGlu(gate, up + bias2).
+//   kPcPair    two matrices of O rows each in one launch (the layer's k and
+//              v): the first half of the tiles along the outputs takes w,
+//              bias and y, the second w2, bias2 and y2; stored as kPcStore.
 // Each output's sum is the same as kPcStore's, so every epilogue gives the
 // separate kernels' values (mlk_add_f32, mlk_swiglu_f32) bit for bit.
-enum PiecesEpi { kPcStore = 0, kPcAdd = 1, kPcSwiGlu = 2 };
+enum PiecesEpi { kPcStore = 0, kPcAdd = 1, kPcSwiGlu = 2, kPcPair = 3 };
 
 template <int WT, int NW, int EPI = kPcStore>
 __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ x,
@@ -491,7 +494,8 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
                                                            int tiles, int64_t per_split,
                                                            float* __restrict__ partial,
                                                            const uint8_t* __restrict__ w2,
-                                                           const float* __restrict__ bias2) {
+                                                           const float* __restrict__ bias2,
+                                                           float* __restrict__ y2) {
     constexpr int BM = 128;
     constexpr int kThreads = 64 * NW;
     constexpr int BNT = 32 * NW;               // W rows per tile
@@ -504,12 +508,15 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
     const int tm = tile % tiles_m;
     const int tn = tile / tiles_m;
     const int64_t m0 = static_cast<int64_t>(tm) * BM;
-    const int64_t n0 = static_cast<int64_t>(tn) * (kDual ? BNT / 2 : BNT);
+    // kPcPair: the tile's matrix (the same for the whole workgroup)
+    const int half_n = tiles / tiles_m / 2;
+    const bool wg_second = EPI == kPcPair && tn >= half_n;
+    const int64_t n0 = static_cast<int64_t>(wg_second ? tn - half_n : tn) * (kDual ? BNT / 2 : BNT);
     // the W rows this thread loads: gate rows n0 .. for the tile's first
     // half, up rows n0 .. (from w2) for the second when kDual
-    const bool w_second = kDual && static_cast<int>(threadIdx.x >> 1) >= BNT / 2;
-    const uint8_t* const wsrc = w_second ? w2 : w;
-    const int64_t n0w = w_second ? n0 - BNT / 2 : n0;
+    const bool t_second = kDual && static_cast<int>(threadIdx.x >> 1) >= BNT / 2;
+    const uint8_t* const wsrc = t_second || wg_second ? w2 : w;
+    const int64_t n0w = t_second ? n0 - BNT / 2 : n0;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int wm = wave & 1, wn = wave >> 1;  // 64 token rows x 64 outputs per wave
@@ -662,8 +669,8 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
         }
         return;
     }
-    float* out = partial != nullptr ? partial + sp * T * O : y;
-    const float* add = partial != nullptr ? nullptr : bias;
+    float* out = partial != nullptr ? partial + sp * T * O : (wg_second ? y2 : y);
+    const float* add = partial != nullptr ? nullptr : (wg_second ? bias2 : bias);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int64_t col = n0 + wn * 64 + 16 * j + i16;
@@ -1594,16 +1601,19 @@ template <int NW, int EPI = kPcStore>
 bool LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
                   const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
                   int tiles_m, int tiles, int64_t per_split, float* partial,
-                  const uint8_t* w2 = nullptr, const float* bias2 = nullptr) {
+                  const uint8_t* w2 = nullptr, const float* bias2 = nullptr,
+                  float* y2 = nullptr) {
     const dim3 block(64 * NW);
     switch (wt) {
         case MLK_Q8_0:
             hipLaunchKernelGGL((GemmPieces<MLK_Q8_0, NW, EPI>), grid, block, 0, s, x, w, bias, y,
-                               T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+                               T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
+                               y2);
             return true;
         case MLK_Q4_0:
             hipLaunchKernelGGL((GemmPieces<MLK_Q4_0, NW, EPI>), grid, block, 0, s, x, w, bias, y,
-                               T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+                               T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
+                               y2);
             return true;
         default:
             break;
@@ -1611,12 +1621,14 @@ bool LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_
     if constexpr (EPI == kPcStore) {
         if (wt == kWPlanarQ8) {
             hipLaunchKernelGGL((GemmPieces<kWPlanarQ8, NW>), grid, block, 0, s, x, w, bias, y, T,
-                               K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+                               K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
+                               y2);
             return true;
         }
         if (wt == kWPlanarQ4) {
             hipLaunchKernelGGL((GemmPieces<kWPlanarQ4, NW>), grid, block, 0, s, x, w, bias, y, T,
-                               K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2);
+                               K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
+                               y2);
             return true;
         }
     }
@@ -1753,11 +1765,15 @@ mlk_status LaunchGemm(int wt, const float* x, const void* w, const float* bias, 
 }
 
 bool TiledFusedApplies(int wt, int64_t T, int64_t K, int64_t O, int mode) {
-    if ((wt != MLK_Q8_0 && wt != MLK_Q4_0) || K % 256 != 0 || TileRows(T) != 128 ||
-        O <= 0 || PlanSplits(T, K, O).splits != 1) {
+    if ((wt != MLK_Q8_0 && wt != MLK_Q4_0) || K % 256 != 0 || TileRows(T) != 128 || O <= 0) {
         return false;
     }
     const int64_t tiles_m = (T + 127) / 128;
+    if (mode == kStreamPlain) {  // a pair in one pass, where that fills the GPU on its own
+        const int64_t tiles = tiles_m * 2 * ((O + 127) / 128);
+        return tiles >= 2 * static_cast<int64_t>(ComputeUnits()) && tiles <= 0x7FFFFFFF;
+    }
+    if (PlanSplits(T, K, O).splits != 1) return false;
     if (mode == kStreamSwiGlu) {
         const int64_t tiles = tiles_m * ((O + 127) / 128);
         return tiles >= 2 * static_cast<int64_t>(ComputeUnits()) && tiles <= 0x7FFFFFFF;
@@ -1772,11 +1788,12 @@ mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const 
     if (!TiledFusedApplies(wt, T, K, O, mode) || !Aligned(x, 16)) {
         return Fail(MLK_ERR_INVALID, "linear (tiled, fused): unsupported shape");
     }
-    if (mode == kStreamSwiGlu) {
+    if (mode == kStreamSwiGlu || mode == kStreamPlain) {
         const StreamSeg& g1 = sa.seg[1];
         if (sa.n_seg != 2 || g1.rows != O || g0.w == nullptr || g1.w == nullptr ||
-            g1.y == nullptr || !Aligned(g0.w, 2) || !Aligned(g1.w, 2)) {
-            return Fail(MLK_ERR_INVALID, "linear (tiled, fused): bad gate / up segments");
+            g1.y == nullptr || (mode == kStreamPlain && g0.y == nullptr) || !Aligned(g0.w, 2) ||
+            !Aligned(g1.w, 2)) {
+            return Fail(MLK_ERR_INVALID, "linear (tiled, fused): bad segment pair");
         }
     } else if (sa.n_seg != 1 || g0.w == nullptr || g0.y == nullptr || g0.res != g0.y ||
                !Aligned(g0.w, 2)) {
@@ -1787,7 +1804,22 @@ mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const 
     const int64_t stages = K / kBK;
     const int tm = static_cast<int>((T + 127) / 128);
     bool ok = false;
-    if (mode == kStreamSwiGlu) {
+    if (mode == kStreamPlain) {
+        // the tile width LaunchTiles takes, over both matrices
+        const int64_t tiles8 = static_cast<int64_t>(tm) * 2 * ((O + 255) / 256);
+        const StreamSeg& g1 = sa.seg[1];
+        if (tiles8 >= 2 * static_cast<int64_t>(ComputeUnits())) {
+            const int tiles = static_cast<int>(tiles8);
+            ok = LaunchPieces<8, kPcPair>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w,
+                                          g0.bias, g0.y, T, K, O, row_bytes, tm, tiles, stages,
+                                          nullptr, g1.w, g1.bias, g1.y);
+        } else {
+            const int tiles = static_cast<int>(tm * 2 * ((O + 127) / 128));
+            ok = LaunchPieces<4, kPcPair>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w,
+                                          g0.bias, g0.y, T, K, O, row_bytes, tm, tiles, stages,
+                                          nullptr, g1.w, g1.bias, g1.y);
+        }
+    } else if (mode == kStreamSwiGlu) {
         const int tiles = static_cast<int>(tm * ((O + 127) / 128));
         ok = LaunchPieces<8, kPcSwiGlu>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w, g0.bias,
                                         sa.seg[1].y, T, K, O, row_bytes, tm, tiles, stages,

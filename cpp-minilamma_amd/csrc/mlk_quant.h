@@ -170,7 +170,11 @@ int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O);
 // with res == y (y = y + (sum + bias), mlk_add_f32's value).  kStreamSwiGlu:
 // gate and up segments of O rows each, seg[1].y = SwiGlu(gate, up) as
 // mlk_swiglu_f32 computes it, when the gate / up tiles fill two workgroups
-// per CU.  x 16-byte aligned, W 2-byte aligned.
+// per CU.  kStreamPlain: two matrices of O rows each (segments 0 and 1,
+// each to its own y) in one launch without a K split, when their tiles
+// together fill two workgroups per CU (where LaunchGemm would split each:
+// the sums are then the unsplit product's, LaunchGemm's without a
+// workspace).  x 16-byte aligned, W 2-byte aligned.
 bool TiledFusedApplies(int wt, int64_t T, int64_t K, int64_t O, int mode);
 mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& a,
                             int mode, hipStream_t s);

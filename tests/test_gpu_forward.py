@@ -280,15 +280,17 @@ def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, T, biases):
     128-row tile GEMM in one K pass (dim 2048, hidden 3072: 512 and more
     tiles) carries their epilogues in that GEMM: wo and down add into the
     residual stream (then plain RMSNorm for the ffn input), gate and up run
-    as one launch that writes SwiGLU(gate, up).  The sums are the plain
-    GEMM's, so the layer equals the separate entry points bit for bit,
-    with biases on all four matrices too (T = 4000: a partial last tile).
-    k and v (1024 tiles' worth of fewer outputs) still split K."""
+    as one launch that writes SwiGLU(gate, up).  k and v (1024 outputs each)
+    run as one launch without a K split, straight into their cache rows,
+    which RoPE rotates there (no copy launch).  The sums are the plain
+    GEMM's (for k and v the unsplit one's: no workspace), so the layer
+    equals the separate entry points bit for bit, with biases on all seven
+    matrices too (T = 4000: a partial last tile)."""
     S = 4096
-    cfg = dict(vocab=64, dim=2048, hidden_dim=3072, layers=1, n_heads=16, n_kv_heads=4,
+    cfg = dict(vocab=64, dim=2048, hidden_dim=3072, layers=1, n_heads=16, n_kv_heads=8,
                head_dim=128, max_seq=S, rope_type=0, theta=500000.0, eps=1e-5)
     model = O.forward_model(cfg, seed=17, weight_type=wt, biases=True)
-    D, F, H, KV, hd = 2048, 3072, 16, 4, 128
+    D, F, H, KV, hd = 2048, 3072, 16, 8, 128
     QD, KD = H * hd, KV * hd
     lw = model["layers"][0]
     dm = fwd.DeviceModel(model)
@@ -318,12 +320,12 @@ def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, T, biases):
     h, q, k, v, a, proj = e((T, D)), e((T, QD)), e((T, KD)), e((T, KD)), e((T, QD)), e((T, D))
     g, u = e((T, F)), e((T, F))
 
-    def linear(name, x_in, y_out, i, o):
-        mlk.linear_quant(wt, x_in, w[name], y_out, T, i, o, bias=bias.get(name))
+    def linear(name, x_in, y_out, i, o, ws="auto"):
+        mlk.linear_quant(wt, x_in, w[name], y_out, T, i, o, bias=bias.get(name), workspace=ws)
     mlk.rmsnorm(x2, an, h, T, D, cfg["eps"])
     linear("wq", h, q, D, QD)
-    linear("wk", h, k, D, KD)
-    linear("wv", h, v, D, KD)
+    linear("wk", h, k, D, KD, ws=None)
+    linear("wv", h, v, D, KD, ws=None)
     mlk.rope(q, k, T, H, KV, hd, pos0=0, theta=cfg["theta"], rope_type=0)
     mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, pos0=0)
     nws = mlk.attention_workspace_bytes(T, H, KV, hd, S)
