@@ -272,25 +272,30 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
         np.testing.assert_array_equal(kc.download()[0, kept], kc0[0, kept])
 
 
+TILED_CASES = [  # dim, hidden, heads, tokens, wo/gate/up/down biases
+    (2048, 3072, 16, 4096, False), (2048, 3072, 16, 4096, True), (2048, 3072, 16, 4000, False),
+    (2048, 3072, 16, 4000, True), (4096, 2048, 32, 4096, True)]
+
+
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
-@pytest.mark.parametrize("T", [4096, 4000])
-@pytest.mark.parametrize("biases", [False, True])
-def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, T, biases):
+@pytest.mark.parametrize("D,F,H,T,biases", TILED_CASES)
+def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, D, F, H, T, biases):
     """A prompt chunk large enough that wo, gate/up and down each take the
-    128-row tile GEMM in one K pass (dim 2048, hidden 3072: 512 and more
-    tiles) carries their epilogues in that GEMM: wo and down add into the
+    128-row tile GEMM in one K pass (512 and more tiles of 128 outputs)
+    carries their epilogues in that GEMM: wo and down add into the
     residual stream (then plain RMSNorm for the ffn input), gate and up run
     as one launch that writes SwiGLU(gate, up).  k and v (1024 outputs each)
     run as one launch without a K split, straight into their cache rows,
     which RoPE rotates there (no copy launch).  The sums are the plain
     GEMM's (for k and v the unsplit one's: no workspace), so the layer
     equals the separate entry points bit for bit, with biases on all seven
-    matrices too (T = 4000: a partial last tile)."""
-    S = 4096
-    cfg = dict(vocab=64, dim=2048, hidden_dim=3072, layers=1, n_heads=16, n_kv_heads=8,
-               head_dim=128, max_seq=S, rope_type=0, theta=500000.0, eps=1e-5)
+    matrices too (T = 4000: a partial last tile).  dim 2048 takes the
+    residual adds on 128-output tiles, dim 4096 (Llama-3-8B's wo and down)
+    on 256-output ones."""
+    S, KV, hd = 4096, 8, 128
+    cfg = dict(vocab=64, dim=D, hidden_dim=F, layers=1, n_heads=H, n_kv_heads=KV,
+               head_dim=hd, max_seq=S, rope_type=0, theta=500000.0, eps=1e-5)
     model = O.forward_model(cfg, seed=17, weight_type=wt, biases=True)
-    D, F, H, KV, hd = 2048, 3072, 16, 8, 128
     QD, KD = H * hd, KV * hd
     lw = model["layers"][0]
     dm = fwd.DeviceModel(model)
