@@ -272,29 +272,32 @@ def test_layer_fused_equals_op_by_op(mlk, fwd, wt, T, case):
         np.testing.assert_array_equal(kc.download()[0, kept], kc0[0, kept])
 
 
-TILED_CASES = [  # dim, hidden, heads, tokens, wo/gate/up/down biases
-    (2048, 3072, 16, 4096, False), (2048, 3072, 16, 4096, True), (2048, 3072, 16, 4000, False),
-    (2048, 3072, 16, 4000, True), (4096, 2048, 32, 4096, True)]
+TILED_CASES = [  # dim, hidden, heads, tokens, wo/gate/up/down biases, RoPE layout
+    (2048, 3072, 16, 4096, False, 0), (2048, 3072, 16, 4096, True, 0),
+    (2048, 3072, 16, 4000, False, 0), (2048, 3072, 16, 4000, True, 0),
+    (4096, 2048, 32, 4096, True, 0), (2048, 3072, 16, 4000, True, 1)]
 
 
 @pytest.mark.parametrize("wt", ["q8_0", "q4_0"])
-@pytest.mark.parametrize("D,F,H,T,biases", TILED_CASES)
-def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, D, F, H, T, biases):
+@pytest.mark.parametrize("D,F,H,T,biases,rope_type", TILED_CASES)
+def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, D, F, H, T, biases, rope_type):
     """A prompt chunk large enough that wo, gate/up and down each take the
     128-row tile GEMM in one K pass (512 and more tiles of 128 outputs)
     carries their epilogues in that GEMM: wo and down add into the
     residual stream (then plain RMSNorm for the ffn input), gate and up run
     as one launch that writes SwiGLU(gate, up).  k and v (1024 outputs each)
     run as one launch without a K split, straight into their cache rows,
-    which RoPE rotates there (no copy launch).  The sums are the plain
+    where the RoPE launch rotates k (q in place; normal and NeoX layouts).
+    The sums are the plain
     GEMM's (for k and v the unsplit one's: no workspace), so the layer
     equals the separate entry points bit for bit, with biases on all seven
-    matrices too (T = 4000: a partial last tile).  dim 2048 takes the
+    matrices too (T = 4000: a partial last tile, at positions 90..4089).  dim 2048 takes the
     residual adds on 128-output tiles, dim 4096 (Llama-3-8B's wo and down)
     on 256-output ones."""
     S, KV, hd = 4096, 8, 128
+    p0 = 0 if T == 4096 else 90
     cfg = dict(vocab=64, dim=D, hidden_dim=F, layers=1, n_heads=H, n_kv_heads=KV,
-               head_dim=hd, max_seq=S, rope_type=0, theta=500000.0, eps=1e-5)
+               head_dim=hd, max_seq=S, rope_type=rope_type, theta=500000.0, eps=1e-5)
     model = O.forward_model(cfg, seed=17, weight_type=wt, biases=True)
     QD, KD = H * hd, KV * hd
     lw = model["layers"][0]
@@ -312,7 +315,7 @@ def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, D, F, H, T, biases):
 
     x, kc, vc = B(x0), B(kc0), B(vc0)
     ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, S, True), np.uint8)
-    fwd.forward_layer_batch(cfg, dm.layers[0], x, T, kc, vc, 1, S, 0, S, ws, pos0=0)
+    fwd.forward_layer_batch(cfg, dm.layers[0], x, T, kc, vc, 1, S, 0, S, ws, pos0=p0)
     got = x.download()
 
     w = {n: B(np.ascontiguousarray(lw[n][1], np.uint8)) for n in fwd.LINEAR_NAMES}
@@ -331,11 +334,11 @@ def test_layer_tiled_epilogues_equal_op_by_op(mlk, fwd, wt, D, F, H, T, biases):
     linear("wq", h, q, D, QD)
     linear("wk", h, k, D, KD, ws=None)
     linear("wv", h, v, D, KD, ws=None)
-    mlk.rope(q, k, T, H, KV, hd, pos0=0, theta=cfg["theta"], rope_type=0)
-    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, pos0=0)
+    mlk.rope(q, k, T, H, KV, hd, pos0=p0, theta=cfg["theta"], rope_type=rope_type)
+    mlk.kv_write(kc2, vc2, 1, S, KV, hd, 0, k, v, T, pos0=p0)
     nws = mlk.attention_workspace_bytes(T, H, KV, hd, S)
     aws = mlk.DeviceBuffer(max(nws, 16), np.uint8)
-    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, pos0=0, workspace=aws,
+    mlk.attention_decode(q, kc2, vc2, 1, S, H, KV, hd, 0, T, a, S, pos0=p0, workspace=aws,
                          workspace_bytes=aws.nbytes)
     linear("wo", a, proj, QD, D)
     mlk.add_rmsnorm(x2, proj, fn, h, T, D, cfg["eps"])
