@@ -1028,7 +1028,7 @@ def layer_bench(mlk, steps, path):
     x = mlk.DeviceBuffer.empty((T, D))
     ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, T, True), np.uint8)
     ws1 = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, T, True), np.uint8)
-    for wt in ("q8_0", "f32"):
+    for wt in ("q8_0", "q4_0", "f32"):
         w, keep = _device_layer(mlk, fwd, cfg, wt, 400)
         mlk.fill_normal(x, T * D, 0.0, 1.0, 21)
         _warm_clock(mlk, st, lambda i: fwd.forward_layer_batch(cfg, w, x, T, kc, vc, 1, T, 0, T, ws,
@@ -1045,6 +1045,10 @@ def layer_bench(mlk, steps, path):
         n = LAYER_LOOP_SAMPLE
         x1 = mlk.DeviceBuffer.empty((n, D))
         mlk.fill_normal(x1, n * D, 0.0, 1.0, 22)
+        # one untimed token first: the first one-token call of a weight type
+        # loads its kernels, which would dominate the sample's average
+        fwd.forward_layer_batch(cfg, w, x1.ptr, 1, kc, vc, 1, T, 0, T, ws1, pos0=0, stream=st)
+        st.synchronize()
         e2, e3 = mlk.Event(), mlk.Event()
         e2.record(st)
         for t in range(n):
