@@ -1800,6 +1800,13 @@ mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const 
         // the residual add runs in place: y = y + sum
         return Fail(MLK_ERR_INVALID, "linear (tiled, fused): the residual must be y");
     }
+    // the outputs are written while other workgroups still read x
+    const auto overlaps_x = [&](const float* y) {
+        return y != nullptr && y < x + T * K && x < y + T * O;
+    };
+    if (overlaps_x(g0.y) || (sa.n_seg == 2 && overlaps_x(sa.seg[1].y))) {
+        return Fail(MLK_ERR_INVALID, "linear (tiled, fused): outputs must not overlap x");
+    }
     const int64_t row_bytes = (K / 32) * BlockBytes(wt);
     const int64_t stages = K / kBK;
     const int tm = static_cast<int>((T + 127) / 128);
