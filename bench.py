@@ -1178,6 +1178,7 @@ def layer_cpu_reference(cfg, n_tokens=2):
 
 ATT_LAYERS = 16  # cache layers rotated per launch: 16 x 64 MB K+V at 8B, S = 8192
 PREFILL_TOKENS = (512, 4096)  # causal prompt chunks from position 0
+PREFILL_IMAGE_MIN_TOKENS = 1024  # the library's pre-split tile images from here (head_dim 128)
 
 
 def attention_bench(mlk, steps, peak, path):
@@ -1243,15 +1244,28 @@ def attention_bench(mlk, steps, peak, path):
                 print(f"attention {name} {case}: {ms * 1e3:.2f} us, {tf:.1f} TFLOP/s "
                       f"({100 * tf / apk:.1f}% of {abasis}; per-token prefixes "
                       f"{gbs:.0f} GB/s)", flush=True)
-        # causal prefill of a prompt chunk at positions 0..T-1 (matrix cores)
-        for T in PREFILL_TOKENS:
+        # causal prefill of a prompt chunk at positions 0..T-1 (matrix cores):
+        # its own entry (each workgroup splits its K/V tiles into bf16
+        # pieces), and the decode entry with a workspace for the pre-split
+        # tile images (one split launch, then the tiles: the batched layer's
+        # path), both launches timed
+        for T, images in [(T, im) for T in PREFILL_TOKENS for im in (False, True)]:
             q = mlk.DeviceBuffer.empty((T, H * hd))
             mlk.fill_normal(q, T * H * hd, 0.0, 0.02, 14)
             o = mlk.DeviceBuffer.empty((T, H * hd))
+            img_bytes = KV * ((T + 31) // 32) * 2 * 3 * 32 * 128 * 2 if hd == 128 else 0
+            if images and (img_bytes == 0 or T < PREFILL_IMAGE_MIN_TOKENS):
+                continue
+            img = mlk.DeviceBuffer(img_bytes, np.uint8) if images else None
 
             def launch(i):
-                mlk.attention_prefill(q, kc, vc, ATT_LAYERS, S, H, KV, hd, i % ATT_LAYERS, 0, T,
-                                      o, stream=st)
+                if images:
+                    mlk.attention_decode(q, kc, vc, ATT_LAYERS, S, H, KV, hd, i % ATT_LAYERS, T,
+                                         o, T, pos0=0, workspace=img, workspace_bytes=img_bytes,
+                                         stream=st)
+                else:
+                    mlk.attention_prefill(q, kc, vc, ATT_LAYERS, S, H, KV, hd, i % ATT_LAYERS,
+                                          0, T, o, stream=st)
             _warm_clock(mlk, st, launch)
             for i in range(2):
                 launch(i)
@@ -1267,11 +1281,15 @@ def attention_bench(mlk, steps, peak, path):
             fl = workloads.flops_prefill_attention(T, H, hd)
             tf = fl / (ms * 1e-3) / 1e12
             apk, abasis = attention_peak(hd)
-            rows["prefill_T%d" % T] = {"us": round(ms * 1e3, 2), "flops": fl,
-                                       "TFLOPs": round(tf, 2), "peak_TFLOPs": round(apk, 1),
-                                       "peak_basis": abasis, "frac_of_peak": round(tf / apk, 4)}
-            print(f"attention {name} prefill T={T}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s "
-                  f"({100 * tf / apk:.1f}% of {abasis})", flush=True)
+            key = "prefill_T%d%s" % (T, "_images" if images else "")
+            rows[key] = {"us": round(ms * 1e3, 2), "flops": fl,
+                         "TFLOPs": round(tf, 2), "peak_TFLOPs": round(apk, 1),
+                         "peak_basis": abasis, "frac_of_peak": round(tf / apk, 4)}
+            print(f"attention {name} prefill T={T}{' (tile images)' if images else ''}: "
+                  f"{ms * 1e3:.1f} us, {tf:.1f} TFLOP/s ({100 * tf / apk:.1f}% of {abasis})",
+                  flush=True)
+            if img is not None:
+                img.close()
         out[name] = {"n_heads": H, "n_kv_heads": KV, "head_dim": hd, "cases": rows}
         del kc, vc
     with open(path, "w") as f:

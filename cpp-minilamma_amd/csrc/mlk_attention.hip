@@ -895,10 +895,11 @@ mlk_status AttentionDecode(const float* q, int64_t q_row_stride, const float* k_
     if (positions == nullptr && n_tokens >= kPrefillMinTokens &&
         PrefillSupported(head_dim, q, q_row_stride, out, k_cache, v_cache)) {
         // a prompt chunk at consecutive positions: the matrix-core prefill
-        // kernel (no workspace)
+        // kernel (a workspace of PrefillImageBytes holds the pre-split tiles)
         return LaunchPrefill(q, q_row_stride, k_cache + layer * max_seq * slot,
                              v_cache + layer * max_seq * slot, slot, n_heads, n_kv_heads,
-                             head_dim, pos0, n_tokens, out, AsStream(stream));
+                             head_dim, pos0, n_tokens, out, AsStream(stream), workspace,
+                             workspace_bytes);
     }
     if (n_tokens >= kTileMinTokens && PrefillSupported(head_dim, q, q_row_stride, out, k_cache, v_cache) &&
         Aligned(workspace, 16)) {

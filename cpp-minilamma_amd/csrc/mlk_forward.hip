@@ -94,9 +94,12 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
     }
     p.off[8] = at;
     at += Align256(p.lin_bytes);
-    // the decode kernel's chunk scratch, for the calls that take that path
+    // the decode kernel's chunk scratch, for the calls that take that path;
+    // a prompt chunk's pre-split K/V tile images (positions up to max_ctx)
     const bool prefill = contiguous && T >= 16 && (c.head_dim == 64 || c.head_dim == 128);
-    p.att_bytes = prefill ? 0
+    p.att_bytes = prefill ? (T >= kPrefillImageMinTokens
+                                 ? PrefillImageBytes(c.n_kv_heads, c.head_dim, max_ctx)
+                                 : 0)
                           : mlk_attention_workspace_bytes(T, c.n_heads, c.n_kv_heads, c.head_dim,
                                                           max_ctx);
     p.off[9] = at;

@@ -181,9 +181,11 @@ struct KvBlockBf {
     // K rows 4 a + r; V^T rows 4 c4 + e at slots s0 .. s0 + 3, where
     // positions 4 a .. 4 a + 3 sit (slot 8 kq + j: position 16 (j / 4) +
     // 4 kq + j % 4)
+    // KL / VLD: the K and V^T plane row strides (the LDS layout's, or the
+    // unpadded images of KvPieces)
+    template <int KL = 128 + kBfKLd, int VLD = kBfVLd>
     __device__ void Store(uint16_t* ks, uint16_t* vs) const {
         constexpr int HD = 128;
-        constexpr int KL = HD + kBfKLd;
         const int tid = static_cast<int>(threadIdx.x);
         const int a = tid / 32, c4 = tid % 32, av = tid % 8, cv = tid / 8;
         const int s0 = av < 4 ? 8 * av : 8 * (av - 4) + 4;
@@ -202,8 +204,87 @@ struct KvBlockBf {
             SplitPieces4(f32x4{v[0][e], v[1][e], v[2][e], v[3][e]}, pc);
 #pragma unroll
             for (int p = 0; p < 3; ++p) {
-                *reinterpret_cast<uint2*>(vs + (p * HD + 4 * cv + e) * kBfVLd + s0) = pc[p];
+                *reinterpret_cast<uint2*>(vs + (p * HD + 4 * cv + e) * VLD + s0) = pc[p];
             }
+        }
+    }
+};
+
+// Pre-split tiles (head_dim 128): per KV head g and tile t of 32 cache
+// positions, the K planes [3][32][128] and the V^T planes [3][128][32] in
+// bf16, exactly what KvBlockBf::Store writes to LDS, without the row
+// padding: one 48 KB image a tile, images of head g at g * n_tiles + t.
+// A prompt chunk's workgroups each stage every tile of their prefix, so
+// the split (most of the VALU work of a tile) is done once here instead of
+// once per 16 tokens.
+constexpr int kPieceHalves = 3 * kPfTile * 128;        // bf16 of a K (or V^T) image
+constexpr int kPieceTileU4 = 2 * kPieceHalves * 2 / 16;  // uint4 of a tile's two images
+
+__global__ __launch_bounds__(kPfThreads) void KvPieces(const float* __restrict__ kc,
+                                                       const float* __restrict__ vc,
+                                                       int64_t slot, int KV, int64_t max_pos,
+                                                       int64_t n_tiles,
+                                                       uint16_t* __restrict__ images) {
+    const int64_t t = blockIdx.x / KV;
+    const int g = static_cast<int>(blockIdx.x % KV);
+    KvBlockBf tile;
+    tile.kb = kc + static_cast<int64_t>(g) * 128;
+    tile.vb = vc + static_cast<int64_t>(g) * 128;
+    tile.slot = slot;
+    tile.max_pos = max_pos;  // positions past it read its row
+    tile.Load(t * kPfTile);
+    uint16_t* ks = images + (static_cast<int64_t>(g) * n_tiles + t) * (2 * kPieceHalves);
+    tile.Store<128, kPfTile>(ks, ks + kPieceHalves);
+}
+
+// The next tile from KvPieces' images: thread tid copies uint4 tid + 256 i
+// (i < 6) of the K image and of the V^T image.  K image uint4 u: piece
+// u / 512, row (u / 16) % 32, dims 8 (u % 16) ..; V^T image: piece u / 512,
+// dim (u / 4) % 128, slots 8 (u % 4) ...  In the workgroup's last tile, V
+// at positions past its last token's is zeroed (their probabilities are 0;
+// KvBlockBf reads the last token's row there, so finite values give the
+// same sums), and K there needs nothing (those scores are replaced by -inf).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct KvBlockPre {
+    u32x4 k[6], v[6];   // native vectors, not uint4 structs (see KvTile::Load)
+    const u32x4* base;  // head g's first image
+    int64_t max_pos;
+    __device__ void Load(int64_t p0) {
+        const u32x4* src = base + (p0 / kPfTile) * kPieceTileU4;
+        const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            k[i] = src[tid + kPfThreads * i];
+            v[i] = src[kPieceTileU4 / 2 + tid + kPfThreads * i];
+        }
+        const int64_t mp = max_pos - p0;  // the last position kept, within the tile
+        if (mp < kPfTile - 1) {
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                // slots 8 q4 + 2d, + 1 (dword d): positions 16 (d / 2) + 4 q4 +
+                // 2 (d % 2), + 1
+                const int64_t b = 4 * ((tid + kPfThreads * i) % 4);
+                const auto keep = [&](int64_t pl) {
+                    return (pl <= mp ? 0x0000FFFFu : 0u) | (pl + 1 <= mp ? 0xFFFF0000u : 0u);
+                };
+                v[i].x &= keep(b);
+                v[i].y &= keep(b + 2);
+                v[i].z &= keep(b + 16);
+                v[i].w &= keep(b + 18);
+            }
+        }
+    }
+    __device__ void Store(uint16_t* ks, uint16_t* vs) const {
+        constexpr int KL = 128 + kBfKLd;
+        const int tid = static_cast<int>(threadIdx.x);
+#pragma unroll
+        for (int i = 0; i < 6; ++i) {
+            const int u = tid + kPfThreads * i;
+            *reinterpret_cast<u32x4*>(ks + ((u / 512) * kPfTile + (u / 16) % kPfTile) * KL +
+                                      8 * (u % 16)) = k[i];
+            *reinterpret_cast<u32x4*>(vs + ((u / 512) * 128 + (u / 4) % 128) * kBfVLd +
+                                      8 * (u % 4)) = v[i];
         }
     }
 };
@@ -220,13 +301,15 @@ struct TileChunks {
     int32_t* err;
 };
 
-template <int HD, bool kChunked, bool kBf, int NBUF = 2>
+template <int HD, bool kChunked, bool kBf, int NBUF = 2, bool kPre = false>
 __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const float* __restrict__ q, int64_t q_stride, const float* __restrict__ kc,
     const float* __restrict__ vc, int64_t slot, int KV, int H, int32_t pos0, int64_t T,
-    float scale, float* __restrict__ out, int head_blocks, TileChunks tc) {
+    float scale, float* __restrict__ out, int head_blocks, TileChunks tc,
+    const uint16_t* __restrict__ images, int64_t n_image_tiles) {
 #pragma clang fp contract(off)
     static_assert(!kBf || HD == 128, "bf16 products: head_dim 128");
+    static_assert(!kPre || (kBf && !kChunked), "pre-split tiles: prompt chunks, bf16 products");
     static_assert(NBUF == 2 || (NBUF == 1 && kBf), "one tile buffer: bf16 products only");
     constexpr int LD = HD + 4;
     constexpr int NC = HD / 16;                          // 16-dim chunks
@@ -300,10 +383,17 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
         for (int c = 0; c < NC; ++c) qv[c] = *reinterpret_cast<const f32x4*>(qrow + 16 * c);
     }
 
-    typename std::conditional<kBf, KvBlockBf, KvTile<HD>>::type tile;
-    tile.kb = kc + static_cast<int64_t>(g) * HD;
-    tile.vb = vc + static_cast<int64_t>(g) * HD;
-    tile.slot = slot;
+    typename std::conditional<kPre, KvBlockPre,
+                              typename std::conditional<kBf, KvBlockBf, KvTile<HD>>::type>::type
+        tile;
+    if constexpr (kPre) {
+        tile.base = reinterpret_cast<const u32x4*>(images) +
+                    static_cast<int64_t>(g) * n_image_tiles * kPieceTileU4;
+    } else {
+        tile.kb = kc + static_cast<int64_t>(g) * HD;
+        tile.vb = vc + static_cast<int64_t>(g) * HD;
+        tile.slot = slot;
+    }
     tile.max_pos = max_pos;
     auto load = [&](int64_t p0) { tile.Load(p0); };
     auto store = [&](int buf) { tile.Store(sm.k[buf], sm.v[buf]); };
@@ -487,9 +577,16 @@ bool PrefillSupported(int32_t head_dim, const float* q, int64_t q_row_stride, co
            Aligned(out, 16) && Aligned(k_cache, 16) && Aligned(v_cache, 16);
 }
 
+int64_t PrefillImageBytes(int32_t n_kv_heads, int32_t head_dim, int64_t n_pos) {
+    if (head_dim != 128 || n_kv_heads <= 0 || n_pos <= 0) return 0;
+    return static_cast<int64_t>(n_kv_heads) * ((n_pos + kPfTile - 1) / kPfTile) * kPieceTileU4 *
+           16;
+}
+
 mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, const float* vc,
                          int64_t slot, int32_t H, int32_t KV, int32_t head_dim, int32_t pos0,
-                         int64_t T, float* out, hipStream_t s) {
+                         int64_t T, float* out, hipStream_t s, void* workspace,
+                         size_t workspace_bytes) {
     const int group = H / KV;
     const int head_blocks = (group + kPfHeads - 1) / kPfHeads;
     const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
@@ -498,14 +595,33 @@ mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, 
     const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
     const dim3 grid(static_cast<unsigned>(blocks));
     const TileChunks none{};
+    // head_dim 128 with room for the tile images: split K and V once
+    // (positions 0 .. pos0 + T - 1), then stage the images
+    const int64_t n_pos = pos0 + T;
+    const int64_t image_bytes = PrefillImageBytes(KV, head_dim, n_pos);
+    if (image_bytes > 0 && T >= kPrefillImageMinTokens && workspace != nullptr &&
+        Aligned(workspace, 16) &&
+        static_cast<int64_t>(workspace_bytes) >= image_bytes) {
+        const int64_t n_tiles = (n_pos + kPfTile - 1) / kPfTile;
+        if (n_tiles * KV > 0x7FFFFFFF) return Fail(MLK_ERR_INVALID, "attention prefill: launch too large");
+        uint16_t* images = static_cast<uint16_t*>(workspace);
+        hipLaunchKernelGGL(KvPieces, dim3(static_cast<unsigned>(n_tiles * KV)), dim3(kPfThreads), 0,
+                           s, kc, vc, slot, KV, n_pos - 1, n_tiles, images);
+        mlk_status st = CheckLaunch("KvPieces");
+        if (st != MLK_OK) return st;
+        hipLaunchKernelGGL((AttnPrefill<128, false, true, 1, true>), grid, dim3(kPfThreads), 0, s,
+                           q, q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
+                           none, images, n_tiles);
+        return CheckLaunch("AttnPrefill");
+    }
     if (head_dim == 64) {
         hipLaunchKernelGGL((AttnPrefill<64, false, false>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           none);
+                           none, nullptr, 0);
     } else {
         hipLaunchKernelGGL((AttnPrefill<128, false, true, 1>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           none);
+                           none, nullptr, 0);
     }
     return CheckLaunch("AttnPrefill");
 }
@@ -540,17 +656,17 @@ mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* k
     if (head_dim == 64) {
         hipLaunchKernelGGL((AttnPrefill<64, true, false>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           tc);
+                           tc, nullptr, 0);
     } else if (blocks <= ComputeUnits()) {
         // bf16 products: their 111 KB of LDS leave one workgroup per unit,
         // which a grid this small uses anyway
         hipLaunchKernelGGL((AttnPrefill<128, true, true>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           tc);
+                           tc, nullptr, 0);
     } else {
         hipLaunchKernelGGL((AttnPrefill<128, true, true, 1>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           tc);
+                           tc, nullptr, 0);
     }
     return CheckLaunch("AttnPrefill (decode tokens)");
 }

@@ -424,12 +424,26 @@ def assert_prefill_close(got, exact, pav, dmax, n, what, pieces=False):
                            f"err {float(err.max()):.3e}")
 
 
-def run_prefill(mlk, cache, q, layer, pos0, via_decode=False):
+def image_bytes(KV, n_pos):
+    """Workspace of the pre-split K/V tile images at head_dim 128: per KV
+    head and 32-position tile, K and V^T in three bf16 pieces (48 KB)."""
+    return KV * ((n_pos + 31) // 32) * 2 * 3 * 32 * 128 * 2
+
+
+def run_prefill(mlk, cache, q, layer, pos0, via_decode=False, images=False):
+    """images: through the decode entry with a workspace that holds the
+    pre-split tile images (head_dim 128), so K and V are split once before
+    the tiles instead of in every workgroup."""
     q = np.ascontiguousarray(q, np.float32)
     T, H, hd = q.shape
     d_q = mlk.DeviceBuffer.from_array(q)
     out = mlk.DeviceBuffer.empty((T, H, hd))
-    if via_decode:
+    if images:
+        ws_bytes = image_bytes(cache.KV, pos0 + T)
+        ws = mlk.DeviceBuffer(ws_bytes, np.uint8)
+        mlk.attention_decode(d_q, cache.k, cache.v, cache.L, cache.S, H, cache.KV, hd, layer, T,
+                             out, pos0 + T, pos0=pos0, workspace=ws, workspace_bytes=ws_bytes)
+    elif via_decode:
         ws_bytes = mlk.attention_workspace_bytes(T, H, cache.KV, hd, pos0 + T)
         ws = mlk.DeviceBuffer(max(ws_bytes, 4), np.uint8)
         mlk.attention_decode(d_q, cache.k, cache.v, cache.L, cache.S, H, cache.KV, hd, layer, T,
@@ -469,6 +483,30 @@ def test_attention_prefill_shapes(mlk, H, KV, hd, T, pos0):
     assert_prefill_close(got, ex, pav, dmax, n, f"prefill H{H} KV{KV} hd{hd} T{T} pos0 {pos0}",
                          pieces=hd == 128)
     np.testing.assert_array_equal(run_prefill(mlk, cache, q, 1, pos0, via_decode=True), got)
+
+
+@pytest.mark.parametrize("H,pos0", [(32, 37), (64, 0)])
+def test_attention_prefill_tile_images(mlk, H, pos0):
+    """From 1024 tokens at head_dim 128 a workspace of the tile images' size
+    makes the decode entry split K and V into bf16 pieces once, then stage
+    the images: bit-identical to the kernel that splits every tile in every
+    workgroup (the same pieces; V past a block's last token is zeroed where
+    its probabilities are 0).  1040 tokens after a 37-position prefix: a
+    partial last block and tiles that straddle block ends; cache slots past
+    the chunk hold NaN (never read); sampled tokens against float64."""
+    rng = np.random.default_rng(H + pos0)
+    KV, hd, T = 8, 128, 1040
+    S = pos0 + T + 40
+    kc, vc = random_cache(rng, 2, S, KV, hd)
+    kc[:, pos0 + T:] = np.nan
+    vc[:, pos0 + T:] = np.nan
+    cache = Cache(mlk, kc, vc)
+    q = rng.standard_normal((T, H, hd)).astype(np.float32)
+    got = run_prefill(mlk, cache, q, 1, pos0)
+    np.testing.assert_array_equal(run_prefill(mlk, cache, q, 1, pos0, images=True), got)
+    for t in (0, 15, 16, 517, 1023, 1024, 1039):
+        ex, pav, dmax, n = attention_exact(q[t], kc, vc, 1, pos0 + t)
+        assert_attention_close(got[t], ex, pav, dmax, n, f"token {t}", pieces=True)
 
 
 def test_attention_prefill_counts_exactly_the_prefix(mlk):
@@ -531,6 +569,8 @@ def test_attention_prefill_bench_shape(mlk):
     for t in (0, 1, 15, 16, 17, 255, 1000, 2047, 2048, 3071, 4094, 4095):
         ex, pav, dmax, n = attention_exact(q[t], kc, vc, 0, t)
         assert_attention_close(got[t], ex, pav, dmax, n, f"token {t}", pieces=True)
+    # the pre-split tile images (what the batched layer runs): every token equal
+    np.testing.assert_array_equal(run_prefill(mlk, cache, q, 0, 0, images=True), got)
 
 
 def full_significand(rng, shape):
