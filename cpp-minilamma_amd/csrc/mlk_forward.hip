@@ -107,7 +107,8 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
     // bf16 planes of the planar layers' x (h, attention's output, then
     // SwiGLU's output)
     const int64_t widest = std::max(D, std::max(F, QD));
-    p.plane_bytes = PlanarRows(T) ? T * widest * 6 : 0;
+    // (many tokens: h's planes for the tiled q, k/v and gate/up launches)
+    p.plane_bytes = PlanarRows(T) ? T * widest * 6 : (T > 64 && D % 32 == 0 ? T * D * 6 : 0);
     p.off[10] = at;
     at += Align256(p.plane_bytes);
     p.total = at;
@@ -320,6 +321,9 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     const bool kv_pair = !(qkv1 || qkvm) && w->wk.type == w->wv.type &&
                          TiledFusedApplies(w->wk.type, T, D, KD, kStreamPlain) &&
                          Aligned(w->wk.data, 2) && Aligned(w->wv.data, 2);
+    // q alone on the tiled launch when h's planes are at hand (below)
+    const bool q_tiled = !(qkv1 || qkvm) && TiledFusedApplies(w->wq.type, T, D, QD, kStreamAdd) &&
+                         Aligned(w->wq.data, 2);
     // Many tokens (128-row tiles, K in one pass): the same groups' epilogues
     // in the GEMM itself, gate/up as one launch with SwiGLU, wo and down
     // adding into x (the plain GEMM's sums, so the separate kernels' values)
@@ -358,7 +362,8 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     const uint32_t* h_planes = nullptr;
     if (attn_fold) {
         // in the q/k/v launch below
-    } else if (qkvp && planes != nullptr && NormPlanesApplies(x, nullptr, w->attention_norm, h, D)) {
+    } else if ((qkvp || q_tiled || kv_pair) && planes != nullptr &&
+               NormPlanesApplies(x, nullptr, w->attention_norm, h, D)) {
         MLK_TRY(AddRmsNormPlanes(x, nullptr, w->attention_norm, h, planes, T, D, eps, hs));
         h_planes = planes;
     } else {
@@ -390,12 +395,21 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
             MLK_TRY(LinearSkinnyFused(w->wq.type, h, T, D, a, mode, lin_ws, lin_b, hs));
         }
     } else {
-        MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
+        if (q_tiled && h_planes != nullptr) {  // h's planes instead of splitting h per tile
+            StreamArgs a{};
+            a.seg[0] = Seg(w->wq, q, QD);
+            a.n_seg = 1;
+            a.x_planes = h_planes;
+            MLK_TRY(LinearTiledFused(w->wq.type, h, T, D, a, kStreamPlain, hs));
+        } else {
+            MLK_TRY(Linear(w->wq, h, q, T, D, QD, lin_ws, lin_b, stream));
+        }
         if (kv_pair) {
             StreamArgs a{};
             a.seg[0] = Seg(w->wk, k_rows, KD);
             a.seg[1] = Seg(w->wv, v_rows, KD);
             a.n_seg = 2;
+            a.x_planes = h_planes;
             MLK_TRY(LinearTiledFused(w->wk.type, h, T, D, a, kStreamPlain, hs));
         } else {
             MLK_TRY(Linear(w->wk, h, k_rows, T, D, KD, lin_ws, lin_b, stream));
@@ -450,9 +464,15 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         } else {
             MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));
         }
-        if (wo_add) {  // x already holds x + proj
+        if (wo_add && ffn_tiled && planes != nullptr &&
+            NormPlanesApplies(x, nullptr, w->ffn_norm, h, D)) {
+            // x already holds x + proj; h's planes for the gate/up launch
+            MLK_TRY(AddRmsNormPlanes(x, nullptr, w->ffn_norm, h, planes, T, D, eps, hs));
+            h_planes = planes;
+        } else if (wo_add) {  // x already holds x + proj
             MLK_TRY(mlk_rmsnorm_f32(x, w->ffn_norm, h, T, D, eps, stream));
-        } else if (ffnp && planes != nullptr && NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
+        } else if ((ffnp || ffn_tiled) && planes != nullptr &&
+                   NormPlanesApplies(x, proj, w->ffn_norm, h, D)) {
             MLK_TRY(AddRmsNormPlanes(x, proj, w->ffn_norm, h, planes, T, D, eps, hs));
             h_planes = planes;
         } else if (!ffn_fold) {
@@ -494,6 +514,7 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
         a.seg[0] = Seg(w->w_gate, gate, F);
         a.seg[1] = Seg(w->w_up, gate, F);
         a.n_seg = 2;
+        a.x_planes = h_planes;
         MLK_TRY(LinearTiledFused(w->w_gate.type, h, T, D, a, kStreamSwiGlu, hs));
     } else {
         MLK_TRY(Linear(w->w_gate, h, gate, T, D, F, lin_ws, lin_b, stream));

@@ -39,6 +39,8 @@
 // FLOPs per call: 2 T O K.
 #include "mlk_quant.h"
 
+#include <type_traits>
+
 namespace mlk {
 namespace {
 
@@ -484,7 +486,14 @@ __device__ inline void TileCodes(const WTile<WT>& t, int32_t (&c)[16]) {
 // separate kernels' values (mlk_add_f32, mlk_swiglu_f32) bit for bit.
 enum PiecesEpi { kPcStore = 0, kPcAdd = 1, kPcSwiGlu = 2, kPcPair = 3 };
 
-template <int WT, int NW, int EPI = kPcStore>
+typedef uint32_t u32x4p __attribute__((ext_vector_type(4)));
+
+// kXP: x comes already split, as the planes StorePlanes writes ([K / 32
+// blocks][3 pieces][T rows][16 dwords], the pieces PiecesOf4 makes, bit for
+// bit, for every value): each stage copies 3 x 128 rows x 4 groups of 8
+// inputs (16 B) into the swizzled LDS layout, with no split in the loop
+// (the split was 7-8.5% of the linears' time at Llama-3-8B's T = 4096).
+template <int WT, int NW, int EPI = kPcStore, bool kXP = false>
 __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ x,
                                                            const uint8_t* __restrict__ w,
                                                            const float* __restrict__ bias,
@@ -495,11 +504,13 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
                                                            float* __restrict__ partial,
                                                            const uint8_t* __restrict__ w2,
                                                            const float* __restrict__ bias2,
-                                                           float* __restrict__ y2) {
+                                                           float* __restrict__ y2,
+                                                           const uint32_t* __restrict__ xp) {
     constexpr int BM = 128;
     constexpr int kThreads = 64 * NW;
     constexpr int BNT = 32 * NW;               // W rows per tile
     constexpr int kXN = BM * kBK / 4 / kThreads;  // x float4s per thread and stage
+    constexpr int kXPN = 3 * BM * 4 / kThreads;   // kXP: 16-byte plane groups per thread and stage
     constexpr bool kDual = EPI == kPcSwiGlu;
     static_assert(!kDual || NW == 8, "gate / up tiles take 8 waves");
     __shared__ PiecesSmem<BNT> sm;
@@ -541,26 +552,51 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
     // stage s - 1 and is in registers by then (requested one ahead, the
     // scheduler moved its split next to its request and every stage waited
     // out the load latency).
-    auto load_x = [&](int64_t k0, float4 (&xv)[kXN]) {
+    using XRegs = typename std::conditional<kXP, u32x4p[kXPN], float4[kXN]>::type;
+    auto load_x = [&](int64_t k0, XRegs& xv) {
+        if constexpr (kXP) {
+            // group idx: piece idx / 512, row (idx / 4) % 128, inputs 8 (idx % 4) ..
+            const uint32_t* blk = xp + (k0 / kBK) * 3 * T * 16;
 #pragma unroll
-        for (int i = 0; i < kXN; ++i) {
-            const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
-            const int64_t r = m0 + (idx >> 3);
-            const int64_t c = k0 + 4 * (idx & 7);
-            xv[i] = *reinterpret_cast<const float4*>(x + (r < T ? r * K + c : c));
+            for (int i = 0; i < kXPN; ++i) {
+                const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
+                const int64_t r = m0 + ((idx >> 2) & (BM - 1));
+                xv[i] = *reinterpret_cast<const u32x4p*>(
+                    blk + ((idx >> 9) * T + (r < T ? r : 0)) * 16 + 4 * (idx & 3));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < kXN; ++i) {
+                const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
+                const int64_t r = m0 + (idx >> 3);
+                const int64_t c = k0 + 4 * (idx & 7);
+                xv[i] = *reinterpret_cast<const float4*>(x + (r < T ? r * K + c : c));
+            }
         }
     };
     // one stage into LDS buffer b: x pieces, W codes as bf16, scales
-    auto store = [&](int b, const float4 (&xv)[kXN], const WTile<WT>& wt) {
+    auto store = [&](int b, const XRegs& xv, const WTile<WT>& wt) {
+        if constexpr (kXP) {
 #pragma unroll
-        for (int i = 0; i < kXN; ++i) {
-            const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
-            const int r = idx >> 3, c8 = idx & 7;
-            uint2 pc[3];
-            PiecesOf4(xv[i], pc);
-            const int at = r * 16 + (((c8 >> 1) ^ ((r >> 1) & 3)) << 2) + 2 * (c8 & 1);
+            for (int i = 0; i < kXPN; ++i) {
+                const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
+                const int r = (idx >> 2) & (BM - 1);
+                const int at = (idx >> 9) * 128 * 16 + r * 16 + (((idx & 3) ^ ((r >> 1) & 3)) << 2);
+                *reinterpret_cast<u32x4p*>(&sm.x[b][at]) = xv[i];
+            }
+        } else {
 #pragma unroll
-            for (int p = 0; p < 3; ++p) *reinterpret_cast<uint2*>(&sm.x[b][p * 128 * 16 + at]) = pc[p];
+            for (int i = 0; i < kXN; ++i) {
+                const int idx = static_cast<int>(threadIdx.x) + kThreads * i;
+                const int r = idx >> 3, c8 = idx & 7;
+                uint2 pc[3];
+                PiecesOf4(xv[i], pc);
+                const int at = r * 16 + (((c8 >> 1) ^ ((r >> 1) & 3)) << 2) + 2 * (c8 & 1);
+#pragma unroll
+                for (int p = 0; p < 3; ++p) {
+                    *reinterpret_cast<uint2*>(&sm.x[b][p * 128 * 16 + at]) = pc[p];
+                }
+            }
         }
         int32_t c[16];
         TileCodes<WT>(wt, c);
@@ -576,8 +612,8 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
     // stage s in LDS buffer (s - s0) & 1, stage s + 1 in registers `held`;
     // stage s + 2 requested into `next` (past the last stage: the last again,
     // never stored where it is read)
-    auto step = [&](int64_t s, const float4 (&held_x)[kXN], const WTile<WT>& held_w,
-                    float4 (&next_x)[kXN], WTile<WT>& next_w) {
+    auto step = [&](int64_t s, const XRegs& held_x, const WTile<WT>& held_w, XRegs& next_x,
+                    WTile<WT>& next_w) {
         const int buf = static_cast<int>((s - s0) & 1);
         const int64_t k2 = (s + 2 < s1 ? s + 2 : s1 - 1) * kBK;
         load_x(k2, next_x);
@@ -611,7 +647,7 @@ __global__ __launch_bounds__(64 * NW) void GemmPieces(const float* __restrict__ 
         store(buf ^ 1, held_x, held_w);
         __syncthreads();
     };
-    float4 xa[kXN], xb[kXN];
+    XRegs xa, xb;
     WTile<WT> wa, wb;
     load_x(s0 * kBK, xa);
     wa.Load(wsrc, O, K, row_bytes, n0w, s0 * kBK);
@@ -1596,24 +1632,43 @@ mlk_status LaunchSkinny(int wt, const float* x, const SkinnyArgs& a, int64_t T, 
 }
 
 // false: no kernel of this epilogue for wt (the fused epilogues are built
-// for block-layout Q8_0 / Q4_0 only)
+// for block-layout Q8_0 / Q4_0 only; x from planes (xp) for them too, with
+// 8 waves and not with the residual add)
 template <int NW, int EPI = kPcStore>
 bool LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
                   const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
                   int tiles_m, int tiles, int64_t per_split, float* partial,
                   const uint8_t* w2 = nullptr, const float* bias2 = nullptr,
-                  float* y2 = nullptr) {
+                  float* y2 = nullptr, const uint32_t* xp = nullptr) {
     const dim3 block(64 * NW);
+    if (xp != nullptr) {
+        // 8 waves only: at 4 the planes' registers leave one wave a SIMD
+        if constexpr (EPI != kPcAdd && NW == 8) {
+            if (wt == MLK_Q8_0) {
+                hipLaunchKernelGGL((GemmPieces<MLK_Q8_0, NW, EPI, true>), grid, block, 0, s, x, w,
+                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split,
+                                   partial, w2, bias2, y2, xp);
+                return true;
+            }
+            if (wt == MLK_Q4_0) {
+                hipLaunchKernelGGL((GemmPieces<MLK_Q4_0, NW, EPI, true>), grid, block, 0, s, x, w,
+                                   bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split,
+                                   partial, w2, bias2, y2, xp);
+                return true;
+            }
+        }
+        return false;
+    }
     switch (wt) {
         case MLK_Q8_0:
             hipLaunchKernelGGL((GemmPieces<MLK_Q8_0, NW, EPI>), grid, block, 0, s, x, w, bias, y,
                                T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
-                               y2);
+                               y2, nullptr);
             return true;
         case MLK_Q4_0:
             hipLaunchKernelGGL((GemmPieces<MLK_Q4_0, NW, EPI>), grid, block, 0, s, x, w, bias, y,
                                T, K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
-                               y2);
+                               y2, nullptr);
             return true;
         default:
             break;
@@ -1622,13 +1677,13 @@ bool LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_
         if (wt == kWPlanarQ8) {
             hipLaunchKernelGGL((GemmPieces<kWPlanarQ8, NW>), grid, block, 0, s, x, w, bias, y, T,
                                K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
-                               y2);
+                               y2, nullptr);
             return true;
         }
         if (wt == kWPlanarQ4) {
             hipLaunchKernelGGL((GemmPieces<kWPlanarQ4, NW>), grid, block, 0, s, x, w, bias, y, T,
                                K, O, row_bytes, tiles_m, tiles, per_split, partial, w2, bias2,
-                               y2);
+                               y2, nullptr);
             return true;
         }
     }
@@ -1785,10 +1840,16 @@ mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const 
                             int mode, hipStream_t s) {
     const StreamSeg& g0 = sa.seg[0];
     const int64_t O = g0.rows;
-    if (!TiledFusedApplies(wt, T, K, O, mode) || !Aligned(x, 16)) {
+    const bool single = mode == kStreamPlain && sa.n_seg == 1;
+    if (!TiledFusedApplies(wt, T, K, O, single ? kStreamAdd : mode) || !Aligned(x, 16) ||
+        (sa.x_planes != nullptr && (mode == kStreamAdd || !Aligned(sa.x_planes, 16)))) {
         return Fail(MLK_ERR_INVALID, "linear (tiled, fused): unsupported shape");
     }
-    if (mode == kStreamSwiGlu || mode == kStreamPlain) {
+    if (single) {
+        if (g0.w == nullptr || g0.y == nullptr || !Aligned(g0.w, 2)) {
+            return Fail(MLK_ERR_INVALID, "linear (tiled, fused): bad segment");
+        }
+    } else if (mode == kStreamSwiGlu || mode == kStreamPlain) {
         const StreamSeg& g1 = sa.seg[1];
         if (sa.n_seg != 2 || g1.rows != O || g0.w == nullptr || g1.w == nullptr ||
             g1.y == nullptr || (mode == kStreamPlain && g0.y == nullptr) || !Aligned(g0.w, 2) ||
@@ -1811,7 +1872,22 @@ mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const 
     const int64_t stages = K / kBK;
     const int tm = static_cast<int>((T + 127) / 128);
     bool ok = false;
-    if (mode == kStreamPlain) {
+    const uint32_t* xp = sa.x_planes;
+    if (single) {
+        // the tile width LaunchTiles takes for the plain product
+        const int64_t tiles8 = static_cast<int64_t>(tm) * ((O + 255) / 256);
+        if (tiles8 >= 2 * static_cast<int64_t>(ComputeUnits())) {
+            const int tiles = static_cast<int>(tiles8);
+            ok = LaunchPieces<8>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w, g0.bias, g0.y,
+                                 T, K, O, row_bytes, tm, tiles, stages, nullptr, nullptr, nullptr,
+                                 nullptr, xp);
+        } else {
+            // 4-wave tiles split x themselves (no planes variant)
+            const int tiles = static_cast<int>(tm * ((O + 127) / 128));
+            ok = LaunchPieces<4>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w, g0.bias, g0.y,
+                                 T, K, O, row_bytes, tm, tiles, stages, nullptr);
+        }
+    } else if (mode == kStreamPlain) {
         // 256-output tiles (TiledFusedApplies leaves at least one a CU):
         // each x split serves twice the outputs of a 128-output tile;
         // measured at Llama-3-8B's k / v (256 tiles) as fast as 512 tiles
@@ -1820,12 +1896,13 @@ mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const 
         const StreamSeg& g1 = sa.seg[1];
         ok = LaunchPieces<8, kPcPair>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w, g0.bias,
                                       g0.y, T, K, O, row_bytes, tm, tiles, stages, nullptr, g1.w,
-                                      g1.bias, g1.y);
+                                      g1.bias, g1.y, xp);
     } else if (mode == kStreamSwiGlu) {
         const int tiles = static_cast<int>(tm * ((O + 127) / 128));
         ok = LaunchPieces<8, kPcSwiGlu>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w,
                                         g0.bias, sa.seg[1].y, T, K, O, row_bytes, tm, tiles,
-                                        stages, nullptr, sa.seg[1].w, sa.seg[1].bias);
+                                        stages, nullptr, sa.seg[1].w, sa.seg[1].bias, nullptr,
+                                        xp);
     } else {
         // the tile width LaunchTiles takes for the plain product
         const int64_t tiles8 = static_cast<int64_t>(tm) * ((O + 255) / 256);

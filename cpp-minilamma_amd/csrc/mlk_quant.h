@@ -122,6 +122,9 @@ struct StreamArgs {
     // outputs also go here as bf16 planes (StorePlanes, mlk_common.h) for
     // the next planar layer; F % 32 == 0
     uint32_t* planes = nullptr;
+    // LinearTiledFused only: x already split into planes (StorePlanes
+    // layout, 16-byte aligned), read instead of x (not with kStreamAdd)
+    const uint32_t* x_planes = nullptr;
 };
 
 // in_features % 64 == 0 and x (16-byte aligned) fits the kernel's LDS
@@ -174,7 +177,11 @@ int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O);
 // each to its own y) in one launch without a K split, when their tiles
 // together fill two workgroups per CU (where LaunchGemm would split each:
 // the sums are then the unsplit product's, LaunchGemm's without a
-// workspace).  x 16-byte aligned, W 2-byte aligned.
+// workspace); with one segment, that matrix alone, under kStreamAdd's shape
+// rule (LaunchGemm's sums).  a.x_planes, when set, holds x as StorePlanes
+// writes it and the 8-wave tiles read it instead of splitting x (the same
+// sums; not with kStreamAdd; 4-wave tiles still read x).  x 16-byte
+// aligned, W 2-byte aligned.
 bool TiledFusedApplies(int wt, int64_t T, int64_t K, int64_t O, int mode);
 mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& a,
                             int mode, hipStream_t s);
