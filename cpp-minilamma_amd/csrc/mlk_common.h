@@ -239,6 +239,23 @@ __device__ inline void StorePlanes(uint32_t* planes, int64_t T, int64_t t, int64
     for (int p = 0; p < 3; ++p) d[p * T * 16] = PackBf(p0[p], p1[p]);
 }
 
+// Inputs k .. k + 3 (k a multiple of 4): two dwords of each plane, one
+// 8-byte store per piece.
+__device__ inline void StorePlanes4(uint32_t* planes, int64_t T, int64_t t, int64_t k, float v0,
+                                    float v1, float v2, float v3) {
+    float p0[3], p1[3], p2[3], p3[3];
+    SplitBf(v0, p0);
+    SplitBf(v1, p1);
+    SplitBf(v2, p2);
+    SplitBf(v3, p3);
+    uint32_t* d = planes + ((k / 32) * 3 * T + t) * 16 + (k % 32) / 2;
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+        *reinterpret_cast<uint2*>(d + p * T * 16) = make_uint2(PackBf(p0[p], p1[p]),
+                                                               PackBf(p2[p], p3[p]));
+    }
+}
+
 // Input k alone: its three bf16 halves of the planes' dwords.
 __device__ inline void StorePlanes1(uint32_t* planes, int64_t T, int64_t t, int64_t k, float v) {
     float p[3];

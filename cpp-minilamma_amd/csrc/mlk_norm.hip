@@ -137,10 +137,7 @@ __global__ __launch_bounds__(kWave * kWaves) void AddRmsNormVec(
                 o.z = static_cast<float>(static_cast<double>(r[v].z) * static_cast<double>(w.z) * scale);
                 o.w = static_cast<float>(static_cast<double>(r[v].w) * static_cast<double>(w.w) * scale);
                 StoreNT(yr + i, o);
-                if (kPlanes) {
-                    StorePlanes(planes, n_rows, row, 4 * i, o.x, o.y);
-                    StorePlanes(planes, n_rows, row, 4 * i + 2, o.z, o.w);
-                }
+                if (kPlanes) StorePlanes4(planes, n_rows, row, 4 * i, o.x, o.y, o.z, o.w);
             }
         }
     }
