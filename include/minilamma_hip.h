@@ -261,7 +261,11 @@ int64_t mlk_attention_workspace_bytes(int64_t n_tokens, int32_t n_heads, int32_t
  * six bf16 piece products above 2^-21 relative, so each product is within
  * 2^-20 of its exact value (fp32 rounds at 2^-24).  With positions == NULL, 16 or more
  * tokens, head_dim 64 or 128 and 16-byte aligned q rows, out and caches, the
- * call runs mlk_attention_prefill_f32's kernel and uses no workspace.
+ * call runs mlk_attention_prefill_f32's kernel; from 1024 tokens at head_dim
+ * 128, a 16-byte aligned workspace of at least 12 * KV * head_dim *
+ * (pos0 + n_tokens rounded up to 32) bytes lets it split K and V into bf16
+ * pieces once (one extra launch) instead of in every workgroup, with the
+ * same results; otherwise it uses no workspace.
  * Replaces CudaAttentionDevice (include/cuda_attention.h:12-13;
  * src/cuda_attention.cu:77-176, 2 launches, one cudaMalloc and a device
  * synchronize per call).
@@ -354,7 +358,11 @@ typedef struct {
 
 /* Device bytes of the workspace of mlk_forward_layer_batch for n_tokens
  * tokens attending up to max_ctx positions; consecutive_positions != 0 when
- * the call passes positions == NULL (0 on bad input). */
+ * the call passes positions == NULL (0 on bad input).  A prompt chunk of
+ * 1024 or more tokens at head_dim 128 includes the attention's pre-split
+ * K/V (12 bytes per cached K and V element of a layer up to max_ctx), and
+ * more than 64 tokens the bf16 planes of the normed rows (6 * n_tokens *
+ * dim bytes). */
 int64_t mlk_forward_layer_workspace_bytes(const mlk_layer_config* cfg, int64_t n_tokens,
                                           int64_t max_ctx, int32_t consecutive_positions);
 
