@@ -21,7 +21,8 @@ and graph-replayed), configs[3] (Q8_0/Q4_0/Q4_1 gathers) and configs[4]
 and "decode_layer_8b": one Llama-3-8B layer through mlk_forward_layer_batch
 as a decode step (one token at position 8191, and 16 tokens at positions in
 0..8191; Q8_0 / Q4_0 on their planar copies), Q8_0 / Q4_0 / F32, weights
-rotated over 4 layers.
+rotated over 4 layers; and "prefill_layer_8b": the same layer (Q8_0) over
+a 4096-token prompt chunk at positions 0..4095.
 Before each measured section a ZeroKernel launch of 4096 * (100 + i) bytes
 marks section i in a rocprofv3 trace (bench.py --rocprof-report uses it).
 
@@ -433,7 +434,7 @@ def gather_fractions(entry):
 
 PHASE_BASE = 100
 PHASES = ("c3_chain", "c3_ops", "c2_decode", "c1_tiny", "c4_gather", "c5_chain", "c5_ops",
-          "c2_decode_graph", "c1_tiny_graph", "decode_layer_8b")
+          "c2_decode_graph", "c1_tiny_graph", "decode_layer_8b", "prefill_layer_8b")
 
 
 class Marks:
@@ -1001,15 +1002,13 @@ def _warm_clock(mlk, st, launch, ms=CLOCK_WARM_MS):
     st.synchronize()
 
 
-def layer_bench(mlk, steps, path):
+def prefill_layer_bench(mlk, fwd, steps, types=("q8_0", "q4_0", "f32"), token_loop=True,
+                        log=sys.stdout, marks=None):
     """One Llama-3-8B layer (attention + SwiGLU FFN) over a T = 4096 prompt
-    chunk at positions 0..4095 through mlk_forward_layer_batch, timed between
-    two events around `steps` calls; beside it the same layer run the
-    reference's way, one token at a time (T = 1 calls at positions 0..63),
-    and the reference's own CPU forward pass (oracle/_ref, one layer, a
-    few tokens)."""
-    import importlib
-    fwd = importlib.import_module(mlk.__name__ + ".forward")
+    chunk at positions 0..4095 through mlk_forward_layer_batch, per weight
+    type: `steps` calls timed between two events after the clock warm-up;
+    with token_loop, the same layer run the reference's way beside it, one
+    token at a time (T = 1 calls at positions 0..63)."""
     cfg = dict(workloads.CONFIGS["c3_prefill_8b"])
     cfg.update(hidden_dim=cfg["ffn"], max_seq=LAYER_TOKENS)
     T = LAYER_TOKENS
@@ -1018,9 +1017,10 @@ def layer_bench(mlk, steps, path):
     fl_att = workloads.flops_prefill_attention(T, cfg["n_heads"], hd)
     out = {"workload": "one Llama-3-8B layer, T = 4096 prompt chunk at positions 0..4095, "
                        "weights N(0, 0.02) quantized on the device, x N(0, 1)",
-           "layer_flops": fl_lin + fl_att, "linear_flops": fl_lin, "attention_flops": fl_att,
-           "peak_TFLOPs": MFMA_FP32_PEAK_TFLOPS}
+           "layer_flops": fl_lin + fl_att, "linear_flops": fl_lin, "attention_flops": fl_att}
     st = mlk.Stream()
+    if marks is not None:
+        marks("prefill_layer_8b", st)
     kc = mlk.DeviceBuffer.empty((1, T, KV, hd))
     vc = mlk.DeviceBuffer.empty((1, T, KV, hd))
     kc.zero()
@@ -1028,7 +1028,7 @@ def layer_bench(mlk, steps, path):
     x = mlk.DeviceBuffer.empty((T, D))
     ws = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, T, T, True), np.uint8)
     ws1 = mlk.DeviceBuffer(fwd.layer_workspace_bytes(cfg, 1, T, True), np.uint8)
-    for wt in ("q8_0", "q4_0", "f32"):
+    for wt in types:
         w, keep = _device_layer(mlk, fwd, cfg, wt, 400)
         mlk.fill_normal(x, T * D, 0.0, 1.0, 21)
         _warm_clock(mlk, st, lambda i: fwd.forward_layer_batch(cfg, w, x, T, kc, vc, 1, T, 0, T, ws,
@@ -1040,36 +1040,51 @@ def layer_bench(mlk, steps, path):
         e1.record(st)
         e1.synchronize()
         ms = e0.elapsed_ms(e1) / steps
-        # the token loop: token t alone at position t (its cache prefix as
-        # the batched call left it)
-        n = LAYER_LOOP_SAMPLE
-        x1 = mlk.DeviceBuffer.empty((n, D))
-        mlk.fill_normal(x1, n * D, 0.0, 1.0, 22)
-        # one untimed token first: the first one-token call of a weight type
-        # loads its kernels, which would dominate the sample's average
-        fwd.forward_layer_batch(cfg, w, x1.ptr, 1, kc, vc, 1, T, 0, T, ws1, pos0=0, stream=st)
-        st.synchronize()
-        e2, e3 = mlk.Event(), mlk.Event()
-        e2.record(st)
-        for t in range(n):
-            fwd.forward_layer_batch(cfg, w, x1.ptr + t * D * 4, 1, kc, vc, 1, T, 0, T, ws1,
-                                    pos0=t, stream=st)
-        e3.record(st)
-        e3.synchronize()
-        loop_us = e2.elapsed_ms(e3) / n * 1e3
         tf = (fl_lin + fl_att) / (ms * 1e-3) / 1e12
         peak, basis = gemm_peak(wt, T)
         out[wt] = {"us": round(ms * 1e3, 1), "layer_ms": round(ms, 3),
                    "tokens_per_s": round(T / (ms * 1e-3), 1),
                    "TFLOPs": round(tf, 2), "peak_TFLOPs": round(peak, 1), "peak_basis": basis,
-                   "frac_of_peak": round(tf / peak, 4),
-                   "token_loop_us_per_token": round(loop_us, 1),
-                   "token_loop_tokens_per_s": round(1e6 / loop_us, 1),
-                   "batch_speedup_over_token_loop": round(loop_us * T / (ms * 1e3), 1)}
-        print(f"layer {wt} T={T}: {ms:.2f} ms ({T / (ms * 1e-3):.0f} tokens/s, {tf:.1f} "
-              f"TFLOP/s); token loop {loop_us:.0f} us/token", flush=True)
-        x1.close()
+                   "frac_of_peak": round(tf / peak, 4)}
+        msg = f"layer {wt} T={T}: {ms:.2f} ms ({T / (ms * 1e-3):.0f} tokens/s, {tf:.1f} TFLOP/s)"
+        if token_loop:
+            # token t alone at position t (its cache prefix as the batched
+            # call left it); one untimed token first: the first one-token
+            # call of a weight type loads its kernels, which would dominate
+            # the sample's average
+            n = LAYER_LOOP_SAMPLE
+            x1 = mlk.DeviceBuffer.empty((n, D))
+            mlk.fill_normal(x1, n * D, 0.0, 1.0, 22)
+            fwd.forward_layer_batch(cfg, w, x1.ptr, 1, kc, vc, 1, T, 0, T, ws1, pos0=0, stream=st)
+            st.synchronize()
+            e2, e3 = mlk.Event(), mlk.Event()
+            e2.record(st)
+            for t in range(n):
+                fwd.forward_layer_batch(cfg, w, x1.ptr + t * D * 4, 1, kc, vc, 1, T, 0, T, ws1,
+                                        pos0=t, stream=st)
+            e3.record(st)
+            e3.synchronize()
+            loop_us = e2.elapsed_ms(e3) / n * 1e3
+            out[wt].update({"token_loop_us_per_token": round(loop_us, 1),
+                            "token_loop_tokens_per_s": round(1e6 / loop_us, 1),
+                            "batch_speedup_over_token_loop": round(loop_us * T / (ms * 1e3), 1)})
+            msg += f"; token loop {loop_us:.0f} us/token"
+            x1.close()
+        print(msg, file=log, flush=True)
         del keep
+    return out
+
+
+def layer_bench(mlk, steps, path):
+    """bench.py --layer: the prefill layer (prefill_layer_bench, Q8_0 /
+    Q4_0 / F32 with the token loop), the decode layer, and the reference's
+    own CPU forward pass (oracle/_ref, one layer, a few tokens)."""
+    import importlib
+    fwd = importlib.import_module(mlk.__name__ + ".forward")
+    cfg = dict(workloads.CONFIGS["c3_prefill_8b"])
+    cfg.update(hidden_dim=cfg["ffn"], max_seq=LAYER_TOKENS)
+    out = prefill_layer_bench(mlk, fwd, steps)
+    out["peak_TFLOPs"] = MFMA_FP32_PEAK_TFLOPS
     out["decode"] = decode_layer_bench(mlk, fwd, steps)
     out["cpu_reference"] = layer_cpu_reference(cfg)
     with open(path, "w") as f:
@@ -1853,6 +1868,10 @@ def main():
     fwd = importlib.import_module(mlk.__name__ + ".forward")
     result["decode_layer_8b"] = decode_layer_bench(mlk, fwd, min(args.steps, 10), log=sys.stderr,
                                                    marks=marks)
+    # and the same layer over a 4096-token prompt chunk (Q8_0)
+    result["prefill_layer_8b"] = prefill_layer_bench(mlk, fwd, min(args.steps, 10), ("q8_0",),
+                                                     token_loop=False, log=sys.stderr,
+                                                     marks=marks)
     print(json.dumps(result))
 
 
