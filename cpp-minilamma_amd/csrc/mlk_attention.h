@@ -21,13 +21,15 @@ bool PrefillSupported(int32_t head_dim, const float* q, int64_t q_row_stride, co
 // workgroup; the sums are the same.  Otherwise no workspace is used.  Below
 // that many tokens a tile is staged by too few workgroups for the extra
 // launch to pay (Llama-3-70B heads, T = 512: 44 -> 48 us with the images;
-// T = 4096: 1569 -> 1443 us).
+// T = 4096: 1569 -> 1443 us).  a_planes (16-byte aligned, H * head_dim a
+// multiple of 32), when set, also receives the output rows as StorePlanes
+// planes.
 constexpr int64_t kPrefillImageMinTokens = 1024;
 int64_t PrefillImageBytes(int32_t n_kv_heads, int32_t head_dim, int64_t n_pos);
 mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, const float* vc,
                          int64_t slot, int32_t H, int32_t KV, int32_t head_dim, int32_t pos0,
                          int64_t T, float* out, hipStream_t s, void* workspace = nullptr,
-                         size_t workspace_bytes = 0);
+                         size_t workspace_bytes = 0, uint32_t* a_planes = nullptr);
 
 // Decode tokens at any positions (positions[t], or pos0 + t) on the same
 // matrix-core tiles: a workgroup holds 16 tokens and shares each K/V tile
@@ -46,7 +48,8 @@ mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* k
 // mlk_attention_decode_f32 with one more output: when the chunk merge runs
 // (more than one chunk of cache positions) and planes is not null, the merge
 // also writes out's bf16 planes (StorePlanes1 over rows of n_heads * head_dim,
-// which must be a multiple of 32) and sets *planes_written; otherwise planes
+// which must be a multiple of 32) and sets *planes_written, and so does the
+// prefill kernel (positions == NULL, 16 or more tokens); otherwise planes
 // are untouched and *planes_written is false.
 mlk_status AttentionDecode(const float* q, int64_t q_row_stride, const float* k_cache,
                            const float* v_cache, int64_t n_layers, int64_t max_seq,

@@ -896,10 +896,12 @@ mlk_status AttentionDecode(const float* q, int64_t q_row_stride, const float* k_
         PrefillSupported(head_dim, q, q_row_stride, out, k_cache, v_cache)) {
         // a prompt chunk at consecutive positions: the matrix-core prefill
         // kernel (a workspace of PrefillImageBytes holds the pre-split tiles)
+        // (and a's planes, when asked, for a tiled wo)
+        if (planes != nullptr && planes_written != nullptr) *planes_written = true;
         return LaunchPrefill(q, q_row_stride, k_cache + layer * max_seq * slot,
                              v_cache + layer * max_seq * slot, slot, n_heads, n_kv_heads,
                              head_dim, pos0, n_tokens, out, AsStream(stream), workspace,
-                             workspace_bytes);
+                             workspace_bytes, planes);
     }
     if (n_tokens >= kTileMinTokens && PrefillSupported(head_dim, q, q_row_stride, out, k_cache, v_cache) &&
         Aligned(workspace, 16)) {

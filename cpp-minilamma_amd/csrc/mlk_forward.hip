@@ -107,8 +107,10 @@ Plan MakePlan(const mlk_layer_config& c, int64_t T, int64_t max_ctx, bool contig
     // bf16 planes of the planar layers' x (h, attention's output, then
     // SwiGLU's output)
     const int64_t widest = std::max(D, std::max(F, QD));
-    // (many tokens: h's planes for the tiled q, k/v and gate/up launches)
-    p.plane_bytes = PlanarRows(T) ? T * widest * 6 : (T > 64 && D % 32 == 0 ? T * D * 6 : 0);
+    // (many tokens: h's planes for the tiled q, k/v and gate/up launches,
+    // and the prefill attention's output planes for wo)
+    p.plane_bytes = PlanarRows(T) ? T * widest * 6
+                                  : (T > 64 && D % 32 == 0 ? T * std::max(D, QD) * 6 : 0);
     p.off[10] = at;
     at += Align256(p.plane_bytes);
     p.total = at;
@@ -431,7 +433,10 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
     MLK_TRY(AttentionDecode(q, QD, k_cache, v_cache, n_layers, max_seq, c.n_heads, c.n_kv_heads,
                             c.head_dim, layer, positions, pos0, T, max_ctx, a, att_ws,
                             static_cast<size_t>(p.att_bytes), err, stream,
-                            wop && QD % 32 == 0 ? planes : nullptr, &a_planes));
+                            (wop || (wo_add && TiledTakesPlanes(T, D))) && QD % 32 == 0
+                                ? planes
+                                : nullptr,
+                            &a_planes));
     h_planes = nullptr;
     const bool wo_norm = wop && ffnp && planes != nullptr && lin_ws != nullptr &&
                          NormPlanesApplies(x, static_cast<const float*>(lin_ws), w->ffn_norm, h,
@@ -460,6 +465,7 @@ mlk_status mlk_forward_layer_batch(const mlk_layer_config* cfg, const mlk_layer_
             StreamArgs sa{};
             sa.seg[0] = Seg(w->wo, x, D, x);
             sa.n_seg = 1;
+            sa.x_planes = a_planes ? planes : nullptr;  // written by the prefill attention
             MLK_TRY(LinearTiledFused(w->wo.type, a, T, QD, sa, kStreamAdd, hs));
         } else {
             MLK_TRY(Linear(w->wo, a, proj, T, QD, D, lin_ws, lin_b, stream));

@@ -1633,7 +1633,7 @@ mlk_status LaunchSkinny(int wt, const float* x, const SkinnyArgs& a, int64_t T, 
 
 // false: no kernel of this epilogue for wt (the fused epilogues are built
 // for block-layout Q8_0 / Q4_0 only; x from planes (xp) for them too, with
-// 8 waves and not with the residual add)
+// 8 waves)
 template <int NW, int EPI = kPcStore>
 bool LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_t* w,
                   const float* bias, float* y, int64_t T, int64_t K, int64_t O, int64_t row_bytes,
@@ -1643,7 +1643,7 @@ bool LaunchPieces(int wt, dim3 grid, hipStream_t s, const float* x, const uint8_
     const dim3 block(64 * NW);
     if (xp != nullptr) {
         // 8 waves only: at 4 the planes' registers leave one wave a SIMD
-        if constexpr (EPI != kPcAdd && NW == 8) {
+        if constexpr (NW == 8) {
             if (wt == MLK_Q8_0) {
                 hipLaunchKernelGGL((GemmPieces<MLK_Q8_0, NW, EPI, true>), grid, block, 0, s, x, w,
                                    bias, y, T, K, O, row_bytes, tiles_m, tiles, per_split,
@@ -1836,13 +1836,17 @@ bool TiledFusedApplies(int wt, int64_t T, int64_t K, int64_t O, int mode) {
     return mode == kStreamAdd && tiles_m * ((O + 127) / 128) <= 0x7FFFFFFF;
 }
 
+bool TiledTakesPlanes(int64_t T, int64_t O) {
+    return ((T + 127) / 128) * ((O + 255) / 256) >= 2 * static_cast<int64_t>(ComputeUnits());
+}
+
 mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& sa,
                             int mode, hipStream_t s) {
     const StreamSeg& g0 = sa.seg[0];
     const int64_t O = g0.rows;
     const bool single = mode == kStreamPlain && sa.n_seg == 1;
     if (!TiledFusedApplies(wt, T, K, O, single ? kStreamAdd : mode) || !Aligned(x, 16) ||
-        (sa.x_planes != nullptr && (mode == kStreamAdd || !Aligned(sa.x_planes, 16)))) {
+        (sa.x_planes != nullptr && !Aligned(sa.x_planes, 16))) {
         return Fail(MLK_ERR_INVALID, "linear (tiled, fused): unsupported shape");
     }
     if (single) {
@@ -1910,7 +1914,7 @@ mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const 
             const int tiles = static_cast<int>(tiles8);
             ok = LaunchPieces<8, kPcAdd>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w,
                                          g0.bias, g0.y, T, K, O, row_bytes, tm, tiles, stages,
-                                         nullptr);
+                                         nullptr, nullptr, nullptr, nullptr, xp);
         } else {
             const int tiles = static_cast<int>(tm * ((O + 127) / 128));
             ok = LaunchPieces<4, kPcAdd>(wt, dim3(static_cast<unsigned>(tiles)), s, x, g0.w,

@@ -306,7 +306,7 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const float* __restrict__ q, int64_t q_stride, const float* __restrict__ kc,
     const float* __restrict__ vc, int64_t slot, int KV, int H, int32_t pos0, int64_t T,
     float scale, float* __restrict__ out, int head_blocks, TileChunks tc,
-    const uint16_t* __restrict__ images, int64_t n_image_tiles) {
+    const uint16_t* __restrict__ images, int64_t n_image_tiles, uint32_t* __restrict__ a_planes) {
 #pragma clang fp contract(off)
     static_assert(!kBf || HD == 128, "bf16 products: head_dim 128");
     static_assert(!kPre || (kBf && !kChunked), "pre-split tiles: prompt chunks, bf16 products");
@@ -564,8 +564,14 @@ __global__ __launch_bounds__(kPfThreads) void AttnPrefill(
     const float inv = 1.0f / l;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-        *reinterpret_cast<float4*>(orow + 16 * c) =
-            make_float4(acc[c][0] * inv, acc[c][1] * inv, acc[c][2] * inv, acc[c][3] * inv);
+        const float4 o = make_float4(acc[c][0] * inv, acc[c][1] * inv, acc[c][2] * inv,
+                                     acc[c][3] * inv);
+        *reinterpret_cast<float4*>(orow + 16 * c) = o;
+        // the output rows [T, H * HD] also as StorePlanes planes (wo's x)
+        if (a_planes != nullptr) {
+            StorePlanes4(a_planes, T, t, static_cast<int64_t>(h) * HD + 16 * c + 4 * kq, o.x, o.y,
+                         o.z, o.w);
+        }
     }
 }
 
@@ -586,7 +592,7 @@ int64_t PrefillImageBytes(int32_t n_kv_heads, int32_t head_dim, int64_t n_pos) {
 mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, const float* vc,
                          int64_t slot, int32_t H, int32_t KV, int32_t head_dim, int32_t pos0,
                          int64_t T, float* out, hipStream_t s, void* workspace,
-                         size_t workspace_bytes) {
+                         size_t workspace_bytes, uint32_t* a_planes) {
     const int group = H / KV;
     const int head_blocks = (group + kPfHeads - 1) / kPfHeads;
     const int64_t n_tb = (T + kPfTokens - 1) / kPfTokens;
@@ -611,17 +617,17 @@ mlk_status LaunchPrefill(const float* q, int64_t q_row_stride, const float* kc, 
         if (st != MLK_OK) return st;
         hipLaunchKernelGGL((AttnPrefill<128, false, true, 1, true>), grid, dim3(kPfThreads), 0, s,
                            q, q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           none, images, n_tiles);
+                           none, images, n_tiles, a_planes);
         return CheckLaunch("AttnPrefill");
     }
     if (head_dim == 64) {
         hipLaunchKernelGGL((AttnPrefill<64, false, false>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           none, nullptr, 0);
+                           none, nullptr, 0, a_planes);
     } else {
         hipLaunchKernelGGL((AttnPrefill<128, false, true, 1>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           none, nullptr, 0);
+                           none, nullptr, 0, a_planes);
     }
     return CheckLaunch("AttnPrefill");
 }
@@ -656,17 +662,17 @@ mlk_status LaunchDecodeTile(const float* q, int64_t q_row_stride, const float* k
     if (head_dim == 64) {
         hipLaunchKernelGGL((AttnPrefill<64, true, false>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           tc, nullptr, 0);
+                           tc, nullptr, 0, nullptr);
     } else if (blocks <= ComputeUnits()) {
         // bf16 products: their 111 KB of LDS leave one workgroup per unit,
         // which a grid this small uses anyway
         hipLaunchKernelGGL((AttnPrefill<128, true, true>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           tc, nullptr, 0);
+                           tc, nullptr, 0, nullptr);
     } else {
         hipLaunchKernelGGL((AttnPrefill<128, true, true, 1>), grid, dim3(kPfThreads), 0, s, q,
                            q_row_stride, kc, vc, slot, KV, H, pos0, T, scale, out, head_blocks,
-                           tc, nullptr, 0);
+                           tc, nullptr, 0, nullptr);
     }
     return CheckLaunch("AttnPrefill (decode tokens)");
 }

@@ -123,7 +123,7 @@ struct StreamArgs {
     // the next planar layer; F % 32 == 0
     uint32_t* planes = nullptr;
     // LinearTiledFused only: x already split into planes (StorePlanes
-    // layout, 16-byte aligned), read instead of x (not with kStreamAdd)
+    // layout, 16-byte aligned), read instead of x by 8-wave tiles
     const uint32_t* x_planes = nullptr;
 };
 
@@ -180,9 +180,11 @@ int64_t GemmWorkspaceBytes(int wt, int64_t T, int64_t K, int64_t O);
 // workspace); with one segment, that matrix alone, under kStreamAdd's shape
 // rule (LaunchGemm's sums).  a.x_planes, when set, holds x as StorePlanes
 // writes it and the 8-wave tiles read it instead of splitting x (the same
-// sums; not with kStreamAdd; 4-wave tiles still read x).  x 16-byte
-// aligned, W 2-byte aligned.
+// sums; 4-wave tiles still read x).  x 16-byte aligned, W 2-byte aligned.
 bool TiledFusedApplies(int wt, int64_t T, int64_t K, int64_t O, int mode);
+// A one-matrix or residual-add launch of O rows takes the 8-wave tiles,
+// which read x_planes (the pair and SwiGLU launches always do).
+bool TiledTakesPlanes(int64_t T, int64_t O);
 mlk_status LinearTiledFused(int wt, const float* x, int64_t T, int64_t K, const StreamArgs& a,
                             int mode, hipStream_t s);
 
